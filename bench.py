@@ -1,0 +1,192 @@
+"""CSR SpMV benchmark on one MI355X: y = alpha*op(A)*x + beta*y through aclsparseSpMV.
+
+A step is one aclsparseSpMV over the whole matrix (Preprocess runs once before
+timing and is reported separately).  Before every timed step a 512 MiB buffer
+is overwritten so that A, x and y come from HBM, not from L2 / MALL; the SpMV
+itself is timed with HIP events recorded on the stream it runs on.
+
+The headline workload is configs[1] of BASELINE.json: the 5-point Laplacian on
+a 2048^2 grid (fp32).  The other configurations are measured in the same run
+(``configs`` field) unless ``--only-headline`` is given.
+
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "ops-sparse_amd"))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "CSR SpMV GFLOP/s + effective HBM GB/s (% of MI355X peak) on one GPU"
+FLUSH_BYTES = 512 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--configs", default="c1,c2,c3,c4h,c4b,c5")
+    return ap.parse_args()
+
+
+def make(name, dev):
+    from ops_sparse import workloads as wl
+
+    if name == "c4h":
+        return wl.uniform_rows_lowp(device=dev, dtype=torch.float16)
+    if name == "c4b":
+        return wl.uniform_rows_lowp(device=dev, dtype=torch.bfloat16)
+    return wl.config(name, dev)
+
+
+def measure(w, steps, warmup, flush_buf):
+    """Median/mean/p90 SpMV time (ms, HIP events) over ``steps`` flushed launches."""
+    from ops_sparse.spmv import CsrSpMV
+    from ops_sparse._lib import Operation
+
+    op = Operation.NON_TRANSPOSE if w.trans == "N" else Operation.TRANSPOSE
+    y = w.y0.to(w.out_dtype).clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
+    stream = torch.cuda.current_stream()
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    p0.record(stream)
+    plan.preprocess()
+    p1.record(stream)
+    torch.cuda.synchronize()
+    pre_ms = p0.elapsed_time(p1)
+    for _ in range(warmup):
+        flush_buf.add_(1)
+        plan.run()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        flush_buf.add_(1)
+        a.record(stream)
+        plan.run()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    times = sorted(a.elapsed_time(b) for a, b in evs)
+    # back-to-back launches without a flush (L2/MALL warm), for reference only
+    torch.cuda.synchronize()
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0.record(stream)
+    for _ in range(steps):
+        plan.run()
+    h1.record(stream)
+    torch.cuda.synchronize()
+    warm = h0.elapsed_time(h1) / steps
+    return dict(median_ms=statistics.median(times), mean_ms=statistics.fmean(times),
+                p90_ms=times[min(len(times) - 1, int(0.9 * len(times)))], wall_ms_per_step=wall,
+                warm_ms=warm, preprocess_ms=pre_ms, workspace_bytes=plan.buffer_size)
+
+
+def cpu_baseline(w, seconds):
+    """Single-threaded oracle SpMV (the reference host golden restated in C) on a bounded sample."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import numpy as np
+    import oracle
+    from ops_sparse.workloads import algorithmic_bytes
+
+    host = w.to("cpu")
+    rp = host.row_ptr.numpy().astype(np.int64)
+    args = (rp, host.col_ind.numpy(), host.values.numpy(), host.x.numpy(), host.y0.numpy())
+    oracle.spmv_f64(*args, w.alpha, w.beta)  # warm the caches / page in
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.spmv_f64(*args, w.alpha, w.beta)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / n
+    return {"value": algorithmic_bytes(w) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "ms_per_spmv": per * 1e3, "gflops": 2 * w.nnz / per / 1e9,
+            "sample": f"{n} full SpMVs of the headline matrix ({w.rows} rows, {w.nnz} nnz) in {el:.1f} s, "
+                      f"oracle/spmv_oracle.c oracle_spmv_f64 (fp64 accumulation), 1 thread",
+            "cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
+
+
+def load_traffic(name):
+    path = os.path.join(REPO, "profiles", f"traffic_{name}.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the SpMV path is single-device, see DESIGN.md for how it would shard", file=sys.stderr)
+        sys.exit(2)
+    from ops_sparse.workloads import algorithmic_bytes, flops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    names = ["c2"] if args.only_headline else [n.strip() for n in args.configs.split(",") if n.strip()]
+    if "c2" not in names:
+        names.insert(0, "c2")
+    results, headline_w, headline = {}, None, None
+    for name in names:
+        w = make(name, dev)
+        torch.cuda.synchronize()
+        m = measure(w, args.steps, args.warmup, flush_buf)
+        nbytes = algorithmic_bytes(w)
+        gbs = nbytes / (m["median_ms"] * 1e-3) / 1e9
+        r = dict(workload=w.name, rows=w.rows, nnz=w.nnz, op=w.trans, dtype=str(w.values.dtype).split(".")[-1],
+                 algorithmic_bytes=nbytes, gbs=gbs, frac=gbs / HBM_PEAK_GBS,
+                 gflops=flops(w) / (m["median_ms"] * 1e-3) / 1e9,
+                 warm_gbs=nbytes / (m["warm_ms"] * 1e-3) / 1e9, **m)
+        print(f"# {name}: {json.dumps(r)}", file=sys.stderr, flush=True)
+        results[name] = r
+        if name == "c2":
+            headline_w, headline = w, r
+        else:
+            del w
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(headline_w, args.cpu_seconds)
+    h = headline
+    out = {
+        "metric": METRIC,
+        "value": round(h["gbs"], 2),
+        "unit": "GB/s",
+        "gflops": round(h["gflops"], 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["median_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded 5-point Laplacian, x/y ~ U(-1,1))",
+        "config": {"workload": h["workload"], "rows": h["rows"], "nnz": h["nnz"], "alpha": 1.5, "beta": 0.5,
+                   "index": "int32", "op": "N", "l2_mall_flushed": True, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(h["frac"], 4), "traffic": load_traffic("c2"),
+                     "kernel": "SpmvRowBlockKernel", "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
+        "cpu_baseline": cpu,
+        "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in results.items()},
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

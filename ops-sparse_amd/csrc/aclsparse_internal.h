@@ -1,0 +1,219 @@
+// Internal types of libaclsparse_hip: handle, descriptors, SpMV workspace
+// layout and the launcher interface between the host C ABI and the gfx950
+// kernels.  Nothing here is part of the public ABI.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "cann_ops_sparse.h"
+
+namespace aclsp {
+
+// Opaque-object signatures.  Same values as the reference so that foreign or
+// stale pointers fail the same way (sparse/common/aclsparse_handle_internal.h:28,
+// sparse/common/aclsparse_descr_internal.h:87-89).
+constexpr uint32_t kHandleSignature = 0xAC1F9501U;
+constexpr uint32_t kSpMatSignature = 0x53504D54U;
+constexpr uint32_t kDnVecSignature = 0xD0D2D4D6U;
+constexpr uint32_t kSpMVOpDescrSignature = 0x534D5644U;  // "SMVD"
+constexpr uint32_t kSpMVOpPlanSignature = 0x534D5650U;   // "SMVP"
+
+constexpr int kVersion = 10000;  // 1.0.0, encoded MAJOR*10000+MINOR*100+PATCH
+constexpr size_t kDefaultWorkspaceBytes = 4U * 1024U * 1024U;
+
+}  // namespace aclsp
+
+// The public typedefs name these structs in the global namespace.
+struct aclsparseContext {
+    uint32_t signature = aclsp::kHandleSignature;
+    aclrtStream stream = nullptr;  // null = unset; ACL_SPARSE_HIP_NULL_STREAM = HIP null stream
+    // Bumped on every stream change; a preprocess plan records it so that a
+    // stream switch A->B->A cannot revive a plan made on the old epoch
+    // (sparse/common/aclsparse_auxiliary.cpp:162-179).
+    uint64_t stream_epoch = 0;
+    aclsparsePointerMode_t pointer_mode = ACL_SPARSE_POINTER_MODE_HOST;
+    void* default_workspace = nullptr;  // allocated lazily by aclsparseGetWorkspace
+    size_t default_workspace_size = 0;
+    void* user_workspace = nullptr;
+    size_t user_workspace_size = 0;
+};
+
+// Fingerprint of the last aclsparseSpMVPreprocess on a matrix.  aclsparseSpMV
+// skips the partition kernel only when every field still matches
+// (sparse/spmv/arch35/spmv.h:46-109).
+struct SpmvPlan {
+    const void* buffer = nullptr;
+    const void* row_offsets = nullptr;
+    const void* col_ind = nullptr;
+    const void* values = nullptr;
+    int64_t row_stride = 1, col_stride = 1, val_stride = 1, x_stride = 1, y_stride = 1;
+    uint64_t rows = 0, cols = 0, nnz = 0;
+    aclsparseIndexBase_t base = ACL_SPARSE_INDEX_BASE_ZERO;
+    aclsparseIndexType_t ptr_type = ACL_SPARSE_INDEX_32I;
+    aclDataType value_type = ACL_FLOAT, x_type = ACL_FLOAT, y_type = ACL_FLOAT, compute_type = ACL_FLOAT;
+    aclsparseOperation_t op = ACL_SPARSE_OP_NON_TRANSPOSE;
+    int32_t alg = -1;
+    aclrtStream stream = nullptr;
+    uint64_t stream_epoch = 0;
+};
+
+struct aclsparseSpMatDescr {
+    uint32_t signature = aclsp::kSpMatSignature;
+    aclsparseFormat_t format = ACL_SPARSE_FORMAT_CSR;
+    uint64_t rows = 0, cols = 0, nnz = 0;
+    void* ptrs = nullptr;    // row offsets
+    void* idxs = nullptr;    // column indices
+    void* values = nullptr;
+    aclsparseIndexType_t ptr_type = ACL_SPARSE_INDEX_32I;
+    aclsparseIndexType_t idx_type = ACL_SPARSE_INDEX_32I;
+    aclsparseIndexBase_t base = ACL_SPARSE_INDEX_BASE_ZERO;
+    aclDataType value_type = ACL_FLOAT;
+    int64_t ptr_stride = 1, idx_stride = 1, value_stride = 1;  // in elements
+    SpmvPlan plan;  // plan.buffer == nullptr means "no active SpMV plan"
+};
+
+struct aclsparseDnVecDescr {
+    uint32_t signature = aclsp::kDnVecSignature;
+    uint64_t nums = 0;
+    void* values = nullptr;
+    aclDataType value_type = ACL_FLOAT;
+    int64_t stride = 1;
+};
+
+namespace aclsp {
+
+// ---------------------------------------------------------------------------
+// SpMV workspace layout (all offsets 64-byte aligned):
+//   [0, 192)            SpmvWsHeader, written by the preprocess kernel
+//   [192, ...)          normalised row offsets: rowPtr[i*stride]-base clamped
+//                       to [0, nnz], rows+1 entries of 4 (I32) or 8 (I64) bytes.
+//                       Same place as the reference's normalised copy
+//                       (sparse/spmv/arch35/spmv_tiling_data.h:77-79).
+//   block_row_start     int32[num_blocks+1]: first row of each row block
+//   accumulator         transpose only: cols x accumulator element
+// ---------------------------------------------------------------------------
+constexpr size_t kWsAlign = 64;
+constexpr size_t kWsHeaderBytes = 192;
+constexpr uint32_t kWsMagic = 0x4D505348U;  // "HSPM"
+
+// Row-block partition parameters.  A row block holds the rows whose
+// merge-path start coordinate (row + rowOffset[row]) lies in
+// [b*T, (b+1)*T); T is chosen so that a block's non-zeros fit one LDS chunk.
+constexpr int64_t kChunkNnz = 2048;        // LDS product slots per chunk
+constexpr int64_t kChunkTarget = 1984;     // nnz per block the T formula aims at
+constexpr int64_t kMinItemsPerBlock = 256;
+constexpr int64_t kMaxItemsPerBlock = 4096;  // also bounds the rows of one block
+
+struct SpmvWsHeader {
+    uint32_t magic;
+    uint32_t version;
+    uint64_t rows;
+    uint64_t cols;
+    uint64_t nnz;
+    uint64_t items_per_block;
+    uint64_t num_blocks;
+    uint64_t rowptr_offset;
+    uint64_t blocks_offset;
+    uint64_t acc_offset;
+    uint32_t rowptr_bytes;
+    uint32_t index_base;
+    uint32_t op;
+    uint32_t reserved[27];
+};
+static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
+
+inline size_t AlignUp(size_t v) { return (v + kWsAlign - 1) & ~(kWsAlign - 1); }
+
+inline int64_t ItemsPerBlock(uint64_t rows, uint64_t nnz)
+{
+    const uint64_t denom = nnz == 0 ? 1 : nnz;
+    // rows + nnz < 2^33 and kChunkTarget < 2^11, so the product fits 64 bits.
+    int64_t t = static_cast<int64_t>((static_cast<uint64_t>(kChunkTarget) * (rows + nnz)) / denom);
+    if (t < kMinItemsPerBlock) t = kMinItemsPerBlock;
+    if (t > kMaxItemsPerBlock) t = kMaxItemsPerBlock;
+    return t;
+}
+
+inline int64_t NumBlocks(uint64_t rows, uint64_t nnz)
+{
+    const int64_t t = ItemsPerBlock(rows, nnz);
+    return static_cast<int64_t>((rows + nnz + static_cast<uint64_t>(t) - 1) / static_cast<uint64_t>(t));
+}
+
+struct SpmvLayout {
+    size_t rowptr_offset = 0;
+    size_t blocks_offset = 0;
+    size_t acc_offset = 0;
+    size_t total = 0;
+    int64_t items_per_block = 0;
+    int64_t num_blocks = 0;
+    uint32_t rowptr_bytes = 4;
+};
+
+inline size_t AccumulatorBytes(aclDataType computeType)
+{
+    return computeType == ACL_INT32 ? 8U : computeType == ACL_COMPLEX64 ? 8U : 4U;
+}
+
+inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
+                                aclDataType computeType, bool transpose)
+{
+    SpmvLayout l;
+    l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
+    l.items_per_block = ItemsPerBlock(rows, nnz);
+    l.num_blocks = NumBlocks(rows, nnz);
+    l.rowptr_offset = kWsHeaderBytes;
+    l.blocks_offset = AlignUp(l.rowptr_offset + static_cast<size_t>(rows + 1) * l.rowptr_bytes);
+    l.acc_offset = AlignUp(l.blocks_offset + static_cast<size_t>(l.num_blocks + 1) * sizeof(int32_t));
+    l.total = l.acc_offset;
+    if (transpose) {
+        l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));
+    }
+    return l;
+}
+
+// ---------------------------------------------------------------------------
+// Launcher interface (implemented in spmv_kernels.hip).
+// ---------------------------------------------------------------------------
+enum class ValKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I8 = 3, C64 = 4 };
+enum class OutKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I32 = 3, C64 = 4 };
+enum class AccKind : int32_t { F32 = 0, I64 = 1, C64 = 2 };
+
+struct SpmvLaunch {
+    // matrix (original descriptor pointers and strides)
+    const void* row_ptr;       // original row offsets
+    int64_t row_stride;
+    const int32_t* col;
+    int64_t col_stride;
+    const void* val;
+    int64_t val_stride;
+    const void* x;
+    int64_t x_stride;
+    void* y;
+    int64_t y_stride;
+    int64_t rows, cols, nnz;
+    int32_t base;
+    int32_t rowptr64;          // 1: row offsets are int64
+    ValKind val_kind;
+    OutKind out_kind;
+    AccKind acc_kind;
+    int32_t op;                // aclsparseOperation_t
+    int32_t alg;               // aclsparseSpMVAlg_t
+    // scalars: host mode fills the values, device mode the pointers
+    int32_t device_scalars;
+    float alpha_re, alpha_im, beta_re, beta_im;
+    int32_t alpha_i, beta_i;
+    const void* alpha_ptr;
+    const void* beta_ptr;
+    // workspace
+    void* ws;
+    SpmvLayout layout;
+};
+
+// Normalises the row offsets and writes the row-block partition and header.
+int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream);
+// Runs y = alpha*op(A)*x + beta*y using the partition already in the workspace.
+int LaunchSpmvCompute(const SpmvLaunch& l, void* stream);
+
+}  // namespace aclsp

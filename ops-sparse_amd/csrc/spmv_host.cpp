@@ -1,0 +1,356 @@
+// aclsparseSpMVGetBufferSize / aclsparseSpMVPreprocess / aclsparseSpMV.
+//
+// Validation order and status codes restate sparse/spmv/arch35/spmv_host.cpp:
+//   handle (:109-126) -> descriptors (:175-183) -> op (:187-190) ->
+//   compute type / alg (:191-196) -> pointer mode + scalar alignment (:142-163)
+//   -> format (:220-233) -> shape (:235-261) -> dtype combo (:44-66, :274-281)
+//   -> strides (:282-292) -> vector sizes (:315-329); execution adds storage
+//   binding + aliasing (:331-355) and the workspace check (:357-368).
+// Deviation: CSR row offsets may be ACL_SPARSE_INDEX_64I (the reference
+// rejects them in SpMV); column indices stay 32-bit.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <limits>
+
+#include "aclsparse_internal.h"
+
+namespace {
+
+using aclsp::SpmvLayout;
+
+bool IsTranspose(aclsparseOperation_t op)
+{
+    return op == ACL_SPARSE_OP_TRANSPOSE || op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE;
+}
+
+bool IsScalarType(aclDataType t) { return t == ACL_INT32 || t == ACL_FLOAT || t == ACL_COMPLEX64; }
+
+bool IsSupportedAlg(aclsparseSpMVAlg_t alg)
+{
+    return alg == ACL_SPARSE_SPMV_ALG_DEFAULT || alg == ACL_SPARSE_SPMV_CSR_ALG1 || alg == ACL_SPARSE_SPMV_CSR_ALG2;
+}
+
+// Supported (A, x, y, compute) combinations (sparse/spmv/arch35/spmv_host.cpp:44-66).
+bool IsSupportedCombo(aclDataType v, aclDataType x, aclDataType y, aclDataType c)
+{
+    if (v != x) return false;
+    if (c == ACL_INT32) return v == ACL_INT8 && y == ACL_INT32;
+    if (c == ACL_COMPLEX64) return (v == ACL_COMPLEX64 || v == ACL_FLOAT) && y == ACL_COMPLEX64;
+    if (c != ACL_FLOAT) return false;
+    return (v == ACL_INT8 && y == ACL_FLOAT) || (v == ACL_FLOAT16 && (y == ACL_FLOAT16 || y == ACL_FLOAT)) ||
+           (v == ACL_BF16 && (y == ACL_BF16 || y == ACL_FLOAT)) || (v == ACL_FLOAT && y == ACL_FLOAT);
+}
+
+size_t ElementBytes(aclDataType t)
+{
+    return t == ACL_INT8 ? 1U : (t == ACL_FLOAT16 || t == ACL_BF16) ? 2U : t == ACL_COMPLEX64 ? 8U : 4U;
+}
+
+size_t ScalarAlignment(aclDataType c)
+{
+    return c == ACL_INT32 ? alignof(int32_t) : c == ACL_COMPLEX64 ? alignof(aclsparseComplex)
+                                              : c == ACL_FLOAT ? alignof(float) : 0U;
+}
+
+bool StrideFits(uint64_t length, int64_t stride, size_t elementBytes)
+{
+    if (stride <= 0 || elementBytes == 0U) return false;
+    const uint64_t maxOffset = static_cast<uint64_t>(std::numeric_limits<int64_t>::max()) / elementBytes;
+    return length <= 1U || static_cast<uint64_t>(stride) <= maxOffset / (length - 1U);
+}
+
+aclsparseStatus_t ValidateHandle(aclsparseHandle_t h)
+{
+    if (h == nullptr) return ACL_SPARSE_STATUS_HANDLE_IS_NULLPTR;
+    if (h->signature != aclsp::kHandleSignature) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (h->stream == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;  // stream must be set
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t ValidateSetup(aclsparseHandle_t h, aclsparseOperation_t op, const void* alpha,
+                                aclsparseConstSpMatDescr_t A, aclsparseConstDnVecDescr_t x, const void* beta,
+                                aclsparseConstDnVecDescr_t y, aclDataType c, aclsparseSpMVAlg_t alg)
+{
+    aclsparseStatus_t st = ValidateHandle(h);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    if (A == nullptr || x == nullptr || y == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (A->signature != aclsp::kSpMatSignature || x->signature != aclsp::kDnVecSignature ||
+        y->signature != aclsp::kDnVecSignature) {
+        return ACL_SPARSE_STATUS_INVALID_VALUE;
+    }
+    if (op != ACL_SPARSE_OP_NON_TRANSPOSE && !IsTranspose(op)) return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    if (!IsScalarType(c) || !IsSupportedAlg(alg)) return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    if (h->pointer_mode != ACL_SPARSE_POINTER_MODE_HOST && h->pointer_mode != ACL_SPARSE_POINTER_MODE_DEVICE) {
+        return ACL_SPARSE_STATUS_INVALID_VALUE;
+    }
+    if (alpha == nullptr || beta == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    const size_t a = ScalarAlignment(c);
+    if (a == 0U || reinterpret_cast<uintptr_t>(alpha) % a != 0U || reinterpret_cast<uintptr_t>(beta) % a != 0U) {
+        return ACL_SPARSE_STATUS_INVALID_VALUE;
+    }
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t ValidateMetadata(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
+                                   const aclsparseDnVecDescr* y, aclDataType c)
+{
+    if (m->format != ACL_SPARSE_FORMAT_CSR ||
+        (m->ptr_type != ACL_SPARSE_INDEX_32I && m->ptr_type != ACL_SPARSE_INDEX_64I) ||
+        m->idx_type != ACL_SPARSE_INDEX_32I ||
+        (m->base != ACL_SPARSE_INDEX_BASE_ZERO && m->base != ACL_SPARSE_INDEX_BASE_ONE)) {
+        return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    }
+    if (m->nnz > 0U && (m->rows == 0U || m->cols == 0U)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    const uint64_t maxI32 = static_cast<uint64_t>(std::numeric_limits<int32_t>::max());
+    const uint64_t baseOffset = m->base == ACL_SPARSE_INDEX_BASE_ONE ? 1U : 0U;
+    // I32 row offsets must hold nnz+base; I64 row offsets are limited by the
+    // 2^40 element bound of this build (block-relative offsets are 32-bit and
+    // every row must stay below 2^31 entries).
+    const uint64_t maxNnz = m->ptr_type == ACL_SPARSE_INDEX_32I ? maxI32 - baseOffset : (uint64_t{1} << 40);
+    if (m->rows > maxI32 || m->cols > maxI32 || m->nnz > maxNnz) return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    if (m->rows != 0U && m->cols > UINT64_MAX / m->rows) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (!IsSupportedCombo(m->value_type, x->value_type, y->value_type, c)) return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    const size_t ptrBytes = m->ptr_type == ACL_SPARSE_INDEX_64I ? 8U : 4U;
+    if (!StrideFits(m->rows + 1U, m->ptr_stride, ptrBytes) || !StrideFits(m->nnz, m->idx_stride, 4U) ||
+        !StrideFits(m->nnz, m->value_stride, ElementBytes(m->value_type)) ||
+        !StrideFits(x->nums, x->stride, ElementBytes(x->value_type)) ||
+        !StrideFits(y->nums, y->stride, ElementBytes(y->value_type))) {
+        return ACL_SPARSE_STATUS_INVALID_VALUE;
+    }
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t ValidateVectorSizes(aclsparseOperation_t op, const aclsparseSpMatDescr* m,
+                                      const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y)
+{
+    const uint64_t xr = IsTranspose(op) ? m->rows : m->cols;
+    const uint64_t yr = IsTranspose(op) ? m->cols : m->rows;
+    return (x->nums != xr || y->nums != yr) ? ACL_SPARSE_STATUS_INVALID_VALUE : ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t ValidateInputs(aclsparseHandle_t h, aclsparseOperation_t op, const void* alpha,
+                                 aclsparseConstSpMatDescr_t A, aclsparseConstDnVecDescr_t x, const void* beta,
+                                 aclsparseConstDnVecDescr_t y, aclDataType c, aclsparseSpMVAlg_t alg)
+{
+    aclsparseStatus_t st = ValidateSetup(h, op, alpha, A, x, beta, y, c, alg);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    st = ValidateMetadata(A, x, y, c);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    return ValidateVectorSizes(op, A, x, y);
+}
+
+bool HasAliases(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y)
+{
+    if (m->ptrs != nullptr &&
+        (m->ptrs == m->idxs || m->ptrs == m->values || m->ptrs == x->values || m->ptrs == y->values)) {
+        return true;
+    }
+    if (m->idxs != nullptr && (m->idxs == m->values || m->idxs == x->values || m->idxs == y->values)) return true;
+    return (m->values != nullptr && (m->values == x->values || m->values == y->values)) ||
+           (x->values != nullptr && x->values == y->values);
+}
+
+aclsparseStatus_t ValidateStorage(aclsparseOperation_t op, const aclsparseSpMatDescr* m,
+                                  const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y)
+{
+    const uint64_t xr = IsTranspose(op) ? m->rows : m->cols;
+    const uint64_t yr = IsTranspose(op) ? m->cols : m->rows;
+    if ((m->rows > 0U && m->ptrs == nullptr) || (m->nnz > 0U && (m->idxs == nullptr || m->values == nullptr)) ||
+        (xr > 0U && x->values == nullptr) || (yr > 0U && y->values == nullptr)) {
+        return ACL_SPARSE_STATUS_INVALID_VALUE;
+    }
+    return HasAliases(m, x, y) ? ACL_SPARSE_STATUS_INVALID_VALUE : ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t ValidateWorkspace(void* buffer)
+{
+    if (buffer == nullptr) return ACL_SPARSE_STATUS_INSUFFICIENT_RESOURCES;
+    if (reinterpret_cast<uintptr_t>(buffer) % aclsp::kWsAlign != 0U) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c)
+{
+    return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op));
+}
+
+SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
+                  aclsparseOperation_t op, aclDataType c, aclsparseSpMVAlg_t alg, const void* buffer,
+                  const aclsparseContext* h)
+{
+    SpmvPlan p;
+    p.buffer = buffer;
+    p.row_offsets = m->ptrs;
+    p.col_ind = m->idxs;
+    p.values = m->values;
+    p.row_stride = m->ptr_stride;
+    p.col_stride = m->idx_stride;
+    p.val_stride = m->value_stride;
+    p.x_stride = x->stride;
+    p.y_stride = y->stride;
+    p.rows = m->rows;
+    p.cols = m->cols;
+    p.nnz = m->nnz;
+    p.base = m->base;
+    p.ptr_type = m->ptr_type;
+    p.value_type = m->value_type;
+    p.x_type = x->value_type;
+    p.y_type = y->value_type;
+    p.compute_type = c;
+    p.op = op;
+    p.alg = static_cast<int32_t>(alg);
+    p.stream = h->stream;
+    p.stream_epoch = h->stream_epoch;
+    return p;
+}
+
+bool PlanMatches(const SpmvPlan& a, const SpmvPlan& b)
+{
+    return a.buffer != nullptr && a.buffer == b.buffer && a.row_offsets == b.row_offsets &&
+           a.col_ind == b.col_ind && a.values == b.values && a.row_stride == b.row_stride &&
+           a.col_stride == b.col_stride && a.val_stride == b.val_stride && a.x_stride == b.x_stride &&
+           a.y_stride == b.y_stride && a.rows == b.rows && a.cols == b.cols && a.nnz == b.nnz &&
+           a.base == b.base && a.ptr_type == b.ptr_type && a.value_type == b.value_type &&
+           a.x_type == b.x_type && a.y_type == b.y_type && a.compute_type == b.compute_type && a.op == b.op &&
+           a.alg == b.alg && a.stream == b.stream && a.stream_epoch == b.stream_epoch;
+}
+
+void* HipStreamOf(const aclsparseContext* h)
+{
+    return h->stream == ACL_SPARSE_HIP_NULL_STREAM ? nullptr : h->stream;
+}
+
+aclsp::SpmvLaunch MakeLaunch(const aclsparseContext* h, aclsparseOperation_t op, const void* alpha,
+                             const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const void* beta,
+                             const aclsparseDnVecDescr* y, aclDataType c, aclsparseSpMVAlg_t alg, void* ws)
+{
+    aclsp::SpmvLaunch l{};
+    l.row_ptr = m->ptrs;
+    l.row_stride = m->ptr_stride;
+    l.col = static_cast<const int32_t*>(m->idxs);
+    l.col_stride = m->idx_stride;
+    l.val = m->values;
+    l.val_stride = m->value_stride;
+    l.x = x->values;
+    l.x_stride = x->stride;
+    l.y = y->values;
+    l.y_stride = y->stride;
+    l.rows = static_cast<int64_t>(m->rows);
+    l.cols = static_cast<int64_t>(m->cols);
+    l.nnz = static_cast<int64_t>(m->nnz);
+    l.base = m->base == ACL_SPARSE_INDEX_BASE_ONE ? 1 : 0;
+    l.rowptr64 = m->ptr_type == ACL_SPARSE_INDEX_64I ? 1 : 0;
+    switch (m->value_type) {
+        case ACL_FLOAT16: l.val_kind = aclsp::ValKind::F16; break;
+        case ACL_BF16: l.val_kind = aclsp::ValKind::BF16; break;
+        case ACL_INT8: l.val_kind = aclsp::ValKind::I8; break;
+        case ACL_COMPLEX64: l.val_kind = aclsp::ValKind::C64; break;
+        default: l.val_kind = aclsp::ValKind::F32; break;
+    }
+    switch (y->value_type) {
+        case ACL_FLOAT16: l.out_kind = aclsp::OutKind::F16; break;
+        case ACL_BF16: l.out_kind = aclsp::OutKind::BF16; break;
+        case ACL_INT32: l.out_kind = aclsp::OutKind::I32; break;
+        case ACL_COMPLEX64: l.out_kind = aclsp::OutKind::C64; break;
+        default: l.out_kind = aclsp::OutKind::F32; break;
+    }
+    l.acc_kind = c == ACL_INT32 ? aclsp::AccKind::I64 : c == ACL_COMPLEX64 ? aclsp::AccKind::C64
+                                                                           : aclsp::AccKind::F32;
+    l.op = static_cast<int32_t>(op);
+    l.alg = static_cast<int32_t>(alg);
+    l.device_scalars = h->pointer_mode == ACL_SPARSE_POINTER_MODE_DEVICE ? 1 : 0;
+    if (l.device_scalars) {
+        l.alpha_ptr = alpha;
+        l.beta_ptr = beta;
+    } else if (c == ACL_INT32) {
+        std::memcpy(&l.alpha_i, alpha, sizeof(int32_t));
+        std::memcpy(&l.beta_i, beta, sizeof(int32_t));
+    } else if (c == ACL_COMPLEX64) {
+        aclsparseComplex a, b;
+        std::memcpy(&a, alpha, sizeof(a));
+        std::memcpy(&b, beta, sizeof(b));
+        l.alpha_re = a.x;
+        l.alpha_im = a.y;
+        l.beta_re = b.x;
+        l.beta_im = b.y;
+    } else {
+        std::memcpy(&l.alpha_re, alpha, sizeof(float));
+        std::memcpy(&l.beta_re, beta, sizeof(float));
+    }
+    l.ws = ws;
+    l.layout = LayoutFor(m, op, c);
+    return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+aclsparseStatus_t aclsparseSpMVGetBufferSize(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                             aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX,
+                                             const void* beta, aclsparseDnVecDescr_t vecY, aclDataType computeType,
+                                             aclsparseSpMVAlg_t alg, size_t* bufferSize)
+{
+    if (bufferSize == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    *bufferSize = 0U;
+    aclsparseStatus_t st = ValidateInputs(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    *bufferSize = LayoutFor(matA, opA, computeType).total;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                          aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX,
+                                          const void* beta, aclsparseDnVecDescr_t vecY, aclDataType computeType,
+                                          aclsparseSpMVAlg_t alg, void* externalBuffer)
+{
+    aclsparseStatus_t st = ValidateInputs(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    auto* m = const_cast<aclsparseSpMatDescr*>(matA);
+    // Preprocess reads only the row offsets; values and vectors may be bound later.
+    if (m->rows > 0U && m->ptrs == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    st = ValidateWorkspace(externalBuffer);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    if (m->rows > 0U) {
+        (void)hipGetLastError();
+        const aclsp::SpmvLaunch l =
+            MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
+        if (aclsp::LaunchSpmvPreprocess(l, HipStreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
+            return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+        }
+    }
+    m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX, const void* beta,
+                                aclsparseDnVecDescr_t vecY, aclDataType computeType, aclsparseSpMVAlg_t alg,
+                                void* externalBuffer)
+{
+    aclsparseStatus_t st = ValidateInputs(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    st = ValidateStorage(opA, matA, vecX, vecY);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    st = ValidateWorkspace(externalBuffer);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    const uint64_t outLen = IsTranspose(opA) ? matA->cols : matA->rows;
+    if (outLen == 0U) return ACL_SPARSE_STATUS_SUCCESS;
+
+    auto* m = const_cast<aclsparseSpMatDescr*>(matA);
+    const aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
+    void* stream = HipStreamOf(handle);
+    (void)hipGetLastError();
+    // The partition is rebuilt unless a matching Preprocess already wrote it
+    // into this very buffer.  A zero-row matrix has no partition to build.
+    const bool planned = m->rows == 0U ||
+                         PlanMatches(m->plan, MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle));
+    if (!planned && aclsp::LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
+        return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    }
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,832 @@
+// gfx950 kernels of the CSR SpMV path: y = alpha*op(A)*x + beta*y.
+//
+// Design (one GPU, HBM-bound, no MFMA):
+//  * Preprocess: one launch normalises the row offsets (rowPtr[i*stride]-base,
+//    clamped to [0, nnz]) into the workspace and computes the row-block
+//    partition: block b owns the rows whose merge-path start coordinate
+//    (row + rowOffset[row]) lies in [b*T, (b+1)*T).  Every row belongs to
+//    exactly one block, so no cross-block fix-up is ever needed, and each
+//    block carries ~T rows+nnz items regardless of the row-length
+//    distribution.  Reference counterpart: the normalising kernel
+//    sparse/spmv/arch35/spmv_kernel.cpp:1144-1163 (one block, scalar loop).
+//  * Non-transpose: one workgroup (256 lanes = 4 wave64) per row block.  The
+//    block streams its col_ind/values span through LDS in chunks of 2048
+//    non-zeros with 16-byte non-temporal loads (so x stays in L2/MALL),
+//    gathers x, and reduces rows with an LDS segmented scan (8 items per lane
+//    + a wave64 shuffle scan).  Rows longer than a chunk carry their partial
+//    sum from chunk to chunk inside the block.  Replaces the warp-per-row
+//    kernel sparse/spmv/arch35/spmv_kernel.cpp:501-577.
+//  * Transpose: the same row blocks scatter alpha*conj?(a_ij)*x_i with
+//    hardware float atomics into y (pre-scaled by beta) or into an fp32/int64
+//    accumulator that a finalize pass converts (reference ALG1:
+//    sparse/spmv/arch35/spmv_kernel.cpp:579-668).
+//  * Block ids are remapped so that each of the 8 XCDs processes one
+//    contiguous eighth of the matrix (x neighbourhoods stay in one L2).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "aclsparse_internal.h"
+
+namespace aclsp {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kChunk = static_cast<int>(kChunkNnz);   // 2048 product slots
+constexpr int kIpt = kChunk / kThreads;               // 8 items per lane in the scan
+constexpr int kMaxRows = static_cast<int>(kMaxItemsPerBlock);
+constexpr int kXcds = 8;
+constexpr int kPadded = kChunk + kChunk / kIpt;
+
+static_assert(kChunk % (4 * kThreads) == 0, "chunk must be a multiple of one 16-byte load per lane");
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned short v4u16 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int Pad(int q) { return q + (q >> 3); }
+
+// ------------------------------ numeric types -------------------------------
+
+struct C64 {
+    float re, im;
+};
+
+__device__ __forceinline__ C64 operator+(C64 a, C64 b) { return {a.re + b.re, a.im + b.im}; }
+__device__ __forceinline__ C64 operator*(C64 a, C64 b) { return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re}; }
+
+template <AccKind A> struct AccOf;
+template <> struct AccOf<AccKind::F32> { using T = float; };
+template <> struct AccOf<AccKind::I64> { using T = long long; };
+template <> struct AccOf<AccKind::C64> { using T = C64; };
+
+template <ValKind V> struct ValOf;
+template <> struct ValOf<ValKind::F32> { using T = float; };
+template <> struct ValOf<ValKind::F16> { using T = uint16_t; };
+template <> struct ValOf<ValKind::BF16> { using T = uint16_t; };
+template <> struct ValOf<ValKind::I8> { using T = int8_t; };
+template <> struct ValOf<ValKind::C64> { using T = C64; };
+
+template <OutKind O> struct OutOf;
+template <> struct OutOf<OutKind::F32> { using T = float; };
+template <> struct OutOf<OutKind::F16> { using T = uint16_t; };
+template <> struct OutOf<OutKind::BF16> { using T = uint16_t; };
+template <> struct OutOf<OutKind::I32> { using T = int32_t; };
+template <> struct OutOf<OutKind::C64> { using T = C64; };
+
+template <typename T> __device__ __forceinline__ T Zero() { return T{}; }
+__device__ __forceinline__ bool IsZero(float v) { return v == 0.0f; }
+__device__ __forceinline__ bool IsZero(long long v) { return v == 0; }
+__device__ __forceinline__ bool IsZero(C64 v) { return v.re == 0.0f && v.im == 0.0f; }
+
+__device__ __forceinline__ float HalfToFloat(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ float Bf16ToFloat(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// IEEE binary32 -> binary16, round to nearest, ties to even (written from
+// the IEEE 754 definition; NaN stays a quiet NaN, overflow goes to inf).
+__device__ __forceinline__ uint16_t FloatToHalfRne(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 16) & 0x8000U;
+    const uint32_t a = u & 0x7FFFFFFFU;
+    if (a >= 0x7F800000U) {
+        return static_cast<uint16_t>(sign | 0x7C00U | (a > 0x7F800000U ? (0x0200U | ((a >> 13) & 0x3FFU)) : 0U));
+    }
+    if (a >= 0x477FF000U) return static_cast<uint16_t>(sign | 0x7C00U);  // >= 65520 rounds to inf
+    if (a < 0x38800000U) {                                                // below 2^-14: subnormal half
+        if (a < 0x33000000U) return static_cast<uint16_t>(sign);          // below 2^-25
+        const uint32_t e = a >> 23;
+        const uint32_t m = (a & 0x7FFFFFU) | 0x800000U;
+        const uint32_t shift = 126U - e;  // value in units of 2^-24 is m >> shift
+        uint32_t r = m >> shift;
+        const uint32_t rem = m & ((1U << shift) - 1U);
+        const uint32_t half = 1U << (shift - 1U);
+        if (rem > half || (rem == half && (r & 1U))) ++r;
+        return static_cast<uint16_t>(sign | r);
+    }
+    uint32_t hb = (a >> 13) - (112U << 10);
+    const uint32_t rem = a & 0x1FFFU;
+    if (rem > 0x1000U || (rem == 0x1000U && (hb & 1U))) ++hb;
+    return static_cast<uint16_t>(sign | hb);
+}
+
+// binary32 -> bfloat16, round to nearest even; NaN stays NaN.
+__device__ __forceinline__ uint16_t FloatToBf16Rne(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000U) == 0x7F800000U && (u & 0x7FFFFFU) != 0U) {
+        return static_cast<uint16_t>((u >> 16) | 0x0040U);
+    }
+    return static_cast<uint16_t>((u + 0x7FFFU + ((u >> 16) & 1U)) >> 16);
+}
+
+template <ValKind V, AccKind A>
+__device__ __forceinline__ typename AccOf<A>::T ToAcc(typename ValOf<V>::T v)
+{
+    if constexpr (V == ValKind::F32) {
+        if constexpr (A == AccKind::C64) return C64{v, 0.0f};
+        else return v;
+    } else if constexpr (V == ValKind::F16) {
+        return HalfToFloat(v);
+    } else if constexpr (V == ValKind::BF16) {
+        return Bf16ToFloat(v);
+    } else if constexpr (V == ValKind::I8) {
+        if constexpr (A == AccKind::I64) return static_cast<long long>(v);
+        else return static_cast<float>(v);
+    } else {
+        return v;
+    }
+}
+
+template <OutKind O, AccKind A>
+__device__ __forceinline__ typename AccOf<A>::T OutToAcc(typename OutOf<O>::T v)
+{
+    if constexpr (O == OutKind::F16) return HalfToFloat(v);
+    else if constexpr (O == OutKind::BF16) return Bf16ToFloat(v);
+    else if constexpr (O == OutKind::I32) return static_cast<long long>(v);
+    else return v;
+}
+
+// INT8 products accumulate exactly in int64; the output saturates to int32
+// while keeping cancellation between alpha*sum and beta*y
+// (sparse/spmv/arch35/spmv_kernel.cpp:341-376).
+__device__ __forceinline__ long long SaturateI32(long long v)
+{
+    return v > 2147483647LL ? 2147483647LL : v < -2147483648LL ? -2147483648LL : v;
+}
+
+__device__ __forceinline__ long long ScaledI64(long long sum, long long alpha, long long beta, long long oldY)
+{
+    const long long betaTerm = beta * oldY;
+    if (alpha == 0) return SaturateI32(betaTerm);
+    const long long mag = sum < 0 ? -sum : sum;
+    const long long scale = alpha < 0 ? -alpha : alpha;
+    const bool negative = (sum < 0) != (alpha < 0);
+    if (mag > 9223372036854775807LL / scale) return negative ? -2147483648LL : 2147483647LL;
+    const long long prod = negative ? -(mag * scale) : mag * scale;
+    if (prod > 2147483647LL - betaTerm) return 2147483647LL;
+    if (prod < -2147483648LL - betaTerm) return -2147483648LL;
+    return prod + betaTerm;
+}
+
+template <OutKind O, AccKind A>
+__device__ __forceinline__ typename OutOf<O>::T FromAcc(typename AccOf<A>::T v)
+{
+    if constexpr (O == OutKind::F16) return FloatToHalfRne(v);
+    else if constexpr (O == OutKind::BF16) return FloatToBf16Rne(v);
+    else if constexpr (O == OutKind::I32) return static_cast<int32_t>(SaturateI32(v));
+    else return v;
+}
+
+// ------------------------------- scalars ------------------------------------
+
+struct Scalars {
+    int32_t device;
+    float alpha_re, alpha_im, beta_re, beta_im;
+    int32_t alpha_i, beta_i;
+    const void* alpha_ptr;
+    const void* beta_ptr;
+};
+
+template <AccKind A>
+__device__ __forceinline__ void LoadScalars(const Scalars& s, typename AccOf<A>::T& alpha,
+                                            typename AccOf<A>::T& beta)
+{
+    if constexpr (A == AccKind::I64) {
+        alpha = s.device ? *static_cast<const int32_t*>(s.alpha_ptr) : s.alpha_i;
+        beta = s.device ? *static_cast<const int32_t*>(s.beta_ptr) : s.beta_i;
+    } else if constexpr (A == AccKind::C64) {
+        if (s.device) {
+            const float* a = static_cast<const float*>(s.alpha_ptr);
+            const float* b = static_cast<const float*>(s.beta_ptr);
+            alpha = C64{a[0], a[1]};
+            beta = C64{b[0], b[1]};
+        } else {
+            alpha = C64{s.alpha_re, s.alpha_im};
+            beta = C64{s.beta_re, s.beta_im};
+        }
+    } else {
+        alpha = s.device ? *static_cast<const float*>(s.alpha_ptr) : s.alpha_re;
+        beta = s.device ? *static_cast<const float*>(s.beta_ptr) : s.beta_re;
+    }
+}
+
+// y = alpha*sum + beta*y; y is not read when beta == 0
+// (sparse/spmv/arch35/spmv_kernel.cpp:341-345,544-552).
+template <OutKind O, AccKind A>
+__device__ __forceinline__ void StoreRow(typename OutOf<O>::T* y, int64_t idx, typename AccOf<A>::T sum,
+                                         typename AccOf<A>::T alpha, typename AccOf<A>::T beta, bool betaNz)
+{
+    using Acc = typename AccOf<A>::T;
+    const Acc oldY = betaNz ? OutToAcc<O, A>(y[idx]) : Zero<Acc>();
+    Acc r;
+    if constexpr (A == AccKind::I64) {
+        r = ScaledI64(sum, alpha, beta, oldY);
+    } else {
+        r = betaNz ? alpha * sum + beta * oldY : alpha * sum;
+    }
+    y[idx] = FromAcc<O, A>(r);
+}
+
+// ------------------------------ shuffles ------------------------------------
+
+__device__ __forceinline__ float ShflUp(float v, int d) { return __shfl_up(v, d, kWave); }
+__device__ __forceinline__ long long ShflUp(long long v, int d) { return __shfl_up(v, d, kWave); }
+__device__ __forceinline__ C64 ShflUp(C64 v, int d) { return C64{__shfl_up(v.re, d, kWave), __shfl_up(v.im, d, kWave)}; }
+
+// ------------------------------ block mapping -------------------------------
+
+// Hardware hands consecutive workgroup ids to the 8 XCDs round-robin.  Remap
+// so that XCD k processes the contiguous block range [k*per, (k+1)*per).
+__device__ __forceinline__ int64_t XcdBlock()
+{
+    const int64_t per = gridDim.x / kXcds;
+    return static_cast<int64_t>(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+}
+
+// ------------------------------ kernel params -------------------------------
+
+struct RowBlockParams {
+    const void* rp;          // normalised row offsets (RowT), rows+1
+    const int32_t* blocks;   // num_blocks+1 block start rows
+    const int32_t* col;
+    int64_t col_stride;
+    const void* val;
+    int64_t val_stride;
+    const void* x;
+    int64_t x_stride;
+    void* y;                 // N: y; T: y (float/complex) or accumulator
+    int64_t y_stride;
+    int64_t rows, cols, nnz;
+    int64_t num_blocks;
+    int32_t base;
+    int32_t conj;
+    Scalars s;
+};
+
+// Loads the block's row offsets relative to its first non-zero into LDS.
+template <typename RowT>
+__device__ __forceinline__ int LoadBlockRows(const RowBlockParams& p, int64_t b, int32_t* sRp, int64_t& r0,
+                                             int64_t& k0)
+{
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    r0 = p.blocks[b];
+    int64_t n = static_cast<int64_t>(p.blocks[b + 1]) - r0;
+    n = n < 0 ? 0 : n > kMaxRows ? kMaxRows : n;
+    const int nr = static_cast<int>(n);
+    k0 = static_cast<int64_t>(rp[r0]);
+    for (int i = threadIdx.x; i <= nr; i += kThreads) {
+        int64_t v = static_cast<int64_t>(rp[r0 + i]) - k0;
+        v = v < 0 ? 0 : v > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : v;
+        sRp[i] = static_cast<int32_t>(v);
+    }
+    return nr;
+}
+
+// First index i in [lo, hi) with key(i) >= target (keys non-decreasing).
+__device__ __forceinline__ int LowerBound(const int32_t* a, int lo, int hi, int32_t target)
+{
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (a[mid] < target) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Product a_p * x[col_p] (zero when p is outside [lo, hi) or col is out of range).
+template <ValKind V, AccKind A>
+__device__ __forceinline__ typename AccOf<A>::T Product(typename ValOf<V>::T a, int32_t rawCol,
+                                                        const typename ValOf<V>::T* x, int64_t xStride,
+                                                        int32_t base, int64_t cols, bool valid)
+{
+    using Acc = typename AccOf<A>::T;
+    const int64_t c = static_cast<int64_t>(rawCol) - base;
+    if (!valid || c < 0 || c >= cols) return Zero<Acc>();
+    return ToAcc<V, A>(a) * ToAcc<V, A>(x[c * xStride]);
+}
+
+// 16-byte (4 element) non-temporal loads of col_ind and values at an aligned
+// non-zero index g (g % 4 == 0, g + 4 <= nnz).
+template <ValKind V>
+__device__ __forceinline__ void Load4(const int32_t* col, const typename ValOf<V>::T* val, int64_t g, int32_t c[4],
+                                      typename ValOf<V>::T v[4])
+{
+    const v4i cc = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(col + g));
+    c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
+    if constexpr (V == ValKind::F32) {
+        const v4f vv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(val + g));
+        v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
+    } else {
+        static_assert(V == ValKind::F16 || V == ValKind::BF16, "vector path is for 32/16-bit values");
+        const v4u16 vv = __builtin_nontemporal_load(reinterpret_cast<const v4u16*>(val + g));
+        v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
+    }
+}
+
+// ------------------------- non-transpose row blocks -------------------------
+
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kVec>
+__global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    using OutT = typename OutOf<O>::T;
+
+    __shared__ int32_t sRp[kMaxRows + 1];
+    __shared__ Acc sVal[kPadded];
+    __shared__ uint32_t sFlagWords[kChunk / 4];
+    __shared__ Acc sCarry[kThreads];
+    __shared__ int32_t sFirst[kThreads];
+    __shared__ Acc sWaveV[kWaves];
+    __shared__ int32_t sWaveF[kWaves];
+    __shared__ Acc sChunkCarry;
+    uint8_t* sFlag = reinterpret_cast<uint8_t*>(sFlagWords);
+
+    const int64_t b = XcdBlock();
+    if (b >= p.num_blocks) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+
+    int64_t r0, k0;
+    const int nr = LoadBlockRows<RowT>(p, b, sRp, r0, k0);
+    Acc alpha, beta;
+    LoadScalars<A>(p.s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    const ValT* val = static_cast<const ValT*>(p.val);
+    const ValT* x = static_cast<const ValT*>(p.x);
+    OutT* y = static_cast<OutT*>(p.y);
+    if (tid == 0) sChunkCarry = Zero<Acc>();
+    __syncthreads();
+
+    const int32_t kspan = sRp[nr];
+    int32_t c0 = 0;
+    for (;;) {
+        const int64_t gStart = k0 + c0;
+        const int64_t a0 = kVec ? (gStart & ~static_cast<int64_t>(3)) : gStart;
+        const int32_t d = static_cast<int32_t>(k0 - a0);  // LDS slot of relative offset r is r + d
+        const int32_t lim = static_cast<int32_t>(a0 - k0) + kChunk;
+        const int32_t c1 = kspan < lim ? kspan : lim;
+        const bool last = c1 >= kspan;
+        const int64_t gEnd = k0 + c1;
+
+        for (int w = tid; w < kChunk / 4; w += kThreads) sFlagWords[w] = 0U;
+
+        // Stream col_ind / values of [gStart, gEnd) and form the products.
+        if constexpr (kVec) {
+            for (int v = tid; v < kChunk / 4; v += kThreads) {
+                const int64_t g = a0 + 4 * static_cast<int64_t>(v);
+                Acc prod[4] = {Zero<Acc>(), Zero<Acc>(), Zero<Acc>(), Zero<Acc>()};
+                if (g < gEnd) {
+                    int32_t c[4];
+                    ValT a[4];
+                    if (g + 4 <= p.nnz) {
+                        Load4<V>(p.col, val, g, c, a);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const bool in = g + e < p.nnz;
+                            c[e] = in ? p.col[g + e] : 0;
+                            a[e] = in ? val[g + e] : ValT{};
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool valid = g + e >= gStart && g + e < gEnd;
+                        prod[e] = Product<V, A>(a[e], c[e], x, 1, p.base, p.cols, valid);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sVal[Pad(4 * v + e)] = prod[e];
+            }
+        } else {
+            for (int q = tid; q < kChunk; q += kThreads) {
+                const int64_t g = a0 + q;
+                Acc prod = Zero<Acc>();
+                if (g < gEnd) {
+                    prod = Product<V, A>(val[g * p.val_stride], p.col[g * p.col_stride], x, p.x_stride, p.base,
+                                         p.cols, true);
+                }
+                sVal[Pad(q)] = prod;
+            }
+        }
+
+        __syncthreads();  // flag words are cleared before any lane sets a head
+
+        // Rows that can touch this chunk.
+        int lo = 0, hi = nr;
+        if (!(c0 == 0 && last)) {
+            lo = LowerBound(sRp + 1, 0, nr, c0);
+            if (!last) hi = LowerBound(sRp, lo, nr, c1);
+        }
+        // Segment heads: the first non-zero of every non-empty row in the chunk.
+        for (int i = lo + tid; i < hi; i += kThreads) {
+            const int32_t s = sRp[i], e = sRp[i + 1];
+            if (e > s && s >= c0 && s < c1) sFlag[s + d] = 1;
+        }
+        __syncthreads();
+
+        // Per-lane segmented inclusive scan of 8 consecutive products.
+        Acc run = Zero<Acc>();
+        int first = kIpt;
+#pragma unroll
+        for (int j = 0; j < kIpt; ++j) {
+            const int q = tid * kIpt + j;
+            if (sFlag[q]) {
+                if (first == kIpt) first = j;
+                run = Zero<Acc>();
+            }
+            run = run + sVal[Pad(q)];
+            sVal[Pad(q)] = run;
+        }
+        const int has = first < kIpt ? 1 : 0;
+
+        // Block-wide exclusive segmented scan of the lane tails.
+        Acc v = run;
+        int f = has;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const Acc vo = ShflUp(v, off);
+            const int fo = __shfl_up(f, off, kWave);
+            if (lane >= off) {
+                if (!f) v = vo + v;
+                f |= fo;
+            }
+        }
+        Acc ve = ShflUp(v, 1);
+        int fe = __shfl_up(f, 1, kWave);
+        if (lane == 0) {
+            ve = Zero<Acc>();
+            fe = 0;
+        }
+        if (lane == kWave - 1) {
+            sWaveV[wave] = v;
+            sWaveF[wave] = f;
+        }
+        __syncthreads();
+        Acc pv = sChunkCarry;
+        for (int u = 0; u < wave; ++u) {
+            if (sWaveF[u]) pv = sWaveV[u];
+            else pv = pv + sWaveV[u];
+        }
+        const Acc excl = fe ? ve : pv + ve;
+        sCarry[tid] = excl;
+        sFirst[tid] = first;
+        const Acc chunkTotal = has ? run : excl + run;  // meaningful on the last lane
+        __syncthreads();
+
+        // Finish the rows that end inside this chunk.
+        for (int i = lo + tid; i < hi; i += kThreads) {
+            const int32_t s = sRp[i], e = sRp[i + 1];
+            if (e <= s) {
+                if ((s >= c0 && s < c1) || (last && s >= c1)) {
+                    StoreRow<O, A>(y, (r0 + i) * p.y_stride, Zero<Acc>(), alpha, beta, betaNz);
+                }
+            } else if (e > c0 && e <= c1) {
+                const int q = e - 1 + d;
+                const int t = q / kIpt;
+                Acc sum = sVal[Pad(q)];
+                if ((q % kIpt) < sFirst[t]) sum = sum + sCarry[t];
+                StoreRow<O, A>(y, (r0 + i) * p.y_stride, sum, alpha, beta, betaNz);
+            }
+        }
+        if (last) break;
+        __syncthreads();
+        if (tid == kThreads - 1) sChunkCarry = chunkTotal;
+        c0 = c1;
+        __syncthreads();
+    }
+}
+
+// ------------------------------- transpose ----------------------------------
+
+// y = beta*y in place (y is not read when beta == 0); the scatter then adds
+// alpha*A^T*x on top.  Used when y's type is the accumulator type.
+template <OutKind O, AccKind A>
+__global__ __launch_bounds__(kThreads) void ScaleKernel(typename OutOf<O>::T* y, int64_t n, int64_t stride,
+                                                         Scalars s)
+{
+    using Acc = typename AccOf<A>::T;
+    Acc alpha, beta;
+    LoadScalars<A>(s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; j < n;
+         j += static_cast<int64_t>(gridDim.x) * kThreads) {
+        y[j * stride] = betaNz ? beta * y[j * stride] : Zero<Acc>();
+    }
+}
+
+template <AccKind A>
+__global__ __launch_bounds__(kThreads) void ClearKernel(typename AccOf<A>::T* acc, int64_t n)
+{
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; j < n;
+         j += static_cast<int64_t>(gridDim.x) * kThreads) {
+        acc[j] = Zero<typename AccOf<A>::T>();
+    }
+}
+
+// y = finalize(acc): float accumulators already hold alpha*A^T*x; the int64
+// accumulator holds the unscaled sum (sparse/spmv/arch35/spmv_kernel.cpp:626-668).
+template <OutKind O, AccKind A>
+__global__ __launch_bounds__(kThreads) void FinalizeKernel(const typename AccOf<A>::T* acc,
+                                                            typename OutOf<O>::T* y, int64_t n, int64_t stride,
+                                                            Scalars s)
+{
+    using Acc = typename AccOf<A>::T;
+    Acc alpha, beta;
+    LoadScalars<A>(s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; j < n;
+         j += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const Acc oldY = betaNz ? OutToAcc<O, A>(y[j * stride]) : Zero<Acc>();
+        Acc r;
+        if constexpr (A == AccKind::I64) r = ScaledI64(acc[j], alpha, beta, oldY);
+        else r = betaNz ? acc[j] + beta * oldY : acc[j];
+        y[j * stride] = FromAcc<O, A>(r);
+    }
+}
+
+__device__ __forceinline__ void AtomicAddAcc(float* dst, float v) { unsafeAtomicAdd(dst, v); }
+__device__ __forceinline__ void AtomicAddAcc(long long* dst, long long v)
+{
+    atomicAdd(reinterpret_cast<unsigned long long*>(dst), static_cast<unsigned long long>(v));
+}
+__device__ __forceinline__ void AtomicAddAcc(C64* dst, C64 v)
+{
+    unsafeAtomicAdd(&dst->re, v.re);
+    unsafeAtomicAdd(&dst->im, v.im);
+}
+
+template <ValKind V, AccKind A>
+__device__ __forceinline__ typename AccOf<A>::T MaybeConj(typename AccOf<A>::T v, int conj)
+{
+    if constexpr (A == AccKind::C64) return conj ? C64{v.re, -v.im} : v;
+    else return v;
+}
+
+// Scatter of one row block: every non-zero (i, j) adds alpha*conj?(a_ij)*x_i
+// (float/complex) or a_ij*x_i (int64) to out[j*stride].
+template <typename RowT, ValKind V, AccKind A>
+__global__ __launch_bounds__(kThreads) void SpmvScatterKernel(RowBlockParams p)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    __shared__ int32_t sRp[kMaxRows + 1];
+    const int64_t b = XcdBlock();
+    if (b >= p.num_blocks) return;
+    int64_t r0, k0;
+    const int nr = LoadBlockRows<RowT>(p, b, sRp, r0, k0);
+    Acc alpha, beta;
+    LoadScalars<A>(p.s, alpha, beta);
+    const ValT* val = static_cast<const ValT*>(p.val);
+    const ValT* x = static_cast<const ValT*>(p.x);
+    Acc* out = static_cast<Acc*>(p.y);
+    __syncthreads();
+    const int32_t kspan = sRp[nr];
+    for (int32_t r = threadIdx.x; r < kspan; r += kThreads) {
+        // Row of relative non-zero r: last i with sRp[i] <= r.
+        int lo = 0, hi = nr;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (sRp[mid] <= r) lo = mid;
+            else hi = mid - 1;
+        }
+        const int64_t row = r0 + lo;
+        const int64_t g = k0 + r;
+        const int64_t c = static_cast<int64_t>(p.col[g * p.col_stride]) - p.base;
+        if (c < 0 || c >= p.cols) continue;
+        const Acc a = MaybeConj<V, A>(ToAcc<V, A>(val[g * p.val_stride]), p.conj);
+        Acc contrib = a * ToAcc<V, A>(x[row * p.x_stride]);
+        if constexpr (A != AccKind::I64) contrib = alpha * contrib;
+        AtomicAddAcc(out + c * p.y_stride, contrib);
+    }
+}
+
+// ------------------------------- preprocess ---------------------------------
+
+struct PrepParams {
+    const void* rp;        // original row offsets
+    int64_t stride;
+    int64_t base;
+    int64_t rows, cols, nnz;
+    void* norm;            // normalised row offsets (RowT)
+    int32_t* blocks;
+    int64_t num_blocks;
+    int64_t items;         // T
+    SpmvWsHeader* header;
+    SpmvWsHeader header_value;
+};
+
+template <typename SrcT>
+__device__ __forceinline__ int64_t NormRow(const PrepParams& p, int64_t i)
+{
+    int64_t v = static_cast<int64_t>(static_cast<const SrcT*>(p.rp)[i * p.stride]) - p.base;
+    return v < 0 ? 0 : v > p.nnz ? p.nnz : v;
+}
+
+template <typename SrcT>
+__global__ __launch_bounds__(kThreads) void SpmvPreprocessKernel(PrepParams p)
+{
+    const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+    if (i <= p.rows) static_cast<SrcT*>(p.norm)[i] = static_cast<SrcT>(NormRow<SrcT>(p, i));
+    if (i <= p.num_blocks) {
+        int32_t start;
+        if (i == p.num_blocks) {
+            start = static_cast<int32_t>(p.rows);
+        } else {
+            // First row r in [0, rows] whose start coordinate r + offset(r) >= i*T.
+            const int64_t diag = i * p.items;
+            int64_t lo = 0, hi = p.rows;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) >> 1;
+                if (mid + NormRow<SrcT>(p, mid) >= diag) hi = mid;
+                else lo = mid + 1;
+            }
+            start = static_cast<int32_t>(lo);
+        }
+        p.blocks[i] = start;
+    }
+    if (i == 0) *p.header = p.header_value;
+}
+
+int GridFor(int64_t n)
+{
+    int64_t g = (n + kThreads - 1) / kThreads;
+    if (g < 1) g = 1;
+    if (g > 65536) g = 65536;
+    return static_cast<int>(g);
+}
+
+template <typename T>
+T* At(void* ws, size_t off) { return reinterpret_cast<T*>(static_cast<uint8_t*>(ws) + off); }
+
+RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
+{
+    RowBlockParams p{};
+    p.rp = At<void>(l.ws, l.layout.rowptr_offset);
+    p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
+    p.col = l.col;
+    p.col_stride = l.col_stride;
+    p.val = l.val;
+    p.val_stride = l.val_stride;
+    p.x = l.x;
+    p.x_stride = l.x_stride;
+    p.y = l.y;
+    p.y_stride = l.y_stride;
+    p.rows = l.rows;
+    p.cols = l.cols;
+    p.nnz = l.nnz;
+    p.num_blocks = l.layout.num_blocks;
+    p.base = l.base;
+    p.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
+    p.s.device = l.device_scalars;
+    p.s.alpha_re = l.alpha_re;
+    p.s.alpha_im = l.alpha_im;
+    p.s.beta_re = l.beta_re;
+    p.s.beta_im = l.beta_im;
+    p.s.alpha_i = l.alpha_i;
+    p.s.beta_i = l.beta_i;
+    p.s.alpha_ptr = l.alpha_ptr;
+    p.s.beta_ptr = l.beta_ptr;
+    return p;
+}
+
+unsigned RowBlockGrid(int64_t numBlocks)
+{
+    const int64_t per = (numBlocks + kXcds - 1) / kXcds;
+    return static_cast<unsigned>(per * kXcds);
+}
+
+bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
+{
+    const RowBlockParams p = MakeRowBlockParams(l);
+    const unsigned grid = RowBlockGrid(p.num_blocks);
+    constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
+    const bool vec = kCanVec && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && Aligned16(l.col) &&
+                     Aligned16(l.val);
+    if constexpr (kCanVec) {
+        if (vec) {
+            hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+            return 0;
+        }
+    }
+    hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+    return 0;
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
+{
+    using Acc = typename AccOf<A>::T;
+    RowBlockParams p = MakeRowBlockParams(l);
+    const int64_t n = l.cols;
+    // y already has the accumulator type: scale it by beta and scatter into it.
+    constexpr bool kDirect = (O == OutKind::F32 && A == AccKind::F32) || (O == OutKind::C64 && A == AccKind::C64);
+    Acc* acc = At<Acc>(l.ws, l.layout.acc_offset);
+    if constexpr (kDirect) {
+        hipLaunchKernelGGL((ScaleKernel<O, A>), dim3(GridFor(n)), dim3(kThreads), 0, stream,
+                           static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, p.s);
+    } else {
+        hipLaunchKernelGGL((ClearKernel<A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc, n);
+        p.y = acc;
+        p.y_stride = 1;
+    }
+    if (l.rows > 0 && l.nnz > 0) {
+        hipLaunchKernelGGL((SpmvScatterKernel<RowT, V, A>), dim3(RowBlockGrid(p.num_blocks)), dim3(kThreads), 0,
+                           stream, p);
+    }
+    if constexpr (!kDirect) {
+        hipLaunchKernelGGL((FinalizeKernel<O, A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc,
+                           static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, p.s);
+    }
+    return 0;
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+int LaunchTyped(const SpmvLaunch& l, hipStream_t stream)
+{
+    if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE) return LaunchRowBlock<RowT, V, O, A>(l, stream);
+    return LaunchTranspose<RowT, V, O, A>(l, stream);
+}
+
+template <typename RowT>
+int DispatchTypes(const SpmvLaunch& l, hipStream_t s)
+{
+    using VK = ValKind;
+    using OK = OutKind;
+    using AK = AccKind;
+    if (l.acc_kind == AK::I64) return LaunchTyped<RowT, VK::I8, OK::I32, AK::I64>(l, s);
+    if (l.acc_kind == AK::C64) {
+        if (l.val_kind == VK::F32) return LaunchTyped<RowT, VK::F32, OK::C64, AK::C64>(l, s);
+        return LaunchTyped<RowT, VK::C64, OK::C64, AK::C64>(l, s);
+    }
+    switch (l.val_kind) {
+        case VK::I8: return LaunchTyped<RowT, VK::I8, OK::F32, AK::F32>(l, s);
+        case VK::F16:
+            return l.out_kind == OK::F16 ? LaunchTyped<RowT, VK::F16, OK::F16, AK::F32>(l, s)
+                                         : LaunchTyped<RowT, VK::F16, OK::F32, AK::F32>(l, s);
+        case VK::BF16:
+            return l.out_kind == OK::BF16 ? LaunchTyped<RowT, VK::BF16, OK::BF16, AK::F32>(l, s)
+                                          : LaunchTyped<RowT, VK::BF16, OK::F32, AK::F32>(l, s);
+        case VK::F32: return LaunchTyped<RowT, VK::F32, OK::F32, AK::F32>(l, s);
+        default: return 1;
+    }
+}
+
+}  // namespace
+
+int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
+{
+    if (l.rows <= 0) return 0;
+    PrepParams p{};
+    p.rp = l.row_ptr;
+    p.stride = l.row_stride;
+    p.base = l.base;
+    p.rows = l.rows;
+    p.cols = l.cols;
+    p.nnz = l.nnz;
+    p.norm = At<void>(l.ws, l.layout.rowptr_offset);
+    p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
+    p.num_blocks = l.layout.num_blocks;
+    p.items = l.layout.items_per_block;
+    p.header = At<SpmvWsHeader>(l.ws, 0);
+    SpmvWsHeader& h = p.header_value;
+    h.magic = kWsMagic;
+    h.version = 1;
+    h.rows = static_cast<uint64_t>(l.rows);
+    h.cols = static_cast<uint64_t>(l.cols);
+    h.nnz = static_cast<uint64_t>(l.nnz);
+    h.items_per_block = static_cast<uint64_t>(l.layout.items_per_block);
+    h.num_blocks = static_cast<uint64_t>(l.layout.num_blocks);
+    h.rowptr_offset = l.layout.rowptr_offset;
+    h.blocks_offset = l.layout.blocks_offset;
+    h.acc_offset = l.layout.acc_offset;
+    h.rowptr_bytes = l.layout.rowptr_bytes;
+    h.index_base = static_cast<uint32_t>(l.base);
+    h.op = static_cast<uint32_t>(l.op);
+    const int64_t n = (l.rows > p.num_blocks ? l.rows : p.num_blocks) + 1;
+    const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (l.rowptr64) {
+        hipLaunchKernelGGL((SpmvPreprocessKernel<int64_t>), dim3(grid), dim3(kThreads), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
+    }
+    return 0;
+}
+
+int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= 0) return 0;
+    return l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
+}
+
+}  // namespace aclsp

@@ -1,0 +1,296 @@
+"""GPU parity of aclsparseSpMV (through the C ABI) against the CPU oracle and the reference KATs."""
+import ctypes
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close, host_bits, oracle_result
+from ops_sparse import _lib, spmv_npu
+from ops_sparse._lib import DataType, IndexBase, Operation, PointerMode, SpMVAlg, Status
+from ops_sparse.spmv import CsrDescr, CsrSpMV, DnVecDescr, Handle, HostScalar
+from ops_sparse import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+ALG = {"DEFAULT": SpMVAlg.DEFAULT, "CSR_ALG1": SpMVAlg.CSR_ALG1, "CSR_ALG2": SpMVAlg.CSR_ALG2}
+OP = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}
+
+
+def run_workload(w, dev, alg=SpMVAlg.DEFAULT, preprocess=True):
+    w = w.to(dev)
+    y = w.y0.to(w.out_dtype).clone()
+    op = OP[w.trans]
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op, alg=alg)
+    if preprocess:
+        plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    return w, y, plan
+
+
+def t(data, dtype, dev):
+    return torch.tensor(data, dtype=dtype, device=dev)
+
+
+# --------------------------- reference KATs ---------------------------------
+
+@pytest.mark.parametrize("case", KATS["csv_cases"], ids=lambda c: c["name"])
+def test_reference_csv_three_stage_and_reexecute(case, dev):
+    rp = t(case["row_ptr"], torch.int32, dev)
+    ci = t(case["col_ind"], torch.int32, dev)
+    va = t(case["values"], torch.float32, dev)
+    x = t(case["x"], torch.float32, dev)
+    y = t(case["y"], torch.float32, dev)
+    op = OP[case["op"]]
+    plan = CsrSpMV(case["rows"], case["cols"], rp, ci, va, x, y, case["alpha"], case["beta"], op=op,
+                   base=case["base"], alg=ALG[case["alg"]])
+    assert plan.buffer_size >= 64 and plan.buffer_size % 64 == 0
+    if case["pointer_mode"] == "DEVICE":
+        plan.handle.set_pointer_mode(PointerMode.DEVICE)
+        da = t([case["alpha"]], torch.float32, dev)
+        db = t([case["beta"]], torch.float32, dev)
+        plan.alpha = type("P", (), {"ptr": ctypes.c_void_p(da.data_ptr())})()
+        plan.beta = type("P", (), {"ptr": ctypes.c_void_p(db.data_ptr())})()
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy(), case["expected_first"], atol=case["tolerance"], rtol=0)
+    plan.run()  # same pattern and workspace: still valid for a second call
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy(), case["expected_second"], atol=case["tolerance"], rtol=0)
+
+
+def test_reference_zero_nnz_beta_and_misaligned_workspace(dev):
+    k = KATS["zero_nnz_beta"]
+    rp = t(k["row_ptr"], torch.int32, dev)
+    x = t(k["x"], torch.float32, dev)
+    y = t(k["y"], torch.float32, dev)
+    empty_i = torch.empty(0, dtype=torch.int32, device=dev)
+    empty_f = torch.empty(0, dtype=torch.float32, device=dev)
+    plan = CsrSpMV(k["rows"], k["cols"], rp, empty_i, empty_f, x, y, k["alpha"], k["beta"])
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), k["expected"])
+    lib = _lib.lib()
+    st = lib.aclsparseSpMV(plan.handle.h, 0, plan.alpha.ptr, plan.mat.d, plan.x.d, plan.beta.ptr, plan.y.d,
+                           int(DataType.FLOAT), 0, ctypes.c_void_p(plan.workspace.data_ptr() + 1))
+    assert st == Status.INVALID_VALUE
+
+
+def test_reference_repeated_coordinates(dev):
+    k = KATS["repeated_coordinates"]
+    y = t(k["y"], torch.float32, dev)
+    plan = CsrSpMV(1, 1, t(k["row_ptr"], torch.int32, dev), t(k["col_ind"], torch.int32, dev),
+                   t(k["values"], torch.float32, dev), t(k["x"], torch.float32, dev), y, k["alpha"], k["beta"],
+                   alg=ALG[k["alg"]])
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    assert y.item() == k["expected"][0]
+
+
+@pytest.mark.parametrize("op", ["N", "T", "H"])
+@pytest.mark.parametrize("alg", ["DEFAULT", "CSR_ALG2"])
+@pytest.mark.parametrize("rows", [2, 4096])
+def test_reference_int8_saturation(op, alg, rows, dev):
+    k = KATS["int8_saturation"]
+    rp = [0, 1] + [2] * (rows - 1)
+    transpose = op != "N"
+    x = torch.full((rows if transpose else 2,), 127, dtype=torch.int8, device=dev)
+    y = torch.zeros(2 if transpose else rows, dtype=torch.int32, device=dev)
+    plan = CsrSpMV(rows, 2, t(rp, torch.int32, dev), t(k["col_ind"], torch.int32, dev),
+                   t(k["values"], torch.int8, dev), x, y, k["alpha"], k["beta"], op=OP[op], alg=ALG[alg])
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert list(got[:2]) == k["expected_head"]
+    assert np.all(got[2:] == 0)
+
+
+def test_reference_fp16_round_half_even(dev):
+    k = KATS["fp16_halfway"]
+    h = lambda bits: torch.tensor(np.array(bits, dtype=np.uint16).view(np.int16), device=dev).view(torch.float16)
+    y = h(k["y_bits"]).clone()
+    plan = CsrSpMV(2, 2, t(k["row_ptr"], torch.int32, dev), t(k["col_ind"], torch.int32, dev), h(k["values_bits"]),
+                   h(k["x_bits"]), y, k["alpha"], k["beta"])
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    assert list(host_bits(y)) == k["expected_bits"]
+
+
+def test_reference_complex_conjugate_transpose(dev):
+    k = KATS["complex_conj_transpose"]
+    c = lambda v: torch.tensor([complex(a, b) for a, b in v], dtype=torch.complex64, device=dev)
+    y = c(k["y"])
+    plan = CsrSpMV(2, 2, t(k["row_ptr"], torch.int32, dev), t(k["col_ind"], torch.int32, dev), c(k["values"]),
+                   c(k["x"]), y, complex(*k["alpha"]), complex(*k["beta"]), op=Operation.CONJUGATE_TRANSPOSE,
+                   alg=ALG[k["alg"]])
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy(), [complex(a, b) for a, b in k["expected"]], atol=1e-6)
+
+
+def _strided_fixture(rows, is_sorted):
+    rp, ci, va = [1], [], []
+    for r in range(rows):
+        if r % 2 == 0:
+            ci += [1, 3] if is_sorted else [3, 1]
+            va += [2.0, 3.0] if is_sorted else [3.0, 2.0]
+        else:
+            ci.append(2)
+            va.append(4.0)
+        rp.append(len(va) + 1)
+    return rp, ci, va
+
+
+def _with_stride(vals, stride, sentinel):
+    out = [sentinel] * (len(vals) * stride)
+    out[::stride] = vals
+    return out
+
+
+@pytest.mark.parametrize("case", KATS["strided"]["cases"], ids=lambda c: f"{c['op']}{c['rows']}{c['alg']}{c['sorted']}")
+def test_reference_strided_storage_preserves_padding(case, dev):
+    k = KATS["strided"]
+    s = k["strides"]
+    rows, op = case["rows"], case["op"]
+    transpose = op != "N"
+    rp, ci, va = _strided_fixture(rows, case["sorted"])
+    xl = [1.0] * rows if transpose else [1.0, 2.0, 3.0]
+    out_len = 3 if transpose else rows
+    sent = k["sentinel"]
+    d_rp = t(_with_stride(rp, s["row"], k["index_sentinel"]), torch.int32, dev)
+    d_ci = t(_with_stride(ci, s["col"], k["index_sentinel"]), torch.int32, dev)
+    d_va = t(_with_stride(va, s["val"], sent), torch.float32, dev)
+    d_x = t(_with_stride(xl, s["x"], sent), torch.float32, dev)
+    y_init = _with_stride([k["y_init"]] * out_len, s["y"], sent)
+    d_y = t(y_init, torch.float32, dev)
+    lib = _lib.lib()
+    h = Handle(torch.cuda.current_stream().cuda_stream or _lib.HIP_NULL_STREAM)
+    mat = CsrDescr(rows, 3, d_rp, d_ci, d_va, base=1)
+    mat.set_strides(s["row"], s["col"], s["val"])
+    vx = DnVecDescr(len(xl), d_x)
+    vx.set_stride(s["x"])
+    vy = DnVecDescr(out_len, d_y)
+    vy.set_stride(s["y"])
+    a, b = HostScalar(k["alpha"], DataType.FLOAT), HostScalar(k["beta"], DataType.FLOAT)
+    size = ctypes.c_size_t()
+    opv, algv = int(OP[op]), int(ALG[case["alg"]])
+    assert lib.aclsparseSpMVGetBufferSize(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, algv,
+                                          ctypes.byref(size)) == 0
+    ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
+    even, odd = (rows + 1) // 2, rows // 2
+    for preprocess in (False, True):
+        d_y.copy_(t(y_init, torch.float32, dev))
+        if preprocess:
+            assert lib.aclsparseSpMVPreprocess(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, algv,
+                                               ctypes.c_void_p(ws.data_ptr())) == 0
+        assert lib.aclsparseSpMV(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, algv,
+                                 ctypes.c_void_p(ws.data_ptr())) == 0
+        torch.cuda.synchronize()
+        got = d_y.cpu().numpy()
+        texp = [4.0 * even + 15.0, 8.0 * odd + 15.0, 6.0 * even + 15.0]
+        for i, v in enumerate(got):
+            logical = i // s["y"]
+            if i % s["y"]:
+                exp = sent
+            elif transpose:
+                exp = texp[logical]
+            else:
+                exp = k["expected_n"]["even_row"] if logical % 2 == 0 else k["expected_n"]["odd_row"]
+            assert v == pytest.approx(exp, rel=1e-6), (i, v, exp, preprocess)
+
+
+# --------------------------- workload parity --------------------------------
+
+@pytest.mark.parametrize("name,scale", [("c1", 1), ("c2", 64), ("c3", 64), ("c5", 64)])
+def test_config_parity_scaled(name, scale, dev):
+    w, y, _ = run_workload(wl.config(name, "cpu", scale), dev)
+    print(f"{w.name}: rows={w.rows} nnz={w.nnz} err={assert_close(w, y):.3e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_config4_lowp_parity_scaled(dtype, dev):
+    w, y, _ = run_workload(wl.config("c4", "cpu", 256, dtype=dtype), dev)
+    assert_close(w, y)
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c5"])
+def test_config_parity_full_size(name, dev):
+    w = wl.config(name, dev, 1)
+    w, y, _ = run_workload(w, dev)
+    print(f"{w.name}: rows={w.rows} nnz={w.nnz} err={assert_close(w.to('cpu'), y):.3e}")
+
+
+def test_partition_metadata_bit_exact(dev):
+    w = wl.config("c3", "cpu", 64)
+    w, y, plan = run_workload(w, dev)
+    ws = plan.workspace.cpu().numpy()
+    hdr = np.frombuffer(ws[:192].tobytes(), dtype=np.uint64)
+    nb, rp_off, bl_off = int(hdr[5]), int(hdr[6]), int(hdr[7])
+    norm_ref, blocks_ref = oracle.partition(w.row_ptr.cpu().numpy(), w.nnz)
+    assert nb == oracle.num_blocks(w.rows, w.nnz) and int(hdr[4]) == oracle.items_per_block(w.rows, w.nnz)
+    norm = np.frombuffer(ws[rp_off:rp_off + 4 * (w.rows + 1)].tobytes(), dtype=np.int32)
+    blocks = np.frombuffer(ws[bl_off:bl_off + 4 * (nb + 1)].tobytes(), dtype=np.int32)
+    np.testing.assert_array_equal(norm, norm_ref)
+    np.testing.assert_array_equal(blocks, blocks_ref)
+
+
+def test_beta_zero_never_reads_y(dev):
+    w = wl.config("c2", "cpu", 256)
+    w.beta = 0.0
+    w.y0 = torch.full_like(w.y0, float("nan"))
+    w2, y, _ = run_workload(w, dev)
+    w.y0 = torch.zeros_like(w.y0)
+    assert_close(w, y)
+
+
+def test_long_rows_and_empty_rows(dev):
+    # one 100k-entry row among short and empty rows: spans many LDS chunks
+    lengths = torch.tensor([3, 0, 100000, 0, 0, 7] + [1] * 5000 + [0] * 3000 + [5000], dtype=torch.int64)
+    g = torch.Generator().manual_seed(7)
+    rp, col = wl.csr_from_lengths(lengths, 200000, g, "cpu")
+    n = col.numel()
+    w = wl.Workload("long_rows", lengths.numel(), 200000, rp.to(torch.int32), col,
+                    torch.rand(n, generator=g) * 2 - 1, torch.rand(200000, generator=g) * 2 - 1,
+                    torch.rand(lengths.numel(), generator=g) * 2 - 1, 1.25, -0.75)
+    for pre in (True, False):
+        w2, y, _ = run_workload(w, dev, preprocess=pre)
+        assert_close(w, y)
+
+
+def test_int64_row_offsets_fp32(dev):
+    w = wl.config("c3", "cpu", 128)
+    w.row_ptr = w.row_ptr.to(torch.int64)
+    w2, y, _ = run_workload(w, dev)
+    assert_close(w, y)
+
+
+def test_no_preprocess_matches_preprocess(dev):
+    w = wl.config("c3", "cpu", 128)
+    _, y1, _ = run_workload(w, dev, preprocess=False)
+    _, y2, _ = run_workload(w, dev, preprocess=True)
+    assert torch.equal(y1, y2)
+
+
+def test_spmv_npu_mirror_and_mv(dev):
+    w = wl.config("c1", "cpu")
+    d = w.to(dev)
+    y = spmv_npu(d.row_ptr, d.col_ind, d.values, d.x, d.y0, w.alpha, w.beta)
+    torch.cuda.synchronize()
+    assert_close(w, y)
+    from ops_sparse import mv
+    a = torch.sparse_csr_tensor(d.row_ptr.to(torch.int64), d.col_ind.to(torch.int64), d.values,
+                                size=(w.rows, w.cols))
+    y2 = mv(a, d.x)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y)
