@@ -38,7 +38,32 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--configs", default="c1,c2,c3,c4h,c4b,c5")
+    ap.add_argument("--profile", default=None,
+                    help="profiling mode: build only this config, run --steps SpMVs and a 1 GiB copy "
+                         "(the calibration kernel for FETCH_SIZE/WRITE_SIZE), print nothing else")
     return ap.parse_args()
+
+
+def profile_mode(name, steps):
+    """Minimal launch sequence for rocprofv3: Preprocess once, ``steps`` SpMVs, one 1 GiB device copy."""
+    from ops_sparse.spmv import CsrSpMV
+    from ops_sparse._lib import Operation
+    from ops_sparse.workloads import algorithmic_bytes
+
+    dev = torch.device("cuda:0")
+    w = make(name, dev)
+    y = w.y0.to(w.out_dtype).clone()
+    op = Operation.NON_TRANSPOSE if w.trans == "N" else Operation.TRANSPOSE
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
+    plan.preprocess()
+    for _ in range(steps):
+        plan.run()
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # 1 GiB read + 1 GiB write: scales the per-dispatch counters
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": name, "workload": w.name, "algorithmic_bytes": algorithmic_bytes(w),
+                      "copy_bytes_each_way": src.numel() * 4, "steps": steps}))
 
 
 def make(name, dev):
@@ -136,6 +161,9 @@ def main():
         sys.exit(2)
     from ops_sparse.workloads import algorithmic_bytes, flops
 
+    if args.profile:
+        profile_mode(args.profile, args.steps)
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)

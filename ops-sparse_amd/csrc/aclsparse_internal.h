@@ -91,19 +91,25 @@ namespace aclsp {
 //                       Same place as the reference's normalised copy
 //                       (sparse/spmv/arch35/spmv_tiling_data.h:77-79).
 //   block_row_start     int32[num_blocks+1]: first row of each row block
+//   block_nnz_start     RowT[num_blocks+1]: normalised offset of that row
+//                       (lets a block start streaming before reading its rows)
 //   accumulator         transpose only: cols x accumulator element
 // ---------------------------------------------------------------------------
 constexpr size_t kWsAlign = 64;
 constexpr size_t kWsHeaderBytes = 192;
 constexpr uint32_t kWsMagic = 0x4D505348U;  // "HSPM"
 
-// Row-block partition parameters.  A row block holds the rows whose
-// merge-path start coordinate (row + rowOffset[row]) lies in
-// [b*T, (b+1)*T); T is chosen so that a block's non-zeros fit one LDS chunk.
+// Row-block partition parameters.  Row r has the partition coordinate
+// kRowWeight*r + rowOffset[r] (non-decreasing).  Block b holds the rows whose
+// coordinate lies in [b*T, (b+1)*T): at most ceil(T/kRowWeight) <= 511 rows
+// and about T - kRowWeight*rows non-zeros, so a block's rows fit the kernel's
+// registers and its non-zeros one LDS chunk for typical row lengths; a longer
+// row simply makes its block span several chunks.
 constexpr int64_t kChunkNnz = 2048;        // LDS product slots per chunk
-constexpr int64_t kChunkTarget = 1984;     // nnz per block the T formula aims at
-constexpr int64_t kMinItemsPerBlock = 256;
-constexpr int64_t kMaxItemsPerBlock = 4096;  // also bounds the rows of one block
+constexpr int64_t kChunkTarget = 1984;     // non-zeros per block the T formula aims at
+constexpr int64_t kRowWeight = 16;
+constexpr int64_t kMaxItemsPerBlock = 8176;  // ceil(8176/16) = 511 rows per block
+constexpr int64_t kMaxRowsPerBlock = 511;
 
 struct SpmvWsHeader {
     uint32_t magic;
@@ -115,11 +121,12 @@ struct SpmvWsHeader {
     uint64_t num_blocks;
     uint64_t rowptr_offset;
     uint64_t blocks_offset;
+    uint64_t block_nnz_offset;
     uint64_t acc_offset;
     uint32_t rowptr_bytes;
     uint32_t index_base;
     uint32_t op;
-    uint32_t reserved[27];
+    uint32_t reserved[25];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 
@@ -127,23 +134,23 @@ inline size_t AlignUp(size_t v) { return (v + kWsAlign - 1) & ~(kWsAlign - 1); }
 
 inline int64_t ItemsPerBlock(uint64_t rows, uint64_t nnz)
 {
-    const uint64_t denom = nnz == 0 ? 1 : nnz;
-    // rows + nnz < 2^33 and kChunkTarget < 2^11, so the product fits 64 bits.
-    int64_t t = static_cast<int64_t>((static_cast<uint64_t>(kChunkTarget) * (rows + nnz)) / denom);
-    if (t < kMinItemsPerBlock) t = kMinItemsPerBlock;
-    if (t > kMaxItemsPerBlock) t = kMaxItemsPerBlock;
-    return t;
+    // T = target + kRowWeight * (rows a target-sized block holds), capped.
+    if (nnz == 0) return kMaxItemsPerBlock;
+    const uint64_t extra = (static_cast<uint64_t>(kRowWeight * kChunkTarget) * rows) / nnz;
+    const uint64_t t = static_cast<uint64_t>(kChunkTarget) + extra;
+    return t > static_cast<uint64_t>(kMaxItemsPerBlock) ? kMaxItemsPerBlock : static_cast<int64_t>(t);
 }
 
 inline int64_t NumBlocks(uint64_t rows, uint64_t nnz)
 {
-    const int64_t t = ItemsPerBlock(rows, nnz);
-    return static_cast<int64_t>((rows + nnz + static_cast<uint64_t>(t) - 1) / static_cast<uint64_t>(t));
+    const uint64_t t = static_cast<uint64_t>(ItemsPerBlock(rows, nnz));
+    return static_cast<int64_t>((static_cast<uint64_t>(kRowWeight) * rows + nnz + t - 1) / t);
 }
 
 struct SpmvLayout {
     size_t rowptr_offset = 0;
     size_t blocks_offset = 0;
+    size_t block_nnz_offset = 0;
     size_t acc_offset = 0;
     size_t total = 0;
     int64_t items_per_block = 0;
@@ -165,7 +172,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.num_blocks = NumBlocks(rows, nnz);
     l.rowptr_offset = kWsHeaderBytes;
     l.blocks_offset = AlignUp(l.rowptr_offset + static_cast<size_t>(rows + 1) * l.rowptr_bytes);
-    l.acc_offset = AlignUp(l.blocks_offset + static_cast<size_t>(l.num_blocks + 1) * sizeof(int32_t));
+    l.block_nnz_offset = AlignUp(l.blocks_offset + static_cast<size_t>(l.num_blocks + 1) * sizeof(int32_t));
+    l.acc_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
     l.total = l.acc_offset;
     if (transpose) {
         l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));

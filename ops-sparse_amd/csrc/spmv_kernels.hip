@@ -3,11 +3,11 @@
 // Design (one GPU, HBM-bound, no MFMA):
 //  * Preprocess: one launch normalises the row offsets (rowPtr[i*stride]-base,
 //    clamped to [0, nnz]) into the workspace and computes the row-block
-//    partition: block b owns the rows whose merge-path start coordinate
-//    (row + rowOffset[row]) lies in [b*T, (b+1)*T).  Every row belongs to
-//    exactly one block, so no cross-block fix-up is ever needed, and each
-//    block carries ~T rows+nnz items regardless of the row-length
-//    distribution.  Reference counterpart: the normalising kernel
+//    partition: block b owns the rows whose weighted merge-path coordinate
+//    (16*row + rowOffset[row]) lies in [b*T, (b+1)*T).  Every row belongs to
+//    exactly one block, so no cross-block fix-up is ever needed; a block has
+//    at most 511 rows and ~2000 non-zeros regardless of the row-length
+//    distribution (only a row longer than a chunk makes its block longer).  Reference counterpart: the normalising kernel
 //    sparse/spmv/arch35/spmv_kernel.cpp:1144-1163 (one block, scalar loop).
 //  * Non-transpose: one workgroup (256 lanes = 4 wave64) per row block.  The
 //    block streams its col_ind/values span through LDS in chunks of 2048
@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 #include "aclsparse_internal.h"
@@ -37,7 +39,7 @@ constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kChunk = static_cast<int>(kChunkNnz);   // 2048 product slots
 constexpr int kIpt = kChunk / kThreads;               // 8 items per lane in the scan
-constexpr int kMaxRows = static_cast<int>(kMaxItemsPerBlock);
+constexpr int kMaxRows = static_cast<int>(kMaxRowsPerBlock);
 constexpr int kXcds = 8;
 constexpr int kPadded = kChunk + kChunk / kIpt;
 
@@ -252,6 +254,7 @@ __device__ __forceinline__ int64_t XcdBlock()
 struct RowBlockParams {
     const void* rp;          // normalised row offsets (RowT), rows+1
     const int32_t* blocks;   // num_blocks+1 block start rows
+    const void* block_nnz;   // num_blocks+1 block start offsets (RowT)
     const int32_t* col;
     int64_t col_stride;
     const void* val;
@@ -265,6 +268,11 @@ struct RowBlockParams {
     int32_t base;
     int32_t conj;
     Scalars s;
+    // persistent scheduling: worker w serves XCD (w % 8) and walks that XCD's
+    // contiguous block range [xcd*per_xcd, (xcd+1)*per_xcd) with stride
+    // workers_per_xcd.
+    int64_t per_xcd;
+    int32_t workers_per_xcd;
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -502,6 +510,329 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
     }
 }
 
+
+// ----------------- pipelined persistent kernel (contiguous data) -----------------
+//
+// Each workgroup is persistent and walks its row blocks one LDS chunk
+// ("stage") at a time.  While stage s is reduced in LDS, the x gathers of
+// stage s+1 and the col_ind/values/row-offset/y loads of stage s+2 are already
+// in flight, so every workgroup keeps ~2 stages of HBM traffic outstanding
+// across its barriers (barriers only wait for LDS traffic).  Blocks with more
+// than kPipeRows rows are handled by SpmvRowBlockKernel instead.
+
+constexpr int kPipeRows = 2 * kThreads - 1;  // rows per block the register path covers
+static_assert(kPipeRows >= kMaxRowsPerBlock, "every row block must fit the register path");
+
+struct Stage {
+    int64_t tile;   // row block index
+    int64_t r0;     // first row
+    int64_t k0;     // first non-zero (normalised offset of r0)
+    int64_t a0;     // 16-byte aligned global start of this chunk
+    int32_t nr;     // rows in the block
+    int32_t kspan;  // non-zeros in the block
+    int32_t c0, c1; // chunk range, relative to k0
+    bool first, last, valid;
+};
+
+template <typename RowT>
+__device__ __forceinline__ void ChunkBounds(Stage& s)
+{
+    const int64_t gStart = s.k0 + s.c0;
+    s.a0 = gStart & ~static_cast<int64_t>(3);
+    const int32_t lim = static_cast<int32_t>(s.a0 - s.k0) + kChunk;
+    s.c1 = s.kspan < lim ? s.kspan : lim;
+    s.last = s.c1 >= s.kspan;
+}
+
+template <typename RowT>
+__device__ __forceinline__ Stage OpenTile(const RowBlockParams& p, int64_t tile, int64_t tileEnd)
+{
+    Stage s{};
+    s.tile = tile;
+    s.valid = tile < tileEnd;
+    if (!s.valid) return s;
+    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
+    s.r0 = p.blocks[tile];
+    int64_t n = static_cast<int64_t>(p.blocks[tile + 1]) - s.r0;
+    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kMaxRows ? kMaxRows : n);
+    s.k0 = static_cast<int64_t>(bn[tile]);
+    int64_t span = static_cast<int64_t>(bn[tile + 1]) - s.k0;
+    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
+    s.c0 = 0;
+    s.first = true;
+    ChunkBounds<RowT>(s);
+    return s;
+}
+
+template <typename RowT>
+__device__ __forceinline__ Stage NextStage(const RowBlockParams& p, const Stage& s, int64_t stride, int64_t tileEnd)
+{
+    if (!s.valid) return s;
+    if (!s.last) {
+        Stage n = s;
+        n.c0 = s.c1;
+        n.first = false;
+        ChunkBounds<RowT>(n);
+        return n;
+    }
+    return OpenTile<RowT>(p, s.tile + stride, tileEnd);
+}
+
+// Register bundle of one stage: 8 non-zeros per lane (two 16-byte groups at
+// slots 4*tid and 4*tid+1024), two rows per lane (tid, tid+256).
+template <typename RowT, ValKind V, OutKind O>
+struct Bundle {
+    int32_t col[8];
+    typename ValOf<V>::T val[8];
+    RowT rp[2];
+    typename OutOf<O>::T yold[2];
+};
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__device__ __forceinline__ void LoadStage(const RowBlockParams& p, const Stage& s, bool betaNz,
+                                          Bundle<RowT, V, O>& b)
+{
+    using ValT = typename ValOf<V>::T;
+    const ValT* val = static_cast<const ValT*>(p.val);
+    const int64_t gEnd = s.k0 + s.c1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t g = s.a0 + 4 * static_cast<int64_t>(threadIdx.x + h * kThreads);
+        if (s.valid && g < gEnd) {
+            if (g + 4 <= p.nnz) {
+                Load4<V>(p.col, val, g, &b.col[4 * h], &b.val[4 * h]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool in = g + e < p.nnz;
+                    b.col[4 * h + e] = in ? p.col[g + e] : 0;
+                    b.val[4 * h + e] = in ? val[g + e] : ValT{};
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                b.col[4 * h + e] = -1;
+                b.val[4 * h + e] = ValT{};
+            }
+        }
+    }
+    if (s.valid && s.first) {
+        const RowT* rp = static_cast<const RowT*>(p.rp);
+        const typename OutOf<O>::T* y = static_cast<const typename OutOf<O>::T*>(p.y);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = threadIdx.x + h * kThreads;
+            b.rp[h] = i <= s.nr ? rp[s.r0 + i] : RowT{};
+            b.yold[h] = (betaNz && i < s.nr) ? y[s.r0 + i] : typename OutOf<O>::T{};
+        }
+    }
+}
+
+// Issues the x gathers of a loaded stage; out-of-chunk or out-of-range
+// entries gather nothing and later contribute exactly zero.
+template <typename RowT, ValKind V, OutKind O>
+__device__ __forceinline__ void GatherStage(const RowBlockParams& p, const Stage& s, Bundle<RowT, V, O>& b,
+                                            typename ValOf<V>::T xg[8])
+{
+    using ValT = typename ValOf<V>::T;
+    const ValT* x = static_cast<const ValT*>(p.x);
+    const int64_t gStart = s.k0 + s.c0, gEnd = s.k0 + s.c1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t g = s.a0 + 4 * static_cast<int64_t>(threadIdx.x + (j >> 2) * kThreads) + (j & 3);
+        const int64_t c = static_cast<int64_t>(b.col[j]) - p.base;
+        const bool ok = s.valid && g >= gStart && g < gEnd && c >= 0 && c < p.cols;
+        b.col[j] = ok ? 1 : 0;  // col is dead after the gather; keep the validity bit
+        xg[j] = ok ? x[c] : ValT{};
+    }
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__device__ __forceinline__ void Products(const Bundle<RowT, V, O>& b, const typename ValOf<V>::T xg[8],
+                                         typename AccOf<A>::T prod[8])
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        prod[j] = b.col[j] ? ToAcc<V, A>(b.val[j]) * ToAcc<V, A>(xg[j]) : Zero<typename AccOf<A>::T>();
+    }
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__global__ __launch_bounds__(kThreads) void SpmvPipeKernel(RowBlockParams p)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    using OutT = typename OutOf<O>::T;
+    using B = Bundle<RowT, V, O>;
+
+    __shared__ int32_t sRp[kPipeRows + 1];
+    __shared__ Acc sVal[kPadded];
+    __shared__ uint32_t sFlag[kChunk / 32];
+    __shared__ Acc sCarry[kThreads];
+    __shared__ int32_t sFirst[kThreads];
+    __shared__ Acc sWaveV[kWaves];
+    __shared__ int32_t sWaveF[kWaves];
+    __shared__ Acc sChunkCarry;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int64_t xcd = blockIdx.x % kXcds;
+    const int64_t worker = blockIdx.x / kXcds;
+    const int64_t tileBegin = xcd * p.per_xcd;
+    int64_t tileEnd = tileBegin + p.per_xcd;
+    if (tileEnd > p.num_blocks) tileEnd = p.num_blocks;
+    const int64_t stride = p.workers_per_xcd;
+
+    Acc alpha, beta;
+    LoadScalars<A>(p.s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    OutT* y = static_cast<OutT*>(p.y);
+
+    // Prologue: stage 0 loaded and gathered, stage 1 loaded.
+    Stage cur = OpenTile<RowT>(p, tileBegin + worker, tileEnd);
+    B bc, bn;
+    ValT xg[8];
+    LoadStage<RowT, V, O, A>(p, cur, betaNz, bc);
+    GatherStage<RowT, V, O>(p, cur, bc, xg);
+    Stage nxt = NextStage<RowT>(p, cur, stride, tileEnd);
+    LoadStage<RowT, V, O, A>(p, nxt, betaNz, bn);
+    Acc prod[8];
+    Products<RowT, V, O, A>(bc, xg, prod);
+    RowT rpc[2] = {bc.rp[0], bc.rp[1]};
+    OutT yc[2] = {bc.yold[0], bc.yold[1]};
+
+    while (cur.valid) {
+        // Keep two stages of memory traffic in flight while this one reduces.
+        GatherStage<RowT, V, O>(p, nxt, bn, xg);
+        const Stage after = NextStage<RowT>(p, nxt, stride, tileEnd);
+        B ba;
+        LoadStage<RowT, V, O, A>(p, after, betaNz, ba);
+
+        __syncthreads();  // the previous stage is done with LDS
+        if (cur.first) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int i = tid + h * kThreads;
+                if (i <= cur.nr) {
+                    int64_t v = static_cast<int64_t>(rpc[h]) - cur.k0;
+                    sRp[i] = static_cast<int32_t>(v < 0 ? 0 : v > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : v);
+                }
+            }
+            if (tid == 0) sChunkCarry = Zero<Acc>();
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sVal[Pad(4 * (tid + (j >> 2) * kThreads) + (j & 3))] = prod[j];
+        if (tid < kChunk / 32) sFlag[tid] = 0U;
+        __syncthreads();
+
+        const int32_t c0 = cur.c0, c1 = cur.c1;
+        const int32_t d = static_cast<int32_t>(cur.k0 - cur.a0);
+        const int nr = cur.nr;
+        // Segment heads: first non-zero of each non-empty row that starts here.
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = tid + h * kThreads;
+            if (i < nr) {
+                const int32_t s0 = sRp[i], e0 = sRp[i + 1];
+                if (e0 > s0 && s0 >= c0 && s0 < c1) {
+                    const int q = s0 + d;
+                    atomicOr(&sFlag[q >> 5], 1U << (q & 31));
+                }
+            }
+        }
+        __syncthreads();
+
+        // Lane-local segmented scan of 8 consecutive slots.
+        const uint32_t bits = (sFlag[tid >> 2] >> ((tid & 3) * 8)) & 0xFFU;
+        Acc run = Zero<Acc>();
+#pragma unroll
+        for (int j = 0; j < kIpt; ++j) {
+            const int q = tid * kIpt + j;
+            if (bits & (1U << j)) run = Zero<Acc>();
+            run = run + sVal[Pad(q)];
+            sVal[Pad(q)] = run;
+        }
+        const int first = bits ? __builtin_ctz(bits) : kIpt;
+        const int has = bits ? 1 : 0;
+
+        Acc v = run;
+        int f = has;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const Acc vo = ShflUp(v, off);
+            const int fo = __shfl_up(f, off, kWave);
+            if (lane >= off) {
+                if (!f) v = vo + v;
+                f |= fo;
+            }
+        }
+        Acc ve = ShflUp(v, 1);
+        int fe = __shfl_up(f, 1, kWave);
+        if (lane == 0) {
+            ve = Zero<Acc>();
+            fe = 0;
+        }
+        if (lane == kWave - 1) {
+            sWaveV[wave] = v;
+            sWaveF[wave] = f;
+        }
+        __syncthreads();
+        Acc pv = sChunkCarry;
+        for (int u = 0; u < wave; ++u) {
+            if (sWaveF[u]) pv = sWaveV[u];
+            else pv = pv + sWaveV[u];
+        }
+        const Acc excl = fe ? ve : pv + ve;
+        sCarry[tid] = excl;
+        sFirst[tid] = first;
+        __syncthreads();
+        if (!cur.last && tid == kThreads - 1) sChunkCarry = has ? run : excl + run;
+
+        // Rows that end inside this chunk (each lane owns rows tid, tid+256).
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = tid + h * kThreads;
+            if (i < nr) {
+                const int32_t s0 = sRp[i], e0 = sRp[i + 1];
+                bool done = false;
+                Acc sum = Zero<Acc>();
+                if (e0 <= s0) {
+                    done = (s0 >= c0 && s0 < c1) || (cur.last && s0 >= c1);
+                } else if (e0 > c0 && e0 <= c1) {
+                    const int q = e0 - 1 + d;
+                    const int t = q / kIpt;
+                    sum = sVal[Pad(q)];
+                    if ((q % kIpt) < sFirst[t]) sum = sum + sCarry[t];
+                    done = true;
+                }
+                if (done) {
+                    Acc r;
+                    if constexpr (A == AccKind::I64) {
+                        r = ScaledI64(sum, alpha, beta, betaNz ? OutToAcc<O, A>(yc[h]) : 0);
+                    } else {
+                        r = betaNz ? alpha * sum + beta * OutToAcc<O, A>(yc[h]) : alpha * sum;
+                    }
+                    y[(cur.r0 + i) * p.y_stride] = FromAcc<O, A>(r);
+                }
+            }
+        }
+
+        // Rotate the pipeline.
+        Products<RowT, V, O, A>(bn, xg, prod);
+        if (nxt.first) {
+            rpc[0] = bn.rp[0];
+            rpc[1] = bn.rp[1];
+            yc[0] = bn.yold[0];
+            yc[1] = bn.yold[1];
+        }
+        cur = nxt;
+        nxt = after;
+        bn = ba;
+    }
+}
+
 // ------------------------------- transpose ----------------------------------
 
 // y = beta*y in place (y is not read when beta == 0); the scatter then adds
@@ -615,6 +946,7 @@ struct PrepParams {
     int64_t rows, cols, nnz;
     void* norm;            // normalised row offsets (RowT)
     int32_t* blocks;
+    void* block_nnz;
     int64_t num_blocks;
     int64_t items;         // T
     SpmvWsHeader* header;
@@ -638,17 +970,18 @@ __global__ __launch_bounds__(kThreads) void SpmvPreprocessKernel(PrepParams p)
         if (i == p.num_blocks) {
             start = static_cast<int32_t>(p.rows);
         } else {
-            // First row r in [0, rows] whose start coordinate r + offset(r) >= i*T.
+            // First row r in [0, rows] whose coordinate 16*r + offset(r) >= i*T.
             const int64_t diag = i * p.items;
             int64_t lo = 0, hi = p.rows;
             while (lo < hi) {
                 const int64_t mid = (lo + hi) >> 1;
-                if (mid + NormRow<SrcT>(p, mid) >= diag) hi = mid;
+                if (kRowWeight * mid + NormRow<SrcT>(p, mid) >= diag) hi = mid;
                 else lo = mid + 1;
             }
             start = static_cast<int32_t>(lo);
         }
         p.blocks[i] = start;
+        static_cast<SrcT*>(p.block_nnz)[i] = static_cast<SrcT>(NormRow<SrcT>(p, start));
     }
     if (i == 0) *p.header = p.header_value;
 }
@@ -669,6 +1002,7 @@ RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
     RowBlockParams p{};
     p.rp = At<void>(l.ws, l.layout.rowptr_offset);
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
+    p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
     p.col = l.col;
     p.col_stride = l.col_stride;
     p.val = l.val;
@@ -703,17 +1037,66 @@ unsigned RowBlockGrid(int64_t numBlocks)
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
 
+// Resident workgroups per CU of a kernel (cached per device and kernel).
+int ResidentBlocksPerCu(const void* kernel)
+{
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, kernel});
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess || n < 1) n = 1;
+    cache[{dev, kernel}] = n;
+    return n;
+}
+
+int CuCount()
+{
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < kXcds) n = 256;
+    cache[dev] = n;
+    return n;
+}
+
+// Persistent grid: the blocks of each XCD's range are split evenly over
+// J <= resident-slots workers so that every worker runs the same number of
+// blocks (+-1), i.e. J = ceil(per / ceil(per / slots)).
+void PersistentShape(RowBlockParams& p, const void* kernel, unsigned& grid)
+{
+    const int64_t per = (p.num_blocks + kXcds - 1) / kXcds;
+    const int64_t slots = static_cast<int64_t>(CuCount() / kXcds) * ResidentBlocksPerCu(kernel);
+    const int64_t rounds = (per + slots - 1) / slots;
+    int64_t j = rounds > 0 ? (per + rounds - 1) / rounds : 1;
+    if (j < 1) j = 1;
+    p.per_xcd = per;
+    p.workers_per_xcd = static_cast<int32_t>(j);
+    grid = static_cast<unsigned>(j * kXcds);
+}
+
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
 {
-    const RowBlockParams p = MakeRowBlockParams(l);
+    RowBlockParams p = MakeRowBlockParams(l);
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
-    const bool vec = kCanVec && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && Aligned16(l.col) &&
-                     Aligned16(l.val);
+    const bool vec = kCanVec && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && l.y_stride == 1 &&
+                     Aligned16(l.col) && Aligned16(l.val);
     if constexpr (kCanVec) {
         if (vec) {
-            hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+            const void* k = reinterpret_cast<const void*>(&SpmvPipeKernel<RowT, V, O, A>);
+            unsigned pg = 0;
+            PersistentShape(p, k, pg);
+            hipLaunchKernelGGL((SpmvPipeKernel<RowT, V, O, A>), dim3(pg), dim3(kThreads), 0, stream, p);
             return 0;
         }
     }
@@ -794,6 +1177,7 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     p.nnz = l.nnz;
     p.norm = At<void>(l.ws, l.layout.rowptr_offset);
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
+    p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
     p.num_blocks = l.layout.num_blocks;
     p.items = l.layout.items_per_block;
     p.header = At<SpmvWsHeader>(l.ws, 0);
@@ -807,6 +1191,7 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     h.num_blocks = static_cast<uint64_t>(l.layout.num_blocks);
     h.rowptr_offset = l.layout.rowptr_offset;
     h.blocks_offset = l.layout.blocks_offset;
+    h.block_nnz_offset = l.layout.block_nnz_offset;
     h.acc_offset = l.layout.acc_offset;
     h.rowptr_bytes = l.layout.rowptr_bytes;
     h.index_base = static_cast<uint32_t>(l.base);

@@ -171,7 +171,7 @@ def num_blocks(rows, nnz):
 
 
 def partition(row_ptr, nnz, rows=None, stride=1, base=0):
-    """(normalised row offsets int64, block start rows int32) of the row-block partition.
+    """(normalised row offsets, block start rows, block start offsets) of the row-block partition.
 
     ``row_ptr`` is the physical array (``rows+1`` logical entries ``stride`` apart).
     """
@@ -181,8 +181,9 @@ def partition(row_ptr, nnz, rows=None, stride=1, base=0):
     norm = np.empty(rows + 1, dtype=np.int64)
     nb = num_blocks(rows, nnz)
     blocks = np.empty(nb + 1, dtype=np.int32)
-    lib().oracle_spmv_partition(_I(rows), _I(nnz), _p(rp), _I(stride), _I(base), _p(norm), _p(blocks))
-    return norm, blocks
+    bnnz = np.empty(nb + 1, dtype=np.int64)
+    lib().oracle_spmv_partition(_I(rows), _I(nnz), _p(rp), _I(stride), _I(base), _p(norm), _p(blocks), _p(bnnz))
+    return norm, blocks, bnnz
 
 
 def verify_mixed(golden, actual, rtol, atol, max_abs, ratio, exact=False):

@@ -26,7 +26,7 @@
  *                          this build's row-block partition (no reference
  *                          counterpart; restated from its definition:
  *                          block b starts at the first row r with
- *                          r + rowOffset[r] >= b*T)
+ *                          16*r + rowOffset[r] >= b*T)
  *   oracle_verify_mixed    Verification() mixed tolerance,
  *                          test/spmv/arch22/spmv_test_verification.h:23-101
  *
@@ -261,26 +261,27 @@ void oracle_spmv_c64(int64_t rows, int64_t cols, const int64_t *rp, const int32_
 
 /* ----------------------------- partition ---------------------------------- */
 
+/* T = min(8176, 1984 + floor(16*1984*rows/nnz)) (8176 when nnz == 0);
+ * blocks = ceil((16*rows + nnz) / T). */
 int64_t oracle_items_per_block(int64_t rows, int64_t nnz)
 {
-    const int64_t denom = nnz == 0 ? 1 : nnz;
-    int64_t t = (int64_t)(((uint64_t)1984 * (uint64_t)(rows + nnz)) / (uint64_t)denom);
-    if (t < 256) t = 256;
-    if (t > 4096) t = 4096;
-    return t;
+    if (nnz == 0) return 8176;
+    const uint64_t t = 1984u + ((uint64_t)(16 * 1984) * (uint64_t)rows) / (uint64_t)nnz;
+    return t > 8176u ? 8176 : (int64_t)t;
 }
 
 int64_t oracle_num_blocks(int64_t rows, int64_t nnz)
 {
     const int64_t t = oracle_items_per_block(rows, nnz);
-    return (rows + nnz + t - 1) / t;
+    return (16 * rows + nnz + t - 1) / t;
 }
 
 /* norm[i] = clamp(rowPtr[i*stride] - base, 0, nnz) for i in [0, rows];
- * blocks[b] = first row r with r + norm[r] >= b*T (b < B), blocks[B] = rows.
- * Computed by a forward sweep, independently of the device's binary search. */
+ * blocks[b] = first row r with 16*r + norm[r] >= b*T (b < B), blocks[B] = rows;
+ * block_nnz[b] = norm[blocks[b]].  Computed by a forward sweep, independently
+ * of the device's per-block binary search. */
 void oracle_spmv_partition(int64_t rows, int64_t nnz, const int64_t *rowPtr, int64_t stride, int64_t base,
-                           int64_t *norm, int32_t *blocks)
+                           int64_t *norm, int32_t *blocks, int64_t *blockNnz)
 {
     const int64_t t = oracle_items_per_block(rows, nnz);
     const int64_t nb = oracle_num_blocks(rows, nnz);
@@ -290,10 +291,12 @@ void oracle_spmv_partition(int64_t rows, int64_t nnz, const int64_t *rowPtr, int
     }
     int64_t r = 0;
     for (int64_t b = 0; b < nb; ++b) {
-        while (r < rows && r + norm[r] < b * t) ++r;
+        while (r < rows && 16 * r + norm[r] < b * t) ++r;
         blocks[b] = (int32_t)r;
+        blockNnz[b] = norm[r];
     }
     blocks[nb] = (int32_t)rows;
+    blockNnz[nb] = norm[rows];
 }
 
 /* ------------------------- mixed-tolerance verify -------------------------- */

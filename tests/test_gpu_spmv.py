@@ -231,18 +231,27 @@ def test_config_parity_full_size(name, dev):
     print(f"{w.name}: rows={w.rows} nnz={w.nnz} err={assert_close(w.to('cpu'), y):.3e}")
 
 
-def test_partition_metadata_bit_exact(dev):
-    w = wl.config("c3", "cpu", 64)
+@pytest.mark.parametrize("name,scale,i64", [("c3", 64, False), ("c2", 16, False), ("c5", 64, False),
+                                            ("c3", 64, True)])
+def test_partition_metadata_bit_exact(name, scale, i64, dev):
+    w = wl.config(name, "cpu", scale)
+    if i64:
+        w.row_ptr = w.row_ptr.to(torch.int64)
     w, y, plan = run_workload(w, dev)
     ws = plan.workspace.cpu().numpy()
     hdr = np.frombuffer(ws[:192].tobytes(), dtype=np.uint64)
-    nb, rp_off, bl_off = int(hdr[5]), int(hdr[6]), int(hdr[7])
-    norm_ref, blocks_ref = oracle.partition(w.row_ptr.cpu().numpy(), w.nnz)
+    nb, rp_off, bl_off, bn_off = int(hdr[5]), int(hdr[6]), int(hdr[7]), int(hdr[8])
+    norm_ref, blocks_ref, bnnz_ref = oracle.partition(w.row_ptr.cpu().numpy(), w.nnz)
     assert nb == oracle.num_blocks(w.rows, w.nnz) and int(hdr[4]) == oracle.items_per_block(w.rows, w.nnz)
-    norm = np.frombuffer(ws[rp_off:rp_off + 4 * (w.rows + 1)].tobytes(), dtype=np.int32)
+    rdt = np.int64 if i64 else np.int32
+    rb = 8 if i64 else 4
+    norm = np.frombuffer(ws[rp_off:rp_off + rb * (w.rows + 1)].tobytes(), dtype=rdt)
     blocks = np.frombuffer(ws[bl_off:bl_off + 4 * (nb + 1)].tobytes(), dtype=np.int32)
+    bnnz = np.frombuffer(ws[bn_off:bn_off + rb * (nb + 1)].tobytes(), dtype=rdt)
     np.testing.assert_array_equal(norm, norm_ref)
     np.testing.assert_array_equal(blocks, blocks_ref)
+    np.testing.assert_array_equal(bnnz, bnnz_ref)
+    assert np.all(np.diff(blocks) <= 511)
 
 
 def test_beta_zero_never_reads_y(dev):
