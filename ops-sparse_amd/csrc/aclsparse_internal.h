@@ -93,23 +93,26 @@ namespace aclsp {
 //   block_row_start     int32[num_blocks+1]: first row of each row block
 //   block_nnz_start     RowT[num_blocks+1]: normalised offset of that row
 //                       (lets a block start streaming before reading its rows)
+//   sink                512 bytes the kernel stores into for lanes that have
+//                       no output row this chunk (keeps stores branch-free)
 //   accumulator         transpose only: cols x accumulator element
 // ---------------------------------------------------------------------------
 constexpr size_t kWsAlign = 64;
 constexpr size_t kWsHeaderBytes = 192;
 constexpr uint32_t kWsMagic = 0x4D505348U;  // "HSPM"
+constexpr size_t kSinkBytes = 512;
 
 // Row-block partition parameters.  Row r has the partition coordinate
 // kRowWeight*r + rowOffset[r] (non-decreasing).  Block b holds the rows whose
-// coordinate lies in [b*T, (b+1)*T): at most ceil(T/kRowWeight) <= 511 rows
-// and about T - kRowWeight*rows non-zeros, so a block's rows fit the kernel's
-// registers and its non-zeros one LDS chunk for typical row lengths; a longer
-// row simply makes its block span several chunks.
-constexpr int64_t kChunkNnz = 2048;        // LDS product slots per chunk
-constexpr int64_t kChunkTarget = 1984;     // non-zeros per block the T formula aims at
+// coordinate lies in [b*T, (b+1)*T): at most ceil(T/kRowWeight) <= 127 rows
+// (two per lane of a wave64) and about T - kRowWeight*rows non-zeros, so one
+// wave handles one block with 8 non-zeros per lane for typical row lengths;
+// a longer row simply makes its block span several wave chunks.
+constexpr int64_t kChunkNnz = 512;         // non-zeros one wave reduces per chunk
+constexpr int64_t kChunkTarget = 496;      // non-zeros per block the T formula aims at
 constexpr int64_t kRowWeight = 16;
-constexpr int64_t kMaxItemsPerBlock = 8176;  // ceil(8176/16) = 511 rows per block
-constexpr int64_t kMaxRowsPerBlock = 511;
+constexpr int64_t kMaxItemsPerBlock = 2032;  // ceil(2032/16) = 127 rows per block
+constexpr int64_t kMaxRowsPerBlock = 127;
 
 struct SpmvWsHeader {
     uint32_t magic;
@@ -122,11 +125,12 @@ struct SpmvWsHeader {
     uint64_t rowptr_offset;
     uint64_t blocks_offset;
     uint64_t block_nnz_offset;
+    uint64_t sink_offset;
     uint64_t acc_offset;
     uint32_t rowptr_bytes;
     uint32_t index_base;
     uint32_t op;
-    uint32_t reserved[25];
+    uint32_t reserved[23];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 
@@ -151,6 +155,7 @@ struct SpmvLayout {
     size_t rowptr_offset = 0;
     size_t blocks_offset = 0;
     size_t block_nnz_offset = 0;
+    size_t sink_offset = 0;
     size_t acc_offset = 0;
     size_t total = 0;
     int64_t items_per_block = 0;
@@ -173,7 +178,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.rowptr_offset = kWsHeaderBytes;
     l.blocks_offset = AlignUp(l.rowptr_offset + static_cast<size_t>(rows + 1) * l.rowptr_bytes);
     l.block_nnz_offset = AlignUp(l.blocks_offset + static_cast<size_t>(l.num_blocks + 1) * sizeof(int32_t));
-    l.acc_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
+    l.sink_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
+    l.acc_offset = l.sink_offset + kSinkBytes;
     l.total = l.acc_offset;
     if (transpose) {
         l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));

@@ -37,7 +37,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kChunk = static_cast<int>(kChunkNnz);   // 2048 product slots
+constexpr int kChunk = 2048;                          // LDS product slots of the block kernel
 constexpr int kIpt = kChunk / kThreads;               // 8 items per lane in the scan
 constexpr int kMaxRows = static_cast<int>(kMaxRowsPerBlock);
 constexpr int kXcds = 8;
@@ -273,6 +273,7 @@ struct RowBlockParams {
     // workers_per_xcd.
     int64_t per_xcd;
     int32_t workers_per_xcd;
+    void* sink;  // per-lane dummy outputs
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -511,20 +512,30 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
 }
 
 
-// ----------------- pipelined persistent kernel (contiguous data) -----------------
+// ------------------- wave-per-block persistent kernel --------------------
 //
-// Each workgroup is persistent and walks its row blocks one LDS chunk
-// ("stage") at a time.  While stage s is reduced in LDS, the x gathers of
-// stage s+1 and the col_ind/values/row-offset/y loads of stage s+2 are already
-// in flight, so every workgroup keeps ~2 stages of HBM traffic outstanding
-// across its barriers (barriers only wait for LDS traffic).  Blocks with more
-// than kPipeRows rows are handled by SpmvRowBlockKernel instead.
+// One wave64 owns one row block at a time (<= 127 rows, ~500 non-zeros) and
+// reduces it without any workgroup barrier: lane l holds the 8 consecutive
+// non-zeros [8l, 8l+8) of the chunk (two 16-byte non-temporal loads), forms
+// the products in registers, runs a lane-local segmented scan, then a 6-step
+// shuffle scan carries partial rows across lanes.  Row-start flags, the
+// block's row offsets and the finished prefixes go through a private
+// per-wave LDS slice.  The waves of a workgroup are independent persistent
+// workers; each keeps the x gathers of its next chunk and the col/values/
+// row-offset/y loads of the chunk after that in flight while it reduces the
+// current one.
 
-constexpr int kPipeRows = 2 * kThreads - 1;  // rows per block the register path covers
-static_assert(kPipeRows >= kMaxRowsPerBlock, "every row block must fit the register path");
+constexpr int kWaveChunk = static_cast<int>(kChunkNnz);  // 512 slots, 8 per lane
+constexpr int kLaneItems = kWaveChunk / kWave;           // 8
+constexpr int kWaveRows = static_cast<int>(kMaxRowsPerBlock);
+constexpr int kWavesPerGroup = 4;
+constexpr int kWavePadded = kWaveChunk + kWaveChunk / kLaneItems;
+
+static_assert(kLaneItems == 8, "lane scan is written for 8 items per lane");
+static_assert(kWaveRows <= 2 * kWave - 1, "two rows per lane");
 
 struct Stage {
-    int64_t tile;   // row block index
+    int64_t tile;   // ordinal of the block among this worker's blocks
     int64_t r0;     // first row
     int64_t k0;     // first non-zero (normalised offset of r0)
     int64_t a0;     // 16-byte aligned global start of this chunk
@@ -534,231 +545,265 @@ struct Stage {
     bool first, last, valid;
 };
 
-template <typename RowT>
 __device__ __forceinline__ void ChunkBounds(Stage& s)
 {
     const int64_t gStart = s.k0 + s.c0;
     s.a0 = gStart & ~static_cast<int64_t>(3);
-    const int32_t lim = static_cast<int32_t>(s.a0 - s.k0) + kChunk;
+    const int32_t lim = static_cast<int32_t>(s.a0 - s.k0) + kWaveChunk;
     s.c1 = s.kspan < lim ? s.kspan : lim;
     s.last = s.c1 >= s.kspan;
 }
 
+// The partition arrays do not change while a kernel runs: read them through
+// the constant address space so that the (wave-uniform) reads become scalar
+// loads, which never wait on the vector-memory counter of the prefetches.
+template <typename T>
+__device__ __forceinline__ T ConstLoad(const void* base, int64_t i)
+{
+    typedef const __attribute__((address_space(4))) T* CPtr;
+    return reinterpret_cast<CPtr>(reinterpret_cast<uintptr_t>(base))[i];
+}
+
+// Opens the ordinal-th block of this worker (block first + ordinal*stride).
 template <typename RowT>
-__device__ __forceinline__ Stage OpenTile(const RowBlockParams& p, int64_t tile, int64_t tileEnd)
+__device__ __forceinline__ Stage OpenTile(const RowBlockParams& p, int64_t ordinal, int64_t first, int64_t stride,
+                                          int64_t tileEnd)
 {
     Stage s{};
-    s.tile = tile;
-    s.valid = tile < tileEnd;
+    s.tile = ordinal;
+    const int64_t t = first + ordinal * stride;
+    s.valid = t < tileEnd;
     if (!s.valid) return s;
-    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
-    s.r0 = p.blocks[tile];
-    int64_t n = static_cast<int64_t>(p.blocks[tile + 1]) - s.r0;
-    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kMaxRows ? kMaxRows : n);
-    s.k0 = static_cast<int64_t>(bn[tile]);
-    int64_t span = static_cast<int64_t>(bn[tile + 1]) - s.k0;
+    s.r0 = ConstLoad<int32_t>(p.blocks, t);
+    const int64_t n = static_cast<int64_t>(ConstLoad<int32_t>(p.blocks, t + 1)) - s.r0;
+    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kWaveRows ? kWaveRows : n);
+    s.k0 = static_cast<int64_t>(ConstLoad<RowT>(p.block_nnz, t));
+    const int64_t span = static_cast<int64_t>(ConstLoad<RowT>(p.block_nnz, t + 1)) - s.k0;
     s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
     s.c0 = 0;
     s.first = true;
-    ChunkBounds<RowT>(s);
+    ChunkBounds(s);
     return s;
 }
 
 template <typename RowT>
-__device__ __forceinline__ Stage NextStage(const RowBlockParams& p, const Stage& s, int64_t stride, int64_t tileEnd)
+__device__ __forceinline__ Stage NextStage(const RowBlockParams& p, const Stage& s, int64_t first, int64_t stride,
+                                           int64_t tileEnd)
 {
     if (!s.valid) return s;
     if (!s.last) {
         Stage n = s;
         n.c0 = s.c1;
         n.first = false;
-        ChunkBounds<RowT>(n);
+        ChunkBounds(n);
         return n;
     }
-    return OpenTile<RowT>(p, s.tile + stride, tileEnd);
+    return OpenTile<RowT>(p, s.tile + 1, first, stride, tileEnd);
 }
 
-// Register bundle of one stage: 8 non-zeros per lane (two 16-byte groups at
-// slots 4*tid and 4*tid+1024), two rows per lane (tid, tid+256).
+// Register bundle of one chunk for one lane: slots [8l, 8l+8) and rows l, l+64.
 template <typename RowT, ValKind V, OutKind O>
 struct Bundle {
-    int32_t col[8];
-    typename ValOf<V>::T val[8];
+    int32_t col[kLaneItems];
+    typename ValOf<V>::T val[kLaneItems];
     RowT rp[2];
     typename OutOf<O>::T yold[2];
 };
 
-template <typename RowT, ValKind V, OutKind O, AccKind A>
-__device__ __forceinline__ void LoadStage(const RowBlockParams& p, const Stage& s, bool betaNz,
-                                          Bundle<RowT, V, O>& b)
+// The last nnz % 4 entries of col_ind / values, which a 16-byte load
+// cannot fetch without reading past the arrays.
+template <ValKind V>
+struct ArrayTail {
+    int64_t start;  // nnz rounded down to a multiple of 4
+    int32_t col[3];
+    typename ValOf<V>::T val[3];
+};
+
+// Every load is issued unconditionally (clamped to valid addresses) so the
+// compiler's wait-counter bookkeeping stays exact across loop iterations:
+// a conditional load here would make it wait for the whole prefetch queue.
+template <typename RowT, ValKind V, OutKind O, bool kBeta>
+__device__ __forceinline__ void LoadStage(const RowBlockParams& p, const Stage& s, const ArrayTail<V>& tail,
+                                          int lane, Bundle<RowT, V, O>& b)
 {
     using ValT = typename ValOf<V>::T;
     const ValT* val = static_cast<const ValT*>(p.val);
-    const int64_t gEnd = s.k0 + s.c1;
+    const int64_t g0 = s.valid ? s.a0 + kLaneItems * lane : 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int64_t g = s.a0 + 4 * static_cast<int64_t>(threadIdx.x + h * kThreads);
-        if (s.valid && g < gEnd) {
-            if (g + 4 <= p.nnz) {
-                Load4<V>(p.col, val, g, &b.col[4 * h], &b.val[4 * h]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const bool in = g + e < p.nnz;
-                    b.col[4 * h + e] = in ? p.col[g + e] : 0;
-                    b.val[4 * h + e] = in ? val[g + e] : ValT{};
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                b.col[4 * h + e] = -1;
-                b.val[4 * h + e] = ValT{};
-            }
-        }
+        const int64_t g = g0 + 4 * h;
+        const int64_t gv = g + 4 <= tail.start ? g : 0;  // a vector that would cross the end re-reads [0,4)
+        Load4<V>(p.col, val, gv, &b.col[4 * h], &b.val[4 * h]);
     }
-    if (s.valid && s.first) {
-        const RowT* rp = static_cast<const RowT*>(p.rp);
-        const typename OutOf<O>::T* y = static_cast<const typename OutOf<O>::T*>(p.y);
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    const int lastRow = s.nr > 0 ? s.nr - 1 : 0;
+    const int64_t r0 = s.valid ? s.r0 : 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int i = threadIdx.x + h * kThreads;
-            b.rp[h] = i <= s.nr ? rp[s.r0 + i] : RowT{};
-            b.yold[h] = (betaNz && i < s.nr) ? y[s.r0 + i] : typename OutOf<O>::T{};
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave;
+        b.rp[h] = rp[r0 + (i <= s.nr ? i : s.nr)];  // row offsets have rows+1 entries
+        if constexpr (kBeta) {
+            // a block can start at row == rows (past a long last row): clamp into y
+            int64_t yi = r0 + (i <= lastRow ? i : lastRow);
+            yi = yi < p.rows ? yi : p.rows - 1;
+            const typename OutOf<O>::T* y = static_cast<const typename OutOf<O>::T*>(p.y);
+            b.yold[h] = y[yi * p.y_stride];
         }
     }
 }
 
-// Issues the x gathers of a loaded stage; out-of-chunk or out-of-range
-// entries gather nothing and later contribute exactly zero.
+// Issues the x gathers of a loaded chunk; slots outside the chunk or with an
+// out-of-range column gather x[0] and are masked to contribute exactly zero.
 template <typename RowT, ValKind V, OutKind O>
-__device__ __forceinline__ void GatherStage(const RowBlockParams& p, const Stage& s, Bundle<RowT, V, O>& b,
-                                            typename ValOf<V>::T xg[8])
+__device__ __forceinline__ void GatherStage(const RowBlockParams& p, const Stage& s, const ArrayTail<V>& tail,
+                                            int lane, Bundle<RowT, V, O>& b, typename ValOf<V>::T xg[kLaneItems])
 {
     using ValT = typename ValOf<V>::T;
     const ValT* x = static_cast<const ValT*>(p.x);
-    const int64_t gStart = s.k0 + s.c0, gEnd = s.k0 + s.c1;
+    const int64_t gStart = s.k0 + s.c0, gEnd = s.valid ? s.k0 + s.c1 : gStart;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int64_t g = s.a0 + 4 * static_cast<int64_t>(threadIdx.x + (j >> 2) * kThreads) + (j & 3);
-        const int64_t c = static_cast<int64_t>(b.col[j]) - p.base;
-        const bool ok = s.valid && g >= gStart && g < gEnd && c >= 0 && c < p.cols;
-        b.col[j] = ok ? 1 : 0;  // col is dead after the gather; keep the validity bit
-        xg[j] = ok ? x[c] : ValT{};
+    for (int j = 0; j < kLaneItems; ++j) {
+        const int64_t g = s.a0 + kLaneItems * lane + j;
+        // entries of the array tail were not covered by the 16-byte loads
+        const int64_t k = g - tail.start;
+        const bool inTail = k >= 0 && k < 3;
+        const int kk = inTail ? static_cast<int>(k) : 0;
+        const int32_t colv = inTail ? (kk == 0 ? tail.col[0] : kk == 1 ? tail.col[1] : tail.col[2]) : b.col[j];
+        if (inTail) b.val[j] = kk == 0 ? tail.val[0] : kk == 1 ? tail.val[1] : tail.val[2];
+        const int64_t c = static_cast<int64_t>(colv) - p.base;
+        const bool ok = g >= gStart && g < gEnd && c >= 0 && c < p.cols;
+        b.col[j] = ok ? 1 : 0;  // the column is dead after the gather; keep the validity bit
+        xg[j] = x[ok ? c : 0];
     }
 }
 
 template <typename RowT, ValKind V, OutKind O, AccKind A>
-__device__ __forceinline__ void Products(const Bundle<RowT, V, O>& b, const typename ValOf<V>::T xg[8],
-                                         typename AccOf<A>::T prod[8])
+__device__ __forceinline__ void Products(const Bundle<RowT, V, O>& b, const typename ValOf<V>::T xg[kLaneItems],
+                                         typename AccOf<A>::T prod[kLaneItems])
 {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < kLaneItems; ++j) {
         prod[j] = b.col[j] ? ToAcc<V, A>(b.val[j]) * ToAcc<V, A>(xg[j]) : Zero<typename AccOf<A>::T>();
     }
 }
 
-template <typename RowT, ValKind V, OutKind O, AccKind A>
-__global__ __launch_bounds__(kThreads) void SpmvPipeKernel(RowBlockParams p)
+// Orders this wave's LDS accesses (LDS ops of one wave complete in order;
+// the clobber keeps the compiler from moving accesses across the wait).
+__device__ __forceinline__ void WaveLdsSync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ float ReadLane(float v, int l) { return __shfl(v, l, kWave); }
+__device__ __forceinline__ long long ReadLane(long long v, int l) { return __shfl(v, l, kWave); }
+__device__ __forceinline__ C64 ReadLane(C64 v, int l) { return C64{__shfl(v.re, l, kWave), __shfl(v.im, l, kWave)}; }
+
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kBeta>
+__global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvWaveKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
     using ValT = typename ValOf<V>::T;
     using OutT = typename OutOf<O>::T;
     using B = Bundle<RowT, V, O>;
 
-    __shared__ int32_t sRp[kPipeRows + 1];
-    __shared__ Acc sVal[kPadded];
-    __shared__ uint32_t sFlag[kChunk / 32];
-    __shared__ Acc sCarry[kThreads];
-    __shared__ int32_t sFirst[kThreads];
-    __shared__ Acc sWaveV[kWaves];
-    __shared__ int32_t sWaveF[kWaves];
-    __shared__ Acc sChunkCarry;
+    __shared__ int32_t sRpAll[kWavesPerGroup][kWaveRows + 1];
+    __shared__ Acc sValAll[kWavesPerGroup][kWavePadded];
+    __shared__ uint32_t sFlagAll[kWavesPerGroup][kWaveChunk / 32];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    // The wave index is uniform within a wave; say so, so that all block
+    // bookkeeping stays in scalar registers.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    int32_t* sRp = sRpAll[wv];
+    Acc* sVal = sValAll[wv];
+    uint32_t* sFlag = sFlagAll[wv];
+
     const int64_t xcd = blockIdx.x % kXcds;
-    const int64_t worker = blockIdx.x / kXcds;
+    const int64_t worker = (blockIdx.x / kXcds) * kWavesPerGroup + wv;
     const int64_t tileBegin = xcd * p.per_xcd;
     int64_t tileEnd = tileBegin + p.per_xcd;
     if (tileEnd > p.num_blocks) tileEnd = p.num_blocks;
     const int64_t stride = p.workers_per_xcd;
+    const int64_t firstTile = tileBegin + worker;
 
     Acc alpha, beta;
     LoadScalars<A>(p.s, alpha, beta);
-    const bool betaNz = !IsZero(beta);
     OutT* y = static_cast<OutT*>(p.y);
+    OutT* sink = static_cast<OutT*>(p.sink) + lane;
 
-    // Prologue: stage 0 loaded and gathered, stage 1 loaded.
-    Stage cur = OpenTile<RowT>(p, tileBegin + worker, tileEnd);
+    ArrayTail<V> tail;
+    tail.start = p.nnz & ~static_cast<int64_t>(3);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+        const int64_t k = tail.start + e < p.nnz ? tail.start + e : (p.nnz > 0 ? p.nnz - 1 : 0);
+        tail.col[e] = p.nnz > 0 ? ConstLoad<int32_t>(p.col, k) : 0;
+        tail.val[e] = p.nnz > 0 ? ConstLoad<ValT>(p.val, k) : ValT{};
+    }
+
+    // Prologue: chunk 0 loaded and gathered, chunk 1 loaded.
+    Stage cur = OpenTile<RowT>(p, 0, firstTile, stride, tileEnd);
+    if (!cur.valid) return;
     B bc, bn;
-    ValT xg[8];
-    LoadStage<RowT, V, O, A>(p, cur, betaNz, bc);
-    GatherStage<RowT, V, O>(p, cur, bc, xg);
-    Stage nxt = NextStage<RowT>(p, cur, stride, tileEnd);
-    LoadStage<RowT, V, O, A>(p, nxt, betaNz, bn);
-    Acc prod[8];
+    ValT xg[kLaneItems];
+    LoadStage<RowT, V, O, kBeta>(p, cur, tail, lane, bc);
+    GatherStage<RowT, V, O>(p, cur, tail, lane, bc, xg);
+    Stage nxt = NextStage<RowT>(p, cur, firstTile, stride, tileEnd);
+    LoadStage<RowT, V, O, kBeta>(p, nxt, tail, lane, bn);
+    Acc prod[kLaneItems];
     Products<RowT, V, O, A>(bc, xg, prod);
     RowT rpc[2] = {bc.rp[0], bc.rp[1]};
     OutT yc[2] = {bc.yold[0], bc.yold[1]};
+    Acc chunkCarry = Zero<Acc>();
 
     while (cur.valid) {
-        // Keep two stages of memory traffic in flight while this one reduces.
-        GatherStage<RowT, V, O>(p, nxt, bn, xg);
-        const Stage after = NextStage<RowT>(p, nxt, stride, tileEnd);
+        // Keep two chunks of memory traffic in flight while this one reduces.
+        GatherStage<RowT, V, O>(p, nxt, tail, lane, bn, xg);
+        const Stage after = NextStage<RowT>(p, nxt, firstTile, stride, tileEnd);
         B ba;
-        LoadStage<RowT, V, O, A>(p, after, betaNz, ba);
+        LoadStage<RowT, V, O, kBeta>(p, after, tail, lane, ba);
 
-        __syncthreads();  // the previous stage is done with LDS
+        const int32_t c0 = cur.c0, c1 = cur.c1;
+        const int32_t d = static_cast<int32_t>(cur.k0 - cur.a0);  // slot of relative offset r is r + d
+        const int nr = cur.nr;
         if (cur.first) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int i = tid + h * kThreads;
-                if (i <= cur.nr) {
+                const int i = lane + h * kWave;
+                if (i <= nr) {
                     int64_t v = static_cast<int64_t>(rpc[h]) - cur.k0;
                     sRp[i] = static_cast<int32_t>(v < 0 ? 0 : v > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : v);
                 }
             }
-            if (tid == 0) sChunkCarry = Zero<Acc>();
+            chunkCarry = Zero<Acc>();
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sVal[Pad(4 * (tid + (j >> 2) * kThreads) + (j & 3))] = prod[j];
-        if (tid < kChunk / 32) sFlag[tid] = 0U;
-        __syncthreads();
-
-        const int32_t c0 = cur.c0, c1 = cur.c1;
-        const int32_t d = static_cast<int32_t>(cur.k0 - cur.a0);
-        const int nr = cur.nr;
+        if (lane < kWaveChunk / 32) sFlag[lane] = 0U;
+        WaveLdsSync();
         // Segment heads: first non-zero of each non-empty row that starts here.
+        int32_t rs[2], re[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int i = tid + h * kThreads;
-            if (i < nr) {
-                const int32_t s0 = sRp[i], e0 = sRp[i + 1];
-                if (e0 > s0 && s0 >= c0 && s0 < c1) {
-                    const int q = s0 + d;
-                    atomicOr(&sFlag[q >> 5], 1U << (q & 31));
-                }
+            const int i = lane + h * kWave;
+            rs[h] = i < nr ? sRp[i] : 0;
+            re[h] = i < nr ? sRp[i + 1] : 0;
+            if (i < nr && re[h] > rs[h] && rs[h] >= c0 && rs[h] < c1) {
+                const int q = rs[h] + d;
+                atomicOr(&sFlag[q >> 5], 1U << (q & 31));
             }
         }
-        __syncthreads();
+        WaveLdsSync();
+        const uint32_t bits = (sFlag[lane >> 2] >> ((lane & 3) * 8)) & 0xFFU;
 
-        // Lane-local segmented scan of 8 consecutive slots.
-        const uint32_t bits = (sFlag[tid >> 2] >> ((tid & 3) * 8)) & 0xFFU;
+        // Lane-local segmented scan of slots [8l, 8l+8).
+        Acc pre[kLaneItems];
         Acc run = Zero<Acc>();
 #pragma unroll
-        for (int j = 0; j < kIpt; ++j) {
-            const int q = tid * kIpt + j;
+        for (int j = 0; j < kLaneItems; ++j) {
             if (bits & (1U << j)) run = Zero<Acc>();
-            run = run + sVal[Pad(q)];
-            sVal[Pad(q)] = run;
+            run = run + prod[j];
+            pre[j] = run;
         }
-        const int first = bits ? __builtin_ctz(bits) : kIpt;
-        const int has = bits ? 1 : 0;
-
+        const int firstHead = bits ? __builtin_ctz(bits) : kLaneItems;
+        // Wave-wide exclusive segmented scan of the lane tails (carry-in from
+        // the previous chunk of the same block enters at lane 0).
         Acc v = run;
-        int f = has;
+        int f = bits ? 1 : 0;
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
             const Acc vo = ShflUp(v, off);
@@ -774,50 +819,43 @@ __global__ __launch_bounds__(kThreads) void SpmvPipeKernel(RowBlockParams p)
             ve = Zero<Acc>();
             fe = 0;
         }
-        if (lane == kWave - 1) {
-            sWaveV[wave] = v;
-            sWaveF[wave] = f;
+        const Acc carryIn = fe ? ve : chunkCarry + ve;
+        // Finished prefixes: slots before the first head continue the row
+        // that entered this lane.
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            sVal[kLaneItems * lane + j + lane] = j < firstHead ? pre[j] + carryIn : pre[j];
         }
-        __syncthreads();
-        Acc pv = sChunkCarry;
-        for (int u = 0; u < wave; ++u) {
-            if (sWaveF[u]) pv = sWaveV[u];
-            else pv = pv + sWaveV[u];
-        }
-        const Acc excl = fe ? ve : pv + ve;
-        sCarry[tid] = excl;
-        sFirst[tid] = first;
-        __syncthreads();
-        if (!cur.last && tid == kThreads - 1) sChunkCarry = has ? run : excl + run;
+        const Acc inclusive = f ? v : chunkCarry + v;
+        chunkCarry = ReadLane(inclusive, kWave - 1);
+        WaveLdsSync();
 
-        // Rows that end inside this chunk (each lane owns rows tid, tid+256).
+        // Rows that end inside this chunk (lane owns rows l and l+64).  Lanes
+        // without a finished row store into the sink, so the store is
+        // unconditional.
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int i = tid + h * kThreads;
-            if (i < nr) {
-                const int32_t s0 = sRp[i], e0 = sRp[i + 1];
-                bool done = false;
-                Acc sum = Zero<Acc>();
-                if (e0 <= s0) {
-                    done = (s0 >= c0 && s0 < c1) || (cur.last && s0 >= c1);
-                } else if (e0 > c0 && e0 <= c1) {
-                    const int q = e0 - 1 + d;
-                    const int t = q / kIpt;
-                    sum = sVal[Pad(q)];
-                    if ((q % kIpt) < sFirst[t]) sum = sum + sCarry[t];
-                    done = true;
-                }
-                if (done) {
-                    Acc r;
-                    if constexpr (A == AccKind::I64) {
-                        r = ScaledI64(sum, alpha, beta, betaNz ? OutToAcc<O, A>(yc[h]) : 0);
-                    } else {
-                        r = betaNz ? alpha * sum + beta * OutToAcc<O, A>(yc[h]) : alpha * sum;
-                    }
-                    y[(cur.r0 + i) * p.y_stride] = FromAcc<O, A>(r);
-                }
+            const int i = lane + h * kWave;
+            const int32_t s0 = rs[h], e0 = re[h];
+            const bool inRange = i < nr;
+            const bool empty = e0 <= s0;
+            const bool endsHere = !empty && e0 > c0 && e0 <= c1;
+            const bool done = inRange && ((empty && ((s0 >= c0 && s0 < c1) || (cur.last && s0 >= c1))) || endsHere);
+            const int q = endsHere ? e0 - 1 + d : 0;
+            Acc sum = sVal[q + q / kLaneItems];
+            if (!endsHere) sum = Zero<Acc>();
+            Acc r;
+            if constexpr (A == AccKind::I64) {
+                r = ScaledI64(sum, alpha, beta, kBeta ? OutToAcc<O, A>(yc[h]) : 0);
+            } else if constexpr (kBeta) {
+                r = alpha * sum + beta * OutToAcc<O, A>(yc[h]);
+            } else {
+                r = alpha * sum;
             }
+            OutT* dst = done ? y + (cur.r0 + i) * p.y_stride : sink;
+            *dst = FromAcc<O, A>(r);
         }
+        WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 
         // Rotate the pipeline.
         Products<RowT, V, O, A>(bn, xg, prod);
@@ -1003,6 +1041,7 @@ RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
     p.rp = At<void>(l.ws, l.layout.rowptr_offset);
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
     p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
+    p.sink = At<void>(l.ws, l.layout.sink_offset);
     p.col = l.col;
     p.col_stride = l.col_stride;
     p.val = l.val;
@@ -1048,7 +1087,7 @@ int ResidentBlocksPerCu(const void* kernel)
     auto it = cache.find({dev, kernel});
     if (it != cache.end()) return it->second;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess || n < 1) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWave * kWavesPerGroup, 0) != hipSuccess || n < 1) n = 1;
     cache[{dev, kernel}] = n;
     return n;
 }
@@ -1071,16 +1110,19 @@ int CuCount()
 // Persistent grid: the blocks of each XCD's range are split evenly over
 // J <= resident-slots workers so that every worker runs the same number of
 // blocks (+-1), i.e. J = ceil(per / ceil(per / slots)).
+// Each workgroup carries kWavesPerGroup independent wave workers.
 void PersistentShape(RowBlockParams& p, const void* kernel, unsigned& grid)
 {
     const int64_t per = (p.num_blocks + kXcds - 1) / kXcds;
-    const int64_t slots = static_cast<int64_t>(CuCount() / kXcds) * ResidentBlocksPerCu(kernel);
+    const int64_t slots =
+        static_cast<int64_t>(CuCount() / kXcds) * ResidentBlocksPerCu(kernel) * kWavesPerGroup;
     const int64_t rounds = (per + slots - 1) / slots;
     int64_t j = rounds > 0 ? (per + rounds - 1) / rounds : 1;
-    if (j < 1) j = 1;
+    j = (j + kWavesPerGroup - 1) / kWavesPerGroup * kWavesPerGroup;  // whole workgroups
+    if (j < kWavesPerGroup) j = kWavesPerGroup;
     p.per_xcd = per;
     p.workers_per_xcd = static_cast<int32_t>(j);
-    grid = static_cast<unsigned>(j * kXcds);
+    grid = static_cast<unsigned>((j / kWavesPerGroup) * kXcds);
 }
 
 template <typename RowT, ValKind V, OutKind O, AccKind A>
@@ -1089,14 +1131,24 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     RowBlockParams p = MakeRowBlockParams(l);
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
-    const bool vec = kCanVec && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && l.y_stride == 1 &&
-                     Aligned16(l.col) && Aligned16(l.val);
+    // The wave kernel issues its loads unconditionally (clamped into the
+    // arrays), which needs at least one 16-byte group of col_ind / values.
+    const bool vec = kCanVec && l.nnz >= 4 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 &&
+                     l.y_stride == 1 && Aligned16(l.col) && Aligned16(l.val);
     if constexpr (kCanVec) {
         if (vec) {
-            const void* k = reinterpret_cast<const void*>(&SpmvPipeKernel<RowT, V, O, A>);
+            // beta is known on the host unless it lives in device memory.
+            const bool betaNz = l.device_scalars || l.beta_re != 0.0f || l.beta_im != 0.0f || l.beta_i != 0;
             unsigned pg = 0;
-            PersistentShape(p, k, pg);
-            hipLaunchKernelGGL((SpmvPipeKernel<RowT, V, O, A>), dim3(pg), dim3(kThreads), 0, stream, p);
+            if (betaNz) {
+                PersistentShape(p, reinterpret_cast<const void*>(&SpmvWaveKernel<RowT, V, O, A, true>), pg);
+                hipLaunchKernelGGL((SpmvWaveKernel<RowT, V, O, A, true>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
+                                   stream, p);
+            } else {
+                PersistentShape(p, reinterpret_cast<const void*>(&SpmvWaveKernel<RowT, V, O, A, false>), pg);
+                hipLaunchKernelGGL((SpmvWaveKernel<RowT, V, O, A, false>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
+                                   stream, p);
+            }
             return 0;
         }
     }
@@ -1192,6 +1244,7 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     h.rowptr_offset = l.layout.rowptr_offset;
     h.blocks_offset = l.layout.blocks_offset;
     h.block_nnz_offset = l.layout.block_nnz_offset;
+    h.sink_offset = l.layout.sink_offset;
     h.acc_offset = l.layout.acc_offset;
     h.rowptr_bytes = l.layout.rowptr_bytes;
     h.index_base = static_cast<uint32_t>(l.base);

@@ -9,7 +9,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(os.path.dirname(_HERE), "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libaclsparse_hip.so")
+LIB_PATH = os.environ.get("ACLSPARSE_HIP_LIB", os.path.join(LIB_DIR, "libaclsparse_hip.so"))
 
 
 class Status(enum.IntEnum):

@@ -261,13 +261,13 @@ void oracle_spmv_c64(int64_t rows, int64_t cols, const int64_t *rp, const int32_
 
 /* ----------------------------- partition ---------------------------------- */
 
-/* T = min(8176, 1984 + floor(16*1984*rows/nnz)) (8176 when nnz == 0);
+/* T = min(2032, 496 + floor(16*496*rows/nnz)) (2032 when nnz == 0);
  * blocks = ceil((16*rows + nnz) / T). */
 int64_t oracle_items_per_block(int64_t rows, int64_t nnz)
 {
-    if (nnz == 0) return 8176;
-    const uint64_t t = 1984u + ((uint64_t)(16 * 1984) * (uint64_t)rows) / (uint64_t)nnz;
-    return t > 8176u ? 8176 : (int64_t)t;
+    if (nnz == 0) return 2032;
+    const uint64_t t = 496u + ((uint64_t)(16 * 496) * (uint64_t)rows) / (uint64_t)nnz;
+    return t > 2032u ? 2032 : (int64_t)t;
 }
 
 int64_t oracle_num_blocks(int64_t rows, int64_t nnz)

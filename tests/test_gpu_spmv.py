@@ -303,3 +303,31 @@ def test_spmv_npu_mirror_and_mv(dev):
     y2 = mv(a, d.x)
     torch.cuda.synchronize()
     assert torch.equal(y2, y)
+
+
+@pytest.mark.parametrize("nnz", [1, 2, 3, 5, 7])
+def test_tiny_nnz_counts(nnz, dev):
+    # fewer non-zeros than one 16-byte group, and nnz % 4 != 0 tails
+    rows, cols = 3, 4
+    lengths = torch.tensor([nnz, 0, 0], dtype=torch.int64)
+    g = torch.Generator().manual_seed(nnz)
+    rp, col = wl.csr_from_lengths(lengths, cols, g, "cpu", distinct=False)
+    w = wl.Workload("tiny", rows, cols, rp.to(torch.int32), col, torch.rand(col.numel(), generator=g),
+                    torch.rand(cols, generator=g), torch.rand(rows, generator=g), 2.0, 0.5)
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
+
+
+def test_long_last_row_with_beta(dev):
+    # the last row spans many partition windows, so trailing blocks start at row == rows
+    lengths = torch.tensor([2] * 300 + [60000], dtype=torch.int64)
+    g = torch.Generator().manual_seed(11)
+    rp, col = wl.csr_from_lengths(lengths, 100000, g, "cpu")
+    n = col.numel()
+    w = wl.Workload("long_last", lengths.numel(), 100000, rp.to(torch.int32), col,
+                    torch.rand(n, generator=g) * 2 - 1, torch.rand(100000, generator=g) * 2 - 1,
+                    torch.rand(lengths.numel(), generator=g) * 2 - 1, 1.0, 3.0)
+    norm, blocks, _ = oracle.partition(rp.numpy(), n)
+    assert (blocks[:-1] == lengths.numel()).any(), "fixture must produce blocks that start at row == rows"
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
