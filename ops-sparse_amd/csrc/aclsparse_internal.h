@@ -231,3 +231,51 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream);
 int LaunchSpmvCompute(const SpmvLaunch& l, void* stream);
 
 }  // namespace aclsp
+
+// ---------------------------------------------------------------------------
+// SpMVOp (Z = alpha*A*X + beta*Y with a compensated dot product).
+// ---------------------------------------------------------------------------
+struct aclsparseSpMVOpDescr {
+    uint32_t signature = aclsp::kSpMVOpDescrSignature;
+    uint64_t m = 0, n = 0, nnz = 0;
+    aclsparseIndexBase_t base = ACL_SPARSE_INDEX_BASE_ZERO;
+    aclsparseIndexType_t row_type = ACL_SPARSE_INDEX_32I;
+    const void* row_offsets = nullptr;
+    const int32_t* col_ind = nullptr;
+    const float* values = nullptr;
+    aclsparseSpMVOpAlg_t alg = ACL_SPARSE_SPMVOP_ALG1;
+    void* buffer = nullptr;   // ALG2 reorder / bin_edge tables (caller-owned)
+    uint32_t num_bins = 0;    // ALG2 bins (workgroups)
+};
+
+struct aclsparseSpMVOpPlan {
+    uint32_t signature = aclsp::kSpMVOpPlanSignature;
+    aclsparseSpMVOpDescr* descr = nullptr;  // weak: the descriptor must outlive the plan
+    aclsparseSpMVOpAlg_t alg = ACL_SPARSE_SPMVOP_ALG1;
+};
+
+namespace aclsp {
+
+// ALG2 workspace: the reference's fixed part (sparse/spmv_op/arch35/spmv_op.h:65-86):
+//   [0,256) header | reorder[m] | tmpReorder[m] | scratch[m] | tmpScratch[m] |
+//   binEdge[bins+1], every array 64-byte aligned, followed by this build's
+//   extension: running[m] (int64 inclusive sums of the sorted row lengths) and
+//   the device sort/scan temporary storage.
+constexpr size_t kOpHeaderBytes = 256;
+constexpr uint32_t kOpRowsPerBin = 128;
+
+struct SpmvOpLayout {
+    size_t reorder = 0, tmp_reorder = 0, scratch = 0, tmp_scratch = 0, bin_edge = 0;
+    size_t running = 0, temp = 0, temp_bytes = 0, total = 0;
+};
+
+// numBins = min(CUs, ceil(m/128)) (sparse/spmv_op/arch35/spmv_op_host.cpp:305-327 with
+// the AIV core count replaced by the CU count).
+uint32_t SpmvOpNumBins(int64_t m);
+SpmvOpLayout SpmvOpComputeLayout(int64_t m, uint32_t bins);
+
+int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream);
+int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
+                        float beta, const void* alphaPtr, const void* betaPtr, bool deviceScalars, void* stream);
+
+}  // namespace aclsp

@@ -1,0 +1,404 @@
+// gfx950 kernels of aclsparseSpMVOp: Z = alpha*A*X + beta*Y (fp32) with a
+// doubly compensated dot product per row.
+//
+// The reference runs one scalar thread per row with Priest's accumulator
+// (TwoProduct by FMA + two TwoSum stages, sparse/spmv_op/arch35/spmv_op_kernel.cpp:87-128)
+// and builds the ALG2 tables with one scalar thread (:425-540).  Here:
+//  * W lanes of a wave64 share a row (W from the mean row length of the
+//    matrix or of the ALG2 bin); every lane keeps its own Priest triple
+//    (hi, md, lo) over a strided subset of the row and the W triples are
+//    merged by an exact TwoSum butterfly.  The order is fixed, so results
+//    are bit-reproducible run to run.
+//  * ALG2 preprocess is parallel: row lengths, a stable descending radix
+//    sort (hipCUB), an int64 inclusive scan, and the bin edges by binary
+//    search plus the reference's one-edge-per-row rule.  reorder, scratch
+//    and bin_edge are bit-identical to the reference's serial tables.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <cstdint>
+
+#include "aclsparse_internal.h"
+
+// The error-free transformations below (TwoSum, TwoProduct) rely on every
+// operation being rounded as written: no contraction of a*b + c into FMA.
+#pragma clang fp contract(off)
+
+namespace aclsp {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+
+struct Triple {
+    float hi, md, lo;
+};
+
+// Priest's update of (hi, md, lo) with the exact product a*b
+// (same recurrence as spmv_op_kernel.cpp:100-124).
+__device__ __forceinline__ void PriestAdd(Triple& t, float a, float b)
+{
+    const float prod = a * b;
+    const float pi = __fmaf_rn(a, b, -prod);
+    const float s1 = t.hi + prod;
+    const float v1 = s1 - t.hi;
+    const float e1 = (t.hi - (s1 - v1)) + (prod - v1);
+    t.hi = s1;
+    const float ee = e1 + pi;
+    const float s2 = t.md + ee;
+    const float v2 = s2 - t.md;
+    const float e2 = (t.md - (s2 - v2)) + (ee - v2);
+    t.md = s2;
+    t.lo = t.lo + e2;
+}
+
+__device__ __forceinline__ void TwoSum(float a, float b, float& s, float& e)
+{
+    s = a + b;
+    const float v = s - a;
+    e = (a - (s - v)) + (b - v);
+}
+
+// Merges two triples keeping the rounding error of both leading sums.
+__device__ __forceinline__ Triple Merge(const Triple& a, const Triple& b)
+{
+    Triple r;
+    float e1, e2;
+    TwoSum(a.hi, b.hi, r.hi, e1);
+    float m;
+    TwoSum(a.md, b.md, m, e2);
+    float e3;
+    TwoSum(m, e1, r.md, e3);
+    r.lo = a.lo + b.lo + e2 + e3;
+    return r;
+}
+
+__device__ __forceinline__ Triple ShflXor(const Triple& t, int m)
+{
+    return Triple{__shfl_xor(t.hi, m, kWave), __shfl_xor(t.md, m, kWave), __shfl_xor(t.lo, m, kWave)};
+}
+
+struct OpParams {
+    const void* rp;
+    const int32_t* col;
+    const float* val;
+    const float* x;
+    const float* y;
+    float* z;
+    int64_t m, n, nnz;
+    int32_t base;
+    float alpha, beta;
+    const float* alpha_ptr;
+    const float* beta_ptr;
+    int32_t device_scalars;
+    int32_t wlog;             // ALG1: log2 lanes per row
+    const int32_t* reorder;   // ALG2
+    const int32_t* bin_edge;  // ALG2
+    const int64_t* running;   // ALG2 inclusive sums of sorted lengths
+};
+
+__device__ __forceinline__ void Scalars(const OpParams& p, float& a, float& b)
+{
+    a = p.device_scalars ? *p.alpha_ptr : p.alpha;
+    b = p.device_scalars ? *p.beta_ptr : p.beta;
+}
+
+// One row reduced by the W = 2^wlog lanes that share `sub`; returns the
+// merged triple on every lane of the group.
+template <typename RowT>
+__device__ __forceinline__ Triple RowDot(const OpParams& p, int64_t row, bool active, int wlog, int sub)
+{
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    Triple t{0.0f, 0.0f, 0.0f};
+    if (active) {
+        const int64_t s = static_cast<int64_t>(rp[row]) - p.base;
+        const int64_t e = static_cast<int64_t>(rp[row + 1]) - p.base;
+        for (int64_t q = s + sub; q < e; q += (int64_t{1} << wlog)) {
+            const int64_t c = static_cast<int64_t>(p.col[q]) - p.base;
+            PriestAdd(t, p.val[q], p.x[c]);
+        }
+    }
+    for (int msk = (1 << wlog) >> 1; msk > 0; msk >>= 1) t = Merge(t, ShflXor(t, msk));
+    return t;
+}
+
+// z = a*(hi + md + lo) + b*y.  The reference folds this as
+// fma(a, hi, fma(a, md + lo, b*y)) (spmv_op_kernel.cpp:177-181), whose inner
+// rounding happens at the magnitude of b*y: when A*x nearly cancels y the
+// relative error of z grows without bound.  Here both leading products are
+// split exactly (TwoProduct by FMA) and added by TwoSum, so z is rounded
+// once at its own magnitude, up to the small tail terms.
+__device__ __forceinline__ void StoreZ(const OpParams& p, int64_t row, const Triple& t, float a, float b)
+{
+    const float yv = b == 0.0f ? 0.0f : p.y[row];
+    const float p1 = a * t.hi;
+    const float e1 = __fmaf_rn(a, t.hi, -p1);
+    const float p2 = b * yv;
+    const float e2 = __fmaf_rn(b, yv, -p2);
+    float s, es;
+    TwoSum(p1, p2, s, es);
+    const float tail = __fmaf_rn(a, t.md + t.lo, es + (e1 + e2));
+    // non-finite terms: keep the reference's fold so Inf/NaN propagate alike
+    p.z[row] = __builtin_isfinite(s) ? s + tail : __fmaf_rn(a, t.hi, __fmaf_rn(a, t.md + t.lo, p2));
+}
+
+// ALG1: rows in natural order, 64/W rows per wave pass, grid-stride.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void SpmvOpAlg1Kernel(OpParams p)
+{
+    float a, b;
+    Scalars(p, a, b);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wlog = p.wlog;
+    const int sub = lane & ((1 << wlog) - 1);
+    const int64_t rowsPerWave = kWave >> wlog;
+    const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / kWave;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
+    for (int64_t r0 = wave * rowsPerWave; r0 < p.m; r0 += waves * rowsPerWave) {
+        const int64_t row = r0 + (lane >> wlog);
+        const bool active = row < p.m;
+        const Triple t = RowDot<RowT>(p, active ? row : 0, active, wlog, sub);
+        if (active && sub == 0) StoreZ(p, row, t, a, b);
+    }
+}
+
+// ALG2: workgroup b owns sorted positions [bin_edge[b], bin_edge[b+1]); the
+// original row of position i is reorder[i]; W comes from the bin's mean
+// row length.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void SpmvOpAlg2Kernel(OpParams p)
+{
+    float a, b;
+    Scalars(p, a, b);
+    const int32_t lo = p.bin_edge[blockIdx.x];
+    const int32_t hi = p.bin_edge[blockIdx.x + 1];
+    if (hi <= lo) return;
+    const int64_t binNnz = p.running[hi - 1] - (lo > 0 ? p.running[lo - 1] : 0);
+    const int64_t mean = binNnz / (hi - lo);
+    int wlog = 0;
+    while (wlog < 6 && (int64_t{4} << wlog) < mean) ++wlog;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int sub = lane & ((1 << wlog) - 1);
+    const int rowsPerWave = kWave >> wlog;
+    const int wv = threadIdx.x / kWave;
+    for (int32_t i0 = lo + wv * rowsPerWave; i0 < hi; i0 += (kThreads / kWave) * rowsPerWave) {
+        const int32_t i = i0 + (lane >> wlog);
+        const bool active = i < hi;
+        const int64_t row = active ? p.reorder[i] : 0;
+        const Triple t = RowDot<RowT>(p, row, active, wlog, sub);
+        if (active && sub == 0) StoreZ(p, row, t, a, b);
+    }
+}
+
+// nnz == 0: Z = beta*Y; Y is not read when beta == 0.
+__global__ __launch_bounds__(kThreads) void SpmvOpBetaYKernel(OpParams p)
+{
+    float a, b;
+    Scalars(p, a, b);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < p.m;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const float yv = b == 0.0f ? 0.0f : p.y[i];
+        p.z[i] = b * yv;
+    }
+}
+
+// ---------------------------- ALG2 preprocess -----------------------------
+
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void OpLengthsKernel(const RowT* rp, int64_t m, int32_t* len, int32_t* iota)
+{
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        len[i] = static_cast<int32_t>(rp[i + 1] - rp[i]);
+        iota[i] = static_cast<int32_t>(i);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void OpWidenKernel(const int32_t* sortedLen, int64_t m, int32_t* scratch,
+                                                          int64_t* running)
+{
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < m;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        scratch[i] = sortedLen[i];
+        running[i] = sortedLen[i];
+    }
+}
+
+// bin_edge[b] for b in [1, bins): the first sorted position i whose running
+// sum reaches b*ceil(total/bins), but never the same position as the
+// previous edge (the reference advances one edge per row); edges past the
+// last row are m (spmv_op_kernel.cpp:505-528).
+__global__ __launch_bounds__(kThreads) void OpBinEdgeKernel(const int64_t* running, int64_t m, uint32_t bins,
+                                                            int32_t* binEdge)
+{
+    __shared__ int64_t lb[kThreads + 1];
+    const int64_t total = running[m - 1];
+    const int64_t perBin = (total > 0 && bins > 0) ? (total + bins - 1) / bins : 0;
+    for (uint32_t b = threadIdx.x + 1; b < bins; b += kThreads) {
+        const int64_t target = perBin * static_cast<int64_t>(b);
+        int64_t lo = 0, hi = m;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (running[mid] >= target) hi = mid;
+            else lo = mid + 1;
+        }
+        lb[b] = lo;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        binEdge[0] = 0;
+        uint32_t b = 1;
+        int64_t prev = -1;
+        for (; b < bins; ++b) {
+            const int64_t i = lb[b] > prev + 1 ? lb[b] : prev + 1;
+            if (i >= m) break;
+            binEdge[b] = static_cast<int32_t>(i + 1);
+            prev = i;
+        }
+        for (; b <= bins; ++b) binEdge[b] = static_cast<int32_t>(m);
+    }
+}
+
+int CuCount()
+{
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    return n;
+}
+
+size_t SortScanTempBytes(int64_t m)
+{
+    size_t sortBytes = 0, scanBytes = 0;
+    const int items = static_cast<int>(m);
+    if (hipcub::DeviceRadixSort::SortPairsDescending(nullptr, sortBytes, static_cast<int32_t*>(nullptr),
+                                                     static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
+                                                     static_cast<int32_t*>(nullptr), items) != hipSuccess) {
+        sortBytes = static_cast<size_t>(m) * 16 + (1 << 20);
+    }
+    if (hipcub::DeviceScan::InclusiveSum(nullptr, scanBytes, static_cast<int64_t*>(nullptr),
+                                         static_cast<int64_t*>(nullptr), items) != hipSuccess) {
+        scanBytes = static_cast<size_t>(m) * 8 + (1 << 20);
+    }
+    return sortBytes > scanBytes ? sortBytes : scanBytes;
+}
+
+int GridFor(int64_t n)
+{
+    int64_t g = (n + kThreads - 1) / kThreads;
+    return static_cast<int>(g < 1 ? 1 : g > 65536 ? 65536 : g);
+}
+
+}  // namespace
+
+uint32_t SpmvOpNumBins(int64_t m)
+{
+    if (m <= 0) return 0;
+    const int64_t need = (m + kOpRowsPerBin - 1) / kOpRowsPerBin;
+    const int64_t cus = CuCount();
+    const int64_t bins = need < cus ? need : cus;
+    return static_cast<uint32_t>(bins < 1 ? 1 : bins);
+}
+
+SpmvOpLayout SpmvOpComputeLayout(int64_t m, uint32_t bins)
+{
+    SpmvOpLayout l;
+    const size_t rb = static_cast<size_t>(m) * sizeof(int32_t);
+    l.reorder = kOpHeaderBytes;
+    l.tmp_reorder = AlignUp(l.reorder + rb);
+    l.scratch = AlignUp(l.tmp_reorder + rb);
+    l.tmp_scratch = AlignUp(l.scratch + rb);
+    l.bin_edge = AlignUp(l.tmp_scratch + rb);
+    l.running = AlignUp(l.bin_edge + static_cast<size_t>(bins + 1) * sizeof(int32_t));
+    l.temp = AlignUp(l.running + static_cast<size_t>(m) * sizeof(int64_t));
+    l.temp_bytes = m > 0 ? SortScanTempBytes(m) : 0;
+    l.total = AlignUp(l.temp + l.temp_bytes + 256);  // +256: the temp area is re-aligned to 256 bytes
+    return l;
+}
+
+int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream)
+{
+    const int64_t m = static_cast<int64_t>(d.m);
+    if (m <= 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const SpmvOpLayout l = SpmvOpComputeLayout(m, d.num_bins);
+    uint8_t* ws = static_cast<uint8_t*>(d.buffer);
+    int32_t* reorder = reinterpret_cast<int32_t*>(ws + l.reorder);
+    int32_t* tmpReorder = reinterpret_cast<int32_t*>(ws + l.tmp_reorder);
+    int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
+    int32_t* tmpScratch = reinterpret_cast<int32_t*>(ws + l.tmp_scratch);
+    int32_t* binEdge = reinterpret_cast<int32_t*>(ws + l.bin_edge);
+    int64_t* running = reinterpret_cast<int64_t*>(ws + l.running);
+    // device sort/scan temporary storage, aligned to 256 bytes in absolute terms
+    void* temp = reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(ws + l.temp) + 255) & ~uintptr_t{255});
+    size_t tempBytes = l.temp_bytes;
+    if (d.row_type == ACL_SPARSE_INDEX_64I) {
+        hipLaunchKernelGGL(OpLengthsKernel<int64_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
+                           static_cast<const int64_t*>(d.row_offsets), m, scratch, tmpReorder);
+    } else {
+        hipLaunchKernelGGL(OpLengthsKernel<int32_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
+                           static_cast<const int32_t*>(d.row_offsets), m, scratch, tmpReorder);
+    }
+    // Stable: equal lengths keep ascending row order, as the reference's
+    // merge that takes the left run on ties.
+    if (hipcub::DeviceRadixSort::SortPairsDescending(temp, tempBytes, scratch, tmpScratch, tmpReorder, reorder,
+                                                     static_cast<int>(m), 0, 32, s) != hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(OpWidenKernel, dim3(GridFor(m)), dim3(kThreads), 0, s, tmpScratch, m, scratch, running);
+    tempBytes = l.temp_bytes;
+    if (hipcub::DeviceScan::InclusiveSum(temp, tempBytes, running, running, static_cast<int>(m), s) != hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(OpBinEdgeKernel, dim3(1), dim3(kThreads), 0, s, running, m, d.num_bins, binEdge);
+    return 0;
+}
+
+int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
+                        float beta, const void* alphaPtr, const void* betaPtr, bool deviceScalars, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    OpParams p{};
+    p.rp = d.row_offsets;
+    p.col = d.col_ind;
+    p.val = d.values;
+    p.x = static_cast<const float*>(x);
+    p.y = static_cast<const float*>(y);
+    p.z = static_cast<float*>(z);
+    p.m = static_cast<int64_t>(d.m);
+    p.n = static_cast<int64_t>(d.n);
+    p.nnz = static_cast<int64_t>(d.nnz);
+    p.base = d.base == ACL_SPARSE_INDEX_BASE_ONE ? 1 : 0;
+    p.alpha = alpha;
+    p.beta = beta;
+    p.alpha_ptr = static_cast<const float*>(alphaPtr);
+    p.beta_ptr = static_cast<const float*>(betaPtr);
+    p.device_scalars = deviceScalars ? 1 : 0;
+    if (p.nnz == 0) {
+        hipLaunchKernelGGL(SpmvOpBetaYKernel, dim3(GridFor(p.m)), dim3(kThreads), 0, s, p);
+        return 0;
+    }
+    const bool i64 = d.row_type == ACL_SPARSE_INDEX_64I;
+    if (d.alg == ACL_SPARSE_SPMVOP_ALG2) {
+        const SpmvOpLayout l = SpmvOpComputeLayout(p.m, d.num_bins);
+        uint8_t* ws = static_cast<uint8_t*>(d.buffer);
+        p.reorder = reinterpret_cast<const int32_t*>(ws + l.reorder);
+        p.bin_edge = reinterpret_cast<const int32_t*>(ws + l.bin_edge);
+        p.running = reinterpret_cast<const int64_t*>(ws + l.running);
+        if (i64) hipLaunchKernelGGL(SpmvOpAlg2Kernel<int64_t>, dim3(d.num_bins), dim3(kThreads), 0, s, p);
+        else hipLaunchKernelGGL(SpmvOpAlg2Kernel<int32_t>, dim3(d.num_bins), dim3(kThreads), 0, s, p);
+        return 0;
+    }
+    const int64_t mean = p.nnz / p.m;
+    int wlog = 0;
+    while (wlog < 6 && (int64_t{4} << wlog) < mean) ++wlog;
+    p.wlog = wlog;
+    const int64_t waves = (p.m + (kWave >> wlog) - 1) / (kWave >> wlog);
+    int64_t grid = (waves + kThreads / kWave - 1) / (kThreads / kWave);
+    grid = grid < 1 ? 1 : grid > 65536 ? 65536 : grid;
+    if (i64) hipLaunchKernelGGL(SpmvOpAlg1Kernel<int64_t>, dim3(grid), dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(SpmvOpAlg1Kernel<int32_t>, dim3(grid), dim3(kThreads), 0, s, p);
+    return 0;
+}
+
+}  // namespace aclsp

@@ -161,9 +161,7 @@ def lib():
                 "(there is no CPU fallback for the SpMV path)")
         handle = ctypes.CDLL(LIB_PATH)
         for name, args in SIGNATURES.items():
-            fn = getattr(handle, name, None)
-            if fn is None:
-                continue
+            fn = getattr(handle, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
         _LIB = handle

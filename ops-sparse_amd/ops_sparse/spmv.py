@@ -294,3 +294,62 @@ def mv(mat, vec):
     plan.preprocess()
     plan.run()
     return y
+
+
+class SpMVOp:
+    """aclsparseSpMVOp on torch tensors: Z = alpha*A*X + beta*Y (fp32, NON_TRANSPOSE).
+
+    Mirrors the reference's seven-call sequence (sparse/spmv_op/arch35/spmv_op_host.cpp):
+    bufferSize -> createDescr (ALG2 builds the reorder / bin_edge tables) ->
+    createPlan -> execute (:meth:`run`) -> destroyPlan / destroyDescr.
+    """
+
+    def __init__(self, rows, cols, row_ptr, col_ind, values, x, y, z, alg=_lib.SpMVOpAlg.DEFAULT, base=0):
+        self._lib = _lib.lib()
+        self.handle = Handle(_stream_ptr(values.device))
+        self.mat = CsrDescr(rows, cols, row_ptr, col_ind, values, base)
+        self.x = DnVecDescr(cols, x)
+        self.y = DnVecDescr(rows, y)
+        self.z = DnVecDescr(rows, z)
+        self.tensors = (row_ptr, col_ind, values, x, y, z)
+        size = ctypes.c_size_t(0)
+        check("aclsparseSpMVOp_bufferSize", self._lib.aclsparseSpMVOp_bufferSize(
+            self.handle.h, int(Operation.NON_TRANSPOSE), self.mat.d, self.x.d, self.y.d, self.z.d,
+            int(DataType.FLOAT), int(alg), ctypes.byref(size)))
+        self.buffer_size = size.value
+        self.buffer = torch.empty(max(size.value, 64), dtype=torch.uint8, device=values.device)
+        self.descr = ctypes.c_void_p(0)
+        check("aclsparseSpMVOp_createDescr", self._lib.aclsparseSpMVOp_createDescr(
+            self.handle.h, ctypes.byref(self.descr), int(Operation.NON_TRANSPOSE), self.mat.d, self.x.d, self.y.d,
+            self.z.d, int(DataType.FLOAT), int(alg), ctypes.c_void_p(self.buffer.data_ptr())))
+        self.plan = ctypes.c_void_p(0)
+        check("aclsparseSpMVOp_createPlan", self._lib.aclsparseSpMVOp_createPlan(
+            self.handle.h, self.descr, ctypes.byref(self.plan), None, 0))
+
+    def run(self, alpha=1.0, beta=0.0):
+        """Execute; alpha/beta are Python floats (HOST pointer mode) or one-element
+        device tensors (the handle is switched to DEVICE pointer mode)."""
+        if isinstance(alpha, torch.Tensor):
+            self.handle.set_pointer_mode(PointerMode.DEVICE)
+            a, b = ctypes.c_void_p(alpha.data_ptr()), ctypes.c_void_p(beta.data_ptr())
+            check("aclsparseSpMVOp", self._lib.aclsparseSpMVOp(
+                self.handle.h, self.plan, a, b, self.x.d, self.y.d, self.z.d))
+            return
+        self.handle.set_pointer_mode(PointerMode.HOST)
+        a, b = ctypes.c_float(alpha), ctypes.c_float(beta)
+        check("aclsparseSpMVOp", self._lib.aclsparseSpMVOp(
+            self.handle.h, self.plan, ctypes.byref(a), ctypes.byref(b), self.x.d, self.y.d, self.z.d))
+
+    def close(self):
+        if self.plan:
+            self._lib.aclsparseSpMVOp_destroyPlan(self.plan)
+            self.plan = ctypes.c_void_p(0)
+        if self.descr:
+            self._lib.aclsparseSpMVOp_destroyDescr(self.descr)
+            self.descr = ctypes.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

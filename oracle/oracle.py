@@ -206,3 +206,27 @@ MIXED_TOL = {
     "bfloat16": (2.0 ** -6, 2.0 ** -6, 1.0, 0.99),
     "int32": (0.0, 0.0, 0.0, 1.0),
 }
+
+
+def spmvop_tables(row_ptr, num_blocks):
+    """(reorder, scratch, bin_edge) of the reference's SpMVOp ALG2 preprocess."""
+    rp = _i64(row_ptr)
+    m = rp.size - 1
+    reorder = np.empty(max(m, 1), dtype=np.int32)
+    scratch = np.empty(max(m, 1), dtype=np.int32)
+    t1 = np.empty(max(m, 1), dtype=np.int32)
+    t2 = np.empty(max(m, 1), dtype=np.int32)
+    edge = np.empty(num_blocks + 1, dtype=np.int32)
+    lib().oracle_spmvop_tables(ctypes.c_int32(m), _p(rp), ctypes.c_uint32(num_blocks), _p(reorder), _p(scratch),
+                               _p(t1), _p(t2), _p(edge))
+    return reorder[:m], scratch[:m], edge
+
+
+def verify_mere_mare(golden, actual, threshold, multiplier):
+    """(passed, mere, mare) of the reference's MERE/MARE strategy."""
+    g = np.ascontiguousarray(golden, dtype=np.float32)
+    a = np.ascontiguousarray(actual, dtype=np.float32)
+    mere, mare = ctypes.c_double(0), ctypes.c_double(0)
+    ok = lib().oracle_verify_mere_mare(_I(g.size), _p(g), _p(a), _D(threshold), _D(multiplier), ctypes.byref(mere),
+                                       ctypes.byref(mare))
+    return bool(ok), mere.value, mare.value

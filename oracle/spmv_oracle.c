@@ -27,6 +27,9 @@
  *                          counterpart; restated from its definition:
  *                          block b starts at the first row r with
  *                          16*r + rowOffset[r] >= b*T)
+ *   oracle_spmvop_tables   SpMVOp ALG2 reorder / scratch / bin_edge
+ *                          (sparse/spmv_op/arch35/spmv_op_kernel.cpp:425-540)
+ *   oracle_verify_mere_mare MERE/MARE check, test/frame/verify.h:126-175
  *   oracle_verify_mixed    Verification() mixed tolerance,
  *                          test/spmv/arch22/spmv_test_verification.h:23-101
  *
@@ -297,6 +300,79 @@ void oracle_spmv_partition(int64_t rows, int64_t nnz, const int64_t *rowPtr, int
     }
     blocks[nb] = (int32_t)rows;
     blockNnz[nb] = norm[rows];
+}
+
+/* ---------------------------- SpMVOp ALG2 ---------------------------------- */
+
+/* Restates the reference's ALG2 tables (sparse/spmv_op/arch35/spmv_op_kernel.cpp:425-540)
+ * for a given bin count: scratch[i] = rowPtr[i+1]-rowPtr[i], reorder = iota,
+ * bottom-up merge sort descending by scratch taking the left run on ties,
+ * then bin_edge by the running-sum loop.  tmp arrays: m entries each. */
+void oracle_spmvop_tables(int32_t m, const int64_t *rowPtr, uint32_t numBlocks, int32_t *reorder, int32_t *scratch,
+                          int32_t *tmpReorder, int32_t *tmpNnz, int32_t *binEdge)
+{
+    for (int32_t i = 0; i < m; ++i) {
+        scratch[i] = (int32_t)(rowPtr[i + 1] - rowPtr[i]);
+        reorder[i] = i;
+    }
+    for (int32_t width = 1; width < m; width *= 2) {
+        for (int32_t i = 0; i < m; i += 2 * width) {
+            const int32_t left = i;
+            const int32_t mid = (i + width < m) ? (i + width) : m;
+            const int32_t right = (i + 2 * width < m) ? (i + 2 * width) : m;
+            int32_t a = left, b = mid, k = left;
+            while (a < mid && b < right) {
+                if (scratch[a] >= scratch[b]) { tmpReorder[k] = reorder[a]; tmpNnz[k] = scratch[a]; ++a; }
+                else { tmpReorder[k] = reorder[b]; tmpNnz[k] = scratch[b]; ++b; }
+                ++k;
+            }
+            while (a < mid) { tmpReorder[k] = reorder[a]; tmpNnz[k] = scratch[a]; ++a; ++k; }
+            while (b < right) { tmpReorder[k] = reorder[b]; tmpNnz[k] = scratch[b]; ++b; ++k; }
+            for (int32_t idx = left; idx < right; ++idx) {
+                reorder[idx] = tmpReorder[idx];
+                scratch[idx] = tmpNnz[idx];
+            }
+        }
+    }
+    int64_t total = 0;
+    for (int32_t i = 0; i < m; ++i) total += scratch[i];
+    const int64_t perBlock = (total > 0 && numBlocks > 0) ? (total + numBlocks - 1) / numBlocks : 0;
+    binEdge[0] = 0;
+    uint32_t bin = 1;
+    int64_t running = 0;
+    for (int32_t i = 0; i < m; ++i) {
+        running += scratch[i];
+        if (bin < numBlocks && running >= perBlock * (int64_t)bin) {
+            binEdge[bin] = i + 1;
+            ++bin;
+        }
+    }
+    while (bin <= numBlocks) binEdge[bin++] = m;
+}
+
+/* MERE/MARE of test/frame/verify.h:126-175 (epsilon 2^-14 in the denominator);
+ * returns 1 when MERE < threshold and MARE < multiplier*threshold and no
+ * one-sided non-finite value. */
+int oracle_verify_mere_mare(int64_t n, const float *golden, const float *actual, double threshold,
+                            double multiplier, double *mereOut, double *mareOut)
+{
+    const double eps = 0.00006103515625;
+    double sum = 0.0, mare = 0.0;
+    int64_t mismatch = 0, skipped = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int oa = isnan(actual[i]) || isinf(actual[i]);
+        const int ga = isnan(golden[i]) || isinf(golden[i]);
+        if (oa && ga) { ++skipped; continue; }
+        if (oa || ga) { ++mismatch; continue; }
+        const double rel = fabs((double)actual[i] - (double)golden[i]) / (fabs((double)golden[i]) + eps);
+        sum += rel;
+        if (rel > mare) mare = rel;
+    }
+    const int64_t eff = n - skipped - mismatch;
+    const double mere = eff > 0 ? sum / (double)eff : 0.0;
+    *mereOut = mere;
+    *mareOut = mare;
+    return mismatch == 0 && mere < threshold && mare < multiplier * threshold;
 }
 
 /* ------------------------- mixed-tolerance verify -------------------------- */
