@@ -60,20 +60,28 @@ _D = ctypes.c_double
 _I = ctypes.c_int64
 
 
+def _map(fn, v, out_dtype):
+    """Applies a scalar conversion elementwise (scalars in, scalar out)."""
+    if np.ndim(v) == 0:
+        return fn(v)
+    a = np.asarray(v).ravel()
+    return np.fromiter((fn(e) for e in a.tolist()), dtype=out_dtype, count=a.size).reshape(np.shape(v))
+
+
 def half_from_float(v):
-    return lib().oracle_half_from_float(float(v))
+    return _map(lambda e: lib().oracle_half_from_float(float(e)), v, np.uint16)
 
 
 def float_from_half(b):
-    return lib().oracle_float_from_half(int(b))
+    return _map(lambda e: lib().oracle_float_from_half(int(e)), b, np.float32)
 
 
 def bf16_from_float(v):
-    return lib().oracle_bf16_from_float(float(v))
+    return _map(lambda e: lib().oracle_bf16_from_float(float(e)), v, np.uint16)
 
 
 def float_from_bf16(b):
-    return lib().oracle_float_from_bf16(int(b))
+    return _map(lambda e: lib().oracle_float_from_bf16(int(e)), b, np.float32)
 
 
 def spmv_f64(row_ptr, col, val, x, y, alpha, beta):

@@ -20,3 +20,13 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+def pytest_sessionstart(session):
+    """Builds the HIP library once if nothing is built yet (hipcc cross-compiles without a GPU)."""
+    from ops_sparse import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        from ops_sparse.build import build_library
+
+        build_library()

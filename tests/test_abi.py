@@ -1,0 +1,332 @@
+"""CPU checks of the C ABI: the library loads, exports every function the
+public header declares, and the host-side entry points (handle, descriptors,
+argument validation) return the reference's status codes.  No call here
+reaches a kernel launch: every SpMV/SpMVOp call either fails validation or
+only sizes a workspace, so the suite runs without a GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from ops_sparse import _lib
+from ops_sparse._lib import (DataType, Format, IndexBase, IndexType, Operation, PointerMode, SpMVAlg, SpMVOpAlg,
+                             Status)
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "cann_ops_sparse.h")
+N, T, H = int(Operation.NON_TRANSPOSE), int(Operation.TRANSPOSE), int(Operation.CONJUGATE_TRANSPOSE)
+F32 = int(DataType.FLOAT)
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*aclsparseStatus_t\s+(aclsparse\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 39
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing
+    # the ctypes table covers exactly the header
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_library_has_no_cpu_fallback_symbols():
+    """The product library never links the oracle."""
+    out = open(_lib.LIB_PATH, "rb").read()
+    assert b"oracle_" not in out
+
+
+class Env:
+    """Host stand-ins for device buffers: validation reads only the addresses."""
+
+    def __init__(self, lib, rows=2, cols=3, nnz=3):
+        self.lib = lib
+        self.h = ctypes.c_void_p(0)
+        assert lib.aclsparseCreate(ctypes.byref(self.h)) == Status.SUCCESS
+        assert lib.aclsparseSetStream(self.h, ctypes.c_void_p(_lib.HIP_NULL_STREAM)) == Status.SUCCESS
+        self.bufs = [np.zeros(max(n, 1) * 8 + 64, np.uint8) for n in (rows + 1, nnz, nnz, cols, rows, cols, rows)]
+        self.rp, self.ci, self.va, self.xv, self.yv, self.xt, self.yt = [self._al(b) for b in self.bufs]
+        self.rows, self.cols, self.nnz = rows, cols, nnz
+        self.alpha, self.beta = ctypes.c_float(1.0), ctypes.c_float(0.0)
+
+    @staticmethod
+    def _al(b):
+        return (b.ctypes.data + 63) & ~63
+
+    def csr(self, rows=None, cols=None, nnz=None, ptrs=True, vtype=DataType.FLOAT, ptr_type=IndexType.I32,
+            idx_type=IndexType.I32, base=IndexBase.ZERO):
+        d = ctypes.c_void_p(0)
+        r = self.rows if rows is None else rows
+        c = self.cols if cols is None else cols
+        n = self.nnz if nnz is None else nnz
+        p = (lambda a: ctypes.c_void_p(a)) if ptrs else (lambda a: ctypes.c_void_p(0))
+        st = self.lib.aclsparseCreateCsr(ctypes.byref(d), r, c, n, p(self.rp), p(self.ci), p(self.va), int(ptr_type),
+                                         int(idx_type), int(base), int(vtype))
+        assert st == Status.SUCCESS
+        return d
+
+    def vec(self, n, addr, vtype=DataType.FLOAT):
+        d = ctypes.c_void_p(0)
+        assert self.lib.aclsparseCreateDnVec(ctypes.byref(d), n, ctypes.c_void_p(addr), int(vtype)) == Status.SUCCESS
+        return d
+
+    def size(self, op, A, x, y, c=F32, alg=0, alpha=None, beta=None, h=None):
+        s = ctypes.c_size_t(0)
+        st = self.lib.aclsparseSpMVGetBufferSize(self.h if h is None else h, op,
+                                                 ctypes.byref(self.alpha) if alpha is None else alpha, A, x,
+                                                 ctypes.byref(self.beta) if beta is None else beta, y, c, alg,
+                                                 ctypes.byref(s))
+        return st, s.value
+
+    def run(self, fn, op, A, x, y, ws, c=F32, alg=0):
+        return getattr(self.lib, fn)(self.h, op, ctypes.byref(self.alpha), A, x, ctypes.byref(self.beta), y, c, alg,
+                                     ws)
+
+
+@pytest.fixture
+def env(lib):
+    e = Env(lib)
+    yield e
+    lib.aclsparseDestroy(e.h)
+
+
+# ------------------------------- handle --------------------------------------
+
+def test_handle_lifecycle(lib):
+    h = ctypes.c_void_p(0)
+    assert lib.aclsparseCreate(None) == Status.HANDLE_IS_NULLPTR
+    assert lib.aclsparseCreate(ctypes.byref(h)) == Status.SUCCESS
+    assert lib.aclsparseCreate(ctypes.byref(h)) == Status.INVALID_VALUE  # would overwrite a live handle
+    v = ctypes.c_int(0)
+    assert lib.aclsparseGetVersion(h, ctypes.byref(v)) == Status.SUCCESS and v.value > 0
+    # the reference answers the version without a handle (aclsparse_auxiliary.cpp:239-247)
+    assert lib.aclsparseGetVersion(None, ctypes.byref(v)) == Status.SUCCESS
+    assert lib.aclsparseGetVersion(h, None) == Status.INVALID_VALUE
+    mode = ctypes.c_int32(-1)
+    assert lib.aclsparseGetPointerMode(h, ctypes.byref(mode)) == Status.SUCCESS and mode.value == PointerMode.HOST
+    assert lib.aclsparseSetPointerMode(h, int(PointerMode.DEVICE)) == Status.SUCCESS
+    assert lib.aclsparseGetPointerMode(h, ctypes.byref(mode)) == Status.SUCCESS and mode.value == PointerMode.DEVICE
+    assert lib.aclsparseSetPointerMode(h, 7) == Status.INVALID_VALUE
+    s = ctypes.c_void_p(0)
+    assert lib.aclsparseSetStream(h, ctypes.c_void_p(0x1234)) == Status.SUCCESS
+    assert lib.aclsparseGetStream(h, ctypes.byref(s)) == Status.SUCCESS and s.value == 0x1234
+    assert lib.aclsparseGetStream(h, None) == Status.INVALID_VALUE
+    buf = np.zeros(4096, np.uint8)
+    assert lib.aclsparseSetWorkspace(h, ctypes.c_void_p(buf.ctypes.data), 0) == Status.INVALID_VALUE
+    assert lib.aclsparseSetWorkspace(h, ctypes.c_void_p(buf.ctypes.data), 4096) == Status.SUCCESS
+    w, n = ctypes.c_void_p(0), ctypes.c_size_t(0)
+    assert lib.aclsparseGetWorkspace(h, ctypes.byref(w), ctypes.byref(n)) == Status.SUCCESS
+    assert w.value == buf.ctypes.data and n.value == 4096
+    assert lib.aclsparseSetWorkspace(h, None, 0) == Status.SUCCESS  # unbinds
+    assert lib.aclsparseSetStream(h, None) == Status.SUCCESS
+    assert lib.aclsparseDestroy(h) == Status.SUCCESS
+    assert lib.aclsparseDestroy(None) == Status.HANDLE_IS_NULLPTR  # aclsparse_auxiliary.cpp:133-139
+
+
+# ------------------------------ descriptors -----------------------------------
+
+def test_dnvec_descriptor(lib):
+    data = np.zeros(16, np.float32)
+    d = ctypes.c_void_p(0)
+    assert lib.aclsparseCreateDnVec(ctypes.byref(d), -1, None, F32) == Status.INVALID_VALUE
+    assert lib.aclsparseCreateDnVec(ctypes.byref(d), 16, ctypes.c_void_p(data.ctypes.data), F32) == Status.SUCCESS
+    n, p, t = ctypes.c_int64(0), ctypes.c_void_p(0), ctypes.c_int32(0)
+    assert lib.aclsparseDnVecGet(d, ctypes.byref(n), ctypes.byref(p), ctypes.byref(t)) == Status.SUCCESS
+    assert (n.value, p.value, t.value) == (16, data.ctypes.data, F32)
+    s = ctypes.c_int64(0)
+    assert lib.aclsparseDnVecGetStride(d, ctypes.byref(s)) == Status.SUCCESS and s.value == 1
+    assert lib.aclsparseDnVecSetStride(d, 0) == Status.INVALID_VALUE
+    assert lib.aclsparseDnVecSetStride(d, 3) == Status.SUCCESS
+    assert lib.aclsparseDnVecGetStride(d, ctypes.byref(s)) == Status.SUCCESS and s.value == 3
+    assert lib.aclsparseDnVecSetValues(d, None) == Status.SUCCESS  # delayed binding
+    assert lib.aclsparseDnVecGetValues(d, ctypes.byref(p)) == Status.SUCCESS and p.value is None
+    assert lib.aclsparseDestroyDnVec(d) == Status.SUCCESS
+    assert lib.aclsparseDestroyDnVec(None) == Status.SUCCESS
+
+
+def test_csr_descriptor(lib):
+    e = Env(lib)
+    A = e.csr(base=IndexBase.ONE)
+    f = ctypes.c_int32(-1)
+    assert lib.aclsparseSpMatGetFormat(A, ctypes.byref(f)) == Status.SUCCESS and f.value == Format.CSR
+    assert lib.aclsparseSpMatGetIndexBase(A, ctypes.byref(f)) == Status.SUCCESS and f.value == IndexBase.ONE
+    r, c, n = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    assert lib.aclsparseSpMatGetSize(A, ctypes.byref(r), ctypes.byref(c), ctypes.byref(n)) == Status.SUCCESS
+    assert (r.value, c.value, n.value) == (2, 3, 3)
+    ptrs = [ctypes.c_void_p(0) for _ in range(3)]
+    ts = [ctypes.c_int32(0) for _ in range(4)]
+    assert lib.aclsparseCsrGet(A, ctypes.byref(r), ctypes.byref(c), ctypes.byref(n), *[ctypes.byref(p) for p in ptrs],
+                               *[ctypes.byref(t) for t in ts]) == Status.SUCCESS
+    assert [p.value for p in ptrs] == [e.rp, e.ci, e.va]
+    assert [t.value for t in ts] == [IndexType.I32, IndexType.I32, IndexBase.ONE, F32]
+    s = [ctypes.c_int64(0) for _ in range(3)]
+    assert lib.aclsparseCsrGetStrides(A, *[ctypes.byref(v) for v in s]) == Status.SUCCESS
+    assert [v.value for v in s] == [1, 1, 1]
+    assert lib.aclsparseCsrSetStrides(A, 2, 3, 4) == Status.SUCCESS
+    assert lib.aclsparseCsrGetStrides(A, *[ctypes.byref(v) for v in s]) == Status.SUCCESS
+    assert [v.value for v in s] == [2, 3, 4]
+    assert lib.aclsparseCsrSetStrides(A, 0, 1, 1) == Status.INVALID_VALUE
+    # row offsets are required when rows > 0, indices and values when nnz > 0
+    assert lib.aclsparseCsrSetPointers(A, None, None, None) == Status.INVALID_VALUE
+    assert lib.aclsparseCsrSetPointers(A, ctypes.c_void_p(e.rp), ctypes.c_void_p(e.ci), None) == Status.INVALID_VALUE
+    assert lib.aclsparseCsrSetPointers(A, ctypes.c_void_p(e.rp), ctypes.c_void_p(e.ci),
+                                       ctypes.c_void_p(e.va)) == Status.SUCCESS
+    assert lib.aclsparseSpMatSetValues(A, ctypes.c_void_p(e.va)) == Status.SUCCESS
+    v = ctypes.c_void_p(0)
+    assert lib.aclsparseSpMatGetValues(A, ctypes.byref(v)) == Status.SUCCESS and v.value == e.va
+    assert lib.aclsparseDestroySpMat(A) == Status.SUCCESS
+    assert lib.aclsparseDestroySpMat(None) == Status.SUCCESS
+    d = ctypes.c_void_p(0)
+    assert lib.aclsparseCreateCsr(ctypes.byref(d), -1, 3, 0, None, None, None, 0, 0, 0, F32) == Status.INVALID_VALUE
+    lib.aclsparseDestroy(e.h)
+
+
+# --------------------------- SpMV validation ----------------------------------
+
+def test_spmv_buffer_size_positive_and_aligned(env):
+    A = env.csr()
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    st, n = env.size(N, A, x, y)
+    assert st == Status.SUCCESS and n >= 64 and n % 64 == 0
+    # transpose needs the accumulator of cols entries as well
+    xt, yt = env.vec(2, env.xt), env.vec(3, env.yt)
+    st, nt = env.size(T, A, xt, yt)
+    assert st == Status.SUCCESS and nt >= n
+
+
+def test_spmv_handle_checks(env, lib):
+    A = env.csr()
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    s = ctypes.c_size_t(0)
+    assert lib.aclsparseSpMVGetBufferSize(None, N, ctypes.byref(env.alpha), A, x, ctypes.byref(env.beta), y, F32, 0,
+                                          ctypes.byref(s)) == Status.HANDLE_IS_NULLPTR
+    h = ctypes.c_void_p(0)
+    assert lib.aclsparseCreate(ctypes.byref(h)) == Status.SUCCESS
+    # the stream must be set before any SpMV call
+    assert env.size(N, A, x, y, h=h)[0] == Status.INVALID_VALUE
+    lib.aclsparseDestroy(h)
+
+
+def test_spmv_rejects_unsupported_op_compute_alg(env):
+    A = env.csr()
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    assert env.size(9, A, x, y)[0] == Status.NOT_SUPPORTED
+    assert env.size(N, A, x, y, c=int(DataType.FLOAT16))[0] == Status.NOT_SUPPORTED
+    assert env.size(N, A, x, y, alg=17)[0] == Status.NOT_SUPPORTED
+    assert env.size(N, None, x, y)[0] == Status.INVALID_VALUE
+
+
+def test_spmv_rejects_null_and_misaligned_scalars(env):
+    A = env.csr()
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    raw = (ctypes.c_uint8 * 16)()
+    mis = ctypes.c_void_p(ctypes.addressof(raw) + 1)
+    assert env.size(N, A, x, y, alpha=ctypes.c_void_p(0))[0] == Status.INVALID_VALUE
+    assert env.size(N, A, x, y, alpha=mis)[0] == Status.INVALID_VALUE
+
+
+def test_spmv_rejects_type_combinations(env):
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    A16 = env.csr(vtype=DataType.FLOAT16)
+    assert env.size(N, A16, x, y)[0] == Status.NOT_SUPPORTED  # fp16 A with fp32 x
+    x16, y16 = env.vec(3, env.xv, DataType.FLOAT16), env.vec(2, env.yv, DataType.FLOAT16)
+    assert env.size(N, A16, x16, y16)[0] == Status.SUCCESS
+    yb = env.vec(2, env.yv, DataType.BF16)
+    assert env.size(N, A16, x16, yb)[0] == Status.NOT_SUPPORTED
+    A8 = env.csr(vtype=DataType.INT8)
+    x8, y32 = env.vec(3, env.xv, DataType.INT8), env.vec(2, env.yv, DataType.INT32)
+    ai = ctypes.c_int32(1)
+    assert env.size(N, A8, x8, y32, c=int(DataType.INT32), alpha=ctypes.byref(ai), beta=ctypes.byref(ai))[0] == \
+        Status.SUCCESS
+    assert env.size(N, A8, x8, env.vec(2, env.yv, DataType.FLOAT))[0] == Status.SUCCESS
+    assert env.size(N, env.csr(idx_type=IndexType.I64), x, y)[0] == Status.NOT_SUPPORTED
+
+
+def test_spmv_accepts_i64_row_offsets(env):
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    assert env.size(N, env.csr(ptr_type=IndexType.I64), x, y)[0] == Status.SUCCESS
+
+
+def test_spmv_rejects_wrong_vector_sizes(env):
+    A = env.csr()
+    assert env.size(N, A, env.vec(2, env.xv), env.vec(2, env.yv))[0] == Status.INVALID_VALUE
+    assert env.size(T, A, env.vec(3, env.xv), env.vec(2, env.yv))[0] == Status.INVALID_VALUE
+
+
+def test_spmv_rejects_nonzero_nnz_with_zero_dimensions(env):
+    """spmv_test.cpp:543-568: nnz > 0 with rows == 0 or cols == 0."""
+    ws = np.zeros(512, np.uint8)
+    wsp = ctypes.c_void_p(Env._al(ws))
+    for zero_rows in (False, True):
+        A = env.csr(rows=0 if zero_rows else 2, cols=2 if zero_rows else 0, nnz=1, ptrs=False)
+        for op in (N, T):
+            tr = op == T
+            x = env.vec(0 if zero_rows == tr else 2, 0)
+            y = env.vec(2 if zero_rows == tr else 0, 0)
+            assert env.size(op, A, x, y)[0] == Status.INVALID_VALUE
+            assert env.run("aclsparseSpMVPreprocess", op, A, x, y, wsp) == Status.INVALID_VALUE
+            assert env.run("aclsparseSpMV", op, A, x, y, wsp) == Status.INVALID_VALUE
+
+
+def test_spmv_workspace_query_before_binding_storage(env):
+    """spmv_test.cpp:570-593: sizes are known before storage is bound; running unbound fails."""
+    A = env.csr(ptrs=False)
+    x, y = env.vec(3, 0), env.vec(2, 0)
+    st, n = env.size(N, A, x, y)
+    assert st == Status.SUCCESS and n > 0
+    ws = np.zeros(n + 64, np.uint8)
+    assert env.run("aclsparseSpMVPreprocess", N, A, x, y, ctypes.c_void_p(Env._al(ws))) == Status.INVALID_VALUE
+    assert env.run("aclsparseSpMV", N, A, x, y, ctypes.c_void_p(Env._al(ws))) == Status.INVALID_VALUE
+
+
+def test_spmv_workspace_checks(env):
+    A = env.csr()
+    x, y = env.vec(3, env.xv), env.vec(2, env.yv)
+    assert env.run("aclsparseSpMV", N, A, x, y, None) == Status.INSUFFICIENT_RESOURCES
+    ws = np.zeros(4096, np.uint8)
+    assert env.run("aclsparseSpMV", N, A, x, y, ctypes.c_void_p(Env._al(ws) + 4)) == Status.INVALID_VALUE
+
+
+def test_spmv_rejects_aliased_storage(env):
+    A = env.csr()
+    x = env.vec(3, env.xv)
+    y = env.vec(2, env.xv)  # y aliases x
+    ws = np.zeros(8192, np.uint8)
+    assert env.run("aclsparseSpMV", N, A, x, y, ctypes.c_void_p(Env._al(ws))) == Status.INVALID_VALUE
+
+
+# --------------------------- SpMVOp validation --------------------------------
+
+def test_spmvop_validation(env, lib):
+    A = env.csr()
+    x, y, z = env.vec(3, env.xv), env.vec(2, env.yv), env.vec(2, env.yt)
+    s = ctypes.c_size_t(7)
+    bs = lib.aclsparseSpMVOp_bufferSize
+    assert bs(None, N, A, x, y, z, F32, 0, ctypes.byref(s)) == Status.HANDLE_IS_NULLPTR
+    assert bs(env.h, T, A, x, y, z, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, A, x, y, z, int(DataType.INT32), 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, env.csr(vtype=DataType.FLOAT16), x, y, z, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, A, x, y, z, F32, 9, ctypes.byref(s)) != Status.SUCCESS
+    assert bs(env.h, N, A, x, y, z, F32, int(SpMVOpAlg.ALG1), ctypes.byref(s)) == Status.SUCCESS and s.value == 0
+    d = ctypes.c_void_p(0)
+    cd = lib.aclsparseSpMVOp_createDescr
+    assert cd(env.h, ctypes.byref(d), N, A, x, y, z, F32, int(SpMVOpAlg.ALG2), None) == Status.INVALID_VALUE
+    assert cd(env.h, None, N, A, x, y, z, F32, 1, None) == Status.INVALID_VALUE
+    assert cd(env.h, ctypes.byref(d), N, A, x, y, z, F32, int(SpMVOpAlg.DEFAULT), None) == Status.SUCCESS
+    plan = ctypes.c_void_p(0)
+    assert lib.aclsparseSpMVOp_createPlan(env.h, d, ctypes.byref(plan), None, 0) == Status.SUCCESS
+    assert lib.aclsparseSpMVOp_createPlan(env.h, d, None, None, 0) == Status.INVALID_VALUE
+    a, b = ctypes.c_float(1), ctypes.c_float(0)
+    ex = lib.aclsparseSpMVOp
+    assert ex(env.h, plan, None, ctypes.byref(b), x, y, z) == Status.INVALID_VALUE
+    assert ex(env.h, plan, ctypes.byref(a), ctypes.byref(b), x, y, env.vec(3, env.yt)) == Status.INVALID_VALUE
+    assert lib.aclsparseSpMVOp_destroyPlan(plan) == Status.SUCCESS
+    assert lib.aclsparseSpMVOp_destroyDescr(d) == Status.SUCCESS
