@@ -25,7 +25,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <map>
+#include <string>
 #include <mutex>
 #include <type_traits>
 
@@ -46,6 +48,7 @@ constexpr int kPadded = kChunk + kChunk / kIpt;
 static_assert(kChunk % (4 * kThreads) == 0, "chunk must be a multiple of one 16-byte load per lane");
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned short v4u16 __attribute__((ext_vector_type(4)));
 
@@ -871,6 +874,556 @@ __global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvWaveKernel(RowBlock
     }
 }
 
+// ------------------------- stream row kernel (fp32 sums) ---------------------
+//
+// Same persistent wave workers, row blocks and 512-slot chunks as the kernel
+// above, with a cheaper reduction for the common case of short rows:
+//  * col_ind / values are read with 16-byte buffer loads whose resource
+//    starts at the chunk (a scalar base, a constant per-lane offset); the
+//    resource ends at the last whole 16-byte group of the arrays, so loads
+//    past it return zero instead of faulting, and x is gathered through a
+//    resource bounded by the vector's length (32-bit offsets, no masking);
+//  * the products of a chunk go to the wave's LDS slice in slot order;
+//  * phase 1: rows that lie inside the chunk and are short (SerialCap) are summed from LDS by groups of G lanes (G = 1 for blocks of
+//    many short rows, up to 64 for a block of one row), then reduced across
+//    the group;
+//  * phase 2: the remaining rows (longer ones, and the rows that continue
+//    from the previous chunk or into the next) are summed by the whole wave,
+//    one after another; a row that crosses a chunk boundary carries its
+//    partial sum in a scalar register.
+// Every row of a block is owned by lane i % 64 (output slot i / 64), which
+// writes y or, when the row does not finish in this chunk, the sink, so
+// every lane issues the same stores in every chunk.
+
+// Phase-1 row length limit: 8 entries for one lane per row, 16 per lane for
+// groups (rows of medium length, few rows per block).
+constexpr int kSerialCapOne = 8;
+__device__ __forceinline__ int SerialCap(int lg) { return lg == 0 ? kSerialCapOne : (16 << lg); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* base, int64_t bytes)
+{
+    const int64_t b = bytes < 0 ? 0 : bytes > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(b), 0x00020000);
+}
+
+// Block metadata (blocks[t], blocks[t+1], block_nnz[t], block_nnz[t+1]) of
+// this worker's blocks, kept in a rolling window of 64 lanes: lane l holds
+// the block of ordinal o with o % 64 == l, for the 64 ordinals after the last
+// one opened.  Opening a block is four lane reads.  The window is refilled by
+// one unconditional load pair per chunk (the ordinal 64 ahead of the last
+// opened block), merged one chunk later, so no wait for it ever lands on the
+// loop's critical path and the prefetches stay in flight.
+template <typename RowT>
+struct TileCache {
+    int32_t r0, r1;
+    RowT k0, k1;
+};
+
+template <typename RowT>
+struct TileRefill {
+    int64_t ordinal;  // ordinal loaded (uniform)
+    int32_t r0, r1;
+    RowT k0, k1;
+};
+
+template <typename RowT>
+__device__ __forceinline__ int64_t TileIndex(int64_t ordinal, int64_t first, int64_t stride, int64_t tileEnd)
+{
+    const int64_t t = first + ordinal * stride;
+    return t < tileEnd ? t : first;  // first < tileEnd: always a valid block
+}
+
+template <typename RowT>
+__device__ __forceinline__ void FillTiles(const RowBlockParams& p, TileCache<RowT>& c, int64_t first, int64_t stride,
+                                          int64_t tileEnd, int lane)
+{
+    const int64_t tt = TileIndex<RowT>(lane, first, stride, tileEnd);
+    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
+    c.r0 = p.blocks[tt];
+    c.r1 = p.blocks[tt + 1];
+    c.k0 = bn[tt];
+    c.k1 = bn[tt + 1];
+}
+
+template <typename RowT>
+__device__ __forceinline__ void IssueRefill(const RowBlockParams& p, TileRefill<RowT>& f, int64_t ordinal,
+                                            int64_t first, int64_t stride, int64_t tileEnd)
+{
+    f.ordinal = ordinal;
+    const int64_t tt = TileIndex<RowT>(ordinal, first, stride, tileEnd);
+    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
+    f.r0 = p.blocks[tt];
+    f.r1 = p.blocks[tt + 1];
+    f.k0 = bn[tt];
+    f.k1 = bn[tt + 1];
+}
+
+template <typename RowT>
+__device__ __forceinline__ void MergeRefill(TileCache<RowT>& c, const TileRefill<RowT>& f, int lane)
+{
+    const bool mine = lane == static_cast<int>(f.ordinal & (kWave - 1));
+    c.r0 = mine ? f.r0 : c.r0;
+    c.r1 = mine ? f.r1 : c.r1;
+    c.k0 = mine ? f.k0 : c.k0;
+    c.k1 = mine ? f.k1 : c.k1;
+}
+
+__device__ __forceinline__ int64_t ReadLane64(int64_t v, int l)
+{
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <typename RowT>
+__device__ __forceinline__ Stage OpenTileCached(const TileCache<RowT>& c, int64_t ordinal, int64_t first,
+                                                int64_t stride, int64_t tileEnd, int64_t& lastOpened)
+{
+    Stage s{};
+    s.tile = ordinal;
+    const int64_t t = first + ordinal * stride;
+    s.valid = t < tileEnd;
+    if (!s.valid) return s;
+    lastOpened = ordinal;
+    const int l = static_cast<int>(ordinal & (kWave - 1));
+    s.r0 = __builtin_amdgcn_readlane(c.r0, l);
+    const int64_t n = static_cast<int64_t>(__builtin_amdgcn_readlane(c.r1, l)) - s.r0;
+    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kWaveRows ? kWaveRows : n);
+    int64_t span;
+    if constexpr (sizeof(RowT) == 8) {
+        s.k0 = ReadLane64(c.k0, l);
+        span = ReadLane64(c.k1, l) - s.k0;
+    } else {
+        s.k0 = __builtin_amdgcn_readlane(c.k0, l);
+        span = static_cast<int64_t>(__builtin_amdgcn_readlane(c.k1, l)) - s.k0;
+    }
+    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
+    s.c0 = 0;
+    s.first = true;
+    ChunkBounds(s);
+    return s;
+}
+
+template <typename RowT>
+__device__ __forceinline__ Stage NextStageCached(const TileCache<RowT>& c, const Stage& s, int64_t first,
+                                                 int64_t stride, int64_t tileEnd, int64_t& lastOpened)
+{
+    if (!s.valid) return s;
+    if (!s.last) {
+        Stage n = s;
+        n.c0 = s.c1;
+        n.first = false;
+        ChunkBounds(n);
+        return n;
+    }
+    return OpenTileCached<RowT>(c, s.tile + 1, first, stride, tileEnd, lastOpened);
+}
+
+constexpr int kBufNonTemporal = 2;  // cache policy bit of buffer loads: streaming data
+
+template <ValKind V>
+struct StreamVals;
+template <>
+struct StreamVals<ValKind::F32> {
+    v4f v[2];
+};
+template <>
+struct StreamVals<ValKind::F16> {
+    v4i v;  // 8 halves
+};
+template <>
+struct StreamVals<ValKind::BF16> {
+    v4i v;
+};
+
+template <ValKind V>
+__device__ __forceinline__ uint32_t RawVal(const StreamVals<V>& s, int j)
+{
+    if constexpr (V == ValKind::F32) {
+        return __float_as_uint(s.v[j >> 2][j & 3]);
+    } else {
+        const uint32_t w = static_cast<uint32_t>(s.v[j >> 1]);
+        return (j & 1) ? (w >> 16) : (w & 0xFFFFU);
+    }
+}
+
+template <ValKind V>
+__device__ __forceinline__ float ValToFloat(uint32_t raw)
+{
+    if constexpr (V == ValKind::F32) return __uint_as_float(raw);
+    else if constexpr (V == ValKind::F16) return HalfToFloat(static_cast<uint16_t>(raw));
+    else return Bf16ToFloat(static_cast<uint16_t>(raw));
+}
+
+// Chunk slot held in register j (0..7) of a lane.
+__device__ __forceinline__ int StreamSlot(int lane, int j) { return (j >> 2) * 256 + 4 * lane + (j & 3); }
+
+template <typename RowT, ValKind V, OutKind O>
+struct StreamLoad {
+    v4i col[2];
+    StreamVals<V> val;
+    RowT rp[2];
+    typename OutOf<O>::T yold[2];
+    uint32_t xg[kLaneItems];  // gathered x of the 8 slots
+};
+
+template <typename RowT, ValKind V, OutKind O, bool kBeta>
+__device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
+                                                StreamLoad<RowT, V, O>& b)
+{
+    using ValT = typename ValOf<V>::T;
+    using OutT = typename OutOf<O>::T;
+    // An invalid stage loads from an empty resource: every load returns 0.
+    const int64_t a0 = s.valid ? s.a0 : 0;
+    const int64_t avail = s.valid ? tailStart - a0 : 0;
+    const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
+    const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
+    // Lane-contiguous 16-byte groups: load h of lane l holds slots
+    // 256h + 4l .. 256h + 4l + 3, so each load instruction reads 1 KiB of
+    // col_ind (values: 1 KiB fp32, 512 B fp16) without gaps.
+    b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
+    b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    if constexpr (V == ValKind::F32) {
+        b.val.v[0] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
+        b.val.v[1] =
+            __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, 1024 + lane * 16, 0, kBufNonTemporal));
+    } else {
+        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rv, lane * 8, 0, kBufNonTemporal));
+        const v2i hi = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rv, 512 + lane * 8, 0, kBufNonTemporal));
+        b.val.v = v4i{lo.x, lo.y, hi.x, hi.y};
+    }
+    // Row offsets r0 .. r0+nr and old y of rows r0 .. r0+nr-1 (entries past
+    // the block read as 0 and are never used).
+    const int64_t r0 = s.valid ? s.r0 : 0;
+    const int64_t nrp = s.valid ? s.nr + 1 : 0;
+    const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
+    int64_t ny = s.valid ? s.nr : 0;
+    if (ny > p.rows - r0) ny = p.rows - r0;
+    const __amdgpu_buffer_rsrc_t ry = Rsrc(static_cast<const OutT*>(p.y) + r0, ny * sizeof(OutT));
+#if defined(SPMV_EXP_NO_RPY)
+    b.rp[0] = static_cast<RowT>(lane * 5); b.rp[1] = static_cast<RowT>(lane * 5 + 320);
+    b.yold[0] = OutT{}; b.yold[1] = OutT{};
+    if (false)
+#endif
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave;
+        if constexpr (sizeof(RowT) == 8) {
+            b.rp[h] = static_cast<RowT>(__builtin_bit_cast(
+                long long, __builtin_amdgcn_raw_buffer_load_b64(rr, i * 8, 0, 0)));
+        } else {
+            b.rp[h] = static_cast<RowT>(__builtin_amdgcn_raw_buffer_load_b32(rr, i * 4, 0, 0));
+        }
+        if constexpr (kBeta) {
+            if constexpr (sizeof(OutT) == 4) {
+                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b32(ry, i * 4, 0, 0));
+            } else {
+                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b16(ry, i * 2, 0, 0));
+            }
+        } else {
+            b.yold[h] = OutT{};
+        }
+    }
+}
+
+// Gathers x for the 8 slots of this lane.  The last nnz % 4 entries of the
+// arrays (not covered by any 16-byte group) are read here, in the one chunk
+// that reaches them.
+template <typename RowT, ValKind V, OutKind O>
+__device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stage& s, int64_t tailStart,
+                                             __amdgpu_buffer_rsrc_t rx, int lane, StreamLoad<RowT, V, O>& b,
+                                             uint32_t xg[kLaneItems])
+{
+    using ValT = typename ValOf<V>::T;
+    if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
+        // Uniform branch: only the chunk that reaches the end of the arrays.
+        int32_t tc[3];
+        ValT tv3[3];
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            const int64_t k = tailStart + e < p.nnz ? tailStart + e : p.nnz - 1;
+            tc[e] = ConstLoad<int32_t>(p.col, k);
+            tv3[e] = ConstLoad<ValT>(p.val, k);
+        }
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            const int64_t k = s.a0 + StreamSlot(lane, j) - tailStart;
+            if (k >= 0 && k < 3) {
+                const int kk = static_cast<int>(k);
+                b.col[j >> 2][j & 3] = kk == 0 ? tc[0] : kk == 1 ? tc[1] : tc[2];
+                const ValT tv = kk == 0 ? tv3[0] : kk == 1 ? tv3[1] : tv3[2];
+                if constexpr (V == ValKind::F32) {
+                    b.val.v[j >> 2][j & 3] = tv;
+                } else {
+                    const uint32_t raw = static_cast<uint32_t>(tv);
+                    uint32_t w = static_cast<uint32_t>(b.val.v[j >> 1]);
+                    w = (j & 1) ? ((w & 0xFFFFU) | (raw << 16)) : ((w & 0xFFFF0000U) | raw);
+                    b.val.v[j >> 1] = static_cast<int>(w);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) {
+#if defined(SPMV_EXP_LINEAR_X)
+        const uint32_t off = static_cast<uint32_t>((s.a0 + StreamSlot(lane, j)) % p.cols) * static_cast<uint32_t>(sizeof(ValT));
+#elif defined(SPMV_EXP_NO_GATHER)
+        xg[j] = 0x3f800000u + (b.col[j >> 2][j & 3] & 1);
+        continue;
+        const uint32_t off = 0;
+#else
+        const uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
+#endif
+        if constexpr (sizeof(ValT) == 4) {
+            xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, 0);
+        } else {
+            xg[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, static_cast<int>(off), 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ float WaveSum(float v)
+{
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// LDS product slots per wave: one chunk plus 8 so that a predicated read of
+// 8 entries from any slot stays inside the wave's slice.
+constexpr int kStreamLds = kWaveChunk + 8;
+
+// Reduces one loaded and gathered chunk: products to LDS, phase 1 (short
+// rows, lane groups), phase 2 (long or chunk-crossing rows, whole wave), y.
+// Row i of the block (i = lane + 64h) has its offsets in registers: its
+// start in this lane's rp[h], its end in the next row's.
+template <typename RowT, ValKind V, OutKind O, bool kBeta>
+__device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<RowT, V, O>& lc, float* sVal, int lane,
+                                            float alpha, float beta, float& carry, int& lg, typename OutOf<O>::T* y,
+                                            typename OutOf<O>::T* sink)
+{
+    using OutT = typename OutOf<O>::T;
+    float prod[kLaneItems];
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) prod[j] = ValToFloat<V>(RawVal<V>(lc.val, j)) * ValToFloat<V>(lc.xg[j]);
+
+    const int32_t c0 = cur.c0, c1 = cur.c1;
+    const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);  // LDS slot of relative offset r: r - shift
+    const int nr = cur.nr;
+    if (cur.first) {
+        carry = 0.0f;
+        // Lanes per row: as many as keep every row of the block on its own
+        // lane group, 1 when the block spans several chunks.
+        lg = 0;
+        if (cur.last) {
+            while (lg < 6 && (nr << (lg + 1)) <= kWave) ++lg;
+        }
+    }
+    *reinterpret_cast<v4f*>(&sVal[4 * lane]) = v4f{prod[0], prod[1], prod[2], prod[3]};
+    *reinterpret_cast<v4f*>(&sVal[256 + 4 * lane]) = v4f{prod[4], prod[5], prod[6], prod[7]};
+
+    // Row offsets relative to the block's first non-zero.
+    const int32_t k0lo = static_cast<int32_t>(cur.k0);
+    int32_t rs[2], re[2];
+    rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
+    rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
+    const int32_t nxt0 = __shfl_down(rs[0], 1, kWave);
+    const int32_t nxt1 = __shfl_down(rs[1], 1, kWave);
+    const int32_t r64 = __shfl(rs[1], 0, kWave);
+    re[0] = lane == kWave - 1 ? r64 : nxt0;
+    re[1] = nxt1;
+
+    const int gsz = 1 << lg;
+    const int cap = SerialCap(lg);
+    bool fin[2], defer[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave;
+        const bool in = i < nr;
+        const bool empty = re[h] <= rs[h];
+        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                         : (rs[h] < c1 && re[h] > c0));
+        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
+        defer[h] = active && (crosses || re[h] - rs[h] > cap);
+        fin[h] = active && !defer[h];
+    }
+    WaveLdsSync();
+
+    // Phase 1.
+    float sum[2] = {0.0f, 0.0f};
+    if (lg == 0) {
+        // One lane per row, at most 8 entries: 8 predicated reads, no branch.
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 1 && nr <= kWave) break;
+            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
+            const int32_t base = fin[h] ? rs[h] - shift : 0;
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < kSerialCapOne; ++t) {
+                const float v = sVal[base + t];
+                acc += t < len ? v : 0.0f;
+            }
+            sum[h] = acc;
+        }
+    } else {
+        const int g = lane >> lg;
+        const int sub = lane & (gsz - 1);
+        const bool in = g < nr;
+        const int32_t gs = __shfl(rs[0], g, kWave);
+        const int32_t ge = __shfl(re[0], g, kWave);
+        float part = 0.0f;
+        if (in && ge - gs <= cap) {
+            for (int32_t q = gs + sub; q < ge; q += gsz) part += sVal[q - shift];
+        }
+        for (int m = 1; m < gsz; m <<= 1) part += __shfl_xor(part, m, kWave);
+        sum[0] = __shfl(part, lane << lg, kWave);  // lane i owns row i (nr <= 32 here)
+    }
+
+    // Phase 2: deferred rows, whole wave per row, in row order.
+    uint64_t pending[2] = {__ballot(defer[0]), __ballot(defer[1])};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        while (pending[h]) {
+            const int l = __builtin_ctzll(pending[h]);
+            pending[h] &= pending[h] - 1;
+            const int32_t s0 = __shfl(rs[h], l, kWave), e0 = __shfl(re[h], l, kWave);
+            const int32_t lo = s0 > c0 ? s0 : c0;
+            const int32_t hi = e0 < c1 ? e0 : c1;
+            float part = 0.0f;
+            for (int32_t q = lo + lane; q < hi; q += kWave) part += sVal[q - shift];
+            float total = WaveSum(part);
+            if (s0 < c0) total += carry;
+            if (e0 > c1) {
+                carry = total;
+            } else if (lane == l) {
+                sum[h] = total;
+                fin[h] = true;
+            }
+        }
+    }
+
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave;
+        float r = alpha * sum[h];
+        // beta == 0 (possible at run time with device scalars) never reads y
+        if constexpr (kBeta) {
+            if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
+        }
+        OutT* dst = fin[h] ? y + (cur.r0 + i) : sink;
+        *dst = FromAcc<O, AccKind::F32>(r);
+    }
+    WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
+}
+
+template <typename RowT, ValKind V, OutKind O, bool kBeta>
+__global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvStreamKernel(RowBlockParams p)
+{
+    using ValT = typename ValOf<V>::T;
+    using OutT = typename OutOf<O>::T;
+    using L = StreamLoad<RowT, V, O>;
+
+    __shared__ float sValAll[kWavesPerGroup][kStreamLds];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    float* sVal = sValAll[wv];
+
+    const int64_t xcd = blockIdx.x % kXcds;
+    const int64_t worker = (blockIdx.x / kXcds) * kWavesPerGroup + wv;
+    const int64_t tileBegin = xcd * p.per_xcd;
+    int64_t tileEnd = tileBegin + p.per_xcd;
+    if (tileEnd > p.num_blocks) tileEnd = p.num_blocks;
+    const int64_t stride = p.workers_per_xcd;
+    const int64_t firstTile = tileBegin + worker;
+    if (firstTile >= tileEnd) return;
+
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(p.s, alpha, beta);
+    OutT* y = static_cast<OutT*>(p.y);
+    OutT* sink = static_cast<OutT*>(p.sink) + lane;
+    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
+
+    const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
+
+    // Three register bundles rotate through the roles (current: gathered,
+    // next: loaded, after: loading) by unrolling the loop three times, so no
+    // register copy ever waits on a load in flight.
+    TileCache<RowT> tiles;
+    FillTiles<RowT>(p, tiles, firstTile, stride, tileEnd, lane);
+    int64_t lastOpened = 0;
+    L b0, b1, b2;
+    Stage cur = OpenTileCached<RowT>(tiles, 0, firstTile, stride, tileEnd, lastOpened);
+    StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b0);
+    StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b0, b0.xg);
+    // Ordinal 0 has been read: its slot takes ordinal 64 before nxt is opened.
+    TileRefill<RowT> refill;
+    IssueRefill<RowT>(p, refill, 64, firstTile, stride, tileEnd);
+    MergeRefill<RowT>(tiles, refill, lane);
+    Stage nxt = NextStageCached<RowT>(tiles, cur, firstTile, stride, tileEnd, lastOpened);
+    IssueRefill<RowT>(p, refill, lastOpened + kWave, firstTile, stride, tileEnd);
+    StreamLoadStage<RowT, V, O, kBeta>(p, nxt, tailStart, lane, b1);
+    float carry = 0.0f;
+    int lg = 0;  // log2 of the lanes per row in phase 1 (per block)
+
+    auto step = [&](L& lc, L& ln, L& la) __attribute__((always_inline)) {
+        StreamGather<RowT, V, O>(p, nxt, tailStart, rx, lane, ln, ln.xg);
+        MergeRefill<RowT>(tiles, refill, lane);  // loaded one chunk ago
+        const Stage after = NextStageCached<RowT>(tiles, nxt, firstTile, stride, tileEnd, lastOpened);
+        IssueRefill<RowT>(p, refill, lastOpened + kWave, firstTile, stride, tileEnd);
+        StreamLoadStage<RowT, V, O, kBeta>(p, after, tailStart, lane, la);
+
+        StreamChunk<RowT, V, O, kBeta>(cur, lc, sVal, lane, alpha, beta, carry, lg, y, sink);
+
+        // A chunk of a multi-chunk block keeps the block's row offsets / old
+        // y in its own bundle: every chunk loads them.
+        cur = nxt;
+        nxt = after;
+        return cur.valid;
+    };
+    while (step(b0, b1, b2) && step(b1, b2, b0) && step(b2, b0, b1)) {
+    }
+}
+
+// One block per wave, no persistence: the hardware keeps as many waves
+// resident as registers allow (the kernel is built for 8 waves per SIMD) and
+// their independent loads keep HBM busy.  Chunks of a multi-chunk block are
+// processed one after another.
+template <typename RowT, ValKind V, OutKind O, bool kBeta>
+__global__ __launch_bounds__(kWave* kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(7)))
+void SpmvStreamFlatKernel(RowBlockParams p)
+{
+    using ValT = typename ValOf<V>::T;
+    using OutT = typename OutOf<O>::T;
+    using L = StreamLoad<RowT, V, O>;
+
+    __shared__ float sValAll[kWavesPerGroup][kStreamLds];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    float* sVal = sValAll[wv];
+    const int64_t tile = XcdBlock() * kWavesPerGroup + wv;
+    if (tile >= p.num_blocks) return;
+
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(p.s, alpha, beta);
+    OutT* y = static_cast<OutT*>(p.y);
+    OutT* sink = static_cast<OutT*>(p.sink) + lane;
+    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
+    const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
+    float carry = 0.0f;
+    int lg = 0;
+    Stage cur = OpenTile<RowT>(p, 0, tile, 1, tile + 1);
+    while (cur.valid) {
+        L b;
+        StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
+        StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
+        StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
+        cur = NextStage<RowT>(p, cur, tile, 1, tile + 1);
+    }
+}
+
 // ------------------------------- transpose ----------------------------------
 
 // y = beta*y in place (y is not read when beta == 0); the scatter then adds
@@ -1125,9 +1678,32 @@ void PersistentShape(RowBlockParams& p, const void* kernel, unsigned& grid)
     grid = static_cast<unsigned>((j / kWavesPerGroup) * kXcds);
 }
 
+// Selects the previous wave kernel instead of the stream kernel
+// (ACLSPARSE_HIP_SPMV_KERNEL=wave), for comparisons.
+bool UseWaveKernel()
+{
+    static const bool wave = [] {
+        const char* e = std::getenv("ACLSPARSE_HIP_SPMV_KERNEL");
+        return e != nullptr && std::string(e) == "wave";
+    }();
+    return wave;
+}
+
+// The one-block-per-wave kernel is the default; ACLSPARSE_HIP_SPMV_KERNEL=
+// stream selects the persistent pipelined variant (for comparisons).
+bool UseFlatKernel()
+{
+    static const bool flat = [] {
+        const char* e = std::getenv("ACLSPARSE_HIP_SPMV_KERNEL");
+        return e == nullptr || std::string(e) != "stream";
+    }();
+    return flat;
+}
+
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
 {
+    hipStream_t stream_ = stream;
     RowBlockParams p = MakeRowBlockParams(l);
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
@@ -1135,6 +1711,38 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     // arrays), which needs at least one 16-byte group of col_ind / values.
     const bool vec = kCanVec && l.nnz >= 4 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 &&
                      l.y_stride == 1 && Aligned16(l.col) && Aligned16(l.val);
+    if constexpr (kCanVec && A == AccKind::F32) {
+        // Stream kernel: 32-bit buffer offsets into x, contiguous y.
+        const bool stream = vec && static_cast<int64_t>(l.cols) * static_cast<int64_t>(sizeof(typename ValOf<V>::T)) <=
+                                       0x7FFFFFFFLL && !UseWaveKernel();
+        if (stream && UseFlatKernel()) {
+            const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+            const int64_t wgs = (p.num_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
+            const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+            if (betaNz) {
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kWavesPerGroup), 0,
+                                   stream_, p);
+            } else {
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kWavesPerGroup),
+                                   0, stream_, p);
+            }
+            return 0;
+        }
+        if (stream) {
+            const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+            unsigned pg = 0;
+            if (betaNz) {
+                PersistentShape(p, reinterpret_cast<const void*>(&SpmvStreamKernel<RowT, V, O, true>), pg);
+                hipLaunchKernelGGL((SpmvStreamKernel<RowT, V, O, true>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
+                                   stream_, p);
+            } else {
+                PersistentShape(p, reinterpret_cast<const void*>(&SpmvStreamKernel<RowT, V, O, false>), pg);
+                hipLaunchKernelGGL((SpmvStreamKernel<RowT, V, O, false>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
+                                   stream_, p);
+            }
+            return 0;
+        }
+    }
     if constexpr (kCanVec) {
         if (vec) {
             // beta is known on the host unless it lives in device memory.
