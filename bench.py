@@ -56,7 +56,9 @@ def profile_mode(name, steps):
     op = Operation.NON_TRANSPOSE if w.trans == "N" else Operation.TRANSPOSE
     plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
     plan.preprocess()
+    flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
     for _ in range(steps):
+        flush_buf.add_(1)  # same L2/MALL state as a bench step
         plan.run()
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -76,8 +78,29 @@ def make(name, dev):
     return wl.config(name, dev)
 
 
+def _timed(stream, fn, reps):
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
 def measure(w, steps, warmup, flush_buf):
-    """Median/mean/p90 SpMV time (ms, HIP events) over ``steps`` flushed launches."""
+    """SpMV time per step (ms) with L2/MALL flushed before every SpMV.
+
+    A step is one 512 MiB flush write followed by one SpMV, so the SpMV starts
+    with its inputs in HBM only.  ``median_ms`` is the median over ``steps``
+    of an event pair around each SpMV launch on the launch stream: it agrees
+    with the kernel duration rocprofv3 reports for the same launches (it
+    includes the dispatch latency of one launch, a few microseconds).
+    ``paired_ms`` (events around back-to-back flush+SpMV steps minus flushes
+    alone) and ``warm_ms`` (back-to-back SpMVs, L2/MALL warm) are for
+    reference only.
+    """
     from ops_sparse.spmv import CsrSpMV
     from ops_sparse._lib import Operation
 
@@ -91,32 +114,39 @@ def measure(w, steps, warmup, flush_buf):
     p1.record(stream)
     torch.cuda.synchronize()
     pre_ms = p0.elapsed_time(p1)
-    for _ in range(warmup):
+
+    def flush():
+        flush_buf.add_(1)
+
+    def step():
         flush_buf.add_(1)
         plan.run()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    torch.cuda.synchronize()
+
+    for _ in range(warmup):
+        step()
+    rounds = 5
+    per_round = max(1, steps // rounds)
+    diffs = []
     t0 = time.perf_counter()
+    for _ in range(rounds):
+        both = _timed(stream, step, per_round)
+        alone = _timed(stream, flush, per_round)
+        diffs.append(both - alone)
+    wall = (time.perf_counter() - t0) * 1e3 / (rounds * per_round)
+    # one event pair per launch (includes the launch latency)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for a, b in evs:
         flush_buf.add_(1)
         a.record(stream)
         plan.run()
         b.record(stream)
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
-    times = sorted(a.elapsed_time(b) for a, b in evs)
+    ev = statistics.median(a.elapsed_time(b) for a, b in evs)
     # back-to-back launches without a flush (L2/MALL warm), for reference only
-    torch.cuda.synchronize()
-    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    h0.record(stream)
-    for _ in range(steps):
-        plan.run()
-    h1.record(stream)
-    torch.cuda.synchronize()
-    warm = h0.elapsed_time(h1) / steps
-    return dict(median_ms=statistics.median(times), mean_ms=statistics.fmean(times),
-                p90_ms=times[min(len(times) - 1, int(0.9 * len(times)))], wall_ms_per_step=wall,
-                warm_ms=warm, preprocess_ms=pre_ms, workspace_bytes=plan.buffer_size)
+    warm = _timed(stream, plan.run, steps)
+    return dict(median_ms=ev, paired_ms=statistics.median(diffs), paired_min_ms=min(diffs),
+                paired_max_ms=max(diffs), wall_ms_per_step=wall, warm_ms=warm, preprocess_ms=pre_ms,
+                workspace_bytes=plan.buffer_size)
 
 
 def cpu_baseline(w, seconds):
@@ -208,7 +238,7 @@ def main():
                    "index": "int32", "op": "N", "l2_mall_flushed": True, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(h["frac"], 4), "traffic": load_traffic("c2"),
-                     "kernel": "SpmvRowBlockKernel", "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
+                     "kernel": "SpmvStreamFlatKernel", "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
