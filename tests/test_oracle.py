@@ -354,3 +354,32 @@ def test_mere_mare_closed_form():
     a[0] = 1.0 + 2 ** -15
     ok, mere, mare = oracle.verify_mere_mare(g, a, 1e-6, 5.0)
     assert mere < 1e-6 and mare > 5e-6 and not ok
+
+
+def test_trans_lowp_and_row_scale_closed_forms():
+    """Transposed fp16/bf16 oracle against an fp32 brute force; the tolerance scale against numpy."""
+    rows, cols = 120, 90
+    rp, col, val = rand_csr(rows, cols, 0.08, 13)
+    rng = np.random.default_rng(14)
+    x = rng.uniform(-2, 2, rows).astype(np.float32)
+    y = rng.uniform(-2, 2, cols).astype(np.float32)
+    vb = torch.from_numpy(val).to(torch.bfloat16)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    vbits = vb.view(torch.int16).numpy().view(np.uint16)
+    xbits = xb.view(torch.int16).numpy().view(np.uint16)
+    z = oracle.spmv_lowp(rp, col, vbits, xbits, y, oracle.K_BF16, oracle.K_F32, 0.75, -1.5, transpose=True,
+                         cols=cols)
+    acc = np.zeros(cols, np.float32)
+    vf, xf = vb.float().numpy(), xb.float().numpy()
+    for r in range(rows):
+        for q in range(rp[r], rp[r + 1]):
+            acc[col[q]] = np.float32(acc[col[q]] + np.float32(vf[q] * xf[r]))
+    exp = np.float32(0.75) * acc + np.float32(-1.5) * y
+    np.testing.assert_allclose(z, exp, rtol=1e-6, atol=1e-6)
+    A = sp.csr_matrix((val.astype(np.float64), col, rp), shape=(rows, cols))
+    xn = rng.uniform(-2, 2, cols).astype(np.float32)
+    yn = rng.uniform(-2, 2, rows).astype(np.float32)
+    s = oracle.row_scale(rp, col, val, xn, yn, oracle.K_F32, oracle.K_F32, -2.0, 0.5, cols=cols)
+    np.testing.assert_allclose(s, 2.0 * (abs(A) @ np.abs(xn.astype(np.float64))) + 0.5 * np.abs(yn), rtol=1e-12)
+    st = oracle.row_scale(rp, col, val, x, y, oracle.K_F32, oracle.K_F32, -2.0, 0.5, transpose=True, cols=cols)
+    np.testing.assert_allclose(st, 2.0 * (abs(A).T @ np.abs(x.astype(np.float64))) + 0.5 * np.abs(y), rtol=1e-12)
