@@ -161,7 +161,19 @@ struct SpmvLayout {
     int64_t items_per_block = 0;
     int64_t num_blocks = 0;
     uint32_t rowptr_bytes = 4;
+    // Transpose by columns (CSC pattern built by Preprocess): column offsets
+    // colptr[cols+1] (RowT), the row of every entry csc_row[nnz] (int32) and
+    // its position in the CSR arrays csc_pos[nnz] (RowT), plus the sort's
+    // temporary arrays (key_a/key_b int32[nnz], val_b RowT[nnz], radix-sort
+    // storage).  Without it (nnz beyond the sort's int range) the transpose
+    // scatters with atomics into the accumulator at acc_offset.
+    bool csc = false;
+    size_t colptr_offset = 0, csc_row_offset = 0, csc_pos_offset = 0;
+    size_t key_a_offset = 0, key_b_offset = 0, val_b_offset = 0, sort_offset = 0, sort_bytes = 0;
 };
+
+// Radix-sort temporary storage for the CSC build (implemented in spmv_kernels.hip).
+size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes);
 
 inline size_t AccumulatorBytes(aclDataType computeType)
 {
@@ -182,7 +194,22 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.acc_offset = l.sink_offset + kSinkBytes;
     l.total = l.acc_offset;
     if (transpose) {
-        l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));
+        l.csc = nnz > 0 && nnz <= 0x7FFFFFFFULL;
+        if (!l.csc) {
+            l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));
+        } else {
+            const size_t n = static_cast<size_t>(nnz);
+            const size_t rb = l.rowptr_bytes;
+            l.colptr_offset = AlignUp(l.acc_offset);
+            l.csc_row_offset = AlignUp(l.colptr_offset + static_cast<size_t>(cols + 1) * rb);
+            l.csc_pos_offset = AlignUp(l.csc_row_offset + n * sizeof(int32_t));
+            l.key_a_offset = AlignUp(l.csc_pos_offset + n * rb);
+            l.key_b_offset = AlignUp(l.key_a_offset + n * sizeof(int32_t));
+            l.val_b_offset = AlignUp(l.key_b_offset + n * sizeof(int32_t));
+            l.sort_offset = AlignUp(l.val_b_offset + n * rb);
+            l.sort_bytes = CscSortTempBytes(static_cast<int64_t>(nnz), l.rowptr_bytes);
+            l.total = AlignUp(l.sort_offset + l.sort_bytes + 256);  // re-aligned to 256 bytes at use
+        }
     }
     return l;
 }

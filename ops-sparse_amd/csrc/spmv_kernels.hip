@@ -23,6 +23,7 @@
 //  * Block ids are remapped so that each of the 8 XCDs processes one
 //    contiguous eighth of the matrix (x neighbourhoods stay in one L2).
 #include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
 
 #include <cstdint>
 #include <cstdlib>
@@ -1020,6 +1021,18 @@ __device__ __forceinline__ Stage NextStageCached(const TileCache<RowT>& c, const
 }
 
 constexpr int kBufNonTemporal = 2;  // cache policy bit of buffer loads: streaming data
+#if defined(SPMV_EXP_XPOL)
+constexpr int kGatherPolicy = SPMV_EXP_XPOL;
+#else
+constexpr int kGatherPolicy = 0;
+#endif
+#if defined(SPMV_EXP_ROW_NT)
+constexpr int kRowPolicy = kBufNonTemporal;
+#elif defined(SPMV_EXP_ROW_SC)
+constexpr int kRowPolicy = 1;
+#else
+constexpr int kRowPolicy = 0;
+#endif
 
 template <ValKind V>
 struct StreamVals;
@@ -1110,15 +1123,15 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
         const int i = lane + h * kWave;
         if constexpr (sizeof(RowT) == 8) {
             b.rp[h] = static_cast<RowT>(__builtin_bit_cast(
-                long long, __builtin_amdgcn_raw_buffer_load_b64(rr, i * 8, 0, 0)));
+                long long, __builtin_amdgcn_raw_buffer_load_b64(rr, i * 8, 0, kRowPolicy)));
         } else {
-            b.rp[h] = static_cast<RowT>(__builtin_amdgcn_raw_buffer_load_b32(rr, i * 4, 0, 0));
+            b.rp[h] = static_cast<RowT>(__builtin_amdgcn_raw_buffer_load_b32(rr, i * 4, 0, kRowPolicy));
         }
         if constexpr (kBeta) {
             if constexpr (sizeof(OutT) == 4) {
-                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b32(ry, i * 4, 0, 0));
+                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b32(ry, i * 4, 0, kRowPolicy));
             } else {
-                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b16(ry, i * 2, 0, 0));
+                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b16(ry, i * 2, 0, kRowPolicy));
             }
         } else {
             b.yold[h] = OutT{};
@@ -1175,18 +1188,46 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
         const uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
 #endif
         if constexpr (sizeof(ValT) == 4) {
-            xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, 0);
+            xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else {
-            xg[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, static_cast<int>(off), 0, 0);
+            xg[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, static_cast<int>(off), 0, kGatherPolicy);
         }
     }
 }
 
+// Butterfly step across lanes l and l^m (m < 32) without address setup.
+template <int M>
+__device__ __forceinline__ float SwizzleXor(float v)
+{
+    static_assert(M > 0 && M < 32, "swizzle reaches within 32 lanes");
+    constexpr int kPattern = 0x1F | (M << 10);  // and 0x1F, or 0, xor M
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kPattern));
+}
+
+// Sum over the lanes of groups of 2^lg consecutive lanes (lg <= 5), on every lane.
+__device__ __forceinline__ float GroupSum(float v, int lg)
+{
+    if (lg >= 1) v += SwizzleXor<1>(v);
+    if (lg >= 2) v += SwizzleXor<2>(v);
+    if (lg >= 3) v += SwizzleXor<4>(v);
+    if (lg >= 4) v += SwizzleXor<8>(v);
+    if (lg >= 5) v += SwizzleXor<16>(v);
+    return v;
+}
+
+// Sum over the wave (wave-uniform result).
 __device__ __forceinline__ float WaveSum(float v)
 {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
-    return v;
+    v = GroupSum(v, 5);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+// Value of lane l+1 (lane 63 receives `last`).
+__device__ __forceinline__ int32_t FromNextLane(int32_t v, int32_t last)
+{
+    constexpr int kWaveShl1 = 0x130;
+    return __builtin_amdgcn_update_dpp(last, v, kWaveShl1, 0xF, 0xF, false);
 }
 
 // LDS product slots per wave: one chunk plus 8 so that a predicated read of
@@ -1227,11 +1268,8 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     int32_t rs[2], re[2];
     rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
     rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
-    const int32_t nxt0 = __shfl_down(rs[0], 1, kWave);
-    const int32_t nxt1 = __shfl_down(rs[1], 1, kWave);
-    const int32_t r64 = __shfl(rs[1], 0, kWave);
-    re[0] = lane == kWave - 1 ? r64 : nxt0;
-    re[1] = nxt1;
+    re[0] = FromNextLane(rs[0], __builtin_amdgcn_readlane(rs[1], 0));
+    re[1] = FromNextLane(rs[1], rs[1]);
 
     const int gsz = 1 << lg;
     const int cap = SerialCap(lg);
@@ -1251,6 +1289,12 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
 
     // Phase 1.
     float sum[2] = {0.0f, 0.0f};
+#if defined(SPMV_EXP_NO_REDUCE)
+    if (true) {
+        sum[0] = prod[0] + prod[1] + prod[2] + prod[3] + prod[4] + prod[5] + prod[6] + prod[7];
+        defer[0] = defer[1] = false;
+    } else
+#endif
     if (lg == 0) {
         // One lane per row, at most 8 entries: 8 predicated reads, no branch.
 #pragma unroll
@@ -1276,8 +1320,12 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         if (in && ge - gs <= cap) {
             for (int32_t q = gs + sub; q < ge; q += gsz) part += sVal[q - shift];
         }
-        for (int m = 1; m < gsz; m <<= 1) part += __shfl_xor(part, m, kWave);
-        sum[0] = __shfl(part, lane << lg, kWave);  // lane i owns row i (nr <= 32 here)
+        if (lg <= 5) {
+            part = GroupSum(part, lg);
+        } else {
+            part = WaveSum(part);
+        }
+        sum[0] = __shfl(part, (lane << lg) & (kWave - 1), kWave);  // lane i owns row i (nr <= 32 here)
     }
 
     // Phase 2: deferred rows, whole wave per row, in row order.
@@ -1287,7 +1335,7 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         while (pending[h]) {
             const int l = __builtin_ctzll(pending[h]);
             pending[h] &= pending[h] - 1;
-            const int32_t s0 = __shfl(rs[h], l, kWave), e0 = __shfl(re[h], l, kWave);
+            const int32_t s0 = __builtin_amdgcn_readlane(rs[h], l), e0 = __builtin_amdgcn_readlane(re[h], l);
             const int32_t lo = s0 > c0 ? s0 : c0;
             const int32_t hi = e0 < c1 ? e0 : c1;
             float part = 0.0f;
@@ -1311,8 +1359,12 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         if constexpr (kBeta) {
             if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
         }
+#if defined(SPMV_EXP_COND_STORE)
+        if (fin[h]) y[cur.r0 + i] = FromAcc<O, AccKind::F32>(r);
+#else
         OutT* dst = fin[h] ? y + (cur.r0 + i) : sink;
         *dst = FromAcc<O, AccKind::F32>(r);
+#endif
     }
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 }
@@ -1386,6 +1438,39 @@ __global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvStreamKernel(RowBlo
     }
 }
 
+// Opens block `tile` with both metadata pairs loaded at once (no dependent
+// scalar loads).
+template <typename RowT>
+__device__ __forceinline__ Stage OpenTileFlat(const RowBlockParams& p, int64_t tile)
+{
+    typedef int v2s __attribute__((ext_vector_type(2)));
+    Stage s{};
+    s.tile = 0;
+    s.valid = true;
+    const v2s rr = ConstLoad<v2s>(p.blocks + tile, 0);
+    int64_t k0, k1;
+    if constexpr (sizeof(RowT) == 8) {
+        typedef long long v2l __attribute__((ext_vector_type(2)));
+        const v2l kk = ConstLoad<v2l>(static_cast<const int64_t*>(p.block_nnz) + tile, 0);
+        k0 = kk.x;
+        k1 = kk.y;
+    } else {
+        const v2s kk = ConstLoad<v2s>(static_cast<const int32_t*>(p.block_nnz) + tile, 0);
+        k0 = kk.x;
+        k1 = kk.y;
+    }
+    s.r0 = rr.x;
+    const int32_t n = rr.y - rr.x;
+    s.nr = n < 0 ? 0 : n > kWaveRows ? kWaveRows : n;
+    s.k0 = k0;
+    const int64_t span = k1 - k0;
+    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
+    s.c0 = 0;
+    s.first = true;
+    ChunkBounds(s);
+    return s;
+}
+
 // One block per wave, no persistence: the hardware keeps as many waves
 // resident as registers allow (the kernel is built for 8 waves per SIMD) and
 // their independent loads keep HBM busy.  Chunks of a multi-chunk block are
@@ -1414,13 +1499,16 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
     float carry = 0.0f;
     int lg = 0;
-    Stage cur = OpenTile<RowT>(p, 0, tile, 1, tile + 1);
+    Stage cur = OpenTileFlat<RowT>(p, tile);
     while (cur.valid) {
         L b;
         StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
         StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
         StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
-        cur = NextStage<RowT>(p, cur, tile, 1, tile + 1);
+        if (cur.last) break;
+        cur.c0 = cur.c1;
+        cur.first = false;
+        ChunkBounds(cur);
     }
 }
 
@@ -1525,6 +1613,130 @@ __global__ __launch_bounds__(kThreads) void SpmvScatterKernel(RowBlockParams p)
         Acc contrib = a * ToAcc<V, A>(x[row * p.x_stride]);
         if constexpr (A != AccKind::I64) contrib = alpha * contrib;
         AtomicAddAcc(out + c * p.y_stride, contrib);
+    }
+}
+
+// ------------------------- transpose by columns ------------------------------
+//
+// Preprocess sorts the entries by column (stable radix sort of (column,
+// position) pairs), so y_j = alpha * sum_{i} conj?(a_ij) * x_i + beta * y_j is
+// a gather over column j's entries: no atomics, a fixed summation order
+// (deterministic results, the reference's CSR_ALG2 transpose semantics,
+// sparse/spmv/arch35/spmv_kernel.cpp:861-879), and the values are read from
+// the caller's array at execution time.
+
+struct CscBuildParams {
+    const int32_t* col;
+    int64_t col_stride;
+    int32_t base;
+    int64_t rows, cols, nnz;
+    const void* norm;  // normalised row offsets (RowT)
+    int32_t* key;      // sort keys: column, or cols for entries outside the matrix
+    void* pos;         // sort values: position in the CSR arrays
+};
+
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void CscInitKernel(CscBuildParams q)
+{
+    const RowT* norm = static_cast<const RowT*>(q.norm);
+    const int64_t first = static_cast<int64_t>(norm[0]);
+    const int64_t last = static_cast<int64_t>(norm[q.rows]);
+    RowT* pos = static_cast<RowT*>(q.pos);
+    for (int64_t k = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; k < q.nnz;
+         k += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t c = static_cast<int64_t>(q.col[k * q.col_stride]) - q.base;
+        const bool ok = k >= first && k < last && c >= 0 && c < q.cols;
+        q.key[k] = static_cast<int32_t>(ok ? c : q.cols);
+        pos[k] = static_cast<RowT>(k);
+    }
+}
+
+// colptr[c] = first sorted entry with column >= c, for c in [0, cols].
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void CscColPtrKernel(const int32_t* keys, int64_t nnz, int64_t cols,
+                                                            RowT* colptr)
+{
+    for (int64_t k = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; k <= nnz;
+         k += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t prev = k == 0 ? -1 : static_cast<int64_t>(keys[k - 1]);
+        const int64_t cur = k == nnz ? cols : static_cast<int64_t>(keys[k]);
+        for (int64_t c = prev + 1; c <= cur; ++c) colptr[c] = static_cast<RowT>(k);
+    }
+}
+
+// Row of every sorted entry (last row whose normalised offset is <= the
+// entry's position); the positions move to their final array if the sort
+// left them in the other buffer.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPos, RowT* pos, int32_t* row,
+                                                            const RowT* norm, int64_t rows, int64_t n)
+{
+    for (int64_t k = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; k < n;
+         k += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const RowT p = sortedPos[k];
+        if (sortedPos != pos) pos[k] = p;
+        int64_t lo = 0, hi = rows - 1;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if (norm[mid] <= p) lo = mid;
+            else hi = mid - 1;
+        }
+        row[k] = static_cast<int32_t>(lo);
+    }
+}
+
+__device__ __forceinline__ float ShflXorAcc(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ long long ShflXorAcc(long long v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
+{
+    return C64{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
+}
+
+struct CscParams {
+    const void* colptr;  // RowT[cols+1]
+    const int32_t* row;
+    const void* pos;     // RowT[nnz]
+    const void* val;
+    int64_t val_stride;
+    const void* x;
+    int64_t x_stride;
+    void* y;
+    int64_t y_stride;
+    int64_t cols;
+    int32_t lg;  // log2 lanes per column
+    int32_t conj;
+    Scalars s;
+};
+
+// 2^lg lanes per column, each over a strided subset of the column's entries,
+// merged by a fixed butterfly; the first lane applies the epilogue.
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__global__ __launch_bounds__(kThreads) void SpmvCscGatherKernel(CscParams q)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    const int lg = q.lg;
+    const int g = 1 << lg;
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> lg;
+    const int sub = threadIdx.x & (g - 1);
+    Acc alpha, beta;
+    LoadScalars<A>(q.s, alpha, beta);
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    const RowT* pos = static_cast<const RowT*>(q.pos);
+    const ValT* val = static_cast<const ValT*>(q.val);
+    const ValT* x = static_cast<const ValT*>(q.x);
+    Acc sum = Zero<Acc>();
+    if (c < q.cols) {
+        const int64_t k1 = static_cast<int64_t>(colptr[c + 1]);
+        for (int64_t k = static_cast<int64_t>(colptr[c]) + sub; k < k1; k += g) {
+            const int64_t pk = static_cast<int64_t>(pos[k]);
+            const Acc a = MaybeConj<V, A>(ToAcc<V, A>(val[pk * q.val_stride]), q.conj);
+            sum = sum + a * ToAcc<V, A>(x[static_cast<int64_t>(q.row[k]) * q.x_stride]);
+        }
+    }
+    for (int m = 1; m < g; m <<= 1) sum = sum + ShflXorAcc(sum, m);
+    if (c < q.cols && sub == 0) {
+        StoreRow<O, A>(static_cast<typename OutOf<O>::T*>(q.y), c * q.y_stride, sum, alpha, beta, !IsZero(beta));
     }
 }
 
@@ -1770,6 +1982,31 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
     using Acc = typename AccOf<A>::T;
     RowBlockParams p = MakeRowBlockParams(l);
     const int64_t n = l.cols;
+    if (l.layout.csc) {
+        if (n <= 0) return 0;
+        CscParams q{};
+        q.colptr = At<void>(l.ws, l.layout.colptr_offset);
+        q.row = At<int32_t>(l.ws, l.layout.csc_row_offset);
+        q.pos = At<void>(l.ws, l.layout.csc_pos_offset);
+        q.val = l.val;
+        q.val_stride = l.val_stride;
+        q.x = l.x;
+        q.x_stride = l.x_stride;
+        q.y = l.y;
+        q.y_stride = l.y_stride;
+        q.cols = n;
+        q.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
+        q.s = p.s;
+        // lanes per column: the power of two nearest below the mean column length, <= 64
+        const int64_t mean = l.nnz / n;
+        int lg = 0;
+        while (lg < 6 && (int64_t{2} << lg) <= mean) ++lg;
+        q.lg = lg;
+        const int64_t threads = n << lg;
+        const unsigned grid = static_cast<unsigned>((threads + kThreads - 1) / kThreads);
+        hipLaunchKernelGGL((SpmvCscGatherKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, q);
+        return 0;
+    }
     // y already has the accumulator type: scale it by beta and scatter into it.
     constexpr bool kDirect = (O == OutKind::F32 && A == AccKind::F32) || (O == OutKind::C64 && A == AccKind::C64);
     Acc* acc = At<Acc>(l.ws, l.layout.acc_offset);
@@ -1823,7 +2060,58 @@ int DispatchTypes(const SpmvLaunch& l, hipStream_t s)
     }
 }
 
+template <typename RowT>
+int BuildCsc(const SpmvLaunch& l, hipStream_t s)
+{
+    const int64_t nnz = l.nnz;
+    CscBuildParams q{};
+    q.col = l.col;
+    q.col_stride = l.col_stride;
+    q.base = l.base;
+    q.rows = l.rows;
+    q.cols = l.cols;
+    q.nnz = nnz;
+    q.norm = At<void>(l.ws, l.layout.rowptr_offset);
+    q.key = At<int32_t>(l.ws, l.layout.key_a_offset);
+    q.pos = At<void>(l.ws, l.layout.csc_pos_offset);
+    hipLaunchKernelGGL((CscInitKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, q);
+    hipcub::DoubleBuffer<int32_t> keys(At<int32_t>(l.ws, l.layout.key_a_offset),
+                                       At<int32_t>(l.ws, l.layout.key_b_offset));
+    hipcub::DoubleBuffer<RowT> vals(At<RowT>(l.ws, l.layout.csc_pos_offset), At<RowT>(l.ws, l.layout.val_b_offset));
+    int endBit = 1;
+    while (endBit < 31 && (int64_t{1} << endBit) <= l.cols) ++endBit;
+    void* temp = reinterpret_cast<void*>(
+        (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, l.layout.sort_offset)) + 255) & ~uintptr_t{255});
+    size_t tempBytes = l.layout.sort_bytes;
+    if (hipcub::DeviceRadixSort::SortPairs(temp, tempBytes, keys, vals, static_cast<int>(nnz), 0, endBit, s) !=
+        hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL((CscColPtrKernel<RowT>), dim3(GridFor(nnz + 1)), dim3(kThreads), 0, s, keys.Current(), nnz,
+                       l.cols, At<RowT>(l.ws, l.layout.colptr_offset));
+    hipLaunchKernelGGL((CscFinishKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, vals.Current(),
+                       At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.csc_row_offset),
+                       At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, nnz);
+    return 0;
+}
+
 }  // namespace
+
+size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes)
+{
+    size_t bytes = 0;
+    hipcub::DoubleBuffer<int32_t> k(nullptr, nullptr);
+    hipError_t e;
+    if (posBytes == 8) {
+        hipcub::DoubleBuffer<int64_t> v(nullptr, nullptr);
+        e = hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, k, v, static_cast<int>(nnz), 0, 31);
+    } else {
+        hipcub::DoubleBuffer<int32_t> v(nullptr, nullptr);
+        e = hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, k, v, static_cast<int>(nnz), 0, 31);
+    }
+    if (e != hipSuccess) bytes = static_cast<size_t>(nnz) * 16 + (1 << 20);
+    return bytes;
+}
 
 int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
 {
@@ -1862,8 +2150,10 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (l.rowptr64) {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int64_t>), dim3(grid), dim3(kThreads), 0, s, p);
+        if (l.layout.csc) return BuildCsc<int64_t>(l, s);
     } else {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
+        if (l.layout.csc) return BuildCsc<int32_t>(l, s);
     }
     return 0;
 }
