@@ -331,3 +331,44 @@ def test_long_last_row_with_beta(dev):
     assert (blocks[:-1] == lengths.numel()).any(), "fixture must produce blocks that start at row == rows"
     _, y, _ = run_workload(w, dev)
     assert_close(w, y)
+
+
+@pytest.mark.parametrize("op", ["T", "H"])
+def test_transpose_by_columns_is_deterministic(op, dev):
+    """The column-gather transpose sums every column in a fixed order: two runs agree bit for bit,
+    also with a different algorithm id and without Preprocess (reference CSR_ALG2 semantics)."""
+    w = wl.config("c5", "cpu", 32)
+    if op == "H":
+        g = torch.Generator().manual_seed(3)
+        w.values = torch.complex(w.values, torch.rand(w.nnz, generator=g) - 0.5)
+        w.x = torch.complex(w.x, torch.rand(w.x.numel(), generator=g) - 0.5)
+        w.y0 = torch.complex(w.y0, torch.zeros_like(w.y0))
+        w.out_dtype = torch.complex64
+    w.trans = op
+    outs = []
+    for alg, pre in ((SpMVAlg.DEFAULT, True), (SpMVAlg.CSR_ALG2, True), (SpMVAlg.DEFAULT, False)):
+        _, y, _ = run_workload(w, dev, alg=alg, preprocess=pre)
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    if op == "T":
+        assert_close(w, outs[0].to(dev))
+    else:
+        rp = w.row_ptr.numpy().astype(np.int64)
+        z = oracle.spmv_c64(rp, w.col_ind.numpy(), w.values.numpy(), w.x.numpy(), w.y0.numpy(), w.cols, 2,
+                            w.alpha, w.beta)
+        np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+
+
+def test_transpose_skips_entries_outside_the_rows(dev):
+    """Row offsets that start past 0 (base 1 with rowPtr[0] = 3): entries before the first row and
+    after the last are not part of the matrix."""
+    rp = t([3, 5, 6], torch.int32, dev)          # base 1: rows own entries 2..4 (0-based 2,3 and 4)
+    ci = t([1, 2, 1, 3, 2, 3], torch.int32, dev)  # entries 0, 1 and 5 are outside the rows
+    va = t([100.0, 100.0, 2.0, 3.0, 4.0, 100.0], torch.float32, dev)
+    x = t([1.0, 10.0], torch.float32, dev)
+    y = t([0.0, 0.0, 0.0], torch.float32, dev)
+    plan = CsrSpMV(2, 3, rp, ci, va, x, y, 1.0, 0.0, op=Operation.TRANSPOSE, base=1)
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy(), [2.0, 40.0, 3.0])
