@@ -170,7 +170,22 @@ struct SpmvLayout {
     bool csc = false;
     size_t colptr_offset = 0, csc_row_offset = 0, csc_pos_offset = 0;
     size_t key_a_offset = 0, key_b_offset = 0, val_b_offset = 0, sort_offset = 0, sort_bytes = 0;
+    // Long-block tasks (non-transpose, fp32 compute): a block of more than
+    // kLongChunks chunks is split into one task per chunk.  task_start[B+1]
+    // (exclusive scan of the per-block task counts; task_start[B] = total),
+    // task_block[max_tasks], the partial sums of the rows crossing each task's
+    // first / last slot (task_head / task_tail, float[max_tasks]), a per-block
+    // arrival counter (task_cnt, uint32[B]) and the scan's temporary storage.
+    bool tasks = false;
+    int64_t max_tasks = 0;
+    size_t task_start_offset = 0, task_block_offset = 0, task_head_offset = 0, task_tail_offset = 0;
+    size_t task_cnt_offset = 0, task_scan_offset = 0, task_scan_bytes = 0;
 };
+
+constexpr int64_t kLongChunks = 4;  // blocks with more chunks than this are split into tasks
+
+// Exclusive-scan temporary storage of the task table (implemented in spmv_kernels.hip).
+size_t TaskScanTempBytes(int64_t n);
 
 // Radix-sort temporary storage for the CSC build (implemented in spmv_kernels.hip).
 size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes);
@@ -193,6 +208,23 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.sink_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
     l.acc_offset = l.sink_offset + kSinkBytes;
     l.total = l.acc_offset;
+    if (!transpose && computeType == ACL_FLOAT && nnz > 0) {
+        const int64_t maxTasks = static_cast<int64_t>(nnz / kChunkNnz) + l.num_blocks + 1;
+        if (maxTasks < 0x7FFFFFFFLL) {
+            l.tasks = true;
+            l.max_tasks = maxTasks;
+            const size_t mt = static_cast<size_t>(maxTasks);
+            const size_t nb1 = static_cast<size_t>(l.num_blocks + 1);
+            l.task_start_offset = AlignUp(l.total);
+            l.task_block_offset = AlignUp(l.task_start_offset + nb1 * sizeof(int32_t));
+            l.task_head_offset = AlignUp(l.task_block_offset + mt * sizeof(int32_t));
+            l.task_tail_offset = AlignUp(l.task_head_offset + mt * sizeof(float));
+            l.task_cnt_offset = AlignUp(l.task_tail_offset + mt * sizeof(float));
+            l.task_scan_offset = AlignUp(l.task_cnt_offset + nb1 * sizeof(uint32_t));
+            l.task_scan_bytes = TaskScanTempBytes(l.num_blocks + 1);
+            l.total = AlignUp(l.task_scan_offset + l.task_scan_bytes + 256);  // re-aligned to 256 bytes at use
+        }
+    }
     if (transpose) {
         l.csc = nnz > 0 && nnz <= 0x7FFFFFFFULL;
         if (!l.csc) {

@@ -278,6 +278,15 @@ struct RowBlockParams {
     int64_t per_xcd;
     int32_t workers_per_xcd;
     void* sink;  // per-lane dummy outputs
+    // long-block tasks (see SpmvLayout): tables built by Preprocess
+    const int32_t* task_start;
+    const int32_t* task_block;
+    float* task_head;
+    float* task_tail;
+    uint32_t* task_cnt;
+    int32_t task_waves;  // waves serving tasks (0: tasks off)
+    int32_t task_wgs;    // workgroups serving tasks (the first ones of the grid)
+    int64_t max_tasks;   // capacity of the task arrays
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -1238,10 +1247,15 @@ constexpr int kStreamLds = kWaveChunk + 8;
 // rows, lane groups), phase 2 (long or chunk-crossing rows, whole wave), y.
 // Row i of the block (i = lane + 64h) has its offsets in registers: its
 // start in this lane's rp[h], its end in the next row's.
-template <typename RowT, ValKind V, OutKind O, bool kBeta>
+// Task mode (kTask): the chunk is one task of a long block; rows that cross
+// the chunk's first slot leave their partial sum in `head` (also when they
+// cross both ends), the row that crosses its last slot in `tail`, and neither
+// is written to y here.
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false>
 __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<RowT, V, O>& lc, float* sVal, int lane,
                                             float alpha, float beta, float& carry, int& lg, typename OutOf<O>::T* y,
-                                            typename OutOf<O>::T* sink)
+                                            typename OutOf<O>::T* sink, float* head = nullptr,
+                                            float* tail = nullptr)
 {
     using OutT = typename OutOf<O>::T;
     float prod[kLaneItems];
@@ -1251,7 +1265,11 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     const int32_t c0 = cur.c0, c1 = cur.c1;
     const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);  // LDS slot of relative offset r: r - shift
     const int nr = cur.nr;
-    if (cur.first) {
+    if constexpr (kTask) {
+        lg = 0;
+        *head = 0.0f;
+        *tail = 0.0f;
+    } else if (cur.first) {
         carry = 0.0f;
         // Lanes per row: as many as keep every row of the block on its own
         // lane group, 1 when the block spans several chunks.
@@ -1341,12 +1359,23 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
             float part = 0.0f;
             for (int32_t q = lo + lane; q < hi; q += kWave) part += sVal[q - shift];
             float total = WaveSum(part);
-            if (s0 < c0) total += carry;
-            if (e0 > c1) {
-                carry = total;
-            } else if (lane == l) {
-                sum[h] = total;
-                fin[h] = true;
+            if constexpr (kTask) {
+                if (s0 < c0) {
+                    *head = total;
+                } else if (e0 > c1) {
+                    *tail = total;
+                } else if (lane == l) {
+                    sum[h] = total;
+                    fin[h] = true;
+                }
+            } else {
+                if (s0 < c0) total += carry;
+                if (e0 > c1) {
+                    carry = total;
+                } else if (lane == l) {
+                    sum[h] = total;
+                    fin[h] = true;
+                }
             }
         }
     }
@@ -1471,10 +1500,68 @@ __device__ __forceinline__ Stage OpenTileFlat(const RowBlockParams& p, int64_t t
     return s;
 }
 
+// Number of chunks of a block (the first chunk starts at the block's
+// 16-byte-aligned first non-zero).
+__device__ __forceinline__ int64_t BlockChunks(int64_t k0, int64_t kspan)
+{
+    return (kspan + (k0 & 3) + kWaveChunk - 1) / kWaveChunk;
+}
+
+// Combines the partial sums of the rows of long block b that cross chunk
+// boundaries, in chunk order: tail of the chunk where the row starts, then the
+// heads of the following chunks up to the one where it ends.  Run by the last
+// task of the block to arrive.
+template <typename RowT, OutKind O>
+__device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const Stage& blk, int32_t ts, int32_t nT,
+                                               int lane, float alpha, float beta)
+{
+    using OutT = typename OutOf<O>::T;
+    const int64_t r0 = blk.r0;
+    const int nr = blk.nr;
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    const int32_t k0lo = static_cast<int32_t>(blk.k0);
+    int32_t rs[2], re[2];
+    bool in[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave;
+        in[h] = i < nr;
+        rs[h] = in[h] ? static_cast<int32_t>(rp[r0 + i]) - k0lo : 0;
+        re[h] = in[h] ? static_cast<int32_t>(rp[r0 + i + 1]) - k0lo : 0;
+    }
+    const int32_t sh = static_cast<int32_t>(blk.k0 & 3);
+    OutT* y = static_cast<OutT*>(p.y);
+    for (int32_t j = 1; j < nT;) {
+        const int32_t cj = j * kWaveChunk - sh;
+        const uint64_t m0 = __ballot(in[0] && rs[0] < cj && re[0] > cj);
+        const uint64_t m1 = __ballot(in[1] && rs[1] < cj && re[1] > cj);
+        if (m0 == 0 && m1 == 0) {
+            ++j;
+            continue;
+        }
+        const int h = m0 != 0 ? 0 : 1;
+        const int l = __builtin_ctzll(m0 != 0 ? m0 : m1);
+        const int32_t e0 = __builtin_amdgcn_readlane(h == 0 ? re[0] : re[1], l);
+        const int32_t jend = (e0 - 1 + sh) / kWaveChunk;  // chunk of the row's last entry
+        float part = 0.0f;
+        for (int32_t u = j + lane; u <= jend; u += kWave) {
+            part += __hip_atomic_load(p.task_head + ts + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const float total =
+            WaveSum(part) + __hip_atomic_load(p.task_tail + ts + j - 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) StoreRow<O, AccKind::F32>(y, r0 + l + h * kWave, total, alpha, beta, beta != 0.0f);
+        j = jend + 1;
+    }
+}
+
 // One block per wave, no persistence: the hardware keeps as many waves
-// resident as registers allow (the kernel is built for 8 waves per SIMD) and
-// their independent loads keep HBM busy.  Chunks of a multi-chunk block are
-// processed one after another.
+// resident as registers allow (the kernel is built for 7-8 waves per SIMD) and
+// their independent loads keep HBM busy.  Chunks of a block of up to
+// kLongChunks chunks are processed one after another; longer blocks (rows of
+// thousands of entries) are split by Preprocess into one task per chunk,
+// served round-robin by the first task_waves waves of the grid, so a long row
+// is reduced by many waves at once.  Each task stores the partial sums of its
+// chunk-crossing rows; the block's last task to arrive combines them.
 template <typename RowT, ValKind V, OutKind O, bool kBeta>
 __global__ __launch_bounds__(kWave* kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(7)))
 void SpmvStreamFlatKernel(RowBlockParams p)
@@ -1488,8 +1575,6 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float* sVal = sValAll[wv];
-    const int64_t tile = XcdBlock() * kWavesPerGroup + wv;
-    if (tile >= p.num_blocks) return;
 
     float alpha, beta;
     LoadScalars<AccKind::F32>(p.s, alpha, beta);
@@ -1499,7 +1584,58 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
     float carry = 0.0f;
     int lg = 0;
+
+    if (static_cast<int32_t>(blockIdx.x) < p.task_wgs) {
+        // Task worker.
+        const int64_t e = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + wv;
+        int64_t total = ConstLoad<int32_t>(p.task_start, p.num_blocks);
+        total = total < p.max_tasks ? total : p.max_tasks;
+        for (int64_t t = e; t < total; t += p.task_waves) {
+            const int32_t b = ConstLoad<int32_t>(p.task_block, t);
+            if (b < 0 || b >= p.num_blocks) continue;
+            const int32_t ts = ConstLoad<int32_t>(p.task_start, b);
+            const int32_t nT = ConstLoad<int32_t>(p.task_start, b + 1) - ts;
+            const int32_t j = static_cast<int32_t>(t) - ts;
+            const Stage blk = OpenTileFlat<RowT>(p, b);
+            Stage cur = blk;
+            cur.c0 = j == 0 ? 0 : j * kWaveChunk - static_cast<int32_t>(blk.k0 & 3);
+            cur.first = j == 0;
+            ChunkBounds(cur);
+            L bl;
+            StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, bl);
+            StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, bl, bl.xg);
+            float head = 0.0f, tail = 0.0f;
+            StreamChunk<RowT, V, O, kBeta, true>(cur, bl, sVal, lane, alpha, beta, carry, lg, y, sink, &head, &tail);
+            // The partial sums go to memory with device-scope stores (they
+            // bypass this XCD's L2), complete before the arrival is counted,
+            // and the last task reads them with device-scope loads: no
+            // whole-cache write-back or invalidate per task.
+            uint32_t prev = 0;
+            if (lane == 0) {
+                __hip_atomic_store(p.task_head + t, head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.task_tail + t, tail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                prev = __hip_atomic_fetch_add(p.task_cnt + b, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            prev = __builtin_amdgcn_readfirstlane(prev);
+            if (prev == static_cast<uint32_t>(nT - 1)) {
+                if (lane == 0) p.task_cnt[b] = 0U;  // ready for the next call
+                FixupLongBlock<RowT, O>(p, blk, ts, nT, lane, alpha, beta);
+            }
+        }
+        return;
+    }
+
+    // Block worker.
+    const int64_t wg = static_cast<int64_t>(blockIdx.x) - p.task_wgs;
+    const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
+    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kWavesPerGroup + wv;
+    if (tile >= p.num_blocks) return;
     Stage cur = OpenTileFlat<RowT>(p, tile);
+    if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
+#if defined(SPMV_EXP_SKIP_LONG)
+    if (cur.kspan > SPMV_EXP_SKIP_LONG) return;
+#endif
     while (cur.valid) {
         L b;
         StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
@@ -1807,6 +1943,14 @@ RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
     p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
     p.sink = At<void>(l.ws, l.layout.sink_offset);
+    if (l.layout.tasks) {
+        p.task_start = At<int32_t>(l.ws, l.layout.task_start_offset);
+        p.task_block = At<int32_t>(l.ws, l.layout.task_block_offset);
+        p.task_head = At<float>(l.ws, l.layout.task_head_offset);
+        p.task_tail = At<float>(l.ws, l.layout.task_tail_offset);
+        p.task_cnt = At<uint32_t>(l.ws, l.layout.task_cnt_offset);
+        p.max_tasks = l.layout.max_tasks;
+    }
     p.col = l.col;
     p.col_stride = l.col_stride;
     p.val = l.val;
@@ -1930,7 +2074,15 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
         if (stream && UseFlatKernel()) {
             const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
             const int64_t wgs = (p.num_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
-            const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+            int64_t taskWgs = 0;
+            if (l.layout.tasks) {
+                // up to 4096 task waves, a multiple of 8 workgroups (even over the XCDs)
+                int64_t waves = l.layout.max_tasks < 4096 ? l.layout.max_tasks : 4096;
+                taskWgs = (waves + kWavesPerGroup * kXcds - 1) / (kWavesPerGroup * kXcds) * kXcds;
+            }
+            p.task_wgs = static_cast<int32_t>(taskWgs);
+            p.task_waves = static_cast<int32_t>(taskWgs * kWavesPerGroup);
+            const unsigned g = static_cast<unsigned>(taskWgs + (wgs + kXcds - 1) / kXcds * kXcds);
             if (betaNz) {
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kWavesPerGroup), 0,
                                    stream_, p);
@@ -2060,6 +2212,56 @@ int DispatchTypes(const SpmvLaunch& l, hipStream_t s)
     }
 }
 
+// Task table of the long blocks: counts[b] = chunks of block b when it has
+// more than kLongChunks, else 0 (counts[B] = 0); arrival counters cleared.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void TaskCountKernel(const RowT* blockNnz, int64_t numBlocks, int32_t* counts,
+                                                            uint32_t* cnt)
+{
+    for (int64_t b = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; b <= numBlocks;
+         b += static_cast<int64_t>(gridDim.x) * kThreads) {
+        int32_t n = 0;
+        if (b < numBlocks) {
+            const int64_t k0 = static_cast<int64_t>(blockNnz[b]);
+            const int64_t kspan = static_cast<int64_t>(blockNnz[b + 1]) - k0;
+            const int64_t chunks = (kspan + (k0 & 3) + kChunkNnz - 1) / kChunkNnz;
+            n = chunks > kLongChunks ? static_cast<int32_t>(chunks) : 0;
+        }
+        counts[b] = n;
+        cnt[b] = 0U;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void TaskFillKernel(const int32_t* taskStart, int64_t numBlocks,
+                                                           int32_t* taskBlock)
+{
+    for (int64_t b = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; b < numBlocks;
+         b += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int32_t t0 = taskStart[b], t1 = taskStart[b + 1];
+        for (int32_t t = t0; t < t1; ++t) taskBlock[t] = static_cast<int32_t>(b);
+    }
+}
+
+template <typename RowT>
+int BuildTasks(const SpmvLaunch& l, hipStream_t s)
+{
+    const int64_t nb = l.layout.num_blocks;
+    int32_t* counts = At<int32_t>(l.ws, l.layout.task_head_offset);  // temporary: max_tasks >= nb + 1
+    int32_t* start = At<int32_t>(l.ws, l.layout.task_start_offset);
+    hipLaunchKernelGGL((TaskCountKernel<RowT>), dim3(GridFor(nb + 1)), dim3(kThreads), 0, s,
+                       At<const RowT>(l.ws, l.layout.block_nnz_offset), nb, counts,
+                       At<uint32_t>(l.ws, l.layout.task_cnt_offset));
+    void* temp = reinterpret_cast<void*>(
+        (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, l.layout.task_scan_offset)) + 255) & ~uintptr_t{255});
+    size_t tempBytes = l.layout.task_scan_bytes;
+    if (hipcub::DeviceScan::ExclusiveSum(temp, tempBytes, counts, start, static_cast<int>(nb + 1), s) != hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(TaskFillKernel, dim3(GridFor(nb)), dim3(kThreads), 0, s, start, nb,
+                       At<int32_t>(l.ws, l.layout.task_block_offset));
+    return 0;
+}
+
 template <typename RowT>
 int BuildCsc(const SpmvLaunch& l, hipStream_t s)
 {
@@ -2096,6 +2298,16 @@ int BuildCsc(const SpmvLaunch& l, hipStream_t s)
 }
 
 }  // namespace
+
+size_t TaskScanTempBytes(int64_t n)
+{
+    size_t bytes = 0;
+    if (hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, static_cast<int32_t*>(nullptr),
+                                         static_cast<int32_t*>(nullptr), static_cast<int>(n)) != hipSuccess) {
+        bytes = static_cast<size_t>(n) * 8 + (1 << 20);
+    }
+    return bytes;
+}
 
 size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes)
 {
@@ -2151,9 +2363,11 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     if (l.rowptr64) {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int64_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) return BuildCsc<int64_t>(l, s);
+        if (l.layout.tasks) return BuildTasks<int64_t>(l, s);
     } else {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) return BuildCsc<int32_t>(l, s);
+        if (l.layout.tasks) return BuildTasks<int32_t>(l, s);
     }
     return 0;
 }

@@ -372,3 +372,30 @@ def test_transpose_skips_entries_outside_the_rows(dev):
     plan.run()
     torch.cuda.synchronize()
     np.testing.assert_allclose(y.cpu().numpy(), [2.0, 40.0, 3.0])
+
+
+@pytest.mark.parametrize("i64,dtype,beta", [(False, torch.float32, 0.5), (True, torch.float32, 0.0),
+                                             (False, torch.float16, 1.0), (True, torch.bfloat16, -0.25)])
+def test_long_rows_split_into_tasks(i64, dtype, beta, dev):
+    """Rows of thousands of entries are reduced by many waves (one task per chunk) and combined by the
+    block's last task; neighbouring short, empty and medium rows inside the same blocks stay exact."""
+    g = torch.Generator().manual_seed(11)
+    pattern = [0, 3, 60000, 0, 2, 2500, 1, 0, 0, 4097, 5, 130000, 7, 0, 2049, 2048, 2047] + [3] * 3000 + [70000]
+    lengths = torch.tensor(pattern, dtype=torch.int64)
+    cols = 150000
+    rp, col = wl.csr_from_lengths(lengths, cols, g, "cpu")
+    n = col.numel()
+    vals = (torch.rand(n, generator=g) * 2 - 1).to(dtype)
+    x = (torch.rand(cols, generator=g) * 2 - 1).to(dtype)
+    w = wl.Workload("tasks", lengths.numel(), cols, rp.to(torch.int64 if i64 else torch.int32), col, vals, x,
+                    (torch.rand(lengths.numel(), generator=g) * 2 - 1), 1.5, beta, out_dtype=dtype)
+    for pre in (True, False):
+        _, y, plan = run_workload(w, dev, preprocess=pre)
+        assert_close(w, y)
+    # more calls on the same plan and workspace: the arrival counters are reset by each block's last task
+    d = w.to(dev)
+    for _ in range(3):
+        y.copy_(d.y0.to(dtype))
+        plan.run()
+        torch.cuda.synchronize()
+        assert_close(w, y)
