@@ -182,7 +182,10 @@ struct SpmvLayout {
     size_t task_cnt_offset = 0, task_scan_offset = 0, task_scan_bytes = 0;
 };
 
-constexpr int64_t kLongChunks = 4;  // blocks with more chunks than this are split into tasks
+#ifndef SPMV_LONG_CHUNKS
+#define SPMV_LONG_CHUNKS 4
+#endif
+constexpr int64_t kLongChunks = SPMV_LONG_CHUNKS;  // blocks with more chunks than this are split into tasks
 
 // Exclusive-scan temporary storage of the task table (implemented in spmv_kernels.hip).
 size_t TaskScanTempBytes(int64_t n);

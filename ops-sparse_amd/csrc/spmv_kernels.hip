@@ -2047,6 +2047,17 @@ bool UseWaveKernel()
 
 // The one-block-per-wave kernel is the default; ACLSPARSE_HIP_SPMV_KERNEL=
 // stream selects the persistent pipelined variant (for comparisons).
+// Waves serving long-block tasks (ACLSPARSE_HIP_TASK_WAVES overrides, for tuning).
+int64_t TaskWaves()
+{
+    static const int64_t waves = [] {
+        const char* e = std::getenv("ACLSPARSE_HIP_TASK_WAVES");
+        const long long v = e != nullptr ? std::atoll(e) : 0;
+        return v > 0 ? static_cast<int64_t>(v) : int64_t{2048};
+    }();
+    return waves;
+}
+
 bool UseFlatKernel()
 {
     static const bool flat = [] {
@@ -2077,7 +2088,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             int64_t taskWgs = 0;
             if (l.layout.tasks) {
                 // up to 4096 task waves, a multiple of 8 workgroups (even over the XCDs)
-                int64_t waves = l.layout.max_tasks < 4096 ? l.layout.max_tasks : 4096;
+                int64_t waves = l.layout.max_tasks < TaskWaves() ? l.layout.max_tasks : TaskWaves();
                 taskWgs = (waves + kWavesPerGroup * kXcds - 1) / (kWavesPerGroup * kXcds) * kXcds;
             }
             p.task_wgs = static_cast<int32_t>(taskWgs);
