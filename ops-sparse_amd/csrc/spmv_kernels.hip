@@ -916,132 +916,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void* base, int64_t
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(b), 0x00020000);
 }
 
-// Block metadata (blocks[t], blocks[t+1], block_nnz[t], block_nnz[t+1]) of
-// this worker's blocks, kept in a rolling window of 64 lanes: lane l holds
-// the block of ordinal o with o % 64 == l, for the 64 ordinals after the last
-// one opened.  Opening a block is four lane reads.  The window is refilled by
-// one unconditional load pair per chunk (the ordinal 64 ahead of the last
-// opened block), merged one chunk later, so no wait for it ever lands on the
-// loop's critical path and the prefetches stay in flight.
-template <typename RowT>
-struct TileCache {
-    int32_t r0, r1;
-    RowT k0, k1;
-};
-
-template <typename RowT>
-struct TileRefill {
-    int64_t ordinal;  // ordinal loaded (uniform)
-    int32_t r0, r1;
-    RowT k0, k1;
-};
-
-template <typename RowT>
-__device__ __forceinline__ int64_t TileIndex(int64_t ordinal, int64_t first, int64_t stride, int64_t tileEnd)
-{
-    const int64_t t = first + ordinal * stride;
-    return t < tileEnd ? t : first;  // first < tileEnd: always a valid block
-}
-
-template <typename RowT>
-__device__ __forceinline__ void FillTiles(const RowBlockParams& p, TileCache<RowT>& c, int64_t first, int64_t stride,
-                                          int64_t tileEnd, int lane)
-{
-    const int64_t tt = TileIndex<RowT>(lane, first, stride, tileEnd);
-    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
-    c.r0 = p.blocks[tt];
-    c.r1 = p.blocks[tt + 1];
-    c.k0 = bn[tt];
-    c.k1 = bn[tt + 1];
-}
-
-template <typename RowT>
-__device__ __forceinline__ void IssueRefill(const RowBlockParams& p, TileRefill<RowT>& f, int64_t ordinal,
-                                            int64_t first, int64_t stride, int64_t tileEnd)
-{
-    f.ordinal = ordinal;
-    const int64_t tt = TileIndex<RowT>(ordinal, first, stride, tileEnd);
-    const RowT* bn = static_cast<const RowT*>(p.block_nnz);
-    f.r0 = p.blocks[tt];
-    f.r1 = p.blocks[tt + 1];
-    f.k0 = bn[tt];
-    f.k1 = bn[tt + 1];
-}
-
-template <typename RowT>
-__device__ __forceinline__ void MergeRefill(TileCache<RowT>& c, const TileRefill<RowT>& f, int lane)
-{
-    const bool mine = lane == static_cast<int>(f.ordinal & (kWave - 1));
-    c.r0 = mine ? f.r0 : c.r0;
-    c.r1 = mine ? f.r1 : c.r1;
-    c.k0 = mine ? f.k0 : c.k0;
-    c.k1 = mine ? f.k1 : c.k1;
-}
-
-__device__ __forceinline__ int64_t ReadLane64(int64_t v, int l)
-{
-    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
-    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
-    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-template <typename RowT>
-__device__ __forceinline__ Stage OpenTileCached(const TileCache<RowT>& c, int64_t ordinal, int64_t first,
-                                                int64_t stride, int64_t tileEnd, int64_t& lastOpened)
-{
-    Stage s{};
-    s.tile = ordinal;
-    const int64_t t = first + ordinal * stride;
-    s.valid = t < tileEnd;
-    if (!s.valid) return s;
-    lastOpened = ordinal;
-    const int l = static_cast<int>(ordinal & (kWave - 1));
-    s.r0 = __builtin_amdgcn_readlane(c.r0, l);
-    const int64_t n = static_cast<int64_t>(__builtin_amdgcn_readlane(c.r1, l)) - s.r0;
-    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kWaveRows ? kWaveRows : n);
-    int64_t span;
-    if constexpr (sizeof(RowT) == 8) {
-        s.k0 = ReadLane64(c.k0, l);
-        span = ReadLane64(c.k1, l) - s.k0;
-    } else {
-        s.k0 = __builtin_amdgcn_readlane(c.k0, l);
-        span = static_cast<int64_t>(__builtin_amdgcn_readlane(c.k1, l)) - s.k0;
-    }
-    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
-    s.c0 = 0;
-    s.first = true;
-    ChunkBounds(s);
-    return s;
-}
-
-template <typename RowT>
-__device__ __forceinline__ Stage NextStageCached(const TileCache<RowT>& c, const Stage& s, int64_t first,
-                                                 int64_t stride, int64_t tileEnd, int64_t& lastOpened)
-{
-    if (!s.valid) return s;
-    if (!s.last) {
-        Stage n = s;
-        n.c0 = s.c1;
-        n.first = false;
-        ChunkBounds(n);
-        return n;
-    }
-    return OpenTileCached<RowT>(c, s.tile + 1, first, stride, tileEnd, lastOpened);
-}
-
 constexpr int kBufNonTemporal = 2;  // cache policy bit of buffer loads: streaming data
-#if defined(SPMV_EXP_XPOL)
-constexpr int kGatherPolicy = SPMV_EXP_XPOL;
-#else
-constexpr int kGatherPolicy = 0;
-#endif
-#if defined(SPMV_EXP_ROW_NT)
-constexpr int kRowPolicy = kBufNonTemporal;
-#elif defined(SPMV_EXP_ROW_SC)
-constexpr int kRowPolicy = 1;
-#else
-constexpr int kRowPolicy = 0;
-#endif
+constexpr int kGatherPolicy = 0;  // x gathers: default cache policy (the cached lines are reused)
+constexpr int kRowPolicy = 0;  // row offsets / old y: default cache policy
 
 template <ValKind V>
 struct StreamVals;
@@ -1122,11 +999,6 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     int64_t ny = s.valid ? s.nr : 0;
     if (ny > p.rows - r0) ny = p.rows - r0;
     const __amdgpu_buffer_rsrc_t ry = Rsrc(static_cast<const OutT*>(p.y) + r0, ny * sizeof(OutT));
-#if defined(SPMV_EXP_NO_RPY)
-    b.rp[0] = static_cast<RowT>(lane * 5); b.rp[1] = static_cast<RowT>(lane * 5 + 320);
-    b.yold[0] = OutT{}; b.yold[1] = OutT{};
-    if (false)
-#endif
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = lane + h * kWave;
@@ -1187,15 +1059,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
     }
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
-#if defined(SPMV_EXP_LINEAR_X)
-        const uint32_t off = static_cast<uint32_t>((s.a0 + StreamSlot(lane, j)) % p.cols) * static_cast<uint32_t>(sizeof(ValT));
-#elif defined(SPMV_EXP_NO_GATHER)
-        xg[j] = 0x3f800000u + (b.col[j >> 2][j & 3] & 1);
-        continue;
-        const uint32_t off = 0;
-#else
         const uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
-#endif
         if constexpr (sizeof(ValT) == 4) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else {
@@ -1307,12 +1171,6 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
 
     // Phase 1.
     float sum[2] = {0.0f, 0.0f};
-#if defined(SPMV_EXP_NO_REDUCE)
-    if (true) {
-        sum[0] = prod[0] + prod[1] + prod[2] + prod[3] + prod[4] + prod[5] + prod[6] + prod[7];
-        defer[0] = defer[1] = false;
-    } else
-#endif
     if (lg == 0) {
         // One lane per row, at most 8 entries: 8 predicated reads, no branch.
 #pragma unroll
@@ -1388,83 +1246,10 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         if constexpr (kBeta) {
             if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
         }
-#if defined(SPMV_EXP_COND_STORE)
-        if (fin[h]) y[cur.r0 + i] = FromAcc<O, AccKind::F32>(r);
-#else
         OutT* dst = fin[h] ? y + (cur.r0 + i) : sink;
         *dst = FromAcc<O, AccKind::F32>(r);
-#endif
     }
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
-}
-
-template <typename RowT, ValKind V, OutKind O, bool kBeta>
-__global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvStreamKernel(RowBlockParams p)
-{
-    using ValT = typename ValOf<V>::T;
-    using OutT = typename OutOf<O>::T;
-    using L = StreamLoad<RowT, V, O>;
-
-    __shared__ float sValAll[kWavesPerGroup][kStreamLds];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    float* sVal = sValAll[wv];
-
-    const int64_t xcd = blockIdx.x % kXcds;
-    const int64_t worker = (blockIdx.x / kXcds) * kWavesPerGroup + wv;
-    const int64_t tileBegin = xcd * p.per_xcd;
-    int64_t tileEnd = tileBegin + p.per_xcd;
-    if (tileEnd > p.num_blocks) tileEnd = p.num_blocks;
-    const int64_t stride = p.workers_per_xcd;
-    const int64_t firstTile = tileBegin + worker;
-    if (firstTile >= tileEnd) return;
-
-    float alpha, beta;
-    LoadScalars<AccKind::F32>(p.s, alpha, beta);
-    OutT* y = static_cast<OutT*>(p.y);
-    OutT* sink = static_cast<OutT*>(p.sink) + lane;
-    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
-
-    const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
-
-    // Three register bundles rotate through the roles (current: gathered,
-    // next: loaded, after: loading) by unrolling the loop three times, so no
-    // register copy ever waits on a load in flight.
-    TileCache<RowT> tiles;
-    FillTiles<RowT>(p, tiles, firstTile, stride, tileEnd, lane);
-    int64_t lastOpened = 0;
-    L b0, b1, b2;
-    Stage cur = OpenTileCached<RowT>(tiles, 0, firstTile, stride, tileEnd, lastOpened);
-    StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b0);
-    StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b0, b0.xg);
-    // Ordinal 0 has been read: its slot takes ordinal 64 before nxt is opened.
-    TileRefill<RowT> refill;
-    IssueRefill<RowT>(p, refill, 64, firstTile, stride, tileEnd);
-    MergeRefill<RowT>(tiles, refill, lane);
-    Stage nxt = NextStageCached<RowT>(tiles, cur, firstTile, stride, tileEnd, lastOpened);
-    IssueRefill<RowT>(p, refill, lastOpened + kWave, firstTile, stride, tileEnd);
-    StreamLoadStage<RowT, V, O, kBeta>(p, nxt, tailStart, lane, b1);
-    float carry = 0.0f;
-    int lg = 0;  // log2 of the lanes per row in phase 1 (per block)
-
-    auto step = [&](L& lc, L& ln, L& la) __attribute__((always_inline)) {
-        StreamGather<RowT, V, O>(p, nxt, tailStart, rx, lane, ln, ln.xg);
-        MergeRefill<RowT>(tiles, refill, lane);  // loaded one chunk ago
-        const Stage after = NextStageCached<RowT>(tiles, nxt, firstTile, stride, tileEnd, lastOpened);
-        IssueRefill<RowT>(p, refill, lastOpened + kWave, firstTile, stride, tileEnd);
-        StreamLoadStage<RowT, V, O, kBeta>(p, after, tailStart, lane, la);
-
-        StreamChunk<RowT, V, O, kBeta>(cur, lc, sVal, lane, alpha, beta, carry, lg, y, sink);
-
-        // A chunk of a multi-chunk block keeps the block's row offsets / old
-        // y in its own bundle: every chunk loads them.
-        cur = nxt;
-        nxt = after;
-        return cur.valid;
-    };
-    while (step(b0, b1, b2) && step(b1, b2, b0) && step(b2, b0, b1)) {
-    }
 }
 
 // Opens block `tile` with both metadata pairs loaded at once (no dependent
@@ -1633,9 +1418,6 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     if (tile >= p.num_blocks) return;
     Stage cur = OpenTileFlat<RowT>(p, tile);
     if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
-#if defined(SPMV_EXP_SKIP_LONG)
-    if (cur.kspan > SPMV_EXP_SKIP_LONG) return;
-#endif
     while (cur.valid) {
         L b;
         StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
@@ -2034,19 +1816,6 @@ void PersistentShape(RowBlockParams& p, const void* kernel, unsigned& grid)
     grid = static_cast<unsigned>((j / kWavesPerGroup) * kXcds);
 }
 
-// Selects the previous wave kernel instead of the stream kernel
-// (ACLSPARSE_HIP_SPMV_KERNEL=wave), for comparisons.
-bool UseWaveKernel()
-{
-    static const bool wave = [] {
-        const char* e = std::getenv("ACLSPARSE_HIP_SPMV_KERNEL");
-        return e != nullptr && std::string(e) == "wave";
-    }();
-    return wave;
-}
-
-// The one-block-per-wave kernel is the default; ACLSPARSE_HIP_SPMV_KERNEL=
-// stream selects the persistent pipelined variant (for comparisons).
 // Waves serving long-block tasks (ACLSPARSE_HIP_TASK_WAVES overrides, for tuning).
 int64_t TaskWaves()
 {
@@ -2056,15 +1825,6 @@ int64_t TaskWaves()
         return v > 0 ? static_cast<int64_t>(v) : int64_t{2048};
     }();
     return waves;
-}
-
-bool UseFlatKernel()
-{
-    static const bool flat = [] {
-        const char* e = std::getenv("ACLSPARSE_HIP_SPMV_KERNEL");
-        return e == nullptr || std::string(e) != "stream";
-    }();
-    return flat;
 }
 
 template <typename RowT, ValKind V, OutKind O, AccKind A>
@@ -2081,14 +1841,14 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     if constexpr (kCanVec && A == AccKind::F32) {
         // Stream kernel: 32-bit buffer offsets into x, contiguous y.
         const bool stream = vec && static_cast<int64_t>(l.cols) * static_cast<int64_t>(sizeof(typename ValOf<V>::T)) <=
-                                       0x7FFFFFFFLL && !UseWaveKernel();
-        if (stream && UseFlatKernel()) {
+                                       0x7FFFFFFFLL;
+        if (stream) {
             const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
             const int64_t wgs = (p.num_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
             int64_t taskWgs = 0;
             if (l.layout.tasks) {
-                // up to 4096 task waves, a multiple of 8 workgroups (even over the XCDs)
-                int64_t waves = l.layout.max_tasks < TaskWaves() ? l.layout.max_tasks : TaskWaves();
+                // task waves: a multiple of 8 workgroups (even over the XCDs)
+                const int64_t waves = l.layout.max_tasks < TaskWaves() ? l.layout.max_tasks : TaskWaves();
                 taskWgs = (waves + kWavesPerGroup * kXcds - 1) / (kWavesPerGroup * kXcds) * kXcds;
             }
             p.task_wgs = static_cast<int32_t>(taskWgs);
@@ -2100,20 +1860,6 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             } else {
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kWavesPerGroup),
                                    0, stream_, p);
-            }
-            return 0;
-        }
-        if (stream) {
-            const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
-            unsigned pg = 0;
-            if (betaNz) {
-                PersistentShape(p, reinterpret_cast<const void*>(&SpmvStreamKernel<RowT, V, O, true>), pg);
-                hipLaunchKernelGGL((SpmvStreamKernel<RowT, V, O, true>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
-                                   stream_, p);
-            } else {
-                PersistentShape(p, reinterpret_cast<const void*>(&SpmvStreamKernel<RowT, V, O, false>), pg);
-                hipLaunchKernelGGL((SpmvStreamKernel<RowT, V, O, false>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
-                                   stream_, p);
             }
             return 0;
         }
