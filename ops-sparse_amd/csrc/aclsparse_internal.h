@@ -206,7 +206,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.items_per_block = ItemsPerBlock(rows, nnz);
     l.num_blocks = NumBlocks(rows, nnz);
     l.rowptr_offset = kWsHeaderBytes;
-    l.blocks_offset = AlignUp(l.rowptr_offset + static_cast<size_t>(rows + 1) * l.rowptr_bytes);
+    // rows + 2 entries: one pad entry, so that row offsets can be read in pairs
+    l.blocks_offset = AlignUp(l.rowptr_offset + static_cast<size_t>(rows + 2) * l.rowptr_bytes);
     l.block_nnz_offset = AlignUp(l.blocks_offset + static_cast<size_t>(l.num_blocks + 1) * sizeof(int32_t));
     l.sink_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
     l.acc_offset = l.sink_offset + kSinkBytes;

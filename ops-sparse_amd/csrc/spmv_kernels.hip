@@ -991,23 +991,31 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
         const v2i hi = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rv, 512 + lane * 8, 0, kBufNonTemporal));
         b.val.v = v4i{lo.x, lo.y, hi.x, hi.y};
     }
-    // Row offsets r0 .. r0+nr and old y of rows r0 .. r0+nr-1 (entries past
-    // the block read as 0 and are never used).
+    // Rows 2l and 2l+1 of the block belong to lane l: their row offsets come
+    // in one 8-byte (int32) or 16-byte (int64) load.  The resource covers
+    // nr+1 offsets rounded up to an even count (the workspace array has a pad
+    // entry), so a pair is either wholly inside or wholly past it (past: 0,
+    // never used).  Old y values are loaded one per row.
     const int64_t r0 = s.valid ? s.r0 : 0;
-    const int64_t nrp = s.valid ? s.nr + 1 : 0;
+    const int64_t nrp = s.valid ? ((s.nr + 2) & ~1) : 0;
     const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
+    if constexpr (sizeof(RowT) == 8) {
+        const v4i w = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, kRowPolicy));
+        b.rp[0] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.y)) << 32) |
+                                    static_cast<uint32_t>(w.x));
+        b.rp[1] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.w)) << 32) |
+                                    static_cast<uint32_t>(w.z));
+    } else {
+        const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rr, lane * 8, 0, kRowPolicy));
+        b.rp[0] = static_cast<RowT>(w.x);
+        b.rp[1] = static_cast<RowT>(w.y);
+    }
     int64_t ny = s.valid ? s.nr : 0;
     if (ny > p.rows - r0) ny = p.rows - r0;
     const __amdgpu_buffer_rsrc_t ry = Rsrc(static_cast<const OutT*>(p.y) + r0, ny * sizeof(OutT));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int i = lane + h * kWave;
-        if constexpr (sizeof(RowT) == 8) {
-            b.rp[h] = static_cast<RowT>(__builtin_bit_cast(
-                long long, __builtin_amdgcn_raw_buffer_load_b64(rr, i * 8, 0, kRowPolicy)));
-        } else {
-            b.rp[h] = static_cast<RowT>(__builtin_amdgcn_raw_buffer_load_b32(rr, i * 4, 0, kRowPolicy));
-        }
+        const int i = 2 * lane + h;
         if constexpr (kBeta) {
             if constexpr (sizeof(OutT) == 4) {
                 b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b32(ry, i * 4, 0, kRowPolicy));
@@ -1145,20 +1153,22 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     *reinterpret_cast<v4f*>(&sVal[4 * lane]) = v4f{prod[0], prod[1], prod[2], prod[3]};
     *reinterpret_cast<v4f*>(&sVal[256 + 4 * lane]) = v4f{prod[4], prod[5], prod[6], prod[7]};
 
-    // Row offsets relative to the block's first non-zero.
+    // Row offsets relative to the block's first non-zero.  Lane l holds rows
+    // 2l and 2l+1: row 2l ends where row 2l+1 starts, row 2l+1 where lane
+    // l+1's first row starts (row 127 never exists: blocks have <= 127 rows).
     const int32_t k0lo = static_cast<int32_t>(cur.k0);
     int32_t rs[2], re[2];
     rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
     rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
-    re[0] = FromNextLane(rs[0], __builtin_amdgcn_readlane(rs[1], 0));
-    re[1] = FromNextLane(rs[1], rs[1]);
+    re[0] = rs[1];
+    re[1] = FromNextLane(rs[0], rs[1]);
 
     const int gsz = 1 << lg;
     const int cap = SerialCap(lg);
     bool fin[2], defer[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int i = lane + h * kWave;
+        const int i = 2 * lane + h;
         const bool in = i < nr;
         const bool empty = re[h] <= rs[h];
         const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
@@ -1175,7 +1185,6 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         // One lane per row, at most 8 entries: 8 predicated reads, no branch.
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if (h == 1 && nr <= kWave) break;
             const int32_t len = fin[h] ? re[h] - rs[h] : 0;
             const int32_t base = fin[h] ? rs[h] - shift : 0;
             float acc = 0.0f;
@@ -1187,11 +1196,16 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
             sum[h] = acc;
         }
     } else {
+        // Group g = lane >> lg reduces row g (nr <= 32 here); lane g/2 holds
+        // its offsets in half g&1.
         const int g = lane >> lg;
         const int sub = lane & (gsz - 1);
         const bool in = g < nr;
-        const int32_t gs = __shfl(rs[0], g, kWave);
-        const int32_t ge = __shfl(re[0], g, kWave);
+        const int src = (g >> 1) & (kWave - 1);
+        const int32_t a0s = __shfl(rs[0], src, kWave), a1s = __shfl(rs[1], src, kWave);
+        const int32_t a1e = __shfl(re[1], src, kWave);
+        const int32_t gs = (g & 1) ? a1s : a0s;
+        const int32_t ge = (g & 1) ? a1e : a1s;
         float part = 0.0f;
         if (in && ge - gs <= cap) {
             for (int32_t q = gs + sub; q < ge; q += gsz) part += sVal[q - shift];
@@ -1201,52 +1215,67 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         } else {
             part = WaveSum(part);
         }
-        sum[0] = __shfl(part, (lane << lg) & (kWave - 1), kWave);  // lane i owns row i (nr <= 32 here)
+        // the group of row 2l+h starts at lane (2l+h) << lg
+        sum[0] = __shfl(part, ((2 * lane) << lg) & (kWave - 1), kWave);
+        sum[1] = __shfl(part, ((2 * lane + 1) << lg) & (kWave - 1), kWave);
     }
 
-    // Phase 2: deferred rows, whole wave per row, in row order.
-    uint64_t pending[2] = {__ballot(defer[0]), __ballot(defer[1])};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        while (pending[h]) {
-            const int l = __builtin_ctzll(pending[h]);
-            pending[h] &= pending[h] - 1;
-            const int32_t s0 = __builtin_amdgcn_readlane(rs[h], l), e0 = __builtin_amdgcn_readlane(re[h], l);
-            const int32_t lo = s0 > c0 ? s0 : c0;
-            const int32_t hi = e0 < c1 ? e0 : c1;
-            float part = 0.0f;
-            for (int32_t q = lo + lane; q < hi; q += kWave) part += sVal[q - shift];
-            float total = WaveSum(part);
-            if constexpr (kTask) {
-                if (s0 < c0) {
-                    *head = total;
-                } else if (e0 > c1) {
-                    *tail = total;
-                } else if (lane == l) {
-                    sum[h] = total;
-                    fin[h] = true;
-                }
+    // Phase 2: deferred rows, whole wave per row, in row order (rows 2l+h).
+    uint64_t pending0 = __ballot(defer[0]), pending1 = __ballot(defer[1]);
+    while (pending0 | pending1) {
+        const int l0 = pending0 ? __builtin_ctzll(pending0) : kWave;
+        const int l1 = pending1 ? __builtin_ctzll(pending1) : kWave;
+        const int h = (2 * l1 + 1 < 2 * l0) ? 1 : 0;
+        const int l = h ? l1 : l0;
+        if (h) {
+            pending1 &= pending1 - 1;
+        } else {
+            pending0 &= pending0 - 1;
+        }
+        const int32_t s0 = __builtin_amdgcn_readlane(h ? rs[1] : rs[0], l);
+        const int32_t e0 = __builtin_amdgcn_readlane(h ? re[1] : re[0], l);
+        const int32_t lo = s0 > c0 ? s0 : c0;
+        const int32_t hi = e0 < c1 ? e0 : c1;
+        float part = 0.0f;
+        for (int32_t q = lo + lane; q < hi; q += kWave) part += sVal[q - shift];
+        float total = WaveSum(part);
+        bool finish = false;
+        if constexpr (kTask) {
+            if (s0 < c0) {
+                *head = total;
+            } else if (e0 > c1) {
+                *tail = total;
             } else {
-                if (s0 < c0) total += carry;
-                if (e0 > c1) {
-                    carry = total;
-                } else if (lane == l) {
-                    sum[h] = total;
-                    fin[h] = true;
-                }
+                finish = true;
+            }
+        } else {
+            if (s0 < c0) total += carry;
+            if (e0 > c1) {
+                carry = total;
+            } else {
+                finish = true;
+            }
+        }
+        if (finish && lane == l) {
+            if (h) {
+                sum[1] = total;
+                fin[1] = true;
+            } else {
+                sum[0] = total;
+                fin[0] = true;
             }
         }
     }
 
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int i = lane + h * kWave;
+        const int i = 2 * lane + h;
         float r = alpha * sum[h];
         // beta == 0 (possible at run time with device scalars) never reads y
         if constexpr (kBeta) {
             if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
         }
-        OutT* dst = fin[h] ? y + (cur.r0 + i) : sink;
+        OutT* dst = fin[h] ? y + (cur.r0 + i) : sink + h * kWave;
         *dst = FromAcc<O, AccKind::F32>(r);
     }
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
