@@ -57,8 +57,9 @@ def profile_mode(name, steps):
     plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
     plan.preprocess()
     flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    sink = torch.empty((), dtype=torch.float32, device=dev)
     for _ in range(steps):
-        flush_buf.add_(1)  # same L2/MALL state as a bench step
+        torch.sum(flush_buf, dim=0, out=sink)  # same L2/MALL state as a bench step
         plan.run()
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -92,14 +93,16 @@ def _timed(stream, fn, reps):
 def measure(w, steps, warmup, flush_buf):
     """SpMV time per step (ms) with L2/MALL flushed before every SpMV.
 
-    A step is one 512 MiB flush write followed by one SpMV, so the SpMV starts
-    with its inputs in HBM only.  ``median_ms`` is the median over ``steps``
-    of an event pair around each SpMV launch on the launch stream: it agrees
-    with the kernel duration rocprofv3 reports for the same launches (it
-    includes the dispatch latency of one launch, a few microseconds).
-    ``paired_ms`` (events around back-to-back flush+SpMV steps minus flushes
-    alone) and ``warm_ms`` (back-to-back SpMVs, L2/MALL warm) are for
-    reference only.
+    A step is a read of a 512 MiB buffer (evicting the L2 and the 256 MB
+    MALL) followed by one SpMV, so the SpMV starts with its inputs in HBM
+    only.  ``median_ms`` is the median over ``steps`` of an event pair around
+    each SpMV launch on the launch stream: it agrees with the kernel
+    duration rocprofv3 reports for the same launches (it includes the
+    dispatch latency of one launch, a few microseconds).  For reference only:
+    ``dirty_flush_ms`` (the same after a read-modify-write flush, whose dirty
+    lines the SpMV then has to write back), ``paired_ms`` (back-to-back
+    flush+SpMV steps minus flushes alone) and ``warm_ms`` (back-to-back
+    SpMVs, L2/MALL warm).
     """
     from ops_sparse.spmv import CsrSpMV
     from ops_sparse._lib import Operation
@@ -115,11 +118,15 @@ def measure(w, steps, warmup, flush_buf):
     torch.cuda.synchronize()
     pre_ms = p0.elapsed_time(p1)
 
+    sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
+
     def flush():
-        flush_buf.add_(1)
+        # read-only: evicts L2/MALL without leaving dirty lines whose
+        # write-back the next kernel would pay for
+        torch.sum(flush_buf, dim=0, out=sink)
 
     def step():
-        flush_buf.add_(1)
+        flush()
         plan.run()
 
     for _ in range(warmup):
@@ -134,17 +141,23 @@ def measure(w, steps, warmup, flush_buf):
         diffs.append(both - alone)
     wall = (time.perf_counter() - t0) * 1e3 / (rounds * per_round)
     # one event pair per launch (includes the launch latency)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for a, b in evs:
-        flush_buf.add_(1)
-        a.record(stream)
-        plan.run()
-        b.record(stream)
-    torch.cuda.synchronize()
-    ev = statistics.median(a.elapsed_time(b) for a, b in evs)
+    def per_launch(pre):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for a, b in evs:
+            pre()
+            a.record(stream)
+            plan.run()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+    ev = per_launch(flush)
+    # reference: after a 512 MiB read-modify-write flush, the SpMV also pays
+    # for writing back the flush's dirty L2/MALL lines
+    ev_dirty = per_launch(lambda: flush_buf.add_(1))
     # back-to-back launches without a flush (L2/MALL warm), for reference only
     warm = _timed(stream, plan.run, steps)
-    return dict(median_ms=ev, paired_ms=statistics.median(diffs), paired_min_ms=min(diffs),
+    return dict(median_ms=ev, dirty_flush_ms=ev_dirty, paired_ms=statistics.median(diffs), paired_min_ms=min(diffs),
                 paired_max_ms=max(diffs), wall_ms_per_step=wall, warm_ms=warm, preprocess_ms=pre_ms,
                 workspace_bytes=plan.buffer_size)
 
