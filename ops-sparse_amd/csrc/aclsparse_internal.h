@@ -130,7 +130,11 @@ struct SpmvWsHeader {
     uint32_t rowptr_bytes;
     uint32_t index_base;
     uint32_t op;
-    uint32_t reserved[23];
+    uint32_t long_chunks;        // blocks of more chunks than this run as tasks
+    uint64_t task_start_offset;  // 0 when the plan has no task table
+    uint64_t task_block_offset;
+    uint64_t max_tasks;
+    uint32_t reserved[16];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 

@@ -2143,6 +2143,10 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     h.rowptr_bytes = l.layout.rowptr_bytes;
     h.index_base = static_cast<uint32_t>(l.base);
     h.op = static_cast<uint32_t>(l.op);
+    h.long_chunks = static_cast<uint32_t>(kLongChunks);
+    h.task_start_offset = l.layout.tasks ? l.layout.task_start_offset : 0;
+    h.task_block_offset = l.layout.tasks ? l.layout.task_block_offset : 0;
+    h.max_tasks = l.layout.tasks ? static_cast<uint64_t>(l.layout.max_tasks) : 0;
     const int64_t n = (l.rows > p.num_blocks ? l.rows : p.num_blocks) + 1;
     const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
     hipStream_t s = static_cast<hipStream_t>(stream);

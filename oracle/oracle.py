@@ -194,6 +194,25 @@ def partition(row_ptr, nnz, rows=None, stride=1, base=0):
     return norm, blocks, bnnz
 
 
+def task_table(block_nnz, long_chunks, chunk=512):
+    """(task_start[B+1], task_block[total]) of the long-block task table.
+
+    This build's own design (no reference counterpart): block b, whose
+    non-zeros are [block_nnz[b], block_nnz[b+1]), is read in chunks of
+    ``chunk`` slots starting at its first non-zero rounded down to a multiple
+    of 4; a block of more than ``long_chunks`` chunks becomes one task per
+    chunk.  task_start is the exclusive scan of the per-block task counts and
+    task_block names the block of every task.
+    """
+    bn = _i64(block_nnz)
+    k0, k1 = bn[:-1], bn[1:]
+    chunks = (k1 - k0 + (k0 & 3) + chunk - 1) // chunk
+    counts = np.where(chunks > long_chunks, chunks, 0)
+    start = np.zeros(bn.size, dtype=np.int64)
+    np.cumsum(counts, out=start[1:])
+    return start.astype(np.int32), np.repeat(np.arange(k0.size, dtype=np.int32), counts)
+
+
 def verify_mixed(golden, actual, rtol, atol, max_abs, ratio, exact=False):
     """Reference Verification(): returns (passed, matched_ratio, max_abs_error)."""
     g = np.ascontiguousarray(golden, dtype=np.float64)

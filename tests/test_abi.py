@@ -329,3 +329,12 @@ def test_spmvop_validation(env, lib):
     assert ex(env.h, plan, ctypes.byref(a), ctypes.byref(b), x, y, env.vec(3, env.yt)) == Status.INVALID_VALUE
     assert lib.aclsparseSpMVOp_destroyPlan(plan) == Status.SUCCESS
     assert lib.aclsparseSpMVOp_destroyDescr(d) == Status.SUCCESS
+
+
+def test_package_import_registers_aten_mv_for_csr_on_rocm():
+    # the reference's package implements aten::mv for its device's CSR key on import
+    import torch
+    import ops_sparse  # noqa: F401
+    dump = torch._C._dispatch_dump("aten::mv")
+    line = next(l for l in dump.splitlines() if l.startswith("SparseCsrCUDA:"))
+    assert "ops_sparse" in line and "aten.py" in line

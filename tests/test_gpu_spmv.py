@@ -252,6 +252,19 @@ def test_partition_metadata_bit_exact(name, scale, i64, dev):
     np.testing.assert_array_equal(blocks, blocks_ref)
     np.testing.assert_array_equal(bnnz, bnnz_ref)
     assert np.all(np.diff(blocks) <= 511)
+    ts_off, tb_off, max_tasks, long_chunks = int(hdr[13]), int(hdr[14]), int(hdr[15]), int(hdr[12] >> 32)
+    if w.trans == "N" and w.values.dtype == torch.float32:
+        # the long-block task table (fp32 non-transpose plans)
+        start_ref, tblock_ref = oracle.task_table(bnnz_ref, long_chunks)
+        assert ts_off and tb_off and long_chunks >= 1 and tblock_ref.size <= max_tasks
+        start = np.frombuffer(ws[ts_off:ts_off + 4 * (nb + 1)].tobytes(), dtype=np.int32)
+        tblock = np.frombuffer(ws[tb_off:tb_off + 4 * tblock_ref.size].tobytes(), dtype=np.int32)
+        np.testing.assert_array_equal(start, start_ref)
+        np.testing.assert_array_equal(tblock, tblock_ref)
+        if name == "c3":
+            assert tblock_ref.size > 0  # power-law rows do produce long blocks
+    else:
+        assert ts_off == 0 and tb_off == 0
 
 
 def test_beta_zero_never_reads_y(dev):
@@ -303,6 +316,35 @@ def test_spmv_npu_mirror_and_mv(dev):
     y2 = mv(a, d.x)
     torch.cuda.synchronize()
     assert torch.equal(y2, y)
+
+
+def test_torch_mv_dispatches_here(dev):
+    # torch.mv(csr, vec) on the GPU runs ops_sparse.mv (aten::mv, SparseCsrCUDA),
+    # as the reference's package routes it for the NPU (torch_extension/spmv.py:43-46)
+    import ops_sparse  # noqa: F401  (the import registers the kernel)
+    w = wl.config("c1", "cpu")
+    d = w.to(dev)
+    a = torch.sparse_csr_tensor(d.row_ptr.to(torch.int64), d.col_ind.to(torch.int64), d.values,
+                                size=(w.rows, w.cols))
+    y = torch.mv(a, d.x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ops_sparse.mv(a, d.x))
+    w0 = wl.Workload(w.name, w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, w.y0, 1.0, 0.0)
+    assert_close(w0, y)
+    # int8 values: SpMvCsr accumulates and returns int32, which PyTorch's own kernel does not offer
+    g = torch.Generator().manual_seed(5)
+    v8 = torch.randint(-128, 128, (w.col_ind.numel(),), generator=g, dtype=torch.int8)
+    x8 = torch.randint(-128, 128, (w.cols,), generator=g, dtype=torch.int8)
+    a8 = torch.sparse_csr_tensor(d.row_ptr.to(torch.int64), d.col_ind.to(torch.int64), v8.to(dev),
+                                 size=(w.rows, w.cols))
+    y8 = torch.mv(a8, x8.to(dev))
+    torch.cuda.synchronize()
+    assert y8.dtype == torch.int32
+    ref = torch.zeros(w.rows, dtype=torch.int64)
+    rp = w.row_ptr.to(torch.int64)
+    prod = v8.to(torch.int64) * x8.to(torch.int64)[w.col_ind.to(torch.int64)]
+    ref.index_add_(0, torch.repeat_interleave(torch.arange(w.rows), rp[1:] - rp[:-1]), prod)
+    assert torch.equal(y8.cpu(), ref.to(torch.int32))
 
 
 @pytest.mark.parametrize("nnz", [1, 2, 3, 5, 7])

@@ -279,6 +279,38 @@ def test_partition_brute_force(seed):
     assert np.all(np.diff(blocks[:-1]) <= t // 16 + 1)
 
 
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("long_chunks", [1, 4])
+def test_task_table_covers_long_blocks_exactly(seed, long_chunks):
+    # brute force on the slots: walking each block's 512-slot chunks from its 16-byte-aligned
+    # first non-zero must cover [k0, k1) exactly; blocks of more than long_chunks chunks get one
+    # task per chunk, in block order, and no other block gets any
+    rng = np.random.default_rng(100 + seed)
+    rows = int(rng.integers(1, 2000))
+    lengths = rng.choice([0, 2, 9, 300, 4000, 40000], size=rows, p=[0.2, 0.3, 0.3, 0.15, 0.04, 0.01])
+    rp = np.zeros(rows + 1, np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    nnz = int(rp[-1])
+    _, _, bnnz = oracle.partition(rp, nnz)
+    start, tblock = oracle.task_table(bnnz, long_chunks)
+    nb = bnnz.size - 1
+    assert start[0] == 0 and start[nb] == tblock.size
+    covered = np.zeros(nnz, np.int32)
+    for b in range(nb):
+        k0, k1 = int(bnnz[b]), int(bnnz[b + 1])
+        s0 = k0 - k0 % 4
+        chunks = []
+        while s0 + 512 * len(chunks) < k1:
+            lo = max(k0, s0 + 512 * len(chunks))
+            hi = min(k1, s0 + 512 * (len(chunks) + 1))
+            covered[lo:hi] += 1
+            chunks.append((lo, hi))
+        n = int(start[b + 1] - start[b])
+        assert n == (len(chunks) if len(chunks) > long_chunks else 0)
+        assert np.all(tblock[start[b]:start[b + 1]] == b)
+    assert np.all(covered == 1)
+
+
 def test_partition_clamps_out_of_range_offsets():
     rp = np.array([5, 3, 100, 7], np.int64)  # base 1: logical [4, 2, 99, 6], nnz 6
     norm, _, _ = oracle.partition(rp, 6, base=1)
