@@ -166,13 +166,17 @@ struct SpmvLayout {
     int64_t num_blocks = 0;
     uint32_t rowptr_bytes = 4;
     // Transpose by columns (CSC pattern built by Preprocess): column offsets
-    // colptr[cols+1] (RowT), the row of every entry csc_row[nnz] (int32) and
-    // its position in the CSR arrays csc_pos[nnz] (RowT), plus the sort's
-    // temporary arrays (key_a/key_b int32[nnz], val_b RowT[nnz], radix-sort
-    // storage).  Without it (nnz beyond the sort's int range) the transpose
-    // scatters with atomics into the accumulator at acc_offset.
+    // colptr[cols+1] (RowT), the row of every entry in CSR order
+    // entry_row[nnz] (int32) and, in column order, each entry's position in
+    // the CSR arrays csc_pos[nnz] (RowT), plus the sort's temporary arrays
+    // (key_a/key_b int32[nnz], val_b RowT[nnz], radix-sort storage).  At
+    // execution time the products a_k * x_row(k) go to prod[nnz] (the
+    // accumulator type, at most 8 bytes: it reuses key_a/key_b, which only
+    // Preprocess needs).  Without a CSC pattern (nnz beyond the sort's int
+    // range) the transpose scatters with atomics into the accumulator at
+    // acc_offset.
     bool csc = false;
-    size_t colptr_offset = 0, csc_row_offset = 0, csc_pos_offset = 0;
+    size_t colptr_offset = 0, entry_row_offset = 0, csc_pos_offset = 0, prod_offset = 0;
     size_t key_a_offset = 0, key_b_offset = 0, val_b_offset = 0, sort_offset = 0, sort_bytes = 0;
     // Long-block tasks (non-transpose, fp32 compute): a block of more than
     // kLongChunks chunks is split into one task per chunk.  task_start[B+1]
@@ -241,11 +245,12 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             const size_t n = static_cast<size_t>(nnz);
             const size_t rb = l.rowptr_bytes;
             l.colptr_offset = AlignUp(l.acc_offset);
-            l.csc_row_offset = AlignUp(l.colptr_offset + static_cast<size_t>(cols + 1) * rb);
-            l.csc_pos_offset = AlignUp(l.csc_row_offset + n * sizeof(int32_t));
+            l.entry_row_offset = AlignUp(l.colptr_offset + static_cast<size_t>(cols + 1) * rb);
+            l.csc_pos_offset = AlignUp(l.entry_row_offset + n * sizeof(int32_t));
             l.key_a_offset = AlignUp(l.csc_pos_offset + n * rb);
             l.key_b_offset = AlignUp(l.key_a_offset + n * sizeof(int32_t));
             l.val_b_offset = AlignUp(l.key_b_offset + n * sizeof(int32_t));
+            l.prod_offset = l.key_a_offset;  // prod[nnz] of <= 8 bytes ends before val_b
             l.sort_offset = AlignUp(l.val_b_offset + n * rb);
             l.sort_bytes = CscSortTempBytes(static_cast<int64_t>(nnz), l.rowptr_bytes);
             l.total = AlignUp(l.sort_offset + l.sort_bytes + 256);  // re-aligned to 256 bytes at use

@@ -1611,24 +1611,29 @@ __global__ __launch_bounds__(kThreads) void CscColPtrKernel(const int32_t* keys,
     }
 }
 
-// Row of every sorted entry (last row whose normalised offset is <= the
-// entry's position); the positions move to their final array if the sort
-// left them in the other buffer.
+// Row of every entry in CSR order (the last row whose normalised offset is
+// <= k; entries outside [norm[0], norm[rows]) get row 0 and are never used);
+// the sorted positions move to their final array if the sort left them in
+// the other buffer.
 template <typename RowT>
-__global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPos, RowT* pos, int32_t* row,
+__global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPos, RowT* pos, int32_t* entryRow,
                                                             const RowT* norm, int64_t rows, int64_t n)
 {
+    const int64_t first = static_cast<int64_t>(norm[0]);
+    const int64_t last = static_cast<int64_t>(norm[rows]);
     for (int64_t k = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; k < n;
          k += static_cast<int64_t>(gridDim.x) * kThreads) {
-        const RowT p = sortedPos[k];
-        if (sortedPos != pos) pos[k] = p;
-        int64_t lo = 0, hi = rows - 1;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi + 1) >> 1;
-            if (norm[mid] <= p) lo = mid;
-            else hi = mid - 1;
+        if (sortedPos != pos) pos[k] = sortedPos[k];
+        int64_t lo = 0;
+        if (k >= first && k < last) {
+            int64_t hi = rows - 1;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi + 1) >> 1;
+                if (static_cast<int64_t>(norm[mid]) <= k) lo = mid;
+                else hi = mid - 1;
+            }
         }
-        row[k] = static_cast<int32_t>(lo);
+        entryRow[k] = static_cast<int32_t>(lo);
     }
 }
 
@@ -1641,27 +1646,67 @@ __device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
 
 struct CscParams {
     const void* colptr;  // RowT[cols+1]
-    const int32_t* row;
+    const int32_t* entry_row;
     const void* pos;     // RowT[nnz]
+    void* prod;          // Acc[nnz]
     const void* val;
     int64_t val_stride;
     const void* x;
     int64_t x_stride;
     void* y;
     int64_t y_stride;
+    const void* norm;     // RowT[rows+1]: entries [norm[0], norm[rows]) belong to rows
+    int64_t rows;
     int64_t cols;
     int32_t lg;  // log2 lanes per column
     int32_t conj;
     Scalars s;
 };
 
-// 2^lg lanes per column, each over a strided subset of the column's entries,
-// merged by a fixed butterfly; the first lane applies the epilogue.
+// Pass 1, in CSR order: prod[k] = conj?(a_k) * x[row(k)].  A pure stream:
+// values, entry rows and products are read/written once, contiguously, and
+// x is read in row order.
+template <typename RowT, ValKind V, AccKind A>
+__global__ __launch_bounds__(kThreads) void CscProductKernel(CscParams q)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    const ValT* val = static_cast<const ValT*>(q.val);
+    const ValT* x = static_cast<const ValT*>(q.x);
+    Acc* prod = static_cast<Acc*>(q.prod);
+    const RowT* norm = static_cast<const RowT*>(q.norm);
+    const int64_t first = static_cast<int64_t>(norm[0]);
+    const int64_t last = static_cast<int64_t>(norm[q.rows]);
+    // 4 entries per thread and step (kThreads apart, so every load stays
+    // coalesced) to keep more row-index -> x dependencies in flight
+    constexpr int kU = 4;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kThreads * kU;
+    for (int64_t k0 = first + blockIdx.x * static_cast<int64_t>(kThreads) * kU + threadIdx.x; k0 < last;
+         k0 += step) {
+        int32_t r[kU];
+        ValT v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t k = k0 + u * kThreads;
+            r[u] = k < last ? q.entry_row[k] : 0;
+            v[u] = k < last ? val[k * q.val_stride] : ValT{};
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t k = k0 + u * kThreads;
+            const Acc xr = ToAcc<V, A>(x[static_cast<int64_t>(r[u]) * q.x_stride]);
+            if (k < last) prod[k] = MaybeConj<V, A>(ToAcc<V, A>(v[u]), q.conj) * xr;
+        }
+    }
+}
+
+// Pass 2, by columns: 2^lg lanes per column, each summing the products of a
+// strided subset of the column's entries (one random read per entry), merged
+// by a fixed butterfly; the first lane applies the epilogue.
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 __global__ __launch_bounds__(kThreads) void SpmvCscGatherKernel(CscParams q)
 {
     using Acc = typename AccOf<A>::T;
-    using ValT = typename ValOf<V>::T;
     const int lg = q.lg;
     const int g = 1 << lg;
     const int64_t c = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> lg;
@@ -1670,15 +1715,12 @@ __global__ __launch_bounds__(kThreads) void SpmvCscGatherKernel(CscParams q)
     LoadScalars<A>(q.s, alpha, beta);
     const RowT* colptr = static_cast<const RowT*>(q.colptr);
     const RowT* pos = static_cast<const RowT*>(q.pos);
-    const ValT* val = static_cast<const ValT*>(q.val);
-    const ValT* x = static_cast<const ValT*>(q.x);
+    const Acc* prod = static_cast<const Acc*>(q.prod);
     Acc sum = Zero<Acc>();
     if (c < q.cols) {
         const int64_t k1 = static_cast<int64_t>(colptr[c + 1]);
         for (int64_t k = static_cast<int64_t>(colptr[c]) + sub; k < k1; k += g) {
-            const int64_t pk = static_cast<int64_t>(pos[k]);
-            const Acc a = MaybeConj<V, A>(ToAcc<V, A>(val[pk * q.val_stride]), q.conj);
-            sum = sum + a * ToAcc<V, A>(x[static_cast<int64_t>(q.row[k]) * q.x_stride]);
+            sum = sum + prod[static_cast<int64_t>(pos[k])];
         }
     }
     for (int m = 1; m < g; m <<= 1) sum = sum + ShflXorAcc(sum, m);
@@ -1924,8 +1966,11 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         if (n <= 0) return 0;
         CscParams q{};
         q.colptr = At<void>(l.ws, l.layout.colptr_offset);
-        q.row = At<int32_t>(l.ws, l.layout.csc_row_offset);
+        q.entry_row = At<int32_t>(l.ws, l.layout.entry_row_offset);
         q.pos = At<void>(l.ws, l.layout.csc_pos_offset);
+        q.prod = At<void>(l.ws, l.layout.prod_offset);
+        q.norm = At<const void>(l.ws, l.layout.rowptr_offset);
+        q.rows = l.rows;
         q.val = l.val;
         q.val_stride = l.val_stride;
         q.x = l.x;
@@ -1942,6 +1987,7 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         q.lg = lg;
         const int64_t threads = n << lg;
         const unsigned grid = static_cast<unsigned>((threads + kThreads - 1) / kThreads);
+        hipLaunchKernelGGL((CscProductKernel<RowT, V, A>), dim3(GridFor((l.nnz + 3) / 4)), dim3(kThreads), 0, stream, q);
         hipLaunchKernelGGL((SpmvCscGatherKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, q);
         return 0;
     }
@@ -2078,7 +2124,7 @@ int BuildCsc(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL((CscColPtrKernel<RowT>), dim3(GridFor(nnz + 1)), dim3(kThreads), 0, s, keys.Current(), nnz,
                        l.cols, At<RowT>(l.ws, l.layout.colptr_offset));
     hipLaunchKernelGGL((CscFinishKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, vals.Current(),
-                       At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.csc_row_offset),
+                       At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.entry_row_offset),
                        At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, nnz);
     return 0;
 }
