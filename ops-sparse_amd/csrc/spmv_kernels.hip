@@ -51,6 +51,7 @@ static_assert(kChunk % (4 * kThreads) == 0, "chunk must be a multiple of one 16-
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned short v4u16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int Pad(int q) { return q + (q >> 3); }
@@ -702,6 +703,13 @@ __device__ __forceinline__ void Products(const Bundle<RowT, V, O>& b, const type
 
 // Orders this wave's LDS accesses (LDS ops of one wave complete in order;
 // the clobber keeps the compiler from moving accesses across the wait).
+// LDS byte address of a pointer into __shared__ memory (for inline asm).
+__device__ __forceinline__ uint32_t LdsAddr(const float* p)
+{
+    typedef const __attribute__((address_space(3))) float* LdsPtr;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsPtr)(p)));
+}
+
 __device__ __forceinline__ void WaveLdsSync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ float ReadLane(float v, int l) { return __shfl(v, l, kWave); }
@@ -1182,17 +1190,30 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     // Phase 1.
     float sum[2] = {0.0f, 0.0f};
     if (lg == 0) {
-        // One lane per row, at most 8 entries: 8 predicated reads, no branch.
+        // One lane per row, at most 8 entries: 8 predicated reads per row,
+        // no branch.  All 16 reads are issued before one wait (the
+        // compiler's own schedule waits after each read pair).
+        v2f e[2][4];
+        int32_t len[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
-            const int32_t base = fin[h] ? rs[h] - shift : 0;
+            len[h] = fin[h] ? re[h] - rs[h] : 0;
+            const uint32_t addr = LdsAddr(sVal + (fin[h] ? rs[h] - shift : 0));
+            asm volatile("ds_read2_b32 %0, %4 offset1:1\n\t"
+                         "ds_read2_b32 %1, %4 offset0:2 offset1:3\n\t"
+                         "ds_read2_b32 %2, %4 offset0:4 offset1:5\n\t"
+                         "ds_read2_b32 %3, %4 offset0:6 offset1:7"
+                         : "=&v"(e[h][0]), "=&v"(e[h][1]), "=&v"(e[h][2]), "=&v"(e[h][3])
+                         : "v"(addr));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(e[0][0]), "+v"(e[0][1]), "+v"(e[0][2]), "+v"(e[0][3]), "+v"(e[1][0]), "+v"(e[1][1]),
+                       "+v"(e[1][2]), "+v"(e[1][3]));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
             float acc = 0.0f;
 #pragma unroll
-            for (int t = 0; t < kSerialCapOne; ++t) {
-                const float v = sVal[base + t];
-                acc += t < len ? v : 0.0f;
-            }
+            for (int t = 0; t < kSerialCapOne; ++t) acc += t < len[h] ? e[h][t >> 1][t & 1] : 0.0f;
             sum[h] = acc;
         }
     } else {
@@ -1206,10 +1227,43 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         const int32_t a1e = __shfl(re[1], src, kWave);
         const int32_t gs = (g & 1) ? a1s : a0s;
         const int32_t ge = (g & 1) ? a1e : a1s;
+        // cap = 16 * gsz, so a lane reads at most 16 entries: 16 predicated
+        // reads issued back to back (two asm groups walking one address
+        // register), one wait.
+        const bool ok = in && ge - gs <= cap;
+        const int32_t n = ok ? ge - gs - sub : 0;  // this lane's entries: t * gsz < n
+        uint32_t addr = LdsAddr(sVal + (ok ? gs + sub - shift : 0));
+        const uint32_t step = static_cast<uint32_t>(gsz) * 4U;
+        float e[16];
+        asm volatile("ds_read_b32 %0, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %1, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %2, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %3, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %4, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %5, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %6, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %7, %8\n\tv_add_u32 %8, %8, %9"
+                     : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3]), "=&v"(e[4]), "=&v"(e[5]), "=&v"(e[6]),
+                       "=&v"(e[7]), "+&v"(addr)
+                     : "v"(step));
+        asm volatile("ds_read_b32 %0, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %1, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %2, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %3, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %4, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %5, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %6, %8\n\tv_add_u32 %8, %8, %9\n\t"
+                     "ds_read_b32 %7, %8"
+                     : "=&v"(e[8]), "=&v"(e[9]), "=&v"(e[10]), "=&v"(e[11]), "=&v"(e[12]), "=&v"(e[13]),
+                       "=&v"(e[14]), "=&v"(e[15]), "+&v"(addr)
+                     : "v"(step));
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]), "+v"(e[7]),
+                       "+v"(e[8]), "+v"(e[9]), "+v"(e[10]), "+v"(e[11]), "+v"(e[12]), "+v"(e[13]), "+v"(e[14]),
+                       "+v"(e[15]));
         float part = 0.0f;
-        if (in && ge - gs <= cap) {
-            for (int32_t q = gs + sub; q < ge; q += gsz) part += sVal[q - shift];
-        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) part += t * gsz < n ? e[t] : 0.0f;
         if (lg <= 5) {
             part = GroupSum(part, lg);
         } else {
