@@ -543,6 +543,9 @@ constexpr int kWaveChunk = static_cast<int>(kChunkNnz);  // 512 slots, 8 per lan
 constexpr int kLaneItems = kWaveChunk / kWave;           // 8
 constexpr int kWaveRows = static_cast<int>(kMaxRowsPerBlock);
 constexpr int kWavesPerGroup = 4;
+// Waves per workgroup of the flat stream kernel (1 and 2 measured slower on
+// the power-law and fp16 matrices, equal on the Laplacian).
+constexpr int kFlatWaves = 4;
 constexpr int kWavePadded = kWaveChunk + kWaveChunk / kLaneItems;
 
 static_assert(kLaneItems == 8, "lane scan is written for 8 items per lane");
@@ -1431,14 +1434,14 @@ __device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const St
 // is reduced by many waves at once.  Each task stores the partial sums of its
 // chunk-crossing rows; the block's last task to arrive combines them.
 template <typename RowT, ValKind V, OutKind O, bool kBeta>
-__global__ __launch_bounds__(kWave* kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(7)))
+__global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(7)))
 void SpmvStreamFlatKernel(RowBlockParams p)
 {
     using ValT = typename ValOf<V>::T;
     using OutT = typename OutOf<O>::T;
     using L = StreamLoad<RowT, V, O>;
 
-    __shared__ float sValAll[kWavesPerGroup][kStreamLds];
+    __shared__ float sValAll[kFlatWaves][kStreamLds];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1455,7 +1458,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
 
     if (static_cast<int32_t>(blockIdx.x) < p.task_wgs) {
         // Task worker.
-        const int64_t e = static_cast<int64_t>(blockIdx.x) * kWavesPerGroup + wv;
+        const int64_t e = static_cast<int64_t>(blockIdx.x) * kFlatWaves + wv;
         int64_t total = ConstLoad<int32_t>(p.task_start, p.num_blocks);
         total = total < p.max_tasks ? total : p.max_tasks;
         for (int64_t t = e; t < total; t += p.task_waves) {
@@ -1497,7 +1500,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     // Block worker.
     const int64_t wg = static_cast<int64_t>(blockIdx.x) - p.task_wgs;
     const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
-    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kWavesPerGroup + wv;
+    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
     if (tile >= p.num_blocks) return;
     Stage cur = OpenTileFlat<RowT>(p, tile);
     if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
@@ -1969,21 +1972,21 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
                                        0x7FFFFFFFLL;
         if (stream) {
             const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
-            const int64_t wgs = (p.num_blocks + kWavesPerGroup - 1) / kWavesPerGroup;
+            const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
             int64_t taskWgs = 0;
             if (l.layout.tasks) {
                 // task waves: a multiple of 8 workgroups (even over the XCDs)
                 const int64_t waves = l.layout.max_tasks < TaskWaves() ? l.layout.max_tasks : TaskWaves();
-                taskWgs = (waves + kWavesPerGroup * kXcds - 1) / (kWavesPerGroup * kXcds) * kXcds;
+                taskWgs = (waves + kFlatWaves * kXcds - 1) / (kFlatWaves * kXcds) * kXcds;
             }
             p.task_wgs = static_cast<int32_t>(taskWgs);
-            p.task_waves = static_cast<int32_t>(taskWgs * kWavesPerGroup);
+            p.task_waves = static_cast<int32_t>(taskWgs * kFlatWaves);
             const unsigned g = static_cast<unsigned>(taskWgs + (wgs + kXcds - 1) / kXcds * kXcds);
             if (betaNz) {
-                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kWavesPerGroup), 0,
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kFlatWaves), 0,
                                    stream_, p);
             } else {
-                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kWavesPerGroup),
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kFlatWaves),
                                    0, stream_, p);
             }
             return 0;
