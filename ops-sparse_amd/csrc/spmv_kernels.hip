@@ -984,8 +984,14 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     using ValT = typename ValOf<V>::T;
     using OutT = typename OutOf<O>::T;
     // An invalid stage loads from an empty resource: every load returns 0.
+    // The resource ends at the chunk's last non-zero (rounded up to a whole
+    // 16-byte group, never past the last whole group of the arrays): slots
+    // past the chunk read 0 without touching memory, so a short block does
+    // not stream (and gather for) the next block's entries.
     const int64_t a0 = s.valid ? s.a0 : 0;
-    const int64_t avail = s.valid ? tailStart - a0 : 0;
+    int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
+    end = end < tailStart ? end : tailStart;
+    const int64_t avail = s.valid ? end - a0 : 0;
     const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
     // Lane-contiguous 16-byte groups: load h of lane l holds slots
@@ -1076,9 +1082,13 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
             }
         }
     }
+    // Slots past the chunk's last non-zero gather nothing (an offset past the
+    // resource reads 0 without a memory request).
+    const int32_t hiSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c1 - s.a0) : 0;
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
-        const uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
+        uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
+        off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
         if constexpr (sizeof(ValT) == 4) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else {
