@@ -360,6 +360,28 @@ def test_tiny_nnz_counts(nnz, dev):
     assert_close(w, y)
 
 
+@pytest.mark.parametrize("shift", [0, 1, 2, 3])
+@pytest.mark.parametrize("tail", [0, 1, 2, 3])
+def test_chunk_edges_at_every_alignment(shift, tail, dev):
+    """Loads and gathers stop at each chunk's last non-zero: blocks and chunks that start and end at
+    every offset within a 16-byte group, multi-chunk blocks, and nnz % 4 tail entries must all be read."""
+    g = torch.Generator().manual_seed(100 + 4 * shift + tail)
+    body = torch.randint(0, 12, (3000,), generator=g)
+    body[::97] = torch.randint(500, 1600, (body[::97].numel(),), generator=g)  # blocks of 1-4 chunks
+    lengths = torch.cat([torch.tensor([shift], dtype=torch.int64), body.to(torch.int64)])
+    extra = (tail - int(lengths.sum()) % 4) % 4
+    lengths = torch.cat([lengths, torch.tensor([extra + 1], dtype=torch.int64)])
+    cols = 4096
+    rp, col = wl.csr_from_lengths(lengths, cols, g, "cpu", distinct=False)  # exact lengths (repeats allowed)
+    n = col.numel()
+    assert n % 4 == (tail + 1) % 4
+    w = wl.Workload("edges", lengths.numel(), cols, rp.to(torch.int32), col,
+                    torch.rand(n, generator=g) * 2 - 1, torch.rand(cols, generator=g) * 2 - 1,
+                    torch.rand(lengths.numel(), generator=g) * 2 - 1, -0.5, 1.25)
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
+
+
 def test_long_last_row_with_beta(dev):
     # the last row spans many partition windows, so trailing blocks start at row == rows
     lengths = torch.tensor([2] * 300 + [60000], dtype=torch.int64)
