@@ -210,6 +210,34 @@ def graph_ms(w, launches=1000, replays=5):
     return statistics.median(ts)
 
 
+def measure_spmvop(w, alg, steps, warmup, flush_buf):
+    """aclsparseSpMVOp (Z = alpha*A*X + beta*Y, compensated fp32 dot) on the same matrix:
+    median per-launch time (ms) after the same read-only flush, and the createDescr time."""
+    from ops_sparse.spmv import SpMVOp
+
+    z = torch.empty_like(w.y0)
+    stream = torch.cuda.current_stream()
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    p0.record(stream)
+    op = SpMVOp(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, w.y0, z, alg=alg)
+    p1.record(stream)
+    torch.cuda.synchronize()
+    sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
+    for _ in range(warmup):
+        torch.sum(flush_buf, dim=0, out=sink)
+        op.run(w.alpha, w.beta)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        torch.sum(flush_buf, dim=0, out=sink)
+        a.record(stream)
+        op.run(w.alpha, w.beta)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in evs)
+    op.close()
+    return statistics.median(ts), p0.elapsed_time(p1)
+
+
 def cpu_baseline(w, seconds):
     """Single-threaded oracle SpMV (the reference host golden restated in C) on a bounded sample."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -279,6 +307,14 @@ def main():
         results[name] = r
         if name == "c2":
             headline_w, headline = w, r
+            from ops_sparse._lib import SpMVOpAlg
+            for alg in (SpMVOpAlg.ALG1, SpMVOpAlg.ALG2):
+                t, setup = measure_spmvop(w, alg, args.steps, args.warmup, flush_buf)
+                key = f"c2_spmvop_{alg.name.lower()}"
+                results[key] = dict(workload=f"{w.name} through aclsparseSpMVOp {alg.name} (Z != Y)", rows=w.rows,
+                                    nnz=w.nnz, op="N", dtype="float32", algorithmic_bytes=nbytes, median_ms=t,
+                                    gbs=nbytes / (t * 1e-3) / 1e9, frac=nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                    create_descr_ms=setup)
         else:
             del w
             torch.cuda.empty_cache()

@@ -95,6 +95,7 @@ struct OpParams {
     const int32_t* reorder;   // ALG2
     const int32_t* bin_edge;  // ALG2
     const int64_t* running;   // ALG2 inclusive sums of sorted lengths
+    int32_t split;            // ALG2: workgroups per bin
 };
 
 __device__ __forceinline__ void Scalars(const OpParams& p, float& a, float& b)
@@ -162,16 +163,19 @@ __global__ __launch_bounds__(kThreads) void SpmvOpAlg1Kernel(OpParams p)
     }
 }
 
-// ALG2: workgroup b owns sorted positions [bin_edge[b], bin_edge[b+1]); the
-// original row of position i is reorder[i]; W comes from the bin's mean
-// row length.
+// ALG2: bin b owns sorted positions [bin_edge[b], bin_edge[b+1]) and is
+// served by `split` workgroups (blockIdx = b*split + s) that interleave its
+// row groups; the original row of position i is reorder[i]; W comes from the
+// bin's mean row length.
 template <typename RowT>
 __global__ __launch_bounds__(kThreads) void SpmvOpAlg2Kernel(OpParams p)
 {
     float a, b;
     Scalars(p, a, b);
-    const int32_t lo = p.bin_edge[blockIdx.x];
-    const int32_t hi = p.bin_edge[blockIdx.x + 1];
+    const int32_t bin = static_cast<int32_t>(blockIdx.x) / p.split;
+    const int32_t part = static_cast<int32_t>(blockIdx.x) % p.split;
+    const int32_t lo = p.bin_edge[bin];
+    const int32_t hi = p.bin_edge[bin + 1];
     if (hi <= lo) return;
     const int64_t binNnz = p.running[hi - 1] - (lo > 0 ? p.running[lo - 1] : 0);
     const int64_t mean = binNnz / (hi - lo);
@@ -181,8 +185,10 @@ __global__ __launch_bounds__(kThreads) void SpmvOpAlg2Kernel(OpParams p)
     const int sub = lane & ((1 << wlog) - 1);
     const int rowsPerWave = kWave >> wlog;
     const int wv = threadIdx.x / kWave;
-    for (int32_t i0 = lo + wv * rowsPerWave; i0 < hi; i0 += (kThreads / kWave) * rowsPerWave) {
-        const int32_t i = i0 + (lane >> wlog);
+    const int64_t stride = static_cast<int64_t>(p.split) * (kThreads / kWave) * rowsPerWave;
+    for (int64_t i0 = lo + (static_cast<int64_t>(part) * (kThreads / kWave) + wv) * rowsPerWave; i0 < hi;
+         i0 += stride) {
+        const int64_t i = i0 + (lane >> wlog);
         const bool active = i < hi;
         const int64_t row = active ? p.reorder[i] : 0;
         const Triple t = RowDot<RowT>(p, row, active, wlog, sub);
@@ -385,8 +391,15 @@ int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void
         p.reorder = reinterpret_cast<const int32_t*>(ws + l.reorder);
         p.bin_edge = reinterpret_cast<const int32_t*>(ws + l.bin_edge);
         p.running = reinterpret_cast<const int64_t*>(ws + l.running);
-        if (i64) hipLaunchKernelGGL(SpmvOpAlg2Kernel<int64_t>, dim3(d.num_bins), dim3(kThreads), 0, s, p);
-        else hipLaunchKernelGGL(SpmvOpAlg2Kernel<int32_t>, dim3(d.num_bins), dim3(kThreads), 0, s, p);
+        // Bins hold m/bins rows on average (bins <= CU count): enough workgroups
+        // per bin that each wave handles a few row groups, not thousands.
+        const int64_t perBin = (p.m + d.num_bins - 1) / d.num_bins;
+        int64_t split = perBin / 512;
+        split = split < 1 ? 1 : split > 64 ? 64 : split;
+        p.split = static_cast<int32_t>(split);
+        const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(d.num_bins) * split);
+        if (i64) hipLaunchKernelGGL(SpmvOpAlg2Kernel<int64_t>, dim3(grid), dim3(kThreads), 0, s, p);
+        else hipLaunchKernelGGL(SpmvOpAlg2Kernel<int32_t>, dim3(grid), dim3(kThreads), 0, s, p);
         return 0;
     }
     const int64_t mean = p.nnz / p.m;
