@@ -114,9 +114,26 @@ __device__ __forceinline__ Triple RowDot(const OpParams& p, int64_t row, bool ac
     if (active) {
         const int64_t s = static_cast<int64_t>(rp[row]) - p.base;
         const int64_t e = static_cast<int64_t>(rp[row + 1]) - p.base;
-        for (int64_t q = s + sub; q < e; q += (int64_t{1} << wlog)) {
-            const int64_t c = static_cast<int64_t>(p.col[q]) - p.base;
-            PriestAdd(t, p.val[q], p.x[c]);
+        const int64_t w = int64_t{1} << wlog;
+        // Batches of 4 entries per lane: the 4 column/value loads, then the 4
+        // x gathers, are in flight together (one dependent round trip per
+        // batch instead of one per entry); the additions keep the entry order.
+        constexpr int kB = 4;
+        for (int64_t q0 = s + sub; q0 < e; q0 += kB * w) {
+            int32_t c[kB];
+            float v[kB], xv[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const int64_t q = q0 + u * w;
+                c[u] = q < e ? p.col[q] - p.base : 0;
+                v[u] = q < e ? p.val[q] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) xv[u] = q0 + u * w < e ? p.x[c[u]] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (q0 + u * w < e) PriestAdd(t, v[u], xv[u]);
+            }
         }
     }
     for (int msk = (1 << wlog) >> 1; msk > 0; msk >>= 1) t = Merge(t, ShflXor(t, msk));
