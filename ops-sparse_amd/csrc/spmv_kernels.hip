@@ -4,21 +4,29 @@
 //  * Preprocess: one launch normalises the row offsets (rowPtr[i*stride]-base,
 //    clamped to [0, nnz]) into the workspace and computes the row-block
 //    partition: block b owns the rows whose weighted merge-path coordinate
-//    (16*row + rowOffset[row]) lies in [b*T, (b+1)*T).  Every row belongs to
-//    exactly one block, so no cross-block fix-up is ever needed; a block has
-//    at most 511 rows and ~2000 non-zeros regardless of the row-length
-//    distribution (only a row longer than a chunk makes its block longer).  Reference counterpart: the normalising kernel
-//    sparse/spmv/arch35/spmv_kernel.cpp:1144-1163 (one block, scalar loop).
-//  * Non-transpose: one workgroup (256 lanes = 4 wave64) per row block.  The
-//    block streams its col_ind/values span through LDS in chunks of 2048
-//    non-zeros with 16-byte non-temporal loads (so x stays in L2/MALL),
-//    gathers x, and reduces rows with an LDS segmented scan (8 items per lane
-//    + a wave64 shuffle scan).  Rows longer than a chunk carry their partial
-//    sum from chunk to chunk inside the block.  Replaces the warp-per-row
-//    kernel sparse/spmv/arch35/spmv_kernel.cpp:501-577.
-//  * Transpose: the same row blocks scatter alpha*conj?(a_ij)*x_i with
-//    hardware float atomics into y (pre-scaled by beta) or into an fp32/int64
-//    accumulator that a finalize pass converts (reference ALG1:
+//    (16*row + rowOffset[row]) lies in [b*T, (b+1)*T), T <= 2032.  A block
+//    has at most 127 rows (two per lane of a wave64) and about 500
+//    non-zeros; only a row longer than that makes its block longer.  Blocks
+//    of more than kLongChunks chunks are split into one task per 512-entry
+//    chunk (task table: count, hipCUB scan, fill).  Reference counterpart:
+//    the normalising kernel sparse/spmv/arch35/spmv_kernel.cpp:1144-1163
+//    (one block, scalar loop).
+//  * Non-transpose, real x/y (SpmvStreamFlatKernel): one wave64 per row
+//    block, 4 waves per workgroup.  col_ind/values stream through 16-byte
+//    buffer loads in 512-slot chunks, x is gathered, the products go to LDS
+//    and rows are reduced by lane groups (short rows) or by the whole wave
+//    (long rows, with a carried partial sum).  The first workgroups serve the
+//    long-block tasks; the last task of a block combines the partial sums of
+//    the rows that cross its chunks.  Replaces the warp-per-row kernel
+//    sparse/spmv/arch35/spmv_kernel.cpp:501-577.  Real A with complex x/y
+//    (SpmvWaveKernel) and strided or int8/complex operands
+//    (SpmvRowBlockKernel) use the general kernels below.
+//  * Transpose: Preprocess builds a CSC pattern (radix sort of (column,
+//    position) pairs); each SpMV streams the products a_k*x_row(k) in CSR
+//    order and then sums every column's products in a fixed order
+//    (deterministic, the reference's CSR_ALG2 semantics,
+//    sparse/spmv/arch35/spmv_kernel.cpp:861-879).  Beyond the sort's int
+//    range the transpose scatters with float/int64 atomics (reference ALG1:
 //    sparse/spmv/arch35/spmv_kernel.cpp:579-668).
 //  * Block ids are remapped so that each of the 8 XCDs processes one
 //    contiguous eighth of the matrix (x neighbourhoods stay in one L2).
@@ -897,24 +905,26 @@ __global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvWaveKernel(RowBlock
 
 // ------------------------- stream row kernel (fp32 sums) ---------------------
 //
-// Same persistent wave workers, row blocks and 512-slot chunks as the kernel
-// above, with a cheaper reduction for the common case of short rows:
+// The same row blocks and 512-slot chunks as the kernel above, one block per
+// wave (no persistence), with a cheaper reduction for the common case of
+// short rows:
 //  * col_ind / values are read with 16-byte buffer loads whose resource
-//    starts at the chunk (a scalar base, a constant per-lane offset); the
-//    resource ends at the last whole 16-byte group of the arrays, so loads
-//    past it return zero instead of faulting, and x is gathered through a
-//    resource bounded by the vector's length (32-bit offsets, no masking);
+//    starts at the chunk (a scalar base, a constant per-lane offset) and
+//    ends at the chunk's last non-zero (rounded up to a 16-byte group), so
+//    loads past it return zero without a memory request; x is gathered
+//    through a resource bounded by the vector's length (32-bit offsets), and
+//    slots past the chunk gather nothing;
 //  * the products of a chunk go to the wave's LDS slice in slot order;
-//  * phase 1: rows that lie inside the chunk and are short (SerialCap) are summed from LDS by groups of G lanes (G = 1 for blocks of
-//    many short rows, up to 64 for a block of one row), then reduced across
-//    the group;
+//  * phase 1: rows that lie inside the chunk and are short (SerialCap) are
+//    summed from LDS by groups of G lanes (G = 1 for blocks of many short
+//    rows, up to 64 for a block of one row), then reduced across the group;
 //  * phase 2: the remaining rows (longer ones, and the rows that continue
 //    from the previous chunk or into the next) are summed by the whole wave,
 //    one after another; a row that crosses a chunk boundary carries its
 //    partial sum in a scalar register.
-// Every row of a block is owned by lane i % 64 (output slot i / 64), which
-// writes y or, when the row does not finish in this chunk, the sink, so
-// every lane issues the same stores in every chunk.
+// Rows 2l and 2l+1 of a block are owned by lane l, which writes y or, when a
+// row does not finish in this chunk, the sink, so every lane issues the same
+// stores in every chunk.
 
 // Phase-1 row length limit: 8 entries for one lane per row, 16 per lane for
 // groups (rows of medium length, few rows per block).
@@ -1138,8 +1148,8 @@ constexpr int kStreamLds = kWaveChunk + 8;
 
 // Reduces one loaded and gathered chunk: products to LDS, phase 1 (short
 // rows, lane groups), phase 2 (long or chunk-crossing rows, whole wave), y.
-// Row i of the block (i = lane + 64h) has its offsets in registers: its
-// start in this lane's rp[h], its end in the next row's.
+// Row i = 2*lane + h of the block has its offsets in registers: its start
+// in this lane's rp[h], its end in the next row's.
 // Task mode (kTask): the chunk is one task of a long block; rows that cross
 // the chunk's first slot leave their partial sum in `head` (also when they
 // cross both ends), the row that crosses its last slot in `tail`, and neither
