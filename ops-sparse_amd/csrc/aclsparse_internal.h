@@ -207,7 +207,7 @@ inline size_t AccumulatorBytes(aclDataType computeType)
 }
 
 inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
-                                aclDataType computeType, bool transpose)
+                                aclDataType computeType, bool transpose, bool allowTasks = true)
 {
     SpmvLayout l;
     l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
@@ -220,7 +220,7 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     l.sink_offset = AlignUp(l.block_nnz_offset + static_cast<size_t>(l.num_blocks + 1) * l.rowptr_bytes);
     l.acc_offset = l.sink_offset + kSinkBytes;
     l.total = l.acc_offset;
-    if (!transpose && computeType == ACL_FLOAT && nnz > 0) {
+    if (allowTasks && !transpose && computeType == ACL_FLOAT && nnz > 0) {
         const int64_t maxTasks = static_cast<int64_t>(nnz / kChunkNnz) + l.num_blocks + 1;
         if (maxTasks < 0x7FFFFFFFLL) {
             l.tasks = true;
@@ -299,6 +299,9 @@ struct SpmvLaunch {
 
 // Normalises the row offsets and writes the row-block partition and header.
 int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream);
+// SpMVOp on the row-block partition of l (fp32, non-transpose, no tasks):
+// z = alpha*(A*x, doubly compensated) + beta*y, y read from l.y.
+int LaunchSpmvOpStream(const SpmvLaunch& l, float* z, void* stream);
 // Runs y = alpha*op(A)*x + beta*y using the partition already in the workspace.
 int LaunchSpmvCompute(const SpmvLaunch& l, void* stream);
 
@@ -336,15 +339,18 @@ namespace aclsp {
 constexpr size_t kOpHeaderBytes = 256;
 constexpr uint32_t kOpRowsPerBin = 128;
 
+//   After them: the row-block partition of the execution kernel (an SpMV
+//   workspace without long-block tasks, `spmv` bytes in, laid out by `sl`).
 struct SpmvOpLayout {
     size_t reorder = 0, tmp_reorder = 0, scratch = 0, tmp_scratch = 0, bin_edge = 0;
-    size_t running = 0, temp = 0, temp_bytes = 0, total = 0;
+    size_t running = 0, temp = 0, temp_bytes = 0, spmv = 0, total = 0;
+    SpmvLayout sl;
 };
 
 // numBins = min(CUs, ceil(m/128)) (sparse/spmv_op/arch35/spmv_op_host.cpp:305-327 with
 // the AIV core count replaced by the CU count).
 uint32_t SpmvOpNumBins(int64_t m);
-SpmvOpLayout SpmvOpComputeLayout(int64_t m, uint32_t bins);
+SpmvOpLayout SpmvOpComputeLayout(int64_t m, int64_t n, int64_t nnz, aclsparseIndexType_t rowType, uint32_t bins);
 
 int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream);
 int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,

@@ -41,6 +41,7 @@
 #include <type_traits>
 
 #include "aclsparse_internal.h"
+#include "compensated.h"
 
 namespace aclsp {
 namespace {
@@ -296,6 +297,7 @@ struct RowBlockParams {
     int32_t task_waves;  // waves serving tasks (0: tasks off)
     int32_t task_wgs;    // workgroups serving tasks (the first ones of the grid)
     int64_t max_tasks;   // capacity of the task arrays
+    float* z;            // SpMVOp: output (y is then only read)
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -1536,6 +1538,173 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     }
 }
 
+// ------------------------ SpMVOp on the row blocks ---------------------------
+//
+// z = alpha*(A*x) + beta*y with Priest's doubly compensated dot product, on
+// the same row blocks, chunk loads and gathers as the stream kernel above.
+// Each product is split exactly (prod, err) and both halves go to LDS; a row
+// is accumulated in a triple by one lane (short rows), a lane group (medium
+// rows; group triples merged by TwoSum butterflies) or the whole wave (long
+// or chunk-crossing rows, with a triple carried from chunk to chunk).  The
+// summation order depends only on the matrix, so results are reproducible.
+// Long blocks are processed chunk by chunk by their own wave (no tasks).
+
+template <typename RowT, bool kBeta>
+__device__ __forceinline__ void StreamChunkOp(const Stage& cur, const StreamLoad<RowT, ValKind::F32, OutKind::F32>& lc,
+                                              float* sP, float* sE, int lane, float alpha, float beta, Triple& carry,
+                                              int& lg, float* z, float* sink)
+{
+#pragma clang fp contract(off)
+    float pr[kLaneItems], er[kLaneItems];
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) {
+        const float a = lc.val.v[j >> 2][j & 3];
+        const float xv = __uint_as_float(lc.xg[j]);
+        pr[j] = a * xv;
+        er[j] = __fmaf_rn(a, xv, -pr[j]);
+    }
+    const int32_t c0 = cur.c0, c1 = cur.c1;
+    const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);
+    const int nr = cur.nr;
+    if (cur.first) {
+        carry = Triple{0.0f, 0.0f, 0.0f};
+        lg = 0;
+        if (cur.last) {
+            while (lg < 6 && (nr << (lg + 1)) <= kWave) ++lg;
+        }
+    }
+    *reinterpret_cast<v4f*>(&sP[4 * lane]) = v4f{pr[0], pr[1], pr[2], pr[3]};
+    *reinterpret_cast<v4f*>(&sP[256 + 4 * lane]) = v4f{pr[4], pr[5], pr[6], pr[7]};
+    *reinterpret_cast<v4f*>(&sE[4 * lane]) = v4f{er[0], er[1], er[2], er[3]};
+    *reinterpret_cast<v4f*>(&sE[256 + 4 * lane]) = v4f{er[4], er[5], er[6], er[7]};
+
+    const int32_t k0lo = static_cast<int32_t>(cur.k0);
+    int32_t rs[2], re[2];
+    rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
+    rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
+    re[0] = rs[1];
+    re[1] = FromNextLane(rs[0], rs[1]);
+
+    const int gsz = 1 << lg;
+    const int cap = SerialCap(lg);
+    bool fin[2], defer[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = 2 * lane + h;
+        const bool in = i < nr;
+        const bool empty = re[h] <= rs[h];
+        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                         : (rs[h] < c1 && re[h] > c0));
+        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
+        defer[h] = active && (crosses || re[h] - rs[h] > cap);
+        fin[h] = active && !defer[h];
+    }
+    WaveLdsSync();
+
+    // Phase 1.  Adding (0, 0) to a triple is exact, so masked entries add zeros.
+    Triple sum[2] = {Triple{0.0f, 0.0f, 0.0f}, Triple{0.0f, 0.0f, 0.0f}};
+    if (lg == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
+            const int32_t base = fin[h] ? rs[h] - shift : 0;
+#pragma unroll
+            for (int t = 0; t < kSerialCapOne; ++t) {
+                const bool on = t < len;
+                PriestAddSplit(sum[h], on ? sP[base + t] : 0.0f, on ? sE[base + t] : 0.0f);
+            }
+        }
+    } else {
+        const int g = lane >> lg;
+        const int sub = lane & (gsz - 1);
+        const bool in = g < nr;
+        const int src = (g >> 1) & (kWave - 1);
+        const int32_t a0s = __shfl(rs[0], src, kWave), a1s = __shfl(rs[1], src, kWave);
+        const int32_t a1e = __shfl(re[1], src, kWave);
+        const int32_t gs = (g & 1) ? a1s : a0s;
+        const int32_t ge = (g & 1) ? a1e : a1s;
+        Triple part{0.0f, 0.0f, 0.0f};
+        if (in && ge - gs <= cap) {
+            for (int32_t q = gs + sub; q < ge; q += gsz) PriestAddSplit(part, sP[q - shift], sE[q - shift]);
+        }
+        for (int m = 1; m < gsz; m <<= 1) part = Merge(part, ShflXor(part, m));
+        sum[0] = Shfl(part, ((2 * lane) << lg) & (kWave - 1));
+        sum[1] = Shfl(part, ((2 * lane + 1) << lg) & (kWave - 1));
+    }
+
+    // Phase 2: deferred rows, whole wave per row, in row order.
+    uint64_t pending0 = __ballot(defer[0]), pending1 = __ballot(defer[1]);
+    while (pending0 | pending1) {
+        const int l0 = pending0 ? __builtin_ctzll(pending0) : kWave;
+        const int l1 = pending1 ? __builtin_ctzll(pending1) : kWave;
+        const int h = (2 * l1 + 1 < 2 * l0) ? 1 : 0;
+        const int l = h ? l1 : l0;
+        if (h) {
+            pending1 &= pending1 - 1;
+        } else {
+            pending0 &= pending0 - 1;
+        }
+        const int32_t s0 = __builtin_amdgcn_readlane(h ? rs[1] : rs[0], l);
+        const int32_t e0 = __builtin_amdgcn_readlane(h ? re[1] : re[0], l);
+        const int32_t lo = s0 > c0 ? s0 : c0;
+        const int32_t hi = e0 < c1 ? e0 : c1;
+        Triple part{0.0f, 0.0f, 0.0f};
+        for (int32_t q = lo + lane; q < hi; q += kWave) PriestAddSplit(part, sP[q - shift], sE[q - shift]);
+        for (int m = 1; m < kWave; m <<= 1) part = Merge(part, ShflXor(part, m));
+        if (s0 < c0) part = Merge(carry, part);
+        if (e0 > c1) {
+            carry = part;
+        } else if (lane == l) {
+            sum[h] = part;
+            fin[h] = true;
+        }
+    }
+
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = 2 * lane + h;
+        float yv = 0.0f;
+        if constexpr (kBeta) {
+            if (beta != 0.0f) yv = lc.yold[h];
+        }
+        float* dst = fin[h] ? z + (cur.r0 + i) : sink + h * kWave;
+        *dst = CombineZ(sum[h], alpha, beta, yv);
+    }
+    WaveLdsSync();
+}
+
+template <typename RowT, bool kBeta>
+__global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlockParams p)
+{
+    using L = StreamLoad<RowT, ValKind::F32, OutKind::F32>;
+    __shared__ float sPAll[kFlatWaves][kStreamLds];
+    __shared__ float sEAll[kFlatWaves][kStreamLds];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(p.s, alpha, beta);
+    float* sink = static_cast<float*>(p.sink) + lane;
+    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(float)));
+    const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
+    const int64_t wg = static_cast<int64_t>(blockIdx.x);
+    const int64_t per = static_cast<int64_t>(gridDim.x) / kXcds;
+    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
+    if (tile >= p.num_blocks) return;
+    Stage cur = OpenTileFlat<RowT>(p, tile);
+    Triple carry{0.0f, 0.0f, 0.0f};
+    int lg = 0;
+    while (cur.valid) {
+        L b;
+        StreamLoadStage<RowT, ValKind::F32, OutKind::F32, kBeta>(p, cur, tailStart, lane, b);
+        StreamGather<RowT, ValKind::F32, OutKind::F32>(p, cur, tailStart, rx, lane, b, b.xg);
+        StreamChunkOp<RowT, kBeta>(cur, b, sPAll[wv], sEAll[wv], lane, alpha, beta, carry, lg, p.z, sink);
+        if (cur.last) break;
+        cur.c0 = cur.c1;
+        cur.first = false;
+        ChunkBounds(cur);
+    }
+}
+
 // ------------------------------- transpose ----------------------------------
 
 // y = beta*y in place (y is not read when beta == 0); the scatter then adds
@@ -2232,6 +2401,25 @@ size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes)
     }
     if (e != hipSuccess) bytes = static_cast<size_t>(nnz) * 16 + (1 << 20);
     return bytes;
+}
+
+int LaunchSpmvOpStream(const SpmvLaunch& l, float* z, void* stream)
+{
+    if (l.rows <= 0) return 0;
+    RowBlockParams p = MakeRowBlockParams(l);
+    p.z = z;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
+    const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+    const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+    if (l.rowptr64) {
+        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+        else hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, false>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+    } else {
+        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+        else hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, false>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+    }
+    return 0;
 }
 
 int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)

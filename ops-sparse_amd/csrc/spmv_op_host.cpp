@@ -77,7 +77,9 @@ aclsparseStatus_t aclsparseSpMVOp_bufferSize(aclsparseHandle_t handle, aclsparse
     if (matA->rows > 0x7FFFFFFFULL) return ACL_SPARSE_STATUS_NOT_SUPPORTED;
     if (alg == ACL_SPARSE_SPMVOP_ALG2) {
         const int64_t m = static_cast<int64_t>(matA->rows);
-        *bufferSize = aclsp::SpmvOpComputeLayout(m, aclsp::SpmvOpNumBins(m)).total;
+        *bufferSize = aclsp::SpmvOpComputeLayout(m, static_cast<int64_t>(matA->cols), static_cast<int64_t>(matA->nnz),
+                                                 matA->ptr_type, aclsp::SpmvOpNumBins(m))
+                          .total;
     } else {
         *bufferSize = 0;
     }

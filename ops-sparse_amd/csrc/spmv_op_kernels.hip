@@ -4,21 +4,26 @@
 // The reference runs one scalar thread per row with Priest's accumulator
 // (TwoProduct by FMA + two TwoSum stages, sparse/spmv_op/arch35/spmv_op_kernel.cpp:87-128)
 // and builds the ALG2 tables with one scalar thread (:425-540).  Here:
-//  * W lanes of a wave64 share a row (W from the mean row length of the
-//    matrix or of the ALG2 bin); every lane keeps its own Priest triple
-//    (hi, md, lo) over a strided subset of the row and the W triples are
-//    merged by an exact TwoSum butterfly.  The order is fixed, so results
-//    are bit-reproducible run to run.
-//  * ALG2 preprocess is parallel: row lengths, a stable descending radix
-//    sort (hipCUB), an int64 inclusive scan, and the bin edges by binary
-//    search plus the reference's one-edge-per-row rule.  reorder, scratch
-//    and bin_edge are bit-identical to the reference's serial tables.
+//  * ALG1 (no buffer): W lanes of a wave64 share a row (W from the mean row
+//    length); every lane keeps its own Priest triple (hi, md, lo) over a
+//    strided subset of the row and the W triples are merged by an exact
+//    TwoSum butterfly.
+//  * ALG2 (buffer): createDescr builds the reference's tables in parallel
+//    (row lengths, a stable descending radix sort (hipCUB), an int64
+//    inclusive scan, the bin edges by binary search plus the reference's
+//    one-edge-per-row rule; reorder, scratch and bin_edge are bit-identical
+//    to the reference's serial tables) and, after them, the SpMV row-block
+//    partition; execution runs the SpMV stream kernel with the compensated
+//    accumulator (SpmvOpStreamKernel in spmv_kernels.hip).
+//  Summation orders depend only on the matrix: results are bit-reproducible
+//  run to run.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
 #include <cstdint>
 
 #include "aclsparse_internal.h"
+#include "compensated.h"
 
 // The error-free transformations below (TwoSum, TwoProduct) rely on every
 // operation being rounded as written: no contraction of a*b + c into FMA.
@@ -30,53 +35,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
 
-struct Triple {
-    float hi, md, lo;
-};
-
-// Priest's update of (hi, md, lo) with the exact product a*b
-// (same recurrence as spmv_op_kernel.cpp:100-124).
-__device__ __forceinline__ void PriestAdd(Triple& t, float a, float b)
-{
-    const float prod = a * b;
-    const float pi = __fmaf_rn(a, b, -prod);
-    const float s1 = t.hi + prod;
-    const float v1 = s1 - t.hi;
-    const float e1 = (t.hi - (s1 - v1)) + (prod - v1);
-    t.hi = s1;
-    const float ee = e1 + pi;
-    const float s2 = t.md + ee;
-    const float v2 = s2 - t.md;
-    const float e2 = (t.md - (s2 - v2)) + (ee - v2);
-    t.md = s2;
-    t.lo = t.lo + e2;
-}
-
-__device__ __forceinline__ void TwoSum(float a, float b, float& s, float& e)
-{
-    s = a + b;
-    const float v = s - a;
-    e = (a - (s - v)) + (b - v);
-}
-
-// Merges two triples keeping the rounding error of both leading sums.
-__device__ __forceinline__ Triple Merge(const Triple& a, const Triple& b)
-{
-    Triple r;
-    float e1, e2;
-    TwoSum(a.hi, b.hi, r.hi, e1);
-    float m;
-    TwoSum(a.md, b.md, m, e2);
-    float e3;
-    TwoSum(m, e1, r.md, e3);
-    r.lo = a.lo + b.lo + e2 + e3;
-    return r;
-}
-
-__device__ __forceinline__ Triple ShflXor(const Triple& t, int m)
-{
-    return Triple{__shfl_xor(t.hi, m, kWave), __shfl_xor(t.md, m, kWave), __shfl_xor(t.lo, m, kWave)};
-}
 
 struct OpParams {
     const void* rp;
@@ -92,10 +50,6 @@ struct OpParams {
     const float* beta_ptr;
     int32_t device_scalars;
     int32_t wlog;             // ALG1: log2 lanes per row
-    const int32_t* reorder;   // ALG2
-    const int32_t* bin_edge;  // ALG2
-    const int64_t* running;   // ALG2 inclusive sums of sorted lengths
-    int32_t split;            // ALG2: workgroups per bin
 };
 
 __device__ __forceinline__ void Scalars(const OpParams& p, float& a, float& b)
@@ -140,24 +94,10 @@ __device__ __forceinline__ Triple RowDot(const OpParams& p, int64_t row, bool ac
     return t;
 }
 
-// z = a*(hi + md + lo) + b*y.  The reference folds this as
-// fma(a, hi, fma(a, md + lo, b*y)) (spmv_op_kernel.cpp:177-181), whose inner
-// rounding happens at the magnitude of b*y: when A*x nearly cancels y the
-// relative error of z grows without bound.  Here both leading products are
-// split exactly (TwoProduct by FMA) and added by TwoSum, so z is rounded
-// once at its own magnitude, up to the small tail terms.
 __device__ __forceinline__ void StoreZ(const OpParams& p, int64_t row, const Triple& t, float a, float b)
 {
     const float yv = b == 0.0f ? 0.0f : p.y[row];
-    const float p1 = a * t.hi;
-    const float e1 = __fmaf_rn(a, t.hi, -p1);
-    const float p2 = b * yv;
-    const float e2 = __fmaf_rn(b, yv, -p2);
-    float s, es;
-    TwoSum(p1, p2, s, es);
-    const float tail = __fmaf_rn(a, t.md + t.lo, es + (e1 + e2));
-    // non-finite terms: keep the reference's fold so Inf/NaN propagate alike
-    p.z[row] = __builtin_isfinite(s) ? s + tail : __fmaf_rn(a, t.hi, __fmaf_rn(a, t.md + t.lo, p2));
+    p.z[row] = CombineZ(t, a, b, yv);
 }
 
 // ALG1: rows in natural order, 64/W rows per wave pass, grid-stride.
@@ -176,39 +116,6 @@ __global__ __launch_bounds__(kThreads) void SpmvOpAlg1Kernel(OpParams p)
         const int64_t row = r0 + (lane >> wlog);
         const bool active = row < p.m;
         const Triple t = RowDot<RowT>(p, active ? row : 0, active, wlog, sub);
-        if (active && sub == 0) StoreZ(p, row, t, a, b);
-    }
-}
-
-// ALG2: bin b owns sorted positions [bin_edge[b], bin_edge[b+1]) and is
-// served by `split` workgroups (blockIdx = b*split + s) that interleave its
-// row groups; the original row of position i is reorder[i]; W comes from the
-// bin's mean row length.
-template <typename RowT>
-__global__ __launch_bounds__(kThreads) void SpmvOpAlg2Kernel(OpParams p)
-{
-    float a, b;
-    Scalars(p, a, b);
-    const int32_t bin = static_cast<int32_t>(blockIdx.x) / p.split;
-    const int32_t part = static_cast<int32_t>(blockIdx.x) % p.split;
-    const int32_t lo = p.bin_edge[bin];
-    const int32_t hi = p.bin_edge[bin + 1];
-    if (hi <= lo) return;
-    const int64_t binNnz = p.running[hi - 1] - (lo > 0 ? p.running[lo - 1] : 0);
-    const int64_t mean = binNnz / (hi - lo);
-    int wlog = 0;
-    while (wlog < 6 && (int64_t{4} << wlog) < mean) ++wlog;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int sub = lane & ((1 << wlog) - 1);
-    const int rowsPerWave = kWave >> wlog;
-    const int wv = threadIdx.x / kWave;
-    const int64_t stride = static_cast<int64_t>(p.split) * (kThreads / kWave) * rowsPerWave;
-    for (int64_t i0 = lo + (static_cast<int64_t>(part) * (kThreads / kWave) + wv) * rowsPerWave; i0 < hi;
-         i0 += stride) {
-        const int64_t i = i0 + (lane >> wlog);
-        const bool active = i < hi;
-        const int64_t row = active ? p.reorder[i] : 0;
-        const Triple t = RowDot<RowT>(p, row, active, wlog, sub);
         if (active && sub == 0) StoreZ(p, row, t, a, b);
     }
 }
@@ -323,7 +230,7 @@ uint32_t SpmvOpNumBins(int64_t m)
     return static_cast<uint32_t>(bins < 1 ? 1 : bins);
 }
 
-SpmvOpLayout SpmvOpComputeLayout(int64_t m, uint32_t bins)
+SpmvOpLayout SpmvOpComputeLayout(int64_t m, int64_t n, int64_t nnz, aclsparseIndexType_t rowType, uint32_t bins)
 {
     SpmvOpLayout l;
     const size_t rb = static_cast<size_t>(m) * sizeof(int32_t);
@@ -335,16 +242,56 @@ SpmvOpLayout SpmvOpComputeLayout(int64_t m, uint32_t bins)
     l.running = AlignUp(l.bin_edge + static_cast<size_t>(bins + 1) * sizeof(int32_t));
     l.temp = AlignUp(l.running + static_cast<size_t>(m) * sizeof(int64_t));
     l.temp_bytes = m > 0 ? SortScanTempBytes(m) : 0;
-    l.total = AlignUp(l.temp + l.temp_bytes + 256);  // +256: the temp area is re-aligned to 256 bytes
+    l.spmv = AlignUp(l.temp + l.temp_bytes + 256);  // +256: the temp area is re-aligned to 256 bytes
+    l.sl = ComputeLayout(static_cast<uint64_t>(m), static_cast<uint64_t>(n), static_cast<uint64_t>(nnz), rowType,
+                         ACL_FLOAT, false, false);
+    l.total = AlignUp(l.spmv + l.sl.total);
     return l;
 }
+
+namespace {
+
+SpmvOpLayout LayoutOf(const aclsparseSpMVOpDescr& d)
+{
+    return SpmvOpComputeLayout(static_cast<int64_t>(d.m), static_cast<int64_t>(d.n), static_cast<int64_t>(d.nnz),
+                               d.row_type, d.num_bins);
+}
+
+// The SpMV launch description of the execution kernel's partition, which
+// sits in the ALG2 buffer after the reference's tables.
+SpmvLaunch OpLaunch(const aclsparseSpMVOpDescr& d, const SpmvOpLayout& l)
+{
+    SpmvLaunch sl{};
+    sl.row_ptr = d.row_offsets;
+    sl.row_stride = 1;
+    sl.col = d.col_ind;
+    sl.col_stride = 1;
+    sl.val = d.values;
+    sl.val_stride = 1;
+    sl.x_stride = 1;
+    sl.y_stride = 1;
+    sl.rows = static_cast<int64_t>(d.m);
+    sl.cols = static_cast<int64_t>(d.n);
+    sl.nnz = static_cast<int64_t>(d.nnz);
+    sl.base = d.base == ACL_SPARSE_INDEX_BASE_ONE ? 1 : 0;
+    sl.rowptr64 = d.row_type == ACL_SPARSE_INDEX_64I ? 1 : 0;
+    sl.val_kind = ValKind::F32;
+    sl.out_kind = OutKind::F32;
+    sl.acc_kind = AccKind::F32;
+    sl.op = ACL_SPARSE_OP_NON_TRANSPOSE;
+    sl.ws = static_cast<uint8_t*>(d.buffer) + l.spmv;
+    sl.layout = l.sl;
+    return sl;
+}
+
+}  // namespace
 
 int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream)
 {
     const int64_t m = static_cast<int64_t>(d.m);
     if (m <= 0) return 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const SpmvOpLayout l = SpmvOpComputeLayout(m, d.num_bins);
+    const SpmvOpLayout l = LayoutOf(d);
     uint8_t* ws = static_cast<uint8_t*>(d.buffer);
     int32_t* reorder = reinterpret_cast<int32_t*>(ws + l.reorder);
     int32_t* tmpReorder = reinterpret_cast<int32_t*>(ws + l.tmp_reorder);
@@ -374,7 +321,8 @@ int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream)
         return 1;
     }
     hipLaunchKernelGGL(OpBinEdgeKernel, dim3(1), dim3(kThreads), 0, s, running, m, d.num_bins, binEdge);
-    return 0;
+    // the execution kernel's row-block partition
+    return LaunchSpmvPreprocess(OpLaunch(d, l), stream);
 }
 
 int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
@@ -403,21 +351,20 @@ int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void
     }
     const bool i64 = d.row_type == ACL_SPARSE_INDEX_64I;
     if (d.alg == ACL_SPARSE_SPMVOP_ALG2) {
-        const SpmvOpLayout l = SpmvOpComputeLayout(p.m, d.num_bins);
-        uint8_t* ws = static_cast<uint8_t*>(d.buffer);
-        p.reorder = reinterpret_cast<const int32_t*>(ws + l.reorder);
-        p.bin_edge = reinterpret_cast<const int32_t*>(ws + l.bin_edge);
-        p.running = reinterpret_cast<const int64_t*>(ws + l.running);
-        // Bins hold m/bins rows on average (bins <= CU count): enough workgroups
-        // per bin that each wave handles a few row groups, not thousands.
-        const int64_t perBin = (p.m + d.num_bins - 1) / d.num_bins;
-        int64_t split = perBin / 512;
-        split = split < 1 ? 1 : split > 64 ? 64 : split;
-        p.split = static_cast<int32_t>(split);
-        const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(d.num_bins) * split);
-        if (i64) hipLaunchKernelGGL(SpmvOpAlg2Kernel<int64_t>, dim3(grid), dim3(kThreads), 0, s, p);
-        else hipLaunchKernelGGL(SpmvOpAlg2Kernel<int32_t>, dim3(grid), dim3(kThreads), 0, s, p);
-        return 0;
+        // ALG2 has a buffer: it runs on the row-block partition that
+        // createDescr built there, with the stream kernel's coalesced chunk
+        // loads (the length-sorted tables are the reference's load balance
+        // for its cores; the merge-path row blocks balance any row-length
+        // distribution without them).
+        SpmvLaunch sl = OpLaunch(d, LayoutOf(d));
+        sl.x = x;
+        sl.y = const_cast<void*>(y);
+        sl.device_scalars = deviceScalars ? 1 : 0;
+        sl.alpha_re = alpha;
+        sl.beta_re = beta;
+        sl.alpha_ptr = alphaPtr;
+        sl.beta_ptr = betaPtr;
+        return LaunchSpmvOpStream(sl, static_cast<float*>(z), stream);
     }
     const int64_t mean = p.nnz / p.m;
     int wlog = 0;

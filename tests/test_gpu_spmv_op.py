@@ -325,3 +325,37 @@ def test_status_codes(dev):
     assert lib.aclsparseSpMVOp_destroyDescr(descr) == Status.SUCCESS
     assert lib.aclsparseSpMVOp_destroyPlan(None) == Status.SUCCESS
     assert lib.aclsparseSpMVOp_destroyDescr(None) == Status.SUCCESS
+
+
+@pytest.mark.parametrize("i64", [False, True])
+def test_alg2_row_blocks_reproducible_and_correctly_rounded(i64, dev):
+    """ALG2 runs on the SpMV row blocks (short rows per lane, lane groups, whole-wave rows carried
+    across chunks): repeated runs and rebuilt descriptors are bit-identical, and every z is within
+    2 ulp of the fp64 golden (plus 1e-12 of the row scale for cancelling rows)."""
+    rng = np.random.default_rng(77)
+    lengths = np.concatenate([rng.integers(0, 6, 20000), rng.integers(20, 60, 500), [3000, 0, 9000, 1],
+                              rng.integers(0, 3, 4000)])
+    m, k = lengths.size, 50000
+    rp = np.zeros(m + 1, np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    col = rng.integers(0, k, int(rp[-1])).astype(np.int32)
+    val = rng.uniform(-3, 3, col.size).astype(np.float32)
+    x = rng.uniform(-3, 3, k).astype(np.float32)
+    y = rng.uniform(-3, 3, m).astype(np.float32)
+    d = [torch.from_numpy(a).to(dev) for a in (rp.astype(np.int64 if i64 else np.int32), col, val, x, y)]
+    outs = []
+    for _ in range(2):
+        z = torch.full((m,), float("nan"), device=dev)
+        op = SpMVOp(m, k, *d, z, alg=SpMVOpAlg.ALG2)
+        op.run(1.25, -0.5)
+        op.run(1.25, -0.5)
+        torch.cuda.synchronize()
+        outs.append(z.cpu().numpy())
+        op.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    golden = oracle.spmv_f64(rp, col, val, x, y, 1.25, -0.5)
+    scale = oracle.row_scale(rp, col, val, x, y, oracle.K_F32, oracle.K_F32, 1.25, -0.5, cols=k)
+    g32 = golden.astype(np.float32)
+    ulp = np.spacing(np.abs(g32)).astype(np.float64)
+    err = np.abs(outs[0].astype(np.float64) - golden)
+    assert np.all(err <= 2 * ulp + 1e-12 * scale), float(np.max(err / (ulp + 1e-30)))
