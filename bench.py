@@ -71,6 +71,34 @@ def profile_mode(name, steps):
                       "copy_bytes_each_way": src.numel() * 4, "steps": steps}))
 
 
+def dtype_variants(w):
+    """The headline matrix through the other paths of the dtype/op matrix (same sparsity)."""
+    from ops_sparse.workloads import Workload
+
+    g = torch.Generator(device=w.values.device)
+    g.manual_seed(99)
+    n = w.nnz
+
+    def i8(k):
+        return torch.randint(-128, 128, (k,), generator=g, device=w.values.device, dtype=torch.int8)
+
+    def c64(v):
+        return torch.complex(v, 0.5 * v.flip(0))
+
+    out = {
+        "c2_T": Workload(w.name + "_T", w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, w.y0, 1.5, 0.5,
+                         trans="T"),
+        "c2_f16": Workload(w.name + "_f16", w.rows, w.cols, w.row_ptr, w.col_ind, w.values.half(), w.x.half(),
+                           w.y0.half(), 1.5, 0.5, out_dtype=torch.float16),
+        "c2_i8": Workload(w.name + "_i8", w.rows, w.cols, w.row_ptr, w.col_ind, i8(n), i8(w.cols),
+                          torch.randint(-1000, 1000, (w.rows,), generator=g, device=w.values.device,
+                                        dtype=torch.int32), 2, 1, out_dtype=torch.int32),
+        "c2_c64": Workload(w.name + "_c64", w.rows, w.cols, w.row_ptr, w.col_ind, c64(w.values), c64(w.x),
+                           c64(w.y0), 1.5, 0.5, out_dtype=torch.complex64),
+    }
+    return out
+
+
 def make(name, dev):
     from ops_sparse import workloads as wl
 
@@ -307,6 +335,17 @@ def main():
         results[name] = r
         if name == "c2":
             headline_w, headline = w, r
+            if not args.only_headline:
+                for key, v in dtype_variants(w).items():
+                    mv = measure(v, args.steps, args.warmup, flush_buf)
+                    vb = algorithmic_bytes(v)
+                    results[key] = dict(workload=v.name, rows=v.rows, nnz=v.nnz, op=v.trans,
+                                        dtype=str(v.values.dtype).split(".")[-1], algorithmic_bytes=vb,
+                                        gbs=vb / (mv["median_ms"] * 1e-3) / 1e9,
+                                        frac=vb / (mv["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                        median_ms=mv["median_ms"], p90_ms=mv["p90_ms"], warm_ms=mv["warm_ms"],
+                                        preprocess_ms=mv["preprocess_ms"])
+                    del v
             from ops_sparse._lib import SpMVOpAlg
             for alg in (SpMVOpAlg.ALG1, SpMVOpAlg.ALG2):
                 t, setup = measure_spmvop(w, alg, args.steps, args.warmup, flush_buf)
