@@ -728,6 +728,13 @@ __device__ __forceinline__ void WaveLdsSync() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ float ReadLane(float v, int l) { return __shfl(v, l, kWave); }
 __device__ __forceinline__ long long ReadLane(long long v, int l) { return __shfl(v, l, kWave); }
 __device__ __forceinline__ C64 ReadLane(C64 v, int l) { return C64{__shfl(v.re, l, kWave), __shfl(v.im, l, kWave)}; }
+__device__ __forceinline__ float ShflXorAcc(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ long long ShflXorAcc(long long v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
+{
+    return C64{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
+}
+
 
 template <typename RowT, ValKind V, OutKind O, AccKind A, bool kBeta>
 __global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvWaveKernel(RowBlockParams p)
@@ -1538,6 +1545,256 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     }
 }
 
+// --------------- stream kernel for int8 and complex64 operands ---------------
+//
+// The stream kernel's row blocks, chunk loads (16-byte col_ind groups, value
+// loads clipped to the chunk) and gathers, for operands whose accumulator is
+// not fp32: int8 values and x summed exactly in int64 (int32 output, with the
+// reference's saturating epilogue), and complex64.  Products go to LDS in the
+// accumulator type; rows are reduced by one lane, a lane group or the whole
+// wave as in the fp32 kernel, without the fp32 kernel's tasks (a long block is
+// processed chunk by chunk by its own wave).
+
+template <ValKind V, AccKind A>
+struct GenLoad {
+    v4i col[2];
+    // values of the 8 slots: int8 -> 2 words of 4 bytes; complex64 -> 4 x 16 bytes
+    typename std::conditional<V == ValKind::I8, uint32_t[2], v4f[4]>::type val;
+    int64_t rp[2];
+    typename AccOf<A>::T xg[kLaneItems];
+};
+
+template <typename RowT, ValKind V, AccKind A>
+__device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
+                                             __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b)
+{
+    using ValT = typename ValOf<V>::T;
+    const int64_t a0 = s.valid ? s.a0 : 0;
+    int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
+    end = end < tailStart ? end : tailStart;
+    const int64_t avail = s.valid ? end - a0 : 0;
+    const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
+    const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
+    b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
+    b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    if constexpr (V == ValKind::I8) {
+        b.val[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
+        b.val[1] = __builtin_amdgcn_raw_buffer_load_b32(rv, 256 + lane * 4, 0, kBufNonTemporal);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int off = (q >> 1) * 2048 + lane * 32 + (q & 1) * 16;
+            b.val[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kBufNonTemporal));
+        }
+    }
+    const int64_t r0 = s.valid ? s.r0 : 0;
+    const int64_t nrp = s.valid ? ((s.nr + 2) & ~1) : 0;
+    const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
+    if constexpr (sizeof(RowT) == 8) {
+        const v4i w = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, kRowPolicy));
+        b.rp[0] = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(w.y)) << 32) |
+                                       static_cast<uint32_t>(w.x));
+        b.rp[1] = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(w.w)) << 32) |
+                                       static_cast<uint32_t>(w.z));
+    } else {
+        const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rr, lane * 8, 0, kRowPolicy));
+        b.rp[0] = w.x;
+        b.rp[1] = w.y;
+    }
+    // the last nnz % 4 entries (no whole 16-byte group): scalar loads, only
+    // in the chunk that reaches them
+    if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            const int64_t k = s.a0 + StreamSlot(lane, j);
+            if (k >= tailStart && k < p.nnz) {
+                b.col[j >> 2][j & 3] = p.col[k];
+                const ValT v = static_cast<const ValT*>(p.val)[k];
+                if constexpr (V == ValKind::I8) {
+                    const uint32_t sh = 8U * static_cast<uint32_t>(j & 3);
+                    b.val[j >> 2] = (b.val[j >> 2] & ~(0xFFU << sh)) | (static_cast<uint32_t>(static_cast<uint8_t>(v)) << sh);
+                } else {
+                    b.val[j >> 1][(j & 1) * 2] = v.re;
+                    b.val[j >> 1][(j & 1) * 2 + 1] = v.im;
+                }
+            }
+        }
+    }
+    const int32_t hiSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c1 - s.a0) : 0;
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) {
+        uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
+        off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+        if constexpr (V == ValKind::I8) {
+            const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b8(rx, static_cast<int>(off), 0, kGatherPolicy);
+            b.xg[j] = static_cast<long long>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
+        } else {
+            const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0,
+                                                                                     kGatherPolicy));
+            b.xg[j] = C64{w.x, w.y};
+        }
+    }
+}
+
+template <ValKind V, AccKind A>
+__device__ __forceinline__ typename AccOf<A>::T GenVal(const GenLoad<V, A>& b, int j)
+{
+    if constexpr (V == ValKind::I8) {
+        return static_cast<long long>(static_cast<int8_t>((b.val[j >> 2] >> (8 * (j & 3))) & 0xFFU));
+    } else {
+        return C64{b.val[j >> 1][(j & 1) * 2], b.val[j >> 1][(j & 1) * 2 + 1]};
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T WaveAllSum(T v)
+{
+    for (int m = 1; m < kWave; m <<= 1) v = v + ShflXorAcc(v, m);
+    return v;
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& cur, const GenLoad<V, A>& lc,
+                                         typename AccOf<A>::T* sVal, int lane, typename AccOf<A>::T alpha,
+                                         typename AccOf<A>::T beta, bool betaNz, typename AccOf<A>::T& carry, int& lg)
+{
+    using Acc = typename AccOf<A>::T;
+    using OutT = typename OutOf<O>::T;
+    Acc prod[kLaneItems];
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) prod[j] = GenVal<V, A>(lc, j) * lc.xg[j];
+    const int32_t c0 = cur.c0, c1 = cur.c1;
+    const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);
+    const int nr = cur.nr;
+    if (cur.first) {
+        carry = Zero<Acc>();
+        lg = 0;
+        if (cur.last) {
+            while (lg < 6 && (nr << (lg + 1)) <= kWave) ++lg;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kLaneItems; ++j) sVal[StreamSlot(lane, j)] = prod[j];
+
+    const int32_t k0lo = static_cast<int32_t>(cur.k0);
+    int32_t rs[2], re[2];
+    rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
+    rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
+    re[0] = rs[1];
+    re[1] = FromNextLane(rs[0], rs[1]);
+    const int gsz = 1 << lg;
+    const int cap = SerialCap(lg);
+    bool fin[2], defer[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = 2 * lane + h;
+        const bool in = i < nr;
+        const bool empty = re[h] <= rs[h];
+        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                         : (rs[h] < c1 && re[h] > c0));
+        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
+        defer[h] = active && (crosses || re[h] - rs[h] > cap);
+        fin[h] = active && !defer[h];
+    }
+    WaveLdsSync();
+
+    Acc sum[2] = {Zero<Acc>(), Zero<Acc>()};
+    if (lg == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
+            const int32_t base = fin[h] ? rs[h] - shift : 0;
+            Acc acc = Zero<Acc>();
+#pragma unroll
+            for (int t = 0; t < kSerialCapOne; ++t) {
+                const Acc v = sVal[base + t];
+                acc = acc + (t < len ? v : Zero<Acc>());
+            }
+            sum[h] = acc;
+        }
+    } else {
+        const int g = lane >> lg;
+        const int sub = lane & (gsz - 1);
+        const bool in = g < nr;
+        const int src = (g >> 1) & (kWave - 1);
+        const int32_t a0s = __shfl(rs[0], src, kWave), a1s = __shfl(rs[1], src, kWave);
+        const int32_t a1e = __shfl(re[1], src, kWave);
+        const int32_t gs = (g & 1) ? a1s : a0s;
+        const int32_t ge = (g & 1) ? a1e : a1s;
+        Acc part = Zero<Acc>();
+        if (in && ge - gs <= cap) {
+            for (int32_t q = gs + sub; q < ge; q += gsz) part = part + sVal[q - shift];
+        }
+        for (int m = 1; m < gsz; m <<= 1) part = part + ShflXorAcc(part, m);
+        sum[0] = ReadLane(part, ((2 * lane) << lg) & (kWave - 1));
+        sum[1] = ReadLane(part, ((2 * lane + 1) << lg) & (kWave - 1));
+    }
+
+    uint64_t pending0 = __ballot(defer[0]), pending1 = __ballot(defer[1]);
+    while (pending0 | pending1) {
+        const int l0 = pending0 ? __builtin_ctzll(pending0) : kWave;
+        const int l1 = pending1 ? __builtin_ctzll(pending1) : kWave;
+        const int h = (2 * l1 + 1 < 2 * l0) ? 1 : 0;
+        const int l = h ? l1 : l0;
+        if (h) {
+            pending1 &= pending1 - 1;
+        } else {
+            pending0 &= pending0 - 1;
+        }
+        const int32_t s0 = __builtin_amdgcn_readlane(h ? rs[1] : rs[0], l);
+        const int32_t e0 = __builtin_amdgcn_readlane(h ? re[1] : re[0], l);
+        const int32_t lo = s0 > c0 ? s0 : c0;
+        const int32_t hi = e0 < c1 ? e0 : c1;
+        Acc part = Zero<Acc>();
+        for (int32_t q = lo + lane; q < hi; q += kWave) part = part + sVal[q - shift];
+        Acc total = WaveAllSum(part);
+        if (s0 < c0) total = carry + total;
+        if (e0 > c1) {
+            carry = total;
+        } else if (lane == l) {
+            sum[h] = total;
+            fin[h] = true;
+        }
+    }
+    OutT* y = static_cast<OutT*>(p.y);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (fin[h]) StoreRow<O, A>(y, cur.r0 + 2 * lane + h, sum[h], alpha, beta, betaNz);
+    }
+    WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+__global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    __shared__ Acc sValAll[kFlatWaves][kStreamLds];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    Acc alpha, beta;
+    LoadScalars<A>(p.s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
+    const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
+    const int64_t wg = static_cast<int64_t>(blockIdx.x);
+    const int64_t per = static_cast<int64_t>(gridDim.x) / kXcds;
+    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
+    if (tile >= p.num_blocks) return;
+    Stage cur = OpenTileFlat<RowT>(p, tile);
+    Acc carry = Zero<Acc>();
+    int lg = 0;
+    while (cur.valid) {
+        GenLoad<V, A> b;
+        GenLoadStage<RowT, V, A>(p, cur, tailStart, lane, rx, b);
+        GenChunk<RowT, V, O, A>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
+        if (cur.last) break;
+        cur.c0 = cur.c1;
+        cur.first = false;
+        ChunkBounds(cur);
+    }
+}
+
 // ------------------------ SpMVOp on the row blocks ---------------------------
 //
 // z = alpha*(A*x) + beta*y with Priest's doubly compensated dot product, on
@@ -1883,12 +2140,6 @@ __global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPo
     }
 }
 
-__device__ __forceinline__ float ShflXorAcc(float v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ __forceinline__ long long ShflXorAcc(long long v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
-{
-    return C64{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
-}
 
 struct CscParams {
     const void* colptr;  // RowT[cols+1]
@@ -2002,7 +2253,11 @@ template <typename SrcT>
 __global__ __launch_bounds__(kThreads) void SpmvPreprocessKernel(PrepParams p)
 {
     const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
-    if (i <= p.rows) static_cast<SrcT*>(p.norm)[i] = static_cast<SrcT>(NormRow<SrcT>(p, i));
+    if (i <= p.rows) {
+        const SrcT v = static_cast<SrcT>(NormRow<SrcT>(p, i));
+        static_cast<SrcT*>(p.norm)[i] = v;
+        if (i == p.rows) static_cast<SrcT*>(p.norm)[i + 1] = v;  // pad entry (offsets are read in pairs)
+    }
     if (i <= p.num_blocks) {
         int32_t start;
         if (i == p.num_blocks) {
@@ -2178,6 +2433,20 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kFlatWaves),
                                    0, stream_, p);
             }
+            return 0;
+        }
+    }
+    if constexpr ((V == ValKind::I8 && A == AccKind::I64) || (V == ValKind::C64 && A == AccKind::C64)) {
+        // int8 -> int32 and complex64 on the stream kernel's row blocks
+        const bool gen = l.nnz > 0 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && l.y_stride == 1 &&
+                         Aligned16(l.col) && Aligned16(l.val) &&
+                         static_cast<int64_t>(l.cols) * static_cast<int64_t>(sizeof(typename ValOf<V>::T)) <=
+                             0x7FFFFFFFLL;
+        if (gen) {
+            const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
+            const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+            hipLaunchKernelGGL((SpmvStreamGenKernel<RowT, V, O, A>), dim3(g), dim3(kWave * kFlatWaves), 0, stream_,
+                               p);
             return 0;
         }
     }

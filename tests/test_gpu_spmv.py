@@ -463,3 +463,61 @@ def test_long_rows_split_into_tasks(i64, dtype, beta, dev):
         plan.run()
         torch.cuda.synchronize()
         assert_close(w, y)
+
+
+def _mixed_lengths(seed, tail):
+    """Short, medium, empty and multi-chunk rows, nnz % 4 == tail (exact lengths, repeats allowed)."""
+    g = torch.Generator().manual_seed(seed)
+    body = torch.randint(0, 10, (6000,), generator=g)
+    body[::211] = torch.randint(300, 2500, (body[::211].numel(),), generator=g)
+    lengths = torch.cat([body.to(torch.int64), torch.tensor([0, 1, 5000, 3], dtype=torch.int64)])
+    extra = (tail - int(lengths.sum()) % 4) % 4
+    lengths[-1] += extra
+    cols = 3000
+    rp, col = wl.csr_from_lengths(lengths, cols, g, "cpu", distinct=False)
+    assert col.numel() % 4 == tail
+    return g, lengths.numel(), cols, rp, col
+
+
+@pytest.mark.parametrize("tail", [0, 3])
+@pytest.mark.parametrize("i64", [False, True])
+def test_int8_stream_rows_bit_exact(tail, i64, dev):
+    """int8 values and x, int32 output (int64 accumulation, saturating epilogue) on the row-block
+    stream kernel: bit-exact against the oracle, including alpha/beta and int32 saturation."""
+    g, rows, cols, rp, col = _mixed_lengths(40 + tail, tail)
+    n = col.numel()
+    v8 = torch.randint(-128, 128, (n,), generator=g, dtype=torch.int8)
+    x8 = torch.randint(-128, 128, (cols,), generator=g, dtype=torch.int8)
+    y0 = torch.randint(-2 ** 31, 2 ** 31 - 1, (rows,), generator=g, dtype=torch.int64).to(torch.int32)
+    for alpha, beta in ((3, -2), (70000, 1), (1, 0)):
+        y = y0.to(dev).clone()
+        plan = CsrSpMV(rows, cols, rp.to(torch.int64 if i64 else torch.int32).to(dev), col.to(dev), v8.to(dev),
+                       x8.to(dev), y, alpha, beta)
+        plan.preprocess()
+        plan.run()
+        torch.cuda.synchronize()
+        ref = oracle.spmv_i8(rp.numpy(), col.numpy(), v8.numpy(), x8.numpy(), y0.numpy(), alpha, beta, cols=cols)
+        np.testing.assert_array_equal(y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("tail", [1, 2])
+def test_complex64_stream_rows(tail, dev):
+    """complex64 values, x and y on the row-block stream kernel, against the fp64 oracle."""
+    g, rows, cols, rp, col = _mixed_lengths(50 + tail, tail)
+    n = col.numel()
+    cplx = lambda k: torch.complex(torch.rand(k, generator=g) * 2 - 1, torch.rand(k, generator=g) * 2 - 1)
+    v, x, y0 = cplx(n), cplx(cols), cplx(rows)
+    alpha, beta = complex(1.5, -0.25), complex(0.5, 0.75)
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(rows, cols, rp.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta)
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    ref = oracle.spmv_c64(rp.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), cols, 0, alpha, beta)
+    # row scale |alpha| * sum |a||x| + |beta y|
+    rpn = rp.numpy()
+    absprod = np.abs(v.numpy()) * np.abs(x.numpy())[col.numpy()]
+    scale = abs(alpha) * np.add.reduceat(np.append(absprod, 0.0), rpn[:-1]) * (np.diff(rpn) > 0) + \
+        abs(beta) * np.abs(y0.numpy())
+    err = np.abs(y.cpu().numpy().astype(np.complex128) - ref) / np.maximum(scale, 1e-30)
+    assert err.max() <= 1e-5, float(err.max())
