@@ -1049,17 +1049,23 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     int64_t ny = s.valid ? s.nr : 0;
     if (ny > p.rows - r0) ny = p.rows - r0;
     const __amdgpu_buffer_rsrc_t ry = Rsrc(static_cast<const OutT*>(p.y) + r0, ny * sizeof(OutT));
+    if constexpr (kBeta && sizeof(OutT) == 4) {
+        // both rows of the lane in one 8-byte load; buffer range checks are
+        // per dword, so a row past the block reads 0 (and is never used)
+        // (loaded as a float2: taking __builtin_bit_cast(float, ...) of the
+        // elements of an int2 load makes this hipcc emit a one-dword load)
+        const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(ry, lane * 8, 0, kRowPolicy));
+        b.yold[0] = w.x;
+        b.yold[1] = w.y;
+    } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = 2 * lane + h;
-        if constexpr (kBeta) {
-            if constexpr (sizeof(OutT) == 4) {
-                b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b32(ry, i * 4, 0, kRowPolicy));
-            } else {
+        for (int h = 0; h < 2; ++h) {
+            const int i = 2 * lane + h;
+            if constexpr (kBeta) {
                 b.yold[h] = __builtin_bit_cast(OutT, __builtin_amdgcn_raw_buffer_load_b16(ry, i * 2, 0, kRowPolicy));
+            } else {
+                b.yold[h] = OutT{};
             }
-        } else {
-            b.yold[h] = OutT{};
         }
     }
 }
@@ -1353,16 +1359,34 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         }
     }
 
+    float r[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int i = 2 * lane + h;
-        float r = alpha * sum[h];
+        r[h] = alpha * sum[h];
         // beta == 0 (possible at run time with device scalars) never reads y
         if constexpr (kBeta) {
-            if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
+            if (beta != 0.0f) r[h] += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
         }
-        OutT* dst = fin[h] ? y + (cur.r0 + i) : sink + h * kWave;
-        *dst = FromAcc<O, AccKind::F32>(r);
+    }
+    // When every row of the block that this chunk touches finishes here (one-
+    // chunk blocks), each lane stores its two rows with one 8-byte buffer
+    // store; the range check (per dword) drops rows past the block.
+    bool pair = false;
+    if constexpr (sizeof(OutT) == 4) {
+        const bool ok = (fin[0] || 2 * lane >= nr) && (fin[1] || 2 * lane + 1 >= nr);
+        pair = __ballot(!ok) == 0;
+    }
+    if (pair) {
+        const __amdgpu_buffer_rsrc_t rys = Rsrc(y + cur.r0, static_cast<int64_t>(nr) * 4);
+        const v2i w = {__float_as_int(r[0]), __float_as_int(r[1])};
+        __builtin_amdgcn_raw_buffer_store_b64(w, rys, lane * 8, 0, 0);
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = 2 * lane + h;
+            OutT* dst = fin[h] ? y + (cur.r0 + i) : sink + h * kWave;
+            *dst = FromAcc<O, AccKind::F32>(r[h]);
+        }
     }
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 }
