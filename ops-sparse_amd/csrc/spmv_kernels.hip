@@ -2240,8 +2240,20 @@ __global__ __launch_bounds__(kThreads) void SpmvCscGatherKernel(CscParams q)
     Acc sum = Zero<Acc>();
     if (c < q.cols) {
         const int64_t k1 = static_cast<int64_t>(colptr[c + 1]);
-        for (int64_t k = static_cast<int64_t>(colptr[c]) + sub; k < k1; k += g) {
-            sum = sum + prod[static_cast<int64_t>(pos[k])];
+        // batches of 4 entries per lane: the 4 position loads, then the 4
+        // product reads, are in flight together; the sum keeps entry order
+        constexpr int kB = 4;
+        for (int64_t k0 = static_cast<int64_t>(colptr[c]) + sub; k0 < k1; k0 += kB * g) {
+            int64_t pk[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) pk[u] = k0 + u * g < k1 ? static_cast<int64_t>(pos[k0 + u * g]) : -1;
+            Acc v[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) v[u] = pk[u] >= 0 ? prod[pk[u]] : Zero<Acc>();
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (pk[u] >= 0) sum = sum + v[u];
+            }
         }
     }
     for (int m = 1; m < g; m <<= 1) sum = sum + ShflXorAcc(sum, m);
