@@ -18,9 +18,10 @@
 //    (long rows, with a carried partial sum).  The first workgroups serve the
 //    long-block tasks; the last task of a block combines the partial sums of
 //    the rows that cross its chunks.  Replaces the warp-per-row kernel
-//    sparse/spmv/arch35/spmv_kernel.cpp:501-577.  Real A with complex x/y
-//    (SpmvWaveKernel) and strided or int8/complex operands
-//    (SpmvRowBlockKernel) use the general kernels below.
+//    sparse/spmv/arch35/spmv_kernel.cpp:501-577.  int8 and complex operands
+//    (and real A with complex y) run on the same row blocks and chunk loads
+//    with an int64 / complex accumulator (SpmvStreamGenKernel); strided or
+//    unaligned operands use the general LDS-scan kernel (SpmvRowBlockKernel).
 //  * Transpose: Preprocess builds a CSC pattern (radix sort of (column,
 //    position) pairs); each SpMV streams the products a_k*x_row(k) in CSR
 //    order and then sums every column's products in a fixed order
@@ -35,9 +36,6 @@
 
 #include <cstdint>
 #include <cstdlib>
-#include <map>
-#include <string>
-#include <mutex>
 #include <type_traits>
 
 #include "aclsparse_internal.h"
@@ -282,11 +280,6 @@ struct RowBlockParams {
     int32_t base;
     int32_t conj;
     Scalars s;
-    // persistent scheduling: worker w serves XCD (w % 8) and walks that XCD's
-    // contiguous block range [xcd*per_xcd, (xcd+1)*per_xcd) with stride
-    // workers_per_xcd.
-    int64_t per_xcd;
-    int32_t workers_per_xcd;
     void* sink;  // per-lane dummy outputs
     // long-block tasks (see SpmvLayout): tables built by Preprocess
     const int32_t* task_start;
@@ -536,29 +529,19 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
 }
 
 
-// ------------------- wave-per-block persistent kernel --------------------
+// ------------------------ wave-per-block stream kernels ---------------------
 //
-// One wave64 owns one row block at a time (<= 127 rows, ~500 non-zeros) and
-// reduces it without any workgroup barrier: lane l holds the 8 consecutive
-// non-zeros [8l, 8l+8) of the chunk (two 16-byte non-temporal loads), forms
-// the products in registers, runs a lane-local segmented scan, then a 6-step
-// shuffle scan carries partial rows across lanes.  Row-start flags, the
-// block's row offsets and the finished prefixes go through a private
-// per-wave LDS slice.  The waves of a workgroup are independent persistent
-// workers; each keeps the x gathers of its next chunk and the col/values/
-// row-offset/y loads of the chunk after that in flight while it reduces the
-// current one.
+// One wave64 owns one row block (<= 127 rows, ~500 non-zeros) at a time and
+// reads it in chunks of 512 slots, 8 per lane.
 
 constexpr int kWaveChunk = static_cast<int>(kChunkNnz);  // 512 slots, 8 per lane
 constexpr int kLaneItems = kWaveChunk / kWave;           // 8
 constexpr int kWaveRows = static_cast<int>(kMaxRowsPerBlock);
-constexpr int kWavesPerGroup = 4;
-// Waves per workgroup of the flat stream kernel (1 and 2 measured slower on
-// the power-law and fp16 matrices, equal on the Laplacian).
+// Waves per workgroup of the stream kernels (1 and 2 measured slower on the
+// power-law and fp16 matrices, equal on the Laplacian).
 constexpr int kFlatWaves = 4;
-constexpr int kWavePadded = kWaveChunk + kWaveChunk / kLaneItems;
 
-static_assert(kLaneItems == 8, "lane scan is written for 8 items per lane");
+static_assert(kLaneItems == 8, "the reductions are written for 8 slots per lane");
 static_assert(kWaveRows <= 2 * kWave - 1, "two rows per lane");
 
 struct Stage {
@@ -591,131 +574,6 @@ __device__ __forceinline__ T ConstLoad(const void* base, int64_t i)
     return reinterpret_cast<CPtr>(reinterpret_cast<uintptr_t>(base))[i];
 }
 
-// Opens the ordinal-th block of this worker (block first + ordinal*stride).
-template <typename RowT>
-__device__ __forceinline__ Stage OpenTile(const RowBlockParams& p, int64_t ordinal, int64_t first, int64_t stride,
-                                          int64_t tileEnd)
-{
-    Stage s{};
-    s.tile = ordinal;
-    const int64_t t = first + ordinal * stride;
-    s.valid = t < tileEnd;
-    if (!s.valid) return s;
-    s.r0 = ConstLoad<int32_t>(p.blocks, t);
-    const int64_t n = static_cast<int64_t>(ConstLoad<int32_t>(p.blocks, t + 1)) - s.r0;
-    s.nr = static_cast<int32_t>(n < 0 ? 0 : n > kWaveRows ? kWaveRows : n);
-    s.k0 = static_cast<int64_t>(ConstLoad<RowT>(p.block_nnz, t));
-    const int64_t span = static_cast<int64_t>(ConstLoad<RowT>(p.block_nnz, t + 1)) - s.k0;
-    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
-    s.c0 = 0;
-    s.first = true;
-    ChunkBounds(s);
-    return s;
-}
-
-template <typename RowT>
-__device__ __forceinline__ Stage NextStage(const RowBlockParams& p, const Stage& s, int64_t first, int64_t stride,
-                                           int64_t tileEnd)
-{
-    if (!s.valid) return s;
-    if (!s.last) {
-        Stage n = s;
-        n.c0 = s.c1;
-        n.first = false;
-        ChunkBounds(n);
-        return n;
-    }
-    return OpenTile<RowT>(p, s.tile + 1, first, stride, tileEnd);
-}
-
-// Register bundle of one chunk for one lane: slots [8l, 8l+8) and rows l, l+64.
-template <typename RowT, ValKind V, OutKind O>
-struct Bundle {
-    int32_t col[kLaneItems];
-    typename ValOf<V>::T val[kLaneItems];
-    RowT rp[2];
-    typename OutOf<O>::T yold[2];
-};
-
-// The last nnz % 4 entries of col_ind / values, which a 16-byte load
-// cannot fetch without reading past the arrays.
-template <ValKind V>
-struct ArrayTail {
-    int64_t start;  // nnz rounded down to a multiple of 4
-    int32_t col[3];
-    typename ValOf<V>::T val[3];
-};
-
-// Every load is issued unconditionally (clamped to valid addresses) so the
-// compiler's wait-counter bookkeeping stays exact across loop iterations:
-// a conditional load here would make it wait for the whole prefetch queue.
-template <typename RowT, ValKind V, OutKind O, bool kBeta>
-__device__ __forceinline__ void LoadStage(const RowBlockParams& p, const Stage& s, const ArrayTail<V>& tail,
-                                          int lane, Bundle<RowT, V, O>& b)
-{
-    using ValT = typename ValOf<V>::T;
-    const ValT* val = static_cast<const ValT*>(p.val);
-    const int64_t g0 = s.valid ? s.a0 + kLaneItems * lane : 0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int64_t g = g0 + 4 * h;
-        const int64_t gv = g + 4 <= tail.start ? g : 0;  // a vector that would cross the end re-reads [0,4)
-        Load4<V>(p.col, val, gv, &b.col[4 * h], &b.val[4 * h]);
-    }
-    const RowT* rp = static_cast<const RowT*>(p.rp);
-    const int lastRow = s.nr > 0 ? s.nr - 1 : 0;
-    const int64_t r0 = s.valid ? s.r0 : 0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = lane + h * kWave;
-        b.rp[h] = rp[r0 + (i <= s.nr ? i : s.nr)];  // row offsets have rows+1 entries
-        if constexpr (kBeta) {
-            // a block can start at row == rows (past a long last row): clamp into y
-            int64_t yi = r0 + (i <= lastRow ? i : lastRow);
-            yi = yi < p.rows ? yi : p.rows - 1;
-            const typename OutOf<O>::T* y = static_cast<const typename OutOf<O>::T*>(p.y);
-            b.yold[h] = y[yi * p.y_stride];
-        }
-    }
-}
-
-// Issues the x gathers of a loaded chunk; slots outside the chunk or with an
-// out-of-range column gather x[0] and are masked to contribute exactly zero.
-template <typename RowT, ValKind V, OutKind O>
-__device__ __forceinline__ void GatherStage(const RowBlockParams& p, const Stage& s, const ArrayTail<V>& tail,
-                                            int lane, Bundle<RowT, V, O>& b, typename ValOf<V>::T xg[kLaneItems])
-{
-    using ValT = typename ValOf<V>::T;
-    const ValT* x = static_cast<const ValT*>(p.x);
-    const int64_t gStart = s.k0 + s.c0, gEnd = s.valid ? s.k0 + s.c1 : gStart;
-#pragma unroll
-    for (int j = 0; j < kLaneItems; ++j) {
-        const int64_t g = s.a0 + kLaneItems * lane + j;
-        // entries of the array tail were not covered by the 16-byte loads
-        const int64_t k = g - tail.start;
-        const bool inTail = k >= 0 && k < 3;
-        const int kk = inTail ? static_cast<int>(k) : 0;
-        const int32_t colv = inTail ? (kk == 0 ? tail.col[0] : kk == 1 ? tail.col[1] : tail.col[2]) : b.col[j];
-        if (inTail) b.val[j] = kk == 0 ? tail.val[0] : kk == 1 ? tail.val[1] : tail.val[2];
-        const int64_t c = static_cast<int64_t>(colv) - p.base;
-        const bool ok = g >= gStart && g < gEnd && c >= 0 && c < p.cols;
-        b.col[j] = ok ? 1 : 0;  // the column is dead after the gather; keep the validity bit
-        xg[j] = x[ok ? c : 0];
-    }
-}
-
-template <typename RowT, ValKind V, OutKind O, AccKind A>
-__device__ __forceinline__ void Products(const Bundle<RowT, V, O>& b, const typename ValOf<V>::T xg[kLaneItems],
-                                         typename AccOf<A>::T prod[kLaneItems])
-{
-#pragma unroll
-    for (int j = 0; j < kLaneItems; ++j) {
-        prod[j] = b.col[j] ? ToAcc<V, A>(b.val[j]) * ToAcc<V, A>(xg[j]) : Zero<typename AccOf<A>::T>();
-    }
-}
-
-// Orders this wave's LDS accesses (LDS ops of one wave complete in order;
-// the clobber keeps the compiler from moving accesses across the wait).
 // LDS byte address of a pointer into __shared__ memory (for inline asm).
 __device__ __forceinline__ uint32_t LdsAddr(const float* p)
 {
@@ -735,182 +593,6 @@ __device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
     return C64{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
 }
 
-
-template <typename RowT, ValKind V, OutKind O, AccKind A, bool kBeta>
-__global__ __launch_bounds__(kWave* kWavesPerGroup) void SpmvWaveKernel(RowBlockParams p)
-{
-    using Acc = typename AccOf<A>::T;
-    using ValT = typename ValOf<V>::T;
-    using OutT = typename OutOf<O>::T;
-    using B = Bundle<RowT, V, O>;
-
-    __shared__ int32_t sRpAll[kWavesPerGroup][kWaveRows + 1];
-    __shared__ Acc sValAll[kWavesPerGroup][kWavePadded];
-    __shared__ uint32_t sFlagAll[kWavesPerGroup][kWaveChunk / 32];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    // The wave index is uniform within a wave; say so, so that all block
-    // bookkeeping stays in scalar registers.
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    int32_t* sRp = sRpAll[wv];
-    Acc* sVal = sValAll[wv];
-    uint32_t* sFlag = sFlagAll[wv];
-
-    const int64_t xcd = blockIdx.x % kXcds;
-    const int64_t worker = (blockIdx.x / kXcds) * kWavesPerGroup + wv;
-    const int64_t tileBegin = xcd * p.per_xcd;
-    int64_t tileEnd = tileBegin + p.per_xcd;
-    if (tileEnd > p.num_blocks) tileEnd = p.num_blocks;
-    const int64_t stride = p.workers_per_xcd;
-    const int64_t firstTile = tileBegin + worker;
-
-    Acc alpha, beta;
-    LoadScalars<A>(p.s, alpha, beta);
-    OutT* y = static_cast<OutT*>(p.y);
-    OutT* sink = static_cast<OutT*>(p.sink) + lane;
-
-    ArrayTail<V> tail;
-    tail.start = p.nnz & ~static_cast<int64_t>(3);
-#pragma unroll
-    for (int e = 0; e < 3; ++e) {
-        const int64_t k = tail.start + e < p.nnz ? tail.start + e : (p.nnz > 0 ? p.nnz - 1 : 0);
-        tail.col[e] = p.nnz > 0 ? ConstLoad<int32_t>(p.col, k) : 0;
-        tail.val[e] = p.nnz > 0 ? ConstLoad<ValT>(p.val, k) : ValT{};
-    }
-
-    // Prologue: chunk 0 loaded and gathered, chunk 1 loaded.
-    Stage cur = OpenTile<RowT>(p, 0, firstTile, stride, tileEnd);
-    if (!cur.valid) return;
-    B bc, bn;
-    ValT xg[kLaneItems];
-    LoadStage<RowT, V, O, kBeta>(p, cur, tail, lane, bc);
-    GatherStage<RowT, V, O>(p, cur, tail, lane, bc, xg);
-    Stage nxt = NextStage<RowT>(p, cur, firstTile, stride, tileEnd);
-    LoadStage<RowT, V, O, kBeta>(p, nxt, tail, lane, bn);
-    Acc prod[kLaneItems];
-    Products<RowT, V, O, A>(bc, xg, prod);
-    RowT rpc[2] = {bc.rp[0], bc.rp[1]};
-    OutT yc[2] = {bc.yold[0], bc.yold[1]};
-    Acc chunkCarry = Zero<Acc>();
-
-    while (cur.valid) {
-        // Keep two chunks of memory traffic in flight while this one reduces.
-        GatherStage<RowT, V, O>(p, nxt, tail, lane, bn, xg);
-        const Stage after = NextStage<RowT>(p, nxt, firstTile, stride, tileEnd);
-        B ba;
-        LoadStage<RowT, V, O, kBeta>(p, after, tail, lane, ba);
-
-        const int32_t c0 = cur.c0, c1 = cur.c1;
-        const int32_t d = static_cast<int32_t>(cur.k0 - cur.a0);  // slot of relative offset r is r + d
-        const int nr = cur.nr;
-        if (cur.first) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int i = lane + h * kWave;
-                if (i <= nr) {
-                    int64_t v = static_cast<int64_t>(rpc[h]) - cur.k0;
-                    sRp[i] = static_cast<int32_t>(v < 0 ? 0 : v > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : v);
-                }
-            }
-            chunkCarry = Zero<Acc>();
-        }
-        if (lane < kWaveChunk / 32) sFlag[lane] = 0U;
-        WaveLdsSync();
-        // Segment heads: first non-zero of each non-empty row that starts here.
-        int32_t rs[2], re[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int i = lane + h * kWave;
-            rs[h] = i < nr ? sRp[i] : 0;
-            re[h] = i < nr ? sRp[i + 1] : 0;
-            if (i < nr && re[h] > rs[h] && rs[h] >= c0 && rs[h] < c1) {
-                const int q = rs[h] + d;
-                atomicOr(&sFlag[q >> 5], 1U << (q & 31));
-            }
-        }
-        WaveLdsSync();
-        const uint32_t bits = (sFlag[lane >> 2] >> ((lane & 3) * 8)) & 0xFFU;
-
-        // Lane-local segmented scan of slots [8l, 8l+8).
-        Acc pre[kLaneItems];
-        Acc run = Zero<Acc>();
-#pragma unroll
-        for (int j = 0; j < kLaneItems; ++j) {
-            if (bits & (1U << j)) run = Zero<Acc>();
-            run = run + prod[j];
-            pre[j] = run;
-        }
-        const int firstHead = bits ? __builtin_ctz(bits) : kLaneItems;
-        // Wave-wide exclusive segmented scan of the lane tails (carry-in from
-        // the previous chunk of the same block enters at lane 0).
-        Acc v = run;
-        int f = bits ? 1 : 0;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const Acc vo = ShflUp(v, off);
-            const int fo = __shfl_up(f, off, kWave);
-            if (lane >= off) {
-                if (!f) v = vo + v;
-                f |= fo;
-            }
-        }
-        Acc ve = ShflUp(v, 1);
-        int fe = __shfl_up(f, 1, kWave);
-        if (lane == 0) {
-            ve = Zero<Acc>();
-            fe = 0;
-        }
-        const Acc carryIn = fe ? ve : chunkCarry + ve;
-        // Finished prefixes: slots before the first head continue the row
-        // that entered this lane.
-#pragma unroll
-        for (int j = 0; j < kLaneItems; ++j) {
-            sVal[kLaneItems * lane + j + lane] = j < firstHead ? pre[j] + carryIn : pre[j];
-        }
-        const Acc inclusive = f ? v : chunkCarry + v;
-        chunkCarry = ReadLane(inclusive, kWave - 1);
-        WaveLdsSync();
-
-        // Rows that end inside this chunk (lane owns rows l and l+64).  Lanes
-        // without a finished row store into the sink, so the store is
-        // unconditional.
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int i = lane + h * kWave;
-            const int32_t s0 = rs[h], e0 = re[h];
-            const bool inRange = i < nr;
-            const bool empty = e0 <= s0;
-            const bool endsHere = !empty && e0 > c0 && e0 <= c1;
-            const bool done = inRange && ((empty && ((s0 >= c0 && s0 < c1) || (cur.last && s0 >= c1))) || endsHere);
-            const int q = endsHere ? e0 - 1 + d : 0;
-            Acc sum = sVal[q + q / kLaneItems];
-            if (!endsHere) sum = Zero<Acc>();
-            Acc r;
-            if constexpr (A == AccKind::I64) {
-                r = ScaledI64(sum, alpha, beta, kBeta ? OutToAcc<O, A>(yc[h]) : 0);
-            } else if constexpr (kBeta) {
-                r = alpha * sum + beta * OutToAcc<O, A>(yc[h]);
-            } else {
-                r = alpha * sum;
-            }
-            OutT* dst = done ? y + (cur.r0 + i) * p.y_stride : sink;
-            *dst = FromAcc<O, A>(r);
-        }
-        WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
-
-        // Rotate the pipeline.
-        Products<RowT, V, O, A>(bn, xg, prod);
-        if (nxt.first) {
-            rpc[0] = bn.rp[0];
-            rpc[1] = bn.rp[1];
-            yc[0] = bn.yold[0];
-            yc[1] = bn.yold[1];
-        }
-        cur = nxt;
-        nxt = after;
-        bn = ba;
-    }
-}
 
 // ------------------------- stream row kernel (fp32 sums) ---------------------
 //
@@ -1579,11 +1261,25 @@ void SpmvStreamFlatKernel(RowBlockParams p)
 // wave as in the fp32 kernel, without the fp32 kernel's tasks (a long block is
 // processed chunk by chunk by its own wave).
 
+template <ValKind V>
+struct GenVals;
+template <>
+struct GenVals<ValKind::I8> {
+    uint32_t v[2];  // 4 bytes per 16-byte group of slots
+};
+template <>
+struct GenVals<ValKind::F32> {
+    v4f v[2];
+};
+template <>
+struct GenVals<ValKind::C64> {
+    v4f v[4];  // two complex values per 16 bytes
+};
+
 template <ValKind V, AccKind A>
 struct GenLoad {
     v4i col[2];
-    // values of the 8 slots: int8 -> 2 words of 4 bytes; complex64 -> 4 x 16 bytes
-    typename std::conditional<V == ValKind::I8, uint32_t[2], v4f[4]>::type val;
+    GenVals<V> val;  // values of the lane's 8 slots
     int64_t rp[2];
     typename AccOf<A>::T xg[kLaneItems];
 };
@@ -1602,13 +1298,17 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
     if constexpr (V == ValKind::I8) {
-        b.val[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
-        b.val[1] = __builtin_amdgcn_raw_buffer_load_b32(rv, 256 + lane * 4, 0, kBufNonTemporal);
+        b.val.v[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
+        b.val.v[1] = __builtin_amdgcn_raw_buffer_load_b32(rv, 256 + lane * 4, 0, kBufNonTemporal);
+    } else if constexpr (V == ValKind::F32) {
+        b.val.v[0] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
+        b.val.v[1] =
+            __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, 1024 + lane * 16, 0, kBufNonTemporal));
     } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int off = (q >> 1) * 2048 + lane * 32 + (q & 1) * 16;
-            b.val[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kBufNonTemporal));
+            b.val.v[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kBufNonTemporal));
         }
     }
     const int64_t r0 = s.valid ? s.r0 : 0;
@@ -1636,10 +1336,13 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
                 const ValT v = static_cast<const ValT*>(p.val)[k];
                 if constexpr (V == ValKind::I8) {
                     const uint32_t sh = 8U * static_cast<uint32_t>(j & 3);
-                    b.val[j >> 2] = (b.val[j >> 2] & ~(0xFFU << sh)) | (static_cast<uint32_t>(static_cast<uint8_t>(v)) << sh);
+                    b.val.v[j >> 2] =
+                        (b.val.v[j >> 2] & ~(0xFFU << sh)) | (static_cast<uint32_t>(static_cast<uint8_t>(v)) << sh);
+                } else if constexpr (V == ValKind::F32) {
+                    b.val.v[j >> 2][j & 3] = v;
                 } else {
-                    b.val[j >> 1][(j & 1) * 2] = v.re;
-                    b.val[j >> 1][(j & 1) * 2 + 1] = v.im;
+                    b.val.v[j >> 1][(j & 1) * 2] = v.re;
+                    b.val.v[j >> 1][(j & 1) * 2 + 1] = v.im;
                 }
             }
         }
@@ -1651,7 +1354,10 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
         off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
         if constexpr (V == ValKind::I8) {
             const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b8(rx, static_cast<int>(off), 0, kGatherPolicy);
-            b.xg[j] = static_cast<long long>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
+            b.xg[j] = ToAcc<V, A>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
+        } else if constexpr (V == ValKind::F32) {
+            b.xg[j] = ToAcc<V, A>(
+                __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy)));
         } else {
             const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0,
                                                                                      kGatherPolicy));
@@ -1664,9 +1370,11 @@ template <ValKind V, AccKind A>
 __device__ __forceinline__ typename AccOf<A>::T GenVal(const GenLoad<V, A>& b, int j)
 {
     if constexpr (V == ValKind::I8) {
-        return static_cast<long long>(static_cast<int8_t>((b.val[j >> 2] >> (8 * (j & 3))) & 0xFFU));
+        return ToAcc<V, A>(static_cast<int8_t>((b.val.v[j >> 2] >> (8 * (j & 3))) & 0xFFU));
+    } else if constexpr (V == ValKind::F32) {
+        return ToAcc<V, A>(b.val.v[j >> 2][j & 3]);
     } else {
-        return C64{b.val[j >> 1][(j & 1) * 2], b.val[j >> 1][(j & 1) * 2 + 1]};
+        return C64{b.val.v[j >> 1][(j & 1) * 2], b.val.v[j >> 1][(j & 1) * 2 + 1]};
     }
 }
 
@@ -2375,55 +2083,6 @@ unsigned RowBlockGrid(int64_t numBlocks)
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
 
-// Resident workgroups per CU of a kernel (cached per device and kernel).
-int ResidentBlocksPerCu(const void* kernel)
-{
-    static std::mutex mu;
-    static std::map<std::pair<int, const void*>, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find({dev, kernel});
-    if (it != cache.end()) return it->second;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWave * kWavesPerGroup, 0) != hipSuccess || n < 1) n = 1;
-    cache[{dev, kernel}] = n;
-    return n;
-}
-
-int CuCount()
-{
-    static std::mutex mu;
-    static std::map<int, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(dev);
-    if (it != cache.end()) return it->second;
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < kXcds) n = 256;
-    cache[dev] = n;
-    return n;
-}
-
-// Persistent grid: the blocks of each XCD's range are split evenly over
-// J <= resident-slots workers so that every worker runs the same number of
-// blocks (+-1), i.e. J = ceil(per / ceil(per / slots)).
-// Each workgroup carries kWavesPerGroup independent wave workers.
-void PersistentShape(RowBlockParams& p, const void* kernel, unsigned& grid)
-{
-    const int64_t per = (p.num_blocks + kXcds - 1) / kXcds;
-    const int64_t slots =
-        static_cast<int64_t>(CuCount() / kXcds) * ResidentBlocksPerCu(kernel) * kWavesPerGroup;
-    const int64_t rounds = (per + slots - 1) / slots;
-    int64_t j = rounds > 0 ? (per + rounds - 1) / rounds : 1;
-    j = (j + kWavesPerGroup - 1) / kWavesPerGroup * kWavesPerGroup;  // whole workgroups
-    if (j < kWavesPerGroup) j = kWavesPerGroup;
-    p.per_xcd = per;
-    p.workers_per_xcd = static_cast<int32_t>(j);
-    grid = static_cast<unsigned>((j / kWavesPerGroup) * kXcds);
-}
-
 // Waves serving long-block tasks (ACLSPARSE_HIP_TASK_WAVES overrides, for tuning).
 int64_t TaskWaves()
 {
@@ -2472,8 +2131,10 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             return 0;
         }
     }
-    if constexpr ((V == ValKind::I8 && A == AccKind::I64) || (V == ValKind::C64 && A == AccKind::C64)) {
-        // int8 -> int32 and complex64 on the stream kernel's row blocks
+    if constexpr ((V == ValKind::I8 && A == AccKind::I64) || (V == ValKind::I8 && A == AccKind::F32) ||
+                  (V == ValKind::C64 && A == AccKind::C64) || (V == ValKind::F32 && A == AccKind::C64)) {
+        // int8 -> int32 / fp32, complex64, and real fp32 A with complex y on
+        // the stream kernel's row blocks
         const bool gen = l.nnz > 0 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 && l.y_stride == 1 &&
                          Aligned16(l.col) && Aligned16(l.val) &&
                          static_cast<int64_t>(l.cols) * static_cast<int64_t>(sizeof(typename ValOf<V>::T)) <=
@@ -2483,23 +2144,6 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
             hipLaunchKernelGGL((SpmvStreamGenKernel<RowT, V, O, A>), dim3(g), dim3(kWave * kFlatWaves), 0, stream_,
                                p);
-            return 0;
-        }
-    }
-    if constexpr (kCanVec) {
-        if (vec) {
-            // beta is known on the host unless it lives in device memory.
-            const bool betaNz = l.device_scalars || l.beta_re != 0.0f || l.beta_im != 0.0f || l.beta_i != 0;
-            unsigned pg = 0;
-            if (betaNz) {
-                PersistentShape(p, reinterpret_cast<const void*>(&SpmvWaveKernel<RowT, V, O, A, true>), pg);
-                hipLaunchKernelGGL((SpmvWaveKernel<RowT, V, O, A, true>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
-                                   stream, p);
-            } else {
-                PersistentShape(p, reinterpret_cast<const void*>(&SpmvWaveKernel<RowT, V, O, A, false>), pg);
-                hipLaunchKernelGGL((SpmvWaveKernel<RowT, V, O, A, false>), dim3(pg), dim3(kWave * kWavesPerGroup), 0,
-                                   stream, p);
-            }
             return 0;
         }
     }

@@ -521,3 +521,48 @@ def test_complex64_stream_rows(tail, dev):
         abs(beta) * np.abs(y0.numpy())
     err = np.abs(y.cpu().numpy().astype(np.complex128) - ref) / np.maximum(scale, 1e-30)
     assert err.max() <= 1e-5, float(err.max())
+
+
+def test_int8_to_fp32_stream_rows(dev):
+    """int8 values and x with fp32 compute and output (exact int products, fp32 sums)."""
+    g, rows, cols, rp, col = _mixed_lengths(61, 2)
+    n = col.numel()
+    v8 = torch.randint(-128, 128, (n,), generator=g, dtype=torch.int8)
+    x8 = torch.randint(-128, 128, (cols,), generator=g, dtype=torch.int8)
+    y0 = torch.rand(rows, generator=g) * 2 - 1
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(rows, cols, rp.to(torch.int32).to(dev), col.to(dev), v8.to(dev), x8.to(dev), y, 1.5, 0.5)
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    rpn = rp.numpy()
+    prod = v8.numpy().astype(np.float64) * x8.numpy().astype(np.float64)[col.numpy()]
+    seg = np.add.reduceat(np.append(prod, 0.0), rpn[:-1]) * (np.diff(rpn) > 0)
+    absseg = np.add.reduceat(np.append(np.abs(prod), 0.0), rpn[:-1]) * (np.diff(rpn) > 0)
+    golden = 1.5 * seg + 0.5 * y0.numpy().astype(np.float64)
+    scale = 1.5 * absseg + 0.5 * np.abs(y0.numpy())
+    err = np.abs(y.cpu().numpy().astype(np.float64) - golden) / np.maximum(scale, 1e-30)
+    assert err.max() <= 1e-5, float(err.max())
+
+
+def test_real_matrix_complex_output_stream_rows(dev):
+    """fp32 values and x with complex64 y and complex alpha/beta, against the fp64 oracle."""
+    g, rows, cols, rp, col = _mixed_lengths(62, 1)
+    n = col.numel()
+    v = torch.rand(n, generator=g) * 2 - 1
+    x = torch.rand(cols, generator=g) * 2 - 1
+    y0 = torch.complex(torch.rand(rows, generator=g) * 2 - 1, torch.rand(rows, generator=g) * 2 - 1)
+    alpha, beta = complex(0.75, 1.25), complex(-0.5, 0.25)
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(rows, cols, rp.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta)
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    ref = oracle.spmv_c64(rp.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), cols, 0, alpha, beta,
+                          val_is_real=True)
+    rpn = rp.numpy()
+    absprod = np.abs(v.numpy()) * np.abs(x.numpy())[col.numpy()]
+    scale = abs(alpha) * np.add.reduceat(np.append(absprod, 0.0), rpn[:-1]) * (np.diff(rpn) > 0) + \
+        abs(beta) * np.abs(y0.numpy())
+    err = np.abs(y.cpu().numpy().astype(np.complex128) - ref) / np.maximum(scale, 1e-30)
+    assert err.max() <= 1e-5, float(err.max())
