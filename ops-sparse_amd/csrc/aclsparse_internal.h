@@ -177,6 +177,10 @@ struct SpmvLayout {
     // acc_offset.
     bool csc = false;
     size_t colptr_offset = 0, entry_row_offset = 0, csc_pos_offset = 0, prod_offset = 0;
+    // row-block partition of the CSC pattern (columns as rows), for the
+    // column pass on the stream kernel: csc_blocks int32[Bc+1], csc_block_nnz RowT[Bc+1]
+    size_t csc_blocks_offset = 0, csc_block_nnz_offset = 0;
+    int64_t csc_items_per_block = 0, csc_num_blocks = 0;
     size_t key_a_offset = 0, key_b_offset = 0, val_b_offset = 0, sort_offset = 0, sort_bytes = 0;
     // Long-block tasks (non-transpose, fp32 compute): a block of more than
     // kLongChunks chunks is split into one task per chunk.  task_start[B+1]
@@ -245,7 +249,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             const size_t n = static_cast<size_t>(nnz);
             const size_t rb = l.rowptr_bytes;
             l.colptr_offset = AlignUp(l.acc_offset);
-            l.entry_row_offset = AlignUp(l.colptr_offset + static_cast<size_t>(cols + 1) * rb);
+            // cols + 2 entries: a pad entry, as for the row offsets
+            l.entry_row_offset = AlignUp(l.colptr_offset + static_cast<size_t>(cols + 2) * rb);
             l.csc_pos_offset = AlignUp(l.entry_row_offset + n * sizeof(int32_t));
             l.key_a_offset = AlignUp(l.csc_pos_offset + n * rb);
             l.key_b_offset = AlignUp(l.key_a_offset + n * sizeof(int32_t));
@@ -253,7 +258,12 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.prod_offset = l.key_a_offset;  // prod[nnz] of <= 8 bytes ends before val_b
             l.sort_offset = AlignUp(l.val_b_offset + n * rb);
             l.sort_bytes = CscSortTempBytes(static_cast<int64_t>(nnz), l.rowptr_bytes);
-            l.total = AlignUp(l.sort_offset + l.sort_bytes + 256);  // re-aligned to 256 bytes at use
+            l.csc_items_per_block = ItemsPerBlock(cols, nnz);
+            l.csc_num_blocks = NumBlocks(cols, nnz);
+            l.csc_blocks_offset = AlignUp(l.sort_offset + l.sort_bytes + 256);  // sort temp re-aligned to 256 at use
+            l.csc_block_nnz_offset =
+                AlignUp(l.csc_blocks_offset + static_cast<size_t>(l.csc_num_blocks + 1) * sizeof(int32_t));
+            l.total = AlignUp(l.csc_block_nnz_offset + static_cast<size_t>(l.csc_num_blocks + 1) * rb);
         }
     }
     return l;
@@ -262,7 +272,9 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
 // ---------------------------------------------------------------------------
 // Launcher interface (implemented in spmv_kernels.hip).
 // ---------------------------------------------------------------------------
-enum class ValKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I8 = 3, C64 = 4 };
+// UNIT: no values (every entry is 1); the transpose's column pass reads its
+// fp32 products through the x gather.
+enum class ValKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I8 = 3, C64 = 4, UNIT = 5 };
 enum class OutKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I32 = 3, C64 = 4 };
 enum class AccKind : int32_t { F32 = 0, I64 = 1, C64 = 2 };
 

@@ -83,6 +83,7 @@ template <> struct ValOf<ValKind::F16> { using T = uint16_t; };
 template <> struct ValOf<ValKind::BF16> { using T = uint16_t; };
 template <> struct ValOf<ValKind::I8> { using T = int8_t; };
 template <> struct ValOf<ValKind::C64> { using T = C64; };
+template <> struct ValOf<ValKind::UNIT> { using T = float; };  // the gathered "x" holds the products
 
 template <OutKind O> struct OutOf;
 template <> struct OutOf<OutKind::F32> { using T = float; };
@@ -646,6 +647,9 @@ template <>
 struct StreamVals<ValKind::BF16> {
     v4i v;
 };
+template <>
+struct StreamVals<ValKind::UNIT> {
+};
 
 template <ValKind V>
 __device__ __forceinline__ uint32_t RawVal(const StreamVals<V>& s, int j)
@@ -700,7 +704,9 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     // col_ind (values: 1 KiB fp32, 512 B fp16) without gaps.
     b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
-    if constexpr (V == ValKind::F32) {
+    if constexpr (V == ValKind::UNIT) {
+        (void)rv;  // no values
+    } else if constexpr (V == ValKind::F32) {
         b.val.v[0] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
         b.val.v[1] =
             __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, 1024 + lane * 16, 0, kBufNonTemporal));
@@ -764,12 +770,12 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
     if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
         // Uniform branch: only the chunk that reaches the end of the arrays.
         int32_t tc[3];
-        ValT tv3[3];
+        ValT tv3[3] = {};
 #pragma unroll
         for (int e = 0; e < 3; ++e) {
             const int64_t k = tailStart + e < p.nnz ? tailStart + e : p.nnz - 1;
             tc[e] = ConstLoad<int32_t>(p.col, k);
-            tv3[e] = ConstLoad<ValT>(p.val, k);
+            if constexpr (V != ValKind::UNIT) tv3[e] = ConstLoad<ValT>(p.val, k);
         }
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
@@ -778,7 +784,9 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
                 const int kk = static_cast<int>(k);
                 b.col[j >> 2][j & 3] = kk == 0 ? tc[0] : kk == 1 ? tc[1] : tc[2];
                 const ValT tv = kk == 0 ? tv3[0] : kk == 1 ? tv3[1] : tv3[2];
-                if constexpr (V == ValKind::F32) {
+                if constexpr (V == ValKind::UNIT) {
+                    (void)tv;
+                } else if constexpr (V == ValKind::F32) {
                     b.val.v[j >> 2][j & 3] = tv;
                 } else {
                     const uint32_t raw = static_cast<uint32_t>(tv);
@@ -860,7 +868,10 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     using OutT = typename OutOf<O>::T;
     float prod[kLaneItems];
 #pragma unroll
-    for (int j = 0; j < kLaneItems; ++j) prod[j] = ValToFloat<V>(RawVal<V>(lc.val, j)) * ValToFloat<V>(lc.xg[j]);
+    for (int j = 0; j < kLaneItems; ++j) {
+        if constexpr (V == ValKind::UNIT) prod[j] = __uint_as_float(lc.xg[j]);
+        else prod[j] = ValToFloat<V>(RawVal<V>(lc.val, j)) * ValToFloat<V>(lc.xg[j]);
+    }
 
     const int32_t c0 = cur.c0, c1 = cur.c1;
     const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);  // LDS slot of relative offset r: r - shift
@@ -2020,7 +2031,7 @@ __global__ __launch_bounds__(kThreads) void SpmvPreprocessKernel(PrepParams p)
         p.blocks[i] = start;
         static_cast<SrcT*>(p.block_nnz)[i] = static_cast<SrcT>(NormRow<SrcT>(p, start));
     }
-    if (i == 0) *p.header = p.header_value;
+    if (i == 0 && p.header != nullptr) *p.header = p.header_value;
 }
 
 int GridFor(int64_t n)
@@ -2183,6 +2194,40 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         const int64_t threads = n << lg;
         const unsigned grid = static_cast<unsigned>((threads + kThreads - 1) / kThreads);
         hipLaunchKernelGGL((CscProductKernel<RowT, V, A>), dim3(GridFor((l.nnz + 3) / 4)), dim3(kThreads), 0, stream, q);
+        if constexpr (std::is_same<RowT, int32_t>::value && A == AccKind::F32 && O != OutKind::I32) {
+            // fp32 products and 32-bit positions: the column pass is an SpMV
+            // of the CSC pattern (unit values) with the products as x, on the
+            // stream kernel and the columns' row-block partition.
+            if (l.y_stride == 1 && l.nnz <= 0x1FFFFFFFLL) {
+                RowBlockParams c = p;
+                c.rp = At<void>(l.ws, l.layout.colptr_offset);
+                c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
+                c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
+                c.num_blocks = l.layout.csc_num_blocks;
+                c.col = At<const int32_t>(l.ws, l.layout.csc_pos_offset);
+                c.col_stride = 1;
+                c.val = nullptr;
+                c.val_stride = 1;
+                c.x = q.prod;
+                c.x_stride = 1;
+                c.rows = n;
+                c.cols = l.nnz;  // length of the gathered array
+                c.base = 0;
+                c.task_wgs = 0;
+                c.task_waves = 0;
+                const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
+                const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+                const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+                if (betaNz) {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, true>), dim3(g),
+                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                } else {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, false>), dim3(g),
+                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                }
+                return 0;
+            }
+        }
         hipLaunchKernelGGL((SpmvCscGatherKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, q);
         return 0;
     }
@@ -2321,6 +2366,25 @@ int BuildCsc(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL((CscFinishKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, vals.Current(),
                        At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.entry_row_offset),
                        At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, nnz);
+    // Row-block partition of the columns (the column pass runs the stream
+    // kernel on the CSC pattern); colptr is already normalised, so the
+    // partition kernel rewrites it in place with the same values.
+    PrepParams pp{};
+    pp.rp = At<void>(l.ws, l.layout.colptr_offset);
+    pp.stride = 1;
+    pp.base = 0;
+    pp.rows = l.cols;
+    pp.cols = l.rows;
+    pp.nnz = nnz;
+    pp.norm = At<void>(l.ws, l.layout.colptr_offset);
+    pp.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
+    pp.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
+    pp.num_blocks = l.layout.csc_num_blocks;
+    pp.items = l.layout.csc_items_per_block;
+    pp.header = nullptr;
+    const int64_t n = (l.cols > pp.num_blocks ? l.cols : pp.num_blocks) + 1;
+    hipLaunchKernelGGL((SpmvPreprocessKernel<RowT>), dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, pp);
     return 0;
 }
 
