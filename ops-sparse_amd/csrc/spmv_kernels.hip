@@ -903,24 +903,63 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     re[1] = FromNextLane(rs[0], rs[1]);
 
     const int gsz = 1 << lg;
-    const int cap = SerialCap(lg);
-    bool fin[2], defer[2];
+    bool fin[2], defer[2], active[2], crosses[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = 2 * lane + h;
         const bool in = i < nr;
         const bool empty = re[h] <= rs[h];
-        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
-                                         : (rs[h] < c1 && re[h] > c0));
-        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
-        defer[h] = active && (crosses || re[h] - rs[h] > cap);
-        fin[h] = active && !defer[h];
+        active[h] = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                 : (rs[h] < c1 && re[h] > c0));
+        crosses[h] = !empty && (rs[h] < c0 || re[h] > c1);
+    }
+    // One lane per row reads 8 entries per row; when a row of 9-16 entries
+    // lies inside the chunk, 16 (rows of 9-16 entries would otherwise be
+    // summed one at a time by the whole wave).
+    bool wide = false;
+    if (lg == 0) {
+        const bool mid0 = active[0] && !crosses[0] && re[0] - rs[0] > kSerialCapOne && re[0] - rs[0] <= 16;
+        const bool mid1 = active[1] && !crosses[1] && re[1] - rs[1] > kSerialCapOne && re[1] - rs[1] <= 16;
+        wide = __ballot(mid0 || mid1) != 0;
+    }
+    const int cap = wide ? 16 : SerialCap(lg);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        defer[h] = active[h] && (crosses[h] || re[h] - rs[h] > cap);
+        fin[h] = active[h] && !defer[h];
     }
     WaveLdsSync();
 
     // Phase 1.
     float sum[2] = {0.0f, 0.0f};
-    if (lg == 0) {
+    if (wide) {
+        // rows of up to 16 entries: per row, 16 predicated reads issued
+        // before one wait
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v2f e[8];
+            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
+            const uint32_t addr = LdsAddr(sVal + (fin[h] ? rs[h] - shift : 0));
+            asm volatile("ds_read2_b32 %0, %8 offset1:1\n\t"
+                         "ds_read2_b32 %1, %8 offset0:2 offset1:3\n\t"
+                         "ds_read2_b32 %2, %8 offset0:4 offset1:5\n\t"
+                         "ds_read2_b32 %3, %8 offset0:6 offset1:7\n\t"
+                         "ds_read2_b32 %4, %8 offset0:8 offset1:9\n\t"
+                         "ds_read2_b32 %5, %8 offset0:10 offset1:11\n\t"
+                         "ds_read2_b32 %6, %8 offset0:12 offset1:13\n\t"
+                         "ds_read2_b32 %7, %8 offset0:14 offset1:15"
+                         : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3]), "=&v"(e[4]), "=&v"(e[5]),
+                           "=&v"(e[6]), "=&v"(e[7])
+                         : "v"(addr));
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]),
+                           "+v"(e[7]));
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc += t < len ? e[t >> 1][t & 1] : 0.0f;
+            sum[h] = acc;
+        }
+    } else if (lg == 0) {
         // One lane per row, at most 8 entries: 8 predicated reads per row,
         // no branch.  All 16 reads are issued before one wait (the
         // compiler's own schedule waits after each read pair).

@@ -566,3 +566,23 @@ def test_real_matrix_complex_output_stream_rows(dev):
         abs(beta) * np.abs(y0.numpy())
     err = np.abs(y.cpu().numpy().astype(np.complex128) - ref) / np.maximum(scale, 1e-30)
     assert err.max() <= 1e-5, float(err.max())
+
+
+@pytest.mark.parametrize("per", [9, 12, 16, 17])
+def test_rows_of_nine_to_sixteen_entries(per, dev):
+    """Blocks of many rows of 9-16 entries take the 16-read one-lane-per-row path (17: the
+    whole-wave path); mixed with shorter rows in the same blocks."""
+    g = torch.Generator().manual_seed(per)
+    lengths = torch.full((20000,), per, dtype=torch.int64)
+    lengths[::7] = torch.randint(0, 9, (lengths[::7].numel(),), generator=g)
+    rp, col = wl.csr_from_lengths(lengths, 30000, g, "cpu", distinct=False)
+    n = col.numel()
+    w = wl.Workload("mid_rows", lengths.numel(), 30000, rp.to(torch.int32), col, torch.rand(n, generator=g) * 2 - 1,
+                    torch.rand(30000, generator=g) * 2 - 1, torch.rand(lengths.numel(), generator=g) * 2 - 1,
+                    1.5, -0.5)
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
+    w.trans = "T"
+    w.y0 = torch.rand(30000, generator=g) * 2 - 1
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
