@@ -1465,18 +1465,28 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
     re[0] = rs[1];
     re[1] = FromNextLane(rs[0], rs[1]);
     const int gsz = 1 << lg;
-    const int cap = SerialCap(lg);
-    bool fin[2], defer[2];
+    bool fin[2], defer[2], active[2], crosses[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = 2 * lane + h;
         const bool in = i < nr;
         const bool empty = re[h] <= rs[h];
-        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
-                                         : (rs[h] < c1 && re[h] > c0));
-        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
-        defer[h] = active && (crosses || re[h] - rs[h] > cap);
-        fin[h] = active && !defer[h];
+        active[h] = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                 : (rs[h] < c1 && re[h] > c0));
+        crosses[h] = !empty && (rs[h] < c0 || re[h] > c1);
+    }
+    // one lane per row: 16 entries when a row of 9-16 lies inside the chunk
+    bool wide = false;
+    if (lg == 0) {
+        const bool mid0 = active[0] && !crosses[0] && re[0] - rs[0] > kSerialCapOne && re[0] - rs[0] <= 16;
+        const bool mid1 = active[1] && !crosses[1] && re[1] - rs[1] > kSerialCapOne && re[1] - rs[1] <= 16;
+        wide = __ballot(mid0 || mid1) != 0;
+    }
+    const int cap = wide ? 16 : SerialCap(lg);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        defer[h] = active[h] && (crosses[h] || re[h] - rs[h] > cap);
+        fin[h] = active[h] && !defer[h];
     }
     WaveLdsSync();
 
@@ -1488,9 +1498,11 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
             const int32_t base = fin[h] ? rs[h] - shift : 0;
             Acc acc = Zero<Acc>();
 #pragma unroll
-            for (int t = 0; t < kSerialCapOne; ++t) {
-                const Acc v = sVal[base + t];
-                acc = acc + (t < len ? v : Zero<Acc>());
+            for (int t = 0; t < 16; ++t) {
+                if (t < kSerialCapOne || wide) {
+                    const Acc v = sVal[base + t];
+                    acc = acc + (t < len ? v : Zero<Acc>());
+                }
             }
             sum[h] = acc;
         }
@@ -1625,18 +1637,28 @@ __device__ __forceinline__ void StreamChunkOp(const Stage& cur, const StreamLoad
     re[1] = FromNextLane(rs[0], rs[1]);
 
     const int gsz = 1 << lg;
-    const int cap = SerialCap(lg);
-    bool fin[2], defer[2];
+    bool fin[2], defer[2], active[2], crosses[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = 2 * lane + h;
         const bool in = i < nr;
         const bool empty = re[h] <= rs[h];
-        const bool active = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
-                                         : (rs[h] < c1 && re[h] > c0));
-        const bool crosses = !empty && (rs[h] < c0 || re[h] > c1);
-        defer[h] = active && (crosses || re[h] - rs[h] > cap);
-        fin[h] = active && !defer[h];
+        active[h] = in && (empty ? ((rs[h] >= c0 && rs[h] < c1) || (cur.last && rs[h] >= c1))
+                                 : (rs[h] < c1 && re[h] > c0));
+        crosses[h] = !empty && (rs[h] < c0 || re[h] > c1);
+    }
+    // one lane per row: 16 entries when a row of 9-16 lies inside the chunk
+    bool wide = false;
+    if (lg == 0) {
+        const bool mid0 = active[0] && !crosses[0] && re[0] - rs[0] > kSerialCapOne && re[0] - rs[0] <= 16;
+        const bool mid1 = active[1] && !crosses[1] && re[1] - rs[1] > kSerialCapOne && re[1] - rs[1] <= 16;
+        wide = __ballot(mid0 || mid1) != 0;
+    }
+    const int cap = wide ? 16 : SerialCap(lg);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        defer[h] = active[h] && (crosses[h] || re[h] - rs[h] > cap);
+        fin[h] = active[h] && !defer[h];
     }
     WaveLdsSync();
 
@@ -1648,9 +1670,11 @@ __device__ __forceinline__ void StreamChunkOp(const Stage& cur, const StreamLoad
             const int32_t len = fin[h] ? re[h] - rs[h] : 0;
             const int32_t base = fin[h] ? rs[h] - shift : 0;
 #pragma unroll
-            for (int t = 0; t < kSerialCapOne; ++t) {
-                const bool on = t < len;
-                PriestAddSplit(sum[h], on ? sP[base + t] : 0.0f, on ? sE[base + t] : 0.0f);
+            for (int t = 0; t < 16; ++t) {
+                if (t < kSerialCapOne || wide) {
+                    const bool on = t < len;
+                    PriestAddSplit(sum[h], on ? sP[base + t] : 0.0f, on ? sE[base + t] : 0.0f);
+                }
             }
         }
     } else {
