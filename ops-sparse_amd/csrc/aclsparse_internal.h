@@ -314,6 +314,9 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream);
 // SpMVOp on the row-block partition of l (fp32, non-transpose, no tasks):
 // z = alpha*(A*x, doubly compensated) + beta*y, y read from l.y.
 int LaunchSpmvOpStream(const SpmvLaunch& l, float* z, void* stream);
+// The same without a partition (SpMVOp ALG1 has no buffer): blocks of a fixed
+// row count taken straight from l.row_ptr (base subtracted on the fly).
+int LaunchSpmvOpStreamFixed(const SpmvLaunch& l, float* z, void* stream);
 // Runs y = alpha*op(A)*x + beta*y using the partition already in the workspace.
 int LaunchSpmvCompute(const SpmvLaunch& l, void* stream);
 

@@ -292,6 +292,8 @@ struct RowBlockParams {
     int32_t task_wgs;    // workgroups serving tasks (the first ones of the grid)
     int64_t max_tasks;   // capacity of the task arrays
     float* z;            // SpMVOp: output (y is then only read)
+    int64_t rp_base;     // subtracted from p.rp entries (0 for the normalised copy)
+    int32_t fixed_rows;  // SpMVOp ALG1: rows per block, blocks taken straight from p.rp
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -721,18 +723,21 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     // entry), so a pair is either wholly inside or wholly past it (past: 0,
     // never used).  Old y values are loaded one per row.
     const int64_t r0 = s.valid ? s.r0 : 0;
-    const int64_t nrp = s.valid ? ((s.nr + 2) & ~1) : 0;
+    int64_t nrp = s.valid ? ((s.nr + 2) & ~1) : 0;
+    // never past the offsets array (rows + 1 entries; the pad entry of the
+    // workspace copy is not needed: a pair past it is never used)
+    if (nrp > p.rows + 1 - r0) nrp = p.rows + 1 - r0;
     const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
     if constexpr (sizeof(RowT) == 8) {
         const v4i w = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, kRowPolicy));
         b.rp[0] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.y)) << 32) |
-                                    static_cast<uint32_t>(w.x));
+                                    static_cast<uint32_t>(w.x)) - static_cast<RowT>(p.rp_base);
         b.rp[1] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.w)) << 32) |
-                                    static_cast<uint32_t>(w.z));
+                                    static_cast<uint32_t>(w.z)) - static_cast<RowT>(p.rp_base);
     } else {
         const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rr, lane * 8, 0, kRowPolicy));
-        b.rp[0] = static_cast<RowT>(w.x);
-        b.rp[1] = static_cast<RowT>(w.y);
+        b.rp[0] = static_cast<RowT>(w.x) - static_cast<RowT>(p.rp_base);
+        b.rp[1] = static_cast<RowT>(w.y) - static_cast<RowT>(p.rp_base);
     }
     int64_t ny = s.valid ? s.nr : 0;
     if (ny > p.rows - r0) ny = p.rows - r0;
@@ -1603,7 +1608,7 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
 template <typename RowT, bool kBeta>
 __device__ __forceinline__ void StreamChunkOp(const Stage& cur, const StreamLoad<RowT, ValKind::F32, OutKind::F32>& lc,
                                               float* sP, float* sE, int lane, float alpha, float beta, Triple& carry,
-                                              int& lg, float* z, float* sink)
+                                              int& lg, float* z)
 {
 #pragma clang fp contract(off)
     float pr[kLaneItems], er[kLaneItems];
@@ -1730,13 +1735,35 @@ __device__ __forceinline__ void StreamChunkOp(const Stage& cur, const StreamLoad
         if constexpr (kBeta) {
             if (beta != 0.0f) yv = lc.yold[h];
         }
-        float* dst = fin[h] ? z + (cur.r0 + i) : sink + h * kWave;
-        *dst = CombineZ(sum[h], alpha, beta, yv);
+        if (fin[h]) z[cur.r0 + i] = CombineZ(sum[h], alpha, beta, yv);
     }
     WaveLdsSync();
 }
 
-template <typename RowT, bool kBeta>
+// ALG1 (no buffer, kFixed): block b is rows [b*R, (b+1)*R) of the caller's
+// row offsets, R from the mean row length.
+template <typename RowT>
+__device__ __forceinline__ Stage OpenFixedTile(const RowBlockParams& p, int64_t tile)
+{
+    Stage s{};
+    s.valid = true;
+    const int64_t r0 = tile * p.fixed_rows;
+    int64_t n = p.rows - r0;
+    n = n > p.fixed_rows ? p.fixed_rows : n;
+    s.r0 = r0;
+    s.nr = static_cast<int32_t>(n);
+    const int64_t k0 = static_cast<int64_t>(ConstLoad<RowT>(p.rp, r0)) - p.rp_base;
+    const int64_t k1 = static_cast<int64_t>(ConstLoad<RowT>(p.rp, r0 + n)) - p.rp_base;
+    s.k0 = k0;
+    const int64_t span = k1 - k0;
+    s.kspan = static_cast<int32_t>(span < 0 ? 0 : span > 0x7FFFFFFFLL ? 0x7FFFFFFFLL : span);
+    s.c0 = 0;
+    s.first = true;
+    ChunkBounds(s);
+    return s;
+}
+
+template <typename RowT, bool kBeta, bool kFixed = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlockParams p)
 {
     using L = StreamLoad<RowT, ValKind::F32, OutKind::F32>;
@@ -1746,21 +1773,20 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlock
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float alpha, beta;
     LoadScalars<AccKind::F32>(p.s, alpha, beta);
-    float* sink = static_cast<float*>(p.sink) + lane;
     const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(float)));
     const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
     const int64_t wg = static_cast<int64_t>(blockIdx.x);
     const int64_t per = static_cast<int64_t>(gridDim.x) / kXcds;
     const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
     if (tile >= p.num_blocks) return;
-    Stage cur = OpenTileFlat<RowT>(p, tile);
+    Stage cur = kFixed ? OpenFixedTile<RowT>(p, tile) : OpenTileFlat<RowT>(p, tile);
     Triple carry{0.0f, 0.0f, 0.0f};
     int lg = 0;
     while (cur.valid) {
         L b;
         StreamLoadStage<RowT, ValKind::F32, OutKind::F32, kBeta>(p, cur, tailStart, lane, b);
         StreamGather<RowT, ValKind::F32, OutKind::F32>(p, cur, tailStart, rx, lane, b, b.xg);
-        StreamChunkOp<RowT, kBeta>(cur, b, sPAll[wv], sEAll[wv], lane, alpha, beta, carry, lg, p.z, sink);
+        StreamChunkOp<RowT, kBeta>(cur, b, sPAll[wv], sEAll[wv], lane, alpha, beta, carry, lg, p.z);
         if (cur.last) break;
         cur.c0 = cur.c1;
         cur.first = false;
@@ -2477,6 +2503,50 @@ size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes)
     }
     if (e != hipSuccess) bytes = static_cast<size_t>(nnz) * 16 + (1 << 20);
     return bytes;
+}
+
+int LaunchSpmvOpStreamFixed(const SpmvLaunch& l, float* z, void* stream)
+{
+    if (l.rows <= 0) return 0;
+    RowBlockParams p{};
+    p.rp = l.row_ptr;
+    p.rp_base = l.base;
+    p.col = l.col;
+    p.col_stride = 1;
+    p.val = l.val;
+    p.val_stride = 1;
+    p.x = l.x;
+    p.x_stride = 1;
+    p.y = l.y;
+    p.y_stride = 1;
+    p.z = z;
+    p.rows = l.rows;
+    p.cols = l.cols;
+    p.nnz = l.nnz;
+    p.base = l.base;
+    p.s.device = l.device_scalars;
+    p.s.alpha_re = l.alpha_re;
+    p.s.beta_re = l.beta_re;
+    p.s.alpha_ptr = l.alpha_ptr;
+    p.s.beta_ptr = l.beta_ptr;
+    // about one 512-slot chunk of non-zeros per block, at most 127 rows
+    int64_t r = l.nnz > 0 ? static_cast<int64_t>((496.0 * static_cast<double>(l.rows)) / static_cast<double>(l.nnz))
+                          : kWaveRows;
+    r = r < 1 ? 1 : r > kWaveRows ? kWaveRows : r;
+    p.fixed_rows = static_cast<int32_t>(r);
+    p.num_blocks = (l.rows + r - 1) / r;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
+    const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+    const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+    if (l.rowptr64) {
+        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, true, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+        else hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, false, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+    } else {
+        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, true, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+        else hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, false, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
+    }
+    return 0;
 }
 
 int LaunchSpmvOpStream(const SpmvLaunch& l, float* z, void* stream)

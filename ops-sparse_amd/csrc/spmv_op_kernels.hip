@@ -4,10 +4,10 @@
 // The reference runs one scalar thread per row with Priest's accumulator
 // (TwoProduct by FMA + two TwoSum stages, sparse/spmv_op/arch35/spmv_op_kernel.cpp:87-128)
 // and builds the ALG2 tables with one scalar thread (:425-540).  Here:
-//  * ALG1 (no buffer): W lanes of a wave64 share a row (W from the mean row
-//    length); every lane keeps its own Priest triple (hi, md, lo) over a
-//    strided subset of the row and the W triples are merged by an exact
-//    TwoSum butterfly.
+//  * ALG1 (no buffer): the SpMV stream kernel with the compensated
+//    accumulator (SpmvOpStreamKernel in spmv_kernels.hip) on row blocks of a
+//    fixed row count (about 500 non-zeros each) read straight from the
+//    caller's row offsets.
 //  * ALG2 (buffer): createDescr builds the reference's tables in parallel
 //    (row lengths, a stable descending radix sort (hipCUB), an int64
 //    inclusive scan, the bin edges by binary search plus the reference's
@@ -36,6 +36,7 @@ constexpr int kThreads = 256;
 constexpr int kWave = 64;
 
 
+
 struct OpParams {
     const void* rp;
     const int32_t* col;
@@ -49,75 +50,12 @@ struct OpParams {
     const float* alpha_ptr;
     const float* beta_ptr;
     int32_t device_scalars;
-    int32_t wlog;             // ALG1: log2 lanes per row
 };
 
 __device__ __forceinline__ void Scalars(const OpParams& p, float& a, float& b)
 {
     a = p.device_scalars ? *p.alpha_ptr : p.alpha;
     b = p.device_scalars ? *p.beta_ptr : p.beta;
-}
-
-// One row reduced by the W = 2^wlog lanes that share `sub`; returns the
-// merged triple on every lane of the group.
-template <typename RowT>
-__device__ __forceinline__ Triple RowDot(const OpParams& p, int64_t row, bool active, int wlog, int sub)
-{
-    const RowT* rp = static_cast<const RowT*>(p.rp);
-    Triple t{0.0f, 0.0f, 0.0f};
-    if (active) {
-        const int64_t s = static_cast<int64_t>(rp[row]) - p.base;
-        const int64_t e = static_cast<int64_t>(rp[row + 1]) - p.base;
-        const int64_t w = int64_t{1} << wlog;
-        // Batches of 4 entries per lane: the 4 column/value loads, then the 4
-        // x gathers, are in flight together (one dependent round trip per
-        // batch instead of one per entry); the additions keep the entry order.
-        constexpr int kB = 4;
-        for (int64_t q0 = s + sub; q0 < e; q0 += kB * w) {
-            int32_t c[kB];
-            float v[kB], xv[kB];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                const int64_t q = q0 + u * w;
-                c[u] = q < e ? p.col[q] - p.base : 0;
-                v[u] = q < e ? p.val[q] : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < kB; ++u) xv[u] = q0 + u * w < e ? p.x[c[u]] : 0.0f;
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                if (q0 + u * w < e) PriestAdd(t, v[u], xv[u]);
-            }
-        }
-    }
-    for (int msk = (1 << wlog) >> 1; msk > 0; msk >>= 1) t = Merge(t, ShflXor(t, msk));
-    return t;
-}
-
-__device__ __forceinline__ void StoreZ(const OpParams& p, int64_t row, const Triple& t, float a, float b)
-{
-    const float yv = b == 0.0f ? 0.0f : p.y[row];
-    p.z[row] = CombineZ(t, a, b, yv);
-}
-
-// ALG1: rows in natural order, 64/W rows per wave pass, grid-stride.
-template <typename RowT>
-__global__ __launch_bounds__(kThreads) void SpmvOpAlg1Kernel(OpParams p)
-{
-    float a, b;
-    Scalars(p, a, b);
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wlog = p.wlog;
-    const int sub = lane & ((1 << wlog) - 1);
-    const int64_t rowsPerWave = kWave >> wlog;
-    const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / kWave;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
-    for (int64_t r0 = wave * rowsPerWave; r0 < p.m; r0 += waves * rowsPerWave) {
-        const int64_t row = r0 + (lane >> wlog);
-        const bool active = row < p.m;
-        const Triple t = RowDot<RowT>(p, active ? row : 0, active, wlog, sub);
-        if (active && sub == 0) StoreZ(p, row, t, a, b);
-    }
 }
 
 // nnz == 0: Z = beta*Y; Y is not read when beta == 0.
@@ -366,16 +304,27 @@ int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void
         sl.beta_ptr = betaPtr;
         return LaunchSpmvOpStream(sl, static_cast<float*>(z), stream);
     }
-    const int64_t mean = p.nnz / p.m;
-    int wlog = 0;
-    while (wlog < 6 && (int64_t{4} << wlog) < mean) ++wlog;
-    p.wlog = wlog;
-    const int64_t waves = (p.m + (kWave >> wlog) - 1) / (kWave >> wlog);
-    int64_t grid = (waves + kThreads / kWave - 1) / (kThreads / kWave);
-    grid = grid < 1 ? 1 : grid > 65536 ? 65536 : grid;
-    if (i64) hipLaunchKernelGGL(SpmvOpAlg1Kernel<int64_t>, dim3(grid), dim3(kThreads), 0, s, p);
-    else hipLaunchKernelGGL(SpmvOpAlg1Kernel<int32_t>, dim3(grid), dim3(kThreads), 0, s, p);
-    return 0;
+    // ALG1 has no buffer: the stream kernel on fixed-size row blocks read
+    // straight from the caller's row offsets.
+    {
+        SpmvLaunch sl{};
+        sl.row_ptr = d.row_offsets;
+        sl.col = d.col_ind;
+        sl.val = d.values;
+        sl.x = x;
+        sl.y = const_cast<void*>(y);
+        sl.rows = p.m;
+        sl.cols = p.n;
+        sl.nnz = p.nnz;
+        sl.base = p.base;
+        sl.rowptr64 = i64 ? 1 : 0;
+        sl.device_scalars = deviceScalars ? 1 : 0;
+        sl.alpha_re = alpha;
+        sl.beta_re = beta;
+        sl.alpha_ptr = alphaPtr;
+        sl.beta_ptr = betaPtr;
+        return LaunchSpmvOpStreamFixed(sl, static_cast<float*>(z), stream);
+    }
 }
 
 }  // namespace aclsp
