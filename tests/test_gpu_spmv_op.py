@@ -359,3 +359,28 @@ def test_alg2_row_blocks_reproducible_and_correctly_rounded(i64, dev):
     ulp = np.spacing(np.abs(g32)).astype(np.float64)
     err = np.abs(outs[0].astype(np.float64) - golden)
     assert np.all(err <= 2 * ulp + 1e-12 * scale), float(np.max(err / (ulp + 1e-30)))
+
+
+@pytest.mark.parametrize("alg", [SpMVOpAlg.ALG1, SpMVOpAlg.ALG2])
+@pytest.mark.parametrize("i64", [False, True])
+def test_one_based_indices_and_long_rows(alg, i64, dev):
+    """Index base 1 (row offsets and columns), rows from empty to several chunks long."""
+    rng = np.random.default_rng(5)
+    lengths = np.concatenate([rng.integers(0, 7, 3000), [1500, 0, 40, 700], rng.integers(0, 20, 500)])
+    m, k = lengths.size, 4000
+    rp = np.zeros(m + 1, np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    col = rng.integers(0, k, int(rp[-1])).astype(np.int32)
+    val = rng.uniform(-3, 3, col.size).astype(np.float32)
+    x = rng.uniform(-3, 3, k).astype(np.float32)
+    y = rng.uniform(-3, 3, m).astype(np.float32)
+    d_rp = torch.from_numpy(rp + 1).to(torch.int64 if i64 else torch.int32).to(dev)
+    d = [torch.from_numpy(a).to(dev) for a in (col + 1, val, x, y)]
+    z = torch.full((m,), float("nan"), device=dev)
+    op = SpMVOp(m, k, d_rp, *d, z, alg=alg, base=1)
+    op.run(0.75, 1.5)
+    torch.cuda.synchronize()
+    golden = oracle.spmv_f64(rp, col, val, x, y, 0.75, 1.5).astype(np.float32)
+    ok, mere, mare = oracle.verify_mere_mare(golden, z.cpu().numpy(), 1e-6, 5.0)
+    assert ok, (mere, mare)
+    op.close()
