@@ -2201,8 +2201,8 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     RowBlockParams p = MakeRowBlockParams(l);
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
-    // The wave kernel issues its loads unconditionally (clamped into the
-    // arrays), which needs at least one 16-byte group of col_ind / values.
+    // The stream kernels read col_ind / values as 16-byte groups of arrays
+    // that start 16-byte aligned, with unit strides.
     const bool vec = kCanVec && l.nnz >= 4 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 &&
                      l.y_stride == 1 && Aligned16(l.col) && Aligned16(l.val);
     if constexpr (kCanVec && A == AccKind::F32) {
