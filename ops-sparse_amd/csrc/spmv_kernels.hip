@@ -937,59 +937,39 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
 
     // Phase 1.
     float sum[2] = {0.0f, 0.0f};
-    if (wide) {
-        // rows of up to 16 entries: per row, 16 predicated reads issued
-        // before one wait
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            v2f e[8];
-            const int32_t len = fin[h] ? re[h] - rs[h] : 0;
-            const uint32_t addr = LdsAddr(sVal + (fin[h] ? rs[h] - shift : 0));
-            asm volatile("ds_read2_b32 %0, %8 offset1:1\n\t"
-                         "ds_read2_b32 %1, %8 offset0:2 offset1:3\n\t"
-                         "ds_read2_b32 %2, %8 offset0:4 offset1:5\n\t"
-                         "ds_read2_b32 %3, %8 offset0:6 offset1:7\n\t"
-                         "ds_read2_b32 %4, %8 offset0:8 offset1:9\n\t"
-                         "ds_read2_b32 %5, %8 offset0:10 offset1:11\n\t"
-                         "ds_read2_b32 %6, %8 offset0:12 offset1:13\n\t"
-                         "ds_read2_b32 %7, %8 offset0:14 offset1:15"
-                         : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3]), "=&v"(e[4]), "=&v"(e[5]),
-                           "=&v"(e[6]), "=&v"(e[7])
-                         : "v"(addr));
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]),
-                           "+v"(e[7]));
-            float acc = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) acc += t < len ? e[t >> 1][t & 1] : 0.0f;
-            sum[h] = acc;
-        }
-    } else if (lg == 0) {
-        // One lane per row, at most 8 entries: 8 predicated reads per row,
-        // no branch.  All 16 reads are issued before one wait (the
-        // compiler's own schedule waits after each read pair).
-        v2f e[2][4];
+    if (lg == 0) {
+        // One lane per row: 8 predicated LDS reads per row, all issued
+        // before one wait (the compiler's own schedule waits after each read
+        // pair); a second round of 8 when some row has 9-16 entries.
         int32_t len[2];
+        uint32_t addr[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             len[h] = fin[h] ? re[h] - rs[h] : 0;
-            const uint32_t addr = LdsAddr(sVal + (fin[h] ? rs[h] - shift : 0));
-            asm volatile("ds_read2_b32 %0, %4 offset1:1\n\t"
-                         "ds_read2_b32 %1, %4 offset0:2 offset1:3\n\t"
-                         "ds_read2_b32 %2, %4 offset0:4 offset1:5\n\t"
-                         "ds_read2_b32 %3, %4 offset0:6 offset1:7"
-                         : "=&v"(e[h][0]), "=&v"(e[h][1]), "=&v"(e[h][2]), "=&v"(e[h][3])
-                         : "v"(addr));
+            addr[h] = LdsAddr(sVal + (fin[h] ? rs[h] - shift : 0));
         }
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(e[0][0]), "+v"(e[0][1]), "+v"(e[0][2]), "+v"(e[0][3]), "+v"(e[1][0]), "+v"(e[1][1]),
-                       "+v"(e[1][2]), "+v"(e[1][3]));
+        for (int round = 0; round < 2; ++round) {
+            if (round == 1 && !wide) break;
+            v2f e[2][4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float acc = 0.0f;
+            for (int h = 0; h < 2; ++h) {
+                asm volatile("ds_read2_b32 %0, %4 offset1:1\n\t"
+                             "ds_read2_b32 %1, %4 offset0:2 offset1:3\n\t"
+                             "ds_read2_b32 %2, %4 offset0:4 offset1:5\n\t"
+                             "ds_read2_b32 %3, %4 offset0:6 offset1:7"
+                             : "=&v"(e[h][0]), "=&v"(e[h][1]), "=&v"(e[h][2]), "=&v"(e[h][3])
+                             : "v"(addr[h] + 32U * round));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(e[0][0]), "+v"(e[0][1]), "+v"(e[0][2]), "+v"(e[0][3]), "+v"(e[1][0]), "+v"(e[1][1]),
+                           "+v"(e[1][2]), "+v"(e[1][3]));
 #pragma unroll
-            for (int t = 0; t < kSerialCapOne; ++t) acc += t < len[h] ? e[h][t >> 1][t & 1] : 0.0f;
-            sum[h] = acc;
+            for (int h = 0; h < 2; ++h) {
+                float acc = sum[h];
+#pragma unroll
+                for (int t = 0; t < kSerialCapOne; ++t) acc += t + 8 * round < len[h] ? e[h][t >> 1][t & 1] : 0.0f;
+                sum[h] = acc;
+            }
         }
     } else {
         // Group g = lane >> lg reduces row g (nr <= 32 here); lane g/2 holds
