@@ -586,3 +586,40 @@ def test_rows_of_nine_to_sixteen_entries(per, dev):
     w.y0 = torch.rand(30000, generator=g) * 2 - 1
     _, y, _ = run_workload(w, dev)
     assert_close(w, y)
+
+
+@pytest.mark.parametrize("name,trans", [("c2", "N"), ("c3", "N"), ("c5", "T")])
+def test_hip_graph_capture_and_replay(name, trans, dev):
+    """aclsparseSpMV enqueues only kernels (no memsets or copies), so a caller can capture it in a
+    HIP graph; every replay, with eager work and synchronisations in between, matches eager runs
+    bit for bit (long-row task counters are reset by each block's last task)."""
+    w = wl.config(name, "cpu", 64)
+    w.trans = trans
+    d = w.to(dev)
+    s = torch.cuda.Stream()
+    y = d.y0.clone()
+    with torch.cuda.stream(s):
+        plan = CsrSpMV(w.rows, w.cols, d.row_ptr, d.col_ind, d.values, d.x, y, w.alpha, w.beta, op=OP[trans])
+        plan.preprocess()
+    torch.cuda.synchronize()
+    y.copy_(d.y0)
+    with torch.cuda.stream(s):
+        plan.run()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    assert_close(w, eager)
+    g = torch.cuda.CUDAGraph()
+    y.copy_(d.y0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        plan.run()
+    for _ in range(3):
+        y.copy_(d.y0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        with torch.cuda.stream(s):  # eager work between replays
+            plan.run()
+        torch.cuda.synchronize()
