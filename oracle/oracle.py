@@ -94,6 +94,19 @@ def spmv_f64(row_ptr, col, val, x, y, alpha, beta):
     return z
 
 
+def spmv_f64_threads(row_ptr, col, val, x, y, alpha, beta, threads):
+    """spmv_f64 split over `threads` POSIX threads by row ranges (same per-row arithmetic)."""
+    rp = _i64(row_ptr)
+    rows = rp.size - 1
+    z = np.empty(rows, dtype=np.float64)
+    st = lib().oracle_spmv_f64_threads(_I(rows), _p(rp), _p(_c(col, np.int32)), _p(_c(val, np.float32)),
+                                       _p(_c(x, np.float32)), _p(_c(y, np.float32)), _D(alpha), _D(beta), _p(z),
+                                       ctypes.c_int(int(threads)))
+    if st != 0:
+        raise RuntimeError("oracle_spmv_f64_threads failed")
+    return z
+
+
 def spmv_trans_f64(row_ptr, col, val, x, y, cols, alpha, beta):
     rp = _i64(row_ptr)
     rows = rp.size - 1

@@ -37,6 +37,7 @@
  * base-0 data: spmv_test.cpp ShiftCsrIndexBase); row offsets are int64.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -148,6 +149,56 @@ void oracle_spmv_f64(int64_t rows, const int64_t *rp, const int32_t *col, const 
         for (int64_t p = rp[i]; p < rp[i + 1]; ++p) sum += (double)val[p] * (double)x[col[p]];
         z[i] = alpha * sum + beta * (double)y[i];
     }
+}
+
+/* The same product split over nthreads POSIX threads by row ranges (this
+ * build's parallel restatement, used only as a labelled CPU baseline; the
+ * reference's host golden is the serial loop above). */
+struct oracle_par_arg {
+    int64_t r0, r1;
+    const int64_t *rp;
+    const int32_t *col;
+    const float *val, *x, *y;
+    double alpha, beta;
+    double *z;
+};
+
+static void *oracle_par_run(void *p)
+{
+    const struct oracle_par_arg *a = (const struct oracle_par_arg *)p;
+    for (int64_t i = a->r0; i < a->r1; ++i) {
+        double sum = 0.0;
+        for (int64_t q = a->rp[i]; q < a->rp[i + 1]; ++q) sum += (double)a->val[q] * (double)a->x[a->col[q]];
+        a->z[i] = a->alpha * sum + a->beta * (double)a->y[i];
+    }
+    return NULL;
+}
+
+int oracle_spmv_f64_threads(int64_t rows, const int64_t *rp, const int32_t *col, const float *val, const float *x,
+                            const float *y, double alpha, double beta, double *z, int nthreads)
+{
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    struct oracle_par_arg args[256];
+    for (int t = 0; t < nthreads; ++t) {
+        args[t].r0 = rows * t / nthreads;
+        args[t].r1 = rows * (t + 1) / nthreads;
+        args[t].rp = rp;
+        args[t].col = col;
+        args[t].val = val;
+        args[t].x = x;
+        args[t].y = y;
+        args[t].alpha = alpha;
+        args[t].beta = beta;
+        args[t].z = z;
+        if (pthread_create(&th[t], NULL, oracle_par_run, &args[t]) != 0) {
+            for (int u = 0; u < t; ++u) pthread_join(th[u], NULL);
+            return -1;
+        }
+    }
+    for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+    return 0;
 }
 
 /* z_j = beta*y_j + sum_i alpha*x_i*a_ij, rows with alpha*x_i == 0 skipped. */

@@ -415,3 +415,18 @@ def test_trans_lowp_and_row_scale_closed_forms():
     np.testing.assert_allclose(s, 2.0 * (abs(A) @ np.abs(xn.astype(np.float64))) + 0.5 * np.abs(yn), rtol=1e-12)
     st = oracle.row_scale(rp, col, val, x, y, oracle.K_F32, oracle.K_F32, -2.0, 0.5, transpose=True, cols=cols)
     np.testing.assert_allclose(st, 2.0 * (abs(A).T @ np.abs(x.astype(np.float64))) + 0.5 * np.abs(y), rtol=1e-12)
+
+
+def test_threaded_spmv_matches_serial_bit_for_bit():
+    # the parallel CPU baseline splits rows only: every row keeps the serial summation order
+    rng = np.random.default_rng(3)
+    lengths = rng.integers(0, 40, 5000)
+    rp = np.zeros(lengths.size + 1, np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    col = rng.integers(0, 700, int(rp[-1])).astype(np.int32)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal(700).astype(np.float32)
+    y = rng.standard_normal(lengths.size).astype(np.float32)
+    a = oracle.spmv_f64(rp, col, val, x, y, 1.5, -0.5)
+    for t in (1, 3, 8):
+        assert np.array_equal(oracle.spmv_f64_threads(rp, col, val, x, y, 1.5, -0.5, t), a)
