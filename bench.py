@@ -96,6 +96,8 @@ def dtype_variants(w):
         "c2_c64": Workload(w.name + "_c64", w.rows, w.cols, w.row_ptr, w.col_ind, c64(w.values), c64(w.x),
                            c64(w.y0), 1.5, 0.5, out_dtype=torch.complex64),
     }
+    out["c2_c64_H"] = Workload(w.name + "_c64_H", w.rows, w.cols, w.row_ptr, w.col_ind, out["c2_c64"].values,
+                               out["c2_c64"].x, out["c2_c64"].y0, 1.5, 0.5, trans="H", out_dtype=torch.complex64)
     return out
 
 
@@ -137,7 +139,7 @@ def measure(w, steps, warmup, flush_buf):
     from ops_sparse.spmv import CsrSpMV
     from ops_sparse._lib import Operation
 
-    op = Operation.NON_TRANSPOSE if w.trans == "N" else Operation.TRANSPOSE
+    op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]
     y = w.y0.to(w.out_dtype).clone()
     plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
     stream = torch.cuda.current_stream()

@@ -1310,6 +1310,18 @@ template <>
 struct GenVals<ValKind::C64> {
     v4f v[4];  // two complex values per 16 bytes
 };
+template <>
+struct GenVals<ValKind::UNIT> {
+};
+
+// Bytes of one gathered x element: the accumulator type for UNIT (the
+// transpose's column pass gathers its products), else the value type.
+template <ValKind V, AccKind A>
+constexpr int64_t GenXBytes()
+{
+    return V == ValKind::UNIT ? static_cast<int64_t>(sizeof(typename AccOf<A>::T))
+                              : static_cast<int64_t>(sizeof(typename ValOf<V>::T));
+}
 
 template <ValKind V, AccKind A>
 struct GenLoad {
@@ -1332,7 +1344,9 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
     b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
-    if constexpr (V == ValKind::I8) {
+    if constexpr (V == ValKind::UNIT) {
+        (void)rv;
+    } else if constexpr (V == ValKind::I8) {
         b.val.v[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
         b.val.v[1] = __builtin_amdgcn_raw_buffer_load_b32(rv, 256 + lane * 4, 0, kBufNonTemporal);
     } else if constexpr (V == ValKind::F32) {
@@ -1368,14 +1382,17 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             const int64_t k = s.a0 + StreamSlot(lane, j);
             if (k >= tailStart && k < p.nnz) {
                 b.col[j >> 2][j & 3] = p.col[k];
-                const ValT v = static_cast<const ValT*>(p.val)[k];
-                if constexpr (V == ValKind::I8) {
+                if constexpr (V == ValKind::UNIT) {
+                } else if constexpr (V == ValKind::I8) {
+                    const ValT v = static_cast<const ValT*>(p.val)[k];
                     const uint32_t sh = 8U * static_cast<uint32_t>(j & 3);
                     b.val.v[j >> 2] =
                         (b.val.v[j >> 2] & ~(0xFFU << sh)) | (static_cast<uint32_t>(static_cast<uint8_t>(v)) << sh);
                 } else if constexpr (V == ValKind::F32) {
+                    const ValT v = static_cast<const ValT*>(p.val)[k];
                     b.val.v[j >> 2][j & 3] = v;
                 } else {
+                    const ValT v = static_cast<const ValT*>(p.val)[k];
                     b.val.v[j >> 1][(j & 1) * 2] = v.re;
                     b.val.v[j >> 1][(j & 1) * 2 + 1] = v.im;
                 }
@@ -1385,9 +1402,19 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     const int32_t hiSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c1 - s.a0) : 0;
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
-        uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
+        uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) *
+                       static_cast<uint32_t>(GenXBytes<V, A>());
         off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
-        if constexpr (V == ValKind::I8) {
+        if constexpr (V == ValKind::UNIT) {
+            const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0,
+                                                                                     kGatherPolicy));
+            if constexpr (A == AccKind::C64) {
+                b.xg[j] = C64{__int_as_float(w.x), __int_as_float(w.y)};
+            } else {
+                b.xg[j] = static_cast<long long>((static_cast<uint64_t>(static_cast<uint32_t>(w.y)) << 32) |
+                                                 static_cast<uint32_t>(w.x));
+            }
+        } else if constexpr (V == ValKind::I8) {
             const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b8(rx, static_cast<int>(off), 0, kGatherPolicy);
             b.xg[j] = ToAcc<V, A>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
         } else if constexpr (V == ValKind::F32) {
@@ -1429,7 +1456,10 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
     using OutT = typename OutOf<O>::T;
     Acc prod[kLaneItems];
 #pragma unroll
-    for (int j = 0; j < kLaneItems; ++j) prod[j] = GenVal<V, A>(lc, j) * lc.xg[j];
+    for (int j = 0; j < kLaneItems; ++j) {
+        if constexpr (V == ValKind::UNIT) prod[j] = lc.xg[j];
+        else prod[j] = GenVal<V, A>(lc, j) * lc.xg[j];
+    }
     const int32_t c0 = cur.c0, c1 = cur.c1;
     const int32_t shift = static_cast<int32_t>(cur.a0 - cur.k0);
     const int nr = cur.nr;
@@ -1554,7 +1584,7 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
     Acc alpha, beta;
     LoadScalars<A>(p.s, alpha, beta);
     const bool betaNz = !IsZero(beta);
-    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
+    const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * GenXBytes<V, A>());
     const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
     const int64_t wg = static_cast<int64_t>(blockIdx.x);
     const int64_t per = static_cast<int64_t>(gridDim.x) / kXcds;
@@ -2294,6 +2324,31 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                     hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, false>), dim3(g),
                                        dim3(kWave * kFlatWaves), 0, stream, c);
                 }
+                return 0;
+            }
+        }
+        if constexpr (std::is_same<RowT, int32_t>::value && (A == AccKind::C64 || A == AccKind::I64)) {
+            // complex / int64 products: the same column pass on the stream
+            // loads of the int8/complex kernel (8-byte products as x)
+            if (l.y_stride == 1 && l.nnz <= 0x0FFFFFFFLL) {
+                RowBlockParams c = p;
+                c.rp = At<void>(l.ws, l.layout.colptr_offset);
+                c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
+                c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
+                c.num_blocks = l.layout.csc_num_blocks;
+                c.col = At<const int32_t>(l.ws, l.layout.csc_pos_offset);
+                c.col_stride = 1;
+                c.val = nullptr;
+                c.val_stride = 1;
+                c.x = q.prod;
+                c.x_stride = 1;
+                c.rows = n;
+                c.cols = l.nnz;
+                c.base = 0;
+                const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
+                const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+                hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::UNIT, O, A>), dim3(g),
+                                   dim3(kWave * kFlatWaves), 0, stream, c);
                 return 0;
             }
         }
