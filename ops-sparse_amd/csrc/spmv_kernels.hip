@@ -338,27 +338,9 @@ __device__ __forceinline__ typename AccOf<A>::T Product(typename ValOf<V>::T a, 
     return ToAcc<V, A>(a) * ToAcc<V, A>(x[c * xStride]);
 }
 
-// 16-byte (4 element) non-temporal loads of col_ind and values at an aligned
-// non-zero index g (g % 4 == 0, g + 4 <= nnz).
-template <ValKind V>
-__device__ __forceinline__ void Load4(const int32_t* col, const typename ValOf<V>::T* val, int64_t g, int32_t c[4],
-                                      typename ValOf<V>::T v[4])
-{
-    const v4i cc = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(col + g));
-    c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
-    if constexpr (V == ValKind::F32) {
-        const v4f vv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(val + g));
-        v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
-    } else {
-        static_assert(V == ValKind::F16 || V == ValKind::BF16, "vector path is for 32/16-bit values");
-        const v4u16 vv = __builtin_nontemporal_load(reinterpret_cast<const v4u16*>(val + g));
-        v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
-    }
-}
-
 // ------------------------- non-transpose row blocks -------------------------
 
-template <typename RowT, ValKind V, OutKind O, AccKind A, bool kVec>
+template <typename RowT, ValKind V, OutKind O, AccKind A>
 __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
@@ -396,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
     int32_t c0 = 0;
     for (;;) {
         const int64_t gStart = k0 + c0;
-        const int64_t a0 = kVec ? (gStart & ~static_cast<int64_t>(3)) : gStart;
+        const int64_t a0 = gStart;
         const int32_t d = static_cast<int32_t>(k0 - a0);  // LDS slot of relative offset r is r + d
         const int32_t lim = static_cast<int32_t>(a0 - k0) + kChunk;
         const int32_t c1 = kspan < lim ? kspan : lim;
@@ -405,43 +387,15 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
 
         for (int w = tid; w < kChunk / 4; w += kThreads) sFlagWords[w] = 0U;
 
-        // Stream col_ind / values of [gStart, gEnd) and form the products.
-        if constexpr (kVec) {
-            for (int v = tid; v < kChunk / 4; v += kThreads) {
-                const int64_t g = a0 + 4 * static_cast<int64_t>(v);
-                Acc prod[4] = {Zero<Acc>(), Zero<Acc>(), Zero<Acc>(), Zero<Acc>()};
-                if (g < gEnd) {
-                    int32_t c[4];
-                    ValT a[4];
-                    if (g + 4 <= p.nnz) {
-                        Load4<V>(p.col, val, g, c, a);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const bool in = g + e < p.nnz;
-                            c[e] = in ? p.col[g + e] : 0;
-                            a[e] = in ? val[g + e] : ValT{};
-                        }
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const bool valid = g + e >= gStart && g + e < gEnd;
-                        prod[e] = Product<V, A>(a[e], c[e], x, 1, p.base, p.cols, valid);
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sVal[Pad(4 * v + e)] = prod[e];
+        // Read col_ind / values of [gStart, gEnd) (any strides) and form the products.
+        for (int q = tid; q < kChunk; q += kThreads) {
+            const int64_t g = a0 + q;
+            Acc prod = Zero<Acc>();
+            if (g < gEnd) {
+                prod = Product<V, A>(val[g * p.val_stride], p.col[g * p.col_stride], x, p.x_stride, p.base,
+                                     p.cols, true);
             }
-        } else {
-            for (int q = tid; q < kChunk; q += kThreads) {
-                const int64_t g = a0 + q;
-                Acc prod = Zero<Acc>();
-                if (g < gEnd) {
-                    prod = Product<V, A>(val[g * p.val_stride], p.col[g * p.col_stride], x, p.x_stride, p.base,
-                                         p.cols, true);
-                }
-                sVal[Pad(q)] = prod;
-            }
+            sVal[Pad(q)] = prod;
         }
 
         __syncthreads();  // flag words are cleared before any lane sets a head
@@ -2257,7 +2211,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             return 0;
         }
     }
-    hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, p);
     return 0;
 }
 
