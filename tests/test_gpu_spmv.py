@@ -623,3 +623,52 @@ def test_hip_graph_capture_and_replay(name, trans, dev):
         with torch.cuda.stream(s):  # eager work between replays
             plan.run()
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("op", ["N", "T"])
+def test_strided_operands_mid_size(op, dev):
+    """Strided row offsets, col_ind, values, x and y (the general kernel) on a matrix with short,
+    empty and multi-chunk rows: results match the oracle and padding elements are untouched."""
+    g = torch.Generator().manual_seed(77)
+    lengths = torch.randint(0, 12, (3000,), generator=g)
+    lengths[::250] = 1500
+    rows, cols = lengths.numel(), 2500
+    rp, col = wl.csr_from_lengths(lengths.to(torch.int64), cols, g, "cpu")
+    n = col.numel()
+    val = torch.rand(n, generator=g) * 2 - 1
+    xlen, ylen = (rows, cols) if op == "T" else (cols, rows)
+    x = torch.rand(xlen, generator=g) * 2 - 1
+    y0 = torch.rand(ylen, generator=g) * 2 - 1
+    sr, sc, sv, sx, sy = 2, 3, 2, 2, 3
+    sent = -777.0
+
+    def spread(v, s, fill):
+        out = torch.full((v.numel() * s,), fill, dtype=v.dtype)
+        out[::s] = v
+        return out.to(dev)
+
+    d_rp = spread(rp.to(torch.int32), sr, -1)
+    d_col = spread(col, sc, -1)
+    d_val, d_x, d_y = spread(val, sv, sent), spread(x, sx, sent), spread(y0, sy, sent)
+    h = Handle(torch.cuda.current_stream().cuda_stream or _lib.HIP_NULL_STREAM)
+    mat = CsrDescr(rows, cols, d_rp[::sr], d_col[::sc], d_val[::sv])
+    mat.set_strides(sr, sc, sv)
+    vx, vy = DnVecDescr(xlen, d_x[::sx]), DnVecDescr(ylen, d_y[::sy])
+    vx.set_stride(sx)
+    vy.set_stride(sy)
+    a, b = HostScalar(1.25, DataType.FLOAT), HostScalar(-0.5, DataType.FLOAT)
+    lib = _lib.lib()
+    size = ctypes.c_size_t()
+    opv = int(OP[op])
+    assert lib.aclsparseSpMVGetBufferSize(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, 0, ctypes.byref(size)) == 0
+    ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
+    assert lib.aclsparseSpMVPreprocess(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, 0,
+                                       ctypes.c_void_p(ws.data_ptr())) == 0
+    assert lib.aclsparseSpMV(h.h, opv, a.ptr, mat.d, vx.d, b.ptr, vy.d, 0, 0, ctypes.c_void_p(ws.data_ptr())) == 0
+    torch.cuda.synchronize()
+    got = d_y.cpu()
+    pad = torch.ones(got.numel(), dtype=torch.bool)
+    pad[::sy] = False
+    assert torch.all(got[pad] == sent)
+    w = wl.Workload("strided", rows, cols, rp.to(torch.int32), col, val, x, y0, 1.25, -0.5, trans=op)
+    assert_close(w, got[::sy].contiguous())
