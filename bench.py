@@ -55,7 +55,7 @@ def profile_mode(name, steps):
     dev = torch.device("cuda:0")
     w = make(name, dev)
     y = w.y0.to(w.out_dtype).clone()
-    op = Operation.NON_TRANSPOSE if w.trans == "N" else Operation.TRANSPOSE
+    op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]
     plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
     plan.preprocess()
     flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
@@ -108,6 +108,8 @@ def make(name, dev):
         return wl.uniform_rows_lowp(device=dev, dtype=torch.float16)
     if name == "c4b":
         return wl.uniform_rows_lowp(device=dev, dtype=torch.bfloat16)
+    if name.startswith("c2_") and not name.startswith("c2_spmvop"):
+        return dtype_variants(wl.config("c2", dev))[name]
     return wl.config(name, dev)
 
 

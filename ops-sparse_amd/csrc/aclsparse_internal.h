@@ -181,6 +181,12 @@ struct SpmvLayout {
     // column pass on the stream kernel: csc_blocks int32[Bc+1], csc_block_nnz RowT[Bc+1]
     size_t csc_blocks_offset = 0, csc_block_nnz_offset = 0;
     int64_t csc_items_per_block = 0, csc_num_blocks = 0;
+    // compact entry rows for the product pass: per group of kRowGroup
+    // entries in CSR order, group_row int32[G] (the row of the group's first
+    // entry, or -1 when the group spans more than 255 rows: then entry_row
+    // holds its rows) and row_delta uint8[G*kRowGroup] (row - group_row)
+    size_t group_row_offset = 0, row_delta_offset = 0;
+    int64_t row_groups = 0;
     size_t key_a_offset = 0, key_b_offset = 0, val_b_offset = 0, sort_offset = 0, sort_bytes = 0;
     // Long-block tasks (non-transpose, fp32 compute): a block of more than
     // kLongChunks chunks is split into one task per chunk.  task_start[B+1]
@@ -204,6 +210,9 @@ size_t TaskScanTempBytes(int64_t n);
 
 // Radix-sort temporary storage for the CSC build (implemented in spmv_kernels.hip).
 size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes);
+
+// Entries per group of the transpose's compact row table (one wave of 4 entries per lane).
+constexpr int64_t kRowGroup = 256;
 
 inline size_t AccumulatorBytes(aclDataType computeType)
 {
@@ -263,7 +272,11 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.csc_blocks_offset = AlignUp(l.sort_offset + l.sort_bytes + 256);  // sort temp re-aligned to 256 at use
             l.csc_block_nnz_offset =
                 AlignUp(l.csc_blocks_offset + static_cast<size_t>(l.csc_num_blocks + 1) * sizeof(int32_t));
-            l.total = AlignUp(l.csc_block_nnz_offset + static_cast<size_t>(l.csc_num_blocks + 1) * rb);
+            l.row_groups = static_cast<int64_t>((n + kRowGroup - 1) / kRowGroup);
+            l.group_row_offset =
+                AlignUp(l.csc_block_nnz_offset + static_cast<size_t>(l.csc_num_blocks + 1) * rb);
+            l.row_delta_offset = AlignUp(l.group_row_offset + static_cast<size_t>(l.row_groups) * sizeof(int32_t));
+            l.total = AlignUp(l.row_delta_offset + static_cast<size_t>(l.row_groups) * kRowGroup);
         }
     }
     return l;

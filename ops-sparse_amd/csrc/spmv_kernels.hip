@@ -1937,9 +1937,39 @@ __global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPo
 }
 
 
+// Compact row table: one workgroup per group of kRowGroup entries.  Rows are
+// non-decreasing over [norm[0], norm[rows]), so the span of a group is its
+// last in-range row minus its first; entries outside that range get delta 0.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void CscRowDeltaKernel(const int32_t* entryRow, const RowT* norm, int64_t rows,
+                                                              int32_t* groupRow, uint8_t* delta)
+{
+    static_assert(kRowGroup == kThreads, "one thread per entry of a group");
+    const int64_t g = blockIdx.x;
+    const int64_t first = static_cast<int64_t>(norm[0]);
+    const int64_t last = static_cast<int64_t>(norm[rows]);
+    int64_t kf = g * kRowGroup, kl = kf + kRowGroup - 1;
+    kf = kf > first ? kf : first;
+    kl = kl < last - 1 ? kl : last - 1;
+    int32_t base = 0;
+    bool narrow = true;
+    if (kf <= kl) {
+        base = entryRow[kf];
+        narrow = entryRow[kl] - base <= 255;
+    }
+    const int64_t k = g * kRowGroup + threadIdx.x;
+    const int32_t r = k >= kf && k <= kl ? entryRow[k] : base;
+    delta[k] = narrow ? static_cast<uint8_t>(r - base) : uint8_t{0};
+    // a group with no entry inside the matrix takes the per-entry path (it reads nothing)
+    if (threadIdx.x == 0) groupRow[g] = narrow && kf <= kl ? base : -1;
+}
+
 struct CscParams {
     const void* colptr;  // RowT[cols+1]
     const int32_t* entry_row;
+    const int32_t* group_row;   // compact row table (see the workspace layout)
+    const uint32_t* row_delta;  // four 8-bit deltas per dword
+    int64_t row_groups;
     const void* pos;     // RowT[nnz]
     void* prod;          // Acc[nnz]
     const void* val;
@@ -1956,39 +1986,109 @@ struct CscParams {
     Scalars s;
 };
 
-// Pass 1, in CSR order: prod[k] = conj?(a_k) * x[row(k)].  A pure stream:
-// values, entry rows and products are read/written once, contiguously, and
-// x is read in row order.
-template <typename RowT, ValKind V, AccKind A>
+// Four consecutive elements, moved by one vector access.
+template <typename T>
+struct alignas(4 * sizeof(T)) Quad {
+    T v[4];
+};
+
+// Pass 1, in CSR order: prod[k] = conj?(a_k) * x[row(k)].  One wave per
+// group of kRowGroup entries, four consecutive entries per lane.  The rows
+// come from the compact table: one dword of 8-bit deltas per lane over the
+// group's first row, so the group's x values are the contiguous run
+// x[row0 .. row0 + span], which the wave reads once, coalesced, into LDS and
+// then indexes by delta.  A group spanning more than 255 rows reads its rows
+// from the int32 table and gathers x per entry (so does a strided x).
+// Values and products move as whole 4-entry vectors when the values are
+// contiguous and aligned (kVec; the products always are).
+template <typename RowT, ValKind V, AccKind A, bool kVec>
 __global__ __launch_bounds__(kThreads) void CscProductKernel(CscParams q)
 {
     using Acc = typename AccOf<A>::T;
     using ValT = typename ValOf<V>::T;
+    static_assert(kRowGroup == 4 * kWave, "a group is one wave of 4 entries per lane");
+    __shared__ ValT sx[kThreads / kWave][kRowGroup];
     const ValT* val = static_cast<const ValT*>(q.val);
     const ValT* x = static_cast<const ValT*>(q.x);
     Acc* prod = static_cast<Acc*>(q.prod);
     const RowT* norm = static_cast<const RowT*>(q.norm);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wv;
+    if (g >= q.row_groups) return;
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int64_t first = static_cast<int64_t>(norm[0]);
     const int64_t last = static_cast<int64_t>(norm[q.rows]);
-    // 4 entries per thread and step (kThreads apart, so every load stays
-    // coalesced) to keep more row-index -> x dependencies in flight
-    constexpr int kU = 4;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * kThreads * kU;
-    for (int64_t k0 = first + blockIdx.x * static_cast<int64_t>(kThreads) * kU + threadIdx.x; k0 < last;
-         k0 += step) {
-        int32_t r[kU];
-        ValT v[kU];
+    const int64_t k0 = g * kRowGroup + 4 * lane;
+    const bool full = k0 >= first && k0 + 4 <= last;
+    const int32_t gr = ConstLoad<int32_t>(q.group_row, g);
+    const bool run = gr >= 0 && q.x_stride == 1;  // wave-uniform
+    int32_t row[4];
+    if (gr >= 0) {
+        const uint32_t d = q.row_delta[g * (kRowGroup / 4) + lane];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t k = k0 + u * kThreads;
-            r[u] = k < last ? q.entry_row[k] : 0;
-            v[u] = k < last ? val[k * q.val_stride] : ValT{};
+        for (int u = 0; u < 4; ++u) row[u] = static_cast<int32_t>((d >> (8 * u)) & 0xFFU);
+    } else if (full) {
+        const v4i r = *reinterpret_cast<const v4i*>(q.entry_row + k0);
+        row[0] = r.x;
+        row[1] = r.y;
+        row[2] = r.z;
+        row[3] = r.w;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) row[u] = k0 + u >= first && k0 + u < last ? q.entry_row[k0 + u] : 0;
+    }
+    ValT v[4];
+    if (kVec && full) {
+        const Quad<ValT> w = *reinterpret_cast<const Quad<ValT>*>(val + k0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = w.v[u];
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = k0 + u;
+            v[u] = k >= first && k < last ? val[k * q.val_stride] : ValT{};
+        }
+    }
+    ValT xv[4];
+    if (run) {
+        // span = largest delta of the group (entries outside the matrix have delta 0)
+        int span = row[0] > row[1] ? row[0] : row[1];
+        span = span > row[2] ? span : row[2];
+        span = span > row[3] ? span : row[3];
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const int o = __shfl_xor(span, m, kWave);
+            span = span > o ? span : o;
         }
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t k = k0 + u * kThreads;
-            const Acc xr = ToAcc<V, A>(x[static_cast<int64_t>(r[u]) * q.x_stride]);
-            if (k < last) prod[k] = MaybeConj<V, A>(ToAcc<V, A>(v[u]), q.conj) * xr;
+        for (int j = 0; j < kRowGroup / kWave; ++j) {
+            const int i = lane + j * kWave;
+            if (j * kWave <= span && i <= span) sx[wv][i] = x[static_cast<int64_t>(gr) + i];
+        }
+        WaveLdsSync();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xv[u] = sx[wv][row[u]];
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t r = static_cast<int64_t>(gr >= 0 ? gr + row[u] : row[u]);
+            xv[u] = k0 + u >= first && k0 + u < last ? x[r * q.x_stride] : ValT{};
+        }
+    }
+    Quad<Acc> out;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t k = k0 + u;
+        const Acc xr = k >= first && k < last ? ToAcc<V, A>(xv[u]) : Zero<Acc>();
+        out.v[u] = MaybeConj<V, A>(ToAcc<V, A>(v[u]), q.conj) * xr;
+    }
+    if (full) {
+        *reinterpret_cast<Quad<Acc>*>(prod + k0) = out;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = k0 + u;
+            if (k >= first && k < last) prod[k] = out.v[u];
         }
     }
 }
@@ -2246,7 +2346,16 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         q.lg = lg;
         const int64_t threads = n << lg;
         const unsigned grid = static_cast<unsigned>((threads + kThreads - 1) / kThreads);
-        hipLaunchKernelGGL((CscProductKernel<RowT, V, A>), dim3(GridFor((l.nnz + 3) / 4)), dim3(kThreads), 0, stream, q);
+        q.group_row = At<const int32_t>(l.ws, l.layout.group_row_offset);
+        q.row_delta = At<const uint32_t>(l.ws, l.layout.row_delta_offset);
+        q.row_groups = l.layout.row_groups;
+        const dim3 pg(static_cast<unsigned>((l.layout.row_groups + kThreads / kWave - 1) / (kThreads / kWave)));
+        using ValT = typename ValOf<V>::T;
+        if (l.val_stride == 1 && reinterpret_cast<uintptr_t>(l.val) % (4 * sizeof(ValT)) == 0) {
+            hipLaunchKernelGGL((CscProductKernel<RowT, V, A, true>), pg, dim3(kThreads), 0, stream, q);
+        } else {
+            hipLaunchKernelGGL((CscProductKernel<RowT, V, A, false>), pg, dim3(kThreads), 0, stream, q);
+        }
         if constexpr (std::is_same<RowT, int32_t>::value && A == AccKind::F32 && O != OutKind::I32) {
             // fp32 products and 32-bit positions: the column pass is an SpMV
             // of the CSC pattern (unit values) with the products as x, on the
@@ -2444,6 +2553,10 @@ int BuildCsc(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL((CscFinishKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, vals.Current(),
                        At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.entry_row_offset),
                        At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, nnz);
+    hipLaunchKernelGGL((CscRowDeltaKernel<RowT>), dim3(static_cast<unsigned>(l.layout.row_groups)), dim3(kThreads),
+                       0, s, At<const int32_t>(l.ws, l.layout.entry_row_offset),
+                       At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows,
+                       At<int32_t>(l.ws, l.layout.group_row_offset), At<uint8_t>(l.ws, l.layout.row_delta_offset));
     // Row-block partition of the columns (the column pass runs the stream
     // kernel on the CSC pattern); colptr is already normalised, so the
     // partition kernel rewrites it in place with the same values.

@@ -672,3 +672,38 @@ def test_strided_operands_mid_size(op, dev):
     assert torch.all(got[pad] == sent)
     w = wl.Workload("strided", rows, cols, rp.to(torch.int32), col, val, x, y0, 1.25, -0.5, trans=op)
     assert_close(w, got[::sy].contiguous())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.complex64])
+def test_transpose_groups_spanning_many_rows(dtype, dev):
+    """The transpose's product pass reads rows as 8-bit deltas per 256-entry group; groups that
+    span more than 255 rows (runs of empty rows) fall back to the int32 row table and per-entry x
+    reads. Mixed in one matrix: dense stretches, sparse stretches, a block of empty rows."""
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.zeros(120000, dtype=torch.int64)
+    lengths[:20000] = torch.randint(0, 9, (20000,), generator=g)      # narrow groups
+    lengths[20000:80000:397] = 1                                      # one entry per 397 rows
+    lengths[80000:80300] = 3
+    lengths[100000::1000] = torch.randint(1, 300, (20,), generator=g)  # long rows far apart
+    rp, col = wl.csr_from_lengths(lengths, 5000, g, "cpu", distinct=False)
+    n = col.numel()
+    u = lambda k: torch.rand(k, generator=g) * 2 - 1
+    if dtype == torch.complex64:
+        val, x, y0 = torch.complex(u(n), u(n)), torch.complex(u(120000), u(120000)), torch.complex(u(5000), u(5000))
+        got = _run_complex_t(rp, col, val, x, y0, dev)
+        ref = oracle.spmv_c64(rp.numpy(), col.numpy(), val.numpy(), x.numpy(), y0.numpy(), 5000, 1, 1.5, 0.5)
+        np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=1e-4 * max(1.0, float(np.abs(ref).max())))
+        return
+    w = wl.Workload("span", lengths.numel(), 5000, rp.to(torch.int32), col, u(n), u(120000), u(5000), 1.5, -0.5,
+                    trans="T")
+    _, y, _ = run_workload(w, dev)
+    assert_close(w, y)
+
+
+def _run_complex_t(rp, col, val, x, y0, dev):
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(rp.numel() - 1, y0.numel(), rp.to(torch.int32).to(dev), col.to(dev), val.to(dev), x.to(dev), y,
+                   complex(1.5, 0), complex(0.5, 0), op=OP["T"])
+    plan.run()
+    torch.cuda.synchronize()
+    return y.cpu()
