@@ -75,6 +75,30 @@ typedef struct aclsparseDnVecDescr* aclsparseDnVecDescr_t;
 typedef struct aclsparseSpMatDescr const* aclsparseConstSpMatDescr_t;
 typedef struct aclsparseDnVecDescr const* aclsparseConstDnVecDescr_t;
 
+/* include/cann_ops_sparse.h:63-66 */
+typedef enum aclsparseOrder_t {
+    ACL_SPARSE_ORDER_ROW = 0,
+    ACL_SPARSE_ORDER_COL = 1
+} aclsparseOrder_t;
+
+struct aclsparseDnMatDescr;
+typedef struct aclsparseDnMatDescr* aclsparseDnMatDescr_t;
+typedef struct aclsparseDnMatDescr const* aclsparseConstDnMatDescr_t;
+
+/* include/cann_ops_sparse.h:2412-2417 */
+typedef enum aclsparseSpMMOpAlg_t {
+    ACL_SPARSE_SPMMOP_ALG_DEFAULT = 0,
+    ACL_SPARSE_SPMMOP_ALG1 = 1,
+    ACL_SPARSE_SPMMOP_ALG2 = 2,
+    ACL_SPARSE_SPMMOP_ALG1_HIGH_PRECISION = 3
+} aclsparseSpMMOpAlg_t;
+
+struct aclsparseSpMMOpDescr;
+struct aclsparseSpMMOpPlan;
+typedef struct aclsparseSpMMOpDescr* aclsparseSpMMOpDescr_t;
+typedef struct aclsparseSpMMOpDescr const* aclsparseConstSpMMOpDescr_t;
+typedef struct aclsparseSpMMOpPlan* aclsparseSpMMOpPlan_t;
+
 /* include/cann_ops_sparse.h:69-83 */
 typedef enum aclsparseSpMVOpAlg_t {
     ACL_SPARSE_SPMVOP_ALG_DEFAULT = 0,
@@ -280,6 +304,60 @@ aclsparseStatus_t aclsparseSpMVOp_setGlobalUserData(aclsparseHandle_t handle, ac
 aclsparseStatus_t aclsparseSpMVOp(aclsparseHandle_t handle, aclsparseSpMVOpPlan_t plan, const void* alpha,
                                   const void* beta, aclsparseConstDnVecDescr_t vecX, aclsparseConstDnVecDescr_t vecY,
                                   aclsparseDnVecDescr_t vecZ);
+
+/* ---------------- dense matrix descriptor (sparse/common/aclsparse_descr.cpp:1102-1302) ---------------- */
+
+/* replaces include/cann_ops_sparse.h:1028 */
+aclsparseStatus_t aclsparseCreateDnMat(aclsparseDnMatDescr_t* dnMatDescr, int64_t rows, int64_t cols, int64_t ld,
+                                       void* values, aclDataType valueType, aclsparseOrder_t order);
+/* replaces include/cann_ops_sparse.h:1036 */
+aclsparseStatus_t aclsparseCreateConstDnMat(aclsparseConstDnMatDescr_t* dnMatDescr, int64_t rows, int64_t cols,
+                                            int64_t ld, const void* values, aclDataType valueType,
+                                            aclsparseOrder_t order);
+/* replaces include/cann_ops_sparse.h:1045 */
+aclsparseStatus_t aclsparseDestroyDnMat(aclsparseConstDnMatDescr_t dnMatDescr);
+/* replaces include/cann_ops_sparse.h:1061 */
+aclsparseStatus_t aclsparseDnMatGet(aclsparseDnMatDescr_t dnMatDescr, int64_t* rows, int64_t* cols, int64_t* ld,
+                                    void** values, aclDataType* valueType, aclsparseOrder_t* order);
+/* replaces include/cann_ops_sparse.h:1070 */
+aclsparseStatus_t aclsparseConstDnMatGet(aclsparseConstDnMatDescr_t dnMatDescr, int64_t* rows, int64_t* cols,
+                                         int64_t* ld, const void** values, aclDataType* valueType,
+                                         aclsparseOrder_t* order);
+/* replaces include/cann_ops_sparse.h:1081 */
+aclsparseStatus_t aclsparseDnMatGetValues(aclsparseDnMatDescr_t dnMatDescr, void** values);
+/* replaces include/cann_ops_sparse.h:1086 */
+aclsparseStatus_t aclsparseConstDnMatGetValues(aclsparseConstDnMatDescr_t dnMatDescr, const void** values);
+/* replaces include/cann_ops_sparse.h:1095 */
+aclsparseStatus_t aclsparseDnMatSetValues(aclsparseDnMatDescr_t dnMatDescr, void* values);
+
+/* ---------------- SpMMOp (include/cann_ops_sparse.h:2399-2497) ---------------- */
+
+/* replaces include/cann_ops_sparse.h:2431 (sparse/spmm_op/arch35/spmm_op_host.cpp:695-740) */
+aclsparseStatus_t aclsparseSpMMOp_bufferSize(aclsparseHandle_t handle, aclsparseOperation_t opA,
+                                             aclsparseOperation_t opB, aclsparseConstSpMatDescr_t matA,
+                                             aclsparseConstDnMatDescr_t matB, aclsparseDnMatDescr_t matC,
+                                             aclDataType computeType, aclsparseSpMMOpAlg_t alg, size_t* bufferSize);
+/* replaces include/cann_ops_sparse.h:2442 (sparse/spmm_op/arch35/spmm_op_host.cpp:961-1002) */
+aclsparseStatus_t aclsparseSpMMOp_createDescr(aclsparseHandle_t handle, aclsparseSpMMOpDescr_t* descr,
+                                              aclsparseOperation_t opA, aclsparseOperation_t opB,
+                                              aclsparseConstSpMatDescr_t matA, aclsparseConstDnMatDescr_t matB,
+                                              aclsparseDnMatDescr_t matC, aclDataType computeType,
+                                              aclsparseSpMMOpAlg_t alg, void* buffer);
+/* replaces include/cann_ops_sparse.h:2452 (sparse/spmm_op/arch35/spmm_op_host.cpp:1005-1012) */
+aclsparseStatus_t aclsparseSpMMOp_destroyDescr(aclsparseSpMMOpDescr_t descr);
+/* replaces include/cann_ops_sparse.h:2458 (sparse/spmm_op/arch35/spmm_op_host.cpp:1015-1043) */
+aclsparseStatus_t aclsparseSpMMOp_createPlan(aclsparseHandle_t handle, aclsparseSpMMOpDescr_t descr,
+                                             aclsparseSpMMOpPlan_t* plan, const void* epilogueLTOBuffer,
+                                             size_t epilogueLTOBufferSize);
+/* replaces include/cann_ops_sparse.h:2467 (sparse/spmm_op/arch35/spmm_op_host.cpp:1046-1053) */
+aclsparseStatus_t aclsparseSpMMOp_destroyPlan(aclsparseSpMMOpPlan_t plan);
+/* replaces include/cann_ops_sparse.h:2473 (sparse/spmm_op/arch35/spmm_op_host.cpp:1056-1080) */
+aclsparseStatus_t aclsparseSpMMOp_setGlobalUserData(aclsparseHandle_t handle, aclsparseSpMMOpPlan_t plan,
+                                                    const char* epilogueDataName, void* epilogueData,
+                                                    size_t epilogueDataSize);
+/* replaces include/cann_ops_sparse.h:2484 (sparse/spmm_op/arch35/spmm_op_host.cpp:1083-1102) */
+aclsparseStatus_t aclsparseSpMMOp(aclsparseHandle_t handle, aclsparseSpMMOpPlan_t plan, const void* alpha,
+                                  const void* beta, aclsparseConstDnMatDescr_t matB, aclsparseDnMatDescr_t matC);
 
 #ifdef __cplusplus
 }

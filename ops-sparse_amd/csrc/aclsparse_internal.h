@@ -18,6 +18,9 @@ constexpr uint32_t kSpMatSignature = 0x53504D54U;
 constexpr uint32_t kDnVecSignature = 0xD0D2D4D6U;
 constexpr uint32_t kSpMVOpDescrSignature = 0x534D5644U;  // "SMVD"
 constexpr uint32_t kSpMVOpPlanSignature = 0x534D5650U;   // "SMVP"
+constexpr uint32_t kDnMatSignature = 0xD0D2D4D8U;
+constexpr uint32_t kSpMMOpDescrSignature = 0x534D4D44U;  // "SMMD"
+constexpr uint32_t kSpMMOpPlanSignature = 0x534D4D50U;   // "SMMP"
 
 constexpr int kVersion = 10000;  // 1.0.0, encoded MAJOR*10000+MINOR*100+PATCH
 constexpr size_t kDefaultWorkspaceBytes = 4U * 1024U * 1024U;
@@ -79,6 +82,14 @@ struct aclsparseDnVecDescr {
     void* values = nullptr;
     aclDataType value_type = ACL_FLOAT;
     int64_t stride = 1;
+};
+
+struct aclsparseDnMatDescr {
+    uint32_t signature = aclsp::kDnMatSignature;
+    int64_t rows = 0, cols = 0, ld = 0;
+    void* values = nullptr;
+    aclDataType value_type = ACL_FLOAT;
+    aclsparseOrder_t order = ACL_SPARSE_ORDER_ROW;
 };
 
 namespace aclsp {
@@ -384,4 +395,76 @@ int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream);
 int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
                         float beta, const void* alphaPtr, const void* betaPtr, bool deviceScalars, void* stream);
 
+
+// ---------------------------------------------------------------------------
+// SpMMOp: C = alpha*A*op(B) + beta*C, A CSR (fp32 or fp16, I32/I64 row
+// offsets), B and C dense in either order, fp32 accumulation.
+// ---------------------------------------------------------------------------
+// ALG2 workspace: the reference's part (sparse/spmm_op/arch35/spmm_op.h:63-81):
+//   [0,256) header | reorder[m] | bin_edge[bins+1], 64-byte aligned,
+// followed by this build's extension for the device-side table build:
+//   tmp_reorder[m] | lengths[m] | sorted lengths[m] | running[m] (int64) |
+//   sort/scan temporary storage.
+struct SpmmOpLayout {
+    size_t reorder = 0, bin_edge = 0, ref_total = 0;
+    size_t tmp_reorder = 0, scratch = 0, tmp_scratch = 0, running = 0, temp = 0, temp_bytes = 0, total = 0;
+};
+SpmmOpLayout SpmmOpComputeLayout(int64_t m, uint32_t bins);
+
+// Length-sorted row tables shared by SpMVOp and SpMMOp ALG2: reorder = rows
+// by length, descending, stable; binEdge[0..bins] splits the sorted rows into
+// bins of about ceil(total/bins) non-zeros, one edge per row at most.
+struct LengthTables {
+    const void* row_offsets;
+    bool rowptr64;
+    int64_t m;
+    uint32_t bins;
+    int32_t *reorder, *tmp_reorder, *scratch, *tmp_scratch, *bin_edge;
+    int64_t* running;
+    void* temp;
+    size_t temp_bytes;
+};
+int LaunchLengthTables(const LengthTables& t, void* stream);
+
+struct SpmmLaunch {
+    const void* row_offsets;
+    const int32_t* col_ind;
+    const void* values;
+    const void* b;
+    void* c;
+    int64_t m, k, n, ldb, ldc;
+    int32_t base;
+    int32_t rowptr64;
+    int32_t fp16;
+    int32_t high_precision;  // Kahan-compensated sums (fp32 only)
+    int32_t b_trans;         // opB = T
+    int32_t b_row_major, c_row_major;
+    int64_t nnz;
+    float alpha, beta;
+    const float* alpha_ptr;  // device pointer mode: read on the device
+    const float* beta_ptr;
+};
+int LaunchSpmmOp(const SpmmLaunch& l, void* stream);
+
 }  // namespace aclsp
+
+struct aclsparseSpMMOpDescr {
+    uint32_t signature = aclsp::kSpMMOpDescrSignature;
+    uint64_t m = 0, k = 0, nnz = 0;
+    aclsparseIndexBase_t base = ACL_SPARSE_INDEX_BASE_ZERO;
+    aclsparseIndexType_t row_type = ACL_SPARSE_INDEX_32I;
+    aclDataType value_type = ACL_FLOAT;
+    aclsparseOperation_t op_b = ACL_SPARSE_OP_NON_TRANSPOSE;
+    const void* row_offsets = nullptr;
+    const int32_t* col_ind = nullptr;
+    const void* values = nullptr;
+    aclsparseSpMMOpAlg_t alg = ACL_SPARSE_SPMMOP_ALG1;
+    void* buffer = nullptr;  // ALG2 tables (caller-owned)
+    uint32_t num_bins = 0;
+};
+
+struct aclsparseSpMMOpPlan {
+    uint32_t signature = aclsp::kSpMMOpPlanSignature;
+    aclsparseSpMMOpDescr* descr = nullptr;  // weak: the descriptor must outlive the plan
+    aclsparseSpMMOpAlg_t alg = ACL_SPARSE_SPMMOP_ALG1;
+};

@@ -2,10 +2,11 @@
 //
 // Semantics follow sparse/common/aclsparse_auxiliary.cpp:103-180 (handle) and
 // sparse/common/aclsparse_descr.cpp:346-416,620-720,942-1100 (CSR / DnVec
-// descriptors): status codes, null tolerance of the destroy calls, delayed
+// descriptors) and :1102-1302 (dense matrix descriptors): status codes, null tolerance of the destroy calls, delayed
 // binding of null storage and the plan reset rules.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <limits>
 #include <new>
 
@@ -46,6 +47,7 @@ aclsparseStatus_t CheckHandle(aclsparseHandle_t handle)
 
 bool IsMat(aclsparseConstSpMatDescr_t d) { return d != nullptr && d->signature == aclsp::kSpMatSignature; }
 bool IsVec(aclsparseConstDnVecDescr_t d) { return d != nullptr && d->signature == aclsp::kDnVecSignature; }
+bool IsDnMat(aclsparseConstDnMatDescr_t d) { return d != nullptr && d->signature == aclsp::kDnMatSignature; }
 
 void ResetPlan(aclsparseSpMatDescr* d) { d->plan = SpmvPlan{}; }
 
@@ -409,6 +411,94 @@ aclsparseStatus_t aclsparseCsrGet(aclsparseSpMatDescr_t spMatDescr, int64_t* row
     *csrColIndType = spMatDescr->idx_type;
     *idxBase = spMatDescr->base;
     *valueType = spMatDescr->value_type;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+// ------------------------------- dense matrix -------------------------------
+// Validation order and status codes of sparse/common/aclsparse_descr.cpp:1102-1302.
+
+aclsparseStatus_t aclsparseCreateDnMat(aclsparseDnMatDescr_t* dnMatDescr, int64_t rows, int64_t cols, int64_t ld,
+                                       void* values, aclDataType valueType, aclsparseOrder_t order)
+{
+    if (dnMatDescr == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (rows < 0 || cols < 0) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (rows > INT32_MAX || cols > INT32_MAX) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (ld < 0) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (rows != 0 && cols != 0 && values == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (!IsValidValueType(valueType)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (order != ACL_SPARSE_ORDER_ROW && order != ACL_SPARSE_ORDER_COL) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (order == ACL_SPARSE_ORDER_ROW && ld < cols) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (order == ACL_SPARSE_ORDER_COL && ld < rows) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    auto* d = new (std::nothrow) aclsparseDnMatDescr();
+    if (d == nullptr) return ACL_SPARSE_STATUS_ALLOC_FAILED;
+    d->rows = rows;
+    d->cols = cols;
+    d->ld = ld;
+    d->values = values;
+    d->value_type = valueType;
+    d->order = order;
+    *dnMatDescr = d;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseCreateConstDnMat(aclsparseConstDnMatDescr_t* dnMatDescr, int64_t rows, int64_t cols,
+                                            int64_t ld, const void* values, aclDataType valueType,
+                                            aclsparseOrder_t order)
+{
+    if (dnMatDescr == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    aclsparseDnMatDescr_t tmp = nullptr;
+    aclsparseStatus_t st = aclsparseCreateDnMat(&tmp, rows, cols, ld, const_cast<void*>(values), valueType, order);
+    if (st == ACL_SPARSE_STATUS_SUCCESS) *dnMatDescr = tmp;
+    return st;
+}
+
+aclsparseStatus_t aclsparseDestroyDnMat(aclsparseConstDnMatDescr_t dnMatDescr)
+{
+    if (dnMatDescr == nullptr) return ACL_SPARSE_STATUS_SUCCESS;
+    if (!IsDnMat(dnMatDescr)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    auto* d = const_cast<aclsparseDnMatDescr*>(dnMatDescr);
+    d->signature = 0;
+    delete d;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseConstDnMatGet(aclsparseConstDnMatDescr_t dnMatDescr, int64_t* rows, int64_t* cols,
+                                         int64_t* ld, const void** values, aclDataType* valueType,
+                                         aclsparseOrder_t* order)
+{
+    // every output is optional
+    if (!IsDnMat(dnMatDescr)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (rows != nullptr) *rows = dnMatDescr->rows;
+    if (cols != nullptr) *cols = dnMatDescr->cols;
+    if (ld != nullptr) *ld = dnMatDescr->ld;
+    if (values != nullptr) *values = dnMatDescr->values;
+    if (valueType != nullptr) *valueType = dnMatDescr->value_type;
+    if (order != nullptr) *order = dnMatDescr->order;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseDnMatGet(aclsparseDnMatDescr_t dnMatDescr, int64_t* rows, int64_t* cols, int64_t* ld,
+                                    void** values, aclDataType* valueType, aclsparseOrder_t* order)
+{
+    return aclsparseConstDnMatGet(dnMatDescr, rows, cols, ld, const_cast<const void**>(values), valueType, order);
+}
+
+aclsparseStatus_t aclsparseConstDnMatGetValues(aclsparseConstDnMatDescr_t dnMatDescr, const void** values)
+{
+    if (!IsDnMat(dnMatDescr)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    if (values != nullptr) *values = dnMatDescr->values;
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+aclsparseStatus_t aclsparseDnMatGetValues(aclsparseDnMatDescr_t dnMatDescr, void** values)
+{
+    return aclsparseConstDnMatGetValues(dnMatDescr, const_cast<const void**>(values));
+}
+
+aclsparseStatus_t aclsparseDnMatSetValues(aclsparseDnMatDescr_t dnMatDescr, void* values)
+{
+    if (!IsDnMat(dnMatDescr)) return ACL_SPARSE_STATUS_INVALID_VALUE;
+    dnMatDescr->values = values;
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 

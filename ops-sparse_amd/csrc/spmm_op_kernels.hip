@@ -1,0 +1,342 @@
+// SpMMOp kernels for gfx950: C = alpha * A * op(B) + beta * C with A in CSR
+// (fp32 or fp16 values, I32/I64 row offsets, index base 0/1) and B, C dense
+// in row or column order.
+//
+// Arithmetic restates sparse/spmm_op/arch35/spmm_op_kernel.cpp:
+//  * per output element, the products v_p * op(B)(c_p, j) of the row's
+//    entries are added in CSR order into an fp32 sum, each product and each
+//    sum rounded separately (:386-424, Muls then Add); entries whose column
+//    lies outside [0, k) are skipped there;
+//  * ALG1_HIGH_PRECISION (fp32 only) adds with Kahan compensation
+//    (:529-547: y = p - comp, t = acc + y, comp = (t - acc) - y, acc = t);
+//  * out = alpha * sum, then, when beta != 0, out = out + beta * C_old, each
+//    step rounded (:549-596, :598-640); beta == 0 never reads C;
+//  * fp16 output: clamped to +-65504, then rounded to nearest with ties away
+//    from zero (:89-127, RoundMode::CAST_ROUND);
+//  * nnz == 0: C = beta * C_old, or 0 when beta == 0 (:687-880).
+// The whole kernel is compiled without floating-point contraction so that
+// every step rounds as above: results are bit-identical run to run and to a
+// sequential fp32 restatement of the same steps.
+//
+// Mapping (MI355X-first): one wave covers RPW = 64/G rows and a tile of G*J
+// output columns; the G lanes of a row each own J adjacent columns, so a row
+// of op(B) (row-major B with opB = N, column-major B with opB = T) is read by
+// 16-byte (fp32, J = 4) or 8-byte (fp16) vector loads, fully coalesced.  The
+// row's column indices and values are read once per lane group and four
+// entries are in flight at a time.  Short outputs (n < 64) pack several rows
+// into one wave instead of idling lanes.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "aclsparse_internal.h"
+
+namespace aclsp {
+namespace {
+
+#pragma clang fp contract(off)
+
+constexpr int kMmThreads = 256;
+constexpr int kMmWave = 64;
+constexpr float kFp16Max = 65504.0f;
+
+__device__ __forceinline__ float Half2Float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+// fp32 -> fp16, round to nearest, ties away from zero (|f| <= 65504 or NaN).
+__device__ __forceinline__ uint16_t FloatToHalfAway(float f)
+{
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000U;
+    const uint32_t ax = x & 0x7FFFFFFFU;
+    if (ax > 0x7F800000U) return static_cast<uint16_t>(sign | 0x7E00U);  // NaN
+    if (ax >= 0x38800000U) {                                             // |f| >= 2^-14: normal
+        const uint32_t e = (ax >> 23) - 112U;                            // rebias 127 -> 15
+        const uint32_t h = (e << 10) | ((ax >> 13) & 0x3FFU);
+        return static_cast<uint16_t>(sign | (h + ((ax >> 12) & 1U)));   // carry may bump the exponent
+    }
+    if (ax < 0x33000000U) return static_cast<uint16_t>(sign);           // below 2^-25: zero
+    // subnormal: value = mant * 2^(e-150), fp16 unit 2^-24
+    const uint32_t mant = (ax & 0x7FFFFFU) | 0x800000U;
+    const uint32_t shift = 126U - (ax >> 23);                            // 14..25
+    const uint32_t q = mant >> shift;
+    const uint32_t half = 1U << (shift - 1U);
+    return static_cast<uint16_t>(sign | (q + ((mant & ((1U << shift) - 1U)) >= half ? 1U : 0U)));
+}
+
+template <bool kHalf>
+struct Elem;
+template <>
+struct Elem<false> {
+    using T = float;
+    __device__ static float Load(const T* p, int64_t i) { return p[i]; }
+    __device__ static void Store(T* p, int64_t i, float v) { p[i] = v; }
+};
+template <>
+struct Elem<true> {
+    using T = uint16_t;
+    __device__ static float Load(const T* p, int64_t i) { return Half2Float(p[i]); }
+    __device__ static void Store(T* p, int64_t i, float v)
+    {
+        v = v > kFp16Max ? kFp16Max : v;
+        v = v < -kFp16Max ? -kFp16Max : v;
+        p[i] = FloatToHalfAway(v);
+    }
+};
+
+template <typename T, int J>
+struct alignas(J * sizeof(T)) Vec {
+    T v[J];
+};
+
+struct MmParams {
+    const void* rp;
+    const int32_t* col;
+    const void* val;
+    const void* b;
+    void* c;
+    int64_t m, k, n, ldb, ldc, nnz;
+    int32_t base;
+    int32_t b_contig;    // op(B)(c, j) = b[c*ldb + j]; else b[j*ldb + c]
+    int32_t b_vec;       // rows of op(B) can be read J elements at a time
+    int32_t c_row;       // C(i, j) = c[i*ldc + j]; else c[j*ldc + i]
+    int32_t c_vec;
+    int32_t lg;          // log2 of lanes per row
+    int64_t tiles;       // column tiles per row group
+    int64_t waves;       // row groups * tiles
+    float alpha, beta;
+    const float* alpha_ptr;
+    const float* beta_ptr;
+};
+
+template <bool kHalf, int J>
+__device__ __forceinline__ void LoadRowJ(const typename Elem<kHalf>::T* base, int64_t j0, int64_t n, int64_t stride,
+                                         bool vec, float out[J])
+{
+    using T = typename Elem<kHalf>::T;
+    if (vec && j0 + J <= n) {
+        const Vec<T, J> w = *reinterpret_cast<const Vec<T, J>*>(base + j0);
+#pragma unroll
+        for (int q = 0; q < J; ++q) {
+            if constexpr (kHalf) out[q] = Half2Float(w.v[q]);
+            else out[q] = w.v[q];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < J; ++q) out[q] = j0 + q < n ? Elem<kHalf>::Load(base, (j0 + q) * stride) : 0.0f;
+    }
+}
+
+template <typename RowT, bool kHalf, bool kKahan, int J>
+__global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
+{
+    using T = typename Elem<kHalf>::T;
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    const T* val = static_cast<const T*>(p.val);
+    const T* b = static_cast<const T*>(p.b);
+    T* c = static_cast<T*>(p.c);
+    const float alpha = p.alpha_ptr != nullptr ? *p.alpha_ptr : p.alpha;
+    const float beta = p.beta_ptr != nullptr ? *p.beta_ptr : p.beta;
+    const bool betaZero = beta == 0.0f;
+    const int lane = static_cast<int>(threadIdx.x) & (kMmWave - 1);
+    const int g = 1 << p.lg;
+    const int rpw = kMmWave >> p.lg;
+    const int64_t waveStep = static_cast<int64_t>(gridDim.x) * (kMmThreads / kMmWave);
+    for (int64_t w = static_cast<int64_t>(blockIdx.x) * (kMmThreads / kMmWave) + threadIdx.x / kMmWave; w < p.waves;
+         w += waveStep) {
+        const int64_t tile = w % p.tiles;
+        const int64_t row = (w / p.tiles) * rpw + (lane >> p.lg);
+        const int64_t j0 = (tile * g + (lane & (g - 1))) * J;
+        const bool live = row < p.m && j0 < p.n;
+        int64_t rs = 0, re = 0;
+        if (live) {
+            rs = static_cast<int64_t>(rp[row]) - p.base;
+            re = static_cast<int64_t>(rp[row + 1]) - p.base;
+        }
+        float acc[J], comp[J];
+#pragma unroll
+        for (int q = 0; q < J; ++q) {
+            acc[q] = 0.0f;
+            comp[q] = 0.0f;
+        }
+        for (int64_t e = rs; e < re; e += 4) {
+            int32_t cc[4];
+            float vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool in = e + u < re;
+                const int32_t ci = in ? p.col[e + u] - p.base : -1;
+                cc[u] = ci >= 0 && ci < p.k ? ci : -1;
+                vv[u] = in ? Elem<kHalf>::Load(val, e + u) : 0.0f;
+            }
+            float bv[4][J];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (cc[u] >= 0) {
+                    if (p.b_contig) {
+                        LoadRowJ<kHalf, J>(b + static_cast<int64_t>(cc[u]) * p.ldb, j0, p.n, 1, p.b_vec != 0, bv[u]);
+                    } else {
+                        LoadRowJ<kHalf, J>(b + cc[u], j0, p.n, p.ldb, false, bv[u]);
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < J; ++q) bv[u][q] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (cc[u] < 0) continue;
+#pragma unroll
+                for (int q = 0; q < J; ++q) {
+                    const float prod = vv[u] * bv[u][q];
+                    if constexpr (kKahan) {
+                        const float y = prod - comp[q];
+                        const float t = acc[q] + y;
+                        comp[q] = (t - acc[q]) - y;
+                        acc[q] = t;
+                    } else {
+                        acc[q] = acc[q] + prod;
+                    }
+                }
+            }
+        }
+        if (!live) continue;
+        float out[J];
+#pragma unroll
+        for (int q = 0; q < J; ++q) out[q] = alpha * acc[q];
+        if (p.c_row) {
+            T* crow = c + row * p.ldc;
+            if (!betaZero) {
+                float old[J];
+                LoadRowJ<kHalf, J>(crow, j0, p.n, 1, p.c_vec != 0, old);
+#pragma unroll
+                for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
+            }
+            if (p.c_vec && j0 + J <= p.n && !kHalf) {
+                Vec<T, J> wv;
+#pragma unroll
+                for (int q = 0; q < J; ++q) wv.v[q] = out[q];
+                *reinterpret_cast<Vec<T, J>*>(crow + j0) = wv;
+            } else {
+#pragma unroll
+                for (int q = 0; q < J; ++q) {
+                    if (j0 + q < p.n) Elem<kHalf>::Store(crow, j0 + q, out[q]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < J; ++q) {
+                if (j0 + q >= p.n) continue;
+                const int64_t idx = (j0 + q) * p.ldc + row;
+                float o = out[q];
+                if (!betaZero) o = o + beta * Elem<kHalf>::Load(c, idx);
+                Elem<kHalf>::Store(c, idx, o);
+            }
+        }
+    }
+}
+
+// nnz == 0: C = beta * C_old (0 when beta == 0), every element of the m x n view.
+template <bool kHalf>
+__global__ __launch_bounds__(kMmThreads) void SpmmOpBetaCKernel(MmParams p)
+{
+    using T = typename Elem<kHalf>::T;
+    T* c = static_cast<T*>(p.c);
+    const float beta = p.beta_ptr != nullptr ? *p.beta_ptr : p.beta;
+    const bool betaZero = beta == 0.0f;
+    const int64_t total = p.m * p.n;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kMmThreads + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * kMmThreads) {
+        int64_t idx;
+        if (p.c_row) {
+            idx = (t / p.n) * p.ldc + t % p.n;
+        } else {
+            idx = (t / p.m) * p.ldc + t % p.m;
+        }
+        const float o = betaZero ? 0.0f : beta * Elem<kHalf>::Load(c, idx);
+        Elem<kHalf>::Store(c, idx, o);
+    }
+}
+
+template <typename RowT, bool kHalf>
+void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s)
+{
+#define SPMM_LAUNCH(JJ, KK) \
+    hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, JJ>), dim3(grid), dim3(kMmThreads), 0, s, p)
+    if (kahan && !kHalf) {
+        if (J == 4) SPMM_LAUNCH(4, true);
+        else if (J == 2) SPMM_LAUNCH(2, true);
+        else SPMM_LAUNCH(1, true);
+    } else {
+        if (J == 4) SPMM_LAUNCH(4, false);
+        else if (J == 2) SPMM_LAUNCH(2, false);
+        else SPMM_LAUNCH(1, false);
+    }
+#undef SPMM_LAUNCH
+}
+
+bool AlignedTo(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+}  // namespace
+
+int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (l.m <= 0 || l.n <= 0) return 0;
+    MmParams p{};
+    p.rp = l.row_offsets;
+    p.col = l.col_ind;
+    p.val = l.values;
+    p.b = l.b;
+    p.c = l.c;
+    p.m = l.m;
+    p.k = l.k;
+    p.n = l.n;
+    p.ldb = l.ldb;
+    p.ldc = l.ldc;
+    p.nnz = l.nnz;
+    p.base = l.base;
+    p.b_contig = (l.b_row_major != 0) != (l.b_trans != 0) ? 1 : 0;
+    p.c_row = l.c_row_major;
+    p.alpha = l.alpha;
+    p.beta = l.beta;
+    p.alpha_ptr = l.alpha_ptr;
+    p.beta_ptr = l.beta_ptr;
+    const size_t esz = l.fp16 ? 2 : 4;
+    if (l.nnz == 0) {
+        const int64_t total = l.m * l.n;
+        int64_t g = (total + kMmThreads - 1) / kMmThreads;
+        g = g > 65536 ? 65536 : g;
+        if (l.fp16) hipLaunchKernelGGL(SpmmOpBetaCKernel<true>, dim3(static_cast<unsigned>(g)), dim3(kMmThreads), 0, s, p);
+        else hipLaunchKernelGGL(SpmmOpBetaCKernel<false>, dim3(static_cast<unsigned>(g)), dim3(kMmThreads), 0, s, p);
+        return 0;
+    }
+    // lanes per row (power of two) and columns per lane
+    int J = 1, lg = 6;
+    if (l.n > 2 * kMmWave) J = 4;
+    else if (l.n > kMmWave) J = 2;
+    else {
+        lg = 0;
+        while ((int64_t{1} << lg) < l.n) ++lg;
+    }
+    p.lg = lg;
+    const int64_t tileCols = (int64_t{1} << lg) * J;
+    const int64_t rpw = kMmWave >> lg;
+    p.tiles = (l.n + tileCols - 1) / tileCols;
+    p.waves = ((l.m + rpw - 1) / rpw) * p.tiles;
+    p.b_vec = p.b_contig && l.ldb % J == 0 && AlignedTo(l.b, J * esz) ? 1 : 0;
+    p.c_vec = l.c_row_major && l.ldc % J == 0 && AlignedTo(l.c, J * esz) ? 1 : 0;
+    int64_t grid = (p.waves + kMmThreads / kMmWave - 1) / (kMmThreads / kMmWave);
+    grid = grid > (int64_t{1} << 20) ? (int64_t{1} << 20) : grid;
+    const unsigned g = static_cast<unsigned>(grid);
+    const bool kahan = l.high_precision != 0;
+    if (l.rowptr64) {
+        if (l.fp16) Dispatch<int64_t, true>(p, J, kahan, g, s);
+        else Dispatch<int64_t, false>(p, J, kahan, g, s);
+    } else {
+        if (l.fp16) Dispatch<int32_t, true>(p, J, kahan, g, s);
+        else Dispatch<int32_t, false>(p, J, kahan, g, s);
+    }
+    return 0;
+}
+
+}  // namespace aclsp

@@ -224,41 +224,73 @@ SpmvLaunch OpLaunch(const aclsparseSpMVOpDescr& d, const SpmvOpLayout& l)
 
 }  // namespace
 
+int LaunchLengthTables(const LengthTables& t, void* stream)
+{
+    const int64_t m = t.m;
+    if (m <= 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (t.rowptr64) {
+        hipLaunchKernelGGL(OpLengthsKernel<int64_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
+                           static_cast<const int64_t*>(t.row_offsets), m, t.scratch, t.tmp_reorder);
+    } else {
+        hipLaunchKernelGGL(OpLengthsKernel<int32_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
+                           static_cast<const int32_t*>(t.row_offsets), m, t.scratch, t.tmp_reorder);
+    }
+    // device sort/scan temporary storage, aligned to 256 bytes in absolute terms
+    void* temp = reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(t.temp) + 255) & ~uintptr_t{255});
+    size_t tempBytes = t.temp_bytes;
+    // Stable: equal lengths keep ascending row order, as the reference's
+    // merge that takes the left run on ties.
+    if (hipcub::DeviceRadixSort::SortPairsDescending(temp, tempBytes, t.scratch, t.tmp_scratch, t.tmp_reorder,
+                                                     t.reorder, static_cast<int>(m), 0, 32, s) != hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(OpWidenKernel, dim3(GridFor(m)), dim3(kThreads), 0, s, t.tmp_scratch, m, t.scratch, t.running);
+    tempBytes = t.temp_bytes;
+    if (hipcub::DeviceScan::InclusiveSum(temp, tempBytes, t.running, t.running, static_cast<int>(m), s) != hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(OpBinEdgeKernel, dim3(1), dim3(kThreads), 0, s, t.running, m, t.bins, t.bin_edge);
+    return 0;
+}
+
+SpmmOpLayout SpmmOpComputeLayout(int64_t m, uint32_t bins)
+{
+    SpmmOpLayout l;
+    const size_t rb = static_cast<size_t>(m) * sizeof(int32_t);
+    l.reorder = kOpHeaderBytes;
+    l.bin_edge = AlignUp(l.reorder + rb);
+    l.ref_total = AlignUp(l.bin_edge + static_cast<size_t>(bins + 1) * sizeof(int32_t));
+    l.tmp_reorder = l.ref_total;
+    l.scratch = AlignUp(l.tmp_reorder + rb);
+    l.tmp_scratch = AlignUp(l.scratch + rb);
+    l.running = AlignUp(l.tmp_scratch + rb);
+    l.temp = AlignUp(l.running + static_cast<size_t>(m) * sizeof(int64_t));
+    l.temp_bytes = m > 0 ? SortScanTempBytes(m) : 0;
+    l.total = AlignUp(l.temp + l.temp_bytes + 256);  // +256: the temp area is re-aligned to 256 bytes
+    return l;
+}
+
 int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream)
 {
     const int64_t m = static_cast<int64_t>(d.m);
     if (m <= 0) return 0;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const SpmvOpLayout l = LayoutOf(d);
     uint8_t* ws = static_cast<uint8_t*>(d.buffer);
-    int32_t* reorder = reinterpret_cast<int32_t*>(ws + l.reorder);
-    int32_t* tmpReorder = reinterpret_cast<int32_t*>(ws + l.tmp_reorder);
-    int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
-    int32_t* tmpScratch = reinterpret_cast<int32_t*>(ws + l.tmp_scratch);
-    int32_t* binEdge = reinterpret_cast<int32_t*>(ws + l.bin_edge);
-    int64_t* running = reinterpret_cast<int64_t*>(ws + l.running);
-    // device sort/scan temporary storage, aligned to 256 bytes in absolute terms
-    void* temp = reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(ws + l.temp) + 255) & ~uintptr_t{255});
-    size_t tempBytes = l.temp_bytes;
-    if (d.row_type == ACL_SPARSE_INDEX_64I) {
-        hipLaunchKernelGGL(OpLengthsKernel<int64_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
-                           static_cast<const int64_t*>(d.row_offsets), m, scratch, tmpReorder);
-    } else {
-        hipLaunchKernelGGL(OpLengthsKernel<int32_t>, dim3(GridFor(m)), dim3(kThreads), 0, s,
-                           static_cast<const int32_t*>(d.row_offsets), m, scratch, tmpReorder);
-    }
-    // Stable: equal lengths keep ascending row order, as the reference's
-    // merge that takes the left run on ties.
-    if (hipcub::DeviceRadixSort::SortPairsDescending(temp, tempBytes, scratch, tmpScratch, tmpReorder, reorder,
-                                                     static_cast<int>(m), 0, 32, s) != hipSuccess) {
-        return 1;
-    }
-    hipLaunchKernelGGL(OpWidenKernel, dim3(GridFor(m)), dim3(kThreads), 0, s, tmpScratch, m, scratch, running);
-    tempBytes = l.temp_bytes;
-    if (hipcub::DeviceScan::InclusiveSum(temp, tempBytes, running, running, static_cast<int>(m), s) != hipSuccess) {
-        return 1;
-    }
-    hipLaunchKernelGGL(OpBinEdgeKernel, dim3(1), dim3(kThreads), 0, s, running, m, d.num_bins, binEdge);
+    LengthTables t{};
+    t.row_offsets = d.row_offsets;
+    t.rowptr64 = d.row_type == ACL_SPARSE_INDEX_64I;
+    t.m = m;
+    t.bins = d.num_bins;
+    t.reorder = reinterpret_cast<int32_t*>(ws + l.reorder);
+    t.tmp_reorder = reinterpret_cast<int32_t*>(ws + l.tmp_reorder);
+    t.scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
+    t.tmp_scratch = reinterpret_cast<int32_t*>(ws + l.tmp_scratch);
+    t.bin_edge = reinterpret_cast<int32_t*>(ws + l.bin_edge);
+    t.running = reinterpret_cast<int64_t*>(ws + l.running);
+    t.temp = ws + l.temp;
+    t.temp_bytes = l.temp_bytes;
+    if (LaunchLengthTables(t, stream) != 0) return 1;
     // the execution kernel's row-block partition
     return LaunchSpmvPreprocess(OpLaunch(d, l), stream);
 }

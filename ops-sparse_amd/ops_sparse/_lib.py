@@ -67,6 +67,18 @@ class SpMVOpAlg(enum.IntEnum):
     ALG2 = 2
 
 
+class SpMMOpAlg(enum.IntEnum):
+    DEFAULT = 0
+    ALG1 = 1
+    ALG2 = 2
+    ALG1_HIGH_PRECISION = 3
+
+
+class Order(enum.IntEnum):
+    ROW = 0
+    COL = 1
+
+
 class IndexType(enum.IntEnum):
     I32 = 0
     I64 = 1
@@ -146,6 +158,21 @@ SIGNATURES = {
     "aclsparseSpMVOp_destroyPlan": [_vp],
     "aclsparseSpMVOp_setGlobalUserData": [_vp, _vp, ctypes.c_char_p, _vp, _sz],
     "aclsparseSpMVOp": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "aclsparseCreateDnMat": [_pvp, _i64, _i64, _i64, _vp, _i32, _i32],
+    "aclsparseCreateConstDnMat": [_pvp, _i64, _i64, _i64, _vp, _i32, _i32],
+    "aclsparseDestroyDnMat": [_vp],
+    "aclsparseDnMatGet": [_vp, _pi64, _pi64, _pi64, _pvp, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
+    "aclsparseConstDnMatGet": [_vp, _pi64, _pi64, _pi64, _pvp, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
+    "aclsparseDnMatGetValues": [_vp, _pvp],
+    "aclsparseConstDnMatGetValues": [_vp, _pvp],
+    "aclsparseDnMatSetValues": [_vp, _vp],
+    "aclsparseSpMMOp_bufferSize": [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_sz)],
+    "aclsparseSpMMOp_createDescr": [_vp, _pvp, _i32, _i32, _vp, _vp, _vp, _i32, _i32, _vp],
+    "aclsparseSpMMOp_destroyDescr": [_vp],
+    "aclsparseSpMMOp_createPlan": [_vp, _vp, _pvp, _vp, _sz],
+    "aclsparseSpMMOp_destroyPlan": [_vp],
+    "aclsparseSpMMOp_setGlobalUserData": [_vp, _vp, ctypes.c_char_p, _vp, _sz],
+    "aclsparseSpMMOp": [_vp, _vp, _vp, _vp, _vp, _vp],
 }
 
 _LIB = None

@@ -6,7 +6,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 CSRC = os.path.join(PKG_ROOT, "csrc")
-SOURCES = ["handle_descr.cpp", "spmv_host.cpp", "spmv_kernels.hip", "spmv_op_host.cpp", "spmv_op_kernels.hip"]
+SOURCES = ["handle_descr.cpp", "spmv_host.cpp", "spmv_kernels.hip", "spmv_op_host.cpp", "spmv_op_kernels.hip",
+           "spmm_op_host.cpp", "spmm_op_kernels.hip"]
 OUT = os.path.join(PKG_ROOT, "lib", "libaclsparse_hip.so")
 
 HIPCC_FLAGS = [

@@ -3,7 +3,9 @@
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
 product never imports this module.  Inputs are numpy arrays; CSR data must be
-base 0 and contiguous (row offsets are converted to int64 here).
+contiguous (row offsets are converted to int64 here) and base 0, except for the
+SpMMOp functions, which take the index base.  The SpMV restatement is
+spmv_oracle.c, the SpMMOp one spmm_oracle.c.
 """
 import ctypes
 import os
@@ -270,3 +272,102 @@ def verify_mere_mare(golden, actual, threshold, multiplier):
     ok = lib().oracle_verify_mere_mare(_I(g.size), _p(g), _p(a), _D(threshold), _D(multiplier), ctypes.byref(mere),
                                        ctypes.byref(mare))
     return bool(ok), mere.value, mare.value
+
+
+# ------------------------------- SpMMOp -------------------------------------
+
+def mt19937(seed, count):
+    """The first ``count`` words of std::mt19937(seed)."""
+    out = np.empty(count, dtype=np.uint32)
+    lib().oracle_mt19937_fill(ctypes.c_uint32(seed & 0xFFFFFFFF), _I(count), _p(out))
+    return out
+
+
+def uniform_real(seed, lo, hi, count):
+    """``count`` draws of libstdc++'s uniform_real_distribution<double>(lo, hi) over std::mt19937(seed)."""
+    out = np.empty(count, dtype=np.float64)
+    lib().oracle_uniform_real(ctypes.c_uint32(seed & 0xFFFFFFFF), _D(lo), _D(hi), _I(count), _p(out))
+    return out
+
+
+def half_from_float_away(v):
+    """fp32 -> fp16 bits, round to nearest with ties away from zero."""
+    f = lib().oracle_half_from_float_away
+    f.restype = ctypes.c_uint16
+    f.argtypes = [ctypes.c_float]
+    v = np.asarray(v, dtype=np.float32)
+    return np.array([f(float(x)) for x in v.ravel()], dtype=np.uint16).reshape(v.shape)
+
+
+def spmm_sparsity(m, k, ratio, lo, hi, seed, unsorted=False, base=0):
+    """MakeSpmmSparsity (test/spmm_op/spmm_op_golden.h:82-137): (row_ptr int64, col int32, values fp64),
+    row_ptr / col carrying ``base``."""
+    rp = np.zeros(m + 1, dtype=np.int64)
+    if m <= 0 or k <= 0:
+        return rp + base, np.zeros(0, np.int32), np.zeros(0, np.float64)
+    thr = int(ratio * 100)
+    ii = (np.arange(m) % 100)[:, None] * 7
+    jj = (np.arange(k) % 100)[None, :] * 13
+    mask = (ii + jj) % 100 < thr
+    rows, cols = np.nonzero(mask)  # row-major order, the generator's loop order
+    nnz = rows.size
+    rp[1:] = np.cumsum(mask.sum(axis=1))
+    col = cols.astype(np.int32)
+    val = uniform_real(seed, lo, hi, nnz)
+    if unsorted:  # ShuffleCsrRowPairs (:40-65): per-row Fisher-Yates with std::mt19937(seed + i)
+        for i in range(m):
+            s, e = int(rp[i]), int(rp[i + 1])
+            if e - s <= 1:
+                continue
+            words = mt19937((seed + i) & 0xFFFFFFFF, e - s - 1)
+            for t, j in enumerate(range(e - 1, s, -1)):
+                kk = s + int(words[t]) % (j - s + 1)
+                col[j], col[kk] = col[kk], col[j]
+                val[j], val[kk] = val[kk], val[j]
+    return rp + base, col + base, val
+
+
+def spmm_f32(m, k, n, row_ptr, col, val, base, b, ldb, b_contig, c, ldc, c_row, alpha, beta, kahan=False,
+             half_out=False):
+    """The SpMMOp kernel's fp32 steps; returns the new C storage (float32, same layout as ``c``)."""
+    rp = _i64(row_ptr)
+    out = np.array(c, dtype=np.float32, copy=True).ravel()
+    lib().oracle_spmm_f32(_I(m), _I(k), _I(n), _p(rp), _p(_c(col, np.int32)), _p(_c(val, np.float32)),
+                          _I(len(col)), ctypes.c_int32(base), _p(_c(b, np.float32)), _I(ldb), ctypes.c_int32(b_contig),
+                          _p(out), _I(ldc), ctypes.c_int32(c_row), ctypes.c_float(alpha), ctypes.c_float(beta),
+                          ctypes.c_int32(int(kahan)), ctypes.c_int32(int(half_out)))
+    return out
+
+
+def spmm_golden_f64(m, k, n, row_ptr, col, val, base, b, b_trans, c_init, alpha, beta):
+    """SpmmGolden (fp64): b and c_init in canonical row-major order; returns (m*n,) float64."""
+    out = np.empty(max(m * n, 1), dtype=np.float64)
+    lib().oracle_spmm_golden_f64(_I(m), _I(k), _I(n), _p(_i64(row_ptr)), _p(_c(col, np.int32)),
+                                 _p(_c(val, np.float64)), ctypes.c_int32(base), _p(_c(b, np.float64)),
+                                 ctypes.c_int32(int(b_trans)), _p(_c(c_init, np.float64)), _D(alpha), _D(beta),
+                                 _p(out))
+    return out[:m * n]
+
+
+# MIXED_TOLERANCE rows of test/frame/verify.h:230-236: (rtol, atol, fixed limit, mantissa bits, emin)
+FRAME_MIXED = {"float32": (2.0 ** -13, 2.0 ** -13, 1e-2, 23, -126), "float16": (2.0 ** -10, 2.0 ** -10, 1e-1, 10, -14)}
+
+
+def verify_frame_mixed(golden, actual, dtype):
+    """MixedToleranceStrategy (test/frame/verify.h:207-320): returns (passed, matched_ratio, max_abs_error).
+    An element fails when |a-g| > atol + rtol*|g|; the check fails when fewer than 99% match, or when
+    any |a-g| exceeds max(fixed, 32 ulp(|g|)), or any value is NaN/Inf."""
+    rtol, atol, fixed, mbits, emin = FRAME_MIXED[dtype]
+    g = np.asarray(golden, dtype=np.float32).astype(np.float64).ravel()
+    a = np.asarray(actual, dtype=np.float32).astype(np.float64).ravel()
+    if g.size == 0:
+        return True, 1.0, 0.0
+    bad = ~np.isfinite(g) | ~np.isfinite(a)
+    diff = np.abs(a - g)
+    ga = np.abs(g)
+    _, ex = np.frexp(ga)
+    ulp = np.where(ga == 0, 2.0 ** (emin - mbits), np.ldexp(1.0, np.maximum(ex - 1, emin) - mbits))
+    fails = (diff > atol + rtol * ga) | bad
+    hard = bad | (diff > np.maximum(fixed, 32.0 * ulp))
+    ratio = 1.0 - fails.sum() / g.size
+    return bool(ratio >= 0.99 and not hard.any()), float(ratio), float(np.nanmax(np.where(bad, 0, diff)))

@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 
 from ops_sparse import _lib
-from ops_sparse._lib import (DataType, Format, IndexBase, IndexType, Operation, PointerMode, SpMVAlg, SpMVOpAlg,
-                             Status)
+from ops_sparse._lib import (DataType, Format, IndexBase, IndexType, Operation, Order, PointerMode, SpMMOpAlg, SpMVAlg,
+                             SpMVOpAlg, Status)
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "cann_ops_sparse.h")
 N, T, H = int(Operation.NON_TRANSPOSE), int(Operation.TRANSPOSE), int(Operation.CONJUGATE_TRANSPOSE)
@@ -338,3 +338,118 @@ def test_package_import_registers_aten_mv_for_csr_on_rocm():
     dump = torch._C._dispatch_dump("aten::mv")
     line = next(l for l in dump.splitlines() if l.startswith("SparseCsrCUDA:"))
     assert "ops_sparse" in line and "aten.py" in line
+
+
+# ------------------------- dense matrix / SpMMOp --------------------------------
+
+def test_dnmat_descriptor(lib):
+    """aclsparseCreateDnMat rules (sparse/common/aclsparse_descr.cpp:1102-1152) and the getters."""
+    data = np.zeros(64, np.float32)
+    p = ctypes.c_void_p(data.ctypes.data)
+    d = ctypes.c_void_p(0)
+    cr = lib.aclsparseCreateDnMat
+    R, C = int(Order.ROW), int(Order.COL)
+    assert cr(None, 2, 3, 3, p, F32, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), -1, 3, 3, p, F32, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 2, 1 << 31, 1 << 31, p, F32, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 2, 3, -1, p, F32, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 2, 3, 3, None, F32, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 0, 3, 3, None, F32, R) == Status.SUCCESS  # empty: storage may be null
+    assert lib.aclsparseDestroyDnMat(d) == Status.SUCCESS
+    assert cr(ctypes.byref(d), 2, 3, 3, p, 99, R) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 2, 3, 3, p, F32, 2) == Status.INVALID_VALUE
+    assert cr(ctypes.byref(d), 2, 3, 2, p, F32, R) == Status.INVALID_VALUE  # ld < cols
+    assert cr(ctypes.byref(d), 2, 3, 1, p, F32, C) == Status.INVALID_VALUE  # ld < rows
+    assert cr(ctypes.byref(d), 2, 3, 5, p, F32, R) == Status.SUCCESS
+    r, c, ld, v = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_void_p(0)
+    t, o = ctypes.c_int32(-1), ctypes.c_int32(-1)
+    assert lib.aclsparseDnMatGet(d, ctypes.byref(r), ctypes.byref(c), ctypes.byref(ld), ctypes.byref(v),
+                                 ctypes.byref(t), ctypes.byref(o)) == Status.SUCCESS
+    assert (r.value, c.value, ld.value, v.value, t.value, o.value) == (2, 3, 5, data.ctypes.data, F32, R)
+    assert lib.aclsparseConstDnMatGet(d, None, None, None, None, None, None) == Status.SUCCESS  # outputs optional
+    assert lib.aclsparseDnMatSetValues(d, None) == Status.SUCCESS
+    assert lib.aclsparseDnMatGetValues(d, ctypes.byref(v)) == Status.SUCCESS and not v.value
+    assert lib.aclsparseDestroyDnMat(d) == Status.SUCCESS
+    assert lib.aclsparseDestroyDnMat(None) == Status.SUCCESS
+    assert lib.aclsparseDnMatGetValues(None, ctypes.byref(v)) == Status.INVALID_VALUE
+
+
+def _dnmat(lib, rows, cols, addr, vtype=DataType.FLOAT, order=Order.ROW, ld=None):
+    d = ctypes.c_void_p(0)
+    if ld is None:
+        ld = cols if order == Order.ROW else rows
+    assert lib.aclsparseCreateDnMat(ctypes.byref(d), rows, cols, max(ld, 1), ctypes.c_void_p(addr), int(vtype),
+                                    int(order)) == Status.SUCCESS
+    return d
+
+
+def test_spmmop_validation(env, lib):
+    """Status codes of the SpMMOp exception tests (test/spmm_op/arch35/spmm_op_test.cpp:523-731) and
+    the host checks of sparse/spmm_op/arch35/spmm_op_host.cpp; nothing here reaches a launch."""
+    A = env.csr()  # 2 x 3, fp32
+    B = _dnmat(lib, 3, 4, env.xv)
+    Cm = _dnmat(lib, 2, 4, env.yt)
+    s = ctypes.c_size_t(7)
+    bs = lib.aclsparseSpMMOp_bufferSize
+    assert bs(None, N, N, A, B, Cm, F32, 0, ctypes.byref(s)) == Status.HANDLE_IS_NULLPTR
+    assert bs(env.h, N, N, None, B, Cm, F32, 0, ctypes.byref(s)) == Status.INVALID_VALUE
+    assert bs(env.h, N, N, A, None, Cm, F32, 0, ctypes.byref(s)) == Status.INVALID_VALUE
+    assert bs(env.h, N, N, A, B, None, F32, 0, ctypes.byref(s)) == Status.INVALID_VALUE
+    assert bs(env.h, N, N, A, B, Cm, F32, 0, None) == Status.INVALID_VALUE
+    assert bs(env.h, N, N, A, B, Cm, int(DataType.DOUBLE), 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, T, N, A, B, Cm, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, H, A, B, Cm, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, N, A, B, Cm, F32, 9, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, N, env.csr(vtype=DataType.BF16), B, Cm, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    assert bs(env.h, N, N, env.csr(idx_type=IndexType.I64), B, Cm, F32, 0, ctypes.byref(s)) == Status.NOT_SUPPORTED
+    # null row offsets (nnz = 0, so indices and values may be null)
+    assert bs(env.h, N, N, env.csr(nnz=0, ptrs=False), B, Cm, F32, 0, ctypes.byref(s)) == Status.INVALID_VALUE
+    for alg in (SpMMOpAlg.DEFAULT, SpMMOpAlg.ALG1, SpMMOpAlg.ALG1_HIGH_PRECISION):
+        assert bs(env.h, N, N, A, B, Cm, F32, int(alg), ctypes.byref(s)) == Status.SUCCESS and s.value == 0
+    assert bs(env.h, N, N, A, B, Cm, F32, int(SpMMOpAlg.ALG2), ctypes.byref(s)) == Status.SUCCESS
+    assert s.value >= 256 + 2 * 4 and s.value % 64 == 0
+    d = ctypes.c_void_p(0)
+    cd = lib.aclsparseSpMMOp_createDescr
+    assert cd(None, ctypes.byref(d), N, N, A, B, Cm, F32, 0, None) == Status.HANDLE_IS_NULLPTR
+    assert cd(env.h, None, N, N, A, B, Cm, F32, 0, None) == Status.INVALID_VALUE
+    assert cd(env.h, ctypes.byref(d), N, N, A, B, Cm, F32, int(SpMMOpAlg.ALG2), None) == Status.INVALID_VALUE
+    assert cd(env.h, ctypes.byref(d), N, N, A, B, Cm, F32, int(SpMMOpAlg.ALG1), None) == Status.SUCCESS
+    plan = ctypes.c_void_p(0)
+    cp = lib.aclsparseSpMMOp_createPlan
+    assert cp(None, d, ctypes.byref(plan), None, 0) == Status.HANDLE_IS_NULLPTR
+    assert cp(env.h, None, ctypes.byref(plan), None, 0) == Status.INVALID_VALUE
+    assert cp(env.h, d, None, None, 0) == Status.INVALID_VALUE
+    lto = np.zeros(16, np.uint8)
+    assert cp(env.h, d, ctypes.byref(plan), ctypes.c_void_p(lto.ctypes.data), 16) == Status.NOT_SUPPORTED
+    assert cp(env.h, d, ctypes.byref(plan), None, 0) == Status.SUCCESS
+    sg = lib.aclsparseSpMMOp_setGlobalUserData
+    assert sg(None, plan, b"x", None, 0) == Status.HANDLE_IS_NULLPTR
+    assert sg(env.h, None, b"x", None, 0) == Status.INVALID_VALUE
+    assert sg(env.h, plan, b"x", None, 4) == Status.INVALID_VALUE
+    assert sg(env.h, plan, b"x", None, 0) == Status.SUCCESS
+    a, b = ctypes.c_float(1), ctypes.c_float(0)
+    ex = lib.aclsparseSpMMOp
+    pa, pb = ctypes.byref(a), ctypes.byref(b)
+    assert ex(None, plan, pa, pb, B, Cm) == Status.HANDLE_IS_NULLPTR
+    assert ex(env.h, None, pa, pb, B, Cm) == Status.INVALID_VALUE
+    assert ex(env.h, plan, None, pb, B, Cm) == Status.INVALID_VALUE
+    assert ex(env.h, plan, pa, None, B, Cm) == Status.INVALID_VALUE
+    assert ex(env.h, plan, pa, pb, None, Cm) == Status.INVALID_VALUE
+    # B with k = 2 rows against A's k = 3 (DimMismatch), C with the wrong row count
+    assert ex(env.h, plan, pa, pb, _dnmat(lib, 2, 4, env.xv), Cm) == Status.INVALID_VALUE
+    assert ex(env.h, plan, pa, pb, B, _dnmat(lib, 3, 4, env.yt)) == Status.INVALID_VALUE
+    # B of another dtype (UnsupportedDtypeCombo)
+    assert ex(env.h, plan, pa, pb, _dnmat(lib, 3, 4, env.xv, DataType.FLOAT16), Cm) == Status.NOT_SUPPORTED
+    # ld above the int32 range
+    Bw = _dnmat(lib, 3, 4, env.xv, ld=1 << 31)
+    assert ex(env.h, plan, pa, pb, Bw, Cm) == Status.NOT_SUPPORTED
+    assert lib.aclsparseSpMMOp_destroyPlan(plan) == Status.SUCCESS
+    assert lib.aclsparseSpMMOp_destroyPlan(None) == Status.SUCCESS
+    assert lib.aclsparseSpMMOp_destroyDescr(d) == Status.SUCCESS
+    assert lib.aclsparseSpMMOp_destroyDescr(None) == Status.SUCCESS
+    # opB = T: B is n x k
+    assert cd(env.h, ctypes.byref(d), N, T, A, B, Cm, F32, 0, None) == Status.SUCCESS
+    assert cp(env.h, d, ctypes.byref(plan), None, 0) == Status.SUCCESS
+    assert ex(env.h, plan, pa, pb, B, Cm) == Status.INVALID_VALUE  # 3 x 4 is not n x k = 4 x 3
+    lib.aclsparseSpMMOp_destroyPlan(plan)
+    lib.aclsparseSpMMOp_destroyDescr(d)
