@@ -270,6 +270,69 @@ def measure_spmvop(w, alg, steps, warmup, flush_buf):
     return statistics.median(ts), p0.elapsed_time(p1)
 
 
+def spmm_cases(dev, headline_w):
+    """SpMMOp workloads: the largest shape of the reference's own SpMMOp perf table
+    (test/spmm_op/arch35/spmm_op_perf.cpp:740-790: M=2048, K=128, N=2048, 50% density,
+    alpha=1, beta=0, fp32 and fp16, L2-resident, timed warm as there) and the headline
+    Laplacian times a 16-column dense block (HBM-sized, flushed like the SpMV configs)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import numpy as np
+
+    out = []
+    m, k, n = 2048, 128, 2048
+    thr = 50
+    mask = ((np.arange(m) % 100)[:, None] * 7 + (np.arange(k) % 100)[None, :] * 13) % 100 < thr
+    rows, cols = np.nonzero(mask)
+    rp = np.zeros(m + 1, np.int32)
+    rp[1:] = np.cumsum(mask.sum(axis=1))
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    for dt, tag in ((torch.float32, "fp32"), (torch.float16, "fp16")):
+        vals = (torch.rand(rows.size, generator=g, device=dev) * 2 - 1).to(dt)
+        b = (torch.rand(k, n, generator=g, device=dev) * 2 - 1).to(dt)
+        c = torch.zeros(m, n, dtype=dt, device=dev)
+        out.append((f"spmm_ref_2048x128x2048_{tag}_sp50",
+                    dict(m=m, k=k, n=n, rp=torch.from_numpy(rp).to(dev), col=torch.from_numpy(cols.astype(np.int32)).to(dev),
+                         val=vals, b=b, c=c, alpha=1.0, beta=0.0, flush=False)))
+    w = headline_w
+    n2 = 16
+    b = torch.rand(w.cols, n2, generator=g, device=dev) * 2 - 1
+    c = torch.rand(w.rows, n2, generator=g, device=dev) * 2 - 1
+    out.append((f"spmm_c2_laplacian_x{n2}_fp32", dict(m=w.rows, k=w.cols, n=n2, rp=w.row_ptr, col=w.col_ind,
+                                                      val=w.values, b=b, c=c, alpha=1.5, beta=0.5, flush=True)))
+    return out
+
+
+def measure_spmm(case, steps, warmup, flush_buf):
+    """Median per-launch time of aclsparseSpMMOp (ALG1) with the reference perf test's byte and
+    flop model (spmm_op_perf.cpp:325-360)."""
+    from ops_sparse.spmm import SpMMOp
+
+    cfg = case
+    op = SpMMOp(cfg["m"], cfg["k"], cfg["rp"], cfg["col"], cfg["val"], cfg["b"], cfg["c"])
+    stream = torch.cuda.current_stream()
+    sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
+    for _ in range(warmup):
+        op.run(cfg["b"], cfg["c"], cfg["alpha"], cfg["beta"])
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        if cfg["flush"]:
+            torch.sum(flush_buf, dim=0, out=sink)
+        a.record(stream)
+        op.run(cfg["b"], cfg["c"], cfg["alpha"], cfg["beta"])
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = statistics.median(sorted(a.elapsed_time(b) for a, b in evs))
+    op.close()
+    nnz, m, k, n = cfg["col"].numel(), cfg["m"], cfg["k"], cfg["n"]
+    elem = cfg["val"].element_size()
+    nbytes = nnz * elem + nnz * 4 + (m + 1) * 4 + k * n * elem + (m * n * elem if cfg["beta"] != 0 else 0) + m * n * elem
+    fl = 2.0 * nnz * n + 2.0 * m * n
+    return dict(m=m, k=k, n=n, nnz=nnz, dtype=str(cfg["val"].dtype).split(".")[-1], median_ms=t,
+                algorithmic_bytes=nbytes, gbs=nbytes / (t * 1e-3) / 1e9, frac=nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                gflops=fl / (t * 1e-3) / 1e9, l2_mall_flushed=cfg["flush"])
+
+
 def cpu_baseline(w, seconds):
     """Single-threaded oracle SpMV (the reference host golden restated in C) on a bounded sample."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -373,6 +436,9 @@ def main():
                                     nnz=w.nnz, op="N", dtype="float32", algorithmic_bytes=nbytes, median_ms=t,
                                     gbs=nbytes / (t * 1e-3) / 1e9, frac=nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                     create_descr_ms=setup)
+            for key, case in spmm_cases(dev, w):
+                results[key] = measure_spmm(case, args.steps, args.warmup, flush_buf)
+                print(f"# {key}: {json.dumps(results[key])}", file=sys.stderr, flush=True)
         else:
             del w
             torch.cuda.empty_cache()

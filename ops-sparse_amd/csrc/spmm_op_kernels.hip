@@ -22,8 +22,9 @@
 // output columns; the G lanes of a row each own J adjacent columns, so a row
 // of op(B) (row-major B with opB = N, column-major B with opB = T) is read by
 // 16-byte (fp32, J = 4) or 8-byte (fp16) vector loads, fully coalesced.  The
-// row's column indices and values are read once per lane group and four
-// entries are in flight at a time.  Short outputs (n < 64) pack several rows
+// row's column indices and values are read G at a time (one per lane) and
+// handed to the group by cross-lane reads; eight entries' B rows are in
+// flight at a time.  Short outputs (n < 64) pack several rows
 // into one wave instead of idling lanes.
 #include <hip/hip_runtime.h>
 
@@ -39,6 +40,7 @@ namespace {
 constexpr int kMmThreads = 256;
 constexpr int kMmWave = 64;
 constexpr float kFp16Max = 65504.0f;
+constexpr int kU = 8;  // entries whose B rows are in flight together
 
 __device__ __forceinline__ float Half2Float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
@@ -100,6 +102,7 @@ struct MmParams {
     int32_t b_vec;       // rows of op(B) can be read J elements at a time
     int32_t c_row;       // C(i, j) = c[i*ldc + j]; else c[j*ldc + i]
     int32_t c_vec;
+    int32_t has_b;       // k > 0: op(B) has rows to read
     int32_t lg;          // log2 of lanes per row
     int64_t tiles;       // column tiles per row group
     int64_t waves;       // row groups * tiles
@@ -126,6 +129,87 @@ __device__ __forceinline__ void LoadRowJ(const typename Elem<kHalf>::T* base, in
     }
 }
 
+// Loads the op(B) rows of a batch of kU entries (cc < 0: skipped entry).
+template <bool kHalf, int J>
+__device__ __forceinline__ void SpmmLoad(const MmParams& p, const typename Elem<kHalf>::T* b, int64_t j0, bool fast,
+                                         bool strided, const int32_t cc[kU], float bv[kU][J])
+{
+    using T = typename Elem<kHalf>::T;
+    if (fast) {
+        // one unconditional vector load per entry (a skipped entry reads row 0)
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            const int64_t r = cc[q] >= 0 ? cc[q] : 0;
+            const Vec<T, J> w = *reinterpret_cast<const Vec<T, J>*>(b + r * p.ldb + j0);
+#pragma unroll
+            for (int t = 0; t < J; ++t) {
+                if constexpr (kHalf) bv[q][t] = Half2Float(w.v[t]);
+                else bv[q][t] = w.v[t];
+            }
+        }
+    } else if (strided) {
+        // B(c, j) = b[j*ldb + c]: unconditional element loads at clamped positions
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            const int64_t r = cc[q] >= 0 ? cc[q] : 0;
+#pragma unroll
+            for (int t = 0; t < J; ++t) {
+                const int64_t j = j0 + t < p.n ? j0 + t : p.n - 1;
+                bv[q][t] = Elem<kHalf>::Load(b, j * p.ldb + r);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            if (cc[q] >= 0) {
+                LoadRowJ<kHalf, J>(b + static_cast<int64_t>(cc[q]) * p.ldb, j0, p.n, 1, false, bv[q]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < J; ++t) bv[q][t] = 0.0f;
+            }
+        }
+    }
+}
+
+// Adds a batch's products into the sums, in entry order.
+template <bool kKahan, int J>
+__device__ __forceinline__ void SpmmAccum(const int32_t cc[kU], const float vv[kU], const float bv[kU][J],
+                                          float acc[J], float comp[J])
+{
+#pragma unroll
+    for (int q = 0; q < kU; ++q) {
+        const bool take = cc[q] >= 0;  // skipped entries leave the sums untouched
+#pragma unroll
+        for (int t = 0; t < J; ++t) {
+            const float prod = vv[q] * bv[q][t];
+            if constexpr (kKahan) {
+                const float y = prod - comp[t];
+                const float s2 = acc[t] + y;
+                const float c2 = (s2 - acc[t]) - y;
+                acc[t] = take ? s2 : acc[t];
+                comp[t] = take ? c2 : comp[t];
+            } else {
+                const float s2 = acc[t] + prod;
+                acc[t] = take ? s2 : acc[t];
+            }
+        }
+    }
+}
+
+// Entries u0 .. u0+kU-1 of the group's current window, read from the lanes
+// that loaded them (-1 past the row).
+__device__ __forceinline__ void SpmmFetch(int myc, float myv, int gbase, int g, int u0, int cnt, int32_t cc[kU],
+                                          float vv[kU])
+{
+#pragma unroll
+    for (int q = 0; q < kU; ++q) {
+        const int u = u0 + q < g ? u0 + q : g - 1;
+        const int32_t cq = __shfl(myc, gbase + u, kMmWave);
+        vv[q] = __shfl(myv, gbase + u, kMmWave);
+        cc[q] = u0 + q < cnt ? cq : -1;
+    }
+}
+
 template <typename RowT, bool kHalf, bool kKahan, int J>
 __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
 {
@@ -141,14 +225,21 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
     const int g = 1 << p.lg;
     const int rpw = kMmWave >> p.lg;
     const int64_t waveStep = static_cast<int64_t>(gridDim.x) * (kMmThreads / kMmWave);
-    for (int64_t w = static_cast<int64_t>(blockIdx.x) * (kMmThreads / kMmWave) + threadIdx.x / kMmWave; w < p.waves;
-         w += waveStep) {
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMmWave);
+    for (int64_t w = static_cast<int64_t>(blockIdx.x) * (kMmThreads / kMmWave) + wv; w < p.waves; w += waveStep) {
         const int64_t tile = w % p.tiles;
         const int64_t row = (w / p.tiles) * rpw + (lane >> p.lg);
         const int64_t j0 = (tile * g + (lane & (g - 1))) * J;
+        // every lane of a row's group walks the row (its entries are shared
+        // across the group); only lanes inside [0, n) store
         const bool live = row < p.m && j0 < p.n;
+        // wave-uniform load paths: whole tiles of contiguous, aligned rows of op(B); or B
+        // stored the other way (element loads); else the guarded general path
+        const bool fullTile = (tile + 1) * g * J <= p.n;
+        const bool fast = p.has_b && p.b_contig && p.b_vec && fullTile;
+        const bool strided = p.has_b && !p.b_contig;
         int64_t rs = 0, re = 0;
-        if (live) {
+        if (row < p.m) {
             rs = static_cast<int64_t>(rp[row]) - p.base;
             re = static_cast<int64_t>(rp[row + 1]) - p.base;
         }
@@ -158,45 +249,26 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
             acc[q] = 0.0f;
             comp[q] = 0.0f;
         }
-        for (int64_t e = rs; e < re; e += 4) {
-            int32_t cc[4];
-            float vv[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const bool in = e + u < re;
-                const int32_t ci = in ? p.col[e + u] - p.base : -1;
-                cc[u] = ci >= 0 && ci < p.k ? ci : -1;
-                vv[u] = in ? Elem<kHalf>::Load(val, e + u) : 0.0f;
+        // Each group reads its row's entries G at a time, one per lane, and
+        // hands them to the group by cross-lane reads, kU at a time.
+        const int gl = lane & (g - 1);
+        const int gbase = lane & ~(g - 1);
+        for (int64_t e0 = rs; e0 < re; e0 += g) {
+            int32_t myc = -1;
+            float myv = 0.0f;
+            if (e0 + gl < re) {
+                const int32_t ci = p.col[e0 + gl] - p.base;
+                myc = ci >= 0 && ci < p.k ? ci : -1;
+                myv = Elem<kHalf>::Load(val, e0 + gl);
             }
-            float bv[4][J];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (cc[u] >= 0) {
-                    if (p.b_contig) {
-                        LoadRowJ<kHalf, J>(b + static_cast<int64_t>(cc[u]) * p.ldb, j0, p.n, 1, p.b_vec != 0, bv[u]);
-                    } else {
-                        LoadRowJ<kHalf, J>(b + cc[u], j0, p.n, p.ldb, false, bv[u]);
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < J; ++q) bv[u][q] = 0.0f;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (cc[u] < 0) continue;
-#pragma unroll
-                for (int q = 0; q < J; ++q) {
-                    const float prod = vv[u] * bv[u][q];
-                    if constexpr (kKahan) {
-                        const float y = prod - comp[q];
-                        const float t = acc[q] + y;
-                        comp[q] = (t - acc[q]) - y;
-                        acc[q] = t;
-                    } else {
-                        acc[q] = acc[q] + prod;
-                    }
-                }
+            const int cnt = re - e0 < g ? static_cast<int>(re - e0) : g;
+            for (int u0 = 0; u0 < cnt; u0 += kU) {
+                int32_t cc[kU];
+                float vv[kU];
+                float bv[kU][J];
+                SpmmFetch(myc, myv, gbase, g, u0, cnt, cc, vv);
+                SpmmLoad<kHalf, J>(p, b, j0, fast, strided, cc, bv);
+                SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
             }
         }
         if (!live) continue;
@@ -297,6 +369,7 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     p.base = l.base;
     p.b_contig = (l.b_row_major != 0) != (l.b_trans != 0) ? 1 : 0;
     p.c_row = l.c_row_major;
+    p.has_b = l.k > 0 ? 1 : 0;
     p.alpha = l.alpha;
     p.beta = l.beta;
     p.alpha_ptr = l.alpha_ptr;
