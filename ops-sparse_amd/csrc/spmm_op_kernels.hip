@@ -65,6 +65,28 @@ __device__ __forceinline__ uint16_t FloatToHalfAway(float f)
     return static_cast<uint16_t>(sign | (q + ((mant & ((1U << shift) - 1U)) >= half ? 1U : 0U)));
 }
 
+// Wave-uniform reads of arrays the kernel never writes: through the constant
+// address space, so they become scalar loads.
+template <typename T>
+__device__ __forceinline__ T ConstLoad(const void* base, int64_t i)
+{
+    typedef const __attribute__((address_space(4))) T* CPtr;
+    return reinterpret_cast<CPtr>(reinterpret_cast<uintptr_t>(base))[i];
+}
+
+// Value i of A (fp32 or fp16) by a scalar load (fp16: the aligned dword that holds it).
+template <bool kHalf>
+__device__ __forceinline__ float ScalarVal(const void* val, int64_t i)
+{
+    if constexpr (kHalf) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(val) + static_cast<uintptr_t>(i) * 2;
+        const uint32_t w = ConstLoad<uint32_t>(reinterpret_cast<const void*>(a & ~uintptr_t{3}), 0);
+        return Half2Float(static_cast<uint16_t>(w >> ((a & 2) * 8)));
+    } else {
+        return ConstLoad<float>(val, i);
+    }
+}
+
 template <bool kHalf>
 struct Elem;
 template <>
@@ -196,6 +218,60 @@ __device__ __forceinline__ void SpmmAccum(const int32_t cc[kU], const float vv[k
     }
 }
 
+// out = alpha * sum, then + beta * C_old when beta != 0 (each step rounded),
+// stored with the element type's rounding; one lane's J columns of one row.
+template <bool kHalf, int J>
+__device__ __forceinline__ void SpmmStore(const MmParams& p, typename Elem<kHalf>::T* c, int64_t row, int64_t j0,
+                                          const float acc[J], float alpha, float beta, bool betaZero)
+{
+    using T = typename Elem<kHalf>::T;
+    float out[J];
+#pragma unroll
+    for (int q = 0; q < J; ++q) out[q] = alpha * acc[q];
+    if (p.c_row) {
+        T* crow = c + row * p.ldc;
+        if (!betaZero) {
+            float old[J];
+            LoadRowJ<kHalf, J>(crow, j0, p.n, 1, p.c_vec != 0, old);
+#pragma unroll
+            for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
+        }
+        if (p.c_vec && j0 + J <= p.n && !kHalf) {
+            Vec<T, J> wv;
+#pragma unroll
+            for (int q = 0; q < J; ++q) wv.v[q] = out[q];
+            *reinterpret_cast<Vec<T, J>*>(crow + j0) = wv;
+        } else {
+#pragma unroll
+            for (int q = 0; q < J; ++q) {
+                if (j0 + q < p.n) Elem<kHalf>::Store(crow, j0 + q, out[q]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < J; ++q) {
+            if (j0 + q >= p.n) continue;
+            const int64_t idx = (j0 + q) * p.ldc + row;
+            float o = out[q];
+            if (!betaZero) o = o + beta * Elem<kHalf>::Load(c, idx);
+            Elem<kHalf>::Store(c, idx, o);
+        }
+    }
+}
+
+// One row per wave: entries u0 .. u0+kU-1 of the window, read from the lanes
+// that loaded them into scalar registers (no LDS traffic; -1 past the row).
+__device__ __forceinline__ void SpmmFetchWave(int myc, float myv, int u0, int cnt, int32_t cc[kU], float vv[kU])
+{
+#pragma unroll
+    for (int q = 0; q < kU; ++q) {
+        const int u = u0 + q < kMmWave ? u0 + q : kMmWave - 1;
+        const int32_t cq = __builtin_amdgcn_readlane(myc, u);
+        vv[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), u));
+        cc[q] = u0 + q < cnt ? cq : -1;
+    }
+}
+
 // Entries u0 .. u0+kU-1 of the group's current window, read from the lanes
 // that loaded them (-1 past the row).
 __device__ __forceinline__ void SpmmFetch(int myc, float myv, int gbase, int g, int u0, int cnt, int32_t cc[kU],
@@ -210,7 +286,7 @@ __device__ __forceinline__ void SpmmFetch(int myc, float myv, int gbase, int g, 
     }
 }
 
-template <typename RowT, bool kHalf, bool kKahan, int J>
+template <typename RowT, bool kHalf, bool kKahan, int J, bool kWave>
 __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
 {
     using T = typename Elem<kHalf>::T;
@@ -266,44 +342,118 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
                 int32_t cc[kU];
                 float vv[kU];
                 float bv[kU][J];
-                SpmmFetch(myc, myv, gbase, g, u0, cnt, cc, vv);
+                if constexpr (kWave) SpmmFetchWave(myc, myv, u0, cnt, cc, vv);
+                else SpmmFetch(myc, myv, gbase, g, u0, cnt, cc, vv);
                 SpmmLoad<kHalf, J>(p, b, j0, fast, strided, cc, bv);
                 SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
             }
         }
-        if (!live) continue;
-        float out[J];
+        if (live) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero);
+    }
+}
+
+// Small k (k * 64 * J fp32 values fit the workgroup's 64 KiB of LDS): the
+// workgroup stages the column tile op(B)[0:k, tile] in LDS once (fp16 widened
+// to fp32, exactly) and its four waves then take their rows' products from
+// LDS; op(B) is read from L2 once per workgroup instead of once per entry.
+// One row per wave at a time, its entries shared by cross-lane reads.
+constexpr int kLdsBytes = 64 * 1024;
+constexpr int kLdsThreads = 1024;  // 16 waves share one staged tile
+constexpr int kLdsRowsPerWave = 4;
+
+template <typename RowT, bool kHalf, bool kKahan, int J>
+__global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(8))) void SpmmOpLdsKernel(MmParams p)
+{
+    using T = typename Elem<kHalf>::T;
+    extern __shared__ float sB[];
+    constexpr int TW = kMmWave * J;
+    const RowT* rp = static_cast<const RowT*>(p.rp);
+    const T* val = static_cast<const T*>(p.val);
+    const T* b = static_cast<const T*>(p.b);
+    T* c = static_cast<T*>(p.c);
+    const float alpha = p.alpha_ptr != nullptr ? *p.alpha_ptr : p.alpha;
+    const float beta = p.beta_ptr != nullptr ? *p.beta_ptr : p.beta;
+    const bool betaZero = beta == 0.0f;
+    const int lane = static_cast<int>(threadIdx.x) & (kMmWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMmWave);
+    const int64_t tile = static_cast<int64_t>(blockIdx.x) % p.tiles;
+    const int64_t chunk = static_cast<int64_t>(blockIdx.x) / p.tiles;
+    const int64_t jt = tile * TW;
+    const int k = static_cast<int>(p.k);
+    if (p.b_contig) {
+        for (int idx = static_cast<int>(threadIdx.x); idx < k * TW; idx += kLdsThreads) {
+            const int r = idx / TW, cj = idx - r * TW;
+            const int64_t j = jt + cj;
+            sB[idx] = j < p.n ? Elem<kHalf>::Load(b, static_cast<int64_t>(r) * p.ldb + j) : 0.0f;
+        }
+    } else {
+        for (int idx = static_cast<int>(threadIdx.x); idx < k * TW; idx += kLdsThreads) {
+            const int cj = idx / k, r = idx - cj * k;
+            const int64_t j = jt + cj;
+            sB[r * TW + cj] = j < p.n ? Elem<kHalf>::Load(b, j * p.ldb + r) : 0.0f;
+        }
+    }
+    __syncthreads();
+    const int64_t j0 = jt + lane * J;
+    const int64_t row0 = (chunk * (kLdsThreads / kMmWave) + wv) * kLdsRowsPerWave;
+    for (int rr = 0; rr < kLdsRowsPerWave; ++rr) {
+        const int64_t row = row0 + rr;
+        if (row >= p.m) break;
+        // the row's entries are read 64 at a time, one per lane, and handed out
+        // through scalar registers; their tiles of op(B) come from LDS
+        const int64_t rs = static_cast<int64_t>(rp[row]) - p.base;
+        const int64_t re = static_cast<int64_t>(rp[row + 1]) - p.base;
+        float acc[J], comp[J];
 #pragma unroll
-        for (int q = 0; q < J; ++q) out[q] = alpha * acc[q];
-        if (p.c_row) {
-            T* crow = c + row * p.ldc;
-            if (!betaZero) {
-                float old[J];
-                LoadRowJ<kHalf, J>(crow, j0, p.n, 1, p.c_vec != 0, old);
-#pragma unroll
-                for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
+        for (int q = 0; q < J; ++q) {
+            acc[q] = 0.0f;
+            comp[q] = 0.0f;
+        }
+        for (int64_t e0 = rs; e0 < re; e0 += kMmWave) {
+            int32_t myc = -1;
+            float myv = 0.0f;
+            if (e0 + lane < re) {
+                const int32_t ci = p.col[e0 + lane] - p.base;
+                myc = ci >= 0 && ci < p.k ? ci : -1;
+                myv = Elem<kHalf>::Load(val, e0 + lane);
             }
-            if (p.c_vec && j0 + J <= p.n && !kHalf) {
-                Vec<T, J> wv;
+            const int cnt = re - e0 < kMmWave ? static_cast<int>(re - e0) : kMmWave;
+            for (int u0 = 0; u0 < cnt; u0 += kU) {
+                int32_t cc[kU];
+                float vv[kU];
+                float bv[kU][J];
+                SpmmFetchWave(myc, myv, u0, cnt, cc, vv);
+                bool all = true;
 #pragma unroll
-                for (int q = 0; q < J; ++q) wv.v[q] = out[q];
-                *reinterpret_cast<Vec<T, J>*>(crow + j0) = wv;
-            } else {
+                for (int q = 0; q < kU; ++q) {
+                    const int r = cc[q] >= 0 ? cc[q] : 0;
+                    all = all && cc[q] >= 0;
+                    const Vec<float, J> w = *reinterpret_cast<const Vec<float, J>*>(&sB[r * TW + lane * J]);
 #pragma unroll
-                for (int q = 0; q < J; ++q) {
-                    if (j0 + q < p.n) Elem<kHalf>::Store(crow, j0 + q, out[q]);
+                    for (int t = 0; t < J; ++t) bv[q][t] = w.v[t];
+                }
+                if (all) {  // wave-uniform: every entry of the batch counts, no selects
+#pragma unroll
+                    for (int q = 0; q < kU; ++q) {
+#pragma unroll
+                        for (int t = 0; t < J; ++t) {
+                            const float prod = vv[q] * bv[q][t];
+                            if constexpr (kKahan) {
+                                const float y = prod - comp[t];
+                                const float s2 = acc[t] + y;
+                                comp[t] = (s2 - acc[t]) - y;
+                                acc[t] = s2;
+                            } else {
+                                acc[t] = acc[t] + prod;
+                            }
+                        }
+                    }
+                } else {
+                    SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
                 }
             }
-        } else {
-#pragma unroll
-            for (int q = 0; q < J; ++q) {
-                if (j0 + q >= p.n) continue;
-                const int64_t idx = (j0 + q) * p.ldc + row;
-                float o = out[q];
-                if (!betaZero) o = o + beta * Elem<kHalf>::Load(c, idx);
-                Elem<kHalf>::Store(c, idx, o);
-            }
         }
+        if (j0 < p.n) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero);
     }
 }
 
@@ -332,18 +482,38 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpBetaCKernel(MmParams p)
 template <typename RowT, bool kHalf>
 void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s)
 {
-#define SPMM_LAUNCH(JJ, KK) \
-    hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, JJ>), dim3(grid), dim3(kMmThreads), 0, s, p)
+#define SPMM_LAUNCH(JJ, KK, WW) \
+    hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, JJ, WW>), dim3(grid), dim3(kMmThreads), 0, s, p)
+    const bool wave = p.lg == 6;  // one row per wave
     if (kahan && !kHalf) {
-        if (J == 4) SPMM_LAUNCH(4, true);
-        else if (J == 2) SPMM_LAUNCH(2, true);
-        else SPMM_LAUNCH(1, true);
+        if (J == 4) SPMM_LAUNCH(4, true, true);
+        else if (J == 2) SPMM_LAUNCH(2, true, true);
+        else if (wave) SPMM_LAUNCH(1, true, true);
+        else SPMM_LAUNCH(1, true, false);
     } else {
-        if (J == 4) SPMM_LAUNCH(4, false);
-        else if (J == 2) SPMM_LAUNCH(2, false);
-        else SPMM_LAUNCH(1, false);
+        if (J == 4) SPMM_LAUNCH(4, false, true);
+        else if (J == 2) SPMM_LAUNCH(2, false, true);
+        else if (wave) SPMM_LAUNCH(1, false, true);
+        else SPMM_LAUNCH(1, false, false);
     }
 #undef SPMM_LAUNCH
+}
+
+template <typename RowT, bool kHalf>
+void DispatchLds(const MmParams& p, int J, bool kahan, unsigned grid, unsigned lds, hipStream_t s)
+{
+#define SPMM_LDS(JJ, KK) \
+    hipLaunchKernelGGL((SpmmOpLdsKernel<RowT, kHalf, KK, JJ>), dim3(grid), dim3(kLdsThreads), lds, s, p)
+    if (kahan && !kHalf) {
+        if (J == 4) SPMM_LDS(4, true);
+        else if (J == 2) SPMM_LDS(2, true);
+        else SPMM_LDS(1, true);
+    } else {
+        if (J == 4) SPMM_LDS(4, false);
+        else if (J == 2) SPMM_LDS(2, false);
+        else SPMM_LDS(1, false);
+    }
+#undef SPMM_LDS
 }
 
 bool AlignedTo(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
@@ -383,6 +553,27 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
         else hipLaunchKernelGGL(SpmmOpBetaCKernel<false>, dim3(static_cast<unsigned>(g)), dim3(kMmThreads), 0, s, p);
         return 0;
     }
+    const bool kahan = l.high_precision != 0;
+    // small k: op(B) column tiles staged in LDS (n of at least one wave's width)
+    if (l.k > 0 && l.n >= kMmWave && l.k * kMmWave * 4 <= kLdsBytes) {
+        const int J = l.k * kMmWave * 4 * 4 <= kLdsBytes ? 4 : l.k * kMmWave * 4 * 2 <= kLdsBytes ? 2 : 1;
+        const int64_t tw = int64_t{kMmWave} * J;
+        p.tiles = (l.n + tw - 1) / tw;
+        p.c_vec = l.c_row_major && l.ldc % J == 0 && AlignedTo(l.c, J * esz) ? 1 : 0;
+        const int64_t rowsPerBlock = int64_t{kLdsThreads / kMmWave} * kLdsRowsPerWave;
+        const int64_t blocks = (l.m + rowsPerBlock - 1) / rowsPerBlock * p.tiles;
+        if (blocks <= 0x7FFFFFFF) {
+            const unsigned lds = static_cast<unsigned>(l.k * tw * 4);
+            if (l.rowptr64) {
+                if (l.fp16) DispatchLds<int64_t, true>(p, J, false, static_cast<unsigned>(blocks), lds, s);
+                else DispatchLds<int64_t, false>(p, J, kahan, static_cast<unsigned>(blocks), lds, s);
+            } else {
+                if (l.fp16) DispatchLds<int32_t, true>(p, J, false, static_cast<unsigned>(blocks), lds, s);
+                else DispatchLds<int32_t, false>(p, J, kahan, static_cast<unsigned>(blocks), lds, s);
+            }
+            return 0;
+        }
+    }
     // lanes per row (power of two) and columns per lane
     int J = 1, lg = 6;
     if (l.n > 2 * kMmWave) J = 4;
@@ -401,7 +592,6 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     int64_t grid = (p.waves + kMmThreads / kMmWave - 1) / (kMmThreads / kMmWave);
     grid = grid > (int64_t{1} << 20) ? (int64_t{1} << 20) : grid;
     const unsigned g = static_cast<unsigned>(grid);
-    const bool kahan = l.high_precision != 0;
     if (l.rowptr64) {
         if (l.fp16) Dispatch<int64_t, true>(p, J, kahan, g, s);
         else Dispatch<int64_t, false>(p, J, kahan, g, s);

@@ -236,11 +236,13 @@ def _run_plan(dev, m, k, n, rp, col, val, b_np, c_np, op_b, order_b, order_c, al
 
 @pytest.mark.parametrize("n", [1, 3, 17, 64, 65, 128, 129, 300, 1000])
 @pytest.mark.parametrize("half", [False, True])
-def test_column_tilings_bit_exact(n, half, dev):
-    """Every lane mapping (several rows per wave for n < 64, 1, 2 and 4 columns per lane above)
-    on row-major storage with padded leading dimensions, an unaligned start and entries whose
-    column lies outside [0, k); the padding is never written."""
-    m, k = 150, 90
+@pytest.mark.parametrize("k", [40, 90, 200, 700])
+def test_column_tilings_bit_exact(n, half, k, dev):
+    """Every lane mapping (several rows per wave for n < 64, 1, 2 and 4 columns per lane above;
+    op(B) tiles staged in LDS for k <= 256, read from L2 above) on row-major storage with padded
+    leading dimensions, an unaligned start and entries whose column lies outside [0, k); the
+    padding is never written."""
+    m = 150
     rp, col, val = _rand_csr(m, k, 0.15, n, bad_cols=True)
     rng = np.random.default_rng(n + 1)
     b, c = rng.uniform(-1, 1, k * n), rng.uniform(-1, 1, m * n)
