@@ -53,6 +53,16 @@ def profile_mode(name, steps):
     from ops_sparse.workloads import algorithmic_bytes
 
     dev = torch.device("cuda:0")
+    if name.startswith("spmm"):
+        from ops_sparse.spmm import SpMMOp
+        from ops_sparse import workloads as wl
+
+        case = dict(spmm_cases(dev, wl.config("c2", dev)))[name]
+        op = SpMMOp(case["m"], case["k"], case["rp"], case["col"], case["val"], case["b"], case["c"])
+        for _ in range(steps):
+            op.run(case["b"], case["c"], case["alpha"], case["beta"])
+        torch.cuda.synchronize()
+        return
     w = make(name, dev)
     y = w.y0.to(w.out_dtype).clone()
     op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]

@@ -303,8 +303,19 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
     const int64_t waveStep = static_cast<int64_t>(gridDim.x) * (kMmThreads / kMmWave);
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMmWave);
     for (int64_t w = static_cast<int64_t>(blockIdx.x) * (kMmThreads / kMmWave) + wv; w < p.waves; w += waveStep) {
-        const int64_t tile = w % p.tiles;
-        const int64_t row = (w / p.tiles) * rpw + (lane >> p.lg);
+        // (one column tile, the common case, needs no division; 32-bit division otherwise)
+        int64_t tile = 0, rg = w;
+        if (p.tiles != 1) {
+            if (p.waves <= 0x7FFFFFFF) {
+                const uint32_t wq = static_cast<uint32_t>(w) / static_cast<uint32_t>(p.tiles);
+                tile = static_cast<int64_t>(static_cast<uint32_t>(w) - wq * static_cast<uint32_t>(p.tiles));
+                rg = wq;
+            } else {
+                tile = w % p.tiles;
+                rg = w / p.tiles;
+            }
+        }
+        const int64_t row = rg * rpw + (lane >> p.lg);
         const int64_t j0 = (tile * g + (lane & (g - 1))) * J;
         // every lane of a row's group walks the row (its entries are shared
         // across the group); only lanes inside [0, n) store
