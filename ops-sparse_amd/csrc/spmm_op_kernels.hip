@@ -41,6 +41,10 @@ constexpr int kMmThreads = 256;
 constexpr int kMmWave = 64;
 constexpr float kFp16Max = 65504.0f;
 constexpr int kU = 8;  // entries whose B rows are in flight together
+#ifndef SPMM_MAX_BLOCKS
+#define SPMM_MAX_BLOCKS 8192
+#endif
+constexpr int64_t kMmMaxBlocks = SPMM_MAX_BLOCKS;  // grid cap (32 per CU); waves loop over the rest
 
 __device__ __forceinline__ float Half2Float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
@@ -218,24 +222,37 @@ __device__ __forceinline__ void SpmmAccum(const int32_t cc[kU], const float vv[k
     }
 }
 
+// C_old of one lane's J columns of one row (read before the row's products,
+// so that the read is not a step of the dependent chain); 0 past n.
+template <bool kHalf, int J>
+__device__ __forceinline__ void SpmmLoadC(const MmParams& p, const typename Elem<kHalf>::T* c, int64_t row, int64_t j0,
+                                          float old[J])
+{
+    if (p.c_row) {
+        LoadRowJ<kHalf, J>(c + row * p.ldc, j0, p.n, 1, p.c_vec != 0, old);
+    } else {
+#pragma unroll
+        for (int q = 0; q < J; ++q) old[q] = j0 + q < p.n ? Elem<kHalf>::Load(c, (j0 + q) * p.ldc + row) : 0.0f;
+    }
+}
+
 // out = alpha * sum, then + beta * C_old when beta != 0 (each step rounded),
 // stored with the element type's rounding; one lane's J columns of one row.
 template <bool kHalf, int J>
 __device__ __forceinline__ void SpmmStore(const MmParams& p, typename Elem<kHalf>::T* c, int64_t row, int64_t j0,
-                                          const float acc[J], float alpha, float beta, bool betaZero)
+                                          const float acc[J], float alpha, float beta, bool betaZero,
+                                          const float old[J])
 {
     using T = typename Elem<kHalf>::T;
     float out[J];
 #pragma unroll
     for (int q = 0; q < J; ++q) out[q] = alpha * acc[q];
+    if (!betaZero) {
+#pragma unroll
+        for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
+    }
     if (p.c_row) {
         T* crow = c + row * p.ldc;
-        if (!betaZero) {
-            float old[J];
-            LoadRowJ<kHalf, J>(crow, j0, p.n, 1, p.c_vec != 0, old);
-#pragma unroll
-            for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
-        }
         if (p.c_vec && j0 + J <= p.n && !kHalf) {
             Vec<T, J> wv;
 #pragma unroll
@@ -250,11 +267,7 @@ __device__ __forceinline__ void SpmmStore(const MmParams& p, typename Elem<kHalf
     } else {
 #pragma unroll
         for (int q = 0; q < J; ++q) {
-            if (j0 + q >= p.n) continue;
-            const int64_t idx = (j0 + q) * p.ldc + row;
-            float o = out[q];
-            if (!betaZero) o = o + beta * Elem<kHalf>::Load(c, idx);
-            Elem<kHalf>::Store(c, idx, o);
+            if (j0 + q < p.n) Elem<kHalf>::Store(c, (j0 + q) * p.ldc + row, out[q]);
         }
     }
 }
@@ -330,12 +343,14 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
             rs = static_cast<int64_t>(rp[row]) - p.base;
             re = static_cast<int64_t>(rp[row + 1]) - p.base;
         }
-        float acc[J], comp[J];
+        float acc[J], comp[J], old[J];
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             acc[q] = 0.0f;
             comp[q] = 0.0f;
+            old[q] = 0.0f;
         }
+        if (live && !betaZero) SpmmLoadC<kHalf, J>(p, c, row, j0, old);
         // Each group reads its row's entries G at a time, one per lane, and
         // hands them to the group by cross-lane reads, kU at a time.
         const int gl = lane & (g - 1);
@@ -359,7 +374,7 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
                 SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
             }
         }
-        if (live) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero);
+        if (live) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero, old);
     }
 }
 
@@ -414,12 +429,14 @@ __global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(8))
         // through scalar registers; their tiles of op(B) come from LDS
         const int64_t rs = static_cast<int64_t>(rp[row]) - p.base;
         const int64_t re = static_cast<int64_t>(rp[row + 1]) - p.base;
-        float acc[J], comp[J];
+        float acc[J], comp[J], old[J];
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             acc[q] = 0.0f;
             comp[q] = 0.0f;
+            old[q] = 0.0f;
         }
+        if (j0 < p.n && !betaZero) SpmmLoadC<kHalf, J>(p, c, row, j0, old);
         for (int64_t e0 = rs; e0 < re; e0 += kMmWave) {
             int32_t myc = -1;
             float myv = 0.0f;
@@ -464,7 +481,7 @@ __global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(8))
                 }
             }
         }
-        if (j0 < p.n) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero);
+        if (j0 < p.n) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero, old);
     }
 }
 
@@ -601,7 +618,7 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     p.b_vec = p.b_contig && l.ldb % J == 0 && AlignedTo(l.b, J * esz) ? 1 : 0;
     p.c_vec = l.c_row_major && l.ldc % J == 0 && AlignedTo(l.c, J * esz) ? 1 : 0;
     int64_t grid = (p.waves + kMmThreads / kMmWave - 1) / (kMmThreads / kMmWave);
-    grid = grid > (int64_t{1} << 20) ? (int64_t{1} << 20) : grid;
+    grid = grid > kMmMaxBlocks ? kMmMaxBlocks : grid;
     const unsigned g = static_cast<unsigned>(grid);
     if (l.rowptr64) {
         if (l.fp16) Dispatch<int64_t, true>(p, J, kahan, g, s);
