@@ -322,3 +322,28 @@ def test_beta_zero_never_reads_c_and_device_scalars(dev):
     want = oracle.spmm_f32(m, k, n, rp, col, val.astype(np.float32), 0, b.cpu().numpy().ravel(), n, 1,
                            np.zeros(m * n, np.float32), n, 1, 1.5, 0.0)
     np.testing.assert_array_equal(c.cpu().numpy().ravel().view(np.uint32), want.view(np.uint32))
+
+
+def _fuzz_params(seed):
+    rng = np.random.default_rng(seed)
+    pick = lambda xs: str(xs[int(rng.integers(len(xs)))])
+    return dict(case_name=f"fuzz{seed}", m=str(int(rng.integers(0, 700))), k=str(int(rng.integers(0, 700))),
+                n=pick([0, 1, 2, 5, 16, 31, 64, 65, 100, 128, 200, 257, 513]),
+                sparsity_ratio=pick([0.01, 0.1, 0.3, 0.5, 0.9]), alpha=pick([0.0, 1.0, -1.5, 0.7]),
+                beta=pick([0.0, 1.0, 0.5, -2.0]), dtype=pick(["ACL_FLOAT", "ACL_FLOAT16"]), compute_type="ACL_FLOAT",
+                op_b=pick(["ACL_SPARSE_OP_NON_TRANSPOSE", "ACL_SPARSE_OP_TRANSPOSE"]),
+                order_b=pick(["ACL_SPARSE_ORDER_ROW", "ACL_SPARSE_ORDER_COL"]),
+                order_c=pick(["ACL_SPARSE_ORDER_ROW", "ACL_SPARSE_ORDER_COL"]), alg=pick(sorted(ALG)),
+                pointer_mode=pick(["HOST", "DEVICE"]), value_lo="-1", value_hi="1", random_seed=str(seed),
+                skip_precision="", index_base=pick(["", "ACL_SPARSE_INDEX_BASE_ONE"]),
+                row_offset_type=pick(["", "ACL_SPARSE_INDEX_64I"]), unsorted=str(int(rng.integers(2))))
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_case_bit_exact(seed, dev):
+    """Seeded random shapes (empty ones included), dtypes, opB, orders, algorithms, pointer
+    modes, index bases, row-offset widths and unsorted rows, through the reference-case runner."""
+    p = _fuzz_params(seed)
+    r = run_case(p, dev)
+    if r["m"] * r["n"]:
+        np.testing.assert_array_equal(r["got"].view(np.uint32), r["want"].view(np.uint32))
