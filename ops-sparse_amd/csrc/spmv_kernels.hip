@@ -1531,7 +1531,6 @@ template <typename RowT, ValKind V, OutKind O, AccKind A>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
-    using ValT = typename ValOf<V>::T;
     __shared__ Acc sValAll[kFlatWaves][kStreamLds];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);

@@ -33,7 +33,6 @@ namespace aclsp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWave = 64;
 
 
 
