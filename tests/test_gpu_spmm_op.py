@@ -347,3 +347,39 @@ def test_random_case_bit_exact(seed, dev):
     r = run_case(p, dev)
     if r["m"] * r["n"]:
         np.testing.assert_array_equal(r["got"].view(np.uint32), r["want"].view(np.uint32))
+
+
+@pytest.mark.parametrize("k,n", [(90, 128), (700, 16)])
+def test_hip_graph_capture_and_replay(k, n, dev):
+    """aclsparseSpMMOp enqueues kernels only (no memsets, copies or synchronisation), so it can be
+    captured in a HIP graph: every replay, with eager work in between, matches the eager result."""
+    m = 300
+    rp, col, val = _rand_csr(m, k, 0.05, 31)
+    rng = np.random.default_rng(8)
+    b = torch.from_numpy(rng.uniform(-1, 1, (k, n)).astype(np.float32)).to(dev)
+    c0 = torch.from_numpy(rng.uniform(-1, 1, (m, n)).astype(np.float32)).to(dev)
+    d_rp, d_col = torch.from_numpy(rp.astype(np.int32)).to(dev), torch.from_numpy(col).to(dev)
+    d_val = torch.from_numpy(val.astype(np.float32)).to(dev)
+    s = torch.cuda.Stream()
+    c = c0.clone()
+    with torch.cuda.stream(s):
+        plan = SpMMOp(m, k, d_rp, d_col, d_val, b, c)
+        plan.run(b, c, 1.25, 0.5)
+    torch.cuda.synchronize()
+    eager = c.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        c.copy_(c0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            plan.run(b, c, 1.25, 0.5)
+    for _ in range(3):
+        c.copy_(c0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(c.cpu().numpy().view(np.uint32), eager.cpu().numpy().view(np.uint32))
+        with torch.cuda.stream(s):  # eager work between replays
+            plan.run(b, c, 1.0, 0.0)
+        torch.cuda.synchronize()
