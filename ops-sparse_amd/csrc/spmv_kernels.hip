@@ -1985,6 +1985,13 @@ struct CscParams {
     Scalars s;
 };
 
+#ifndef PROD_MAX_BLOCKS
+#define PROD_MAX_BLOCKS 2048
+#endif
+// Product pass grid: 2048 workgroups (8 per CU), waves looping over the
+// groups (1024 and 4096 measured slower; one workgroup per 4 groups slower still).
+constexpr int64_t kProdMaxBlocks = PROD_MAX_BLOCKS;
+
 // Four consecutive elements, moved by one vector access.
 template <typename T>
 struct alignas(4 * sizeof(T)) Quad {
@@ -2012,83 +2019,85 @@ __global__ __launch_bounds__(kThreads) void CscProductKernel(CscParams q)
     Acc* prod = static_cast<Acc*>(q.prod);
     const RowT* norm = static_cast<const RowT*>(q.norm);
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wv;
-    if (g >= q.row_groups) return;
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int64_t first = static_cast<int64_t>(norm[0]);
     const int64_t last = static_cast<int64_t>(norm[q.rows]);
-    const int64_t k0 = g * kRowGroup + 4 * lane;
-    const bool full = k0 >= first && k0 + 4 <= last;
-    const int32_t gr = ConstLoad<int32_t>(q.group_row, g);
-    const bool run = gr >= 0 && q.x_stride == 1;  // wave-uniform
-    int32_t row[4];
-    if (gr >= 0) {
-        const uint32_t d = q.row_delta[g * (kRowGroup / 4) + lane];
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wv; g < q.row_groups;
+         g += static_cast<int64_t>(gridDim.x) * (kThreads / kWave)) {
+        const int64_t k0 = g * kRowGroup + 4 * lane;
+        const bool full = k0 >= first && k0 + 4 <= last;
+        const int32_t gr = ConstLoad<int32_t>(q.group_row, g);
+        const bool run = gr >= 0 && q.x_stride == 1;  // wave-uniform
+        int32_t row[4];
+        if (gr >= 0) {
+            const uint32_t d = q.row_delta[g * (kRowGroup / 4) + lane];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) row[u] = static_cast<int32_t>((d >> (8 * u)) & 0xFFU);
-    } else if (full) {
-        const v4i r = *reinterpret_cast<const v4i*>(q.entry_row + k0);
-        row[0] = r.x;
-        row[1] = r.y;
-        row[2] = r.z;
-        row[3] = r.w;
-    } else {
+            for (int u = 0; u < 4; ++u) row[u] = static_cast<int32_t>((d >> (8 * u)) & 0xFFU);
+        } else if (full) {
+            const v4i r = *reinterpret_cast<const v4i*>(q.entry_row + k0);
+            row[0] = r.x;
+            row[1] = r.y;
+            row[2] = r.z;
+            row[3] = r.w;
+        } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) row[u] = k0 + u >= first && k0 + u < last ? q.entry_row[k0 + u] : 0;
-    }
-    ValT v[4];
-    if (kVec && full) {
-        const Quad<ValT> w = *reinterpret_cast<const Quad<ValT>*>(val + k0);
+            for (int u = 0; u < 4; ++u) row[u] = k0 + u >= first && k0 + u < last ? q.entry_row[k0 + u] : 0;
+        }
+        ValT v[4];
+        if (kVec && full) {
+            const Quad<ValT> w = *reinterpret_cast<const Quad<ValT>*>(val + k0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = w.v[u];
-    } else {
+            for (int u = 0; u < 4; ++u) v[u] = w.v[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t k = k0 + u;
+                v[u] = k >= first && k < last ? val[k * q.val_stride] : ValT{};
+            }
+        }
+        ValT xv[4];
+        if (run) {
+            // span = largest delta of the group (entries outside the matrix have delta 0)
+            int span = row[0] > row[1] ? row[0] : row[1];
+            span = span > row[2] ? span : row[2];
+            span = span > row[3] ? span : row[3];
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const int o = __shfl_xor(span, m, kWave);
+                span = span > o ? span : o;
+            }
+#pragma unroll
+            for (int j = 0; j < kRowGroup / kWave; ++j) {
+                const int i = lane + j * kWave;
+                if (j * kWave <= span && i <= span) sx[wv][i] = x[static_cast<int64_t>(gr) + i];
+            }
+            WaveLdsSync();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xv[u] = sx[wv][row[u]];
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t r = static_cast<int64_t>(gr >= 0 ? gr + row[u] : row[u]);
+                xv[u] = k0 + u >= first && k0 + u < last ? x[r * q.x_stride] : ValT{};
+            }
+        }
+        Quad<Acc> out;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t k = k0 + u;
-            v[u] = k >= first && k < last ? val[k * q.val_stride] : ValT{};
+            const Acc xr = k >= first && k < last ? ToAcc<V, A>(xv[u]) : Zero<Acc>();
+            out.v[u] = MaybeConj<V, A>(ToAcc<V, A>(v[u]), q.conj) * xr;
         }
-    }
-    ValT xv[4];
-    if (run) {
-        // span = largest delta of the group (entries outside the matrix have delta 0)
-        int span = row[0] > row[1] ? row[0] : row[1];
-        span = span > row[2] ? span : row[2];
-        span = span > row[3] ? span : row[3];
+        if (full) {
+            *reinterpret_cast<Quad<Acc>*>(prod + k0) = out;
+        } else {
 #pragma unroll
-        for (int m = 1; m < kWave; m <<= 1) {
-            const int o = __shfl_xor(span, m, kWave);
-            span = span > o ? span : o;
+            for (int u = 0; u < 4; ++u) {
+                const int64_t k = k0 + u;
+                if (k >= first && k < last) prod[k] = out.v[u];
+            }
         }
-#pragma unroll
-        for (int j = 0; j < kRowGroup / kWave; ++j) {
-            const int i = lane + j * kWave;
-            if (j * kWave <= span && i <= span) sx[wv][i] = x[static_cast<int64_t>(gr) + i];
-        }
-        WaveLdsSync();
-#pragma unroll
-        for (int u = 0; u < 4; ++u) xv[u] = sx[wv][row[u]];
-    } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t r = static_cast<int64_t>(gr >= 0 ? gr + row[u] : row[u]);
-            xv[u] = k0 + u >= first && k0 + u < last ? x[r * q.x_stride] : ValT{};
-        }
-    }
-    Quad<Acc> out;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int64_t k = k0 + u;
-        const Acc xr = k >= first && k < last ? ToAcc<V, A>(xv[u]) : Zero<Acc>();
-        out.v[u] = MaybeConj<V, A>(ToAcc<V, A>(v[u]), q.conj) * xr;
-    }
-    if (full) {
-        *reinterpret_cast<Quad<Acc>*>(prod + k0) = out;
-    } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t k = k0 + u;
-            if (k >= first && k < last) prod[k] = out.v[u];
-        }
+        WaveLdsSync();  // this group's LDS reads complete before the next group's writes
     }
 }
 
@@ -2348,7 +2357,9 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         q.group_row = At<const int32_t>(l.ws, l.layout.group_row_offset);
         q.row_delta = At<const uint32_t>(l.ws, l.layout.row_delta_offset);
         q.row_groups = l.layout.row_groups;
-        const dim3 pg(static_cast<unsigned>((l.layout.row_groups + kThreads / kWave - 1) / (kThreads / kWave)));
+        int64_t pgb = (l.layout.row_groups + kThreads / kWave - 1) / (kThreads / kWave);
+        pgb = pgb > kProdMaxBlocks ? kProdMaxBlocks : pgb;
+        const dim3 pg(static_cast<unsigned>(pgb));
         using ValT = typename ValOf<V>::T;
         if (l.val_stride == 1 && reinterpret_cast<uintptr_t>(l.val) % (4 * sizeof(ValT)) == 0) {
             hipLaunchKernelGGL((CscProductKernel<RowT, V, A, true>), pg, dim3(kThreads), 0, stream, q);
