@@ -371,3 +371,42 @@ def verify_frame_mixed(golden, actual, dtype):
     hard = bad | (diff > np.maximum(fixed, 32.0 * ulp))
     ratio = 1.0 - fails.sum() / g.size
     return bool(ratio >= 0.99 and not hard.any()), float(ratio), float(np.nanmax(np.where(bad, 0, diff)))
+
+
+# ---------------------------- SpMVOp test inputs ------------------------------
+
+_INPUTS = None
+_PATTERNS = {"random": 0, "diag": 1, "empty": 2}
+
+
+def _inputs_lib():
+    global _INPUTS
+    if _INPUTS is None:
+        path = os.path.join(_HERE, "lib", "liboracle_inputs.so")
+        if not os.path.exists(path):
+            build()
+        _INPUTS = ctypes.CDLL(path)
+        f = _INPUTS.oracle_spmvop_inputs
+        f.restype = ctypes.c_int64
+        f.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_double, ctypes.c_double, ctypes.c_uint32,
+                      ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                      ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    return _INPUTS
+
+
+def spmvop_inputs(m, k, sparsity, empty_prob, seed, pattern="random", unsorted=False):
+    """The reference SpMVOp test's A (int64 row offsets, int32 columns, fp32 values), x and y
+    (test/spmv_op/arch35/spmv_op_test.cpp:50-101, test/frame/fill.h:71-141) as this toolchain's
+    C++ standard library draws them (oracle/spmvop_inputs.cpp)."""
+    f = _inputs_lib().oracle_spmvop_inputs
+    pat = _PATTERNS[pattern]
+    mm = max(m, 0)
+    rp = np.zeros(mm + 1, np.int32)
+    nnz = f(m, k, sparsity, empty_prob, seed & 0xFFFFFFFF, pat, int(unsorted), _p(rp), None, None, 0, None, None)
+    col = np.zeros(max(nnz, 1), np.int32)
+    val = np.zeros(max(nnz, 1), np.float32)
+    x = np.zeros(max(k, 1), np.float32)
+    y = np.zeros(max(mm, 1), np.float32)
+    f(m, k, sparsity, empty_prob, seed & 0xFFFFFFFF, pat, int(unsorted), _p(rp), _p(col), _p(val), nnz, _p(x),
+      _p(y))
+    return rp.astype(np.int64), col[:nnz], val[:nnz], x[:max(k, 0)], y[:mm]

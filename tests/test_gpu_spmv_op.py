@@ -4,13 +4,15 @@ Cases come from the reference's own parameter table
 (test/spmv_op/arch35/spmv_op_test.csv, kept as tests/golden/spmv_op_cases.csv):
 shape, sparsity, empty-row probability, seed, alpha, beta, pointer mode, row
 offset type, Z/Y aliasing, unsorted columns, algorithm and the MERE/MARE
-thresholds.  The matrices are drawn by our own seeded generator with the same
-statistics (independent Bernoulli entries of density 1-sparsity, rows emptied
-with the given probability, values and vectors uniform in [-3, 3]), as the
-reference's generator is C++ std::mt19937 code we do not run here.  The golden
-is the fp64 oracle rounded to fp32 (the reference's SpMVOpGolden,
-test/spmv_op/spmv_op_golden.h), checked with the reference's MERE/MARE
-verifier (test/frame/verify.h:126-175) as restated in the oracle.
+thresholds.  The matrices and vectors are the reference's own: the oracle's
+input generator (oracle/spmvop_inputs.cpp) makes the same C++ standard-library
+draws as the reference's SparseFillGenerator and test body (binomial row
+lengths, distinct uniform columns, uniform values in [-5, 5], x and y in
+[-3, 3] from seeds + 1 and + 2, row-wise shuffles for unsorted cases), as this
+toolchain's libstdc++ computes them.  The golden is the fp64 oracle rounded to
+fp32 (the reference's SpMVOpGolden, test/spmv_op/spmv_op_golden.h), checked
+with the reference's MERE/MARE verifier (test/frame/verify.h:126-175) as
+restated in the oracle.
 
 The ALG2 preprocess tables (row reorder by descending length, sorted lengths,
 bin edges) are compared bit-exactly with the oracle's restatement of the
@@ -58,46 +60,16 @@ def num_bins(m, dev):
     return max(1, min(cus, -(-m // 128))) if m > 0 else 0
 
 
-def make_csr(m, k, sparsity, empty_prob, seed, pattern, unsorted):
-    """Seeded CSR with int64 offsets (numpy), values in [-3, 3]."""
-    rng = np.random.default_rng(seed)
-    if pattern == "empty" or m <= 0 or k <= 0:
-        return np.zeros(max(m, 0) + 1, np.int64), np.zeros(0, np.int32), np.zeros(0, np.float32)
-    if pattern == "diag":
-        n = min(m, k)
-        rp = np.concatenate([np.arange(n + 1), np.full(m - n, n)]).astype(np.int64)
-        return rp, np.arange(n, dtype=np.int32), np.ones(n, np.float32)
-    density = 1.0 - sparsity
-    counts = np.zeros(m, np.int64)
-    cols = []
-    step = max(1, (1 << 24) // k)
-    for r0 in range(0, m, step):
-        r1 = min(m, r0 + step)
-        mask = rng.random((r1 - r0, k)) < density
-        if empty_prob > 0:
-            mask[rng.random(r1 - r0) < empty_prob] = False
-        rr, cc = np.nonzero(mask)
-        counts[r0:r1] = mask.sum(axis=1)
-        cols.append(cc.astype(np.int32))
-    col = np.concatenate(cols) if cols else np.zeros(0, np.int32)
-    rp = np.zeros(m + 1, np.int64)
-    np.cumsum(counts, out=rp[1:])
-    if unsorted:
-        for r in range(m):
-            seg = col[rp[r]:rp[r + 1]]
-            rng.shuffle(seg)
-    val = rng.uniform(-3.0, 3.0, col.size).astype(np.float32)
-    return rp, col, val
+def make_inputs(m, k, sparsity, empty_prob, seed, pattern, unsorted):
+    """The reference test's A (int64 offsets), x and y for one CSV row."""
+    return oracle.spmvop_inputs(m, k, sparsity, empty_prob, seed, pattern, unsorted)
 
 
 def run_case(c, dev, alg=None):
     m, k = int(c["m"]), int(c["k"])
     seed = int(c["seed"])
-    rp, col, val = make_csr(m, k, float(c["sparsity"]), float(c["empty_row_prob"]), seed, c["pattern"],
-                            c["unsorted"] == "1")
-    rng = np.random.default_rng(seed + 1)
-    x = rng.uniform(-3.0, 3.0, max(k, 0)).astype(np.float32)
-    y = rng.uniform(-3.0, 3.0, max(m, 0)).astype(np.float32)
+    rp, col, val, x, y = make_inputs(m, k, float(c["sparsity"]), float(c["empty_row_prob"]), seed, c["pattern"],
+                                     c["unsorted"] == "1")
     alpha, beta = float(c["alpha"]), float(c["beta"])
     ptr_dtype = torch.int64 if c["row_offset_type"] == "i64" else torch.int32
     d_rp = torch.from_numpy(rp).to(ptr_dtype).to(dev)
@@ -208,7 +180,7 @@ def test_nnz_zero_beta_y_and_reexecute(dev):
 
 def test_beta_zero_ignores_nan_y(dev):
     """beta == 0 does not read Y: NaN in Y does not reach Z."""
-    rp, col, val = make_csr(500, 400, 0.9, 0.0, 7, "random", False)
+    rp, col, val, _, _ = make_inputs(500, 400, 0.9, 0.0, 7, "random", False)
     rng = np.random.default_rng(8)
     x = rng.uniform(-3, 3, 400).astype(np.float32)
     for alg in (SpMVOpAlg.ALG1, SpMVOpAlg.ALG2):
@@ -226,7 +198,7 @@ def test_beta_zero_ignores_nan_y(dev):
 
 def test_plan_reuse_with_new_vectors(dev):
     """One plan, executed against different X/Y/Z descriptors of the same sizes."""
-    rp, col, val = make_csr(3000, 2000, 0.98, 0.1, 11, "random", False)
+    rp, col, val, _, _ = make_inputs(3000, 2000, 0.98, 0.1, 11, "random", False)
     d = [torch.from_numpy(a).to(dev) for a in (rp.astype(np.int32), col, val)]
     rng = np.random.default_rng(12)
     x1 = rng.uniform(-3, 3, 2000).astype(np.float32)

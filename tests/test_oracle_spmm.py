@@ -203,3 +203,51 @@ def test_frame_mixed_verifier():
     assert not oracle.verify_frame_mixed(g, a, "float32")[0]
     h = np.linspace(-2, 2, 1000).astype(np.float16).astype(np.float32)
     assert oracle.verify_frame_mixed(h, h + np.float32(5e-4), "float16")[0]
+
+
+def _uniform_float(seed, lo, hi, count):
+    """libstdc++ uniform_real_distribution<float>: generate_canonical<float, 24> takes one
+    32-bit word, float(w) / 2^32 (in float), then u * (hi - lo) + lo in float."""
+    w = oracle.mt19937(seed, count).astype(np.float32)
+    u = w / np.float32(4294967296.0)
+    u = np.where(u >= 1, np.nextafter(np.float32(1), np.float32(0)), u).astype(np.float32)
+    return (u * np.float32(hi - lo) + np.float32(lo)).astype(np.float32)
+
+
+def test_spmvop_inputs_follow_the_reference_generator():
+    """SpMVOp test inputs (oracle/spmvop_inputs.cpp): x and y are the float draws of
+    mt19937(seed+1) / mt19937(seed+2) in [-3, 3]; rows hold distinct sorted columns (shuffled
+    row-wise for unsorted cases, same multiset), values in [-5, 5], lengths near the binomial
+    mean; diag and empty patterns; the same call gives the same bits."""
+    m, k, seed = 300, 200, 77
+    rp, col, val, x, y = oracle.spmvop_inputs(m, k, 0.9, 0.0, seed)
+    np.testing.assert_array_equal(x, _uniform_float(seed + 1, -3.0, 3.0, k))
+    np.testing.assert_array_equal(y, _uniform_float(seed + 2, -3.0, 3.0, m))
+    lens = np.diff(rp)
+    assert abs(lens.mean() - 0.1 * k) < 3 and np.all(lens >= 0)
+    for i in range(m):
+        c = col[rp[i]:rp[i + 1]]
+        assert np.all(np.diff(c) > 0) and (c.size == 0 or (c[0] >= 0 and c[-1] < k))
+    assert np.all(np.abs(val) <= 5.0) and np.all(np.isfinite(val))
+    rp2, col2, val2, _, _ = oracle.spmvop_inputs(m, k, 0.9, 0.0, seed)
+    np.testing.assert_array_equal(col, col2)
+    np.testing.assert_array_equal(val, val2)
+    rpu, colu, valu, _, _ = oracle.spmvop_inputs(m, k, 0.9, 0.0, seed, unsorted=True)
+    np.testing.assert_array_equal(rpu, rp)
+    assert not np.array_equal(colu, col)
+    for i in range(m):
+        s, e = rp[i], rp[i + 1]
+        o = np.argsort(colu[s:e])
+        np.testing.assert_array_equal(colu[s:e][o], col[s:e])
+        np.testing.assert_array_equal(valu[s:e][o], val[s:e])
+    rpe, cole, _, _, _ = oracle.spmvop_inputs(m, k, 0.5, 0.9, seed)  # 90% empty rows
+    assert (np.diff(rpe) == 0).mean() > 0.8
+    rpd, cold, vald, _, _ = oracle.spmvop_inputs(5, 5, 0.0, 0.0, 1, "diag")
+    np.testing.assert_array_equal(rpd, np.arange(6))
+    np.testing.assert_array_equal(cold, np.arange(5))
+    np.testing.assert_array_equal(vald, np.ones(5, np.float32))
+    rpz, colz, _, _, _ = oracle.spmvop_inputs(4, 3, 0.5, 0.0, 1, "empty")
+    assert colz.size == 0 and np.all(rpz == 0)
+    # dense rows (sparsity 0): the attempt budget runs out and the row completes from the unused columns
+    rpf, colf, _, _, _ = oracle.spmvop_inputs(20, 50, 0.0, 0.0, 3)
+    np.testing.assert_array_equal(np.diff(rpf), np.full(20, 50))
