@@ -5,7 +5,8 @@ cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
 product never imports this module.  Inputs are numpy arrays; CSR data must be
 contiguous (row offsets are converted to int64 here) and base 0, except for the
 SpMMOp functions, which take the index base.  The SpMV restatement is
-spmv_oracle.c, the SpMMOp one spmm_oracle.c.
+spmv_oracle.c, the SpMMOp one spmm_oracle.c; spmvop_inputs.cpp rebuilds the
+SpMVOp tests' inputs.
 """
 import ctypes
 import os
