@@ -383,3 +383,22 @@ def test_hip_graph_capture_and_replay(k, n, dev):
         with torch.cuda.stream(s):  # eager work between replays
             plan.run(b, c, 1.0, 0.0)
         torch.cuda.synchronize()
+
+
+def test_bench_laplacian_block_full_size_bit_exact(dev):
+    """The bench's HBM-sized SpMMOp workload at full size (c2's 4.19 M-row Laplacian times a
+    4.19 M x 16 block, alpha 1.5, beta 0.5), bit-identical to the oracle's fp32 steps."""
+    from ops_sparse import workloads as wl
+
+    w = wl.config("c2", "cpu")
+    n = 16
+    rng = np.random.default_rng(16)
+    b = rng.uniform(-1, 1, (w.cols, n)).astype(np.float32)
+    c0 = rng.uniform(-1, 1, (w.rows, n)).astype(np.float32)
+    db, dc = torch.from_numpy(b).to(dev), torch.from_numpy(c0).to(dev)
+    plan = SpMMOp(w.rows, w.cols, w.row_ptr.to(dev), w.col_ind.to(dev), w.values.to(dev), db, dc)
+    plan.run(db, dc, 1.5, 0.5)
+    torch.cuda.synchronize()
+    want = oracle.spmm_f32(w.rows, w.cols, n, w.row_ptr.numpy(), w.col_ind.numpy(), w.values.numpy(), 0, b.ravel(), n,
+                           1, c0.ravel(), n, 1, 1.5, 0.5)
+    np.testing.assert_array_equal(dc.cpu().numpy().ravel().view(np.uint32), want.view(np.uint32))
