@@ -25,7 +25,10 @@
 // row's column indices and values are read G at a time (one per lane) and
 // handed to the group by cross-lane reads; eight entries' B rows are in
 // flight at a time.  Short outputs (n < 64) pack several rows
-// into one wave instead of idling lanes.
+// into one wave instead of idling lanes; outputs of 8 to 32 columns (a
+// multiple of 4) give each row 2, 4 or 8 lanes of 4 columns (32, 16 or 8 rows
+// per wave), each lane reading 4, 2 or 1 of a window's 8 entries, so that a
+// wave keeps 8 entries' B rows in flight for many rows at once.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -299,8 +302,17 @@ __device__ __forceinline__ void SpmmFetch(int myc, float myv, int gbase, int g, 
     }
 }
 
-template <typename RowT, bool kHalf, bool kKahan, int J, bool kWave>
-__global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
+// kNG > 0: groups of kNG < kU lanes (g == kNG), each lane reading kU / kNG
+// entries per window, so that a window fills one batch of kU entries.
+// Narrow groups: at least 5 waves per SIMD (at most 102 VGPRs; 4 waves at the
+// 124 the compiler picks otherwise: 264 -> 251 us on the Laplacian x 16; 6
+// waves spill).
+#ifndef SPMM_NARROW_WPE
+#define SPMM_NARROW_WPE 5
+#endif
+template <typename RowT, bool kHalf, bool kKahan, int J, bool kWave, int kNG = 0>
+__global__ __launch_bounds__(kMmThreads) __attribute__((amdgpu_waves_per_eu(kNG > 0 ? SPMM_NARROW_WPE : 1)))
+void SpmmOpKernel(MmParams p)
 {
     using T = typename Elem<kHalf>::T;
     const RowT* rp = static_cast<const RowT*>(p.rp);
@@ -355,6 +367,36 @@ __global__ __launch_bounds__(kMmThreads) void SpmmOpKernel(MmParams p)
         // hands them to the group by cross-lane reads, kU at a time.
         const int gl = lane & (g - 1);
         const int gbase = lane & ~(g - 1);
+        if constexpr (kNG > 0) {
+            constexpr int kE = kU / kNG;
+            for (int64_t e0 = rs; e0 < re; e0 += kU) {
+                int32_t myc[kE];
+                float myv[kE];
+#pragma unroll
+                for (int s = 0; s < kE; ++s) {
+                    const int64_t e = e0 + s * kNG + gl;
+                    myc[s] = -1;
+                    myv[s] = 0.0f;
+                    if (e < re) {
+                        const int32_t ci = p.col[e] - p.base;
+                        myc[s] = ci >= 0 && ci < p.k ? ci : -1;
+                        myv[s] = Elem<kHalf>::Load(val, e);
+                    }
+                }
+                const int cnt = re - e0 < kU ? static_cast<int>(re - e0) : kU;
+                int32_t cc[kU];
+                float vv[kU];
+                float bv[kU][J];
+#pragma unroll
+                for (int q = 0; q < kU; ++q) {
+                    const int32_t cq = __shfl(myc[q / kNG], gbase + q % kNG, kMmWave);
+                    vv[q] = __shfl(myv[q / kNG], gbase + q % kNG, kMmWave);
+                    cc[q] = q < cnt ? cq : -1;
+                }
+                SpmmLoad<kHalf, J>(p, b, j0, fast, strided, cc, bv);
+                SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
+            }
+        } else
         for (int64_t e0 = rs; e0 < re; e0 += g) {
             int32_t myc = -1;
             float myv = 0.0f;
@@ -512,8 +554,15 @@ void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s
 {
 #define SPMM_LAUNCH(JJ, KK, WW) \
     hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, JJ, WW>), dim3(grid), dim3(kMmThreads), 0, s, p)
+#define SPMM_NARROW(KK, NG) \
+    hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, 4, false, NG>), dim3(grid), dim3(kMmThreads), 0, s, p)
     const bool wave = p.lg == 6;  // one row per wave
-    if (kahan && !kHalf) {
+    if (J == 4 && p.lg < 6) {  // narrow groups: 2, 4 or 8 lanes of 4 columns per row
+        const bool k2 = kahan && !kHalf;
+        if (p.lg == 1) { if (k2) SPMM_NARROW(true, 2); else SPMM_NARROW(false, 2); }
+        else if (p.lg == 2) { if (k2) SPMM_NARROW(true, 4); else SPMM_NARROW(false, 4); }
+        else { if (k2) SPMM_NARROW(true, 8); else SPMM_NARROW(false, 8); }
+    } else if (kahan && !kHalf) {
         if (J == 4) SPMM_LAUNCH(4, true, true);
         else if (J == 2) SPMM_LAUNCH(2, true, true);
         else if (wave) SPMM_LAUNCH(1, true, true);
@@ -525,6 +574,7 @@ void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s
         else SPMM_LAUNCH(1, false, false);
     }
 #undef SPMM_LAUNCH
+#undef SPMM_NARROW
 }
 
 template <typename RowT, bool kHalf>
@@ -606,7 +656,11 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     int J = 1, lg = 6;
     if (l.n > 2 * kMmWave) J = 4;
     else if (l.n > kMmWave) J = 2;
-    else {
+    else if (l.n >= 8 && l.n <= 32 && l.n % 4 == 0) {
+        J = 4;  // 2, 4 or 8 lanes of 4 columns per row
+        lg = 1;
+        while ((int64_t{4} << lg) < l.n) ++lg;
+    } else {
         lg = 0;
         while ((int64_t{1} << lg) < l.n) ++lg;
     }

@@ -234,7 +234,7 @@ def _run_plan(dev, m, k, n, rp, col, val, b_np, c_np, op_b, order_b, order_c, al
     return got, want, plan
 
 
-@pytest.mark.parametrize("n", [1, 3, 17, 64, 65, 128, 129, 300, 1000])
+@pytest.mark.parametrize("n", [1, 3, 8, 12, 16, 17, 24, 32, 64, 65, 128, 129, 300, 1000])
 @pytest.mark.parametrize("half", [False, True])
 @pytest.mark.parametrize("k", [40, 90, 200, 700])
 def test_column_tilings_bit_exact(n, half, k, dev):
@@ -250,6 +250,21 @@ def test_column_tilings_bit_exact(n, half, k, dev):
         got, want, _ = _run_plan(dev, m, k, n, rp, col, val, b, c, Operation.NON_TRANSPOSE, Order.ROW, Order.ROW,
                                  SpMMOpAlg.ALG1, half, 1.25, -0.5, ldb_pad, ldc_pad, offset)
         np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [8, 12, 16, 20, 32])
+@pytest.mark.parametrize("alg", [SpMMOpAlg.ALG1, SpMMOpAlg.ALG1_HIGH_PRECISION])
+def test_narrow_groups_bit_exact(n, alg, dev):
+    """Outputs of 8 to 32 columns (2, 4 or 8 lanes of 4 columns per row, 32, 16 or 8 rows per
+    wave, eight entries per window): rows of 0 to 40 entries, so windows end inside and past a
+    row, with plain and compensated sums."""
+    m, k = 700, 300
+    rp, col, val = _rand_csr(m, k, 0.05, n, bad_cols=True)
+    rng = np.random.default_rng(n + 7)
+    b, c = rng.uniform(-1, 1, k * n), rng.uniform(-1, 1, m * n)
+    got, want, _ = _run_plan(dev, m, k, n, rp, col, val, b, c, Operation.NON_TRANSPOSE, Order.ROW, Order.ROW,
+                             alg, False, 0.75, 1.5, 0, 0, 0)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("op_b", [Operation.NON_TRANSPOSE, Operation.TRANSPOSE])
