@@ -28,7 +28,8 @@
 // into one wave instead of idling lanes; outputs of 8 to 32 columns (a
 // multiple of 4) give each row 2, 4 or 8 lanes of 4 columns (32, 16 or 8 rows
 // per wave), each lane reading 4, 2 or 1 of a window's 8 entries, so that a
-// wave keeps 8 entries' B rows in flight for many rows at once.
+// wave keeps 8 entries' B rows in flight for many rows at once; 36 to 64
+// columns (a multiple of 4) give each row 16 lanes of 4 columns.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -348,7 +349,10 @@ void SpmmOpKernel(MmParams p)
         // wave-uniform load paths: whole tiles of contiguous, aligned rows of op(B); or B
         // stored the other way (element loads); else the guarded general path
         const bool fullTile = (tile + 1) * g * J <= p.n;
-        const bool fast = p.has_b && p.b_contig && p.b_vec && fullTile;
+        // (n a multiple of J: a lane's J columns lie wholly inside or wholly
+        // past n, and lanes past n read column 0 of the same rows)
+        const bool fast = p.has_b && p.b_contig && p.b_vec && (fullTile || p.n % J == 0);
+        const int64_t jf = j0 < p.n ? j0 : 0;
         const bool strided = p.has_b && !p.b_contig;
         int64_t rs = 0, re = 0;
         if (row < p.m) {
@@ -393,7 +397,7 @@ void SpmmOpKernel(MmParams p)
                     vv[q] = __shfl(myv[q / kNG], gbase + q % kNG, kMmWave);
                     cc[q] = q < cnt ? cq : -1;
                 }
-                SpmmLoad<kHalf, J>(p, b, j0, fast, strided, cc, bv);
+                SpmmLoad<kHalf, J>(p, b, fast ? jf : j0, fast, strided, cc, bv);
                 SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
             }
         } else
@@ -412,7 +416,7 @@ void SpmmOpKernel(MmParams p)
                 float bv[kU][J];
                 if constexpr (kWave) SpmmFetchWave(myc, myv, u0, cnt, cc, vv);
                 else SpmmFetch(myc, myv, gbase, g, u0, cnt, cc, vv);
-                SpmmLoad<kHalf, J>(p, b, j0, fast, strided, cc, bv);
+                SpmmLoad<kHalf, J>(p, b, fast ? jf : j0, fast, strided, cc, bv);
                 SpmmAccum<kKahan, J>(cc, vv, bv, acc, comp);
             }
         }
@@ -557,7 +561,10 @@ void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s
 #define SPMM_NARROW(KK, NG) \
     hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, 4, false, NG>), dim3(grid), dim3(kMmThreads), 0, s, p)
     const bool wave = p.lg == 6;  // one row per wave
-    if (J == 4 && p.lg < 6) {  // narrow groups: 2, 4 or 8 lanes of 4 columns per row
+    if (J == 4 && p.lg == 4) {  // 16 lanes of 4 columns per row, 4 rows per wave
+        if (kahan && !kHalf) SPMM_LAUNCH(4, true, false);
+        else SPMM_LAUNCH(4, false, false);
+    } else if (J == 4 && p.lg < 6) {  // narrow groups: 2, 4 or 8 lanes of 4 columns per row
         const bool k2 = kahan && !kHalf;
         if (p.lg == 1) { if (k2) SPMM_NARROW(true, 2); else SPMM_NARROW(false, 2); }
         else if (p.lg == 2) { if (k2) SPMM_NARROW(true, 4); else SPMM_NARROW(false, 4); }
@@ -656,7 +663,10 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     int J = 1, lg = 6;
     if (l.n > 2 * kMmWave) J = 4;
     else if (l.n > kMmWave) J = 2;
-    else if (l.n >= 8 && l.n <= 32 && l.n % 4 == 0) {
+    else if (l.n > 32 && l.n % 4 == 0) {
+        J = 4;  // 16 lanes of 4 columns per row
+        lg = 4;
+    } else if (l.n >= 8 && l.n <= 32 && l.n % 4 == 0) {
         J = 4;  // 2, 4 or 8 lanes of 4 columns per row
         lg = 1;
         while ((int64_t{4} << lg) < l.n) ++lg;

@@ -252,7 +252,7 @@ def test_column_tilings_bit_exact(n, half, k, dev):
         np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("n", [8, 12, 16, 20, 32])
+@pytest.mark.parametrize("n", [8, 12, 16, 20, 32, 48, 64])
 @pytest.mark.parametrize("alg", [SpMMOpAlg.ALG1, SpMMOpAlg.ALG1_HIGH_PRECISION])
 def test_narrow_groups_bit_exact(n, alg, dev):
     """Outputs of 8 to 32 columns (2, 4 or 8 lanes of 4 columns per row, 32, 16 or 8 rows per
