@@ -28,8 +28,9 @@
 // into one wave instead of idling lanes; outputs of 8 to 32 columns (a
 // multiple of 4) give each row 2, 4 or 8 lanes of 4 columns (32, 16 or 8 rows
 // per wave), each lane reading 4, 2 or 1 of a window's 8 entries, so that a
-// wave keeps 8 entries' B rows in flight for many rows at once; 36 to 64
-// columns (a multiple of 4) give each row 16 lanes of 4 columns.
+// wave keeps 8 entries' B rows in flight for many rows at once.  Wider
+// outputs whose width is a multiple of 4 give each row 16, 32 or 64 lanes of 4
+// columns (4, 2 or 1 rows per wave).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -561,7 +562,7 @@ void Dispatch(const MmParams& p, int J, bool kahan, unsigned grid, hipStream_t s
 #define SPMM_NARROW(KK, NG) \
     hipLaunchKernelGGL((SpmmOpKernel<RowT, kHalf, KK, 4, false, NG>), dim3(grid), dim3(kMmThreads), 0, s, p)
     const bool wave = p.lg == 6;  // one row per wave
-    if (J == 4 && p.lg == 4) {  // 16 lanes of 4 columns per row, 4 rows per wave
+    if (J == 4 && (p.lg == 4 || p.lg == 5)) {  // 16 or 32 lanes of 4 columns per row
         if (kahan && !kHalf) SPMM_LAUNCH(4, true, false);
         else SPMM_LAUNCH(4, false, false);
     } else if (J == 4 && p.lg < 6) {  // narrow groups: 2, 4 or 8 lanes of 4 columns per row
@@ -661,18 +662,16 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     }
     // lanes per row (power of two) and columns per lane
     int J = 1, lg = 6;
-    if (l.n > 2 * kMmWave) J = 4;
-    else if (l.n > kMmWave) J = 2;
-    else if (l.n > 32 && l.n % 4 == 0) {
-        J = 4;  // 16 lanes of 4 columns per row
-        lg = 4;
-    } else if (l.n >= 8 && l.n <= 32 && l.n % 4 == 0) {
-        J = 4;  // 2, 4 or 8 lanes of 4 columns per row
+    if (l.n >= 8 && l.n % 4 == 0) {
+        J = 4;  // 2, 4, ... 64 lanes of 4 columns per row
         lg = 1;
-        while ((int64_t{4} << lg) < l.n) ++lg;
+        while (lg < 6 && (int64_t{4} << lg) < l.n) ++lg;
+    } else if (l.n > 2 * kMmWave) {
+        J = 4;
+    } else if (l.n > kMmWave) {
+        J = 2;
     } else {
-        lg = 0;
-        while ((int64_t{1} << lg) < l.n) ++lg;
+        while (lg > 0 && (int64_t{1} << (lg - 1)) >= l.n) --lg;
     }
     p.lg = lg;
     const int64_t tileCols = (int64_t{1} << lg) * J;

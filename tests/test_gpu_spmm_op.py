@@ -252,11 +252,11 @@ def test_column_tilings_bit_exact(n, half, k, dev):
         np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("n", [8, 12, 16, 20, 32, 48, 64])
+@pytest.mark.parametrize("n", [8, 12, 16, 20, 32, 48, 64, 100, 128, 200])
 @pytest.mark.parametrize("alg", [SpMMOpAlg.ALG1, SpMMOpAlg.ALG1_HIGH_PRECISION])
 def test_narrow_groups_bit_exact(n, alg, dev):
-    """Outputs of 8 to 32 columns (2, 4 or 8 lanes of 4 columns per row, 32, 16 or 8 rows per
-    wave, eight entries per window): rows of 0 to 40 entries, so windows end inside and past a
+    """Outputs whose width is a multiple of 4 (2 to 64 lanes of 4 columns per row; 2, 4 or 8
+    lanes read a window of eight entries together): rows of 0 to 40 entries, so windows end inside and past a
     row, with plain and compensated sums."""
     m, k = 700, 300
     rp, col, val = _rand_csr(m, k, 0.05, n, bad_cols=True)
