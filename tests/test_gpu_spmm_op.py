@@ -343,7 +343,7 @@ def _fuzz_params(seed):
     rng = np.random.default_rng(seed)
     pick = lambda xs: str(xs[int(rng.integers(len(xs)))])
     return dict(case_name=f"fuzz{seed}", m=str(int(rng.integers(0, 700))), k=str(int(rng.integers(0, 700))),
-                n=pick([0, 1, 2, 5, 16, 31, 64, 65, 100, 128, 200, 257, 513]),
+                n=pick([0, 1, 2, 5, 8, 12, 16, 24, 31, 48, 64, 65, 100, 128, 200, 257, 513]),
                 sparsity_ratio=pick([0.01, 0.1, 0.3, 0.5, 0.9]), alpha=pick([0.0, 1.0, -1.5, 0.7]),
                 beta=pick([0.0, 1.0, 0.5, -2.0]), dtype=pick(["ACL_FLOAT", "ACL_FLOAT16"]), compute_type="ACL_FLOAT",
                 op_b=pick(["ACL_SPARSE_OP_NON_TRANSPOSE", "ACL_SPARSE_OP_TRANSPOSE"]),
@@ -354,7 +354,7 @@ def _fuzz_params(seed):
                 row_offset_type=pick(["", "ACL_SPARSE_INDEX_64I"]), unsorted=str(int(rng.integers(2))))
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(96))
 def test_random_case_bit_exact(seed, dev):
     """Seeded random shapes (empty ones included), dtypes, opB, orders, algorithms, pointer
     modes, index bases, row-offset widths and unsorted rows, through the reference-case runner."""
