@@ -453,3 +453,22 @@ def test_spmmop_validation(env, lib):
     assert ex(env.h, plan, pa, pb, B, Cm) == Status.INVALID_VALUE  # 3 x 4 is not n x k = 4 x 3
     lib.aclsparseSpMMOp_destroyPlan(plan)
     lib.aclsparseSpMMOp_destroyDescr(d)
+
+
+def test_bridge_operators_defined_without_cpu_fallback():
+    # torch_npu/spmv_npu.cpp:410-437: ops_sparse::spmv and the ops_sparse_test::spmv_npu hook,
+    # with device kernels only (test_spmv_npu.py:104-113: CPU tensors raise, no fallback)
+    import torch
+    import ops_sparse  # noqa: F401
+
+    assert "spmv(Tensor mat, Tensor vec) -> Tensor" in str(torch.ops.ops_sparse.spmv.default._schema)
+    schema = str(torch.ops.ops_sparse_test.spmv_npu.default._schema)
+    assert "Tensor(a!) y" in schema and schema.endswith("-> Tensor(a!)")
+    for key in ("CUDA", "SparseCsrCUDA"):
+        assert torch._C._dispatch_has_kernel_for_dispatch_key("ops_sparse::spmv", key)
+    assert torch._C._dispatch_has_kernel_for_dispatch_key("ops_sparse_test::spmv_npu", "CUDA")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key("ops_sparse_test::spmv_npu", "CPU")
+    row_ptr = torch.tensor([0, 0], dtype=torch.int32)
+    empty_i, empty_f = torch.empty(0, dtype=torch.int32), torch.empty(0, dtype=torch.float32)
+    with pytest.raises(RuntimeError):
+        torch.ops.ops_sparse_test.spmv_npu(row_ptr, empty_i, empty_f, empty_f, empty_f, 1.0, 0.0, "N", 0)
