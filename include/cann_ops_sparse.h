@@ -186,6 +186,11 @@ aclsparseStatus_t aclsparseGetStream(aclsparseHandle_t handle, aclrtStream* stre
 aclsparseStatus_t aclsparseSetWorkspace(aclsparseHandle_t handle, void* workspace, size_t workspaceSize);
 /* replaces include/cann_ops_sparse.h:1605 aclsparseGetWorkspace */
 aclsparseStatus_t aclsparseGetWorkspace(aclsparseHandle_t handle, void** workspace, size_t* workspaceSize);
+/* No counterpart in the reference: the build id of this library (the first 32
+ * hex digits of a SHA-256 over its native sources, this header and the
+ * compiler flags), for loaders that refuse a library built from other
+ * sources.  The returned string is static. */
+const char* aclsparseHipBuildId(void);
 /* replaces include/cann_ops_sparse.h:1617 aclsparseGetVersion */
 aclsparseStatus_t aclsparseGetVersion(aclsparseHandle_t handle, int* version);
 /* replaces include/cann_ops_sparse.h:1637 aclsparseSetPointerMode */

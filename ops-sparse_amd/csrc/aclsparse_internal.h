@@ -106,7 +106,7 @@ namespace aclsp {
 //                       (lets a block start streaming before reading its rows)
 //   sink                512 bytes the kernel stores into for lanes that have
 //                       no output row this chunk (keeps stores branch-free)
-//   accumulator         transpose only: cols x accumulator element
+//   accumulator         transpose without non-zeros: cols x accumulator element
 // ---------------------------------------------------------------------------
 constexpr size_t kWsAlign = 64;
 constexpr size_t kWsHeaderBytes = 192;
@@ -183,9 +183,9 @@ struct SpmvLayout {
     // (key_a/key_b int32[nnz], val_b RowT[nnz], radix-sort storage).  At
     // execution time the products a_k * x_row(k) go to prod[nnz] (the
     // accumulator type, at most 8 bytes: it reuses key_a/key_b, which only
-    // Preprocess needs).  Without a CSC pattern (nnz beyond the sort's int
-    // range) the transpose scatters with atomics into the accumulator at
-    // acc_offset.
+    // Preprocess needs).  A transpose without non-zeros has no CSC pattern:
+    // y = beta*y, through the accumulator at acc_offset when y is not of the
+    // accumulator type.  Transposes with nnz > INT32_MAX are rejected.
     bool csc = false;
     size_t colptr_offset = 0, entry_row_offset = 0, csc_pos_offset = 0, prod_offset = 0;
     // row-block partition of the CSC pattern (columns as rows), for the

@@ -148,6 +148,16 @@ aclsparseStatus_t aclsparseGetWorkspace(aclsparseHandle_t handle, void** workspa
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
+// Build id: SHA-256 (first 32 hex digits) of the native sources, the public
+// header and the compiler flags, set by the build script.  The prefix lets the
+// id be read from the library file without loading it.
+#ifndef ACLSPARSE_HIP_BUILD_ID
+#define ACLSPARSE_HIP_BUILD_ID "unknown"
+#endif
+static const char kBuildIdRecord[] = "aclsparse-hip-build-id:" ACLSPARSE_HIP_BUILD_ID;
+
+const char* aclsparseHipBuildId(void) { return kBuildIdRecord + sizeof("aclsparse-hip-build-id:") - 1; }
+
 aclsparseStatus_t aclsparseGetVersion(aclsparseHandle_t handle, int* version)
 {
     (void)handle;  // may be null

@@ -137,6 +137,13 @@ aclsparseStatus_t ValidateInputs(aclsparseHandle_t h, aclsparseOperation_t op, c
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
     st = ValidateMetadata(A, x, y, c);
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    // The transpose sums every column in CSR order through a CSC pattern
+    // whose sort is limited to INT32_MAX entries (the reference's own nnz
+    // limit, sparse/spmv/README.md "nnz 不超过 INT32_MAX"); larger transposes
+    // (possible only with this build's 64-bit row offsets) are not supported.
+    if (IsTranspose(op) && A->nnz > static_cast<uint64_t>(std::numeric_limits<int32_t>::max())) {
+        return ACL_SPARSE_STATUS_NOT_SUPPORTED;
+    }
     return ValidateVectorSizes(op, A, x, y);
 }
 

@@ -26,9 +26,8 @@
 //    position) pairs); each SpMV streams the products a_k*x_row(k) in CSR
 //    order and then sums every column's products in a fixed order
 //    (deterministic, the reference's CSR_ALG2 semantics,
-//    sparse/spmv/arch35/spmv_kernel.cpp:861-879).  Beyond the sort's int
-//    range the transpose scatters with float/int64 atomics (reference ALG1:
-//    sparse/spmv/arch35/spmv_kernel.cpp:579-668).
+//    sparse/spmv/arch35/spmv_kernel.cpp:861-879).  Transposes beyond the
+//    sort's int range (nnz > INT32_MAX) are rejected by the host.
 //  * Block ids are remapped so that each of the 8 XCDs processes one
 //    contiguous eighth of the matrix (x neighbourhoods stay in one L2).
 #include <hip/hip_runtime.h>
@@ -1759,8 +1758,8 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlock
 
 // ------------------------------- transpose ----------------------------------
 
-// y = beta*y in place (y is not read when beta == 0); the scatter then adds
-// alpha*A^T*x on top.  Used when y's type is the accumulator type.
+// Transpose of a matrix without non-zeros: y = beta*y in place (y is not
+// read when beta == 0).  Used when y's type is the accumulator type.
 template <OutKind O, AccKind A>
 __global__ __launch_bounds__(kThreads) void ScaleKernel(typename OutOf<O>::T* y, int64_t n, int64_t stride,
                                                          Scalars s)
@@ -1784,8 +1783,9 @@ __global__ __launch_bounds__(kThreads) void ClearKernel(typename AccOf<A>::T* ac
     }
 }
 
-// y = finalize(acc): float accumulators already hold alpha*A^T*x; the int64
-// accumulator holds the unscaled sum (sparse/spmv/arch35/spmv_kernel.cpp:626-668).
+// y = finalize(acc) with acc cleared (transpose without non-zeros, y not of
+// the accumulator type): the reference's epilogue of a zero sum
+// (sparse/spmv/arch35/spmv_kernel.cpp:626-668).
 template <OutKind O, AccKind A>
 __global__ __launch_bounds__(kThreads) void FinalizeKernel(const typename AccOf<A>::T* acc,
                                                             typename OutOf<O>::T* y, int64_t n, int64_t stride,
@@ -1805,60 +1805,11 @@ __global__ __launch_bounds__(kThreads) void FinalizeKernel(const typename AccOf<
     }
 }
 
-__device__ __forceinline__ void AtomicAddAcc(float* dst, float v) { unsafeAtomicAdd(dst, v); }
-__device__ __forceinline__ void AtomicAddAcc(long long* dst, long long v)
-{
-    atomicAdd(reinterpret_cast<unsigned long long*>(dst), static_cast<unsigned long long>(v));
-}
-__device__ __forceinline__ void AtomicAddAcc(C64* dst, C64 v)
-{
-    unsafeAtomicAdd(&dst->re, v.re);
-    unsafeAtomicAdd(&dst->im, v.im);
-}
-
 template <ValKind V, AccKind A>
 __device__ __forceinline__ typename AccOf<A>::T MaybeConj(typename AccOf<A>::T v, int conj)
 {
     if constexpr (A == AccKind::C64) return conj ? C64{v.re, -v.im} : v;
     else return v;
-}
-
-// Scatter of one row block: every non-zero (i, j) adds alpha*conj?(a_ij)*x_i
-// (float/complex) or a_ij*x_i (int64) to out[j*stride].
-template <typename RowT, ValKind V, AccKind A>
-__global__ __launch_bounds__(kThreads) void SpmvScatterKernel(RowBlockParams p)
-{
-    using Acc = typename AccOf<A>::T;
-    using ValT = typename ValOf<V>::T;
-    __shared__ int32_t sRp[kMaxRows + 1];
-    const int64_t b = XcdBlock();
-    if (b >= p.num_blocks) return;
-    int64_t r0, k0;
-    const int nr = LoadBlockRows<RowT>(p, b, sRp, r0, k0);
-    Acc alpha, beta;
-    LoadScalars<A>(p.s, alpha, beta);
-    const ValT* val = static_cast<const ValT*>(p.val);
-    const ValT* x = static_cast<const ValT*>(p.x);
-    Acc* out = static_cast<Acc*>(p.y);
-    __syncthreads();
-    const int32_t kspan = sRp[nr];
-    for (int32_t r = threadIdx.x; r < kspan; r += kThreads) {
-        // Row of relative non-zero r: last i with sRp[i] <= r.
-        int lo = 0, hi = nr;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (sRp[mid] <= r) lo = mid;
-            else hi = mid - 1;
-        }
-        const int64_t row = r0 + lo;
-        const int64_t g = k0 + r;
-        const int64_t c = static_cast<int64_t>(p.col[g * p.col_stride]) - p.base;
-        if (c < 0 || c >= p.cols) continue;
-        const Acc a = MaybeConj<V, A>(ToAcc<V, A>(val[g * p.val_stride]), p.conj);
-        Acc contrib = a * ToAcc<V, A>(x[row * p.x_stride]);
-        if constexpr (A != AccKind::I64) contrib = alpha * contrib;
-        AtomicAddAcc(out + c * p.y_stride, contrib);
-    }
 }
 
 // ------------------------- transpose by columns ------------------------------
@@ -2428,22 +2379,15 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         hipLaunchKernelGGL((SpmvCscGatherKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, q);
         return 0;
     }
-    // y already has the accumulator type: scale it by beta and scatter into it.
+    // No non-zeros (the CSC path covers 0 < nnz <= INT32_MAX; larger
+    // transposes are rejected by the host): y = beta*y.
     constexpr bool kDirect = (O == OutKind::F32 && A == AccKind::F32) || (O == OutKind::C64 && A == AccKind::C64);
-    Acc* acc = At<Acc>(l.ws, l.layout.acc_offset);
     if constexpr (kDirect) {
         hipLaunchKernelGGL((ScaleKernel<O, A>), dim3(GridFor(n)), dim3(kThreads), 0, stream,
                            static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, p.s);
     } else {
+        Acc* acc = At<Acc>(l.ws, l.layout.acc_offset);
         hipLaunchKernelGGL((ClearKernel<A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc, n);
-        p.y = acc;
-        p.y_stride = 1;
-    }
-    if (l.rows > 0 && l.nnz > 0) {
-        hipLaunchKernelGGL((SpmvScatterKernel<RowT, V, A>), dim3(RowBlockGrid(p.num_blocks)), dim3(kThreads), 0,
-                           stream, p);
-    }
-    if constexpr (!kDirect) {
         hipLaunchKernelGGL((FinalizeKernel<O, A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc,
                            static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, p.s);
     }

@@ -116,8 +116,10 @@ _pi64 = ctypes.POINTER(ctypes.c_int64)
 _i32 = ctypes.c_int32
 _sz = ctypes.c_size_t
 
-# name -> argtypes; every function returns aclsparseStatus_t (int)
+# name -> argtypes; every function returns aclsparseStatus_t (int) unless RESTYPES says otherwise
+RESTYPES = {"aclsparseHipBuildId": ctypes.c_char_p}
 SIGNATURES = {
+    "aclsparseHipBuildId": [],
     "aclsparseCreate": [_pvp],
     "aclsparseDestroy": [_vp],
     "aclsparseSetStream": [_vp, _vp],
@@ -178,8 +180,17 @@ SIGNATURES = {
 _LIB = None
 
 
+def library_build_id(handle):
+    """The build id compiled into a loaded library (aclsparseHipBuildId)."""
+    fn = handle.aclsparseHipBuildId
+    fn.argtypes = []
+    fn.restype = ctypes.c_char_p
+    return fn().decode()
+
+
 def lib():
-    """Loads the HIP library once; raises if it has not been built."""
+    """Loads the HIP library once; raises if it has not been built or was built
+    from sources other than the ones in this tree."""
     global _LIB
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
@@ -187,10 +198,17 @@ def lib():
                 f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
                 "(there is no CPU fallback for the SpMV path)")
         handle = ctypes.CDLL(LIB_PATH)
+        from .build import CSRC, source_hash
+
+        if os.path.isdir(CSRC) and "ACLSPARSE_HIP_LIB" not in os.environ:
+            want, got = source_hash(), library_build_id(handle)
+            if want != got:
+                raise RuntimeError(f"{LIB_PATH} is stale: built from sources {got}, the tree holds {want}; "
+                                   "rebuild it with `python -c 'import __graft_entry__ as g; g.build()'`")
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         _LIB = handle
     return _LIB
 

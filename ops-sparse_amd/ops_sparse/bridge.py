@@ -23,6 +23,9 @@ from .spmv import CsrSpMV, _validate_npu_args, mv as _mv
 
 _LIBS = None
 
+# value dtypes SpmvMv accepts for mat and vec (int8 gives an int32 result)
+_MV_DTYPES = (torch.int8, torch.float16, torch.bfloat16, torch.float32, torch.complex64)
+
 
 def _spmv(mat, vec):
     """SpmvMv: device, layout and shape checks with the bridge's messages, then ``mv``."""
@@ -37,10 +40,27 @@ def _spmv(mat, vec):
     if mat.size(1) != vec.numel():
         raise RuntimeError(f"SpMV matrix columns must equal vector length, got {mat.size(1)} columns and "
                            f"{vec.numel()} elements")
+    if mat.dtype not in _MV_DTYPES or vec.dtype not in _MV_DTYPES:
+        # ToAclDataType (torch_npu/spmv_npu.cpp:286-297): anything else is rejected
+        raise RuntimeError(f"unsupported A5 SpMV tensor dtype: mat {mat.dtype}, vec {vec.dtype} (supported: "
+                           "int8, float16, bfloat16, float32, complex64)")
     try:
         return _mv(mat, vec)
-    except ValueError as e:
+    except (ValueError, TypeError) as e:
         raise RuntimeError(str(e)) from None
+
+
+def _check_int32_scalars(alpha, beta):
+    """MakeScalars for INT32 compute (torch_npu/spmv_npu.cpp:113-124): integral scalars
+    (a Python int; a float such as 2.0 is not integral) that fit int32."""
+    import numbers
+
+    for v in (alpha, beta):
+        if isinstance(v, bool) or not isinstance(v, numbers.Integral):
+            raise RuntimeError("INT32 SpMV alpha/beta must be integral scalars")
+    for v in (alpha, beta):
+        if not -2**31 <= int(v) <= 2**31 - 1:
+            raise RuntimeError("INT32 SpMV alpha/beta must fit int32")
 
 
 def _spmv_npu(row_ptr, col_ind, values, x, y, alpha, beta, trans, base):
@@ -55,8 +75,13 @@ def _spmv_npu(row_ptr, col_ind, values, x, y, alpha, beta, trans, base):
         rows, cols, _ = _validate_npu_args(row_ptr, col_ind, values, x, y, trans, base)
     except ValueError as e:
         raise RuntimeError(str(e)) from None
+    if y.dtype == torch.int32:
+        _check_int32_scalars(alpha, beta)
     op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[trans]
-    plan = CsrSpMV(rows, cols, row_ptr, col_ind, values, x, y, alpha, beta, op=op, base=base)
+    try:
+        plan = CsrSpMV(rows, cols, row_ptr, col_ind, values, x, y, alpha, beta, op=op, base=base)
+    except ValueError as e:  # real compute with a complex scalar
+        raise RuntimeError(str(e)) from None
     plan.preprocess()
     plan.run()
     return y

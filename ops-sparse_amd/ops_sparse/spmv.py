@@ -69,14 +69,27 @@ def _ptr(t):
 
 
 class HostScalar:
-    """alpha/beta in the compute type, kept alive for the duration of a call."""
+    """alpha/beta in the compute type, kept alive for the duration of a call.
+
+    Conversions follow the torch extension's HostScalar
+    (sparse/spmv/torch_extension/csrc/spmv.cpp:162-190): INT32 compute rejects
+    a non-zero imaginary part and values outside the int32 range and truncates
+    the real part; real compute rejects a non-zero imaginary part; complex
+    compute keeps both parts.  Violations raise ValueError.
+    """
 
     def __init__(self, value, compute_type):
         value = complex(value)
-        if compute_type == DataType.INT32:
-            self._obj = ctypes.c_int32(int(value.real))
-        elif compute_type == DataType.COMPLEX64:
+        if compute_type == DataType.COMPLEX64:
             self._obj = _lib.Complex(value.real, value.imag)
+            return
+        if value.imag != 0.0:
+            kind = "int32 SpMV" if compute_type == DataType.INT32 else "real SpMV compute type"
+            raise ValueError(f"{kind} cannot use a complex scalar, but got imaginary part {value.imag}")
+        if compute_type == DataType.INT32:
+            if not -2.0**31 <= value.real <= float(_INT32_MAX):
+                raise ValueError(f"int32 SpMV scalar {value.real} is out of the int32 range")
+            self._obj = ctypes.c_int32(int(value.real))
         else:
             self._obj = ctypes.c_float(value.real)
 

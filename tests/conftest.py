@@ -23,10 +23,12 @@ def dev():
 
 
 def pytest_sessionstart(session):
-    """Builds the HIP library once if nothing is built yet (hipcc cross-compiles without a GPU)."""
+    """Builds the HIP library if it is missing or was built from other sources (hipcc
+    cross-compiles without a GPU); the loader refuses a stale library."""
     from ops_sparse import _lib
+    from ops_sparse.build import build_library, file_build_id, source_hash
 
-    if not os.path.exists(_lib.LIB_PATH):
-        from ops_sparse.build import build_library
-
+    # read from the file, not dlopen'ed: a library loaded once stays mapped
+    # under its path for the life of the process
+    if file_build_id(_lib.LIB_PATH) != source_hash():
         build_library()

@@ -21,7 +21,7 @@ F32 = int(DataType.FLOAT)
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*aclsparseStatus_t\s+(aclsparse\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:aclsparseStatus_t|const char\*)\s+(aclsparse\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -254,6 +254,22 @@ def test_spmv_accepts_i64_row_offsets(env):
     assert env.size(N, env.csr(ptr_type=IndexType.I64), x, y)[0] == Status.SUCCESS
 
 
+def test_spmv_transpose_beyond_int32_nnz_not_supported(env):
+    """Transposes sum each column in CSR order through a CSC pattern limited to
+    INT32_MAX entries (the reference's own nnz bound, sparse/spmv/README.md
+    arch35 constraints); with 64-bit row offsets a larger matrix is still
+    accepted for op = N but rejected, for every algorithm, for T and H."""
+    big = (1 << 31) + 5
+    A = env.csr(rows=1 << 20, cols=1 << 20, nnz=big, ptr_type=IndexType.I64, ptrs=False)
+    xn, yn = env.vec(1 << 20, 0), env.vec(1 << 20, 0)
+    assert env.size(N, A, xn, yn)[0] == Status.SUCCESS
+    for op in (T, H):
+        for alg in (SpMVAlg.DEFAULT, SpMVAlg.CSR_ALG1, SpMVAlg.CSR_ALG2):
+            assert env.size(op, A, xn, yn, alg=int(alg))[0] == Status.NOT_SUPPORTED
+    edge = env.csr(rows=1 << 20, cols=1 << 20, nnz=(1 << 31) - 1, ptr_type=IndexType.I64, ptrs=False)
+    assert env.size(T, edge, xn, yn, alg=int(SpMVAlg.CSR_ALG2))[0] == Status.SUCCESS
+
+
 def test_spmv_rejects_wrong_vector_sizes(env):
     A = env.csr()
     assert env.size(N, A, env.vec(2, env.xv), env.vec(2, env.yv))[0] == Status.INVALID_VALUE
@@ -472,3 +488,68 @@ def test_bridge_operators_defined_without_cpu_fallback():
     empty_i, empty_f = torch.empty(0, dtype=torch.int32), torch.empty(0, dtype=torch.float32)
     with pytest.raises(RuntimeError):
         torch.ops.ops_sparse_test.spmv_npu(row_ptr, empty_i, empty_f, empty_f, empty_f, 1.0, 0.0, "N", 0)
+
+
+def test_library_build_id_matches_the_sources(lib):
+    """The loaded library was compiled from this tree's sources and flags."""
+    from ops_sparse.build import file_build_id, source_hash
+
+    assert _lib.library_build_id(lib) == source_hash() == file_build_id(_lib.LIB_PATH)
+
+
+def test_stale_library_is_refused(tmp_path):
+    """A library whose build id differs from the tree's is refused by the loader
+    (checked in a fresh process on a copy with one byte of its id changed)."""
+    import shutil
+    import subprocess
+    import sys
+
+    from ops_sparse.build import BUILD_ID_PREFIX
+
+    data = bytearray(open(_lib.LIB_PATH, "rb").read())
+    i = data.find(BUILD_ID_PREFIX) + len(BUILD_ID_PREFIX)
+    data[i] = ord("0") if data[i] != ord("0") else ord("1")
+    stale = tmp_path / "lib" / "libaclsparse_hip.so"
+    stale.parent.mkdir()
+    stale.write_bytes(bytes(data))
+    code = ("import sys; sys.path.insert(0, sys.argv[1]); from ops_sparse import _lib; "
+            "_lib.LIB_PATH = sys.argv[2]\n"
+            "try:\n    _lib.lib()\nexcept RuntimeError as e:\n    print('refused' if 'stale' in str(e) else e)\n"
+            "else:\n    print('loaded')")
+    pkg = os.path.dirname(os.path.dirname(_lib.__file__))
+    out = subprocess.run([sys.executable, "-c", code, pkg, str(stale)], capture_output=True, text=True, timeout=120)
+    assert out.stdout.strip().splitlines()[-1] == "refused", out.stdout + out.stderr
+
+
+def test_host_scalars_follow_the_extension_conversions():
+    """HostScalar mirrors the torch extension's (sparse/spmv/torch_extension/csrc/spmv.cpp:162-190)."""
+    from ops_sparse.spmv import HostScalar
+
+    def i32(v):
+        return ctypes.cast(HostScalar(v, DataType.INT32).ptr, ctypes.POINTER(ctypes.c_int32)).contents.value
+
+    assert i32(-7) == -7 and i32(2**31 - 1) == 2**31 - 1 and i32(-2**31) == -2**31
+    assert i32(2.9) == 2 and i32(-2.9) == -2  # static_cast<int32_t> truncates
+    for bad, msg in ((2**31, "out of the int32 range"), (-2**31 - 1, "out of the int32 range"),
+                     (complex(1, 1), "imaginary part")):
+        with pytest.raises(ValueError, match=msg):
+            HostScalar(bad, DataType.INT32)
+    assert ctypes.cast(HostScalar(1.5, DataType.FLOAT).ptr, ctypes.POINTER(ctypes.c_float)).contents.value == 1.5
+    assert ctypes.cast(HostScalar(complex(1.5, 0), DataType.FLOAT).ptr,
+                       ctypes.POINTER(ctypes.c_float)).contents.value == 1.5
+    with pytest.raises(ValueError, match="real SpMV compute type cannot use a complex scalar"):
+        HostScalar(complex(1, 2), DataType.FLOAT)
+    c = ctypes.cast(HostScalar(complex(1, 2), DataType.COMPLEX64).ptr, ctypes.POINTER(_lib.Complex)).contents
+    assert (c.x, c.y) == (1.0, 2.0)
+
+
+def test_bridge_int32_scalar_checks():
+    """The bridge's MakeScalars (torch_npu/spmv_npu.cpp:113-124) wants integral int32 scalars."""
+    from ops_sparse.bridge import _check_int32_scalars
+
+    _check_int32_scalars(2, -3)
+    _check_int32_scalars(np.int64(5), 2**31 - 1)
+    for a, b, msg in ((2.5, 1, "integral"), (2, 1.0, "integral"), (True, 0, "integral"), (2**31, 0, "fit int32"),
+                      (0, -2**31 - 1, "fit int32")):
+        with pytest.raises(RuntimeError, match=msg):
+            _check_int32_scalars(a, b)

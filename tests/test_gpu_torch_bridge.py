@@ -84,3 +84,41 @@ def test_hook_rejects_int64_indices(dev):
     y = torch.zeros(2, device=dev)
     with pytest.raises(RuntimeError, match="int32"):
         torch.ops.ops_sparse_test.spmv_npu(row_ptr.long(), col_ind, values, x, y, 1.0, 0.0, "N", 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.int64, torch.complex128])
+@pytest.mark.parametrize("entry", ["mv", "spmv"])
+def test_unsupported_dtypes_raise_runtime_error(dtype, entry, dev):
+    """ToAclDataType (torch_npu/spmv_npu.cpp:286-297) rejects every other dtype; importing the
+    package replaces PyTorch's CSR mv, so such a call raises instead of computing."""
+    matrix, _, _, _ = _csr(dtype, dev)
+    vector = torch.tensor([1, 2, 3], dtype=dtype, device=dev)
+    fn = torch.mv if entry == "mv" else torch.ops.ops_sparse.spmv
+    with pytest.raises(RuntimeError, match="unsupported A5 SpMV tensor dtype"):
+        fn(matrix, vector)
+
+
+def test_hook_rejects_non_integral_and_out_of_range_int32_scalars(dev):
+    """MakeScalars (torch_npu/spmv_npu.cpp:108-124): INT32 SpMV takes integral scalars that fit int32."""
+    _, row_ptr, col_ind, _ = _csr(torch.float32, dev)
+    values = torch.tensor([2, 3, 4], dtype=torch.int8, device=dev)
+    x = torch.tensor([1, 2, 3], dtype=torch.int8, device=dev)
+    y = torch.tensor([5, 6], dtype=torch.int32, device=dev)
+    hook = torch.ops.ops_sparse_test.spmv_npu
+    with pytest.raises(RuntimeError, match="must be integral scalars"):
+        hook(row_ptr, col_ind, values, x, y, 2.5, 1, "N", 0)
+    with pytest.raises(RuntimeError, match="must be integral scalars"):
+        hook(row_ptr, col_ind, values, x, y, 2, 1.0, "N", 0)
+    with pytest.raises(RuntimeError, match="must fit int32"):
+        hook(row_ptr, col_ind, values, x, y, 2**31, 1, "N", 0)
+    torch.testing.assert_close(y.cpu(), torch.tensor([5, 6], dtype=torch.int32))  # untouched
+    hook(row_ptr, col_ind, values, x, y, 2, 3, "N", 0)
+    torch.testing.assert_close(y.cpu(), torch.tensor([2 * 11 + 15, 2 * 8 + 18], dtype=torch.int32))
+
+
+def test_hook_rejects_complex_scalars_for_real_compute(dev):
+    _, row_ptr, col_ind, values = _csr(torch.float32, dev)
+    x = torch.tensor([1.0, 2.0, 3.0], device=dev)
+    y = torch.tensor([5.0, 6.0], device=dev)
+    with pytest.raises(RuntimeError, match="real SpMV compute type cannot use a complex scalar"):
+        torch.ops.ops_sparse_test.spmv_npu(row_ptr, col_ind, values, x, y, complex(2, 1), 3.0, "N", 0)
