@@ -7,9 +7,12 @@ itself is timed with HIP events recorded on the stream it runs on.  c1
 (1.4 MB, launch-bound) is also timed as 1000 back-to-back SpMVs replayed
 from one HIP graph.
 
-The headline workload is configs[1] of BASELINE.json: the 5-point Laplacian on
-a 2048^2 grid (fp32).  The other configurations are measured in the same run
-(``configs`` field) unless ``--only-headline`` is given.
+The headline workload is the largest configuration of BASELINE.json
+(configs[3], c4): 16,777,216 x 16,777,216 with 32 uniform columns per row
+(536,870,912 non-zeros), fp16 values and x, fp32 compute, fp16 output, int64
+row offsets.  The other configurations (c1, c2, c3, c4 in bf16, c5, and the
+headline-matrix variants of c2) are measured in the same run (``configs``
+field) unless ``--only-headline`` is given.
 
 Prints ONE JSON line.
 """
@@ -27,6 +30,7 @@ sys.path.insert(0, os.path.join(REPO, "ops-sparse_amd"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+HEADLINE = "c4h"  # BASELINE.json configs[3] in fp16: the largest configuration
 METRIC = "CSR SpMV GFLOP/s + effective HBM GB/s (% of MI355X peak) on one GPU"
 FLUSH_BYTES = 512 << 20
 
@@ -344,7 +348,10 @@ def measure_spmm(case, steps, warmup, flush_buf):
 
 
 def cpu_baseline(w, seconds):
-    """Single-threaded oracle SpMV (the reference host golden restated in C) on a bounded sample."""
+    """Single-threaded oracle SpMV (the reference host golden restated in C) on a bounded sample:
+    whole SpMVs of the headline matrix, repeated for about ``seconds``.  fp32 workloads use
+    oracle_spmv_f64 (SpmvCpu<float>: fp64 accumulation), fp16/bf16 ones oracle_spmv_lowp
+    (SpmvCpu<float, half|bf16>: fp32 accumulation, one rounding to the output type)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import numpy as np
     import oracle
@@ -352,11 +359,23 @@ def cpu_baseline(w, seconds):
 
     host = w.to("cpu")
     rp = host.row_ptr.numpy().astype(np.int64)
-    args = (rp, host.col_ind.numpy(), host.values.numpy(), host.x.numpy(), host.y0.numpy())
-    oracle.spmv_f64(*args, w.alpha, w.beta)  # warm the caches / page in
+    lowp = w.values.dtype in (torch.float16, torch.bfloat16)
+    if lowp:
+        kind = oracle.K_F16 if w.values.dtype == torch.float16 else oracle.K_BF16
+        bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        args = (rp, host.col_ind.numpy(), bits(host.values), bits(host.x), bits(host.y0.to(w.out_dtype)))
+        serial = lambda: oracle.spmv_lowp(*args, kind, kind, w.alpha, w.beta)  # noqa: E731
+        par = lambda t: oracle.spmv_lowp_threads(*args, kind, kind, w.alpha, w.beta, t)  # noqa: E731
+        fn_name = "oracle_spmv_lowp (fp32 accumulation, one RNE rounding)"
+    else:
+        args = (rp, host.col_ind.numpy(), host.values.numpy(), host.x.numpy(), host.y0.numpy())
+        serial = lambda: oracle.spmv_f64(*args, w.alpha, w.beta)  # noqa: E731
+        par = lambda t: oracle.spmv_f64_threads(*args, w.alpha, w.beta, t)  # noqa: E731
+        fn_name = "oracle_spmv_f64 (fp64 accumulation)"
+    serial()  # page the arrays in
     n, t0 = 0, time.perf_counter()
     while True:
-        oracle.spmv_f64(*args, w.alpha, w.beta)
+        serial()
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -367,7 +386,7 @@ def cpu_baseline(w, seconds):
     threads = min(len(os.sched_getaffinity(0)), 16)
     m, t0 = 0, time.perf_counter()
     while True:
-        oracle.spmv_f64_threads(*args, w.alpha, w.beta, threads)
+        par(threads)
         m += 1
         el2 = time.perf_counter() - t0
         if el2 >= seconds / 2:
@@ -379,8 +398,8 @@ def cpu_baseline(w, seconds):
     return {"value": algorithmic_bytes(w) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "parallel": parallel,
             "ms_per_spmv": per * 1e3, "gflops": 2 * w.nnz / per / 1e9,
-            "sample": f"{n} full SpMVs of the headline matrix ({w.rows} rows, {w.nnz} nnz) in {el:.1f} s, "
-                      f"oracle/spmv_oracle.c oracle_spmv_f64 (fp64 accumulation), 1 thread",
+            "sample": f"{n} full SpMVs of the headline matrix {w.name} ({w.rows} rows, {w.nnz} nnz) in {el:.1f} s, "
+                      f"oracle/spmv_oracle.c {fn_name}, 1 thread",
             "cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
 
 
@@ -406,9 +425,12 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
-    names = ["c2"] if args.only_headline else [n.strip() for n in args.configs.split(",") if n.strip()]
-    # c2 first: the first SpMV of the process also pays for loading the code objects
-    names = ["c2"] + [n for n in names if n != "c2"]
+    names = [HEADLINE] if args.only_headline else [n.strip() for n in args.configs.split(",") if n.strip()]
+    if HEADLINE not in names:
+        names.append(HEADLINE)
+    # c2 first when measured: the first SpMV of the process also pays for
+    # loading the code objects (and c2's variants reuse its matrix)
+    names = [n for n in names if n == "c2"] + [n for n in names if n != "c2"]
     results, headline_w, headline = {}, None, None
     for name in names:
         w = make(name, dev)
@@ -425,8 +447,10 @@ def main():
             r["graph_gbs"] = nbytes / (r["graph_ms"] * 1e-3) / 1e9
         print(f"# {name}: {json.dumps(r)}", file=sys.stderr, flush=True)
         results[name] = r
-        if name == "c2":
+        if name == HEADLINE:
             headline_w, headline = w, r
+            cpu = None if args.no_cpu_baseline else cpu_baseline(headline_w, args.cpu_seconds)
+        if name == "c2":
             if not args.only_headline:
                 for key, v in dtype_variants(w).items():
                     mv = measure(v, args.steps, args.warmup, flush_buf)
@@ -449,10 +473,8 @@ def main():
             for key, case in spmm_cases(dev, w):
                 results[key] = measure_spmm(case, args.steps, args.warmup, flush_buf)
                 print(f"# {key}: {json.dumps(results[key])}", file=sys.stderr, flush=True)
-        else:
-            del w
-            torch.cuda.empty_cache()
-    cpu = None if args.no_cpu_baseline else cpu_baseline(headline_w, args.cpu_seconds)
+        del w
+        torch.cuda.empty_cache()
     h = headline
     out = {
         "metric": METRIC,
@@ -466,13 +488,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic (seeded 5-point Laplacian, x/y ~ U(-1,1))",
-        "config": {"workload": h["workload"], "rows": h["rows"], "nnz": h["nnz"], "alpha": 1.5, "beta": 0.5,
-                   "index": "int32", "op": "N", "l2_mall_flushed": True, "parallelism": "single GPU"},
+        "dtype": "fp16",
+        "compute_dtype": "fp32",
+        "data": "synthetic (seeded: 32 uniform sorted columns per row, values N(0,1), x U(-1,1), fp16)",
+        "config": {"workload": h["workload"], "rows": h["rows"], "nnz": h["nnz"], "alpha": 1.0, "beta": 0.0,
+                   "row_offsets": "int64", "col_ind": "int32", "values_x_y": "fp16", "op": "N",
+                   "l2_mall_flushed": True, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(h["frac"], 4), "traffic": load_traffic("c2"),
-                     "kernel": "SpmvStreamFlatKernel", "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
+                     "frac": round(h["frac"], 4), "traffic": load_traffic(HEADLINE),
+                     "kernel": h.get("kernel"), "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},

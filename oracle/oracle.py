@@ -144,6 +144,22 @@ def spmv_lowp(row_ptr, col, val_bits, x_bits, y_bits, kind, y_kind, alpha, beta,
     return z
 
 
+def spmv_lowp_threads(row_ptr, col, val_bits, x_bits, y_bits, kind, y_kind, alpha, beta, threads):
+    """spmv_lowp (non-transpose) over ``threads`` POSIX threads by row ranges: bit-identical results."""
+    rp = _i64(row_ptr)
+    rows = rp.size - 1
+    vdt = np.float32 if kind == K_F32 else np.uint16
+    ydt = np.float32 if y_kind == K_F32 else np.uint16
+    z = np.empty(rows, dtype=ydt)
+    rc = lib().oracle_spmv_lowp_threads(_I(rows), _p(rp), _p(_c(col, np.int32)), _p(_c(val_bits, vdt)),
+                                        _p(_c(x_bits, vdt)), _p(_c(y_bits, ydt)), ctypes.c_int(kind),
+                                        ctypes.c_int(y_kind), ctypes.c_float(alpha), ctypes.c_float(beta), _p(z),
+                                        ctypes.c_int(threads))
+    if rc != 0:
+        raise RuntimeError("pthread_create failed")
+    return z
+
+
 def row_scale(row_ptr, col, val, x, y, kind, y_kind, alpha, beta, transpose=False, cols=None):
     """|alpha|*sum|a_ij x_j| + |beta y_i| for every output element (float64)."""
     rp = _i64(row_ptr)

@@ -241,6 +241,52 @@ void oracle_spmv_lowp(int64_t rows, const int64_t *rp, const int32_t *col, const
     }
 }
 
+/* oracle_spmv_lowp split over nthreads POSIX threads by row ranges (this
+ * build's parallel restatement for the labelled CPU baseline; every row is
+ * summed in the serial loop's order, so the results are bit-identical). */
+struct oracle_lowp_arg {
+    int64_t r0, r1;
+    const int64_t *rp;
+    const int32_t *col;
+    const void *val, *x, *y;
+    int kind, yKind;
+    float alpha, beta;
+    void *z;
+};
+
+static void *oracle_lowp_run(void *p)
+{
+    const struct oracle_lowp_arg *a = (const struct oracle_lowp_arg *)p;
+    for (int64_t i = a->r0; i < a->r1; ++i) {
+        float sum = 0.0f;
+        for (int64_t q = a->rp[i]; q < a->rp[i + 1]; ++q) {
+            sum += load_lowp(a->val, q, a->kind) * load_lowp(a->x, a->col[q], a->kind);
+        }
+        store_lowp(a->z, i, a->alpha * sum + a->beta * load_lowp(a->y, i, a->yKind), a->yKind);
+    }
+    return NULL;
+}
+
+int oracle_spmv_lowp_threads(int64_t rows, const int64_t *rp, const int32_t *col, const void *val, const void *x,
+                             const void *y, int kind, int yKind, float alpha, float beta, void *z, int nthreads)
+{
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    struct oracle_lowp_arg args[256];
+    for (int t = 0; t < nthreads; ++t) {
+        struct oracle_lowp_arg a = {rows * t / nthreads, rows * (t + 1) / nthreads, rp, col, val, x, y,
+                                    kind, yKind, alpha, beta, z};
+        args[t] = a;
+        if (pthread_create(&th[t], NULL, oracle_lowp_run, &args[t]) != 0) {
+            for (int u = 0; u < t; ++u) pthread_join(th[u], NULL);
+            return -1;
+        }
+    }
+    for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+    return 0;
+}
+
 void oracle_spmv_trans_lowp(int64_t rows, int64_t cols, const int64_t *rp, const int32_t *col, const void *val,
                             const void *x, const void *y, int kind, int yKind, float alpha, float beta, float *acc,
                             void *z)

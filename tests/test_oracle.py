@@ -430,3 +430,11 @@ def test_threaded_spmv_matches_serial_bit_for_bit():
     a = oracle.spmv_f64(rp, col, val, x, y, 1.5, -0.5)
     for t in (1, 3, 8):
         assert np.array_equal(oracle.spmv_f64_threads(rp, col, val, x, y, 1.5, -0.5, t), a)
+    # fp16 / bf16 values and x, fp32 compute, 16-bit outputs
+    for kind in (oracle.K_F16, oracle.K_BF16):
+        vb = (oracle.half_from_float(val) if kind == oracle.K_F16 else oracle.bf16_from_float(val))
+        xb = (oracle.half_from_float(x) if kind == oracle.K_F16 else oracle.bf16_from_float(x))
+        yb = (oracle.half_from_float(y) if kind == oracle.K_F16 else oracle.bf16_from_float(y))
+        s = oracle.spmv_lowp(rp, col, vb, xb, yb, kind, kind, 1.5, -0.5)
+        for t in (1, 3, 8):
+            assert np.array_equal(oracle.spmv_lowp_threads(rp, col, vb, xb, yb, kind, kind, 1.5, -0.5, t), s)
