@@ -59,6 +59,7 @@ struct SpmvPlan {
     int32_t alg = -1;
     aclrtStream stream = nullptr;
     uint64_t stream_epoch = 0;
+    bool staged = false;  // Preprocess built the staged-gather tables in the buffer
 };
 
 struct aclsparseSpMatDescr {
@@ -145,7 +146,15 @@ struct SpmvWsHeader {
     uint64_t task_start_offset;  // 0 when the plan has no task table
     uint64_t task_block_offset;
     uint64_t max_tasks;
-    uint32_t reserved[16];
+    // staged gather (0 when the plan has none): the path Preprocess chose
+    // (1 = staged kernels, 0 = row kernels), the bucket and tile counts and
+    // where the tile corners are
+    uint32_t staged_flag;
+    uint32_t staged_buckets;
+    uint64_t staged_tiles;
+    uint64_t staged_tile_row_offset;
+    uint64_t staged_tile_nnz_offset;
+    uint32_t reserved[8];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 
@@ -209,6 +218,33 @@ struct SpmvLayout {
     int64_t max_tasks = 0;
     size_t task_start_offset = 0, task_block_offset = 0, task_head_offset = 0, task_tail_offset = 0;
     size_t task_cnt_offset = 0, task_scan_offset = 0, task_scan_bytes = 0;
+    // Staged gather (non-transpose, fp32 compute, fp32/fp16/bf16 values; see
+    // StageEligible): Preprocess cuts the matrix into merge-path tiles of
+    // kStageTileItems rows+entries and buckets every entry by the x segment
+    // of its column (kStageSegmentBytes of x per bucket; bucket S holds
+    // entries whose column is outside [0, cols)).  Sections:
+    //   st_tile_row int32[T+1], st_tile_nnz int64[T+1]   merge-path tile corners
+    //   st_counts / st_start_bm uint32[(S+1)*(T+1)]       per (bucket, tile)
+    //                                                     entry counts and
+    //                                                     their exclusive scan
+    //   st_start uint32[(T+1)*(S+1)]                      the scan tile-major:
+    //                                                     first slot of tile t's
+    //                                                     run in bucket s
+    //   st_scan                                           scan temporary storage
+    //   st_perm uint16[nnz+8]   slot of each entry (CSR order) in its tile's
+    //                           bucket-ordered runs
+    //   st_cl uint16[nnz+8]     bucket order: column within the bucket
+    //   st_xg V[nnz+8]          bucket order: the gathered x values (written
+    //                           by every SpMV)
+    //   st_head / st_tail float[T]  partial sums of the rows crossing tile ends
+    //   st_metric uint64            distinct x lines per tile, summed
+    // The header's staged_flag says which path Preprocess chose.
+    bool staged = false;
+    int64_t st_tiles = 0, st_parts = 0, st_part_size = 0;
+    int32_t st_buckets = 0, st_wshift = 0, st_value_bytes = 0;
+    size_t st_tile_row_offset = 0, st_tile_nnz_offset = 0, st_counts_offset = 0, st_start_bm_offset = 0;
+    size_t st_start_offset = 0, st_scan_offset = 0, st_scan_bytes = 0, st_perm_offset = 0, st_cl_offset = 0;
+    size_t st_xg_offset = 0, st_head_offset = 0, st_tail_offset = 0, st_metric_offset = 0;
 };
 
 #ifndef SPMV_LONG_CHUNKS
@@ -218,6 +254,49 @@ constexpr int64_t kLongChunks = SPMV_LONG_CHUNKS;  // blocks with more chunks th
 
 // Exclusive-scan temporary storage of the task table (implemented in spmv_kernels.hip).
 size_t TaskScanTempBytes(int64_t n);
+
+// ---------------------------------------------------------------------------
+// Staged gather.  A matrix whose x does not fit an XCD's L2 and whose columns
+// are scattered makes the row kernels fetch one 128-byte line per 2- or
+// 4-byte x value.  The staged path instead (pass A) loads each x segment into
+// one workgroup's LDS and writes the values its bucket's entries need, in
+// bucket order (sequential reads and writes), then (pass B) each merge-path
+// tile reads its runs of those values into LDS and sums its rows.  It is used
+// for matrices of at least kStageMinNnz entries whose x is at least
+// kStageMinXBytes; Preprocess measures the columns' spread and keeps the row
+// kernels when x accesses are local (banded matrices).
+// ---------------------------------------------------------------------------
+constexpr int64_t kStageTileItems = 8184;  // rows + entries per tile: <= 2047 groups of 4 entries
+constexpr int64_t kStageMinNnz = int64_t{1} << 25;
+constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
+constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS
+constexpr int32_t kStageMaxBuckets = 1024;
+constexpr int64_t kStageMinParts = 512;           // pass A workgroups (two per CU at least)
+constexpr int64_t kStagePartTarget = int64_t{1} << 20;  // entries per pass A workgroup beyond that
+// Staged gather decision: the staged path is chosen when the tiles' distinct
+// x lines exceed this fraction of the entries (the row kernels then fetch
+// about one line per entry).
+constexpr int64_t kStageLinesPerEntryDen = 4;  // lines * 4 > nnz
+
+size_t StageScanTempBytes(int64_t n);  // implemented in spmv_staged_kernels.hip
+
+// Element bytes of x for which the staged path exists (0 = not eligible).
+inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
+{
+    if (computeType != ACL_FLOAT) return 0U;
+    if (valueType == ACL_FLOAT) return 4U;
+    if (valueType == ACL_FLOAT16 || valueType == ACL_BF16) return 2U;
+    return 0U;
+}
+
+inline bool StageEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t valueBytes)
+{
+    if (valueBytes == 0U || rows == 0U) return false;
+    if (nnz < static_cast<uint64_t>(kStageMinNnz) || nnz > 0xF0000000ULL) return false;
+    if (cols * valueBytes < static_cast<uint64_t>(kStageMinXBytes)) return false;
+    const uint64_t w = static_cast<uint64_t>(kStageSegmentBytes) / valueBytes;
+    return (cols + w - 1) / w <= static_cast<uint64_t>(kStageMaxBuckets);
+}
 
 // Radix-sort temporary storage for the CSC build (implemented in spmv_kernels.hip).
 size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes);
@@ -231,7 +310,8 @@ inline size_t AccumulatorBytes(aclDataType computeType)
 }
 
 inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
-                                aclDataType computeType, bool transpose, bool allowTasks = true)
+                                aclDataType computeType, bool transpose, bool allowTasks = true,
+                                uint32_t stageValueBytes = 0)
 {
     SpmvLayout l;
     l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
@@ -290,6 +370,39 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.total = AlignUp(l.row_delta_offset + static_cast<size_t>(l.row_groups) * kRowGroup);
         }
     }
+    if (!transpose && StageEligible(rows, cols, nnz, stageValueBytes)) {
+        l.staged = true;
+        l.st_value_bytes = static_cast<int32_t>(stageValueBytes);
+        const uint64_t w = static_cast<uint64_t>(kStageSegmentBytes) / stageValueBytes;
+        int32_t shift = 0;
+        while ((uint64_t{1} << shift) < w) ++shift;
+        l.st_wshift = shift;
+        l.st_buckets = static_cast<int32_t>((cols + w - 1) / w);
+        const uint64_t t = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+        l.st_tiles = static_cast<int64_t>(t);
+        int64_t parts = static_cast<int64_t>((nnz + kStagePartTarget - 1) / kStagePartTarget);
+        parts = parts < kStageMinParts ? kStageMinParts : parts;
+        int64_t part = static_cast<int64_t>((nnz + parts - 1) / parts);
+        part = (part + 7) & ~int64_t{7};
+        l.st_part_size = part;
+        l.st_parts = static_cast<int64_t>((nnz + part - 1) / part);
+        const size_t cells = static_cast<size_t>(l.st_buckets + 1) * static_cast<size_t>(t + 1);
+        const size_t n8 = static_cast<size_t>(nnz) + 8;
+        l.st_tile_row_offset = AlignUp(l.total);
+        l.st_tile_nnz_offset = AlignUp(l.st_tile_row_offset + static_cast<size_t>(t + 1) * sizeof(int32_t));
+        l.st_counts_offset = AlignUp(l.st_tile_nnz_offset + static_cast<size_t>(t + 1) * sizeof(int64_t));
+        l.st_start_bm_offset = AlignUp(l.st_counts_offset + cells * sizeof(uint32_t));
+        l.st_start_offset = AlignUp(l.st_start_bm_offset + cells * sizeof(uint32_t));
+        l.st_scan_offset = AlignUp(l.st_start_offset + cells * sizeof(uint32_t));
+        l.st_scan_bytes = StageScanTempBytes(static_cast<int64_t>(cells));
+        l.st_perm_offset = AlignUp(l.st_scan_offset + l.st_scan_bytes + 256);  // re-aligned to 256 at use
+        l.st_cl_offset = AlignUp(l.st_perm_offset + n8 * sizeof(uint16_t));
+        l.st_xg_offset = AlignUp(l.st_cl_offset + n8 * sizeof(uint16_t));
+        l.st_head_offset = AlignUp(l.st_xg_offset + n8 * stageValueBytes);
+        l.st_tail_offset = AlignUp(l.st_head_offset + static_cast<size_t>(t) * sizeof(float));
+        l.st_metric_offset = AlignUp(l.st_tail_offset + static_cast<size_t>(t) * sizeof(float));
+        l.total = AlignUp(l.st_metric_offset + sizeof(uint64_t));
+    }
     return l;
 }
 
@@ -331,7 +444,16 @@ struct SpmvLaunch {
     // workspace
     void* ws;
     SpmvLayout layout;
+    // staged gather: Preprocess builds its tables; SpMV launches its kernels
+    // (which check the path flag Preprocess left in the header)
+    int32_t staged;
 };
+
+// Staged gather: tables and path decision (after LaunchSpmvPreprocess) and
+// the three execution kernels (after the row kernel launched with its skip
+// flag).  Implemented in spmv_staged_kernels.hip.
+int LaunchStagedPreprocess(const SpmvLaunch& l, void* stream);
+int LaunchStagedCompute(const SpmvLaunch& l, void* stream);
 
 // Normalises the row offsets and writes the row-block partition and header.
 int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream);

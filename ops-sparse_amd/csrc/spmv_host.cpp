@@ -179,7 +179,20 @@ aclsparseStatus_t ValidateWorkspace(void* buffer)
 
 SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c)
 {
-    return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op));
+    return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op), true,
+                                aclsp::StageValueBytes(m->value_type, c));
+}
+
+bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
+
+// The staged-gather tables are built when the layout has them and the
+// operands are what its kernels (and the row kernel it falls back to) read:
+// bound, unit-stride, 16-byte aligned column indices and values.
+bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
+                 const aclsparseDnVecDescr* y)
+{
+    return l.staged && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
+           x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values);
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
@@ -319,15 +332,19 @@ aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOpe
     if (m->rows > 0U && m->ptrs == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
     st = ValidateWorkspace(externalBuffer);
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    bool staged = false;
     if (m->rows > 0U) {
         (void)hipGetLastError();
-        const aclsp::SpmvLaunch l =
-            MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
+        aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
+        staged = StageUsable(l.layout, m, vecX, vecY);
+        l.staged = staged ? 1 : 0;
         if (aclsp::LaunchSpmvPreprocess(l, HipStreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
+            m->plan = SpmvPlan{};
             return ACL_SPARSE_STATUS_EXECUTION_FAILED;
         }
     }
     m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
+    m->plan.staged = staged;
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
@@ -346,14 +363,18 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
     if (outLen == 0U) return ACL_SPARSE_STATUS_SUCCESS;
 
     auto* m = const_cast<aclsparseSpMatDescr*>(matA);
-    const aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
+    aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
     void* stream = HipStreamOf(handle);
     (void)hipGetLastError();
     // The partition is rebuilt unless a matching Preprocess already wrote it
     // into this very buffer.  A zero-row matrix has no partition to build.
+    // Without a matching plan the row kernels run (the staged tables are
+    // built only by Preprocess).
     const bool planned = m->rows == 0U ||
                          PlanMatches(m->plan, MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle));
     if (!planned && aclsp::LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    // pass A reads x as 16-byte vectors
+    l.staged = planned && m->rows > 0U && m->plan.staged && Aligned16(vecX->values) ? 1 : 0;
     if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }

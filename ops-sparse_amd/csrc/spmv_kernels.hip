@@ -39,9 +39,12 @@
 
 #include "aclsparse_internal.h"
 #include "compensated.h"
+#include "spmv_device.h"
 
 namespace aclsp {
 namespace {
+
+using namespace dev;
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
@@ -61,189 +64,6 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned short v4u16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int Pad(int q) { return q + (q >> 3); }
-
-// ------------------------------ numeric types -------------------------------
-
-struct C64 {
-    float re, im;
-};
-
-__device__ __forceinline__ C64 operator+(C64 a, C64 b) { return {a.re + b.re, a.im + b.im}; }
-__device__ __forceinline__ C64 operator*(C64 a, C64 b) { return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re}; }
-
-template <AccKind A> struct AccOf;
-template <> struct AccOf<AccKind::F32> { using T = float; };
-template <> struct AccOf<AccKind::I64> { using T = long long; };
-template <> struct AccOf<AccKind::C64> { using T = C64; };
-
-template <ValKind V> struct ValOf;
-template <> struct ValOf<ValKind::F32> { using T = float; };
-template <> struct ValOf<ValKind::F16> { using T = uint16_t; };
-template <> struct ValOf<ValKind::BF16> { using T = uint16_t; };
-template <> struct ValOf<ValKind::I8> { using T = int8_t; };
-template <> struct ValOf<ValKind::C64> { using T = C64; };
-template <> struct ValOf<ValKind::UNIT> { using T = float; };  // the gathered "x" holds the products
-
-template <OutKind O> struct OutOf;
-template <> struct OutOf<OutKind::F32> { using T = float; };
-template <> struct OutOf<OutKind::F16> { using T = uint16_t; };
-template <> struct OutOf<OutKind::BF16> { using T = uint16_t; };
-template <> struct OutOf<OutKind::I32> { using T = int32_t; };
-template <> struct OutOf<OutKind::C64> { using T = C64; };
-
-template <typename T> __device__ __forceinline__ T Zero() { return T{}; }
-__device__ __forceinline__ bool IsZero(float v) { return v == 0.0f; }
-__device__ __forceinline__ bool IsZero(long long v) { return v == 0; }
-__device__ __forceinline__ bool IsZero(C64 v) { return v.re == 0.0f && v.im == 0.0f; }
-
-__device__ __forceinline__ float HalfToFloat(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-__device__ __forceinline__ float Bf16ToFloat(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
-
-// IEEE binary32 -> binary16, round to nearest, ties to even (written from
-// the IEEE 754 definition; NaN stays a quiet NaN, overflow goes to inf).
-__device__ __forceinline__ uint16_t FloatToHalfRne(float f)
-{
-    const uint32_t u = __float_as_uint(f);
-    const uint32_t sign = (u >> 16) & 0x8000U;
-    const uint32_t a = u & 0x7FFFFFFFU;
-    if (a >= 0x7F800000U) {
-        return static_cast<uint16_t>(sign | 0x7C00U | (a > 0x7F800000U ? (0x0200U | ((a >> 13) & 0x3FFU)) : 0U));
-    }
-    if (a >= 0x477FF000U) return static_cast<uint16_t>(sign | 0x7C00U);  // >= 65520 rounds to inf
-    if (a < 0x38800000U) {                                                // below 2^-14: subnormal half
-        if (a < 0x33000000U) return static_cast<uint16_t>(sign);          // below 2^-25
-        const uint32_t e = a >> 23;
-        const uint32_t m = (a & 0x7FFFFFU) | 0x800000U;
-        const uint32_t shift = 126U - e;  // value in units of 2^-24 is m >> shift
-        uint32_t r = m >> shift;
-        const uint32_t rem = m & ((1U << shift) - 1U);
-        const uint32_t half = 1U << (shift - 1U);
-        if (rem > half || (rem == half && (r & 1U))) ++r;
-        return static_cast<uint16_t>(sign | r);
-    }
-    uint32_t hb = (a >> 13) - (112U << 10);
-    const uint32_t rem = a & 0x1FFFU;
-    if (rem > 0x1000U || (rem == 0x1000U && (hb & 1U))) ++hb;
-    return static_cast<uint16_t>(sign | hb);
-}
-
-// binary32 -> bfloat16, round to nearest even; NaN stays NaN.
-__device__ __forceinline__ uint16_t FloatToBf16Rne(float f)
-{
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000U) == 0x7F800000U && (u & 0x7FFFFFU) != 0U) {
-        return static_cast<uint16_t>((u >> 16) | 0x0040U);
-    }
-    return static_cast<uint16_t>((u + 0x7FFFU + ((u >> 16) & 1U)) >> 16);
-}
-
-template <ValKind V, AccKind A>
-__device__ __forceinline__ typename AccOf<A>::T ToAcc(typename ValOf<V>::T v)
-{
-    if constexpr (V == ValKind::F32) {
-        if constexpr (A == AccKind::C64) return C64{v, 0.0f};
-        else return v;
-    } else if constexpr (V == ValKind::F16) {
-        return HalfToFloat(v);
-    } else if constexpr (V == ValKind::BF16) {
-        return Bf16ToFloat(v);
-    } else if constexpr (V == ValKind::I8) {
-        if constexpr (A == AccKind::I64) return static_cast<long long>(v);
-        else return static_cast<float>(v);
-    } else {
-        return v;
-    }
-}
-
-template <OutKind O, AccKind A>
-__device__ __forceinline__ typename AccOf<A>::T OutToAcc(typename OutOf<O>::T v)
-{
-    if constexpr (O == OutKind::F16) return HalfToFloat(v);
-    else if constexpr (O == OutKind::BF16) return Bf16ToFloat(v);
-    else if constexpr (O == OutKind::I32) return static_cast<long long>(v);
-    else return v;
-}
-
-// INT8 products accumulate exactly in int64; the output saturates to int32
-// while keeping cancellation between alpha*sum and beta*y
-// (sparse/spmv/arch35/spmv_kernel.cpp:341-376).
-__device__ __forceinline__ long long SaturateI32(long long v)
-{
-    return v > 2147483647LL ? 2147483647LL : v < -2147483648LL ? -2147483648LL : v;
-}
-
-__device__ __forceinline__ long long ScaledI64(long long sum, long long alpha, long long beta, long long oldY)
-{
-    const long long betaTerm = beta * oldY;
-    if (alpha == 0) return SaturateI32(betaTerm);
-    const long long mag = sum < 0 ? -sum : sum;
-    const long long scale = alpha < 0 ? -alpha : alpha;
-    const bool negative = (sum < 0) != (alpha < 0);
-    if (mag > 9223372036854775807LL / scale) return negative ? -2147483648LL : 2147483647LL;
-    const long long prod = negative ? -(mag * scale) : mag * scale;
-    if (prod > 2147483647LL - betaTerm) return 2147483647LL;
-    if (prod < -2147483648LL - betaTerm) return -2147483648LL;
-    return prod + betaTerm;
-}
-
-template <OutKind O, AccKind A>
-__device__ __forceinline__ typename OutOf<O>::T FromAcc(typename AccOf<A>::T v)
-{
-    if constexpr (O == OutKind::F16) return FloatToHalfRne(v);
-    else if constexpr (O == OutKind::BF16) return FloatToBf16Rne(v);
-    else if constexpr (O == OutKind::I32) return static_cast<int32_t>(SaturateI32(v));
-    else return v;
-}
-
-// ------------------------------- scalars ------------------------------------
-
-struct Scalars {
-    int32_t device;
-    float alpha_re, alpha_im, beta_re, beta_im;
-    int32_t alpha_i, beta_i;
-    const void* alpha_ptr;
-    const void* beta_ptr;
-};
-
-template <AccKind A>
-__device__ __forceinline__ void LoadScalars(const Scalars& s, typename AccOf<A>::T& alpha,
-                                            typename AccOf<A>::T& beta)
-{
-    if constexpr (A == AccKind::I64) {
-        alpha = s.device ? *static_cast<const int32_t*>(s.alpha_ptr) : s.alpha_i;
-        beta = s.device ? *static_cast<const int32_t*>(s.beta_ptr) : s.beta_i;
-    } else if constexpr (A == AccKind::C64) {
-        if (s.device) {
-            const float* a = static_cast<const float*>(s.alpha_ptr);
-            const float* b = static_cast<const float*>(s.beta_ptr);
-            alpha = C64{a[0], a[1]};
-            beta = C64{b[0], b[1]};
-        } else {
-            alpha = C64{s.alpha_re, s.alpha_im};
-            beta = C64{s.beta_re, s.beta_im};
-        }
-    } else {
-        alpha = s.device ? *static_cast<const float*>(s.alpha_ptr) : s.alpha_re;
-        beta = s.device ? *static_cast<const float*>(s.beta_ptr) : s.beta_re;
-    }
-}
-
-// y = alpha*sum + beta*y; y is not read when beta == 0
-// (sparse/spmv/arch35/spmv_kernel.cpp:341-345,544-552).
-template <OutKind O, AccKind A>
-__device__ __forceinline__ void StoreRow(typename OutOf<O>::T* y, int64_t idx, typename AccOf<A>::T sum,
-                                         typename AccOf<A>::T alpha, typename AccOf<A>::T beta, bool betaNz)
-{
-    using Acc = typename AccOf<A>::T;
-    const Acc oldY = betaNz ? OutToAcc<O, A>(y[idx]) : Zero<Acc>();
-    Acc r;
-    if constexpr (A == AccKind::I64) {
-        r = ScaledI64(sum, alpha, beta, oldY);
-    } else {
-        r = betaNz ? alpha * sum + beta * oldY : alpha * sum;
-    }
-    y[idx] = FromAcc<O, A>(r);
-}
 
 // ------------------------------ shuffles ------------------------------------
 
@@ -293,6 +113,10 @@ struct RowBlockParams {
     float* z;            // SpMVOp: output (y is then only read)
     int64_t rp_base;     // subtracted from p.rp entries (0 for the normalised copy)
     int32_t fixed_rows;  // SpMVOp ALG1: rows per block, blocks taken straight from p.rp
+    // When set, the kernel exits at once if the word is non-zero: Preprocess
+    // chose the staged-gather path for this matrix (its kernels are launched
+    // after this one and exit when the word is zero).
+    const uint32_t* skip_flag;
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -1166,6 +990,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
 
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
+    if (p.skip_flag != nullptr && ConstLoad<uint32_t>(p.skip_flag, 0) != 0U) return;
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float* sVal = sValAll[wv];
@@ -2243,6 +2068,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             }
             p.task_wgs = static_cast<int32_t>(taskWgs);
             p.task_waves = static_cast<int32_t>(taskWgs * kFlatWaves);
+            if (l.staged) p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
             const unsigned g = static_cast<unsigned>(taskWgs + (wgs + kXcds - 1) / kXcds * kXcds);
             if (betaNz) {
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kFlatWaves), 0,
@@ -2270,6 +2096,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             return 0;
         }
     }
+    if (l.staged) return 1;  // the staged path needs the stream kernel's operands (unit strides, aligned)
     hipLaunchKernelGGL((SpmvRowBlockKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, p);
     return 0;
 }
@@ -2660,18 +2487,25 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     h.task_start_offset = l.layout.tasks ? l.layout.task_start_offset : 0;
     h.task_block_offset = l.layout.tasks ? l.layout.task_block_offset : 0;
     h.max_tasks = l.layout.tasks ? static_cast<uint64_t>(l.layout.max_tasks) : 0;
+    if (l.staged) {  // staged_flag stays 0 until the staged preprocess decides
+        h.staged_buckets = static_cast<uint32_t>(l.layout.st_buckets);
+        h.staged_tiles = static_cast<uint64_t>(l.layout.st_tiles);
+        h.staged_tile_row_offset = l.layout.st_tile_row_offset;
+        h.staged_tile_nnz_offset = l.layout.st_tile_nnz_offset;
+    }
     const int64_t n = (l.rows > p.num_blocks ? l.rows : p.num_blocks) + 1;
     const unsigned grid = static_cast<unsigned>((n + kThreads - 1) / kThreads);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (l.rowptr64) {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int64_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) return BuildCsc<int64_t>(l, s);
-        if (l.layout.tasks) return BuildTasks<int64_t>(l, s);
+        if (l.layout.tasks && BuildTasks<int64_t>(l, s) != 0) return 1;
     } else {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) return BuildCsc<int32_t>(l, s);
-        if (l.layout.tasks) return BuildTasks<int32_t>(l, s);
+        if (l.layout.tasks && BuildTasks<int32_t>(l, s) != 0) return 1;
     }
+    if (l.staged) return LaunchStagedPreprocess(l, stream);
     return 0;
 }
 
@@ -2679,7 +2513,10 @@ int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= 0) return 0;
-    return l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
+    const int rc = l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
+    // staged gather: the row kernel above exits when Preprocess chose this path
+    if (rc == 0 && l.staged) return LaunchStagedCompute(l, stream);
+    return rc;
 }
 
 }  // namespace aclsp

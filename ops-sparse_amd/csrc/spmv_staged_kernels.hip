@@ -1,0 +1,751 @@
+// Staged-gather SpMV on gfx950: y = alpha*A*x + beta*y for matrices whose x
+// does not fit an XCD's L2 and whose columns are scattered.
+//
+// The row kernels (spmv_kernels.hip) gather x[col] straight from memory: for
+// a random column pattern over a 33.5 MB x every 2- or 4-byte value costs a
+// 128-byte line from the MALL, and the gathers cap the kernel at the MALL's
+// line rate (about 64 G lines/s), 5% of HBM bandwidth.  This path moves the
+// same data with streaming accesses only:
+//
+//  * Preprocess (pattern only; values, x and y may change between calls, the
+//    reference's contract, sparse/spmv/README.md aclsparseSpMVPreprocess):
+//    merge-path tiles of kStageTileItems rows+entries; every entry goes to the
+//    bucket of its column's x segment (128 KiB of x); per tile, a stable radix
+//    sort by column gives each entry its slot in the tile's bucket-ordered runs
+//    (st_perm) and, in bucket order, its column within the bucket (st_cl).  A
+//    per-tile count of distinct x lines decides the path: when the lines are
+//    few (banded matrices) the row kernels keep the matrix.
+//  * Pass A (StageGatherKernel), one workgroup per slice of the bucket-ordered
+//    slots: loads the slice's x segment into LDS (128 KiB) and writes
+//    xg[j] = segment[cl[j]]: a sequential read of cl and a sequential write.
+//  * Pass B (StageTileKernel), one workgroup per tile: copies the tile's run
+//    of every bucket from xg into LDS (runs of neighbouring tiles are
+//    adjacent, so their lines are shared through L2), multiplies each value
+//    a_k (CSR order, coalesced) by its staged x value, and sums the tile's
+//    rows from LDS: short rows one thread each, long rows a wave each.  Rows
+//    crossing tile ends leave partial sums (st_head / st_tail).
+//  * Fix-up (StageFixupKernel): one thread per tile whose first row ends in
+//    it combines that row's partial sums in tile order.
+//
+// Every row is summed in an order fixed by the pattern, so results are
+// reproducible bit for bit.  Reference counterpart of the whole path: the
+// warp-per-row kernels of sparse/spmv/arch35/spmv_kernel.cpp:501-577, which
+// gather x from global memory.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <cstdint>
+
+#include "aclsparse_internal.h"
+#include "spmv_device.h"
+
+namespace aclsp {
+namespace {
+
+using namespace dev;
+
+constexpr int kXcds = 8;
+constexpr int kWave = 64;
+constexpr int kTileThreads = 512;                       // pass B and the per-tile preprocess kernels
+constexpr int kTileWaves = kTileThreads / kWave;
+constexpr int kTileItems = static_cast<int>(kStageTileItems);
+constexpr int kSortIpt = 16;                            // 512 x 16 = 8192 >= kTileItems keys per tile
+constexpr int kGroupSlots = 4;                          // groups of 4 entries per thread in pass B
+constexpr int kGatherThreads = 1024;                    // pass A
+constexpr int kLongRow = 32;                            // in-tile rows longer than this are summed by a wave
+constexpr int kMaxLong = kTileItems / kLongRow + 1;
+constexpr int kScanIpt = 3;                             // 512 x 3 >= kStageMaxBuckets + 1 run offsets
+
+static_assert(kTileThreads * kSortIpt >= kTileItems, "sort capacity");
+static_assert((kTileItems + 3) / 4 + 1 <= kTileThreads * kGroupSlots, "group slots");
+static_assert(kTileThreads * kScanIpt >= kStageMaxBuckets + 1, "run-offset scan capacity");
+
+struct StageParams {
+    const void* norm;  // normalised row offsets, RowT[rows+2]
+    const int32_t* col;
+    int32_t base;
+    int32_t buckets;  // S; bucket S collects columns outside [0, cols)
+    int32_t wshift;   // log2 of the columns per bucket
+    int32_t line_shift;  // log2 of the x values per 128-byte line
+    const void* val;
+    const void* x;
+    void* y;
+    int64_t rows, cols, nnz;
+    int64_t tiles;  // T
+    int32_t* tile_row;
+    int64_t* tile_nnz;
+    uint32_t* counts;
+    uint32_t* start_bm;
+    uint32_t* start;
+    uint16_t* perm;
+    uint16_t* cl;
+    void* xg;
+    float* head;
+    float* tail;
+    unsigned long long* metric;
+    uint32_t* flag;
+    int64_t part;  // pass A: bucket-ordered slots per workgroup
+    Scalars s;
+};
+
+// Workgroup index remapped so that each XCD serves a contiguous range
+// (hardware hands workgroup ids to the 8 XCDs round-robin); the grid is a
+// multiple of 8.
+__device__ __forceinline__ int64_t XcdIndex()
+{
+    const int64_t per = gridDim.x / kXcds;
+    return static_cast<int64_t>(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+}
+
+__device__ __forceinline__ uint32_t FlagSet(const uint32_t* flag)
+{
+    typedef const __attribute__((address_space(4))) uint32_t* CPtr;  // scalar load: written by Preprocess
+    return *reinterpret_cast<CPtr>(reinterpret_cast<uintptr_t>(flag));
+}
+
+template <typename RowT>
+__device__ __forceinline__ int64_t Norm(const StageParams& q, int64_t i)
+{
+    return static_cast<int64_t>(static_cast<const RowT*>(q.norm)[i]);
+}
+
+// Sort key of an entry: its column (bucket = key >> wshift), or the first
+// column of the bucket S when the column is outside the matrix.
+__device__ __forceinline__ uint32_t KeyOf(const StageParams& q, int32_t rawCol)
+{
+    const int64_t c = static_cast<int64_t>(rawCol) - q.base;
+    if (c < 0 || c >= q.cols) return static_cast<uint32_t>(q.buckets) << q.wshift;
+    return static_cast<uint32_t>(c);
+}
+
+// ------------------------------- preprocess ---------------------------------
+
+// Corner (row, entry) of every tile on the merge path of row ends and
+// entries (Merrill & Garland, SC'16): tile t starts at diagonal t*kTileItems.
+template <typename RowT>
+__global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
+{
+    const int64_t t = blockIdx.x * int64_t{256} + threadIdx.x;
+    if (t == 0) *q.metric = 0ULL;
+    if (t > q.tiles) return;
+    const int64_t total = q.rows + q.nnz;
+    const int64_t d = t * kTileItems < total ? t * kTileItems : total;
+    int64_t lo = d - q.nnz > 0 ? d - q.nnz : 0;
+    int64_t hi = d < q.rows ? d : q.rows;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (Norm<RowT>(q, mid + 1) <= d - 1 - mid) lo = mid + 1;
+        else hi = mid;
+    }
+    q.tile_row[t] = static_cast<int32_t>(lo);
+    q.tile_nnz[t] = d - lo;
+}
+
+// counts[s*(T+1) + t] = entries of tile t in bucket s (column T is zero).
+__global__ __launch_bounds__(kTileThreads) void StageCountKernel(StageParams q)
+{
+    __shared__ uint32_t hist[kStageMaxBuckets + 1];
+    const int64_t t = blockIdx.x;
+    const int nb = q.buckets + 1;
+    for (int s = threadIdx.x; s < nb; s += kTileThreads) hist[s] = 0U;
+    __syncthreads();
+    if (t < q.tiles) {
+        const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
+        for (int64_t k = e0 + threadIdx.x; k < e1; k += kTileThreads) {
+            atomicAdd(&hist[KeyOf(q, q.col[k]) >> q.wshift], 1U);
+        }
+    }
+    __syncthreads();
+    for (int s = threadIdx.x; s < nb; s += kTileThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
+}
+
+// start[t*(S+1) + s] = start_bm[s*(T+1) + t].
+__global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
+{
+    __shared__ uint32_t tile[32][33];
+    const int64_t nt = q.tiles + 1;
+    const int nb = q.buckets + 1;
+    const int64_t t0 = blockIdx.x * int64_t{32};
+    const int s0 = blockIdx.y * 32;
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const int s = s0 + i;
+        const int64_t t = t0 + threadIdx.x;
+        if (s < nb && t < nt) tile[i][threadIdx.x] = q.start_bm[s * nt + t];
+    }
+    __syncthreads();
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const int64_t t = t0 + i;
+        const int s = s0 + threadIdx.x;
+        if (s < nb && t < nt) q.start[t * nb + s] = tile[threadIdx.x][i];
+    }
+}
+
+// Per tile: stable radix sort of (column, position) so that the tile's
+// entries are in bucket order; perm[k] = sorted slot of entry k,
+// cl[start(t,s) + rank] = column within the bucket; adds the tile's count of
+// distinct x lines to the metric.
+template <int kEndBit>
+__global__ __launch_bounds__(kTileThreads) void StageSortKernel(StageParams q)
+{
+    using Sort = hipcub::BlockRadixSort<uint32_t, kTileThreads, kSortIpt, uint32_t>;
+    __shared__ typename Sort::TempStorage sortStorage;
+    __shared__ uint32_t firstSlot[kStageMaxBuckets + 1];
+    __shared__ uint32_t lastKey[kTileThreads];
+    __shared__ uint32_t lineCount;
+    const int64_t t = blockIdx.x;
+    const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
+    const int n = static_cast<int>(e1 - e0);
+    uint32_t keys[kSortIpt], vals[kSortIpt];
+    constexpr uint32_t kPad = kEndBit >= 32 ? 0xFFFFFFFFU : ((1U << kEndBit) - 1U);
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        keys[u] = i < n ? KeyOf(q, q.col[e0 + i]) : kPad;
+        vals[u] = static_cast<uint32_t>(i);
+    }
+    if (threadIdx.x == 0) lineCount = 0U;
+    Sort(sortStorage).Sort(keys, vals, 0, kEndBit);
+    lastKey[threadIdx.x] = keys[kSortIpt - 1];
+    __syncthreads();
+    uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
+    uint32_t lines = 0U;
+    const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        if (i < n) {
+            const uint32_t key = keys[u];
+            const uint32_t b = key >> q.wshift;
+            if (prev == 0xFFFFFFFFU || (prev >> q.wshift) != b) firstSlot[b] = static_cast<uint32_t>(i);
+            if (b != nullBucket && (prev == 0xFFFFFFFFU || (prev >> q.line_shift) != (key >> q.line_shift))) ++lines;
+            q.perm[e0 + vals[u]] = static_cast<uint16_t>(i);
+        }
+        prev = keys[u];
+    }
+    if (lines != 0U) atomicAdd(&lineCount, lines);
+    __syncthreads();
+    const uint32_t mask = (1U << q.wshift) - 1U;
+    const int nb = q.buckets + 1;
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        if (i < n) {
+            const uint32_t key = keys[u];
+            const uint32_t b = key >> q.wshift;
+            const uint32_t slot = q.start[t * nb + b] + (static_cast<uint32_t>(i) - firstSlot[b]);
+            q.cl[slot] = static_cast<uint16_t>(b == nullBucket ? 0U : (key & mask));
+        }
+    }
+    if (threadIdx.x == 0 && lineCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(lineCount));
+}
+
+// The path decision: staged when the tiles' distinct x lines exceed
+// nnz / kStageLinesPerEntryDen.
+__global__ void StageDecideKernel(StageParams q)
+{
+    const unsigned long long lines = *q.metric;
+    *q.flag = lines * static_cast<unsigned long long>(kStageLinesPerEntryDen) >
+                      static_cast<unsigned long long>(q.nnz)
+                  ? 1U
+                  : 0U;
+}
+
+// --------------------------------- pass A -----------------------------------
+
+template <typename XT>
+__device__ __forceinline__ void StoreGroup(XT* dst, const XT (&o)[8]);
+
+template <>
+__device__ __forceinline__ void StoreGroup<uint16_t>(uint16_t* dst, const uint16_t (&o)[8])
+{
+    uint4 v;
+    v.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
+    v.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+    v.z = static_cast<uint32_t>(o[4]) | (static_cast<uint32_t>(o[5]) << 16);
+    v.w = static_cast<uint32_t>(o[6]) | (static_cast<uint32_t>(o[7]) << 16);
+    *reinterpret_cast<uint4*>(dst) = v;
+}
+
+template <>
+__device__ __forceinline__ void StoreGroup<uint32_t>(uint32_t* dst, const uint32_t (&o)[8])
+{
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<uint4*>(dst)[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// Workgroup w fills the bucket-ordered slots [w*part, (w+1)*part): for every
+// bucket overlapping them, the bucket's x segment is loaded into LDS and each
+// slot j gets xg[j] = segment[cl[j]] (0 for the out-of-range bucket).  XT is
+// the raw x element (uint16_t for fp16 / bf16, uint32_t for fp32).
+template <typename XT>
+__global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams q)
+{
+    extern __shared__ uint4 segRaw[];
+    XT* seg = reinterpret_cast<XT*>(segRaw);
+    if (FlagSet(q.flag) == 0U) return;
+    const int64_t w = XcdIndex();
+    const int64_t a = w * q.part;
+    if (a >= q.nnz) return;
+    const int64_t b = a + q.part < q.nnz ? a + q.part : q.nnz;
+    const int nb = q.buckets + 1;
+    const uint32_t* base = q.start;                  // row 0: first slot of every bucket
+    const uint32_t* ends = q.start + q.tiles * nb;   // row T: end of every bucket
+    // first bucket that ends after a
+    int lo = 0, hi = nb - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (static_cast<int64_t>(ends[mid]) <= a) lo = mid + 1;
+        else hi = mid;
+    }
+    const int64_t segLen = int64_t{1} << q.wshift;
+    const XT* x = static_cast<const XT*>(q.x);
+    XT* xg = static_cast<XT*>(q.xg);
+    constexpr int kVec = 16 / sizeof(XT);
+    for (int s = lo; s < nb; ++s) {
+        const int64_t sb = base[s], se = ends[s];
+        if (sb >= b) break;
+        const int64_t j0 = sb > a ? sb : a;
+        const int64_t j1 = se < b ? se : b;
+        if (j0 >= j1) continue;
+        const bool real = s < q.buckets;
+        if (real) {
+            const int64_t c0 = static_cast<int64_t>(s) << q.wshift;
+            const int64_t n = q.cols - c0 < segLen ? q.cols - c0 : segLen;
+            const int64_t nv = n / kVec;
+            for (int64_t i = threadIdx.x; i < nv; i += kGatherThreads) {
+                segRaw[i] = reinterpret_cast<const uint4*>(x + c0)[i];
+            }
+            for (int64_t i = nv * kVec + threadIdx.x; i < n; i += kGatherThreads) seg[i] = x[c0 + i];
+            __syncthreads();
+        }
+        for (int64_t g = (j0 >> 3) + threadIdx.x; g * 8 < j1; g += kGatherThreads) {
+            const uint4 c = *reinterpret_cast<const uint4*>(q.cl + g * 8);
+            const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+            XT o[8];
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t ci = (cw[u >> 1] >> ((u & 1) * 16)) & 0xFFFFU;
+                o[u] = real ? seg[ci] : XT{0};
+            }
+            const int64_t j = g * 8;
+            if (j >= j0 && j + 8 <= j1) {
+                StoreGroup<XT>(xg + j, o);
+            } else {
+                for (int u = 0; u < 8; ++u) {
+                    if (j + u >= j0 && j + u < j1) xg[j + u] = o[u];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// --------------------------------- pass B -----------------------------------
+
+template <ValKind V>
+struct StageVal;
+template <>
+struct StageVal<ValKind::F32> {
+    using Raw = uint32_t;
+    using Group = uint4;  // 4 values
+    __device__ static float ToF(uint32_t r) { return __uint_as_float(r); }
+    __device__ static uint32_t Get(const uint4& g, int u) { return u == 0 ? g.x : u == 1 ? g.y : u == 2 ? g.z : g.w; }
+};
+template <>
+struct StageVal<ValKind::F16> {
+    using Raw = uint16_t;
+    using Group = uint2;
+    __device__ static float ToF(uint16_t r) { return HalfToFloat(r); }
+    __device__ static uint16_t Get(const uint2& g, int u)
+    {
+        const uint32_t w = u < 2 ? g.x : g.y;
+        return static_cast<uint16_t>(w >> ((u & 1) * 16));
+    }
+};
+template <>
+struct StageVal<ValKind::BF16> {
+    using Raw = uint16_t;
+    using Group = uint2;
+    __device__ static float ToF(uint16_t r) { return Bf16ToFloat(r); }
+    __device__ static uint16_t Get(const uint2& g, int u)
+    {
+        const uint32_t w = u < 2 ? g.x : g.y;
+        return static_cast<uint16_t>(w >> ((u & 1) * 16));
+    }
+};
+
+__device__ __forceinline__ float WaveSum(float v)
+{
+    for (int m = kWave / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// Row end of a tile's row: y, or the tile's head / tail partial sum.
+template <OutKind O>
+__device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int loc, int nRowsDone, bool headRow,
+                                          bool tailHasEntries, float sum, float alpha, float beta, bool betaNz,
+                                          int64_t r0)
+{
+    using OutT = typename OutOf<O>::T;
+    if (loc < nRowsDone) {
+        if (loc == 0 && headRow) q.head[t] = sum;
+        else StoreRow<O, AccKind::F32>(static_cast<OutT*>(q.y), r0 + loc, sum, alpha, beta, betaNz);
+    } else if (tailHasEntries) {
+        if (nRowsDone == 0 && headRow) q.head[t] = sum;
+        else q.tail[t] = sum;
+    }
+}
+
+// One workgroup per tile (XCD-contiguous).  LDS: run tables, then one area of
+// kTileItems+2 words that holds the staged x values, then (in place) the
+// products, followed by the tile's row offsets relative to its first entry.
+template <typename RowT, ValKind V, OutKind O>
+__global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
+{
+    using SV = StageVal<V>;
+    using Raw = typename SV::Raw;
+    using Group = typename SV::Group;
+    using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
+    __shared__ uint32_t runSrc[kStageMaxBuckets + 1];
+    __shared__ uint32_t runOff[kStageMaxBuckets + 2];
+    __shared__ float area[kTileItems + 2];
+    __shared__ int32_t longRows[kMaxLong];
+    __shared__ int longCount;
+    __shared__ typename Scan::TempStorage scanStorage;
+
+    if (FlagSet(q.flag) == 0U) return;
+    const int64_t t = XcdIndex();
+    if (t >= q.tiles) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid / kWave;
+    const int64_t r0 = q.tile_row[t], r1 = q.tile_row[t + 1];
+    const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
+    const int E = static_cast<int>(e1 - e0);
+    const int R = static_cast<int>(r1 - r0);
+    const int nb = q.buckets + 1;
+
+    // 1. values and slots of this thread's groups of 4 entries (CSR order)
+    const int64_t g0 = e0 >> 2;
+    const int ng = static_cast<int>(((e1 + 3) >> 2) - g0);
+    const Group* vg = reinterpret_cast<const Group*>(q.val);
+    const uint2* pg = reinterpret_cast<const uint2*>(q.perm);
+    const int64_t lastGroup = (q.nnz - 1) >> 2;  // groups past it would read beyond the values
+    Group gv[kGroupSlots];
+    uint2 gp[kGroupSlots];
+    for (int u = 0; u < kGroupSlots; ++u) {
+        const int gi = tid + u * kTileThreads;
+        const int64_t g = g0 + gi;
+        if (gi < ng) {
+            if (g < lastGroup || ((q.nnz & 3) == 0)) {
+                gv[u] = vg[g];
+            } else {
+                // last, partial group: element loads
+                const Raw* vr = static_cast<const Raw*>(q.val);
+                Raw e[4];
+                for (int k = 0; k < 4; ++k) e[k] = g * 4 + k < q.nnz ? vr[g * 4 + k] : Raw{0};
+                if constexpr (sizeof(Raw) == 4) {
+                    gv[u] = make_uint4(e[0], e[1], e[2], e[3]);
+                } else {
+                    gv[u] = make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
+                                       static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
+                }
+            }
+            gp[u] = pg[g];  // st_perm is padded by 8 slots
+        }
+    }
+
+    // 2. run tables: source slot and length of every bucket's run
+    uint32_t cnt[kScanIpt];
+    for (int u = 0; u < kScanIpt; ++u) {
+        const int s = tid * kScanIpt + u;
+        cnt[u] = 0U;
+        if (s < nb) {
+            const uint32_t a = q.start[t * nb + s];
+            runSrc[s] = a;
+            cnt[u] = q.start[(t + 1) * nb + s] - a;
+        }
+    }
+    Scan(scanStorage).ExclusiveSum(cnt, cnt);
+    for (int u = 0; u < kScanIpt; ++u) {
+        const int s = tid * kScanIpt + u;
+        if (s < nb) runOff[s] = cnt[u];
+    }
+    if (tid == 0) {
+        runOff[nb] = static_cast<uint32_t>(E);
+        longCount = 0;
+    }
+    // row offsets relative to e0, clamped to [0, E], after the entry area
+    int32_t* rel = reinterpret_cast<int32_t*>(area + E);
+    const bool lastRowInside = r1 < q.rows;
+    const int nLoc = R + (lastRowInside ? 1 : 0);
+    for (int i = tid; i <= R; i += kTileThreads) {
+        int64_t v = Norm<RowT>(q, r0 + i) - e0;
+        v = v < 0 ? 0 : v > E ? E : v;
+        rel[i] = static_cast<int32_t>(v);
+    }
+    if (tid == 0) rel[R + 1] = E;
+    const bool headRow = Norm<RowT>(q, r0) < e0;
+    __syncthreads();
+
+    // 3. stage the runs: wave w copies slots [w*E/8, (w+1)*E/8) of the tile
+    {
+        Raw* xl = reinterpret_cast<Raw*>(area);
+        const Raw* xg = static_cast<const Raw*>(q.xg);
+        const int i0 = static_cast<int>((static_cast<int64_t>(E) * wv) / kTileWaves);
+        const int i1 = static_cast<int>((static_cast<int64_t>(E) * (wv + 1)) / kTileWaves);
+        if (i0 < i1) {
+            int lo = 0, hi = nb - 1;  // last bucket with runOff <= i0
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (static_cast<int>(runOff[mid]) <= i0) lo = mid;
+                else hi = mid - 1;
+            }
+            int s = lo;
+            int i = i0;
+            while (i < i1) {
+                const int off = static_cast<int>(runOff[s]);
+                int end = static_cast<int>(runOff[s + 1]);
+                end = end < i1 ? end : i1;
+                const int64_t src = static_cast<int64_t>(runSrc[s]) - off;
+                for (int k = i + lane; k < end; k += kWave) xl[k] = xg[src + k];
+                i = end > i ? end : i;
+                ++s;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. products a_k * x_col(k) of this thread's groups, then into the area
+    float prod[kGroupSlots][4];
+    {
+        const Raw* xl = reinterpret_cast<const Raw*>(area);
+        for (int u = 0; u < kGroupSlots; ++u) {
+            const int gi = tid + u * kTileThreads;
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
+                const int64_t e = (g0 + gi) * 4 + k;
+                const bool in = gi < ng && e >= e0 && e < e1;
+                // entries of the neighbouring tiles in the edge groups hold other tiles' slots
+                const int slot = in ? static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU) : 0;
+                prod[u][k] = in ? SV::ToF(SV::Get(gv[u], k)) * SV::ToF(xl[slot]) : 0.0f;
+            }
+        }
+    }
+    __syncthreads();
+    for (int u = 0; u < kGroupSlots; ++u) {
+        const int gi = tid + u * kTileThreads;
+        if (gi < ng) {
+            for (int k = 0; k < 4; ++k) {
+                const int64_t e = (g0 + gi) * 4 + k;
+                if (e >= e0 && e < e1) area[e - e0] = prod[u][k];
+            }
+        }
+    }
+    __syncthreads();
+
+    // 5. rows: short ones by one thread, long ones queued for a wave
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
+    const bool tailHasEntries = lastRowInside && rel[R] < E;
+    for (int loc = tid; loc < nLoc; loc += kTileThreads) {
+        const int a = rel[loc], b = rel[loc + 1];
+        if (b - a > kLongRow) {
+            longRows[atomicAdd(&longCount, 1)] = loc;
+            continue;
+        }
+        float sum = 0.0f;
+        for (int k = a; k < b; ++k) sum += area[k];
+        FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
+    }
+    __syncthreads();
+    const int nLong = longCount;
+    for (int li = wv; li < nLong; li += kTileWaves) {
+        const int loc = longRows[li];
+        const int a = rel[loc], b = rel[loc + 1];
+        float part = 0.0f;
+        for (int k = a + lane; k < b; k += kWave) part += area[k];
+        const float sum = WaveSum(part);
+        if (lane == 0) FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
+    }
+}
+
+// Rows that cross tile ends: the tile where such a row ends adds, in tile
+// order, the tail partial of the tile where it starts and the head partials
+// of every tile after it, then stores y.
+template <typename RowT, OutKind O>
+__global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
+{
+    using OutT = typename OutOf<O>::T;
+    if (FlagSet(q.flag) == 0U) return;
+    const int64_t t = blockIdx.x * int64_t{256} + threadIdx.x;
+    if (t >= q.tiles) return;
+    const int64_t r0 = q.tile_row[t];
+    if (q.tile_row[t + 1] == r0) return;                 // no row ends in tile t
+    const int64_t start = Norm<RowT>(q, r0);
+    if (start >= q.tile_nnz[t]) return;                  // its first row starts inside it
+    int64_t u = t - 1;
+    while (u > 0 && q.tile_row[u] == r0 && start < q.tile_nnz[u]) --u;  // tiles wholly inside the row
+    float sum = q.tail[u];
+    for (int64_t v = u + 1; v <= t; ++v) sum += q.head[v];
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
+    StoreRow<O, AccKind::F32>(static_cast<OutT*>(q.y), r0, sum, alpha, beta, betaNz);
+}
+
+// ------------------------------- launchers ----------------------------------
+
+template <typename T>
+T* At(void* ws, size_t off) { return reinterpret_cast<T*>(static_cast<uint8_t*>(ws) + off); }
+
+StageParams MakeStageParams(const SpmvLaunch& l)
+{
+    const SpmvLayout& L = l.layout;
+    StageParams q{};
+    q.norm = At<void>(l.ws, L.rowptr_offset);
+    q.col = l.col;
+    q.base = l.base;
+    q.buckets = L.st_buckets;
+    q.wshift = L.st_wshift;
+    q.line_shift = L.st_value_bytes == 4 ? 5 : 6;  // 32 or 64 values per 128-byte line
+    q.val = l.val;
+    q.x = l.x;
+    q.y = l.y;
+    q.rows = l.rows;
+    q.cols = l.cols;
+    q.nnz = l.nnz;
+    q.tiles = L.st_tiles;
+    q.tile_row = At<int32_t>(l.ws, L.st_tile_row_offset);
+    q.tile_nnz = At<int64_t>(l.ws, L.st_tile_nnz_offset);
+    q.counts = At<uint32_t>(l.ws, L.st_counts_offset);
+    q.start_bm = At<uint32_t>(l.ws, L.st_start_bm_offset);
+    q.start = At<uint32_t>(l.ws, L.st_start_offset);
+    q.perm = At<uint16_t>(l.ws, L.st_perm_offset);
+    q.cl = At<uint16_t>(l.ws, L.st_cl_offset);
+    q.xg = At<void>(l.ws, L.st_xg_offset);
+    q.head = At<float>(l.ws, L.st_head_offset);
+    q.tail = At<float>(l.ws, L.st_tail_offset);
+    q.metric = At<unsigned long long>(l.ws, L.st_metric_offset);
+    q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
+    q.part = L.st_part_size;
+    q.s.device = l.device_scalars;
+    q.s.alpha_re = l.alpha_re;
+    q.s.beta_re = l.beta_re;
+    q.s.alpha_ptr = l.alpha_ptr;
+    q.s.beta_ptr = l.beta_ptr;
+    return q;
+}
+
+unsigned XcdGrid(int64_t n) { return static_cast<unsigned>((n + kXcds - 1) / kXcds * kXcds); }
+
+template <int kEndBit>
+void LaunchSort(const StageParams& q, hipStream_t s)
+{
+    hipLaunchKernelGGL((StageSortKernel<kEndBit>), dim3(static_cast<unsigned>(q.tiles)), dim3(kTileThreads), 0, s, q);
+}
+
+template <typename RowT>
+int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
+{
+    const SpmvLayout& L = l.layout;
+    StageParams q = MakeStageParams(l);
+    const int64_t T = L.st_tiles;
+    hipLaunchKernelGGL((StageTileSplitKernel<RowT>), dim3(static_cast<unsigned>((T + 1 + 255) / 256)), dim3(256), 0,
+                       s, q);
+    hipLaunchKernelGGL(StageCountKernel, dim3(static_cast<unsigned>(T + 1)), dim3(kTileThreads), 0, s, q);
+    const int64_t cells = static_cast<int64_t>(L.st_buckets + 1) * (T + 1);
+    void* temp = reinterpret_cast<void*>(
+        (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, L.st_scan_offset)) + 255) & ~uintptr_t{255});
+    size_t tempBytes = L.st_scan_bytes;
+    if (hipcub::DeviceScan::ExclusiveSum(temp, tempBytes, q.counts, q.start_bm, static_cast<int>(cells), s) !=
+        hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(StageTransposeKernel,
+                       dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
+                       dim3(32, 8), 0, s, q);
+    // sort keys: columns below (S+1) << wshift, plus an all-ones pad key
+    const uint64_t maxKey = (static_cast<uint64_t>(L.st_buckets) + 1) << L.st_wshift;
+    int bits = 1;
+    while ((uint64_t{1} << bits) <= maxKey) ++bits;
+    if (bits <= 20) LaunchSort<20>(q, s);
+    else if (bits <= 24) LaunchSort<24>(q, s);
+    else if (bits <= 28) LaunchSort<28>(q, s);
+    else LaunchSort<32>(q, s);
+    hipLaunchKernelGGL(StageDecideKernel, dim3(1), dim3(1), 0, s, q);
+    return 0;
+}
+
+template <typename RowT, ValKind V, OutKind O>
+void LaunchStagedTyped(const SpmvLaunch& l, const StageParams& q, hipStream_t s)
+{
+    using Raw = typename StageVal<V>::Raw;
+    const SpmvLayout& L = l.layout;
+    hipLaunchKernelGGL((StageGatherKernel<Raw>), dim3(XcdGrid(L.st_parts)), dim3(kGatherThreads),
+                       static_cast<unsigned>(kStageSegmentBytes), s, q);
+    hipLaunchKernelGGL((StageTileKernel<RowT, V, O>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads), 0, s, q);
+    hipLaunchKernelGGL((StageFixupKernel<RowT, O>), dim3(static_cast<unsigned>((L.st_tiles + 255) / 256)), dim3(256),
+                       0, s, q);
+}
+
+template <typename RowT>
+int LaunchStagedRowT(const SpmvLaunch& l, hipStream_t s)
+{
+    const StageParams q = MakeStageParams(l);
+    switch (l.val_kind) {
+        case ValKind::F32: LaunchStagedTyped<RowT, ValKind::F32, OutKind::F32>(l, q, s); return 0;
+        case ValKind::F16:
+            if (l.out_kind == OutKind::F16) LaunchStagedTyped<RowT, ValKind::F16, OutKind::F16>(l, q, s);
+            else LaunchStagedTyped<RowT, ValKind::F16, OutKind::F32>(l, q, s);
+            return 0;
+        case ValKind::BF16:
+            if (l.out_kind == OutKind::BF16) LaunchStagedTyped<RowT, ValKind::BF16, OutKind::BF16>(l, q, s);
+            else LaunchStagedTyped<RowT, ValKind::BF16, OutKind::F32>(l, q, s);
+            return 0;
+        default: return 1;
+    }
+}
+
+// Pass A's dynamic LDS (128 KiB) is beyond the 64 KiB that older parts
+// allow; gfx950 has 160 KiB per workgroup.  The attribute is set once, and a
+// runtime that does not need it may decline it (the launch reports real
+// failures).
+template <typename XT>
+void AllowGatherLds()
+{
+    static const bool once = [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&StageGatherKernel<XT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kStageSegmentBytes));
+        (void)hipGetLastError();
+        return true;
+    }();
+    (void)once;
+}
+
+}  // namespace
+
+size_t StageScanTempBytes(int64_t n)
+{
+    size_t bytes = 0;
+    if (hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, static_cast<uint32_t*>(nullptr),
+                                         static_cast<uint32_t*>(nullptr), static_cast<int>(n)) != hipSuccess) {
+        bytes = static_cast<size_t>(n) * 8 + (1 << 20);
+    }
+    return bytes;
+}
+
+int LaunchStagedPreprocess(const SpmvLaunch& l, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!l.layout.staged) return 1;
+    return l.rowptr64 ? StagedPreprocessTyped<int64_t>(l, s) : StagedPreprocessTyped<int32_t>(l, s);
+}
+
+int LaunchStagedCompute(const SpmvLaunch& l, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!l.layout.staged) return 1;
+    if (l.layout.st_value_bytes == 4) AllowGatherLds<uint32_t>();
+    else AllowGatherLds<uint16_t>();
+    return l.rowptr64 ? LaunchStagedRowT<int64_t>(l, s) : LaunchStagedRowT<int32_t>(l, s);
+}
+
+}  // namespace aclsp

@@ -226,6 +226,31 @@ def partition(row_ptr, nnz, rows=None, stride=1, base=0):
     return norm, blocks, bnnz
 
 
+def merge_path_tiles(norm_row_ptr, items):
+    """Corners of the merge-path tiles of a CSR matrix (Merrill & Garland, SC'16, "Merge-based
+    parallel sparse matrix-vector multiplication"): the path walks the row ends
+    a[i] = rp[i+1] and the entry indices 0..nnz-1, taking a row end first when
+    a[i] <= the next entry index; tile t starts at diagonal min(t*items, rows+nnz).
+    Returns (rows_done[T+1], entries_done[T+1]) for the normalised row offsets
+    ``norm_row_ptr`` (rp[0] = 0).  The staged-gather tiles of this build; no
+    reference counterpart (the reference has no merge-path partition)."""
+    rp = np.asarray(norm_row_ptr, np.int64)
+    rows = rp.size - 1
+    nnz = int(rp[-1])
+    total = rows + nnz
+    tiles = -(-total // items)
+    d = np.minimum(np.arange(tiles + 1, dtype=np.int64) * items, total)
+    lo = np.maximum(d - nnz, 0)
+    hi = np.minimum(d, rows)
+    while np.any(lo < hi):
+        act = lo < hi
+        mid = (lo + hi) >> 1
+        go_right = act & (rp[np.minimum(mid + 1, rows)] <= d - 1 - mid)
+        lo = np.where(go_right, mid + 1, lo)
+        hi = np.where(act & ~go_right, mid, hi)
+    return lo.astype(np.int32), d - lo
+
+
 def task_table(block_nnz, long_chunks, chunk=512):
     """(task_start[B+1], task_block[total]) of the long-block task table.
 

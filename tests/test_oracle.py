@@ -438,3 +438,44 @@ def test_threaded_spmv_matches_serial_bit_for_bit():
         s = oracle.spmv_lowp(rp, col, vb, xb, yb, kind, kind, 1.5, -0.5)
         for t in (1, 3, 8):
             assert np.array_equal(oracle.spmv_lowp_threads(rp, col, vb, xb, yb, kind, kind, 1.5, -0.5, t), s)
+
+
+def _walk_merge_path(rp, items):
+    """Brute force: walk the merge path one item at a time (row end first when its
+    entries are all consumed) and record the corner at every multiple of ``items``."""
+    rows, nnz = rp.size - 1, int(rp[-1])
+    i = j = 0
+    corners = [(0, 0)]
+    for step in range(1, rows + nnz + 1):
+        if i < rows and rp[i + 1] <= j:
+            i += 1
+        else:
+            j += 1
+        if step % items == 0 or step == rows + nnz:
+            corners.append((i, j))
+    return np.array([c[0] for c in corners]), np.array([c[1] for c in corners])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_merge_path_tiles_match_a_walk_of_the_path(seed):
+    rng = np.random.default_rng(seed)
+    rows = int(rng.integers(1, 300))
+    kind = seed % 3
+    if kind == 0:
+        lengths = rng.integers(0, 12, rows)
+    elif kind == 1:  # many empty rows, a few long ones
+        lengths = np.where(rng.random(rows) < 0.1, rng.integers(20, 400, rows), 0)
+    else:
+        lengths = np.zeros(rows, np.int64)
+        lengths[rng.integers(0, rows)] = int(rng.integers(1, 900))
+    rp = np.zeros(rows + 1, np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    for items in (1, 2, 7, 64, 1000):
+        r, e = oracle.merge_path_tiles(rp, items)
+        rw, ew = _walk_merge_path(rp, items)
+        np.testing.assert_array_equal(r, rw)
+        np.testing.assert_array_equal(e, ew)
+        # every tile holds exactly `items` items but the last; rows done and entries done never decrease
+        assert np.all(np.diff(r + e)[:-1] == items) and np.all(np.diff(r) >= 0) and np.all(np.diff(e) >= 0)
+        # a corner's completed rows have all their entries consumed
+        assert np.all(rp[r] <= e)
