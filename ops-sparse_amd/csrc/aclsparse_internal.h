@@ -266,7 +266,10 @@ size_t TaskScanTempBytes(int64_t n);
 // kStageMinXBytes; Preprocess measures the columns' spread and keeps the row
 // kernels when x accesses are local (banded matrices).
 // ---------------------------------------------------------------------------
-constexpr int64_t kStageTileItems = 8184;  // rows + entries per tile: <= 2047 groups of 4 entries
+#ifndef SPMV_STAGE_TILE_ITEMS
+#define SPMV_STAGE_TILE_ITEMS 8184
+#endif
+constexpr int64_t kStageTileItems = SPMV_STAGE_TILE_ITEMS;  // rows + entries per tile: <= 2047 groups of 4 entries
 constexpr int64_t kStageMinNnz = int64_t{1} << 25;
 constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
 constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS

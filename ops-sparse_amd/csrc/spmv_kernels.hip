@@ -117,6 +117,9 @@ struct RowBlockParams {
     // chose the staged-gather path for this matrix (its kernels are launched
     // after this one and exit when the word is zero).
     const uint32_t* skip_flag;
+    // Stream kernel: when > 0, the grid is capped and each wave loops over
+    // the blocks tile, tile + block_stride, ... (block_stride = all block waves)
+    int64_t block_stride;
 };
 
 // Loads the block's row offsets relative to its first non-zero into LDS.
@@ -320,6 +323,9 @@ constexpr int kWaveRows = static_cast<int>(kMaxRowsPerBlock);
 // Waves per workgroup of the stream kernels (1 and 2 measured slower on the
 // power-law and fp16 matrices, equal on the Laplacian).
 constexpr int kFlatWaves = 4;
+// Block workgroups of the stream kernel when the staged path may take the
+// matrix instead (multiple of the XCD count).
+constexpr int64_t kStagedFallbackWgs = 2048;
 
 static_assert(kLaneItems == 8, "the reductions are written for 8 slots per lane");
 static_assert(kWaveRows <= 2 * kWave - 1, "two rows per lane");
@@ -1045,22 +1051,25 @@ void SpmvStreamFlatKernel(RowBlockParams p)
         return;
     }
 
-    // Block worker.
+    // Block worker: one block per wave, or (block_stride > 0, capped grid)
+    // blocks tile, tile + block_stride, ...
     const int64_t wg = static_cast<int64_t>(blockIdx.x) - p.task_wgs;
     const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
-    const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
-    if (tile >= p.num_blocks) return;
-    Stage cur = OpenTileFlat<RowT>(p, tile);
-    if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
-    while (cur.valid) {
-        L b;
-        StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
-        StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
-        StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
-        if (cur.last) break;
-        cur.c0 = cur.c1;
-        cur.first = false;
-        ChunkBounds(cur);
+    const int64_t stride = p.block_stride > 0 ? p.block_stride : p.num_blocks;
+    for (int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv; tile < p.num_blocks; tile += stride) {
+        Stage cur = OpenTileFlat<RowT>(p, tile);
+        if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) continue;  // served by tasks
+        carry = 0.0f;
+        while (cur.valid) {
+            L b;
+            StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
+            StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
+            StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
+            if (cur.last) break;
+            cur.c0 = cur.c1;
+            cur.first = false;
+            ChunkBounds(cur);
+        }
     }
 }
 
@@ -2068,8 +2077,17 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             }
             p.task_wgs = static_cast<int32_t>(taskWgs);
             p.task_waves = static_cast<int32_t>(taskWgs * kFlatWaves);
-            if (l.staged) p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
-            const unsigned g = static_cast<unsigned>(taskWgs + (wgs + kXcds - 1) / kXcds * kXcds);
+            int64_t blockWgs = (wgs + kXcds - 1) / kXcds * kXcds;
+            if (l.staged) {
+                // The staged kernels may take this matrix (decided on the
+                // device): a capped grid keeps this launch cheap when it exits.
+                p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
+                if (blockWgs > kStagedFallbackWgs) {
+                    blockWgs = kStagedFallbackWgs;
+                    p.block_stride = blockWgs * kFlatWaves;
+                }
+            }
+            const unsigned g = static_cast<unsigned>(taskWgs + blockWgs);
             if (betaNz) {
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kFlatWaves), 0,
                                    stream_, p);

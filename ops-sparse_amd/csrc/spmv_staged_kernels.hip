@@ -55,10 +55,12 @@ constexpr int kGatherThreads = 1024;                    // pass A
 constexpr int kLongRow = 32;                            // in-tile rows longer than this are summed by a wave
 constexpr int kMaxLong = kTileItems / kLongRow + 1;
 constexpr int kScanIpt = 3;                             // 512 x 3 >= kStageMaxBuckets + 1 run offsets
+constexpr int kStageLanes = 16;                         // staged slots per lane: 8 waves x 64 x 16 >= kTileItems
 
 static_assert(kTileThreads * kSortIpt >= kTileItems, "sort capacity");
 static_assert((kTileItems + 3) / 4 + 1 <= kTileThreads * kGroupSlots, "group slots");
 static_assert(kTileThreads * kScanIpt >= kStageMaxBuckets + 1, "run-offset scan capacity");
+static_assert(kTileThreads * kStageLanes >= kTileItems + kTileWaves, "staging capacity (E/8 rounded up per wave)");
 
 struct StageParams {
     const void* norm;  // normalised row offsets, RowT[rows+2]
@@ -421,48 +423,80 @@ __global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
     const int R = static_cast<int>(r1 - r0);
     const int nb = q.buckets + 1;
 
-    // 1. values and slots of this thread's groups of 4 entries (CSR order)
+    // 1. every load of the tile's first memory round trip goes to registers
+    //    before anything is written to LDS (a store that needs a loaded value
+    //    makes the wave wait for all loads issued before it):
+    //    values and slots of this thread's groups of 4 entries (CSR order),
+    //    the run table (first slot and length of every bucket's run) and the
+    //    tile's row offsets.
     const int64_t g0 = e0 >> 2;
     const int ng = static_cast<int>(((e1 + 3) >> 2) - g0);
-    const Group* vg = reinterpret_cast<const Group*>(q.val);
-    const uint2* pg = reinterpret_cast<const uint2*>(q.perm);
-    const int64_t lastGroup = (q.nnz - 1) >> 2;  // groups past it would read beyond the values
+    // values through a buffer resource from the tile's first group: loads past
+    // the array's last dword return zero (the byte count is rounded up to a
+    // dword, which never leaves the array's 16-byte block)
+    const int64_t vBytes = ((q.nnz - g0 * 4) * static_cast<int64_t>(sizeof(Raw)) + 3) & ~int64_t{3};
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<Raw*>(static_cast<const Raw*>(q.val) + g0 * 4), 0,
+        static_cast<int>(vBytes < 0x7FFFFFFFLL ? vBytes : 0x7FFFFFFFLL), 0x00020000);
+    const uint2* pg = reinterpret_cast<const uint2*>(q.perm) + g0;  // st_perm is padded by 8 slots
     Group gv[kGroupSlots];
     uint2 gp[kGroupSlots];
+#pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        const int64_t g = g0 + gi;
         if (gi < ng) {
-            if (g < lastGroup || ((q.nnz & 3) == 0)) {
-                gv[u] = vg[g];
+            if constexpr (sizeof(Raw) == 4) {
+                gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
             } else {
-                // last, partial group: element loads
-                const Raw* vr = static_cast<const Raw*>(q.val);
-                Raw e[4];
-                for (int k = 0; k < 4; ++k) e[k] = g * 4 + k < q.nnz ? vr[g * 4 + k] : Raw{0};
-                if constexpr (sizeof(Raw) == 4) {
-                    gv[u] = make_uint4(e[0], e[1], e[2], e[3]);
-                } else {
-                    gv[u] = make_uint2(static_cast<uint32_t>(e[0]) | (static_cast<uint32_t>(e[1]) << 16),
-                                       static_cast<uint32_t>(e[2]) | (static_cast<uint32_t>(e[3]) << 16));
-                }
+                gv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, gi * 8, 0, 0));
             }
-            gp[u] = pg[g];  // st_perm is padded by 8 slots
+            gp[u] = pg[gi];
         }
     }
-
-    // 2. run tables: source slot and length of every bucket's run
-    uint32_t cnt[kScanIpt];
+    uint32_t runA[kScanIpt], runB[kScanIpt];
+#pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
-        cnt[u] = 0U;
+        runA[u] = runB[u] = 0U;
         if (s < nb) {
-            const uint32_t a = q.start[t * nb + s];
-            runSrc[s] = a;
-            cnt[u] = q.start[(t + 1) * nb + s] - a;
+            runA[u] = q.start[t * nb + s];
+            runB[u] = q.start[(t + 1) * nb + s];
         }
     }
+    int64_t rowOff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        rowOff[u] = i <= R ? Norm<RowT>(q, r0 + i) : 0;
+    }
+    typedef const __attribute__((address_space(4))) RowT* CRow;  // scalar load
+    const bool headRow = static_cast<int64_t>(reinterpret_cast<CRow>(reinterpret_cast<uintptr_t>(q.norm))[r0]) < e0;
+    asm volatile("" ::: "memory");  // keep the loads above the LDS stores below
+
+    // 2. run offsets (exclusive scan of the run lengths) and the row offsets
+    //    relative to e0, clamped to [0, E], stored after the entry area
+    uint32_t cnt[kScanIpt];
+#pragma unroll
+    for (int u = 0; u < kScanIpt; ++u) {
+        const int s = tid * kScanIpt + u;
+        if (s < nb) runSrc[s] = runA[u];
+        cnt[u] = runB[u] - runA[u];
+    }
+    int32_t* rel = reinterpret_cast<int32_t*>(area + E);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        if (i <= R) {
+            const int64_t v = rowOff[u] - e0;
+            rel[i] = static_cast<int32_t>(v < 0 ? 0 : v > E ? E : v);
+        }
+    }
+    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
+        const int64_t v = Norm<RowT>(q, r0 + i) - e0;
+        rel[i] = static_cast<int32_t>(v < 0 ? 0 : v > E ? E : v);
+    }
     Scan(scanStorage).ExclusiveSum(cnt, cnt);
+#pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
         if (s < nb) runOff[s] = cnt[u];
@@ -470,48 +504,65 @@ __global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
     if (tid == 0) {
         runOff[nb] = static_cast<uint32_t>(E);
         longCount = 0;
+        rel[R + 1] = E;
     }
-    // row offsets relative to e0, clamped to [0, E], after the entry area
-    int32_t* rel = reinterpret_cast<int32_t*>(area + E);
     const bool lastRowInside = r1 < q.rows;
     const int nLoc = R + (lastRowInside ? 1 : 0);
-    for (int i = tid; i <= R; i += kTileThreads) {
-        int64_t v = Norm<RowT>(q, r0 + i) - e0;
-        v = v < 0 ? 0 : v > E ? E : v;
-        rel[i] = static_cast<int32_t>(v);
-    }
-    if (tid == 0) rel[R + 1] = E;
-    const bool headRow = Norm<RowT>(q, r0) < e0;
     __syncthreads();
 
-    // 3. stage the runs: wave w copies slots [w*E/8, (w+1)*E/8) of the tile
+#ifdef SPMV_STAGE_EXP_SKIP_STAGE
+    if (false)
+#endif
+    // 3. stage the runs.  Wave w fills slots [w*E/8, (w+1)*E/8) (at most
+    //    kStageLanes per lane), lanes on consecutive slots, so the loads of one
+    //    run are coalesced.  Every lane issues all its loads before any LDS
+    //    store: one memory round trip per tile, not one per run.
     {
         Raw* xl = reinterpret_cast<Raw*>(area);
         const Raw* xg = static_cast<const Raw*>(q.xg);
         const int i0 = static_cast<int>((static_cast<int64_t>(E) * wv) / kTileWaves);
         const int i1 = static_cast<int>((static_cast<int64_t>(E) * (wv + 1)) / kTileWaves);
-        if (i0 < i1) {
-            int lo = 0, hi = nb - 1;  // last bucket with runOff <= i0
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (static_cast<int>(runOff[mid]) <= i0) lo = mid;
-                else hi = mid - 1;
+        int lo = 0, hi = nb - 1;  // last bucket with runOff <= i0
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (static_cast<int>(runOff[mid]) <= i0) lo = mid;
+            else hi = mid - 1;
+        }
+        int s = lo;
+        // Source slot of each of the lane's values: the run of slot i is
+        // found by advancing s from the previous slot's run (runs only grow
+        // with i).  The index work comes first and the loads after it, as
+        // straight-line code (a load under a branch or a loop makes the wave
+        // wait for it where the branches join); lanes past the range load
+        // slot 0 and discard it.  One register per value: 16-bit values packed
+        // two to a register would make each load wait for its predecessor.
+        int64_t src[kStageLanes];
+#pragma unroll
+        for (int m = 0; m < kStageLanes; ++m) {
+            const int i = i0 + m * kWave + lane;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) s += static_cast<int>(runOff[s + 1]) <= i && s + 1 < nb ? 1 : 0;
+            if (static_cast<int>(runOff[s + 1]) <= i && i < i1) {
+                while (static_cast<int>(runOff[s + 1]) <= i) ++s;  // more than 3 runs in 64 slots
             }
-            int s = lo;
-            int i = i0;
-            while (i < i1) {
-                const int off = static_cast<int>(runOff[s]);
-                int end = static_cast<int>(runOff[s + 1]);
-                end = end < i1 ? end : i1;
-                const int64_t src = static_cast<int64_t>(runSrc[s]) - off;
-                for (int k = i + lane; k < end; k += kWave) xl[k] = xg[src + k];
-                i = end > i ? end : i;
-                ++s;
-            }
+            src[m] = i < i1 ? static_cast<int64_t>(runSrc[s]) + (i - static_cast<int>(runOff[s])) : 0;
+        }
+        uint32_t v[kStageLanes];
+#pragma unroll
+        for (int m = 0; m < kStageLanes; ++m) v[m] = xg[src[m]];
+        asm volatile("" ::: "memory");  // all loads before the first store
+#pragma unroll
+        for (int m = 0; m < kStageLanes; ++m) {
+            const int i = i0 + m * kWave + lane;
+            if (i < i1) xl[i] = static_cast<Raw>(v[m]);
         }
     }
     __syncthreads();
 
+#ifdef SPMV_STAGE_EXP_SKIP_ROWS
+    if (tid < 64) q.head[t] = area[tid];
+    return;
+#endif
     // 4. products a_k * x_col(k) of this thread's groups, then into the area
     float prod[kGroupSlots][4];
     {
@@ -551,8 +602,19 @@ __global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
             longRows[atomicAdd(&longCount, 1)] = loc;
             continue;
         }
-        float sum = 0.0f;
-        for (int k = a; k < b; ++k) sum += area[k];
+        // Neighbouring rows start about one row length apart, so reading them
+        // all from their first entry would put a wave's lanes on the same LDS
+        // banks; each row starts at an offset set by its lane instead (the
+        // order is still fixed per row: row loc is always thread loc % 512).
+        const int len = b - a;
+        int k = len > 0 ? lane % len : 0;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent reads in flight
+#pragma unroll 4
+        for (int c = 0; c < len; ++c) {
+            acc[c & 3] += area[a + k];
+            k = k + 1 == len ? 0 : k + 1;
+        }
+        const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
     }
     __syncthreads();
