@@ -273,7 +273,10 @@ constexpr int64_t kStageTileItems = SPMV_STAGE_TILE_ITEMS;  // rows + entries pe
 constexpr int64_t kStageMinNnz = int64_t{1} << 25;
 constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
 constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS
-constexpr int32_t kStageMaxBuckets = 1024;
+#ifndef SPMV_STAGE_MAX_BUCKETS
+#define SPMV_STAGE_MAX_BUCKETS 1024
+#endif
+constexpr int32_t kStageMaxBuckets = SPMV_STAGE_MAX_BUCKETS;
 constexpr int64_t kStageMinParts = 512;           // pass A workgroups (two per CU at least)
 constexpr int64_t kStagePartTarget = int64_t{1} << 20;  // entries per pass A workgroup beyond that
 // Staged gather decision: the staged path is chosen when the tiles' distinct

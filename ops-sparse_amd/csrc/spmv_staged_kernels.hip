@@ -20,10 +20,13 @@
 //    xg[j] = segment[cl[j]]: a sequential read of cl and a sequential write.
 //  * Pass B (StageTileKernel), one workgroup per tile: copies the tile's run
 //    of every bucket from xg into LDS (runs of neighbouring tiles are
-//    adjacent, so their lines are shared through L2), multiplies each value
-//    a_k (CSR order, coalesced) by its staged x value, and sums the tile's
-//    rows from LDS: short rows one thread each, long rows a wave each.  Rows
-//    crossing tile ends leave partial sums (st_head / st_tail).
+//    adjacent, so their lines are shared through L2; a bit map of run starts
+//    gives every slot its run without a search), multiplies each value a_k
+//    (CSR order, coalesced) by its staged x value, and sums the tile's rows
+//    from LDS: short rows one thread each, long rows a wave each.  Rows
+//    crossing tile ends leave partial sums (st_head / st_tail).  The kernel
+//    is bound by instruction issue as much as by memory, so the per-slot
+//    and per-entry work is kept to a few integer operations.
 //  * Fix-up (StageFixupKernel): one thread per tile whose first row ends in
 //    it combines that row's partial sums in tile order.
 //
@@ -46,21 +49,25 @@ using namespace dev;
 
 constexpr int kXcds = 8;
 constexpr int kWave = 64;
-constexpr int kTileThreads = 512;                       // pass B and the per-tile preprocess kernels
+#ifndef SPMV_STAGE_TILE_THREADS
+#define SPMV_STAGE_TILE_THREADS 512
+#endif
+constexpr int kSortThreads = 512;                       // per-tile preprocess kernels
+constexpr int kTileThreads = SPMV_STAGE_TILE_THREADS;   // pass B
 constexpr int kTileWaves = kTileThreads / kWave;
 constexpr int kTileItems = static_cast<int>(kStageTileItems);
 constexpr int kSortIpt = 16;                            // 512 x 16 = 8192 >= kTileItems keys per tile
-constexpr int kGroupSlots = 4;                          // groups of 4 entries per thread in pass B
 constexpr int kGatherThreads = 1024;                    // pass A
 constexpr int kLongRow = 32;                            // in-tile rows longer than this are summed by a wave
 constexpr int kMaxLong = kTileItems / kLongRow + 1;
-constexpr int kScanIpt = 3;                             // 512 x 3 >= kStageMaxBuckets + 1 run offsets
-constexpr int kStageLanes = 16;                         // staged slots per lane: 8 waves x 64 x 16 >= kTileItems
+constexpr int CeilDiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int kGroupSlots = CeilDiv((kTileItems + 3) / 4 + 1, kTileThreads);  // groups of 4 entries per thread
+constexpr int kScanIpt = CeilDiv(kStageMaxBuckets + 1, kTileThreads);         // run lengths per thread
+constexpr int kStageLanes = CeilDiv(kTileItems, kTileThreads);                // staged 64-slot windows per wave
+constexpr int kWindows = (kTileItems + 63) / 64;        // 64-slot windows of a tile
 
-static_assert(kTileThreads * kSortIpt >= kTileItems, "sort capacity");
-static_assert((kTileItems + 3) / 4 + 1 <= kTileThreads * kGroupSlots, "group slots");
-static_assert(kTileThreads * kScanIpt >= kStageMaxBuckets + 1, "run-offset scan capacity");
-static_assert(kTileThreads * kStageLanes >= kTileItems + kTileWaves, "staging capacity (E/8 rounded up per wave)");
+static_assert(kSortThreads * kSortIpt >= kTileItems, "sort capacity");
+static_assert(kTileWaves * kStageLanes * kWave >= kTileItems, "staging capacity");
 
 struct StageParams {
     const void* norm;  // normalised row offsets, RowT[rows+2]
@@ -144,21 +151,21 @@ __global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
 }
 
 // counts[s*(T+1) + t] = entries of tile t in bucket s (column T is zero).
-__global__ __launch_bounds__(kTileThreads) void StageCountKernel(StageParams q)
+__global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
 {
     __shared__ uint32_t hist[kStageMaxBuckets + 1];
     const int64_t t = blockIdx.x;
     const int nb = q.buckets + 1;
-    for (int s = threadIdx.x; s < nb; s += kTileThreads) hist[s] = 0U;
+    for (int s = threadIdx.x; s < nb; s += kSortThreads) hist[s] = 0U;
     __syncthreads();
     if (t < q.tiles) {
         const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-        for (int64_t k = e0 + threadIdx.x; k < e1; k += kTileThreads) {
+        for (int64_t k = e0 + threadIdx.x; k < e1; k += kSortThreads) {
             atomicAdd(&hist[KeyOf(q, q.col[k]) >> q.wshift], 1U);
         }
     }
     __syncthreads();
-    for (int s = threadIdx.x; s < nb; s += kTileThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
+    for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
 }
 
 // start[t*(S+1) + s] = start_bm[s*(T+1) + t].
@@ -187,12 +194,12 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
 // cl[start(t,s) + rank] = column within the bucket; adds the tile's count of
 // distinct x lines to the metric.
 template <int kEndBit>
-__global__ __launch_bounds__(kTileThreads) void StageSortKernel(StageParams q)
+__global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
 {
-    using Sort = hipcub::BlockRadixSort<uint32_t, kTileThreads, kSortIpt, uint32_t>;
+    using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
     __shared__ typename Sort::TempStorage sortStorage;
     __shared__ uint32_t firstSlot[kStageMaxBuckets + 1];
-    __shared__ uint32_t lastKey[kTileThreads];
+    __shared__ uint32_t lastKey[kSortThreads];
     __shared__ uint32_t lineCount;
     const int64_t t = blockIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
@@ -372,6 +379,13 @@ struct StageVal<ValKind::BF16> {
     }
 };
 
+// Sum over groups of 2^lg consecutive lanes (lg <= 6), fixed butterfly order.
+__device__ __forceinline__ float GroupSum(float v, int lg)
+{
+    for (int m = 1; m < (1 << lg); m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
 __device__ __forceinline__ float WaveSum(float v)
 {
     for (int m = kWave / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
@@ -394,208 +408,248 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
     }
 }
 
-// One workgroup per tile (XCD-contiguous).  LDS: run tables, then one area of
-// kTileItems+2 words that holds the staged x values, then (in place) the
-// products, followed by the tile's row offsets relative to its first entry.
+// One workgroup per tile (XCD-contiguous).  LDS: the run map (runDelta,
+// startBits, firstRank), then one area of kTileItems+8 words that holds the
+// staged x values, then (in place) the products by groups of 4 entries,
+// followed by the tile's row offsets relative to the first group.  Six waves
+// per SIMD: three workgroups per CU, as many as the LDS allows.
 template <typename RowT, ValKind V, OutKind O>
-__global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6))) void StageTileKernel(StageParams q)
 {
     using SV = StageVal<V>;
     using Raw = typename SV::Raw;
     using Group = typename SV::Group;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
-    __shared__ uint32_t runSrc[kStageMaxBuckets + 1];
-    __shared__ uint32_t runOff[kStageMaxBuckets + 2];
-    __shared__ float area[kTileItems + 2];
+    __shared__ uint32_t runDelta[kStageMaxBuckets + 1];
+    __shared__ uint32_t startBits[2 * kWindows];
+    __shared__ uint32_t firstRank[kWindows];
+    __shared__ float4 areaV[(kTileItems + 8 + 3) / 4];
     __shared__ int32_t longRows[kMaxLong];
     __shared__ int longCount;
+    __shared__ int headFlag;
+    float* area = reinterpret_cast<float*>(areaV);
     __shared__ typename Scan::TempStorage scanStorage;
 
-    if (FlagSet(q.flag) == 0U) return;
     const int64_t t = XcdIndex();
     if (t >= q.tiles) return;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wv = tid / kWave;
-    const int64_t r0 = q.tile_row[t], r1 = q.tile_row[t + 1];
-    const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-    const int E = static_cast<int>(e1 - e0);
-    const int R = static_cast<int>(r1 - r0);
     const int nb = q.buckets + 1;
 
-    // 1. every load of the tile's first memory round trip goes to registers
-    //    before anything is written to LDS (a store that needs a loaded value
-    //    makes the wave wait for all loads issued before it):
-    //    values and slots of this thread's groups of 4 entries (CSR order),
-    //    the run table (first slot and length of every bucket's run) and the
-    //    tile's row offsets.
+    // The tile's loads are ordered by what they depend on, so that only two
+    // memory round trips separate the launch from the first product:
+    //   1. the path flag and the tile's corners (scalar loads), and the
+    //      tile's two rows of the run table (first slot of every bucket's run
+    //      in this tile and in the next), which depend on t alone;
+    //   2. row offsets, values and slots (need the corners), then the staged
+    //      x runs (need the run table's scan); the wave waits for the row
+    //      offsets, then for the runs, while the values are still arriving.
+    // Every vector load is an unconditional buffer load (a load under a
+    // branch makes the wave wait for it where the branches join): addresses
+    // outside a buffer read zero, and lanes with nothing to load are masked
+    // afterwards.  Compiler barriers keep the issue order.
+    const uint32_t* startRow = q.start + t * nb;
+    asm volatile("" ::"s"(startRow) : "memory");  // the kernel arguments the run loads need, first
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(startRow), 0, static_cast<int>(2 * nb * sizeof(uint32_t)), 0x00020000);
+    uint32_t runA[kScanIpt], runB[kScanIpt];
+#pragma unroll
+    for (int u = 0; u < kScanIpt; ++u) {
+        const int s = tid * kScanIpt + u;
+        runA[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, s * 4, 0, 0);
+        runB[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, (nb + s) * 4, 0, 0);
+    }
+    asm volatile("" ::: "memory");
+    typedef const __attribute__((address_space(4))) int32_t* CI32;
+    typedef const __attribute__((address_space(4))) int64_t* CI64;
+    const uint32_t flag = FlagSet(q.flag);
+    const int64_t r0 = reinterpret_cast<CI32>(reinterpret_cast<uintptr_t>(q.tile_row))[t];
+    const int64_t r1 = reinterpret_cast<CI32>(reinterpret_cast<uintptr_t>(q.tile_row))[t + 1];
+    const int64_t e0 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t];
+    const int64_t e1 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t + 1];
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    asm volatile("" ::: "memory");
+    if (flag == 0U) return;
+    const int E = static_cast<int>(e1 - e0);
+    const int R = static_cast<int>(r1 - r0);
+
+    // 2a. row offsets of the tile's first 2*kTileThreads+1 rows
+    const int64_t nBytes = (q.rows + 2 - r0) * static_cast<int64_t>(sizeof(RowT));
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<RowT*>(static_cast<const RowT*>(q.norm) + r0), 0,
+        static_cast<int>(nBytes < 0x7FFFFFFFLL ? nBytes : 0x7FFFFFFFLL), 0x00020000);
+    int64_t rowOff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        if constexpr (sizeof(RowT) == 8) {
+            rowOff[u] = static_cast<int64_t>(
+                __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rn, i * 8, 0, 0)));
+        } else {
+            rowOff[u] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(rn, i * 4, 0, 0));
+        }
+    }
+    asm volatile("" ::: "memory");
+    // 2b. values and slots of this thread's groups of 4 entries (CSR order),
+    //     from the tile's first group; loads past an array's last dword read
+    //     zero (byte counts are rounded up to a dword, which never leaves the
+    //     array's 16-byte block; st_perm is padded by 8 slots)
     const int64_t g0 = e0 >> 2;
-    const int ng = static_cast<int>(((e1 + 3) >> 2) - g0);
-    // values through a buffer resource from the tile's first group: loads past
-    // the array's last dword return zero (the byte count is rounded up to a
-    // dword, which never leaves the array's 16-byte block)
+    const int a0 = static_cast<int>(e0 - g0 * 4);  // entry e0's place in its group
+    const int ng = (a0 + E + 3) >> 2;              // groups of 4 entries touching the tile
     const int64_t vBytes = ((q.nnz - g0 * 4) * static_cast<int64_t>(sizeof(Raw)) + 3) & ~int64_t{3};
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<Raw*>(static_cast<const Raw*>(q.val) + g0 * 4), 0,
         static_cast<int>(vBytes < 0x7FFFFFFFLL ? vBytes : 0x7FFFFFFFLL), 0x00020000);
-    const uint2* pg = reinterpret_cast<const uint2*>(q.perm) + g0;  // st_perm is padded by 8 slots
+    const int64_t pBytes = (q.nnz + 8 - g0 * 4) * 2;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        q.perm + g0 * 4, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
     Group gv[kGroupSlots];
     uint2 gp[kGroupSlots];
 #pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        if (gi < ng) {
-            if constexpr (sizeof(Raw) == 4) {
-                gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
-            } else {
-                gv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, gi * 8, 0, 0));
-            }
-            gp[u] = pg[gi];
+        if constexpr (sizeof(Raw) == 4) {
+            gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
+        } else {
+            gv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, gi * 8, 0, 0));
         }
+        gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
     }
-    uint32_t runA[kScanIpt], runB[kScanIpt];
-#pragma unroll
-    for (int u = 0; u < kScanIpt; ++u) {
-        const int s = tid * kScanIpt + u;
-        runA[u] = runB[u] = 0U;
-        if (s < nb) {
-            runA[u] = q.start[t * nb + s];
-            runB[u] = q.start[(t + 1) * nb + s];
-        }
-    }
-    int64_t rowOff[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = tid + u * kTileThreads;
-        rowOff[u] = i <= R ? Norm<RowT>(q, r0 + i) : 0;
-    }
-    typedef const __attribute__((address_space(4))) RowT* CRow;  // scalar load
-    const bool headRow = static_cast<int64_t>(reinterpret_cast<CRow>(reinterpret_cast<uintptr_t>(q.norm))[r0]) < e0;
-    asm volatile("" ::: "memory");  // keep the loads above the LDS stores below
+    asm volatile("" ::: "memory");
 
-    // 2. run offsets (exclusive scan of the run lengths) and the row offsets
-    //    relative to e0, clamped to [0, E], stored after the entry area
+    // 3. the slot -> run map of the tile's bucket-ordered slots, from an
+    //    exclusive scan of the run lengths (waits for the run table only).
+    //    Each scanned word packs (non-empty runs before, slots before); for
+    //    every non-empty run of rank r starting at slot o: runDelta[r] = its
+    //    first xg slot - o, bit o of startBits, and firstRank of each 64-slot
+    //    window whose first slot it holds.  The run of slot i = 64*W + l then
+    //    has rank firstRank[W] + (bits 1..l of the window's 64 start bits).
+    for (int w = tid; w < 2 * kWindows; w += kTileThreads) {
+        startBits[w] = 0U;
+        if (w < kWindows) firstRank[w] = 0U;
+    }
     uint32_t cnt[kScanIpt];
 #pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
-        if (s < nb) runSrc[s] = runA[u];
-        cnt[u] = runB[u] - runA[u];
+        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        cnt[u] = c | (c != 0U ? 0x10000U : 0U);
     }
-    int32_t* rel = reinterpret_cast<int32_t*>(area + E);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = tid + u * kTileThreads;
-        if (i <= R) {
-            const int64_t v = rowOff[u] - e0;
-            rel[i] = static_cast<int32_t>(v < 0 ? 0 : v > E ? E : v);
-        }
-    }
-    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
-        const int64_t v = Norm<RowT>(q, r0 + i) - e0;
-        rel[i] = static_cast<int32_t>(v < 0 ? 0 : v > E ? E : v);
-    }
-    Scan(scanStorage).ExclusiveSum(cnt, cnt);
+    Scan(scanStorage).ExclusiveSum(cnt, cnt);  // its barriers also order the clearing above
 #pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
-        if (s < nb) runOff[s] = cnt[u];
+        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        if (c != 0U) {
+            const uint32_t o = cnt[u] & 0xFFFFU, r = cnt[u] >> 16;
+            runDelta[r] = runA[u] - o;
+            atomicOr(&startBits[o >> 5], 1U << (o & 31U));
+            for (uint32_t w = (o + 63U) >> 6; w * 64U < o + c; ++w) firstRank[w] = r;
+        }
     }
-    if (tid == 0) {
-        runOff[nb] = static_cast<uint32_t>(E);
-        longCount = 0;
-        rel[R + 1] = E;
-    }
+    if (tid == 0) longCount = 0;
     const bool lastRowInside = r1 < q.rows;
     const int nLoc = R + (lastRowInside ? 1 : 0);
     __syncthreads();
 
-#ifdef SPMV_STAGE_EXP_SKIP_STAGE
-    if (false)
-#endif
-    // 3. stage the runs.  Wave w fills slots [w*E/8, (w+1)*E/8) (at most
-    //    kStageLanes per lane), lanes on consecutive slots, so the loads of one
-    //    run are coalesced.  Every lane issues all its loads before any LDS
-    //    store: one memory round trip per tile, not one per run.
+    // 4. stage the runs.  Wave w fills the 64-slot windows of slots
+    //    [w*span, (w+1)*span), lanes on consecutive slots, so the loads of
+    //    one run are coalesced.  The source slot of each of the lane's values
+    //    comes first (independent LDS lookups, the window's words are the
+    //    same for the whole wave), the loads after it; lanes past the range
+    //    load slot 0 and discard it.  One register per value: 16-bit values
+    //    packed two to a register would make each load wait for its
+    //    predecessor.
+    Raw* xl = reinterpret_cast<Raw*>(area);
+    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);  // after the products
     {
-        Raw* xl = reinterpret_cast<Raw*>(area);
         const Raw* xg = static_cast<const Raw*>(q.xg);
-        const int i0 = static_cast<int>((static_cast<int64_t>(E) * wv) / kTileWaves);
-        const int i1 = static_cast<int>((static_cast<int64_t>(E) * (wv + 1)) / kTileWaves);
-        int lo = 0, hi = nb - 1;  // last bucket with runOff <= i0
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (static_cast<int>(runOff[mid]) <= i0) lo = mid;
-            else hi = mid - 1;
-        }
-        int s = lo;
-        // Source slot of each of the lane's values: the run of slot i is
-        // found by advancing s from the previous slot's run (runs only grow
-        // with i).  The index work comes first and the loads after it, as
-        // straight-line code (a load under a branch or a loop makes the wave
-        // wait for it where the branches join); lanes past the range load
-        // slot 0 and discard it.  One register per value: 16-bit values packed
-        // two to a register would make each load wait for its predecessor.
-        int64_t src[kStageLanes];
+        const int span = (E + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
+        const int i0 = __builtin_amdgcn_readfirstlane(wv) * span;  // wave-uniform
+        const int i1 = i0 + span < E ? i0 + span : E;
+        const uint32_t maskLo = lane < 32 ? (2U << lane) - 2U : 0xFFFFFFFEU;   // bits 1..l
+        const uint32_t maskHi = lane < 32 ? 0U : (2U << (lane - 32)) - 1U;
+        uint32_t src[kStageLanes];
 #pragma unroll
         for (int m = 0; m < kStageLanes; ++m) {
-            const int i = i0 + m * kWave + lane;
-#pragma unroll
-            for (int k = 0; k < 3; ++k) s += static_cast<int>(runOff[s + 1]) <= i && s + 1 < nb ? 1 : 0;
-            if (static_cast<int>(runOff[s + 1]) <= i && i < i1) {
-                while (static_cast<int>(runOff[s + 1]) <= i) ++s;  // more than 3 runs in 64 slots
-            }
-            src[m] = i < i1 ? static_cast<int64_t>(runSrc[s]) + (i - static_cast<int>(runOff[s])) : 0;
+            const int w = (i0 >> 6) + m;
+            const int i = (w << 6) + lane;
+            const uint32_t fr = firstRank[w];
+            const uint32_t bLo = startBits[2 * w], bHi = startBits[2 * w + 1];
+            const uint32_t r = fr + static_cast<uint32_t>(__builtin_popcount(bLo & maskLo)) +
+                               static_cast<uint32_t>(__builtin_popcount(bHi & maskHi));
+            const uint32_t d = runDelta[r];  // read by every lane: no load under a branch
+            src[m] = i < i1 ? d + static_cast<uint32_t>(i) : 0U;
         }
         uint32_t v[kStageLanes];
 #pragma unroll
-        for (int m = 0; m < kStageLanes; ++m) v[m] = xg[src[m]];
+        for (int m = 0; m < kStageLanes; ++m) v[m] = xg[src[m]];  // xg holds fewer than 2^32 slots
         asm volatile("" ::: "memory");  // all loads before the first store
+
+        // 5. row offsets relative to e0, clamped to [0, E], after the entry
+        //    area (waits for the row offsets only), then the staged values
+        //    (waits for the runs)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + u * kTileThreads;
+            const int64_t d = rowOff[u] - e0;
+            if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        }
+        if (tid == 0) {
+            rel[R + 1] = a0 + E;
+            headFlag = rowOff[0] < e0 ? 1 : 0;  // the tile's first row started in an earlier tile
+        }
 #pragma unroll
         for (int m = 0; m < kStageLanes; ++m) {
             const int i = i0 + m * kWave + lane;
             if (i < i1) xl[i] = static_cast<Raw>(v[m]);
         }
     }
+    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
+        const int64_t d = Norm<RowT>(q, r0 + i) - e0;
+        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+    }
     __syncthreads();
-
-#ifdef SPMV_STAGE_EXP_SKIP_ROWS
-    if (tid < 64) q.head[t] = area[tid];
-    return;
-#endif
-    // 4. products a_k * x_col(k) of this thread's groups, then into the area
-    float prod[kGroupSlots][4];
+    const bool headRow = headFlag != 0;
+    // 6. products a_k * x(slot_k) in registers, then into the area by groups
+    //    of 4 (entry e0 at a0).  The tile's two edge groups also hold entries
+    //    of the neighbouring tiles: their slots are other tiles' (still
+    //    inside the area) and their products are replaced by zero.
+    float4 prod[kGroupSlots];
     {
-        const Raw* xl = reinterpret_cast<const Raw*>(area);
+        const Raw* xlr = reinterpret_cast<const Raw*>(area);
+#pragma unroll
         for (int u = 0; u < kGroupSlots; ++u) {
             const int gi = tid + u * kTileThreads;
+            float pr[4];
+#pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
-                const int64_t e = (g0 + gi) * 4 + k;
-                const bool in = gi < ng && e >= e0 && e < e1;
-                // entries of the neighbouring tiles in the edge groups hold other tiles' slots
-                const int slot = in ? static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU) : 0;
-                prod[u][k] = in ? SV::ToF(SV::Get(gv[u], k)) * SV::ToF(xl[slot]) : 0.0f;
+                const int slot = static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU);
+                pr[k] = SV::ToF(SV::Get(gv[u], k)) * SV::ToF(xlr[slot]);
             }
+            const int lo = a0 - gi * 4, hi = a0 + E - gi * 4;  // entries [lo, hi) of the group are the tile's
+            if (lo > 0 || hi < 4) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) pr[k] = k >= lo && k < hi ? pr[k] : 0.0f;
+            }
+            prod[u] = make_float4(pr[0], pr[1], pr[2], pr[3]);
         }
     }
     __syncthreads();
+#pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        if (gi < ng) {
-            for (int k = 0; k < 4; ++k) {
-                const int64_t e = (g0 + gi) * 4 + k;
-                if (e >= e0 && e < e1) area[e - e0] = prod[u][k];
-            }
-        }
+        if (gi < ng) areaV[gi] = prod[u];
     }
     __syncthreads();
 
-    // 5. rows: short ones by one thread, long ones queued for a wave
-    float alpha, beta;
-    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    // 7. rows: short ones by one thread, long ones queued for a wave
     const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
-    const bool tailHasEntries = lastRowInside && rel[R] < E;
+    const bool tailHasEntries = lastRowInside && rel[R] < a0 + E;
     for (int loc = tid; loc < nLoc; loc += kTileThreads) {
         const int a = rel[loc], b = rel[loc + 1];
         if (b - a > kLongRow) {
@@ -605,7 +659,7 @@ __global__ __launch_bounds__(kTileThreads) void StageTileKernel(StageParams q)
         // Neighbouring rows start about one row length apart, so reading them
         // all from their first entry would put a wave's lanes on the same LDS
         // banks; each row starts at an offset set by its lane instead (the
-        // order is still fixed per row: row loc is always thread loc % 512).
+        // order is still fixed per row: row loc is always thread loc % kTileThreads).
         const int len = b - a;
         int k = len > 0 ? lane % len : 0;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent reads in flight
@@ -701,7 +755,7 @@ unsigned XcdGrid(int64_t n) { return static_cast<unsigned>((n + kXcds - 1) / kXc
 template <int kEndBit>
 void LaunchSort(const StageParams& q, hipStream_t s)
 {
-    hipLaunchKernelGGL((StageSortKernel<kEndBit>), dim3(static_cast<unsigned>(q.tiles)), dim3(kTileThreads), 0, s, q);
+    hipLaunchKernelGGL((StageSortKernel<kEndBit>), dim3(static_cast<unsigned>(q.tiles)), dim3(kSortThreads), 0, s, q);
 }
 
 template <typename RowT>
@@ -712,7 +766,7 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     const int64_t T = L.st_tiles;
     hipLaunchKernelGGL((StageTileSplitKernel<RowT>), dim3(static_cast<unsigned>((T + 1 + 255) / 256)), dim3(256), 0,
                        s, q);
-    hipLaunchKernelGGL(StageCountKernel, dim3(static_cast<unsigned>(T + 1)), dim3(kTileThreads), 0, s, q);
+    hipLaunchKernelGGL(StageCountKernel, dim3(static_cast<unsigned>(T + 1)), dim3(kSortThreads), 0, s, q);
     const int64_t cells = static_cast<int64_t>(L.st_buckets + 1) * (T + 1);
     void* temp = reinterpret_cast<void*>(
         (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, L.st_scan_offset)) + 255) & ~uintptr_t{255});
