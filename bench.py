@@ -27,6 +27,7 @@ import time
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "ops-sparse_amd"))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -165,6 +166,11 @@ def measure(w, steps, warmup, flush_buf):
     p1.record(stream)
     torch.cuda.synchronize()
     pre_ms = p0.elapsed_time(p1)
+    # the path Preprocess chose: staged-gather flag in the workspace header
+    staged = False
+    if w.trans == "N" and plan.workspace is not None and plan.workspace.numel() >= 192:
+        head = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+        staged = bool(head[16] & 0xFFFFFFFF)
 
     sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
 
@@ -208,7 +214,8 @@ def measure(w, steps, warmup, flush_buf):
     warm = _timed(stream, plan.run, steps)
     return dict(median_ms=ev, p90_ms=ev_p90, dirty_flush_ms=ev_dirty, paired_ms=statistics.median(diffs), paired_min_ms=min(diffs),
                 paired_max_ms=max(diffs), wall_ms_per_step=wall, warm_ms=warm, preprocess_ms=pre_ms,
-                workspace_bytes=plan.buffer_size)
+                workspace_bytes=plan.buffer_size, path=("staged gather" if staged else
+                                                        "row kernels" if w.trans == "N" else "transpose"))
 
 
 def graph_ms(w, launches=1000, replays=5):
@@ -403,6 +410,22 @@ def cpu_baseline(w, seconds):
             "cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
 
 
+LINE_RATE = 64e9  # 128-byte lines per second from the MALL (random x gathers), measured on MI355X
+
+
+def ceilings(w, nbytes, path):
+    """Lower bounds on one SpMV's time (ms): algorithmic bytes at 8 TB/s; one
+    MALL line per x gather at the measured line rate (the bound of gathering
+    x straight from memory when x exceeds an XCD's L2); and, on the staged
+    path, its own design traffic at 8 TB/s."""
+    from ops_sparse.workloads import staged_bytes
+
+    c = {"algorithmic_hbm": nbytes / (HBM_PEAK_GBS * 1e6), "random_line_gathers": w.nnz / LINE_RATE * 1e3}
+    if path == "staged gather":
+        c["staged_traffic_hbm"] = staged_bytes(w) / (HBM_PEAK_GBS * 1e6)
+    return c
+
+
 def load_traffic(name):
     path = os.path.join(REPO, "profiles", f"traffic_{name}.json")
     if os.path.exists(path):
@@ -442,6 +465,10 @@ def main():
                  algorithmic_bytes=nbytes, gbs=gbs, frac=gbs / HBM_PEAK_GBS,
                  gflops=flops(w) / (m["median_ms"] * 1e-3) / 1e9,
                  warm_gbs=nbytes / (m["warm_ms"] * 1e-3) / 1e9, **m)
+        r["ceilings_ms"] = ceilings(w, nbytes, m["path"])
+        r["bound"] = "staged traffic at 8 TB/s" if m["path"] == "staged gather" else "hbm"
+        r["frac_of_bound"] = (r["ceilings_ms"]["staged_traffic_hbm"] if m["path"] == "staged gather"
+                              else r["ceilings_ms"]["algorithmic_hbm"]) / m["median_ms"]
         if name == "c1":
             r["graph_ms"] = graph_ms(w)
             r["graph_gbs"] = nbytes / (r["graph_ms"] * 1e-3) / 1e9
@@ -496,7 +523,12 @@ def main():
                    "l2_mall_flushed": True, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(h["frac"], 4), "traffic": load_traffic(HEADLINE),
-                     "kernel": h.get("kernel"), "algorithmic_bytes_per_launch": h["algorithmic_bytes"]},
+                     "kernel": ("StageGatherKernel + StageTileKernel + StageFixupKernel: the staged-gather SpMV "
+                                "(the row kernel launched before them exits at once)"
+                                if h["path"] == "staged gather" else "SpmvStreamFlatKernel"),
+                     "algorithmic_bytes_per_launch": h["algorithmic_bytes"],
+                     "ceilings_ms": {k: round(v, 5) for k, v in h["ceilings_ms"].items()},
+                     "frac_of_path_bound": round(h["frac_of_bound"], 4)},
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
