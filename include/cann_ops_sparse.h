@@ -279,6 +279,23 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
                                 aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX, const void* beta,
                                 aclsparseDnVecDescr_t vecY, aclDataType computeType, aclsparseSpMVAlg_t alg,
                                 void* externalBuffer);
+/* No counterpart in the reference: aclsparseSpMV without a caller workspace,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation).  It calls no
+ * allocator: its partition tables live in a static device array of
+ * ACL_SPARSE_SPMV_NO_ALLOC_MAX_BYTES per GPU, held from library load to process
+ * exit.  Every call rebuilds the row partition (as aclsparseSpMV does without
+ * a matching Preprocess) and runs the row kernels or the transpose path; the
+ * staged-gather path is not used (its tables need Preprocess).  A matrix whose
+ * tables exceed the array returns ACL_SPARSE_STATUS_INSUFFICIENT_RESOURCES.
+ * Calls on one GPU share the array: calls that overlap in time on one GPU
+ * (other streams, other threads) race and must be ordered by the caller.
+ * Launches go to the handle's stream, which must belong to the current device. */
+#define ACL_SPARSE_SPMV_NO_ALLOC_MAX_BYTES (32u * 1024u * 1024u)
+aclsparseStatus_t aclsparseSpMVNoAlloc(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                       aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX,
+                                       const void* beta, aclsparseDnVecDescr_t vecY, aclDataType computeType,
+                                       aclsparseSpMVAlg_t alg);
 
 /* ---------------- SpMVOp (include/cann_ops_sparse.h:2338-2396) ---------------- */
 

@@ -412,6 +412,14 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     return l;
 }
 
+// SpMV into a workspace that scratch() returns (resolved only after the
+// inputs are validated and the layout fits scratchBytes): the tables are
+// rebuilt on every call and the staged path is not used (spmv_host.cpp).
+aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                  aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX, const void* beta,
+                                  aclsparseDnVecDescr_t vecY, aclDataType computeType, aclsparseSpMVAlg_t alg,
+                                  void* (*scratch)(), size_t scratchBytes);
+
 // ---------------------------------------------------------------------------
 // Launcher interface (implemented in spmv_kernels.hip).
 // ---------------------------------------------------------------------------

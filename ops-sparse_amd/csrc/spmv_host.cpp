@@ -382,3 +382,36 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
 }
 
 }  // extern "C"
+
+namespace aclsp {
+
+aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t opA, const void* alpha,
+                                  aclsparseConstSpMatDescr_t matA, aclsparseConstDnVecDescr_t vecX, const void* beta,
+                                  aclsparseDnVecDescr_t vecY, aclDataType computeType, aclsparseSpMVAlg_t alg,
+                                  void* (*scratch)(), size_t scratchBytes)
+{
+    aclsparseStatus_t st = ValidateInputs(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    st = ValidateStorage(opA, matA, vecX, vecY);
+    if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
+    const uint64_t outLen = IsTranspose(opA) ? matA->cols : matA->rows;
+    if (outLen == 0U) return ACL_SPARSE_STATUS_SUCCESS;
+    // the layout without the staged-gather tables (they need Preprocess)
+    const SpmvLayout layout = ComputeLayout(matA->rows, matA->cols, matA->nnz, matA->ptr_type, computeType,
+                                            IsTranspose(opA), true, 0U);
+    if (layout.total > scratchBytes) return ACL_SPARSE_STATUS_INSUFFICIENT_RESOURCES;
+    void* ws = scratch();
+    if (ws == nullptr) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    SpmvLaunch l = MakeLaunch(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg, ws);
+    l.layout = layout;
+    l.staged = 0;
+    void* stream = HipStreamOf(handle);
+    (void)hipGetLastError();
+    if (matA->rows > 0U && LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    if (LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
+        return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+    }
+    return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+}  // namespace aclsp

@@ -153,6 +153,7 @@ SIGNATURES = {
     "aclsparseSpMVGetBufferSize": [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_sz)],
     "aclsparseSpMVPreprocess": [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp],
     "aclsparseSpMV": [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp],
+    "aclsparseSpMVNoAlloc": [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32],
     "aclsparseSpMVOp_bufferSize": [_vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_sz)],
     "aclsparseSpMVOp_createDescr": [_vp, _pvp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _vp],
     "aclsparseSpMVOp_destroyDescr": [_vp],

@@ -16,7 +16,7 @@ REPO_ROOT = os.path.dirname(PKG_ROOT)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 HEADER = os.path.join(REPO_ROOT, "include", "cann_ops_sparse.h")
 SOURCES = ["handle_descr.cpp", "spmv_host.cpp", "spmv_kernels.hip", "spmv_staged_kernels.hip", "spmv_op_host.cpp",
-           "spmv_op_kernels.hip", "spmm_op_host.cpp", "spmm_op_kernels.hip"]
+           "spmv_op_kernels.hip", "spmm_op_host.cpp", "spmm_op_kernels.hip", "spmv_noalloc.hip"]
 OUT = os.path.join(PKG_ROOT, "lib", "libaclsparse_hip.so")
 OBJ_DIR = os.path.join(PKG_ROOT, "lib", "obj")
 
