@@ -304,6 +304,41 @@ inline bool StageEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t v
     return (cols + w - 1) / w <= static_cast<uint64_t>(kStageMaxBuckets);
 }
 
+// ---------------------------------------------------------------------------
+// Column-bucketed transpose (fp32 values and compute, unit strides).  The
+// CSC column pass gathers each product from a CSR-ordered array as large as
+// the matrix: one MALL line per 4-byte product.  Instead, Preprocess cuts the
+// matrix into the same merge-path tiles and buckets every entry by its
+// column (W columns per bucket, W chosen so that a bucket's entries fit one
+// workgroup's LDS); pass 1 writes each tile's products as runs into bucket
+// order, pass 2 loads one bucket's products into LDS, places them in column
+// order (each entry's place, from the CSC pattern, is a Preprocess table) and
+// sums every column in row order.  It reuses the staged sections: st_perm is
+// each entry's slot in its tile's bucket-ordered runs, st_cl each slot's
+// place within its bucket's column-ordered products.
+// ---------------------------------------------------------------------------
+constexpr int64_t kBtMinNnz = int64_t{1} << 20;
+constexpr int32_t kBtMaxBuckets = 2048;
+constexpr int64_t kBtRegionTarget = 12288;  // mean entries per bucket the width aims at
+constexpr int64_t kBtRegionCap = 16384;     // entries per bucket that pass 2's LDS holds
+
+// Columns per bucket (a power of two): about kBtRegionTarget entries each.
+inline int32_t BtBucketShift(uint64_t cols, uint64_t nnz)
+{
+    const uint64_t target = nnz > 0 ? static_cast<uint64_t>(kBtRegionTarget) * cols / nnz : 65536U;
+    int32_t shift = 6;
+    while (shift < 16 && (uint64_t{2} << shift) <= target) ++shift;
+    return shift;
+}
+
+inline bool BtEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t valueBytes)
+{
+    if (valueBytes != 4U || rows == 0U || cols == 0U) return false;
+    if (nnz < static_cast<uint64_t>(kBtMinNnz) || nnz > 0x7FFFFFFFULL) return false;
+    const uint64_t w = uint64_t{1} << BtBucketShift(cols, nnz);
+    return (cols + w - 1) / w <= static_cast<uint64_t>(kBtMaxBuckets);
+}
+
 // Radix-sort temporary storage for the CSC build (implemented in spmv_kernels.hip).
 size_t CscSortTempBytes(int64_t nnz, uint32_t posBytes);
 
@@ -375,6 +410,28 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.row_delta_offset = AlignUp(l.group_row_offset + static_cast<size_t>(l.row_groups) * sizeof(int32_t));
             l.total = AlignUp(l.row_delta_offset + static_cast<size_t>(l.row_groups) * kRowGroup);
         }
+    }
+    if (transpose && l.csc && BtEligible(rows, cols, nnz, stageValueBytes)) {
+        l.staged = true;
+        l.st_value_bytes = 4;
+        l.st_wshift = BtBucketShift(cols, nnz);
+        const uint64_t w = uint64_t{1} << l.st_wshift;
+        l.st_buckets = static_cast<int32_t>((cols + w - 1) / w);
+        const uint64_t t = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+        l.st_tiles = static_cast<int64_t>(t);
+        const size_t cells = static_cast<size_t>(l.st_buckets + 1) * static_cast<size_t>(t + 1);
+        const size_t n8 = static_cast<size_t>(nnz) + 8;
+        l.st_tile_row_offset = AlignUp(l.total);
+        l.st_tile_nnz_offset = AlignUp(l.st_tile_row_offset + static_cast<size_t>(t + 1) * sizeof(int32_t));
+        l.st_counts_offset = AlignUp(l.st_tile_nnz_offset + static_cast<size_t>(t + 1) * sizeof(int64_t));
+        l.st_start_bm_offset = AlignUp(l.st_counts_offset + cells * sizeof(uint32_t));
+        l.st_start_offset = AlignUp(l.st_start_bm_offset + cells * sizeof(uint32_t));
+        l.st_scan_offset = AlignUp(l.st_start_offset + cells * sizeof(uint32_t));
+        l.st_scan_bytes = StageScanTempBytes(static_cast<int64_t>(cells));
+        l.st_perm_offset = AlignUp(l.st_scan_offset + l.st_scan_bytes + 256);  // re-aligned to 256 at use
+        l.st_cl_offset = AlignUp(l.st_perm_offset + n8 * sizeof(uint16_t));
+        l.st_metric_offset = AlignUp(l.st_cl_offset + n8 * sizeof(uint16_t));
+        l.total = AlignUp(l.st_metric_offset + sizeof(uint64_t));
     }
     if (!transpose && StageEligible(rows, cols, nnz, stageValueBytes)) {
         l.staged = true;

@@ -1767,6 +1767,7 @@ struct CscParams {
     int64_t cols;
     int32_t lg;  // log2 lanes per column
     int32_t conj;
+    const uint32_t* skip_flag;  // non-null: exit when it reads 1 (the column-bucketed kernels run instead)
     Scalars s;
 };
 
@@ -1798,6 +1799,7 @@ __global__ __launch_bounds__(kThreads) void CscProductKernel(CscParams q)
     using Acc = typename AccOf<A>::T;
     using ValT = typename ValOf<V>::T;
     static_assert(kRowGroup == 4 * kWave, "a group is one wave of 4 entries per lane");
+    if (q.skip_flag != nullptr && ConstLoad<uint32_t>(q.skip_flag, 0) != 0U) return;
     __shared__ ValT sx[kThreads / kWave][kRowGroup];
     const ValT* val = static_cast<const ValT*>(q.val);
     const ValT* x = static_cast<const ValT*>(q.x);
@@ -1893,6 +1895,7 @@ template <typename RowT, ValKind V, OutKind O, AccKind A>
 __global__ __launch_bounds__(kThreads) void SpmvCscGatherKernel(CscParams q)
 {
     using Acc = typename AccOf<A>::T;
+    if (q.skip_flag != nullptr && ConstLoad<uint32_t>(q.skip_flag, 0) != 0U) return;
     const int lg = q.lg;
     const int g = 1 << lg;
     const int64_t c = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> lg;
@@ -2143,6 +2146,8 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         q.cols = n;
         q.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
         q.s = p.s;
+        // the column-bucketed kernels (launched after these) run instead when Preprocess chose them
+        q.skip_flag = l.staged ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
         // lanes per column: the power of two nearest below the mean column length, <= 64
         const int64_t mean = l.nnz / n;
         int lg = 0;
@@ -2183,6 +2188,7 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 c.base = 0;
                 c.task_wgs = 0;
                 c.task_waves = 0;
+                c.skip_flag = q.skip_flag;
                 const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
                 const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
                 const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
@@ -2516,11 +2522,17 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (l.rowptr64) {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int64_t>), dim3(grid), dim3(kThreads), 0, s, p);
-        if (l.layout.csc) return BuildCsc<int64_t>(l, s);
+        if (l.layout.csc) {
+            if (BuildCsc<int64_t>(l, s) != 0) return 1;
+            return l.staged ? LaunchStagedPreprocess(l, stream) : 0;
+        }
         if (l.layout.tasks && BuildTasks<int64_t>(l, s) != 0) return 1;
     } else {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
-        if (l.layout.csc) return BuildCsc<int32_t>(l, s);
+        if (l.layout.csc) {
+            if (BuildCsc<int32_t>(l, s) != 0) return 1;
+            return l.staged ? LaunchStagedPreprocess(l, stream) : 0;
+        }
         if (l.layout.tasks && BuildTasks<int32_t>(l, s) != 0) return 1;
     }
     if (l.staged) return LaunchStagedPreprocess(l, stream);

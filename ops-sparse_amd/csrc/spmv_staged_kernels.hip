@@ -94,6 +94,11 @@ struct StageParams {
     unsigned long long* metric;
     uint32_t* flag;
     int64_t part;  // pass A: bucket-ordered slots per workgroup
+    // column-bucketed transpose
+    const void* colptr;   // RowT[cols+1], column offsets of the CSC pattern
+    const void* csc_pos;  // RowT[nnz], CSR index of each entry in column order
+    int32_t* inv;         // int32[nnz], column-order place of each CSR entry
+    float* prod;          // float[nnz+8], products in bucket order
     Scalars s;
 };
 
@@ -707,6 +712,411 @@ __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
     StoreRow<O, AccKind::F32>(static_cast<OutT*>(q.y), r0, sum, alpha, beta, betaNz);
 }
 
+// ----------------------- column-bucketed transpose ---------------------------
+//
+// y = alpha * A^T x + beta * y, fp32 values and compute (BtEligible).  The
+// tiles are the staged path's merge-path tiles; bucket b holds the columns
+// [b*W, (b+1)*W), bucket S the entries outside the rows' range or whose
+// column is outside [0, cols).  Preprocess (pattern only, after the CSC
+// build): per (bucket, tile) counts and their bucket-major scan, each entry's
+// slot in its tile's bucket-ordered runs (st_perm), and, for each slot, its
+// place among its bucket's entries in column order (st_cl, from the CSC
+// pattern).  The bucket-major scan gives bucket b the slots
+// [colptr[b*W], colptr[(b+1)*W]): the same count, and the same start, as its
+// columns' CSC range.
+//  * Pass 1 (BtScatterKernel), one workgroup per tile: the products
+//    a_k * x[row(k)] (values in CSR order, coalesced; each row's x spread
+//    over its entries in LDS), placed in LDS at their slots, then written as
+//    the tile's runs; runs of neighbouring tiles are adjacent, so their
+//    partial lines merge in L2.
+//  * Pass 2 (BtColumnKernel), one workgroup per bucket: its products
+//    (sequential) go to LDS at their column-order places, then every column
+//    is summed in row order, the order the reference's ALG2 accumulates in
+//    (sparse/spmv/README.md:252), and y = alpha*sum + beta*y.
+// Counterpart: the transpose of sparse/spmv/arch35/spmv_kernel.cpp:579-668,
+// which scatters a_k * x[row] into y with atomics.
+
+constexpr int kBtScanIpt = CeilDiv(kBtMaxBuckets + 1, kTileThreads);  // run lengths per thread
+constexpr int kBtColThreads = 512;                                     // pass 2
+constexpr int kBtLongCol = 64;  // columns longer than this are summed by a wave
+constexpr int kBtMaxLongCols = static_cast<int>(kBtRegionCap) / (kBtLongCol + 1) + 1;
+
+// Bucket of entry k (S: outside the rows' range or a column outside [0, cols)).
+__device__ __forceinline__ uint32_t BtKey(const StageParams& q, int64_t k, int64_t first, int64_t last)
+{
+    if (k < first || k >= last) return static_cast<uint32_t>(q.buckets);
+    return KeyOf(q, q.col[k]) >> q.wshift;
+}
+
+// inv[csc_pos[j]] = j.
+template <typename RowT>
+__global__ __launch_bounds__(256) void BtInvertKernel(StageParams q)
+{
+    const int64_t j = blockIdx.x * int64_t{256} + threadIdx.x;
+    if (j >= q.nnz) return;
+    q.inv[static_cast<int64_t>(static_cast<const RowT*>(q.csc_pos)[j])] = static_cast<int32_t>(j);
+}
+
+// counts[s*(T+1) + t] = entries of tile t in bucket s (column T is zero).
+template <typename RowT>
+__global__ __launch_bounds__(kSortThreads) void BtCountKernel(StageParams q)
+{
+    __shared__ uint32_t hist[kBtMaxBuckets + 1];
+    const int64_t t = blockIdx.x;
+    const int nb = q.buckets + 1;
+    for (int s = threadIdx.x; s < nb; s += kSortThreads) hist[s] = 0U;
+    __syncthreads();
+    if (t < q.tiles) {
+        const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
+        const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
+        for (int64_t k = e0 + threadIdx.x; k < e1; k += kSortThreads) atomicAdd(&hist[BtKey(q, k, first, last)], 1U);
+    }
+    __syncthreads();
+    for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
+}
+
+// Per tile: stable sort of the entries by bucket; perm[k] = slot of entry k
+// in the tile's bucket-ordered runs; cl[start(t,b) + rank] = the entry's
+// place in bucket b's column-ordered products.
+template <typename RowT>
+__global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
+{
+    using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
+    __shared__ typename Sort::TempStorage sortStorage;
+    __shared__ uint32_t firstSlot[kBtMaxBuckets + 1];
+    __shared__ uint32_t lastKey[kSortThreads];
+    const int64_t t = blockIdx.x;
+    const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
+    const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
+    const int n = static_cast<int>(e1 - e0);
+    uint32_t keys[kSortIpt], vals[kSortIpt];
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        keys[u] = i < n ? BtKey(q, e0 + i, first, last) : 0xFFFFU;
+        vals[u] = static_cast<uint32_t>(i);
+    }
+    Sort(sortStorage).Sort(keys, vals, 0, 16);
+    lastKey[threadIdx.x] = keys[kSortIpt - 1];
+    __syncthreads();
+    uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        if (i < n) {
+            if (keys[u] != prev) firstSlot[keys[u]] = static_cast<uint32_t>(i);
+            q.perm[e0 + vals[u]] = static_cast<uint16_t>(i);
+        }
+        prev = keys[u];
+    }
+    __syncthreads();
+    const int nb = q.buckets + 1;
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    for (int u = 0; u < kSortIpt; ++u) {
+        const int i = threadIdx.x * kSortIpt + u;
+        if (i < n) {
+            const uint32_t b = keys[u];
+            const uint32_t slot = q.start[t * nb + b] + (static_cast<uint32_t>(i) - firstSlot[b]);
+            uint32_t place = 0U;
+            if (b < static_cast<uint32_t>(q.buckets)) {
+                place = static_cast<uint32_t>(static_cast<int64_t>(q.inv[e0 + vals[u]]) -
+                                              static_cast<int64_t>(colptr[static_cast<int64_t>(b) << q.wshift]));
+            }
+            q.cl[slot] = static_cast<uint16_t>(place);
+        }
+    }
+}
+
+// The path decision: the column-bucketed kernels when every bucket's
+// entries fit pass 2's LDS.
+template <typename RowT>
+__global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
+{
+    __shared__ int ok;
+    if (threadIdx.x == 0) ok = 1;
+    __syncthreads();
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    const int64_t w = int64_t{1} << q.wshift;
+    for (int64_t b = threadIdx.x; b < q.buckets; b += 256) {
+        const int64_t c0 = b * w;
+        const int64_t c1 = c0 + w < q.cols ? c0 + w : q.cols;
+        if (static_cast<int64_t>(colptr[c1]) - static_cast<int64_t>(colptr[c0]) > kBtRegionCap) ok = 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *q.flag = ok != 0 ? 1U : 0U;
+}
+
+// Pass 1: products of one tile into its runs (see above).
+template <typename RowT>
+__global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
+{
+    using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
+    __shared__ uint32_t runDelta[kBtMaxBuckets + 1];
+    __shared__ uint32_t startBits[2 * kWindows];
+    __shared__ uint32_t firstRank[kWindows];
+    __shared__ float4 areaV[(kTileItems + 8 + 3) / 4];
+    __shared__ int32_t longRows[kMaxLong];
+    __shared__ int longCount;
+    __shared__ typename Scan::TempStorage scanStorage;
+    float* area = reinterpret_cast<float*>(areaV);
+
+    const int64_t t = XcdIndex();
+    if (t >= q.tiles) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid / kWave;
+    const int nb = q.buckets + 1;
+
+    // 1. the tile's two rows of the run table (depend on t alone), then the
+    //    flag and the tile's corners (scalar loads)
+    const uint32_t* startRow = q.start + t * nb;
+    asm volatile("" ::"s"(startRow) : "memory");
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(startRow), 0, static_cast<int>(2 * nb * sizeof(uint32_t)), 0x00020000);
+    uint32_t runA[kBtScanIpt], runB[kBtScanIpt];
+#pragma unroll
+    for (int u = 0; u < kBtScanIpt; ++u) {
+        const int s = tid * kBtScanIpt + u;
+        runA[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, s * 4, 0, 0);
+        runB[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, (nb + s) * 4, 0, 0);
+    }
+    asm volatile("" ::: "memory");
+    typedef const __attribute__((address_space(4))) int32_t* CI32;
+    typedef const __attribute__((address_space(4))) int64_t* CI64;
+    const uint32_t flag = FlagSet(q.flag);
+    const int64_t r0 = reinterpret_cast<CI32>(reinterpret_cast<uintptr_t>(q.tile_row))[t];
+    const int64_t r1 = reinterpret_cast<CI32>(reinterpret_cast<uintptr_t>(q.tile_row))[t + 1];
+    const int64_t e0 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t];
+    const int64_t e1 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t + 1];
+    asm volatile("" ::: "memory");
+    if (flag == 0U) return;
+    const int E = static_cast<int>(e1 - e0);
+    const int R = static_cast<int>(r1 - r0);
+    const bool lastRowInside = r1 < q.rows;
+    const int nLoc = R + (lastRowInside ? 1 : 0);  // rows with entries in the tile (the last may continue)
+
+    // 2. row offsets and x of the tile's first 2*kTileThreads rows, values
+    //    and slots of this thread's groups of 4 entries (unconditional buffer
+    //    loads; out-of-range addresses read zero)
+    const int64_t nBytes = (q.rows + 2 - r0) * static_cast<int64_t>(sizeof(RowT));
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<RowT*>(static_cast<const RowT*>(q.norm) + r0), 0,
+        static_cast<int>(nBytes < 0x7FFFFFFFLL ? nBytes : 0x7FFFFFFFLL), 0x00020000);
+    const int64_t xBytes = (q.rows - r0) * 4;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(static_cast<const float*>(q.x) + r0), 0,
+        static_cast<int>(xBytes < 0x7FFFFFFFLL ? xBytes : 0x7FFFFFFFLL), 0x00020000);
+    int64_t rowOff[2];
+    float xRow[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        if constexpr (sizeof(RowT) == 8) {
+            rowOff[u] = static_cast<int64_t>(
+                __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rn, i * 8, 0, 0)));
+        } else {
+            rowOff[u] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(rn, i * 4, 0, 0));
+        }
+        xRow[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, i * 4, 0, 0));
+    }
+    const int64_t g0 = e0 >> 2;
+    const int a0 = static_cast<int>(e0 - g0 * 4);  // entry e0's place in its group
+    const int ng = (a0 + E + 3) >> 2;              // groups of 4 entries touching the tile
+    const int64_t vBytes = (q.nnz - g0 * 4) * 4;
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(static_cast<const float*>(q.val) + g0 * 4), 0,
+        static_cast<int>(vBytes < 0x7FFFFFFFLL ? vBytes : 0x7FFFFFFFLL), 0x00020000);
+    const int64_t pBytes = (q.nnz + 8 - g0 * 4) * 2;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        q.perm + g0 * 4, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
+    uint4 gv[kGroupSlots];
+    uint2 gp[kGroupSlots];
+#pragma unroll
+    for (int u = 0; u < kGroupSlots; ++u) {
+        const int gi = tid + u * kTileThreads;
+        gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
+        gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+    }
+    asm volatile("" ::: "memory");
+
+    // 3. the slot -> run map (as in the staged tile kernel): runDelta[r] =
+    //    first destination slot of the run of rank r - its first tile slot
+    for (int w = tid; w < 2 * kWindows; w += kTileThreads) {
+        startBits[w] = 0U;
+        if (w < kWindows) firstRank[w] = 0U;
+    }
+    uint32_t cnt[kBtScanIpt];
+#pragma unroll
+    for (int u = 0; u < kBtScanIpt; ++u) {
+        const int s = tid * kBtScanIpt + u;
+        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        cnt[u] = c | (c != 0U ? 0x10000U : 0U);
+    }
+    Scan(scanStorage).ExclusiveSum(cnt, cnt);  // its barriers also order the clearing above
+#pragma unroll
+    for (int u = 0; u < kBtScanIpt; ++u) {
+        const int s = tid * kBtScanIpt + u;
+        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        if (c != 0U) {
+            const uint32_t o = cnt[u] & 0xFFFFU, r = cnt[u] >> 16;
+            runDelta[r] = runA[u] - o;
+            atomicOr(&startBits[o >> 5], 1U << (o & 31U));
+            for (uint32_t w = (o + 63U) >> 6; w * 64U < o + c; ++w) firstRank[w] = r;
+        }
+    }
+    // row offsets relative to the first group, clamped to the tile, after the entry area
+    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        const int64_t d = rowOff[u] - e0;
+        if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+    }
+    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
+        const int64_t d = Norm<RowT>(q, r0 + i) - e0;
+        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+    }
+    if (tid == 0) {
+        rel[R + 1] = a0 + E;
+        longCount = 0;
+    }
+    __syncthreads();
+
+    // 4. each row's x over its entries (area, by entry), long rows by a wave
+    for (int loc = tid, u = 0; loc < nLoc; loc += kTileThreads, ++u) {
+        const int a = rel[loc], b = rel[loc + 1];
+        if (b - a > kLongRow) {
+            longRows[atomicAdd(&longCount, 1)] = loc;
+            continue;
+        }
+        const float xv = u == 0 ? xRow[0] : u == 1 ? xRow[1] : static_cast<const float*>(q.x)[r0 + loc];
+        for (int k = a; k < b; ++k) area[k] = xv;
+    }
+    __syncthreads();
+    const int nLong = longCount;
+    for (int li = wv; li < nLong; li += kTileWaves) {
+        const int loc = longRows[li];
+        const int a = rel[loc], b = rel[loc + 1];
+        const float xv = static_cast<const float*>(q.x)[r0 + loc];
+        for (int k = a + lane; k < b; k += kWave) area[k] = xv;
+    }
+    __syncthreads();
+
+    // 5. products in registers, then at their slots; the tile's two edge
+    //    groups also hold entries of the neighbouring tiles, which are skipped
+    float pr[kGroupSlots][4];
+#pragma unroll
+    for (int u = 0; u < kGroupSlots; ++u) {
+        const int gi = tid + u * kTileThreads;
+        const float4 xv4 = gi < ng ? areaV[gi] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pr[u][0] = __uint_as_float(gv[u].x) * xv4.x;
+        pr[u][1] = __uint_as_float(gv[u].y) * xv4.y;
+        pr[u][2] = __uint_as_float(gv[u].z) * xv4.z;
+        pr[u][3] = __uint_as_float(gv[u].w) * xv4.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kGroupSlots; ++u) {
+        const int gi = tid + u * kTileThreads;
+        const int lo = a0 - gi * 4, hi = a0 + E - gi * 4;  // entries [lo, hi) of the group are the tile's
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
+            const int slot = static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU);
+            if (k >= lo && k < hi) area[slot] = pr[u][k];
+        }
+    }
+    __syncthreads();
+
+    // 6. the tile's runs: slot i of the 64-slot windows of wave w goes to
+    //    prod[runDelta[run(i)] + i]
+    {
+        const int span = (E + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
+        const int i0 = __builtin_amdgcn_readfirstlane(wv) * span;
+        const int i1 = i0 + span < E ? i0 + span : E;
+        const uint32_t maskLo = lane < 32 ? (2U << lane) - 2U : 0xFFFFFFFEU;
+        const uint32_t maskHi = lane < 32 ? 0U : (2U << (lane - 32)) - 1U;
+#pragma unroll
+        for (int m = 0; m < kStageLanes; ++m) {
+            const int w = (i0 >> 6) + m;
+            const int i = (w << 6) + lane;
+            const uint32_t fr = firstRank[w];
+            const uint32_t bLo = startBits[2 * w], bHi = startBits[2 * w + 1];
+            const uint32_t r = fr + static_cast<uint32_t>(__builtin_popcount(bLo & maskLo)) +
+                               static_cast<uint32_t>(__builtin_popcount(bHi & maskHi));
+            const uint32_t d = runDelta[r];
+            const float v = area[i < i1 ? i : 0];
+            if (i < i1) q.prod[d + static_cast<uint32_t>(i)] = v;
+        }
+    }
+}
+
+// Pass 2: one bucket's columns (see above).
+template <typename RowT>
+__global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
+{
+    __shared__ float buf[kBtRegionCap];
+    __shared__ int32_t longCols[kBtMaxLongCols];
+    __shared__ int longCount;
+    if (FlagSet(q.flag) == 0U) return;
+    const int64_t b = XcdIndex();
+    if (b >= q.buckets) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid / kWave;
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    const int64_t c0 = b << q.wshift;
+    const int64_t c1 = c0 + (int64_t{1} << q.wshift) < q.cols ? c0 + (int64_t{1} << q.wshift) : q.cols;
+    const int64_t rs = static_cast<int64_t>(colptr[c0]);
+    const int n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - rs);
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    if (tid == 0) longCount = 0;
+    // products to their column-order places, 8 per thread per round (loads
+    // first, unconditional: lanes past the bucket read its first slot)
+    constexpr int kU = 8;
+    for (int base = 0; base < n; base += kU * kBtColThreads) {
+        float v[kU];
+        uint32_t p[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = base + u * kBtColThreads + tid;
+            const int64_t j = rs + (i < n ? i : 0);
+            v[u] = q.prod[j];
+            p[u] = q.cl[j];
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = base + u * kBtColThreads + tid;
+            if (i < n) buf[p[u]] = v[u];
+        }
+    }
+    __syncthreads();
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
+    float* y = static_cast<float*>(q.y);
+    for (int64_t c = c0 + tid; c < c1; c += kBtColThreads) {
+        const int a = static_cast<int>(static_cast<int64_t>(colptr[c]) - rs);
+        const int e = static_cast<int>(static_cast<int64_t>(colptr[c + 1]) - rs);
+        if (e - a > kBtLongCol) {
+            longCols[atomicAdd(&longCount, 1)] = static_cast<int32_t>(c - c0);
+            continue;
+        }
+        float sum = 0.0f;
+        for (int k = a; k < e; ++k) sum += buf[k];
+        StoreRow<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz);
+    }
+    __syncthreads();
+    const int nLong = longCount;
+    for (int li = wv; li < nLong; li += kBtColThreads / kWave) {
+        const int64_t c = c0 + longCols[li];
+        const int a = static_cast<int>(static_cast<int64_t>(colptr[c]) - rs);
+        const int e = static_cast<int>(static_cast<int64_t>(colptr[c + 1]) - rs);
+        float part = 0.0f;
+        for (int k = a + lane; k < e; k += kWave) part += buf[k];
+        const float sum = WaveSum(part);
+        if (lane == 0) StoreRow<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz);
+    }
+}
+
 // ------------------------------- launchers ----------------------------------
 
 template <typename T>
@@ -742,6 +1152,10 @@ StageParams MakeStageParams(const SpmvLaunch& l)
     q.metric = At<unsigned long long>(l.ws, L.st_metric_offset);
     q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
     q.part = L.st_part_size;
+    q.colptr = At<void>(l.ws, L.colptr_offset);
+    q.csc_pos = At<void>(l.ws, L.csc_pos_offset);
+    q.inv = At<int32_t>(l.ws, L.key_b_offset);  // free once the CSC build is done
+    q.prod = At<float>(l.ws, L.prod_offset);
     q.s.device = l.device_scalars;
     q.s.alpha_re = l.alpha_re;
     q.s.beta_re = l.beta_re;
@@ -788,6 +1202,40 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     else LaunchSort<32>(q, s);
     hipLaunchKernelGGL(StageDecideKernel, dim3(1), dim3(1), 0, s, q);
     return 0;
+}
+
+template <typename RowT>
+int BtPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
+{
+    const SpmvLayout& L = l.layout;
+    StageParams q = MakeStageParams(l);
+    const int64_t T = L.st_tiles;
+    hipLaunchKernelGGL((StageTileSplitKernel<RowT>), dim3(static_cast<unsigned>((T + 1 + 255) / 256)), dim3(256), 0,
+                       s, q);
+    hipLaunchKernelGGL((BtInvertKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
+    hipLaunchKernelGGL((BtCountKernel<RowT>), dim3(static_cast<unsigned>(T + 1)), dim3(kSortThreads), 0, s, q);
+    const int64_t cells = static_cast<int64_t>(L.st_buckets + 1) * (T + 1);
+    void* temp = reinterpret_cast<void*>(
+        (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, L.st_scan_offset)) + 255) & ~uintptr_t{255});
+    size_t tempBytes = L.st_scan_bytes;
+    if (hipcub::DeviceScan::ExclusiveSum(temp, tempBytes, q.counts, q.start_bm, static_cast<int>(cells), s) !=
+        hipSuccess) {
+        return 1;
+    }
+    hipLaunchKernelGGL(StageTransposeKernel,
+                       dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
+                       dim3(32, 8), 0, s, q);
+    hipLaunchKernelGGL((BtSortKernel<RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
+    hipLaunchKernelGGL((BtDecideKernel<RowT>), dim3(1), dim3(256), 0, s, q);
+    return 0;
+}
+
+template <typename RowT>
+void BtComputeTyped(const SpmvLaunch& l, hipStream_t s)
+{
+    const StageParams q = MakeStageParams(l);
+    hipLaunchKernelGGL((BtScatterKernel<RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads), 0, s, q);
+    hipLaunchKernelGGL((BtColumnKernel<RowT>), dim3(XcdGrid(l.layout.st_buckets)), dim3(kBtColThreads), 0, s, q);
 }
 
 template <typename RowT, ValKind V, OutKind O>
@@ -852,6 +1300,9 @@ int LaunchStagedPreprocess(const SpmvLaunch& l, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!l.layout.staged) return 1;
+    if (l.op != ACL_SPARSE_OP_NON_TRANSPOSE) {
+        return l.rowptr64 ? BtPreprocessTyped<int64_t>(l, s) : BtPreprocessTyped<int32_t>(l, s);
+    }
     return l.rowptr64 ? StagedPreprocessTyped<int64_t>(l, s) : StagedPreprocessTyped<int32_t>(l, s);
 }
 
@@ -859,6 +1310,12 @@ int LaunchStagedCompute(const SpmvLaunch& l, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!l.layout.staged) return 1;
+    if (l.op != ACL_SPARSE_OP_NON_TRANSPOSE) {
+        if (l.val_kind != ValKind::F32 || l.out_kind != OutKind::F32) return 1;
+        if (l.rowptr64) BtComputeTyped<int64_t>(l, s);
+        else BtComputeTyped<int32_t>(l, s);
+        return 0;
+    }
     if (l.layout.st_value_bytes == 4) AllowGatherLds<uint32_t>();
     else AllowGatherLds<uint16_t>();
     return l.rowptr64 ? LaunchStagedRowT<int64_t>(l, s) : LaunchStagedRowT<int32_t>(l, s);

@@ -1,0 +1,140 @@
+"""GPU parity of the column-bucketed transpose (fp32 values, opA = T or H) through the C ABI.
+
+Preprocess takes this path for fp32 transposes of at least 2^20 entries when
+every bucket of columns fits pass 2's LDS; each test reads the choice from the
+workspace header (staged_flag) so that a case meant for the bucketed kernels
+cannot pass on the CSC kernels, and the other way round.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close
+from ops_sparse._lib import Operation, PointerMode
+from ops_sparse.spmv import CsrSpMV
+from ops_sparse import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+REGION_TARGET = 12288
+REGION_CAP = 16384
+
+
+def header(plan):
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+    return int(h[16] & 0xFFFFFFFF), int(h[16] >> 32), int(h[17])
+
+
+def bucket_width(cols, nnz):
+    target = REGION_TARGET * cols // nnz
+    shift = 6
+    while shift < 16 and (2 << shift) <= target:
+        shift += 1
+    return 1 << shift
+
+
+def run(w, op=Operation.TRANSPOSE, preprocess=True, y0=None):
+    y = (w.y0 if y0 is None else y0).clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op,
+                   base=w.meta.get("base", 0))
+    if preprocess:
+        plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    return y, plan
+
+
+def host(w):
+    h = w.to("cpu")
+    b = w.meta.get("base", 0)
+    if b:
+        h.col_ind = h.col_ind - b
+        h.row_ptr = h.row_ptr - b
+    return h
+
+
+def transpose_workload(dev, rows, cols, mean, seed, base=0, rdtype=torch.int32, alpha=1.0, beta=2.0):
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    lengths = torch.poisson(torch.full((rows,), mean), generator=g).to(torch.int64)
+    row_ptr, col = wl.csr_from_lengths(lengths, cols, g, "cpu", distinct=False)
+    n = col.numel()
+    vals = torch.rand(n, generator=g) * 2 - 1
+    x = torch.rand(rows, generator=g) * 2 - 1
+    y0 = torch.rand(cols, generator=g) * 2 - 1
+    w = wl.Workload(f"bt_{rows}x{cols}", rows, cols, (row_ptr + base).to(rdtype), (col + base).to(torch.int32),
+                    vals, x, y0, alpha, beta, trans="T", meta={"base": base})
+    return w.to(dev)
+
+
+def test_c5_takes_the_bucketed_path_and_matches_oracle(dev):
+    w = wl.poisson_transpose().to(dev)
+    y, plan = run(w)
+    flag, buckets, tiles = header(plan)
+    assert flag == 1, "c5's buckets fit the column pass's LDS: the bucketed kernels run"
+    assert buckets == -(-w.cols // bucket_width(w.cols, w.nnz))
+    assert_close(w.to("cpu"), y)
+    # again from the same y: bit-identical (every column is summed in row order)
+    y3, _ = run(w)
+    assert torch.equal(y.view(torch.int32), y3.view(torch.int32))
+
+
+def test_conjugate_transpose_int64_base1_beta0_ignores_nan_y(dev):
+    w = transpose_workload(dev, rows=1 << 20, cols=3 << 18, mean=9.0, seed=5, base=1, rdtype=torch.int64,
+                           alpha=-1.5, beta=0.0)
+    y0 = torch.full((w.cols,), float("nan"), device=dev)
+    y, plan = run(w, op=Operation.CONJUGATE_TRANSPOSE, y0=y0)
+    assert header(plan)[0] == 1
+    assert bool(torch.isfinite(y).all())
+    assert_close(host(w), y)
+
+
+def test_rectangular_device_scalars(dev):
+    w = transpose_workload(dev, rows=3 << 20, cols=1 << 20, mean=2.0, seed=8, alpha=0.75, beta=-0.5)
+    y = w.y0.clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, 1.0, 0.0, op=Operation.TRANSPOSE)
+    plan.handle.set_pointer_mode(PointerMode.DEVICE)
+    da = torch.tensor([0.75], device=dev)
+    db = torch.tensor([-0.5], device=dev)
+    plan.alpha = type("P", (), {"ptr": ctypes.c_void_p(da.data_ptr())})()
+    plan.beta = type("P", (), {"ptr": ctypes.c_void_p(db.data_ptr())})()
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    assert header(plan)[0] == 1
+    assert_close(w.to("cpu"), y)
+
+
+def test_a_giant_column_keeps_the_csc_kernels(dev):
+    """One column holding more entries than pass 2's LDS: Preprocess keeps the CSC kernels."""
+    w = transpose_workload(dev, rows=1 << 20, cols=1 << 20, mean=3.0, seed=9)
+    col = w.col_ind.clone()
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    hot = torch.rand(col.numel(), generator=g, device=dev) < (2 * REGION_CAP) / col.numel()
+    col[hot] = 12345
+    w.col_ind = col
+    y, plan = run(w)
+    assert header(plan)[0] == 0
+    assert_close(w.to("cpu"), y)
+
+
+def test_entries_outside_the_rows_are_ignored(dev):
+    """row_ptr[0] > 0: the leading entries belong to no row and must not reach y."""
+    w = transpose_workload(dev, rows=1 << 20, cols=1 << 19, mean=4.0, seed=10)
+    lead = 7
+    w.row_ptr = w.row_ptr + lead
+    w.col_ind = torch.cat([torch.arange(lead, dtype=torch.int32, device=dev), w.col_ind])
+    w.values = torch.cat([torch.full((lead,), 1e6, device=dev), w.values])
+    y, plan = run(w)
+    assert header(plan)[0] == 1
+    assert_close(w.to("cpu"), y)
+
+
+def test_without_preprocess_runs_the_csc_kernels(dev):
+    w = transpose_workload(dev, rows=1 << 20, cols=1 << 20, mean=6.0, seed=11)
+    y, plan = run(w, preprocess=False)
+    assert header(plan)[0] == 0
+    assert_close(w.to("cpu"), y)
