@@ -75,6 +75,13 @@ struct aclsparseSpMatDescr {
     aclDataType value_type = ACL_FLOAT;
     int64_t ptr_stride = 1, idx_stride = 1, value_stride = 1;  // in elements
     SpmvPlan plan;  // plan.buffer == nullptr means "no active SpMV plan"
+    // The path the last staged Preprocess chose, copied from the workspace
+    // header into pinned host memory, and an event recorded after the copy
+    // (hipEvent_t): once the event has completed, SpMV launches only the
+    // chosen kernels; before that, both sets, which read the device flag.
+    // Created by the first staged Preprocess, released with the descriptor.
+    uint32_t* staged_choice_host = nullptr;
+    void* staged_choice_event = nullptr;
 };
 
 struct aclsparseDnVecDescr {
@@ -518,6 +525,9 @@ struct SpmvLaunch {
     // staged gather: Preprocess builds its tables; SpMV launches its kernels
     // (which check the path flag Preprocess left in the header)
     int32_t staged;
+    // with staged: the path Preprocess chose, if known on the host (1 staged
+    // kernels, 0 row / CSC kernels), or -1: launch both, each reads the flag
+    int32_t staged_choice;
 };
 
 // Staged gather: tables and path decision (after LaunchSpmvPreprocess) and

@@ -195,6 +195,56 @@ bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values);
 }
 
+// After a staged Preprocess: copy the path flag it leaves in the workspace
+// header to pinned host memory and record an event after the copy.  The
+// host value starts as a sentinel, so a copy that has not run reads as
+// "unknown"; a previous copy is waited for first (it may be on another
+// stream).  Any failure leaves the choice unknown (SpMV then launches both
+// kernel sets, which read the device flag).
+void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (m->staged_choice_event != nullptr) {
+        (void)hipEventSynchronize(static_cast<hipEvent_t>(m->staged_choice_event));
+    } else {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        m->staged_choice_event = e;
+    }
+    if (m->staged_choice_host == nullptr) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        m->staged_choice_host = static_cast<uint32_t*>(p);
+    }
+    *m->staged_choice_host = 0xFFFFFFFFU;
+    const auto* header = static_cast<const aclsp::SpmvWsHeader*>(ws);
+    if (hipMemcpyAsync(m->staged_choice_host, &header->staged_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
+            hipSuccess ||
+        hipEventRecord(static_cast<hipEvent_t>(m->staged_choice_event), s) != hipSuccess) {
+        (void)hipGetLastError();
+        *m->staged_choice_host = 0xFFFFFFFFU;
+    }
+}
+
+// The path of the matching staged Preprocess if its copy has completed
+// (1 staged kernels, 0 the others), else -1.
+int32_t StagedChoice(const aclsparseSpMatDescr* m)
+{
+    if (m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
+    if (hipEventQuery(static_cast<hipEvent_t>(m->staged_choice_event)) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    const uint32_t v = *static_cast<volatile const uint32_t*>(m->staged_choice_host);
+    return v <= 1U ? static_cast<int32_t>(v) : -1;
+}
+
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
                   aclsparseOperation_t op, aclDataType c, aclsparseSpMVAlg_t alg, const void* buffer,
                   const aclsparseContext* h)
@@ -342,6 +392,7 @@ aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOpe
             m->plan = SpmvPlan{};
             return ACL_SPARSE_STATUS_EXECUTION_FAILED;
         }
+        if (staged) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
     }
     m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
     m->plan.staged = staged;
@@ -375,6 +426,7 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
     if (!planned && aclsp::LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     // pass A reads x as 16-byte vectors
     l.staged = planned && m->rows > 0U && m->plan.staged && Aligned16(vecX->values) ? 1 : 0;
+    l.staged_choice = l.staged ? StagedChoice(m) : -1;
     if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }

@@ -2058,6 +2058,7 @@ template <typename RowT, ValKind V, OutKind O, AccKind A>
 int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
 {
     hipStream_t stream_ = stream;
+    if (l.staged && l.staged_choice == 1) return 0;  // Preprocess chose the staged kernels
     RowBlockParams p = MakeRowBlockParams(l);
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
@@ -2081,9 +2082,10 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             p.task_wgs = static_cast<int32_t>(taskWgs);
             p.task_waves = static_cast<int32_t>(taskWgs * kFlatWaves);
             int64_t blockWgs = (wgs + kXcds - 1) / kXcds * kXcds;
-            if (l.staged) {
+            if (l.staged && l.staged_choice < 0) {
                 // The staged kernels may take this matrix (decided on the
-                // device): a capped grid keeps this launch cheap when it exits.
+                // device, not yet known here): a capped grid keeps this
+                // launch cheap when it exits.
                 p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
                 if (blockWgs > kStagedFallbackWgs) {
                     blockWgs = kStagedFallbackWgs;
@@ -2130,6 +2132,7 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
     const int64_t n = l.cols;
     if (l.layout.csc) {
         if (n <= 0) return 0;
+        if (l.staged && l.staged_choice == 1) return 0;  // Preprocess chose the column-bucketed kernels
         CscParams q{};
         q.colptr = At<void>(l.ws, l.layout.colptr_offset);
         q.entry_row = At<int32_t>(l.ws, l.layout.entry_row_offset);
@@ -2147,7 +2150,7 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         q.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
         q.s = p.s;
         // the column-bucketed kernels (launched after these) run instead when Preprocess chose them
-        q.skip_flag = l.staged ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
+        q.skip_flag = l.staged && l.staged_choice < 0 ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
         // lanes per column: the power of two nearest below the mean column length, <= 64
         const int64_t mean = l.nnz / n;
         int lg = 0;
@@ -2545,7 +2548,7 @@ int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)
     if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= 0) return 0;
     const int rc = l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
     // staged gather: the row kernel above exits when Preprocess chose this path
-    if (rc == 0 && l.staged) return LaunchStagedCompute(l, stream);
+    if (rc == 0 && l.staged && l.staged_choice != 0) return LaunchStagedCompute(l, stream);
     return rc;
 }
 

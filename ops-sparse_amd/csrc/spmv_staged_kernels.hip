@@ -739,6 +739,7 @@ __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
 constexpr int kBtScanIpt = CeilDiv(kBtMaxBuckets + 1, kTileThreads);  // run lengths per thread
 constexpr int kBtColThreads = 512;                                     // pass 2
 constexpr int kBtLongCol = 64;  // columns longer than this are summed by a wave
+constexpr int kBtRunEntries = 64;  // mean run length (entries) below which the bucketed kernels are chosen
 constexpr int kBtMaxLongCols = static_cast<int>(kBtRegionCap) / (kBtLongCol + 1) + 1;
 
 // Bucket of entry k (S: outside the rows' range or a column outside [0, cols)).
@@ -785,9 +786,11 @@ __global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
     __shared__ typename Sort::TempStorage sortStorage;
     __shared__ uint32_t firstSlot[kBtMaxBuckets + 1];
     __shared__ uint32_t lastKey[kSortThreads];
+    __shared__ uint32_t runCount;
     const int64_t t = blockIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
     const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
+    if (threadIdx.x == 0) runCount = 0U;
     const int n = static_cast<int>(e1 - e0);
     uint32_t keys[kSortIpt], vals[kSortIpt];
     for (int u = 0; u < kSortIpt; ++u) {
@@ -799,15 +802,21 @@ __global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
     lastKey[threadIdx.x] = keys[kSortIpt - 1];
     __syncthreads();
     uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
+    uint32_t runs = 0U;
     for (int u = 0; u < kSortIpt; ++u) {
         const int i = threadIdx.x * kSortIpt + u;
         if (i < n) {
-            if (keys[u] != prev) firstSlot[keys[u]] = static_cast<uint32_t>(i);
+            if (keys[u] != prev) {
+                firstSlot[keys[u]] = static_cast<uint32_t>(i);
+                if (keys[u] < static_cast<uint32_t>(q.buckets)) ++runs;
+            }
             q.perm[e0 + vals[u]] = static_cast<uint16_t>(i);
         }
         prev = keys[u];
     }
+    if (runs != 0U) atomicAdd(&runCount, runs);
     __syncthreads();
+    if (threadIdx.x == 0 && runCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(runCount));
     const int nb = q.buckets + 1;
     const RowT* colptr = static_cast<const RowT*>(q.colptr);
     for (int u = 0; u < kSortIpt; ++u) {
@@ -825,13 +834,19 @@ __global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
     }
 }
 
-// The path decision: the column-bucketed kernels when every bucket's
-// entries fit pass 2's LDS.
+// The path decision: the column-bucketed kernels when the tiles' runs are
+// short (their entries scattered over the columns: mean run below
+// kBtRunEntries entries; banded matrices keep the CSC kernels, whose
+// product gathers are then local) and every bucket's entries fit pass 2's
+// LDS.
 template <typename RowT>
 __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
 {
     __shared__ int ok;
-    if (threadIdx.x == 0) ok = 1;
+    if (threadIdx.x == 0) {
+        ok = *q.metric * static_cast<unsigned long long>(kBtRunEntries) > static_cast<unsigned long long>(q.nnz) ? 1
+                                                                                                                : 0;
+    }
     __syncthreads();
     const RowT* colptr = static_cast<const RowT*>(q.colptr);
     const int64_t w = int64_t{1} << q.wshift;

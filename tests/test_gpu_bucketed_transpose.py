@@ -76,9 +76,16 @@ def test_c5_takes_the_bucketed_path_and_matches_oracle(dev):
     assert flag == 1, "c5's buckets fit the column pass's LDS: the bucketed kernels run"
     assert buckets == -(-w.cols // bucket_width(w.cols, w.nnz))
     assert_close(w.to("cpu"), y)
-    # again from the same y: bit-identical (every column is summed in row order)
+    # again from the same y: bit-identical (every column is summed in row order), on a new plan
+    # (its first SpMV launches both kernel sets, which read the device flag) and on this plan
+    # once Preprocess's choice has reached the host (only the bucketed kernels are launched)
     y3, _ = run(w)
     assert torch.equal(y.view(torch.int32), y3.view(torch.int32))
+    first = y.clone()
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
 
 
 def test_conjugate_transpose_int64_base1_beta0_ignores_nan_y(dev):
