@@ -986,7 +986,12 @@ __device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const St
 // served round-robin by the first task_waves waves of the grid, so a long row
 // is reduced by many waves at once.  Each task stores the partial sums of its
 // chunk-crossing rows; the block's last task to arrive combines them.
-template <typename RowT, ValKind V, OutKind O, bool kBeta>
+//
+// kGated: the launch made when another path may have taken the matrix (the
+// decision is on the device only): the kernel exits when p.skip_flag reads
+// 1, and a capped grid loops over the blocks (block_stride).  Ungated
+// launches carry neither (one block per wave, no flag load).
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(7)))
 void SpmvStreamFlatKernel(RowBlockParams p)
 {
@@ -996,7 +1001,9 @@ void SpmvStreamFlatKernel(RowBlockParams p)
 
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
-    if (p.skip_flag != nullptr && ConstLoad<uint32_t>(p.skip_flag, 0) != 0U) return;
+    if constexpr (kGated) {
+        if (ConstLoad<uint32_t>(p.skip_flag, 0) != 0U) return;
+    }
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float* sVal = sValAll[wv];
@@ -1055,10 +1062,9 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     // blocks tile, tile + block_stride, ...
     const int64_t wg = static_cast<int64_t>(blockIdx.x) - p.task_wgs;
     const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
-    const int64_t stride = p.block_stride > 0 ? p.block_stride : p.num_blocks;
-    for (int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv; tile < p.num_blocks; tile += stride) {
+    auto block = [&](int64_t tile) {
         Stage cur = OpenTileFlat<RowT>(p, tile);
-        if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) continue;  // served by tasks
+        if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
         carry = 0.0f;
         while (cur.valid) {
             L b;
@@ -1070,6 +1076,13 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             cur.first = false;
             ChunkBounds(cur);
         }
+    };
+    const int64_t first = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
+    if constexpr (kGated) {
+        const int64_t stride = p.block_stride > 0 ? p.block_stride : p.num_blocks;
+        for (int64_t tile = first; tile < p.num_blocks; tile += stride) block(tile);
+    } else {
+        if (first < p.num_blocks) block(first);
     }
 }
 
@@ -2093,12 +2106,14 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
                 }
             }
             const unsigned g = static_cast<unsigned>(taskWgs + blockWgs);
-            if (betaNz) {
-                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), dim3(kWave * kFlatWaves), 0,
-                                   stream_, p);
+            const dim3 wg(kWave * kFlatWaves);
+            if (p.skip_flag != nullptr) {
+                if (betaNz) hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, true>), dim3(g), wg, 0, stream_, p);
+                else hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, true>), dim3(g), wg, 0, stream_, p);
+            } else if (betaNz) {
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), wg, 0, stream_, p);
             } else {
-                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), dim3(kWave * kFlatWaves),
-                                   0, stream_, p);
+                hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false>), dim3(g), wg, 0, stream_, p);
             }
             return 0;
         }
@@ -2195,12 +2210,21 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
                 const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
                 const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
-                if (betaNz) {
-                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, true>), dim3(g),
-                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                const dim3 wg(kWave * kFlatWaves);
+                if (c.skip_flag != nullptr) {
+                    if (betaNz) {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, true, true>), dim3(g), wg,
+                                           0, stream, c);
+                    } else {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, false, true>), dim3(g), wg,
+                                           0, stream, c);
+                    }
+                } else if (betaNz) {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, true>), dim3(g), wg, 0, stream,
+                                       c);
                 } else {
-                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, false>), dim3(g),
-                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::UNIT, O, false>), dim3(g), wg, 0,
+                                       stream, c);
                 }
                 return 0;
             }
