@@ -240,9 +240,13 @@ struct SpmvLayout {
     //   st_scan                                           scan temporary storage
     //   st_perm uint16[nnz+8]   slot of each entry (CSR order) in its tile's
     //                           bucket-ordered runs
-    //   st_cl uint16[nnz+8]     bucket order: column within the bucket
-    //   st_xg V[nnz+8]          bucket order: the gathered x values (written
+    //   st_cl uint16[P+8]       bucket order: column within the bucket (0 in
+    //                           the runs' padding)
+    //   st_xg V[P+8]            bucket order: the gathered x values (written
     //                           by every SpMV)
+    // Every (tile, bucket) run is padded to a multiple of StageChunkSlots
+    // slots (8 bytes of x), so the counts, starts and slots above are in
+    // padded units; P = StageSlotCap bounds their total.
     //   st_head / st_tail float[T]  partial sums of the rows crossing tile ends
     //   st_metric uint64            distinct x lines per tile, summed
     // The header's staged_flag says which path Preprocess chose.
@@ -285,7 +289,7 @@ constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in o
 #endif
 constexpr int32_t kStageMaxBuckets = SPMV_STAGE_MAX_BUCKETS;
 constexpr int64_t kStageMinParts = 512;           // pass A workgroups (two per CU at least)
-constexpr int64_t kStagePartTarget = int64_t{1} << 20;  // entries per pass A workgroup beyond that
+constexpr int64_t kStagePartTarget = int64_t{1} << 21;  // slots per pass A workgroup beyond that
 // Staged gather decision: the staged path is chosen when the tiles' distinct
 // x lines exceed this fraction of the entries (the row kernels then fetch
 // about one line per entry).
@@ -302,13 +306,26 @@ inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
     return 0U;
 }
 
+// Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run
+// of staged slots is padded to a multiple of this many slots.
+inline uint64_t StageChunkSlots(uint32_t valueBytes) { return 8U / valueBytes; }
+
+// Upper bound of the staged slots (entries plus run padding) of a matrix.
+inline uint64_t StageSlotCap(uint64_t rows, uint64_t nnz, uint64_t buckets, uint32_t valueBytes)
+{
+    const uint64_t tiles = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+    return nnz + (StageChunkSlots(valueBytes) - 1U) * (buckets + 1U) * tiles;
+}
+
 inline bool StageEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t valueBytes)
 {
     if (valueBytes == 0U || rows == 0U) return false;
     if (nnz < static_cast<uint64_t>(kStageMinNnz) || nnz > 0xF0000000ULL) return false;
     if (cols * valueBytes < static_cast<uint64_t>(kStageMinXBytes)) return false;
     const uint64_t w = static_cast<uint64_t>(kStageSegmentBytes) / valueBytes;
-    return (cols + w - 1) / w <= static_cast<uint64_t>(kStageMaxBuckets);
+    const uint64_t buckets = (cols + w - 1) / w;
+    if (buckets > static_cast<uint64_t>(kStageMaxBuckets)) return false;
+    return StageSlotCap(rows, nnz, buckets, valueBytes) <= 0xF0000000ULL;  // slots are uint32
 }
 
 // ---------------------------------------------------------------------------
@@ -450,14 +467,19 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.st_buckets = static_cast<int32_t>((cols + w - 1) / w);
         const uint64_t t = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
         l.st_tiles = static_cast<int64_t>(t);
-        int64_t parts = static_cast<int64_t>((nnz + kStagePartTarget - 1) / kStagePartTarget);
-        parts = parts < kStageMinParts ? kStageMinParts : parts;
-        int64_t part = static_cast<int64_t>((nnz + parts - 1) / parts);
+        // pass A covers the padded slots: at most slotCap (their count is
+        // known on the device only; workgroups past it exit)
+        // (a whole number of rounds of one workgroup per CU: 256 CUs)
+        const uint64_t slotCap = StageSlotCap(rows, nnz, static_cast<uint64_t>(l.st_buckets), stageValueBytes);
+        int64_t parts = static_cast<int64_t>((slotCap + kStagePartTarget - 1) / kStagePartTarget);
+        parts = parts < kStageMinParts ? kStageMinParts : (parts + 255) / 256 * 256;
+        int64_t part = static_cast<int64_t>((slotCap + parts - 1) / parts);
         part = (part + 7) & ~int64_t{7};
         l.st_part_size = part;
-        l.st_parts = static_cast<int64_t>((nnz + part - 1) / part);
+        l.st_parts = static_cast<int64_t>((slotCap + part - 1) / part);
         const size_t cells = static_cast<size_t>(l.st_buckets + 1) * static_cast<size_t>(t + 1);
         const size_t n8 = static_cast<size_t>(nnz) + 8;
+        const size_t s8 = static_cast<size_t>(slotCap) + 8;
         l.st_tile_row_offset = AlignUp(l.total);
         l.st_tile_nnz_offset = AlignUp(l.st_tile_row_offset + static_cast<size_t>(t + 1) * sizeof(int32_t));
         l.st_counts_offset = AlignUp(l.st_tile_nnz_offset + static_cast<size_t>(t + 1) * sizeof(int64_t));
@@ -467,8 +489,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.st_scan_bytes = StageScanTempBytes(static_cast<int64_t>(cells));
         l.st_perm_offset = AlignUp(l.st_scan_offset + l.st_scan_bytes + 256);  // re-aligned to 256 at use
         l.st_cl_offset = AlignUp(l.st_perm_offset + n8 * sizeof(uint16_t));
-        l.st_xg_offset = AlignUp(l.st_cl_offset + n8 * sizeof(uint16_t));
-        l.st_head_offset = AlignUp(l.st_xg_offset + n8 * stageValueBytes);
+        l.st_xg_offset = AlignUp(l.st_cl_offset + s8 * sizeof(uint16_t));
+        l.st_head_offset = AlignUp(l.st_xg_offset + s8 * stageValueBytes);
         l.st_tail_offset = AlignUp(l.st_head_offset + static_cast<size_t>(t) * sizeof(float));
         l.st_metric_offset = AlignUp(l.st_tail_offset + static_cast<size_t>(t) * sizeof(float));
         l.total = AlignUp(l.st_metric_offset + sizeof(uint64_t));
@@ -489,7 +511,10 @@ aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t
 // ---------------------------------------------------------------------------
 // UNIT: no values (every entry is 1); the transpose's column pass reads its
 // fp32 products through the x gather.
-enum class ValKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I8 = 3, C64 = 4, UNIT = 5 };
+// GATH: fp32 values gathered by position (the "values" array holds each
+// entry's position in the caller's values): the one-pass column kernel of
+// banded fp32 transposes.
+enum class ValKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I8 = 3, C64 = 4, UNIT = 5, GATH = 6 };
 enum class OutKind : int32_t { F32 = 0, F16 = 1, BF16 = 2, I32 = 3, C64 = 4 };
 enum class AccKind : int32_t { F32 = 0, I64 = 1, C64 = 2 };
 
@@ -525,8 +550,9 @@ struct SpmvLaunch {
     // staged gather: Preprocess builds its tables; SpMV launches its kernels
     // (which check the path flag Preprocess left in the header)
     int32_t staged;
-    // with staged: the path Preprocess chose, if known on the host (1 staged
-    // kernels, 0 row / CSC kernels), or -1: launch both, each reads the flag
+    // with staged: the path Preprocess chose, if known on the host (0 row /
+    // CSC kernels, 1 staged or column-bucketed kernels, 2 banded transpose
+    // kernel), or -1: launch every set, each runs only on its flag value
     int32_t staged_choice;
 };
 

@@ -34,6 +34,7 @@ template <> struct ValOf<ValKind::BF16> { using T = uint16_t; };
 template <> struct ValOf<ValKind::I8> { using T = int8_t; };
 template <> struct ValOf<ValKind::C64> { using T = C64; };
 template <> struct ValOf<ValKind::UNIT> { using T = float; };  // the gathered "x" holds the products
+template <> struct ValOf<ValKind::GATH> { using T = float; };  // int32 positions stream; fp32 values gathered
 
 template <OutKind O> struct OutOf;
 template <> struct OutOf<OutKind::F32> { using T = float; };

@@ -233,7 +233,8 @@ void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 }
 
 // The path of the matching staged Preprocess if its copy has completed
-// (1 staged kernels, 0 the others), else -1.
+// (0 the row / CSC kernels, 1 the staged or column-bucketed kernels, 2 the
+// banded transpose kernel), else -1.
 int32_t StagedChoice(const aclsparseSpMatDescr* m)
 {
     if (m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
@@ -242,7 +243,7 @@ int32_t StagedChoice(const aclsparseSpMatDescr* m)
         return -1;
     }
     const uint32_t v = *static_cast<volatile const uint32_t*>(m->staged_choice_host);
-    return v <= 1U ? static_cast<int32_t>(v) : -1;
+    return v <= 2U ? static_cast<int32_t>(v) : -1;
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,

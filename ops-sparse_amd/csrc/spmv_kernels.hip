@@ -113,10 +113,15 @@ struct RowBlockParams {
     float* z;            // SpMVOp: output (y is then only read)
     int64_t rp_base;     // subtracted from p.rp entries (0 for the normalised copy)
     int32_t fixed_rows;  // SpMVOp ALG1: rows per block, blocks taken straight from p.rp
-    // When set, the kernel exits at once if the word is non-zero: Preprocess
-    // chose the staged-gather path for this matrix (its kernels are launched
-    // after this one and exit when the word is zero).
+    // When set, the kernel exits at once unless the word equals run_flag:
+    // Preprocess chose another path for this matrix (the staged gather, the
+    // column-bucketed or the one-pass banded transpose), whose kernels are
+    // launched beside this one.
     const uint32_t* skip_flag;
+    uint32_t run_flag;
+    // ValKind::GATH: the fp32 values the streamed positions index
+    const float* gval;
+    int64_t gval_n;
     // Stream kernel: when > 0, the grid is capped and each wave loops over
     // the blocks tile, tile + block_stride, ... (block_stride = all block waves)
     int64_t block_stride;
@@ -435,6 +440,11 @@ struct StreamVals<ValKind::BF16> {
 template <>
 struct StreamVals<ValKind::UNIT> {
 };
+template <>
+struct StreamVals<ValKind::GATH> {
+    v4i v[2];                 // positions of the 8 slots in the values array
+    uint32_t g[kLaneItems];   // the gathered values
+};
 
 template <ValKind V>
 __device__ __forceinline__ uint32_t RawVal(const StreamVals<V>& s, int j)
@@ -491,6 +501,10 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
     if constexpr (V == ValKind::UNIT) {
         (void)rv;  // no values
+    } else if constexpr (V == ValKind::GATH) {
+        b.val.v[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
+        b.val.v[1] =
+            __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, 1024 + lane * 16, 0, kBufNonTemporal));
     } else if constexpr (V == ValKind::F32) {
         b.val.v[0] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
         b.val.v[1] =
@@ -574,6 +588,8 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
                 const ValT tv = kk == 0 ? tv3[0] : kk == 1 ? tv3[1] : tv3[2];
                 if constexpr (V == ValKind::UNIT) {
                     (void)tv;
+                } else if constexpr (V == ValKind::GATH) {
+                    b.val.v[j >> 2][j & 3] = __float_as_int(tv);
                 } else if constexpr (V == ValKind::F32) {
                     b.val.v[j >> 2][j & 3] = tv;
                 } else {
@@ -596,6 +612,16 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, static_cast<int>(off), 0, kGatherPolicy);
+        }
+    }
+    if constexpr (V == ValKind::GATH) {
+        // the slots' values, by position (positions past the chunk read 0)
+        const __amdgpu_buffer_rsrc_t rg = Rsrc(p.gval, p.gval_n * 4);
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            uint32_t off = static_cast<uint32_t>(b.val.v[j >> 2][j & 3]) * 4U;
+            off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+            b.val.g[j] = __builtin_amdgcn_raw_buffer_load_b32(rg, static_cast<int>(off), 0, kGatherPolicy);
         }
     }
 }
@@ -658,6 +684,7 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
         if constexpr (V == ValKind::UNIT) prod[j] = __uint_as_float(lc.xg[j]);
+        else if constexpr (V == ValKind::GATH) prod[j] = __uint_as_float(lc.val.g[j]) * __uint_as_float(lc.xg[j]);
         else prod[j] = ValToFloat<V>(RawVal<V>(lc.val, j)) * ValToFloat<V>(lc.xg[j]);
     }
 
@@ -1002,7 +1029,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
     if constexpr (kGated) {
-        if (ConstLoad<uint32_t>(p.skip_flag, 0) != 0U) return;
+        if (ConstLoad<uint32_t>(p.skip_flag, 0) != p.run_flag) return;
     }
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -2139,6 +2166,45 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     return 0;
 }
 
+// One-pass column kernel of banded fp32 transposes: the stream kernel on the
+// CSC pattern with each entry's row as its "column" (x gathered by row) and
+// its CSR position as its value (the value gathered by position).
+template <bool kGated>
+void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStream_t stream)
+{
+    RowBlockParams c = p;
+    c.rp = At<void>(l.ws, l.layout.colptr_offset);
+    c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
+    c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
+    c.num_blocks = l.layout.csc_num_blocks;
+    c.col = At<const int32_t>(l.ws, l.layout.key_b_offset);  // csc_row, built by the bucketed Preprocess
+    c.col_stride = 1;
+    c.val = At<const void>(l.ws, l.layout.csc_pos_offset);
+    c.val_stride = 1;
+    c.x = l.x;
+    c.x_stride = 1;
+    c.rows = l.cols;
+    c.cols = l.rows;  // length of x
+    c.base = 0;
+    c.task_wgs = 0;
+    c.task_waves = 0;
+    c.gval = static_cast<const float*>(l.val);
+    c.gval_n = l.nnz;
+    c.skip_flag = kGated ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
+    c.run_flag = 2U;
+    const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
+    const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+    const dim3 wg(kWave * kFlatWaves);
+    const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+    if (betaNz) {
+        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, true, kGated>), dim3(g), wg, 0,
+                           stream, c);
+    } else {
+        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, false, kGated>), dim3(g), wg, 0,
+                           stream, c);
+    }
+}
+
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
 {
@@ -2148,6 +2214,18 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
     if (l.layout.csc) {
         if (n <= 0) return 0;
         if (l.staged && l.staged_choice == 1) return 0;  // Preprocess chose the column-bucketed kernels
+        if constexpr (std::is_same<RowT, int32_t>::value && V == ValKind::F32 && A == AccKind::F32 &&
+                      O == OutKind::F32) {
+            // Banded fp32 transposes (Preprocess's choice 2): one pass over
+            // the CSC pattern gathering each entry's value and x, both local
+            const bool banded = l.staged && l.y_stride == 1 && l.x_stride == 1 && l.val_stride == 1 &&
+                                l.nnz <= 0x1FFFFFFFLL;
+            if (banded && l.staged_choice == 2) {
+                LaunchBandedTranspose<false>(l, p, stream);
+                return 0;
+            }
+            if (banded && l.staged_choice < 0) LaunchBandedTranspose<true>(l, p, stream);  // runs on choice 2 only
+        }
         CscParams q{};
         q.colptr = At<void>(l.ws, l.layout.colptr_offset);
         q.entry_row = At<int32_t>(l.ws, l.layout.entry_row_offset);
@@ -2572,7 +2650,7 @@ int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)
     if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= 0) return 0;
     const int rc = l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
     // staged gather: the row kernel above exits when Preprocess chose this path
-    if (rc == 0 && l.staged && l.staged_choice != 0) return LaunchStagedCompute(l, stream);
+    if (rc == 0 && l.staged && (l.staged_choice == 1 || l.staged_choice < 0)) return LaunchStagedCompute(l, stream);
     return rc;
 }
 

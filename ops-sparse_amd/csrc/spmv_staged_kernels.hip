@@ -94,10 +94,13 @@ struct StageParams {
     unsigned long long* metric;
     uint32_t* flag;
     int64_t part;  // pass A: bucket-ordered slots per workgroup
+    int32_t chunk; // staged slots per 8-byte chunk: runs are padded to a multiple
     // column-bucketed transpose
     const void* colptr;   // RowT[cols+1], column offsets of the CSC pattern
     const void* csc_pos;  // RowT[nnz], CSR index of each entry in column order
-    int32_t* inv;         // int32[nnz], column-order place of each CSR entry
+    int32_t* inv;         // int32[nnz], column-order place of each CSR entry, then (after
+                          // the sort) csc_row: the row of each entry in column order
+    const int32_t* entry_row;  // int32[nnz], the row of each entry in CSR order
     float* prod;          // float[nnz+8], products in bucket order
     Scalars s;
 };
@@ -155,7 +158,8 @@ __global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
     q.tile_nnz[t] = d - lo;
 }
 
-// counts[s*(T+1) + t] = entries of tile t in bucket s (column T is zero).
+// counts[s*(T+1) + t] = staged slots of tile t in bucket s: its entries,
+// padded to a multiple of q.chunk (column T is zero).
 __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
 {
     __shared__ uint32_t hist[kStageMaxBuckets + 1];
@@ -170,7 +174,9 @@ __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
         }
     }
     __syncthreads();
-    for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
+    // padded to whole 8-byte chunks of staged x
+    const uint32_t m = static_cast<uint32_t>(q.chunk) - 1U;
+    for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = (hist[s] + m) & ~m;
 }
 
 // start[t*(S+1) + s] = start_bm[s*(T+1) + t].
@@ -195,20 +201,38 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
 }
 
 // Per tile: stable radix sort of (column, position) so that the tile's
-// entries are in bucket order; perm[k] = sorted slot of entry k,
-// cl[start(t,s) + rank] = column within the bucket; adds the tile's count of
-// distinct x lines to the metric.
+// entries are in bucket order; perm[k] = slot of entry k in the tile's
+// padded bucket-ordered runs, cl[start(t,s) + rank] = column within the
+// bucket (0 in the runs' padding); adds the tile's count of distinct x lines
+// to the metric.
 template <int kEndBit>
 __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
 {
     using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
+    using Scan = hipcub::BlockScan<uint32_t, kSortThreads>;
+    constexpr int kRunIpt = (kStageMaxBuckets + 1 + kSortThreads - 1) / kSortThreads;
     __shared__ typename Sort::TempStorage sortStorage;
+    __shared__ typename Scan::TempStorage scanStorage;
     __shared__ uint32_t firstSlot[kStageMaxBuckets + 1];
+    __shared__ uint32_t padOff[kStageMaxBuckets + 1];
+    __shared__ uint32_t firstKey[kSortThreads + 1];
     __shared__ uint32_t lastKey[kSortThreads];
     __shared__ uint32_t lineCount;
     const int64_t t = blockIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
     const int n = static_cast<int>(e1 - e0);
+    const int nb = q.buckets + 1;
+    // the tile's run offsets in padded slots
+    uint32_t pc[kRunIpt];
+    for (int u = 0; u < kRunIpt; ++u) {
+        const int s = threadIdx.x * kRunIpt + u;
+        pc[u] = s < nb ? q.counts[s * (q.tiles + 1) + t] : 0U;
+    }
+    Scan(scanStorage).ExclusiveSum(pc, pc);
+    for (int u = 0; u < kRunIpt; ++u) {
+        const int s = threadIdx.x * kRunIpt + u;
+        if (s < nb) padOff[s] = pc[u];
+    }
     uint32_t keys[kSortIpt], vals[kSortIpt];
     constexpr uint32_t kPad = kEndBit >= 32 ? 0xFFFFFFFFU : ((1U << kEndBit) - 1U);
     for (int u = 0; u < kSortIpt; ++u) {
@@ -216,9 +240,13 @@ __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
         keys[u] = i < n ? KeyOf(q, q.col[e0 + i]) : kPad;
         vals[u] = static_cast<uint32_t>(i);
     }
-    if (threadIdx.x == 0) lineCount = 0U;
+    if (threadIdx.x == 0) {
+        lineCount = 0U;
+        firstKey[kSortThreads] = 0xFFFFFFFFU;
+    }
     Sort(sortStorage).Sort(keys, vals, 0, kEndBit);
     lastKey[threadIdx.x] = keys[kSortIpt - 1];
+    firstKey[threadIdx.x] = keys[0];
     __syncthreads();
     uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
     uint32_t lines = 0U;
@@ -230,21 +258,27 @@ __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
             const uint32_t b = key >> q.wshift;
             if (prev == 0xFFFFFFFFU || (prev >> q.wshift) != b) firstSlot[b] = static_cast<uint32_t>(i);
             if (b != nullBucket && (prev == 0xFFFFFFFFU || (prev >> q.line_shift) != (key >> q.line_shift))) ++lines;
-            q.perm[e0 + vals[u]] = static_cast<uint16_t>(i);
         }
         prev = keys[u];
     }
     if (lines != 0U) atomicAdd(&lineCount, lines);
     __syncthreads();
     const uint32_t mask = (1U << q.wshift) - 1U;
-    const int nb = q.buckets + 1;
     for (int u = 0; u < kSortIpt; ++u) {
         const int i = threadIdx.x * kSortIpt + u;
         if (i < n) {
             const uint32_t key = keys[u];
             const uint32_t b = key >> q.wshift;
-            const uint32_t slot = q.start[t * nb + b] + (static_cast<uint32_t>(i) - firstSlot[b]);
-            q.cl[slot] = static_cast<uint16_t>(b == nullBucket ? 0U : (key & mask));
+            const uint32_t rank = static_cast<uint32_t>(i) - firstSlot[b];
+            q.perm[e0 + vals[u]] = static_cast<uint16_t>(padOff[b] + rank);
+            const uint32_t start = q.start[t * nb + b];
+            q.cl[start + rank] = static_cast<uint16_t>(b == nullBucket ? 0U : (key & mask));
+            // the run's last entry clears the run's padding
+            const uint32_t next = u + 1 < kSortIpt ? keys[u + 1] : firstKey[threadIdx.x + 1];
+            if (i + 1 == n || (next >> q.wshift) != b) {
+                const uint32_t runSlots = q.counts[b * (q.tiles + 1) + t];
+                for (uint32_t j = rank + 1U; j < runSlots; ++j) q.cl[start + j] = 0U;
+            }
         }
     }
     if (threadIdx.x == 0 && lineCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(lineCount));
@@ -295,12 +329,13 @@ __global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams 
     XT* seg = reinterpret_cast<XT*>(segRaw);
     if (FlagSet(q.flag) == 0U) return;
     const int64_t w = XcdIndex();
-    const int64_t a = w * q.part;
-    if (a >= q.nnz) return;
-    const int64_t b = a + q.part < q.nnz ? a + q.part : q.nnz;
     const int nb = q.buckets + 1;
     const uint32_t* base = q.start;                  // row 0: first slot of every bucket
     const uint32_t* ends = q.start + q.tiles * nb;   // row T: end of every bucket
+    const int64_t total = ends[nb - 1];              // staged slots, padding included
+    const int64_t a = w * q.part;
+    if (a >= total) return;
+    const int64_t b = a + q.part < total ? a + q.part : total;
     // first bucket that ends after a
     int lo = 0, hi = nb - 1;
     while (lo < hi) {
@@ -425,10 +460,16 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
     using Raw = typename SV::Raw;
     using Group = typename SV::Group;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
+    // staged x moves in 8-byte chunks of kP slots (runs are padded to whole chunks)
+    constexpr int kP = 8 / static_cast<int>(sizeof(Raw));
+    constexpr int kChunkCap = (kTileItems + (kP - 1) * (kStageMaxBuckets + 1) + kP - 1) / kP;
+    constexpr int kChunkIters = (kChunkCap + kTileThreads - 1) / kTileThreads;  // 64-chunk windows per wave
+    constexpr int kChunkWindows = kTileWaves * kChunkIters;
+    constexpr int kAreaFloats = (kTileItems + 8 > 2 * kChunkCap ? kTileItems + 8 : 2 * kChunkCap);
     __shared__ uint32_t runDelta[kStageMaxBuckets + 1];
-    __shared__ uint32_t startBits[2 * kWindows];
-    __shared__ uint32_t firstRank[kWindows];
-    __shared__ float4 areaV[(kTileItems + 8 + 3) / 4];
+    __shared__ uint32_t startBits[2 * kChunkWindows];
+    __shared__ uint32_t firstRank[kChunkWindows];
+    __shared__ float4 areaV[(kAreaFloats + 3) / 4];
     __shared__ int32_t longRows[kMaxLong];
     __shared__ int longCount;
     __shared__ int headFlag;
@@ -525,32 +566,35 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
     }
     asm volatile("" ::: "memory");
 
-    // 3. the slot -> run map of the tile's bucket-ordered slots, from an
-    //    exclusive scan of the run lengths (waits for the run table only).
-    //    Each scanned word packs (non-empty runs before, slots before); for
-    //    every non-empty run of rank r starting at slot o: runDelta[r] = its
-    //    first xg slot - o, bit o of startBits, and firstRank of each 64-slot
-    //    window whose first slot it holds.  The run of slot i = 64*W + l then
-    //    has rank firstRank[W] + (bits 1..l of the window's 64 start bits).
-    for (int w = tid; w < 2 * kWindows; w += kTileThreads) {
+    // 3. the chunk -> run map of the tile's bucket-ordered staged slots, from
+    //    an exclusive scan of the run lengths in chunks (waits for the run
+    //    table only).  Each scanned word packs (non-empty runs before, chunks
+    //    before); for every non-empty run of rank r starting at chunk o:
+    //    runDelta[r] = its first xg chunk - o, bit o of startBits, and
+    //    firstRank of each 64-chunk window whose first chunk it holds.  The
+    //    run of chunk i = 64*W + l then has rank firstRank[W] + (bits 1..l
+    //    of the window's 64 start bits).
+    for (int w = tid; w < 2 * kChunkWindows; w += kTileThreads) {
         startBits[w] = 0U;
-        if (w < kWindows) firstRank[w] = 0U;
+        if (w < kChunkWindows) firstRank[w] = 0U;
     }
     uint32_t cnt[kScanIpt];
 #pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
-        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        const uint32_t c = s < nb ? (runB[u] - runA[u]) / kP : 0U;
         cnt[u] = c | (c != 0U ? 0x10000U : 0U);
     }
-    Scan(scanStorage).ExclusiveSum(cnt, cnt);  // its barriers also order the clearing above
+    uint32_t packedTotal;
+    Scan(scanStorage).ExclusiveSum(cnt, cnt, packedTotal);  // its barriers also order the clearing above
+    const int C = static_cast<int>(packedTotal & 0xFFFFU);  // staged chunks of the tile
 #pragma unroll
     for (int u = 0; u < kScanIpt; ++u) {
         const int s = tid * kScanIpt + u;
-        const uint32_t c = s < nb ? runB[u] - runA[u] : 0U;
+        const uint32_t c = s < nb ? (runB[u] - runA[u]) / kP : 0U;
         if (c != 0U) {
             const uint32_t o = cnt[u] & 0xFFFFU, r = cnt[u] >> 16;
-            runDelta[r] = runA[u] - o;
+            runDelta[r] = runA[u] / kP - o;
             atomicOr(&startBits[o >> 5], 1U << (o & 31U));
             for (uint32_t w = (o + 63U) >> 6; w * 64U < o + c; ++w) firstRank[w] = r;
         }
@@ -560,26 +604,23 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
     const int nLoc = R + (lastRowInside ? 1 : 0);
     __syncthreads();
 
-    // 4. stage the runs.  Wave w fills the 64-slot windows of slots
-    //    [w*span, (w+1)*span), lanes on consecutive slots, so the loads of
-    //    one run are coalesced.  The source slot of each of the lane's values
-    //    comes first (independent LDS lookups, the window's words are the
-    //    same for the whole wave), the loads after it; lanes past the range
-    //    load slot 0 and discard it.  One register per value: 16-bit values
-    //    packed two to a register would make each load wait for its
-    //    predecessor.
-    Raw* xl = reinterpret_cast<Raw*>(area);
-    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);  // after the products
+    // 4. stage the runs, 8 bytes per lane.  Wave w fills the 64-chunk
+    //    windows of chunks [w*span, (w+1)*span), lanes on consecutive chunks,
+    //    so the loads of one run are coalesced.  The source chunk of each of
+    //    the lane's loads comes first (independent LDS lookups; the window's
+    //    words are the same for the whole wave), the loads after it; lanes
+    //    past the range load chunk 0 and discard it.
     {
-        const Raw* xg = static_cast<const Raw*>(q.xg);
-        const int span = (E + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
+        const uint2* xg = static_cast<const uint2*>(q.xg);
+        uint2* xl = reinterpret_cast<uint2*>(area);
+        const int span = (C + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
         const int i0 = __builtin_amdgcn_readfirstlane(wv) * span;  // wave-uniform
-        const int i1 = i0 + span < E ? i0 + span : E;
+        const int i1 = i0 + span < C ? i0 + span : C;
         const uint32_t maskLo = lane < 32 ? (2U << lane) - 2U : 0xFFFFFFFEU;   // bits 1..l
         const uint32_t maskHi = lane < 32 ? 0U : (2U << (lane - 32)) - 1U;
-        uint32_t src[kStageLanes];
+        uint32_t src[kChunkIters];
 #pragma unroll
-        for (int m = 0; m < kStageLanes; ++m) {
+        for (int m = 0; m < kChunkIters; ++m) {
             const int w = (i0 >> 6) + m;
             const int i = (w << 6) + lane;
             const uint32_t fr = firstRank[w];
@@ -589,40 +630,26 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
             const uint32_t d = runDelta[r];  // read by every lane: no load under a branch
             src[m] = i < i1 ? d + static_cast<uint32_t>(i) : 0U;
         }
-        uint32_t v[kStageLanes];
+        uint2 v[kChunkIters];
 #pragma unroll
-        for (int m = 0; m < kStageLanes; ++m) v[m] = xg[src[m]];  // xg holds fewer than 2^32 slots
+        for (int m = 0; m < kChunkIters; ++m) v[m] = xg[src[m]];  // xg holds fewer than 2^32 slots
         asm volatile("" ::: "memory");  // all loads before the first store
-
-        // 5. row offsets relative to e0, clamped to [0, E], after the entry
-        //    area (waits for the row offsets only), then the staged values
-        //    (waits for the runs)
+        if (tid == 0) headFlag = rowOff[0] < e0 ? 1 : 0;  // the tile's first row started in an earlier tile
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int i = tid + u * kTileThreads;
-            const int64_t d = rowOff[u] - e0;
-            if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
-        }
-        if (tid == 0) {
-            rel[R + 1] = a0 + E;
-            headFlag = rowOff[0] < e0 ? 1 : 0;  // the tile's first row started in an earlier tile
-        }
-#pragma unroll
-        for (int m = 0; m < kStageLanes; ++m) {
+        for (int m = 0; m < kChunkIters; ++m) {
             const int i = i0 + m * kWave + lane;
-            if (i < i1) xl[i] = static_cast<Raw>(v[m]);
+            if (i < i1) xl[i] = v[m];
         }
-    }
-    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
-        const int64_t d = Norm<RowT>(q, r0 + i) - e0;
-        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
     }
     __syncthreads();
     const bool headRow = headFlag != 0;
-    // 6. products a_k * x(slot_k) in registers, then into the area by groups
-    //    of 4 (entry e0 at a0).  The tile's two edge groups also hold entries
-    //    of the neighbouring tiles: their slots are other tiles' (still
-    //    inside the area) and their products are replaced by zero.
+
+    // 5. products a_k * x(slot_k) in registers, then into the area by groups
+    //    of 4 (entry e0 at a0), with the tile's row offsets relative to the
+    //    first group (clamped to the tile) after them.  The tile's two edge
+    //    groups also hold entries of the neighbouring tiles: their slots are
+    //    other tiles' (still inside the staged area) and their products are
+    //    replaced by zero.
     float4 prod[kGroupSlots];
     {
         const Raw* xlr = reinterpret_cast<const Raw*>(area);
@@ -650,9 +677,21 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
         const int gi = tid + u * kTileThreads;
         if (gi < ng) areaV[gi] = prod[u];
     }
+    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);  // after the products
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kTileThreads;
+        const int64_t d = rowOff[u] - e0;
+        if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+    }
+    if (tid == 0) rel[R + 1] = a0 + E;
+    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
+        const int64_t d = Norm<RowT>(q, r0 + i) - e0;
+        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+    }
     __syncthreads();
 
-    // 7. rows: short ones by one thread, long ones queued for a wave
+    // 6. rows: short ones by one thread, long ones queued for a wave
     const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
     const bool tailHasEntries = lastRowInside && rel[R] < a0 + E;
     for (int loc = tid; loc < nLoc; loc += kTileThreads) {
@@ -834,19 +873,28 @@ __global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
     }
 }
 
-// The path decision: the column-bucketed kernels when the tiles' runs are
-// short (their entries scattered over the columns: mean run below
-// kBtRunEntries entries; banded matrices keep the CSC kernels, whose
-// product gathers are then local) and every bucket's entries fit pass 2's
-// LDS.
+// csc_row[j] = entry_row[csc_pos[j]] (into the inv array, no longer needed).
+template <typename RowT>
+__global__ __launch_bounds__(256) void BtCscRowKernel(StageParams q)
+{
+    const int64_t j = blockIdx.x * int64_t{256} + threadIdx.x;
+    if (j >= q.nnz) return;
+    q.inv[j] = q.entry_row[static_cast<int64_t>(static_cast<const RowT*>(q.csc_pos)[j])];
+}
+
+// The path decision (header flag): 1, the column-bucketed kernels, when the
+// tiles' runs are short (their entries scattered over the columns: mean run
+// below kBtRunEntries entries) and every bucket's entries fit pass 2's LDS;
+// 2, the one-pass banded column kernel, when the runs are long (the values
+// and x an entry needs are then near those of its neighbours in column
+// order); 0, the CSC product and column passes.
 template <typename RowT>
 __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
 {
     __shared__ int ok;
-    if (threadIdx.x == 0) {
-        ok = *q.metric * static_cast<unsigned long long>(kBtRunEntries) > static_cast<unsigned long long>(q.nnz) ? 1
-                                                                                                                : 0;
-    }
+    const bool scattered =
+        *q.metric * static_cast<unsigned long long>(kBtRunEntries) > static_cast<unsigned long long>(q.nnz);
+    if (threadIdx.x == 0) ok = 1;
     __syncthreads();
     const RowT* colptr = static_cast<const RowT*>(q.colptr);
     const int64_t w = int64_t{1} << q.wshift;
@@ -856,7 +904,7 @@ __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
         if (static_cast<int64_t>(colptr[c1]) - static_cast<int64_t>(colptr[c0]) > kBtRegionCap) ok = 0;
     }
     __syncthreads();
-    if (threadIdx.x == 0) *q.flag = ok != 0 ? 1U : 0U;
+    if (threadIdx.x == 0) *q.flag = scattered ? (ok != 0 ? 1U : 0U) : 2U;
 }
 
 // Pass 1: products of one tile into its runs (see above).
@@ -902,7 +950,7 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     const int64_t e0 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t];
     const int64_t e1 = reinterpret_cast<CI64>(reinterpret_cast<uintptr_t>(q.tile_nnz))[t + 1];
     asm volatile("" ::: "memory");
-    if (flag == 0U) return;
+    if (flag != 1U) return;
     const int E = static_cast<int>(e1 - e0);
     const int R = static_cast<int>(r1 - r0);
     const bool lastRowInside = r1 < q.rows;
@@ -1071,7 +1119,7 @@ __global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
     __shared__ float buf[kBtRegionCap];
     __shared__ int32_t longCols[kBtMaxLongCols];
     __shared__ int longCount;
-    if (FlagSet(q.flag) == 0U) return;
+    if (FlagSet(q.flag) != 1U) return;
     const int64_t b = XcdIndex();
     if (b >= q.buckets) return;
     const int tid = threadIdx.x;
@@ -1167,9 +1215,11 @@ StageParams MakeStageParams(const SpmvLaunch& l)
     q.metric = At<unsigned long long>(l.ws, L.st_metric_offset);
     q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
     q.part = L.st_part_size;
+    q.chunk = L.st_value_bytes > 0 ? static_cast<int32_t>(StageChunkSlots(static_cast<uint32_t>(L.st_value_bytes))) : 1;
     q.colptr = At<void>(l.ws, L.colptr_offset);
     q.csc_pos = At<void>(l.ws, L.csc_pos_offset);
     q.inv = At<int32_t>(l.ws, L.key_b_offset);  // free once the CSC build is done
+    q.entry_row = At<const int32_t>(l.ws, L.entry_row_offset);
     q.prod = At<float>(l.ws, L.prod_offset);
     q.s.device = l.device_scalars;
     q.s.alpha_re = l.alpha_re;
@@ -1241,6 +1291,7 @@ int BtPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
     hipLaunchKernelGGL((BtSortKernel<RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
+    hipLaunchKernelGGL((BtCscRowKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
     hipLaunchKernelGGL((BtDecideKernel<RowT>), dim3(1), dim3(256), 0, s, q);
     return 0;
 }

@@ -145,3 +145,39 @@ def test_without_preprocess_runs_the_csc_kernels(dev):
     y, plan = run(w, preprocess=False)
     assert header(plan)[0] == 0
     assert_close(w.to("cpu"), y)
+
+
+def banded_workload(dev, n=1536, beta=0.5, base=0):
+    """A 5-point Laplacian (banded, long runs per tile) as a transpose workload."""
+    w = wl.laplacian_2d(n=n)
+    w = wl.Workload(w.name + "_T", w.rows, w.cols, (w.row_ptr + base).to(torch.int32),
+                    (w.col_ind + base).to(torch.int32), w.values * (1.0 + 0.25 * torch.rand(w.nnz)),
+                    w.x, w.y0, 1.5, beta, trans="T", meta={"base": base})
+    return w.to(dev)
+
+
+def test_banded_transpose_takes_the_one_pass_kernel(dev):
+    """Long runs: Preprocess picks the one-pass banded column kernel (flag 2); repeated runs are
+    bit-identical on a new plan (every kernel set launched, gated on the device flag) and on this plan
+    once the choice has reached the host (only the banded kernel launched)."""
+    w = banded_workload(dev)
+    assert w.nnz >= 1 << 20
+    y, plan = run(w)
+    assert header(plan)[0] == 2
+    assert_close(w.to("cpu"), y)
+    y3, _ = run(w)
+    assert torch.equal(y.view(torch.int32), y3.view(torch.int32))
+    first = y.clone()
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
+
+
+def test_banded_conjugate_transpose_base1_beta0_ignores_nan_y(dev):
+    w = banded_workload(dev, n=1100, beta=0.0, base=1)
+    y0 = torch.full((w.cols,), float("nan"), device=dev)
+    y, plan = run(w, op=Operation.CONJUGATE_TRANSPOSE, y0=y0)
+    assert header(plan)[0] == 2
+    assert bool(torch.isfinite(y).all())
+    assert_close(host(w), y)
