@@ -58,6 +58,10 @@ constexpr int kTileWaves = kTileThreads / kWave;
 constexpr int kTileItems = static_cast<int>(kStageTileItems);
 constexpr int kSortIpt = 16;                            // 512 x 16 = 8192 >= kTileItems keys per tile
 constexpr int kGatherThreads = 1024;                    // pass A
+#ifndef SPMV_STAGE_GATHER_BATCH
+#define SPMV_STAGE_GATHER_BATCH 4
+#endif
+constexpr int kGatherBatch = SPMV_STAGE_GATHER_BATCH;   // pass A: groups of 8 slots per thread per round
 constexpr int kLongRow = 32;                            // in-tile rows longer than this are summed by a wave
 constexpr int kMaxLong = kTileItems / kLongRow + 1;
 constexpr int CeilDiv(int a, int b) { return (a + b - 1) / b; }
@@ -364,20 +368,35 @@ __global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams 
             for (int64_t i = nv * kVec + threadIdx.x; i < n; i += kGatherThreads) seg[i] = x[c0 + i];
             __syncthreads();
         }
-        for (int64_t g = (j0 >> 3) + threadIdx.x; g * 8 < j1; g += kGatherThreads) {
-            const uint4 c = *reinterpret_cast<const uint4*>(q.cl + g * 8);
-            const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-            XT o[8];
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t ci = (cw[u >> 1] >> ((u & 1) * 16)) & 0xFFFFU;
-                o[u] = real ? seg[ci] : XT{0};
+        // groups of 8 slots, kGatherBatch groups per thread per round: the
+        // round's column loads are all issued before its first LDS read
+        const int64_t gEnd = (j1 + 7) >> 3;
+        for (int64_t g0 = (j0 >> 3) + threadIdx.x; g0 < gEnd; g0 += kGatherBatch * kGatherThreads) {
+            uint4 c[kGatherBatch];
+#pragma unroll
+            for (int u = 0; u < kGatherBatch; ++u) {
+                const int64_t g = g0 + u * kGatherThreads;
+                c[u] = *reinterpret_cast<const uint4*>(q.cl + (g < gEnd ? g : g0) * 8);
             }
-            const int64_t j = g * 8;
-            if (j >= j0 && j + 8 <= j1) {
-                StoreGroup<XT>(xg + j, o);
-            } else {
-                for (int u = 0; u < 8; ++u) {
-                    if (j + u >= j0 && j + u < j1) xg[j + u] = o[u];
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < kGatherBatch; ++u) {
+                const int64_t g = g0 + u * kGatherThreads;
+                const uint32_t cw[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+                XT o[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t ci = (cw[k >> 1] >> ((k & 1) * 16)) & 0xFFFFU;
+                    o[k] = real ? seg[ci] : XT{0};
+                }
+                const int64_t j = g * 8;
+                if (g >= gEnd) continue;
+                if (j >= j0 && j + 8 <= j1) {
+                    StoreGroup<XT>(xg + j, o);
+                } else {
+                    for (int k = 0; k < 8; ++k) {
+                        if (j + k >= j0 && j + k < j1) xg[j + k] = o[k];
+                    }
                 }
             }
         }
