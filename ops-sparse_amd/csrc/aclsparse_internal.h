@@ -227,7 +227,7 @@ struct SpmvLayout {
     size_t task_cnt_offset = 0, task_scan_offset = 0, task_scan_bytes = 0;
     // Staged gather (non-transpose, fp32 compute, fp32/fp16/bf16 values; see
     // StageEligible): Preprocess cuts the matrix into merge-path tiles of
-    // kStageTileItems rows+entries and buckets every entry by the x segment
+    // StageTileItems rows+entries and buckets every entry by the x segment
     // of its column (kStageSegmentBytes of x per bucket; bucket S holds
     // entries whose column is outside [0, cols)).  Sections:
     //   st_tile_row int32[T+1], st_tile_nnz int64[T+1]   merge-path tile corners
@@ -251,7 +251,7 @@ struct SpmvLayout {
     //   st_metric uint64            distinct x lines per tile, summed
     // The header's staged_flag says which path Preprocess chose.
     bool staged = false;
-    int64_t st_tiles = 0, st_parts = 0, st_part_size = 0;
+    int64_t st_tiles = 0, st_parts = 0, st_part_size = 0, st_tile_items = 0;
     int32_t st_buckets = 0, st_wshift = 0, st_value_bytes = 0;
     size_t st_tile_row_offset = 0, st_tile_nnz_offset = 0, st_counts_offset = 0, st_start_bm_offset = 0;
     size_t st_start_offset = 0, st_scan_offset = 0, st_scan_bytes = 0, st_perm_offset = 0, st_cl_offset = 0;
@@ -277,10 +277,17 @@ size_t TaskScanTempBytes(int64_t n);
 // kStageMinXBytes; Preprocess measures the columns' spread and keeps the row
 // kernels when x accesses are local (banded matrices).
 // ---------------------------------------------------------------------------
-#ifndef SPMV_STAGE_TILE_ITEMS
-#define SPMV_STAGE_TILE_ITEMS 8184
-#endif
-constexpr int64_t kStageTileItems = SPMV_STAGE_TILE_ITEMS;  // rows + entries per tile: <= 2047 groups of 4 entries
+// Rows + entries per merge-path tile: 8184 for fp32 staged gather, 16376
+// for fp16 / bf16 staged gather and for the column-bucketed transpose (the
+// larger tiles halve the per-tile run tables and lengthen the runs; fp32
+// staged gather measured faster with the smaller ones).  A tile's padded
+// slots stay below 65536 (uint16 slot numbers).
+constexpr int64_t kStageTileItemsNarrow = 8184;
+constexpr int64_t kStageTileItemsWide = 16376;
+inline int64_t StageTileItems(bool transpose, uint32_t valueBytes)
+{
+    return !transpose && valueBytes == 4U ? kStageTileItemsNarrow : kStageTileItemsWide;
+}
 constexpr int64_t kStageMinNnz = int64_t{1} << 25;
 constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
 constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS
@@ -313,7 +320,8 @@ inline uint64_t StageChunkSlots(uint32_t valueBytes) { return 8U / valueBytes; }
 // Upper bound of the staged slots (entries plus run padding) of a matrix.
 inline uint64_t StageSlotCap(uint64_t rows, uint64_t nnz, uint64_t buckets, uint32_t valueBytes)
 {
-    const uint64_t tiles = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+    const uint64_t items = static_cast<uint64_t>(StageTileItems(false, valueBytes));
+    const uint64_t tiles = (rows + nnz + items - 1) / items;
     return nnz + (StageChunkSlots(valueBytes) - 1U) * (buckets + 1U) * tiles;
 }
 
@@ -441,7 +449,9 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.st_wshift = BtBucketShift(cols, nnz);
         const uint64_t w = uint64_t{1} << l.st_wshift;
         l.st_buckets = static_cast<int32_t>((cols + w - 1) / w);
-        const uint64_t t = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+        l.st_tile_items = StageTileItems(transpose, stageValueBytes);
+        const uint64_t items = static_cast<uint64_t>(l.st_tile_items);
+        const uint64_t t = (rows + nnz + items - 1) / items;
         l.st_tiles = static_cast<int64_t>(t);
         const size_t cells = static_cast<size_t>(l.st_buckets + 1) * static_cast<size_t>(t + 1);
         const size_t n8 = static_cast<size_t>(nnz) + 8;
@@ -465,7 +475,9 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         while ((uint64_t{1} << shift) < w) ++shift;
         l.st_wshift = shift;
         l.st_buckets = static_cast<int32_t>((cols + w - 1) / w);
-        const uint64_t t = (rows + nnz + kStageTileItems - 1) / kStageTileItems;
+        l.st_tile_items = StageTileItems(transpose, stageValueBytes);
+        const uint64_t items = static_cast<uint64_t>(l.st_tile_items);
+        const uint64_t t = (rows + nnz + items - 1) / items;
         l.st_tiles = static_cast<int64_t>(t);
         // pass A covers the padded slots: at most slotCap (their count is
         // known on the device only; workgroups past it exit)

@@ -55,23 +55,28 @@ constexpr int kWave = 64;
 constexpr int kSortThreads = 512;                       // per-tile preprocess kernels
 constexpr int kTileThreads = SPMV_STAGE_TILE_THREADS;   // pass B
 constexpr int kTileWaves = kTileThreads / kWave;
-constexpr int kTileItems = static_cast<int>(kStageTileItems);
-constexpr int kSortIpt = 16;                            // 512 x 16 = 8192 >= kTileItems keys per tile
 constexpr int kGatherThreads = 1024;                    // pass A
 #ifndef SPMV_STAGE_GATHER_BATCH
 #define SPMV_STAGE_GATHER_BATCH 4
 #endif
 constexpr int kGatherBatch = SPMV_STAGE_GATHER_BATCH;   // pass A: groups of 8 slots per thread per round
 constexpr int kLongRow = 32;                            // in-tile rows longer than this are summed by a wave
-constexpr int kMaxLong = kTileItems / kLongRow + 1;
 constexpr int CeilDiv(int a, int b) { return (a + b - 1) / b; }
-constexpr int kGroupSlots = CeilDiv((kTileItems + 3) / 4 + 1, kTileThreads);  // groups of 4 entries per thread
 constexpr int kScanIpt = CeilDiv(kStageMaxBuckets + 1, kTileThreads);         // run lengths per thread
-constexpr int kStageLanes = CeilDiv(kTileItems, kTileThreads);                // staged 64-slot windows per wave
-constexpr int kWindows = (kTileItems + 63) / 64;        // 64-slot windows of a tile
+constexpr int kNarrow = static_cast<int>(kStageTileItemsNarrow);
+constexpr int kWide = static_cast<int>(kStageTileItemsWide);
 
-static_assert(kSortThreads * kSortIpt >= kTileItems, "sort capacity");
-static_assert(kTileWaves * kStageLanes * kWave >= kTileItems, "staging capacity");
+// Per-tile shapes of a tile of kItems rows + entries.
+template <int kItems>
+struct Tile {
+    static constexpr int kSortIpt = CeilDiv(kItems, kSortThreads);                  // keys per thread of the sort
+    static constexpr int kMaxLong = kItems / kLongRow + 1;                          // long rows of a tile
+    static constexpr int kGroupSlots = CeilDiv((kItems + 3) / 4 + 1, kTileThreads);  // groups of 4 entries per thread
+    static constexpr int kStageLanes = CeilDiv(kItems, kTileThreads);               // 64-slot windows per wave
+    static constexpr int kWindows = (kItems + 63) / 64;                             // 64-slot windows of a tile
+    static_assert(kTileWaves * kStageLanes * kWave >= kItems, "staging capacity");
+    static_assert(kItems + 3 * (kStageMaxBuckets + 1) < 65536, "uint16 slot numbers");
+};
 
 struct StageParams {
     const void* norm;  // normalised row offsets, RowT[rows+2]
@@ -85,6 +90,7 @@ struct StageParams {
     void* y;
     int64_t rows, cols, nnz;
     int64_t tiles;  // T
+    int64_t tile_items;  // rows + entries per tile
     int32_t* tile_row;
     int64_t* tile_nnz;
     uint32_t* counts;
@@ -142,7 +148,7 @@ __device__ __forceinline__ uint32_t KeyOf(const StageParams& q, int32_t rawCol)
 // ------------------------------- preprocess ---------------------------------
 
 // Corner (row, entry) of every tile on the merge path of row ends and
-// entries (Merrill & Garland, SC'16): tile t starts at diagonal t*kTileItems.
+// entries (Merrill & Garland, SC'16): tile t starts at diagonal t*tile_items.
 template <typename RowT>
 __global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
 {
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
     if (t == 0) *q.metric = 0ULL;
     if (t > q.tiles) return;
     const int64_t total = q.rows + q.nnz;
-    const int64_t d = t * kTileItems < total ? t * kTileItems : total;
+    const int64_t d = t * q.tile_items < total ? t * q.tile_items : total;
     int64_t lo = d - q.nnz > 0 ? d - q.nnz : 0;
     int64_t hi = d < q.rows ? d : q.rows;
     while (lo < hi) {
@@ -209,9 +215,10 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
 // padded bucket-ordered runs, cl[start(t,s) + rank] = column within the
 // bucket (0 in the runs' padding); adds the tile's count of distinct x lines
 // to the metric.
-template <int kEndBit>
+template <int kItems, int kEndBit>
 __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
 {
+    constexpr int kSortIpt = Tile<kItems>::kSortIpt;
     using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
     using Scan = hipcub::BlockScan<uint32_t, kSortThreads>;
     constexpr int kRunIpt = (kStageMaxBuckets + 1 + kSortThreads - 1) / kSortThreads;
@@ -468,13 +475,17 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
 }
 
 // One workgroup per tile (XCD-contiguous).  LDS: the run map (runDelta,
-// startBits, firstRank), then one area of kTileItems+8 words that holds the
-// staged x values, then (in place) the products by groups of 4 entries,
-// followed by the tile's row offsets relative to the first group.  Six waves
-// per SIMD: three workgroups per CU, as many as the LDS allows.
-template <typename RowT, ValKind V, OutKind O>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6))) void StageTileKernel(StageParams q)
+// startBits, firstRank), then one area (at least kItems+8 words) that holds
+// the staged x values, then (in place) the products by groups of 4 entries,
+// followed by the tile's row offsets relative to the first group.  As many
+// waves per SIMD as the LDS allows: six for the narrow tiles (three
+// workgroups per CU), four for the wide ones.
+template <int kItems, typename RowT, ValKind V, OutKind O>
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kNarrow ? 6 : 4))) void StageTileKernel(StageParams q)
 {
+    constexpr int kTileItems = kItems;
+    constexpr int kMaxLong = Tile<kItems>::kMaxLong;
+    constexpr int kGroupSlots = Tile<kItems>::kGroupSlots;
     using SV = StageVal<V>;
     using Raw = typename SV::Raw;
     using Group = typename SV::Group;
@@ -837,9 +848,10 @@ __global__ __launch_bounds__(kSortThreads) void BtCountKernel(StageParams q)
 // Per tile: stable sort of the entries by bucket; perm[k] = slot of entry k
 // in the tile's bucket-ordered runs; cl[start(t,b) + rank] = the entry's
 // place in bucket b's column-ordered products.
-template <typename RowT>
+template <int kItems, typename RowT>
 __global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
 {
+    constexpr int kSortIpt = Tile<kItems>::kSortIpt;
     using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
     __shared__ typename Sort::TempStorage sortStorage;
     __shared__ uint32_t firstSlot[kBtMaxBuckets + 1];
@@ -927,9 +939,14 @@ __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
 }
 
 // Pass 1: products of one tile into its runs (see above).
-template <typename RowT>
+template <int kItems, typename RowT>
 __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
 {
+    constexpr int kTileItems = kItems;
+    constexpr int kMaxLong = Tile<kItems>::kMaxLong;
+    constexpr int kGroupSlots = Tile<kItems>::kGroupSlots;
+    constexpr int kStageLanes = Tile<kItems>::kStageLanes;
+    constexpr int kWindows = Tile<kItems>::kWindows;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
     __shared__ uint32_t runDelta[kBtMaxBuckets + 1];
     __shared__ uint32_t startBits[2 * kWindows];
@@ -1234,6 +1251,7 @@ StageParams MakeStageParams(const SpmvLaunch& l)
     q.metric = At<unsigned long long>(l.ws, L.st_metric_offset);
     q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
     q.part = L.st_part_size;
+    q.tile_items = L.st_tile_items;
     q.chunk = L.st_value_bytes > 0 ? static_cast<int32_t>(StageChunkSlots(static_cast<uint32_t>(L.st_value_bytes))) : 1;
     q.colptr = At<void>(l.ws, L.colptr_offset);
     q.csc_pos = At<void>(l.ws, L.csc_pos_offset);
@@ -1253,7 +1271,13 @@ unsigned XcdGrid(int64_t n) { return static_cast<unsigned>((n + kXcds - 1) / kXc
 template <int kEndBit>
 void LaunchSort(const StageParams& q, hipStream_t s)
 {
-    hipLaunchKernelGGL((StageSortKernel<kEndBit>), dim3(static_cast<unsigned>(q.tiles)), dim3(kSortThreads), 0, s, q);
+    if (q.tile_items == kWide) {
+        hipLaunchKernelGGL((StageSortKernel<kWide, kEndBit>), dim3(static_cast<unsigned>(q.tiles)), dim3(kSortThreads),
+                           0, s, q);
+    } else {
+        hipLaunchKernelGGL((StageSortKernel<kNarrow, kEndBit>), dim3(static_cast<unsigned>(q.tiles)),
+                           dim3(kSortThreads), 0, s, q);
+    }
 }
 
 template <typename RowT>
@@ -1309,7 +1333,7 @@ int BtPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL(StageTransposeKernel,
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
-    hipLaunchKernelGGL((BtSortKernel<RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
+    hipLaunchKernelGGL((BtSortKernel<kWide, RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
     hipLaunchKernelGGL((BtCscRowKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
     hipLaunchKernelGGL((BtDecideKernel<RowT>), dim3(1), dim3(256), 0, s, q);
     return 0;
@@ -1319,7 +1343,8 @@ template <typename RowT>
 void BtComputeTyped(const SpmvLaunch& l, hipStream_t s)
 {
     const StageParams q = MakeStageParams(l);
-    hipLaunchKernelGGL((BtScatterKernel<RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads), 0, s, q);
+    hipLaunchKernelGGL((BtScatterKernel<kWide, RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads), 0, s,
+                       q);
     hipLaunchKernelGGL((BtColumnKernel<RowT>), dim3(XcdGrid(l.layout.st_buckets)), dim3(kBtColThreads), 0, s, q);
 }
 
@@ -1330,7 +1355,9 @@ void LaunchStagedTyped(const SpmvLaunch& l, const StageParams& q, hipStream_t s)
     const SpmvLayout& L = l.layout;
     hipLaunchKernelGGL((StageGatherKernel<Raw>), dim3(XcdGrid(L.st_parts)), dim3(kGatherThreads),
                        static_cast<unsigned>(kStageSegmentBytes), s, q);
-    hipLaunchKernelGGL((StageTileKernel<RowT, V, O>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads), 0, s, q);
+    // fp32 values: the narrow tiles; fp16 / bf16: the wide ones (StageTileItems)
+    constexpr int kItems = V == ValKind::F32 ? kNarrow : kWide;
+    hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads), 0, s, q);
     hipLaunchKernelGGL((StageFixupKernel<RowT, O>), dim3(static_cast<unsigned>((L.st_tiles + 255) / 256)), dim3(256),
                        0, s, q);
 }

@@ -65,27 +65,32 @@ def algorithmic_bytes(w):
     return rb * (w.rows + 1) + (4 + vb) * w.nnz + vb * x_len + y_bytes
 
 
-STAGE_TILE_ITEMS = 8184          # rows + entries per merge-path tile of the staged path
 STAGE_SEGMENT_BYTES = 128 * 1024  # x per bucket of the staged path
 
 
 def staged_bytes(w):
     """Bytes one SpMV moves on the staged-gather path (its design traffic).
 
-    Pass A reads every entry's column within its bucket (2 B) and writes the
-    gathered x value (vb), reading x once; pass B reads the values, every
-    entry's slot (2 B) and the gathered x value again, the normalised row
+    Pass A reads every staged slot's column within its bucket (2 B) and
+    writes the gathered x value (vb), reading x once; pass B reads the values,
+    every entry's slot (2 B) and the staged x values again, the normalised row
     offsets, the run table (4 B per tile and bucket) and y; col_ind is not
-    read at all after Preprocess.
+    read at all after Preprocess.  Staged slots are the entries plus the
+    padding of every (tile, bucket) run to whole 8-byte chunks (half a chunk
+    less one slot per run on average).  Tiles hold 8184 rows + entries for
+    fp32 values and 16376 for fp16 / bf16.
     """
     vb = _elem_bytes(w.values.dtype)
     ob = _elem_bytes(w.out_dtype)
     rb = 8 if w.row_ptr.dtype == torch.int64 else 4
-    tiles = -(-(w.rows + w.nnz) // STAGE_TILE_ITEMS)
+    items = 8184 if vb == 4 else 16376
+    tiles = -(-(w.rows + w.nnz) // items)
     buckets = -(-(w.cols * vb) // STAGE_SEGMENT_BYTES) + 1
+    chunk = 8 // vb
+    slots = w.nnz + (chunk - 1) / 2 * buckets * tiles
     y_bytes = ob * w.rows * (2 if w.beta != 0 else 1)
-    return (rb * (w.rows + 2) + (vb + 2 + vb + 2 + vb) * w.nnz + vb * w.cols + y_bytes
-            + 4 * (tiles + 1) * buckets)
+    return int(rb * (w.rows + 2) + (2 + vb) * slots + (vb + 2) * w.nnz + vb * slots + vb * w.cols + y_bytes
+               + 4 * (tiles + 1) * buckets)
 
 
 def flops(w):

@@ -19,7 +19,11 @@ from ops_sparse.spmv import CsrSpMV
 pytestmark = pytest.mark.gpu
 
 STAGE_MIN_NNZ = 1 << 25
-TILE_ITEMS = 8184
+
+
+def tile_items(values):
+    """Rows + entries per merge-path tile: 8184 for fp32 values, 16376 for fp16 / bf16."""
+    return 8184 if values.dtype == torch.float32 else 16376
 
 
 def header(plan):
@@ -67,7 +71,7 @@ def check_tiles(w, plan):
     flag, buckets, tiles, tr_off, tn_off = header(plan)
     rp = w.row_ptr.cpu().numpy().astype(np.int64)
     rp = rp - rp[0]
-    r_ref, e_ref = oracle.merge_path_tiles(rp, TILE_ITEMS)
+    r_ref, e_ref = oracle.merge_path_tiles(rp, tile_items(w.values))
     assert tiles + 1 == r_ref.size
     ws = plan.workspace
     tr = np.frombuffer(ws[tr_off:tr_off + 4 * (tiles + 1)].cpu().numpy().tobytes(), dtype=np.int32)
