@@ -105,6 +105,7 @@ struct StageParams {
     uint32_t* flag;
     int64_t part;  // pass A: bucket-ordered slots per workgroup
     int32_t chunk; // staged slots per 8-byte chunk: runs are padded to a multiple
+    int32_t banded_ok;  // bucketed transpose: the one-pass banded kernel exists for this matrix
     // column-bucketed transpose
     const void* colptr;   // RowT[cols+1], column offsets of the CSC pattern
     const void* csc_pos;  // RowT[nnz], CSR index of each entry in column order
@@ -481,7 +482,7 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
 // waves per SIMD as the LDS allows: six for the narrow tiles (three
 // workgroups per CU), four for the wide ones.
 template <int kItems, typename RowT, ValKind V, OutKind O>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kNarrow ? 6 : 4))) void StageTileKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kNarrow ? 6 : kTileWaves / 2))) void StageTileKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
@@ -935,7 +936,7 @@ __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
         if (static_cast<int64_t>(colptr[c1]) - static_cast<int64_t>(colptr[c0]) > kBtRegionCap) ok = 0;
     }
     __syncthreads();
-    if (threadIdx.x == 0) *q.flag = scattered ? (ok != 0 ? 1U : 0U) : 2U;
+    if (threadIdx.x == 0) *q.flag = scattered ? (ok != 0 ? 1U : 0U) : (q.banded_ok != 0 ? 2U : 0U);
 }
 
 // Pass 1: products of one tile into its runs (see above).
@@ -1252,6 +1253,9 @@ StageParams MakeStageParams(const SpmvLaunch& l)
     q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
     q.part = L.st_part_size;
     q.tile_items = L.st_tile_items;
+    // the one-pass banded transpose: 32-bit row offsets and positions whose
+    // byte offsets fit a buffer resource (LaunchBandedTranspose)
+    q.banded_ok = !l.rowptr64 && l.nnz <= 0x1FFFFFFFLL ? 1 : 0;
     q.chunk = L.st_value_bytes > 0 ? static_cast<int32_t>(StageChunkSlots(static_cast<uint32_t>(L.st_value_bytes))) : 1;
     q.colptr = At<void>(l.ws, L.colptr_offset);
     q.csc_pos = At<void>(l.ws, L.csc_pos_offset);

@@ -181,3 +181,19 @@ def test_banded_conjugate_transpose_base1_beta0_ignores_nan_y(dev):
     assert header(plan)[0] == 2
     assert bool(torch.isfinite(y).all())
     assert_close(host(w), y)
+
+
+def test_banded_transpose_int64_offsets_keeps_the_csc_kernels(dev):
+    """The one-pass banded kernel takes 32-bit row offsets: with int64 offsets Preprocess keeps the
+    CSC kernels (flag 0) and the result is still right, on the first SpMV (every kernel set launched)
+    and once the choice is on the host."""
+    w = banded_workload(dev, n=1100)
+    w.row_ptr = w.row_ptr.to(torch.int64)
+    y, plan = run(w)
+    assert header(plan)[0] == 0
+    assert_close(w.to("cpu"), y)
+    first = y.clone()
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
