@@ -82,6 +82,7 @@ struct aclsparseSpMatDescr {
     // Created by the first staged Preprocess, released with the descriptor.
     uint32_t* staged_choice_host = nullptr;
     void* staged_choice_event = nullptr;
+    bool staged_choice_valid = false;  // the copy above belongs to the last Preprocess
 };
 
 struct aclsparseDnVecDescr {

@@ -201,9 +201,23 @@ bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
 // "unknown"; a previous copy is waited for first (it may be on another
 // stream).  Any failure leaves the choice unknown (SpMV then launches both
 // kernel sets, which read the device flag).
+bool Capturing(hipStream_t s)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;  // unknown: take the path that needs no host call
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
 void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
+    m->staged_choice_valid = false;
+    // Under stream capture no event, copy, wait or allocation is made: the
+    // choice stays unknown and every SpMV reads the device flag.
+    if (Capturing(s)) return;
     if (m->staged_choice_event != nullptr) {
         (void)hipEventSynchronize(static_cast<hipEvent_t>(m->staged_choice_event));
     } else {
@@ -229,15 +243,18 @@ void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
         hipEventRecord(static_cast<hipEvent_t>(m->staged_choice_event), s) != hipSuccess) {
         (void)hipGetLastError();
         *m->staged_choice_host = 0xFFFFFFFFU;
+        return;
     }
+    m->staged_choice_valid = true;
 }
 
 // The path of the matching staged Preprocess if its copy has completed
 // (0 the row / CSC kernels, 1 the staged or column-bucketed kernels, 2 the
 // banded transpose kernel), else -1.
-int32_t StagedChoice(const aclsparseSpMatDescr* m)
+int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
 {
-    if (m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
+    if (!m->staged_choice_valid || m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
+    if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
     if (hipEventQuery(static_cast<hipEvent_t>(m->staged_choice_event)) != hipSuccess) {
         (void)hipGetLastError();
         return -1;
@@ -427,7 +444,7 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
     if (!planned && aclsp::LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     // pass A reads x as 16-byte vectors
     l.staged = planned && m->rows > 0U && m->plan.staged && Aligned16(vecX->values) ? 1 : 0;
-    l.staged_choice = l.staged ? StagedChoice(m) : -1;
+    l.staged_choice = l.staged ? StagedChoice(m, stream) : -1;
     if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }

@@ -199,3 +199,59 @@ def test_staged_device_scalars_and_beta_zero_ignores_nan_y(dev):
     assert header(plan)[0] == 1
     assert bool(torch.isfinite(y).all())
     assert_close(w.to("cpu"), y)
+
+
+def _graph_matches_eager(w, dev, op=None):
+    """Preprocess, an eager SpMV, then the SpMV captured in a HIP graph and replayed three times with
+    eager SpMVs between the replays: every replay equals the eager result bit for bit.  Under capture
+    the library makes no host calls on the stream (no event query): the captured SpMV launches every
+    kernel set, each reading the path flag Preprocess left on the device."""
+    from ops_sparse._lib import Operation
+    op = Operation.NON_TRANSPOSE if op is None else op
+    s = torch.cuda.Stream()
+    y = w.y0.to(w.out_dtype).clone()
+    with torch.cuda.stream(s):
+        plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op,
+                       base=w.meta.get("base", 0))
+        plan.preprocess()
+        plan.run()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    y.copy_(w.y0.to(w.out_dtype))
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        plan.run()
+    bits = (lambda t: t.view(torch.int16)) if eager.element_size() == 2 else (lambda t: t.view(torch.int32))
+    for _ in range(3):
+        y.copy_(w.y0.to(w.out_dtype))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y), bits(eager))
+        y.copy_(w.y0.to(w.out_dtype))
+        with torch.cuda.stream(s):  # eager work between replays
+            plan.run()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y), bits(eager))
+    return plan
+
+
+def test_staged_spmv_in_a_hip_graph(dev):
+    rows, cols = 1 << 20, 1 << 22
+    w = random_rows(dev, rows, cols, lengths_for("uniform32", rows), torch.float16, torch.int64, 1.0, 0.5)
+    plan = _graph_matches_eager(w, dev)
+    assert header(plan)[0] == 1
+
+
+@pytest.mark.parametrize("kind", ["bucketed", "banded"])
+def test_transposes_in_a_hip_graph(kind, dev):
+    from ops_sparse._lib import Operation
+    if kind == "bucketed":
+        w = wl.poisson_transpose(rows=1 << 20).to(dev)
+    else:
+        w = wl.laplacian_2d(n=1536).to(dev)
+        w.trans = "T"
+    plan = _graph_matches_eager(w, dev, Operation.TRANSPOSE)
+    assert header(plan)[0] == (1 if kind == "bucketed" else 2)
