@@ -292,10 +292,7 @@ inline int64_t StageTileItems(bool transpose, uint32_t valueBytes)
 constexpr int64_t kStageMinNnz = int64_t{1} << 25;
 constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
 constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS
-#ifndef SPMV_STAGE_MAX_BUCKETS
-#define SPMV_STAGE_MAX_BUCKETS 1024
-#endif
-constexpr int32_t kStageMaxBuckets = SPMV_STAGE_MAX_BUCKETS;
+constexpr int32_t kStageMaxBuckets = 1024;  // x up to 128 MiB
 constexpr int64_t kStageMinParts = 512;           // pass A workgroups (two per CU at least)
 constexpr int64_t kStagePartTarget = int64_t{1} << 21;  // slots per pass A workgroup beyond that
 // Staged gather decision: the staged path is chosen when the tiles' distinct
