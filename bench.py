@@ -166,11 +166,11 @@ def measure(w, steps, warmup, flush_buf):
     p1.record(stream)
     torch.cuda.synchronize()
     pre_ms = p0.elapsed_time(p1)
-    # the path Preprocess chose: staged-gather flag in the workspace header
-    staged = False
+    # the path Preprocess chose: the path flag in the workspace header
+    path = "row kernels" if w.trans == "N" else "transpose"
     if w.trans == "N" and plan.workspace is not None and plan.workspace.numel() >= 192:
         head = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
-        staged = bool(head[16] & 0xFFFFFFFF)
+        path = {1: "staged gather", 3: NARROW_PATH}.get(int(head[16] & 0xFFFFFFFF), path)
 
     sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
 
@@ -214,8 +214,7 @@ def measure(w, steps, warmup, flush_buf):
     warm = _timed(stream, plan.run, steps)
     return dict(median_ms=ev, p90_ms=ev_p90, dirty_flush_ms=ev_dirty, paired_ms=statistics.median(diffs), paired_min_ms=min(diffs),
                 paired_max_ms=max(diffs), wall_ms_per_step=wall, warm_ms=warm, preprocess_ms=pre_ms,
-                workspace_bytes=plan.buffer_size, path=("staged gather" if staged else
-                                                        "row kernels" if w.trans == "N" else "transpose"))
+                workspace_bytes=plan.buffer_size, path=path)
 
 
 def graph_ms(w, launches=1000, replays=5):
@@ -410,6 +409,7 @@ def cpu_baseline(w, seconds):
             "cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
 
 
+NARROW_PATH = "row kernels, narrow columns"
 LINE_RATE = 64e9  # 128-byte lines per second from the MALL (random x gathers), measured on MI355X
 
 
@@ -417,12 +417,15 @@ def ceilings(w, nbytes, path):
     """Lower bounds on one SpMV's time (ms): algorithmic bytes at 8 TB/s; one
     MALL line per x gather at the measured line rate (the bound of gathering
     x straight from memory when x exceeds an XCD's L2); and, on the staged
-    path, its own design traffic at 8 TB/s."""
+    path, its own design traffic at 8 TB/s; on the narrow-column row kernel,
+    its bytes (2-byte instead of 4-byte column indices) at 8 TB/s."""
     from ops_sparse.workloads import staged_bytes
 
     c = {"algorithmic_hbm": nbytes / (HBM_PEAK_GBS * 1e6), "random_line_gathers": w.nnz / LINE_RATE * 1e3}
     if path == "staged gather":
         c["staged_traffic_hbm"] = staged_bytes(w) / (HBM_PEAK_GBS * 1e6)
+    if path == NARROW_PATH:
+        c["narrow_traffic_hbm"] = (nbytes - 2 * w.nnz) / (HBM_PEAK_GBS * 1e6)
     return c
 
 
@@ -466,9 +469,11 @@ def main():
                  gflops=flops(w) / (m["median_ms"] * 1e-3) / 1e9,
                  warm_gbs=nbytes / (m["warm_ms"] * 1e-3) / 1e9, **m)
         r["ceilings_ms"] = ceilings(w, nbytes, m["path"])
-        r["bound"] = "staged traffic at 8 TB/s" if m["path"] == "staged gather" else "hbm"
-        r["frac_of_bound"] = (r["ceilings_ms"]["staged_traffic_hbm"] if m["path"] == "staged gather"
-                              else r["ceilings_ms"]["algorithmic_hbm"]) / m["median_ms"]
+        bound_key = {"staged gather": "staged_traffic_hbm", NARROW_PATH: "narrow_traffic_hbm"}.get(
+            m["path"], "algorithmic_hbm")
+        r["bound"] = {"staged_traffic_hbm": "staged traffic at 8 TB/s",
+                      "narrow_traffic_hbm": "narrow-column traffic at 8 TB/s"}.get(bound_key, "hbm")
+        r["frac_of_bound"] = r["ceilings_ms"][bound_key] / m["median_ms"]
         if name == "c1":
             r["graph_ms"] = graph_ms(w)
             r["graph_gbs"] = nbytes / (r["graph_ms"] * 1e-3) / 1e9

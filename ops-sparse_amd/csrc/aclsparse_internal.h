@@ -60,6 +60,7 @@ struct SpmvPlan {
     aclrtStream stream = nullptr;
     uint64_t stream_epoch = 0;
     bool staged = false;  // Preprocess built the staged-gather tables in the buffer
+    bool narrow = false;  // Preprocess built the narrow column copy (if every entry fits)
 };
 
 struct aclsparseSpMatDescr {
@@ -154,15 +155,19 @@ struct SpmvWsHeader {
     uint64_t task_start_offset;  // 0 when the plan has no task table
     uint64_t task_block_offset;
     uint64_t max_tasks;
-    // staged gather (0 when the plan has none): the path Preprocess chose
-    // (1 = staged kernels, 0 = row kernels), the bucket and tile counts and
-    // where the tile corners are
+    // the path Preprocess chose (0 when the plan has no choice): 0 = row /
+    // CSC kernels, 1 = staged gather or column-bucketed transpose, 2 = banded
+    // one-pass transpose, 3 = row kernels on the narrow column copy; the
+    // staged bucket and tile counts and where the tile corners are
     uint32_t staged_flag;
     uint32_t staged_buckets;
     uint64_t staged_tiles;
     uint64_t staged_tile_row_offset;
     uint64_t staged_tile_nnz_offset;
-    uint32_t reserved[8];
+    // narrow columns: nonzero when some entry's column is too far from its
+    // row block's first row for 16 bits (set by Preprocess)
+    uint32_t narrow_bad;
+    uint32_t reserved[7];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 
@@ -257,6 +262,14 @@ struct SpmvLayout {
     size_t st_tile_row_offset = 0, st_tile_nnz_offset = 0, st_counts_offset = 0, st_start_bm_offset = 0;
     size_t st_start_offset = 0, st_scan_offset = 0, st_scan_bytes = 0, st_perm_offset = 0, st_cl_offset = 0;
     size_t st_xg_offset = 0, st_head_offset = 0, st_tail_offset = 0, st_metric_offset = 0;
+    // Narrow columns (non-transpose, the stream kernel's value types): each
+    // entry's column as a signed 16-bit offset from the first row of its row
+    // block, nc int16[nnz+8], written by Preprocess when every entry fits
+    // (the header's staged_flag then reads 3).  The row kernel then streams
+    // 2 bytes per entry of column data instead of 4.  With the staged tables
+    // it overlays st_cl: only one of the two paths is ever chosen.
+    bool narrow = false;
+    size_t nc_offset = 0;
 };
 
 #ifndef SPMV_LONG_CHUNKS
@@ -310,6 +323,10 @@ inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
     if (valueType == ACL_FLOAT16 || valueType == ACL_BF16) return 2U;
     return 0U;
 }
+
+// Narrow columns are built for matrices of at least this many entries.
+constexpr int64_t kNarrowMinNnz = int64_t{1} << 20;
+constexpr int32_t kNarrowFlag = 3;  // staged_flag value of the narrow-column row kernel
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run
 // of staged slots is padded to a multiple of this many slots.
@@ -505,6 +522,16 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.st_metric_offset = AlignUp(l.st_tail_offset + static_cast<size_t>(t) * sizeof(float));
         l.total = AlignUp(l.st_metric_offset + sizeof(uint64_t));
     }
+    if (!transpose && stageValueBytes != 0U && computeType == ACL_FLOAT && rows > 0 &&
+        nnz >= static_cast<uint64_t>(kNarrowMinNnz)) {
+        l.narrow = true;
+        if (l.staged) {
+            l.nc_offset = l.st_cl_offset;  // st_cl holds at least nnz + 8 uint16
+        } else {
+            l.nc_offset = AlignUp(l.total);
+            l.total = AlignUp(l.nc_offset + (static_cast<size_t>(nnz) + 8) * sizeof(int16_t));
+        }
+    }
     return l;
 }
 
@@ -560,9 +587,12 @@ struct SpmvLaunch {
     // staged gather: Preprocess builds its tables; SpMV launches its kernels
     // (which check the path flag Preprocess left in the header)
     int32_t staged;
-    // with staged: the path Preprocess chose, if known on the host (0 row /
-    // CSC kernels, 1 staged or column-bucketed kernels, 2 banded transpose
-    // kernel), or -1: launch every set, each runs only on its flag value
+    // narrow columns: Preprocess may have written the 16-bit column copy
+    int32_t narrow;
+    // with staged or narrow: the path Preprocess chose, if known on the host
+    // (0 row / CSC kernels, 1 staged or column-bucketed kernels, 2 banded
+    // transpose kernel, 3 narrow-column row kernel), or -1: launch every
+    // set, each runs only on its flag values
     int32_t staged_choice;
 };
 

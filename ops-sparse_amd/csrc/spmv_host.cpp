@@ -195,7 +195,18 @@ bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values);
 }
 
-// After a staged Preprocess: copy the path flag it leaves in the workspace
+// The narrow column copy is built when the layout has it and the row kernel
+// would stream this matrix: unit strides, 16-byte aligned column indices and
+// values, x addressable with 32-bit byte offsets.
+bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
+                  const aclsparseDnVecDescr* y)
+{
+    return l.narrow && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
+           x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values) &&
+           m->cols * static_cast<uint64_t>(l.st_value_bytes != 0 ? l.st_value_bytes : 4) <= 0x7FFFFFFFULL;
+}
+
+// After a staged or narrow Preprocess: copy the path flag it leaves in the workspace
 // header to pinned host memory and record an event after the copy.  The
 // host value starts as a sentinel, so a copy that has not run reads as
 // "unknown"; a previous copy is waited for first (it may be on another
@@ -250,7 +261,7 @@ void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 
 // The path of the matching staged Preprocess if its copy has completed
 // (0 the row / CSC kernels, 1 the staged or column-bucketed kernels, 2 the
-// banded transpose kernel), else -1.
+// banded transpose kernel, 3 the narrow-column row kernel), else -1.
 int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
 {
     if (!m->staged_choice_valid || m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
@@ -260,7 +271,7 @@ int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
         return -1;
     }
     const uint32_t v = *static_cast<volatile const uint32_t*>(m->staged_choice_host);
-    return v <= 2U ? static_cast<int32_t>(v) : -1;
+    return v <= static_cast<uint32_t>(aclsp::kNarrowFlag) ? static_cast<int32_t>(v) : -1;
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
@@ -400,20 +411,23 @@ aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOpe
     if (m->rows > 0U && m->ptrs == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
     st = ValidateWorkspace(externalBuffer);
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
-    bool staged = false;
+    bool staged = false, narrow = false;
     if (m->rows > 0U) {
         (void)hipGetLastError();
         aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
         staged = StageUsable(l.layout, m, vecX, vecY);
+        narrow = NarrowUsable(l.layout, m, vecX, vecY);
         l.staged = staged ? 1 : 0;
+        l.narrow = narrow ? 1 : 0;
         if (aclsp::LaunchSpmvPreprocess(l, HipStreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
             m->plan = SpmvPlan{};
             return ACL_SPARSE_STATUS_EXECUTION_FAILED;
         }
-        if (staged) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
+        if (staged || narrow) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
     }
     m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
     m->plan.staged = staged;
+    m->plan.narrow = narrow;
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
@@ -444,7 +458,8 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
     if (!planned && aclsp::LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     // pass A reads x as 16-byte vectors
     l.staged = planned && m->rows > 0U && m->plan.staged && Aligned16(vecX->values) ? 1 : 0;
-    l.staged_choice = l.staged ? StagedChoice(m, stream) : -1;
+    l.narrow = planned && m->rows > 0U && m->plan.narrow ? 1 : 0;
+    l.staged_choice = l.staged || l.narrow ? StagedChoice(m, stream) : -1;
     if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }
@@ -475,6 +490,7 @@ aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t
     SpmvLaunch l = MakeLaunch(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg, ws);
     l.layout = layout;
     l.staged = 0;
+    l.narrow = 0;
     void* stream = HipStreamOf(handle);
     (void)hipGetLastError();
     if (matA->rows > 0U && LaunchSpmvPreprocess(l, stream) != 0) return ACL_SPARSE_STATUS_EXECUTION_FAILED;

@@ -113,12 +113,14 @@ struct RowBlockParams {
     float* z;            // SpMVOp: output (y is then only read)
     int64_t rp_base;     // subtracted from p.rp entries (0 for the normalised copy)
     int32_t fixed_rows;  // SpMVOp ALG1: rows per block, blocks taken straight from p.rp
-    // When set, the kernel exits at once unless the word equals run_flag:
-    // Preprocess chose another path for this matrix (the staged gather, the
-    // column-bucketed or the one-pass banded transpose), whose kernels are
-    // launched beside this one.
+    // When set, the stream kernel exits at once unless bit (word) of run_mask
+    // is set: Preprocess chose another path for this matrix (the staged
+    // gather, the column-bucketed or the one-pass banded transpose, the
+    // narrow columns), whose kernels are launched beside this one.
     const uint32_t* skip_flag;
-    uint32_t run_flag;
+    uint32_t run_mask;
+    // narrow columns: column - base - (first row of the entry's block), int16[nnz]
+    const int16_t* ncol;
     // ValKind::GATH: the fp32 values the streamed positions index
     const float* gval;
     int64_t gval_n;
@@ -477,7 +479,17 @@ struct StreamLoad {
     uint32_t xg[kLaneItems];  // gathered x of the 8 slots
 };
 
-template <typename RowT, ValKind V, OutKind O, bool kBeta>
+// rb plus the signed 16-bit low / high half of w (wrapping 32-bit sums).
+__device__ __forceinline__ int32_t Lo16(int32_t w, uint32_t rb)
+{
+    return static_cast<int32_t>(rb + static_cast<uint32_t>(static_cast<int32_t>(static_cast<int16_t>(w & 0xFFFF))));
+}
+__device__ __forceinline__ int32_t Hi16(int32_t w, uint32_t rb)
+{
+    return static_cast<int32_t>(rb + static_cast<uint32_t>(w >> 16));
+}
+
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kNarrow = false>
 __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                                 StreamLoad<RowT, V, O>& b)
 {
@@ -492,13 +504,29 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
     end = end < tailStart ? end : tailStart;
     const int64_t avail = s.valid ? end - a0 : 0;
-    const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
-    // Lane-contiguous 16-byte groups: load h of lane l holds slots
+    // Lane-contiguous groups of 4 slots: load h of lane l holds slots
     // 256h + 4l .. 256h + 4l + 3, so each load instruction reads 1 KiB of
-    // col_ind (values: 1 KiB fp32, 512 B fp16) without gaps.
-    b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
-    b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    // col_ind (narrow columns 512 B; values: 1 KiB fp32, 512 B fp16) without
+    // gaps.
+    if constexpr (kNarrow) {
+        // 16-bit offsets from the block's first row; decoded to col_ind's
+        // values (the block is the one the chunk belongs to, so entries of
+        // the previous block read before the chunk decode to other columns,
+        // whose products are never summed)
+        const __amdgpu_buffer_rsrc_t rn = Rsrc(p.ncol + a0, avail * 2);
+        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, lane * 8, 0, kBufNonTemporal));
+        const v2i hi =
+            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, 512 + lane * 8, 0, kBufNonTemporal));
+        const uint32_t rb = static_cast<uint32_t>(s.r0) + static_cast<uint32_t>(p.base);
+        b.col[0] = v4i{Lo16(lo.x, rb), Hi16(lo.x, rb), Lo16(lo.y, rb), Hi16(lo.y, rb)};
+        b.col[1] = v4i{Lo16(hi.x, rb), Hi16(hi.x, rb), Lo16(hi.y, rb), Hi16(hi.y, rb)};
+    } else {
+        const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
+        b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
+        b.col[1] =
+            __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    }
     if constexpr (V == ValKind::UNIT) {
         (void)rv;  // no values
     } else if constexpr (V == ValKind::GATH) {
@@ -1015,10 +1043,11 @@ __device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const St
 // chunk-crossing rows; the block's last task to arrive combines them.
 //
 // kGated: the launch made when another path may have taken the matrix (the
-// decision is on the device only): the kernel exits when p.skip_flag reads
-// 1, and a capped grid loops over the blocks (block_stride).  Ungated
-// launches carry neither (one block per wave, no flag load).
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false>
+// decision is on the device only): the kernel exits unless p.skip_flag reads
+// a value whose bit is set in p.run_mask, and a capped grid loops over the
+// blocks (block_stride).  Ungated launches carry neither (one block per wave,
+// no flag load).  kNarrow: column indices from the narrow copy p.ncol.
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false, bool kNarrow = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(7)))
 void SpmvStreamFlatKernel(RowBlockParams p)
 {
@@ -1029,7 +1058,8 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
     if constexpr (kGated) {
-        if (ConstLoad<uint32_t>(p.skip_flag, 0) != p.run_flag) return;
+        const uint32_t flag = ConstLoad<uint32_t>(p.skip_flag, 0);
+        if (flag >= 32U || ((p.run_mask >> flag) & 1U) == 0U) return;
     }
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1061,7 +1091,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             cur.first = j == 0;
             ChunkBounds(cur);
             L bl;
-            StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, bl);
+            StreamLoadStage<RowT, V, O, kBeta, kNarrow>(p, cur, tailStart, lane, bl);
             StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, bl, bl.xg);
             float head = 0.0f, tail = 0.0f;
             StreamChunk<RowT, V, O, kBeta, true>(cur, bl, sVal, lane, alpha, beta, carry, lg, y, sink, &head, &tail);
@@ -1095,7 +1125,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
         carry = 0.0f;
         while (cur.valid) {
             L b;
-            StreamLoadStage<RowT, V, O, kBeta>(p, cur, tailStart, lane, b);
+            StreamLoadStage<RowT, V, O, kBeta, kNarrow>(p, cur, tailStart, lane, b);
             StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
             StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
             if (cur.last) break;
@@ -2037,6 +2067,8 @@ T* At(void* ws, size_t off) { return reinterpret_cast<T*>(static_cast<uint8_t*>(
 RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
 {
     RowBlockParams p{};
+    p.run_mask = 1U;  // gated launches: the row / CSC kernels' flag value 0
+    p.ncol = l.layout.narrow ? At<const int16_t>(l.ws, l.layout.nc_offset) : nullptr;
     p.rp = At<void>(l.ws, l.layout.rowptr_offset);
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
     p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
@@ -2100,6 +2132,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     hipStream_t stream_ = stream;
     if (l.staged && l.staged_choice == 1) return 0;  // Preprocess chose the staged kernels
     RowBlockParams p = MakeRowBlockParams(l);
+    const bool chosen = l.staged || l.narrow;  // Preprocess left a path choice in the header
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
     // The stream kernels read col_ind / values as 16-byte groups of arrays
@@ -2122,21 +2155,46 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             p.task_wgs = static_cast<int32_t>(taskWgs);
             p.task_waves = static_cast<int32_t>(taskWgs * kFlatWaves);
             int64_t blockWgs = (wgs + kXcds - 1) / kXcds * kXcds;
-            if (l.staged && l.staged_choice < 0) {
-                // The staged kernels may take this matrix (decided on the
-                // device, not yet known here): a capped grid keeps this
-                // launch cheap when it exits.
+            const dim3 wg(kWave * kFlatWaves);
+            const bool narrow = l.narrow && p.ncol != nullptr;
+            if (narrow && l.staged_choice == kNarrowFlag) {
+                const unsigned g = static_cast<unsigned>(taskWgs + blockWgs);
+                if (betaNz) {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, false, true>), dim3(g), wg, 0, stream_,
+                                       p);
+                } else {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, false, true>), dim3(g), wg, 0,
+                                       stream_, p);
+                }
+                return 0;
+            }
+            if (chosen && l.staged_choice < 0) {
+                // Another path may take this matrix (decided on the device,
+                // not yet known here): capped grids keep the launches that
+                // exit cheap.  The plain row kernel runs on flag 0, and on
+                // the flags of paths whose kernels are not launched here.
                 p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
+                p.run_mask = 1U | (l.staged ? 0U : 2U) | (narrow ? 0U : 1U << kNarrowFlag);
                 if (blockWgs > kStagedFallbackWgs) {
                     blockWgs = kStagedFallbackWgs;
                     p.block_stride = blockWgs * kFlatWaves;
                 }
             }
             const unsigned g = static_cast<unsigned>(taskWgs + blockWgs);
-            const dim3 wg(kWave * kFlatWaves);
             if (p.skip_flag != nullptr) {
                 if (betaNz) hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, true>), dim3(g), wg, 0, stream_, p);
                 else hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, true>), dim3(g), wg, 0, stream_, p);
+                if (narrow) {
+                    RowBlockParams q = p;
+                    q.run_mask = 1U << kNarrowFlag;
+                    if (betaNz) {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, true, true>), dim3(g), wg, 0,
+                                           stream_, q);
+                    } else {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, true, true>), dim3(g), wg, 0,
+                                           stream_, q);
+                    }
+                }
             } else if (betaNz) {
                 hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true>), dim3(g), wg, 0, stream_, p);
             } else {
@@ -2191,7 +2249,7 @@ void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStre
     c.gval = static_cast<const float*>(l.val);
     c.gval_n = l.nnz;
     c.skip_flag = kGated ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
-    c.run_flag = 2U;
+    c.run_mask = 1U << 2;
     const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
     const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
     const dim3 wg(kWave * kFlatWaves);
@@ -2431,6 +2489,67 @@ int BuildTasks(const SpmvLaunch& l, hipStream_t s)
     return 0;
 }
 
+// Narrow columns: one wave per row block writes each entry's column as a
+// signed 16-bit offset from the block's first row (nc[k] = col[k] - base -
+// r0); a wave that finds an entry out of that range sets narrow_bad.  Entries
+// outside every block (before the first row's offset or after the last) are
+// never summed and are not written.  Nothing is written when the staged
+// gather was chosen: its tables share the storage.
+struct NarrowParams {
+    const int32_t* blocks;
+    const void* block_nnz;
+    const int32_t* col;
+    int16_t* nc;
+    int64_t num_blocks;
+    int32_t base;
+    const uint32_t* flag;  // staged_flag
+    uint32_t* bad;         // narrow_bad
+};
+
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void NarrowColKernel(NarrowParams q)
+{
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (b >= q.num_blocks || *q.flag == 1U) return;
+    const int64_t rb = static_cast<int64_t>(q.blocks[b]) + q.base;
+    const RowT* bn = static_cast<const RowT*>(q.block_nnz);
+    const int64_t k1 = static_cast<int64_t>(bn[b + 1]);
+    bool bad = false;
+    for (int64_t k = static_cast<int64_t>(bn[b]) + lane; k < k1; k += kWave) {
+        const int64_t d = static_cast<int64_t>(q.col[k]) - rb;
+        bad |= d < -32768 || d > 32767;
+        q.nc[k] = static_cast<int16_t>(d);
+    }
+    if (__ballot(bad) != 0 && lane == 0) __hip_atomic_fetch_or(q.bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Flag 3 (the narrow-column row kernel) unless the staged gather was chosen
+// or some entry did not fit.
+__global__ void NarrowDecideKernel(uint32_t* flag, const uint32_t* bad)
+{
+    if (*flag != 1U && *bad == 0U) *flag = static_cast<uint32_t>(kNarrowFlag);
+}
+
+template <typename RowT>
+void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
+{
+    SpmvWsHeader* h = At<SpmvWsHeader>(l.ws, 0);
+    NarrowParams q{};
+    q.blocks = At<const int32_t>(l.ws, l.layout.blocks_offset);
+    q.block_nnz = At<const void>(l.ws, l.layout.block_nnz_offset);
+    q.col = l.col;
+    q.nc = At<int16_t>(l.ws, l.layout.nc_offset);
+    q.num_blocks = l.layout.num_blocks;
+    q.base = l.base;
+    q.flag = &h->staged_flag;
+    q.bad = &h->narrow_bad;
+    const unsigned grid = static_cast<unsigned>((q.num_blocks + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL((NarrowColKernel<RowT>), dim3(grid), dim3(kThreads), 0, s, q);
+    hipLaunchKernelGGL(NarrowDecideKernel, dim3(1), dim3(1), 0, s, &h->staged_flag,
+                       static_cast<const uint32_t*>(&h->narrow_bad));
+}
+
 template <typename RowT>
 int BuildCsc(const SpmvLaunch& l, hipStream_t s)
 {
@@ -2616,7 +2735,7 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
     h.task_start_offset = l.layout.tasks ? l.layout.task_start_offset : 0;
     h.task_block_offset = l.layout.tasks ? l.layout.task_block_offset : 0;
     h.max_tasks = l.layout.tasks ? static_cast<uint64_t>(l.layout.max_tasks) : 0;
-    if (l.staged) {  // staged_flag stays 0 until the staged preprocess decides
+    if (l.staged) {  // staged_flag stays 0 until the staged or narrow preprocess decides
         h.staged_buckets = static_cast<uint32_t>(l.layout.st_buckets);
         h.staged_tiles = static_cast<uint64_t>(l.layout.st_tiles);
         h.staged_tile_row_offset = l.layout.st_tile_row_offset;
@@ -2632,6 +2751,9 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
             return l.staged ? LaunchStagedPreprocess(l, stream) : 0;
         }
         if (l.layout.tasks && BuildTasks<int64_t>(l, s) != 0) return 1;
+        if (l.staged && LaunchStagedPreprocess(l, stream) != 0) return 1;
+        if (l.narrow && l.layout.narrow) BuildNarrow<int64_t>(l, s);
+        return 0;
     } else {
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) {
@@ -2639,9 +2761,10 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
             return l.staged ? LaunchStagedPreprocess(l, stream) : 0;
         }
         if (l.layout.tasks && BuildTasks<int32_t>(l, s) != 0) return 1;
+        if (l.staged && LaunchStagedPreprocess(l, stream) != 0) return 1;
+        if (l.narrow && l.layout.narrow) BuildNarrow<int32_t>(l, s);
+        return 0;
     }
-    if (l.staged) return LaunchStagedPreprocess(l, stream);
-    return 0;
 }
 
 int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)

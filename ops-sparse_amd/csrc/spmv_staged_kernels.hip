@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams 
 {
     extern __shared__ uint4 segRaw[];
     XT* seg = reinterpret_cast<XT*>(segRaw);
-    if (FlagSet(q.flag) == 0U) return;
+    if (FlagSet(q.flag) != 1U) return;
     const int64_t w = XcdIndex();
     const int nb = q.buckets + 1;
     const uint32_t* base = q.start;                  // row 0: first slot of every bucket
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     float alpha, beta;
     LoadScalars<AccKind::F32>(q.s, alpha, beta);
     asm volatile("" ::: "memory");
-    if (flag == 0U) return;
+    if (flag != 1U) return;
     const int E = static_cast<int>(e1 - e0);
     const int R = static_cast<int>(r1 - r0);
 
@@ -759,7 +759,7 @@ template <typename RowT, OutKind O>
 __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
 {
     using OutT = typename OutOf<O>::T;
-    if (FlagSet(q.flag) == 0U) return;
+    if (FlagSet(q.flag) != 1U) return;
     const int64_t t = blockIdx.x * int64_t{256} + threadIdx.x;
     if (t >= q.tiles) return;
     const int64_t r0 = q.tile_row[t];

@@ -1,0 +1,178 @@
+"""GPU parity of the narrow-column row kernel through the C ABI.
+
+For non-transpose matrices of at least 2^20 entries with fp32 / fp16 / bf16
+values and fp32 compute, Preprocess writes every entry's column as a signed
+16-bit offset from the first row of its row block when all of them fit, and
+the header's path flag then reads 3: the row kernel streams that copy (2
+bytes per entry) instead of col_ind (4 bytes).  The sums are the same
+operations in the same order as on col_ind, so each case checks the result
+against the oracle and bit for bit against the same SpMV without Preprocess
+(flag 0, col_ind streamed).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close
+from ops_sparse import workloads as wl
+from ops_sparse.spmv import CsrSpMV
+
+pytestmark = pytest.mark.gpu
+
+NARROW_MIN_NNZ = 1 << 20
+
+
+def flag(plan):
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint32)
+    return int(h[32]), int(h[40])  # staged_flag, narrow_bad
+
+
+def bits(t):
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
+
+
+def run(w, preprocess=True, y0=None, settle=True):
+    y = (w.y0 if y0 is None else y0).to(w.out_dtype).clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta,
+                   base=w.meta.get("base", 0))
+    if preprocess:
+        plan.preprocess()
+        if settle:
+            torch.cuda.synchronize()  # the path choice reaches the host: one kernel set launched
+    plan.run()
+    torch.cuda.synchronize()
+    return y, plan
+
+
+def host(w):
+    h = w.to("cpu")
+    b = w.meta.get("base", 0)
+    if b:
+        h.col_ind = h.col_ind - b
+        h.row_ptr = h.row_ptr - b
+    return h
+
+
+def check(w, expect_flag, y0=None):
+    """Oracle parity, the expected path, and bit equality with the col_ind kernel (no Preprocess)
+    and with the first SpMV after Preprocess (issued before the choice reached the host: every
+    kernel set launched, each gated on the device flag)."""
+    y, plan = run(w, y0=y0)
+    assert flag(plan)[0] == expect_flag
+    assert_close(host(w), y)
+    y_plain, plan0 = run(w, preprocess=False, y0=y0)
+    assert flag(plan0)[0] == 0
+    assert torch.equal(bits(y), bits(y_plain))
+    y_first, _ = run(w, y0=y0, settle=False)
+    assert torch.equal(bits(y), bits(y_first))
+    return y, plan
+
+
+def banded(dev, rows, band, vdtype=torch.float32, rdtype=torch.int32, base=0, alpha=1.25, beta=0.5, seed=4,
+           spread=1):
+    """Rows of `band` entries at columns row + spread*(j - band//2), clipped to the matrix."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    off = (torch.arange(band) - band // 2) * spread
+    col = (torch.arange(rows)[:, None] + off[None, :]).clamp(0, rows - 1).reshape(-1)
+    rp = torch.arange(0, rows * band + 1, band, dtype=torch.int64)
+    vals = (torch.rand(col.numel(), generator=g) * 2 - 1).to(vdtype)
+    x = (torch.rand(rows, generator=g) * 2 - 1).to(vdtype)
+    out = torch.float32 if vdtype == torch.float32 else vdtype
+    y0 = (torch.rand(rows, generator=g) * 2 - 1).to(out)
+    w = wl.Workload(f"banded{band}_{rows}", rows, rows, (rp + base).to(rdtype), (col + base).to(torch.int32),
+                    vals, x, y0, alpha, beta, out_dtype=out, meta={"base": base})
+    return w.to(dev)
+
+
+def test_laplacian_c2_takes_the_narrow_kernel(dev):
+    w = wl.laplacian_2d().to(dev)
+    check(w, 3)
+
+
+@pytest.mark.parametrize("vdtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_half_values_int64_offsets_base1(vdtype, dev):
+    w = banded(dev, rows=1 << 18, band=9, vdtype=vdtype, rdtype=torch.int64, base=1, spread=3000)
+    check(w, 3)
+
+
+def block_first_rows(plan, rows):
+    """First row of each row's block, from the partition Preprocess wrote (blocks int32[B+1])."""
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+    nb, off = int(h[5]), int(h[7])
+    blocks = np.frombuffer(plan.workspace[off:off + 4 * (nb + 1)].cpu().numpy().tobytes(), dtype=np.int32)
+    b = np.searchsorted(blocks[:nb], np.arange(rows), side="right") - 1
+    return torch.from_numpy(blocks[b].astype(np.int64))
+
+
+def test_offsets_at_the_16_bit_limits(dev):
+    """Columns at offsets -32768 and +32767 from the first row of their block fit; one more does not."""
+    rows, band = 1 << 17, 9
+    w = banded(dev, rows=rows, band=band, spread=1)
+    _, plan = run(w)
+    r0 = block_first_rows(plan, rows).to(dev)
+    col = w.col_ind.view(rows, band).clone()
+    lo, hi = r0 - 32768, r0 + 32767
+    col[:, 0] = torch.where(lo >= 0, lo, col[:, 0].to(torch.int64)).to(torch.int32)
+    col[:, -1] = torch.where(hi < rows, hi, col[:, -1].to(torch.int64)).to(torch.int32)
+    w.col_ind = col.reshape(-1).contiguous()
+    assert int((w.col_ind.view(rows, band)[:, 0].to(torch.int64) - r0).min()) == -32768
+    assert int((w.col_ind.view(rows, band)[:, -1].to(torch.int64) - r0).max()) == 32767
+    check(w, 3)
+    for delta in (-32769, 32768):
+        far = w.col_ind.clone()
+        i = rows // 2
+        c = int(r0[i]) + delta
+        assert 0 <= c < rows
+        far[i * band + (0 if delta < 0 else band - 1)] = c
+        w2 = wl.Workload(w.name, w.rows, w.cols, w.row_ptr, far, w.values, w.x, w.y0, w.alpha, w.beta,
+                         out_dtype=w.out_dtype, meta=w.meta)
+        y, plan = run(w2)
+        assert flag(plan) == (0, 1)
+        assert_close(host(w2), y)
+
+
+def test_long_rows_run_as_tasks(dev):
+    """Rows of 3000 entries within +-1500 columns: blocks of one row, split into chunk tasks."""
+    rows = 1 << 10
+    w = banded(dev, rows=rows, band=3001, spread=1, beta=0.0)
+    assert w.nnz >= NARROW_MIN_NNZ
+    y, _ = check(w, 3, y0=torch.full_like(w.y0, float("nan")))  # beta = 0: y is never read
+    assert bool(torch.isfinite(y).all())
+
+
+def test_entries_outside_the_rows_are_ignored(dev):
+    w = banded(dev, rows=1 << 18, band=5, spread=700)
+    lead = 5
+    w.row_ptr = w.row_ptr + lead
+    w.col_ind = torch.cat([torch.full((lead,), 1 << 30, dtype=torch.int32, device=dev), w.col_ind])
+    w.values = torch.cat([torch.full((lead,), 1e6, device=dev), w.values])
+    check(w, 3)
+
+
+def test_small_matrices_keep_col_ind(dev):
+    w = banded(dev, rows=1 << 16, band=5)
+    assert w.nnz < NARROW_MIN_NNZ
+    y, plan = run(w)
+    assert flag(plan)[0] == 0
+    assert_close(host(w), y)
+
+
+def test_values_updated_after_preprocess(dev):
+    """Preprocess reads the pattern only: new values and x are used by the next SpMV."""
+    w = banded(dev, rows=1 << 18, band=7, spread=100)
+    y, plan = run(w)
+    assert flag(plan)[0] == 3
+    w.values.mul_(-0.5).add_(0.25)
+    w.x.copy_(torch.flip(w.x, [0]))
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert_close(host(w), y)
+
+
+def test_narrow_spmv_in_a_hip_graph(dev):
+    from test_gpu_staged import _graph_matches_eager
+    w = banded(dev, rows=1 << 18, band=11, vdtype=torch.float16, spread=50)
+    plan = _graph_matches_eager(w, dev)
+    assert flag(plan)[0] == 3
