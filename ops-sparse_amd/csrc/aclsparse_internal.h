@@ -268,8 +268,11 @@ struct SpmvLayout {
     // (the header's staged_flag then reads 3).  The row kernel then streams
     // 2 bytes per entry of column data instead of 4.  With the staged tables
     // it overlays st_cl: only one of the two paths is ever chosen.
+    // The low 16 bits of the normalised row offsets, nr uint16[rows+2], go
+    // with it: a row block of at most kLongChunks chunks spans fewer than
+    // 65536 entries, so the row kernel reads 2 bytes per row of such blocks.
     bool narrow = false;
-    size_t nc_offset = 0;
+    size_t nc_offset = 0, nr_offset = 0;
 };
 
 #ifndef SPMV_LONG_CHUNKS
@@ -525,6 +528,8 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     if (!transpose && stageValueBytes != 0U && computeType == ACL_FLOAT && rows > 0 &&
         nnz >= static_cast<uint64_t>(kNarrowMinNnz)) {
         l.narrow = true;
+        l.nr_offset = AlignUp(l.total);
+        l.total = AlignUp(l.nr_offset + (static_cast<size_t>(rows) + 2) * sizeof(uint16_t));
         if (l.staged) {
             l.nc_offset = l.st_cl_offset;  // st_cl holds at least nnz + 8 uint16
         } else {

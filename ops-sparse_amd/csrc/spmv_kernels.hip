@@ -121,6 +121,10 @@ struct RowBlockParams {
     uint32_t run_mask;
     // narrow columns: column - base - (first row of the entry's block), int16[nnz]
     const int16_t* ncol;
+    // with ncol: the low 16 bits of the normalised row offsets, uint16[rows+2]
+    // (a row block of at most kLongChunks chunks spans fewer than 65536
+    // entries, so its rows' offsets from its first entry follow from them)
+    const uint16_t* rp16;
     // ValKind::GATH: the fp32 values the streamed positions index
     const float* gval;
     int64_t gval_n;
@@ -475,6 +479,7 @@ struct StreamLoad {
     v4i col[2];
     StreamVals<V> val;
     RowT rp[2];
+    uint32_t rp16;  // kRows16: low halves of the two row offsets
     typename OutOf<O>::T yold[2];
     uint32_t xg[kLaneItems];  // gathered x of the 8 slots
 };
@@ -489,7 +494,7 @@ __device__ __forceinline__ int32_t Hi16(int32_t w, uint32_t rb)
     return static_cast<int32_t>(rb + static_cast<uint32_t>(w >> 16));
 }
 
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kNarrow = false>
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kNarrow = false, bool kRows16 = false>
 __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                                 StreamLoad<RowT, V, O>& b)
 {
@@ -552,14 +557,24 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     // never past the offsets array (rows + 1 entries; the pad entry of the
     // workspace copy is not needed: a pair past it is never used)
     if (nrp > p.rows + 1 - r0) nrp = p.rows + 1 - r0;
-    const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
-    if constexpr (sizeof(RowT) == 8) {
+    if constexpr (kRows16) {
+        // The lane's two low halves, entries r0 + 2l and r0 + 2l + 1, from
+        // an 8-byte load at the even entry below (4-byte aligned; the copy
+        // has rows + 2 entries, so the rounded range stays inside it).
+        const int64_t odd = r0 & 1;
+        const __amdgpu_buffer_rsrc_t r16 = Rsrc(p.rp16 + (r0 - odd), ((odd + nrp + 1) & ~int64_t{1}) * 2);
+        const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r16, lane * 4, 0, kRowPolicy));
+        b.rp16 = __builtin_amdgcn_alignbit(static_cast<uint32_t>(w.y), static_cast<uint32_t>(w.x),
+                                           static_cast<uint32_t>(odd) * 16U);
+    } else if constexpr (sizeof(RowT) == 8) {
+        const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
         const v4i w = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, kRowPolicy));
         b.rp[0] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.y)) << 32) |
                                     static_cast<uint32_t>(w.x)) - static_cast<RowT>(p.rp_base);
         b.rp[1] = static_cast<RowT>((static_cast<uint64_t>(static_cast<uint32_t>(w.w)) << 32) |
                                     static_cast<uint32_t>(w.z)) - static_cast<RowT>(p.rp_base);
     } else {
+        const __amdgpu_buffer_rsrc_t rr = Rsrc(static_cast<const RowT*>(p.rp) + r0, nrp * sizeof(RowT));
         const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rr, lane * 8, 0, kRowPolicy));
         b.rp[0] = static_cast<RowT>(w.x) - static_cast<RowT>(p.rp_base);
         b.rp[1] = static_cast<RowT>(w.y) - static_cast<RowT>(p.rp_base);
@@ -701,7 +716,7 @@ constexpr int kStreamLds = kWaveChunk + 8;
 // the chunk's first slot leave their partial sum in `head` (also when they
 // cross both ends), the row that crosses its last slot in `tail`, and neither
 // is written to y here.
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false>
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false, bool kRows16 = false>
 __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<RowT, V, O>& lc, float* sVal, int lane,
                                             float alpha, float beta, float& carry, int& lg, typename OutOf<O>::T* y,
                                             typename OutOf<O>::T* sink, float* head = nullptr,
@@ -740,8 +755,15 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     // l+1's first row starts (row 127 never exists: blocks have <= 127 rows).
     const int32_t k0lo = static_cast<int32_t>(cur.k0);
     int32_t rs[2], re[2];
-    rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
-    rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
+    if constexpr (kRows16) {
+        // offsets from the block's first entry, below 65536 in such a block
+        const uint32_t k0l16 = static_cast<uint32_t>(cur.k0) & 0xFFFFU;
+        rs[0] = static_cast<int32_t>(((lc.rp16 & 0xFFFFU) - k0l16) & 0xFFFFU);
+        rs[1] = static_cast<int32_t>(((lc.rp16 >> 16) - k0l16) & 0xFFFFU);
+    } else {
+        rs[0] = static_cast<int32_t>(lc.rp[0]) - k0lo;
+        rs[1] = static_cast<int32_t>(lc.rp[1]) - k0lo;
+    }
     re[0] = rs[1];
     re[1] = FromNextLane(rs[0], rs[1]);
 
@@ -1121,18 +1143,25 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
     auto block = [&](int64_t tile) {
         Stage cur = OpenTileFlat<RowT>(p, tile);
-        if (p.task_waves > 0 && BlockChunks(cur.k0, cur.kspan) > kLongChunks) return;  // served by tasks
+        const bool shortBlock = BlockChunks(cur.k0, cur.kspan) <= kLongChunks;
+        if (p.task_waves > 0 && !shortBlock) return;  // served by tasks
         carry = 0.0f;
-        while (cur.valid) {
-            L b;
-            StreamLoadStage<RowT, V, O, kBeta, kNarrow>(p, cur, tailStart, lane, b);
-            StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
-            StreamChunk<RowT, V, O, kBeta>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
-            if (cur.last) break;
-            cur.c0 = cur.c1;
-            cur.first = false;
-            ChunkBounds(cur);
-        }
+        auto chunks = [&](auto rows16) {
+            constexpr bool k16 = decltype(rows16)::value;
+            while (cur.valid) {
+                L b;
+                StreamLoadStage<RowT, V, O, kBeta, kNarrow, k16>(p, cur, tailStart, lane, b);
+                StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
+                StreamChunk<RowT, V, O, kBeta, false, k16>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
+                if (cur.last) break;
+                cur.c0 = cur.c1;
+                cur.first = false;
+                ChunkBounds(cur);
+            }
+        };
+        // the narrow kernel reads the 16-bit row offsets of short blocks
+        if (kNarrow && shortBlock) chunks(std::true_type{});
+        else chunks(std::false_type{});
     };
     const int64_t first = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
     if constexpr (kGated) {
@@ -2069,6 +2098,7 @@ RowBlockParams MakeRowBlockParams(const SpmvLaunch& l)
     RowBlockParams p{};
     p.run_mask = 1U;  // gated launches: the row / CSC kernels' flag value 0
     p.ncol = l.layout.narrow ? At<const int16_t>(l.ws, l.layout.nc_offset) : nullptr;
+    p.rp16 = l.layout.narrow ? At<const uint16_t>(l.ws, l.layout.nr_offset) : nullptr;
     p.rp = At<void>(l.ws, l.layout.rowptr_offset);
     p.blocks = At<int32_t>(l.ws, l.layout.blocks_offset);
     p.block_nnz = At<void>(l.ws, l.layout.block_nnz_offset);
@@ -2524,6 +2554,15 @@ __global__ __launch_bounds__(kThreads) void NarrowColKernel(NarrowParams q)
     if (__ballot(bad) != 0 && lane == 0) __hip_atomic_fetch_or(q.bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Low 16 bits of the normalised row offsets (the pad entry reads 0).
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void NarrowRowsKernel(const RowT* norm, int64_t rows, uint16_t* rp16)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i <= rows) rp16[i] = static_cast<uint16_t>(static_cast<uint64_t>(norm[i]) & 0xFFFFU);
+    if (i == rows + 1) rp16[i] = 0;
+}
+
 // Flag 3 (the narrow-column row kernel) unless the staged gather was chosen
 // or some entry did not fit.
 __global__ void NarrowDecideKernel(uint32_t* flag, const uint32_t* bad)
@@ -2546,6 +2585,9 @@ void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
     q.bad = &h->narrow_bad;
     const unsigned grid = static_cast<unsigned>((q.num_blocks + kWaves - 1) / kWaves);
     hipLaunchKernelGGL((NarrowColKernel<RowT>), dim3(grid), dim3(kThreads), 0, s, q);
+    hipLaunchKernelGGL((NarrowRowsKernel<RowT>), dim3(static_cast<unsigned>((l.rows + 2 + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows,
+                       At<uint16_t>(l.ws, l.layout.nr_offset));
     hipLaunchKernelGGL(NarrowDecideKernel, dim3(1), dim3(1), 0, s, &h->staged_flag,
                        static_cast<const uint32_t*>(&h->narrow_bad));
 }
