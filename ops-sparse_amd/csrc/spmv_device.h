@@ -51,32 +51,13 @@ __device__ __forceinline__ bool IsZero(C64 v) { return v.re == 0.0f && v.im == 0
 __device__ __forceinline__ float HalfToFloat(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 __device__ __forceinline__ float Bf16ToFloat(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// IEEE binary32 -> binary16, round to nearest, ties to even (written from
-// the IEEE 754 definition; NaN stays a quiet NaN, overflow goes to inf).
+// IEEE binary32 -> binary16, round to nearest, ties to even: the hardware
+// conversion (overflow goes to inf, NaN stays NaN, results below the
+// smallest normal half are rounded to subnormal halves: these kernels keep
+// fp16 denormals).
 __device__ __forceinline__ uint16_t FloatToHalfRne(float f)
 {
-    const uint32_t u = __float_as_uint(f);
-    const uint32_t sign = (u >> 16) & 0x8000U;
-    const uint32_t a = u & 0x7FFFFFFFU;
-    if (a >= 0x7F800000U) {
-        return static_cast<uint16_t>(sign | 0x7C00U | (a > 0x7F800000U ? (0x0200U | ((a >> 13) & 0x3FFU)) : 0U));
-    }
-    if (a >= 0x477FF000U) return static_cast<uint16_t>(sign | 0x7C00U);  // >= 65520 rounds to inf
-    if (a < 0x38800000U) {                                                // below 2^-14: subnormal half
-        if (a < 0x33000000U) return static_cast<uint16_t>(sign);          // below 2^-25
-        const uint32_t e = a >> 23;
-        const uint32_t m = (a & 0x7FFFFFU) | 0x800000U;
-        const uint32_t shift = 126U - e;  // value in units of 2^-24 is m >> shift
-        uint32_t r = m >> shift;
-        const uint32_t rem = m & ((1U << shift) - 1U);
-        const uint32_t half = 1U << (shift - 1U);
-        if (rem > half || (rem == half && (r & 1U))) ++r;
-        return static_cast<uint16_t>(sign | r);
-    }
-    uint32_t hb = (a >> 13) - (112U << 10);
-    const uint32_t rem = a & 0x1FFFU;
-    if (rem > 0x1000U || (rem == 0x1000U && (hb & 1U))) ++hb;
-    return static_cast<uint16_t>(sign | hb);
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
 // binary32 -> bfloat16, round to nearest even; NaN stays NaN.

@@ -453,6 +453,60 @@ __device__ __forceinline__ float WaveSum(float v)
     return v;
 }
 
+// Sum of elements lo..hi (0 <= lo, hi <= 3) of a group of 4 products.
+__device__ __forceinline__ float GroupPart(const float4& f, int lo, int hi)
+{
+    const float x0 = lo == 0 ? f.x : 0.0f;
+    const float x1 = lo <= 1 && hi >= 1 ? f.y : 0.0f;
+    const float x2 = lo <= 2 && hi >= 2 ? f.z : 0.0f;
+    const float x3 = hi == 3 ? f.w : 0.0f;
+    return (x0 + x1) + (x2 + x3);
+}
+
+// Sum of the products [a, b) of a row of at most kLongRow entries, read from
+// LDS as groups of 4: the first and last group masked, the whole groups
+// between them (at most 7) in an order rotated by the lane, so that the
+// lanes of rows of equal length (which start a multiple of the length apart)
+// spread over the LDS banks.  A fixed order per row and lane: the same row
+// always has the same lane.
+__device__ __forceinline__ float ShortRowSum(const float4* areaV, int a, int b, int lane)
+{
+    if (b <= a) return 0.0f;
+    const int q0 = a >> 2, q1 = (b - 1) >> 2;
+    const float4 f = areaV[q0];
+    const float4 g = areaV[q1];
+    float sum = GroupPart(f, a & 3, q1 == q0 ? (b - 1) & 3 : 3);
+    const int m = q1 - q0 - 1;  // whole groups between the two ends
+    if (__ballot(m > 0) != 0) {
+        // rotation start: the lane's low bits, below the largest power of 2 <= m
+        const int p = m > 0 ? 1 << (31 - __builtin_clz(static_cast<uint32_t>(m))) : 1;
+        const int r = (lane & 7) & (p - 1);
+        float mid[2] = {0.0f, 0.0f};
+        if (__ballot(m > 3) != 0) {
+#pragma unroll
+            for (int c = 0; c < 7; ++c) {
+                int u = r + c;
+                u = u >= m ? u - m : u;
+                const float4 v = areaV[q0 + 1 + (c < m ? u : 0)];
+                const float s4 = (v.x + v.y) + (v.z + v.w);
+                mid[c & 1] += c < m ? s4 : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                int u = r + c;
+                u = u >= m ? u - m : u;
+                const float4 v = areaV[q0 + 1 + (c < m ? u : 0)];
+                const float s4 = (v.x + v.y) + (v.z + v.w);
+                mid[c & 1] += c < m ? s4 : 0.0f;
+            }
+        }
+        sum += mid[0] + mid[1];
+    }
+    if (q1 != q0) sum += GroupPart(g, 0, (b - 1) & 3);
+    return sum;
+}
+
 // Row end of a tile's row: y, or the tile's head / tail partial sum.
 template <OutKind O>
 __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int loc, int nRowsDone, bool headRow,
@@ -725,19 +779,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
             longRows[atomicAdd(&longCount, 1)] = loc;
             continue;
         }
-        // Neighbouring rows start about one row length apart, so reading them
-        // all from their first entry would put a wave's lanes on the same LDS
-        // banks; each row starts at an offset set by its lane instead (the
-        // order is still fixed per row: row loc is always thread loc % kTileThreads).
-        const int len = b - a;
-        int k = len > 0 ? lane % len : 0;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent reads in flight
-#pragma unroll 4
-        for (int c = 0; c < len; ++c) {
-            acc[c & 3] += area[a + k];
-            k = k + 1 == len ? 0 : k + 1;
-        }
-        const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        const float sum = ShortRowSum(areaV, a, b, lane);
         FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
     }
     __syncthreads();

@@ -707,3 +707,29 @@ def _run_complex_t(rp, col, val, x, y0, dev):
     plan.run()
     torch.cuda.synchronize()
     return y.cpu()
+
+
+def test_fp16_output_rounding_edges(dev):
+    """fp16 y: alpha * (a * x) with a = 1, x = 2 hits chosen fp32 values exactly; each must round to the
+    nearest fp16, ties to even: overflow to inf at 65520, the largest half below it, subnormal halves,
+    a tie at half the smallest subnormal (to zero) and just above it (to the smallest subnormal)."""
+    targets = np.array([70000.0, 65519.0, 65520.0, -65536.0, 1.0e-6, -3.0e-6, 2.0 ** -25, 2.0 ** -25 * 1.0000001,
+                        6.0e-5, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 0.0], dtype=np.float32)
+    n = targets.size
+    x = torch.full((n,), 2.0, dtype=torch.float16, device=dev)
+    for tv in targets:
+        assert np.float32(np.float32(tv / 2) * 2) == tv  # alpha * 2 is exact in fp32
+    for i, tv in enumerate(targets):
+        y = torch.zeros(n, dtype=torch.float16, device=dev)
+        rp = torch.arange(n + 1, dtype=torch.int32, device=dev)
+        col = torch.arange(n, dtype=torch.int32, device=dev)
+        # one non-zero in row i only: y_i = alpha * 1 * 2
+        vals = torch.zeros(n, dtype=torch.float16, device=dev)
+        vals[i] = 1.0
+        plan = CsrSpMV(n, n, rp, col, vals, x, y, float(np.float32(tv / 2)), 0.0)
+        plan.preprocess()
+        plan.run()
+        torch.cuda.synchronize()
+        got = host_bits(y)[i]
+        want = np.array([tv], dtype=np.float32).astype(np.float16).view(np.uint16)[0]
+        assert got == want, f"{tv!r}: got {got:#06x} want {want:#06x}"
