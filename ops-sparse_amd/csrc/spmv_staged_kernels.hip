@@ -119,6 +119,25 @@ __device__ __forceinline__ int64_t XcdIndex()
     return static_cast<int64_t>(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
 }
 
+// Workgroup -> tile of pass B (and slice of pass A): tiles in chunks of
+// kTileChunk per XCD, the chunks dealt to the XCDs round-robin, so that the
+// tiles in flight at any time are consecutive over the whole chip (their
+// staged runs lie close together in every bucket of xg, which HBM serves
+// better than eight separate stretches), while neighbouring tiles, whose
+// runs share cache lines, mostly stay on one XCD.  The grid is a multiple of
+// 8; a last, partial round is split evenly over the XCDs.
+constexpr int64_t kTileChunk = 8;
+__device__ __forceinline__ int64_t ChunkedXcdIndex()
+{
+    constexpr int64_t kRound = kXcds * kTileChunk;
+    const int64_t bx = blockIdx.x;
+    const int64_t r0 = bx / kRound * kRound;
+    const int64_t per = r0 + kRound <= static_cast<int64_t>(gridDim.x) ? kTileChunk
+                                                                      : (static_cast<int64_t>(gridDim.x) - r0) / kXcds;
+    const int64_t within = bx - r0;
+    return r0 + (within % kXcds) * per + within / kXcds;
+}
+
 __device__ __forceinline__ uint32_t FlagSet(const uint32_t* flag)
 {
     typedef const __attribute__((address_space(4))) uint32_t* CPtr;  // scalar load: written by Preprocess
@@ -334,7 +353,7 @@ __global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams 
     extern __shared__ uint4 segRaw[];
     XT* seg = reinterpret_cast<XT*>(segRaw);
     if (FlagSet(q.flag) != 1U) return;
-    const int64_t w = XcdIndex();
+    const int64_t w = ChunkedXcdIndex();
     const int nb = q.buckets + 1;
     const uint32_t* base = q.start;                  // row 0: first slot of every bucket
     const uint32_t* ends = q.start + q.tiles * nb;   // row T: end of every bucket
@@ -555,7 +574,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     float* area = reinterpret_cast<float*>(areaV);
     __shared__ typename Scan::TempStorage scanStorage;
 
-    const int64_t t = XcdIndex();
+    const int64_t t = ChunkedXcdIndex();
     if (t >= q.tiles) return;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
