@@ -73,6 +73,7 @@ def profile_mode(name, steps):
     op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]
     plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
     plan.preprocess()
+    torch.cuda.synchronize()  # as in a bench run: Preprocess's path choice is on the host before the SpMVs
     flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
     sink = torch.empty((), dtype=torch.float32, device=dev)
     for _ in range(steps):

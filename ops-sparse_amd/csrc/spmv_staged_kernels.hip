@@ -126,7 +126,7 @@ __device__ __forceinline__ int64_t XcdIndex()
 // better than eight separate stretches), while neighbouring tiles, whose
 // runs share cache lines, mostly stay on one XCD.  The grid is a multiple of
 // 8; a last, partial round is split evenly over the XCDs.
-constexpr int64_t kTileChunk = 8;
+constexpr int64_t kTileChunk = 32;
 __device__ __forceinline__ int64_t ChunkedXcdIndex()
 {
     constexpr int64_t kRound = kXcds * kTileChunk;
