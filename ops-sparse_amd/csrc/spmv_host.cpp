@@ -201,9 +201,10 @@ bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
 bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
                   const aclsparseDnVecDescr* y)
 {
+    const uint64_t xBytes = m->value_type == ACL_FLOAT16 || m->value_type == ACL_BF16 ? 2U : 4U;
     return l.narrow && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values) &&
-           m->cols * static_cast<uint64_t>(l.st_value_bytes != 0 ? l.st_value_bytes : 4) <= 0x7FFFFFFFULL;
+           m->cols * xBytes <= 0x7FFFFFFFULL;
 }
 
 // After a staged or narrow Preprocess: copy the path flag it leaves in the workspace

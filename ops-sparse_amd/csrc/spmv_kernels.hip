@@ -384,6 +384,8 @@ __device__ __forceinline__ float ReadLane(float v, int l) { return __shfl(v, l, 
 __device__ __forceinline__ long long ReadLane(long long v, int l) { return __shfl(v, l, kWave); }
 __device__ __forceinline__ C64 ReadLane(C64 v, int l) { return C64{__shfl(v.re, l, kWave), __shfl(v.im, l, kWave)}; }
 __device__ __forceinline__ float ShflXorAcc(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ int32_t ShflXorAcc(int32_t v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ int32_t ReadLane(int32_t v, int l) { return __shfl(v, l, kWave); }
 __device__ __forceinline__ long long ShflXorAcc(long long v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ __forceinline__ C64 ShflXorAcc(C64 v, int m)
 {
@@ -1209,12 +1211,19 @@ constexpr int64_t GenXBytes()
                               : static_cast<int64_t>(sizeof(typename ValOf<V>::T));
 }
 
+// In-chunk type of products and partial sums: int8 products (|a*x| <=
+// 16384) summed over one 512-slot chunk stay below 2^23, so they are added
+// exactly in int32; a row's chunks are combined, and the epilogue computed,
+// in the int64 accumulator.  Other kinds use the accumulator throughout.
+template <ValKind V, AccKind A>
+using GenPart = typename std::conditional<V == ValKind::I8 && A == AccKind::I64, int32_t, typename AccOf<A>::T>::type;
+
 template <ValKind V, AccKind A>
 struct GenLoad {
     v4i col[2];
     GenVals<V> val;  // values of the lane's 8 slots
     int64_t rp[2];
-    typename AccOf<A>::T xg[kLaneItems];
+    GenPart<V, A> xg[kLaneItems];
 };
 
 template <typename RowT, ValKind V, AccKind A>
@@ -1302,7 +1311,8 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             }
         } else if constexpr (V == ValKind::I8) {
             const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b8(rx, static_cast<int>(off), 0, kGatherPolicy);
-            b.xg[j] = ToAcc<V, A>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
+            if constexpr (A == AccKind::I64) b.xg[j] = static_cast<int8_t>(static_cast<uint8_t>(raw));
+            else b.xg[j] = ToAcc<V, A>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
         } else if constexpr (V == ValKind::F32) {
             b.xg[j] = ToAcc<V, A>(
                 __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy)));
@@ -1315,9 +1325,11 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
 }
 
 template <ValKind V, AccKind A>
-__device__ __forceinline__ typename AccOf<A>::T GenVal(const GenLoad<V, A>& b, int j)
+__device__ __forceinline__ GenPart<V, A> GenVal(const GenLoad<V, A>& b, int j)
 {
-    if constexpr (V == ValKind::I8) {
+    if constexpr (V == ValKind::I8 && A == AccKind::I64) {
+        return static_cast<int8_t>((b.val.v[j >> 2] >> (8 * (j & 3))) & 0xFFU);
+    } else if constexpr (V == ValKind::I8) {
         return ToAcc<V, A>(static_cast<int8_t>((b.val.v[j >> 2] >> (8 * (j & 3))) & 0xFFU));
     } else if constexpr (V == ValKind::F32) {
         return ToAcc<V, A>(b.val.v[j >> 2][j & 3]);
@@ -1335,12 +1347,13 @@ __device__ __forceinline__ T WaveAllSum(T v)
 
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& cur, const GenLoad<V, A>& lc,
-                                         typename AccOf<A>::T* sVal, int lane, typename AccOf<A>::T alpha,
+                                         GenPart<V, A>* sVal, int lane, typename AccOf<A>::T alpha,
                                          typename AccOf<A>::T beta, bool betaNz, typename AccOf<A>::T& carry, int& lg)
 {
     using Acc = typename AccOf<A>::T;
+    using Part = GenPart<V, A>;
     using OutT = typename OutOf<O>::T;
-    Acc prod[kLaneItems];
+    Part prod[kLaneItems];
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
         if constexpr (V == ValKind::UNIT) prod[j] = lc.xg[j];
@@ -1397,15 +1410,15 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
         for (int h = 0; h < 2; ++h) {
             const int32_t len = fin[h] ? re[h] - rs[h] : 0;
             const int32_t base = fin[h] ? rs[h] - shift : 0;
-            Acc acc = Zero<Acc>();
+            Part acc = Zero<Part>();
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
                 if (t < kSerialCapOne || wide) {
-                    const Acc v = sVal[base + t];
-                    acc = acc + (t < len ? v : Zero<Acc>());
+                    const Part v = sVal[base + t];
+                    acc = acc + (t < len ? v : Zero<Part>());
                 }
             }
-            sum[h] = acc;
+            sum[h] = static_cast<Acc>(acc);
         }
     } else {
         const int g = lane >> lg;
@@ -1416,13 +1429,13 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
         const int32_t a1e = __shfl(re[1], src, kWave);
         const int32_t gs = (g & 1) ? a1s : a0s;
         const int32_t ge = (g & 1) ? a1e : a1s;
-        Acc part = Zero<Acc>();
+        Part part = Zero<Part>();
         if (in && ge - gs <= cap) {
             for (int32_t q = gs + sub; q < ge; q += gsz) part = part + sVal[q - shift];
         }
         for (int m = 1; m < gsz; m <<= 1) part = part + ShflXorAcc(part, m);
-        sum[0] = ReadLane(part, ((2 * lane) << lg) & (kWave - 1));
-        sum[1] = ReadLane(part, ((2 * lane + 1) << lg) & (kWave - 1));
+        sum[0] = static_cast<Acc>(ReadLane(part, ((2 * lane) << lg) & (kWave - 1)));
+        sum[1] = static_cast<Acc>(ReadLane(part, ((2 * lane + 1) << lg) & (kWave - 1)));
     }
 
     uint64_t pending0 = __ballot(defer[0]), pending1 = __ballot(defer[1]);
@@ -1440,9 +1453,9 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
         const int32_t e0 = __builtin_amdgcn_readlane(h ? re[1] : re[0], l);
         const int32_t lo = s0 > c0 ? s0 : c0;
         const int32_t hi = e0 < c1 ? e0 : c1;
-        Acc part = Zero<Acc>();
+        Part part = Zero<Part>();
         for (int32_t q = lo + lane; q < hi; q += kWave) part = part + sVal[q - shift];
-        Acc total = WaveAllSum(part);
+        Acc total = static_cast<Acc>(WaveAllSum(part));
         if (s0 < c0) total = carry + total;
         if (e0 > c1) {
             carry = total;
@@ -1463,7 +1476,7 @@ template <typename RowT, ValKind V, OutKind O, AccKind A>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
-    __shared__ Acc sValAll[kFlatWaves][kStreamLds];
+    __shared__ GenPart<V, A> sValAll[kFlatWaves][kStreamLds];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     Acc alpha, beta;
