@@ -262,7 +262,7 @@ struct SpmvLayout {
     size_t st_tile_row_offset = 0, st_tile_nnz_offset = 0, st_counts_offset = 0, st_start_bm_offset = 0;
     size_t st_start_offset = 0, st_scan_offset = 0, st_scan_bytes = 0, st_perm_offset = 0, st_cl_offset = 0;
     size_t st_xg_offset = 0, st_head_offset = 0, st_tail_offset = 0, st_metric_offset = 0;
-    // Narrow columns (non-transpose, the stream kernel's value types): each
+    // Narrow columns (non-transpose, NarrowTypes): each
     // entry's column as a signed 16-bit offset from the first row of its row
     // block, nc int16[nnz+8], written by Preprocess when every entry fits
     // (the header's staged_flag then reads 3).  The row kernel then streams
@@ -325,6 +325,14 @@ inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
     if (valueType == ACL_FLOAT) return 4U;
     if (valueType == ACL_FLOAT16 || valueType == ACL_BF16) return 2U;
     return 0U;
+}
+
+// Value / compute types whose row kernel can read narrow columns: fp32,
+// fp16 and bf16 values with fp32 compute, int8 values with int32 compute.
+inline bool NarrowTypes(aclDataType valueType, aclDataType computeType)
+{
+    if (computeType == ACL_FLOAT) return valueType == ACL_FLOAT || valueType == ACL_FLOAT16 || valueType == ACL_BF16;
+    return computeType == ACL_INT32 && valueType == ACL_INT8;
 }
 
 // Narrow columns are built for matrices of at least this many entries.
@@ -402,7 +410,7 @@ inline size_t AccumulatorBytes(aclDataType computeType)
 
 inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
                                 aclDataType computeType, bool transpose, bool allowTasks = true,
-                                uint32_t stageValueBytes = 0)
+                                uint32_t stageValueBytes = 0, bool narrowTypes = false)
 {
     SpmvLayout l;
     l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
@@ -525,8 +533,7 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.st_metric_offset = AlignUp(l.st_tail_offset + static_cast<size_t>(t) * sizeof(float));
         l.total = AlignUp(l.st_metric_offset + sizeof(uint64_t));
     }
-    if (!transpose && stageValueBytes != 0U && computeType == ACL_FLOAT && rows > 0 &&
-        nnz >= static_cast<uint64_t>(kNarrowMinNnz)) {
+    if (!transpose && narrowTypes && rows > 0 && nnz >= static_cast<uint64_t>(kNarrowMinNnz)) {
         l.narrow = true;
         l.nr_offset = AlignUp(l.total);
         l.total = AlignUp(l.nr_offset + (static_cast<size_t>(rows) + 2) * sizeof(uint16_t));

@@ -112,7 +112,9 @@ __device__ __forceinline__ long long ScaledI64(long long sum, long long alpha, l
     const long long mag = sum < 0 ? -sum : sum;
     const long long scale = alpha < 0 ? -alpha : alpha;
     const bool negative = (sum < 0) != (alpha < 0);
-    if (mag > 9223372036854775807LL / scale) return negative ? -2147483648LL : 2147483647LL;
+    // |alpha| <= 2^31, so mag * scale can only overflow int64 when mag >= 2^32;
+    // the (slow, software) 64-bit division is taken only then
+    if (mag >= (1LL << 32) && mag > 9223372036854775807LL / scale) return negative ? -2147483648LL : 2147483647LL;
     const long long prod = negative ? -(mag * scale) : mag * scale;
     if (prod > 2147483647LL - betaTerm) return 2147483647LL;
     if (prod < -2147483648LL - betaTerm) return -2147483648LL;

@@ -180,7 +180,7 @@ aclsparseStatus_t ValidateWorkspace(void* buffer)
 SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c)
 {
     return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op), true,
-                                aclsp::StageValueBytes(m->value_type, c));
+                                aclsp::StageValueBytes(m->value_type, c), aclsp::NarrowTypes(m->value_type, c));
 }
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
@@ -201,7 +201,9 @@ bool StageUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
 bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
                   const aclsparseDnVecDescr* y)
 {
-    const uint64_t xBytes = m->value_type == ACL_FLOAT16 || m->value_type == ACL_BF16 ? 2U : 4U;
+    const uint64_t xBytes = m->value_type == ACL_FLOAT16 || m->value_type == ACL_BF16 ? 2U
+                            : m->value_type == ACL_INT8                                 ? 1U
+                                                                                        : 4U;
     return l.narrow && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values) &&
            m->cols * xBytes <= 0x7FFFFFFFULL;

@@ -446,8 +446,21 @@ struct StreamVals<ValKind::BF16> {
     v4i v;
 };
 template <>
+struct StreamVals<ValKind::I8> {
+    uint32_t v[2];  // 4 bytes per group of 4 slots
+};
+template <>
 struct StreamVals<ValKind::UNIT> {
 };
+
+// int8 operands on the stream kernel: products (|a*x| <= 16384) and their
+// sums within one 512-slot chunk (below 2^23) are integers that fp32 holds
+// exactly, whatever the order; a row's chunks are combined in double (exact
+// up to 2^53) and the epilogue is the int64 one with saturation to int32.
+template <ValKind V>
+using StreamScal = typename std::conditional<V == ValKind::I8, long long, float>::type;  // alpha, beta
+template <ValKind V>
+using StreamSum = typename std::conditional<V == ValKind::I8, double, float>::type;  // row sums across chunks
 template <>
 struct StreamVals<ValKind::GATH> {
     v4i v[2];                 // positions of the 8 slots in the values array
@@ -459,6 +472,8 @@ __device__ __forceinline__ uint32_t RawVal(const StreamVals<V>& s, int j)
 {
     if constexpr (V == ValKind::F32) {
         return __float_as_uint(s.v[j >> 2][j & 3]);
+    } else if constexpr (V == ValKind::I8) {
+        return (s.v[j >> 2] >> (8 * (j & 3))) & 0xFFU;
     } else {
         const uint32_t w = static_cast<uint32_t>(s.v[j >> 1]);
         return (j & 1) ? (w >> 16) : (w & 0xFFFFU);
@@ -469,6 +484,7 @@ template <ValKind V>
 __device__ __forceinline__ float ValToFloat(uint32_t raw)
 {
     if constexpr (V == ValKind::F32) return __uint_as_float(raw);
+    else if constexpr (V == ValKind::I8) return static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(raw)));
     else if constexpr (V == ValKind::F16) return HalfToFloat(static_cast<uint16_t>(raw));
     else return Bf16ToFloat(static_cast<uint16_t>(raw));
 }
@@ -544,6 +560,9 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
         b.val.v[0] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
         b.val.v[1] =
             __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rv, 1024 + lane * 16, 0, kBufNonTemporal));
+    } else if constexpr (V == ValKind::I8) {
+        b.val.v[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
+        b.val.v[1] = __builtin_amdgcn_raw_buffer_load_b32(rv, 256 + lane * 4, 0, kBufNonTemporal);
     } else {
         const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rv, lane * 8, 0, kBufNonTemporal));
         const v2i hi = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rv, 512 + lane * 8, 0, kBufNonTemporal));
@@ -589,9 +608,15 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
         // per dword, so a row past the block reads 0 (and is never used)
         // (loaded as a float2: taking __builtin_bit_cast(float, ...) of the
         // elements of an int2 load makes this hipcc emit a one-dword load)
-        const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(ry, lane * 8, 0, kRowPolicy));
-        b.yold[0] = w.x;
-        b.yold[1] = w.y;
+        if constexpr (O == OutKind::I32) {
+            const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(ry, lane * 8, 0, kRowPolicy));
+            b.yold[0] = w.x;
+            b.yold[1] = w.y;
+        } else {
+            const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(ry, lane * 8, 0, kRowPolicy));
+            b.yold[0] = w.x;
+            b.yold[1] = w.y;
+        }
     } else {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -637,6 +662,10 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
                     b.val.v[j >> 2][j & 3] = __float_as_int(tv);
                 } else if constexpr (V == ValKind::F32) {
                     b.val.v[j >> 2][j & 3] = tv;
+                } else if constexpr (V == ValKind::I8) {
+                    const uint32_t sh = 8U * static_cast<uint32_t>(j & 3);
+                    b.val.v[j >> 2] =
+                        (b.val.v[j >> 2] & ~(0xFFU << sh)) | (static_cast<uint32_t>(static_cast<uint8_t>(tv)) << sh);
                 } else {
                     const uint32_t raw = static_cast<uint32_t>(tv);
                     uint32_t w = static_cast<uint32_t>(b.val.v[j >> 1]);
@@ -655,8 +684,10 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
         off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
         if constexpr (sizeof(ValT) == 4) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
-        } else {
+        } else if constexpr (sizeof(ValT) == 2) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, static_cast<int>(off), 0, kGatherPolicy);
+        } else {
+            xg[j] = __builtin_amdgcn_raw_buffer_load_b8(rx, static_cast<int>(off), 0, kGatherPolicy);
         }
     }
     if constexpr (V == ValKind::GATH) {
@@ -720,7 +751,8 @@ constexpr int kStreamLds = kWaveChunk + 8;
 // is written to y here.
 template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false, bool kRows16 = false>
 __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<RowT, V, O>& lc, float* sVal, int lane,
-                                            float alpha, float beta, float& carry, int& lg, typename OutOf<O>::T* y,
+                                            StreamScal<V> alpha, StreamScal<V> beta, StreamSum<V>& carry, int& lg,
+                                            typename OutOf<O>::T* y,
                                             typename OutOf<O>::T* sink, float* head = nullptr,
                                             float* tail = nullptr)
 {
@@ -741,7 +773,7 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         *head = 0.0f;
         *tail = 0.0f;
     } else if (cur.first) {
-        carry = 0.0f;
+        carry = 0;
         // Lanes per row: as many as keep every row of the block on its own
         // lane group, 1 when the block spans several chunks.
         lg = 0;
@@ -798,7 +830,7 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     WaveLdsSync();
 
     // Phase 1.
-    float sum[2] = {0.0f, 0.0f};
+    StreamSum<V> sum[2] = {0, 0};
     if (lg == 0) {
         // One lane per row: 8 predicated LDS reads per row, all issued
         // before one wait (the compiler's own schedule waits after each read
@@ -909,7 +941,7 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         const int32_t hi = e0 < c1 ? e0 : c1;
         float part = 0.0f;
         for (int32_t q = lo + lane; q < hi; q += kWave) part += sVal[q - shift];
-        float total = WaveSum(part);
+        StreamSum<V> total = WaveSum(part);
         bool finish = false;
         if constexpr (kTask) {
             if (s0 < c0) {
@@ -938,13 +970,19 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
         }
     }
 
-    float r[2];
+    OutT out[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        r[h] = alpha * sum[h];
         // beta == 0 (possible at run time with device scalars) never reads y
-        if constexpr (kBeta) {
-            if (beta != 0.0f) r[h] += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
+        if constexpr (V == ValKind::I8) {
+            const long long old = kBeta && beta != 0 ? static_cast<long long>(lc.yold[h]) : 0LL;
+            out[h] = FromAcc<O, AccKind::I64>(ScaledI64(static_cast<long long>(sum[h]), alpha, beta, old));
+        } else {
+            float r = alpha * sum[h];
+            if constexpr (kBeta) {
+                if (beta != 0.0f) r += beta * OutToAcc<O, AccKind::F32>(lc.yold[h]);
+            }
+            out[h] = FromAcc<O, AccKind::F32>(r);
         }
     }
     // When every row of the block that this chunk touches finishes here (one-
@@ -957,14 +995,16 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
     }
     if (pair) {
         const __amdgpu_buffer_rsrc_t rys = Rsrc(y + cur.r0, static_cast<int64_t>(nr) * 4);
-        const v2i w = {__float_as_int(r[0]), __float_as_int(r[1])};
-        __builtin_amdgcn_raw_buffer_store_b64(w, rys, lane * 8, 0, 0);
+        if constexpr (sizeof(OutT) == 4) {  // pair is false otherwise
+            const v2i w = {__builtin_bit_cast(int32_t, out[0]), __builtin_bit_cast(int32_t, out[1])};
+            __builtin_amdgcn_raw_buffer_store_b64(w, rys, lane * 8, 0, 0);
+        }
     } else {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int i = 2 * lane + h;
             OutT* dst = fin[h] ? y + (cur.r0 + i) : sink + h * kWave;
-            *dst = FromAcc<O, AccKind::F32>(r[h]);
+            *dst = out[h];
         }
     }
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
@@ -1089,16 +1129,17 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float* sVal = sValAll[wv];
 
-    float alpha, beta;
-    LoadScalars<AccKind::F32>(p.s, alpha, beta);
+    StreamScal<V> alpha, beta;
+    LoadScalars<V == ValKind::I8 ? AccKind::I64 : AccKind::F32>(p.s, alpha, beta);
     OutT* y = static_cast<OutT*>(p.y);
     OutT* sink = static_cast<OutT*>(p.sink) + lane;
     const __amdgpu_buffer_rsrc_t rx = Rsrc(p.x, p.cols * static_cast<int64_t>(sizeof(ValT)));
     const int64_t tailStart = p.nnz & ~static_cast<int64_t>(3);
-    float carry = 0.0f;
+    StreamSum<V> carry = 0;
     int lg = 0;
 
-    if (static_cast<int32_t>(blockIdx.x) < p.task_wgs) {
+    // (int8 launches have no tasks: a long block is summed chunk by chunk by its own wave)
+    if (V != ValKind::I8 && static_cast<int32_t>(blockIdx.x) < p.task_wgs) {
         // Task worker.
         const int64_t e = static_cast<int64_t>(blockIdx.x) * kFlatWaves + wv;
         int64_t total = ConstLoad<int32_t>(p.task_start, p.num_blocks);
@@ -1147,7 +1188,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
         Stage cur = OpenTileFlat<RowT>(p, tile);
         const bool shortBlock = BlockChunks(cur.k0, cur.kspan) <= kLongChunks;
         if (p.task_waves > 0 && !shortBlock) return;  // served by tasks
-        carry = 0.0f;
+        carry = 0;
         auto chunks = [&](auto rows16) {
             constexpr bool k16 = decltype(rows16)::value;
             while (cur.valid) {
@@ -2178,19 +2219,21 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
     const bool chosen = l.staged || l.narrow;  // Preprocess left a path choice in the header
     const unsigned grid = RowBlockGrid(p.num_blocks);
     constexpr bool kCanVec = V == ValKind::F32 || V == ValKind::F16 || V == ValKind::BF16;
+    // int8 values and x, int32 y, exact int64 semantics (see StreamSum)
+    constexpr bool kInt8 = V == ValKind::I8 && A == AccKind::I64 && O == OutKind::I32;
     // The stream kernels read col_ind / values as 16-byte groups of arrays
     // that start 16-byte aligned, with unit strides.
-    const bool vec = kCanVec && l.nnz >= 4 && l.col_stride == 1 && l.val_stride == 1 && l.x_stride == 1 &&
-                     l.y_stride == 1 && Aligned16(l.col) && Aligned16(l.val);
-    if constexpr (kCanVec && A == AccKind::F32) {
+    const bool vec = (kCanVec || kInt8) && l.nnz >= 4 && l.col_stride == 1 && l.val_stride == 1 &&
+                     l.x_stride == 1 && l.y_stride == 1 && Aligned16(l.col) && Aligned16(l.val);
+    if constexpr ((kCanVec && A == AccKind::F32) || kInt8) {
         // Stream kernel: 32-bit buffer offsets into x, contiguous y.
         const bool stream = vec && static_cast<int64_t>(l.cols) * static_cast<int64_t>(sizeof(typename ValOf<V>::T)) <=
                                        0x7FFFFFFFLL;
         if (stream) {
-            const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
+            const bool betaNz = l.device_scalars || (kInt8 ? l.beta_i != 0 : l.beta_re != 0.0f);
             const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
             int64_t taskWgs = 0;
-            if (l.layout.tasks) {
+            if (l.layout.tasks && !kInt8) {
                 // task waves: a multiple of 8 workgroups (even over the XCDs)
                 const int64_t waves = l.layout.max_tasks < TaskWaves() ? l.layout.max_tasks : TaskWaves();
                 taskWgs = (waves + kFlatWaves * kXcds - 1) / (kFlatWaves * kXcds) * kXcds;

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
 from helpers import assert_close
 from ops_sparse import workloads as wl
 from ops_sparse.spmv import CsrSpMV
@@ -176,3 +177,63 @@ def test_narrow_spmv_in_a_hip_graph(dev):
     w = banded(dev, rows=1 << 18, band=11, vdtype=torch.float16, spread=50)
     plan = _graph_matches_eager(w, dev)
     assert flag(plan)[0] == 3
+
+
+def int8_case(dev, rows, band, spread, alpha, beta, seed=7, extreme=False, i64=False):
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    off = (torch.arange(band) - band // 2) * spread
+    col = (torch.arange(rows)[:, None] + off[None, :]).clamp(0, rows - 1).reshape(-1).to(torch.int32)
+    rp = torch.arange(0, rows * band + 1, band, dtype=torch.int64)
+    if extreme:  # every product 16384 (or -16384 for negative x): row sums far beyond 2^24
+        val = torch.full((col.numel(),), -128, dtype=torch.int8)
+        x = torch.where(torch.rand(rows, generator=g) < 0.5, -128, 127).to(torch.int8)
+    else:
+        val = torch.randint(-128, 128, (col.numel(),), generator=g, dtype=torch.int8)
+        x = torch.randint(-128, 128, (rows,), generator=g, dtype=torch.int8)
+    y0 = torch.randint(-(1 << 30), 1 << 30, (rows,), generator=g, dtype=torch.int32)
+    ref = oracle.spmv_i8(rp.numpy(), col.numpy(), val.numpy(), x.numpy(), y0.numpy(), alpha, beta)
+    rpd = rp.to(torch.int64 if i64 else torch.int32).to(dev)
+    return (rows, rpd, col.to(dev), val.to(dev), x.to(dev), y0.to(dev)), ref
+
+
+def run_int8(args, alpha, beta, preprocess=True, settle=True):
+    from ops_sparse._lib import DataType
+    rows, rp, col, val, x, y0 = args
+    y = y0.clone()
+    plan = CsrSpMV(rows, rows, rp, col, val, x, y, alpha, beta, compute_type=DataType.INT32)
+    if preprocess:
+        plan.preprocess()
+        if settle:
+            torch.cuda.synchronize()
+    plan.run()
+    torch.cuda.synchronize()
+    return y, plan
+
+
+@pytest.mark.parametrize("i64", [False, True], ids=["i32", "i64"])
+def test_int8_narrow_exact(i64, dev):
+    """int8 values and x, int32 y: the fp32 row kernel on the narrow copy, bit-exact against the int64
+    oracle (saturating epilogue), and equal to the col_ind kernel and to the first SpMV after Preprocess."""
+    args, ref = int8_case(dev, rows=1 << 18, band=9, spread=1000, alpha=3, beta=-2, i64=i64)
+    y, plan = run_int8(args, 3, -2)
+    assert flag(plan)[0] == 3
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+    y0, plan0 = run_int8(args, 3, -2, preprocess=False)
+    assert flag(plan0)[0] == 0
+    np.testing.assert_array_equal(y0.cpu().numpy(), ref)
+    y1, _ = run_int8(args, 3, -2, settle=False)
+    np.testing.assert_array_equal(y1.cpu().numpy(), ref)
+
+
+def test_int8_long_rows_beyond_fp32_exactness(dev):
+    """Rows of 3001 products of magnitude 16384 (sums near 2^25.6, past fp32's exact integers) split over
+    several chunks, and an alpha that saturates some rows: exact, on the narrow copy and on col_ind."""
+    args, ref = int8_case(dev, rows=1 << 10, band=3001, spread=1, alpha=50, beta=1, extreme=True)
+    sat = (ref == 2147483647) | (ref == -2147483648)
+    assert np.any(sat) and not np.all(sat)
+    y, plan = run_int8(args, 50, 1)
+    assert flag(plan)[0] == 3
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+    y0, _ = run_int8(args, 50, 1, preprocess=False)
+    np.testing.assert_array_equal(y0.cpu().numpy(), ref)
