@@ -338,6 +338,11 @@ inline bool NarrowTypes(aclDataType valueType, aclDataType computeType)
 // Narrow columns are built for matrices of at least this many entries.
 constexpr int64_t kNarrowMinNnz = int64_t{1} << 20;
 constexpr int32_t kNarrowFlag = 3;  // staged_flag value of the narrow-column row kernel
+// staged_flag value of the banded one-pass transpose on 16-bit copies of its
+// two per-entry streams (each entry's row as an offset from its CSC block's
+// first column, its CSR position as an offset from its CSC index), written
+// by Preprocess into key_a and val_b when every entry fits
+constexpr int32_t kBandedNarrowFlag = 4;
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run
 // of staged slots is padded to a multiple of this many slots.

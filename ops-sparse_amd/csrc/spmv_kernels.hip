@@ -125,6 +125,9 @@ struct RowBlockParams {
     // (a row block of at most kLongChunks chunks spans fewer than 65536
     // entries, so its rows' offsets from its first entry follow from them)
     const uint16_t* rp16;
+    // GATH with ncol: each streamed position as an offset from the entry's own
+    // index in the streamed arrays, int16[nnz]
+    const int16_t* npos;
     // ValKind::GATH: the fp32 values the streamed positions index
     const float* gval;
     int64_t gval_n;
@@ -552,6 +555,17 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     }
     if constexpr (V == ValKind::UNIT) {
         (void)rv;  // no values
+    } else if constexpr (V == ValKind::GATH && kNarrow) {
+        // positions from their 16-bit offsets to the slot's own index
+        const __amdgpu_buffer_rsrc_t rq = Rsrc(p.npos + a0, avail * 2);
+        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, lane * 8, 0, kBufNonTemporal));
+        const v2i hi =
+            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, 512 + lane * 8, 0, kBufNonTemporal));
+        const uint32_t k0 = static_cast<uint32_t>(a0) + 4U * static_cast<uint32_t>(lane);
+        const uint32_t k1 = k0 + 256U;
+        b.val.v[0] = v4i{Lo16(lo.x, k0), Hi16(lo.x, k0 + 1U), Lo16(lo.y, k0 + 2U), Hi16(lo.y, k0 + 3U)};
+        b.val.v[1] = v4i{Lo16(hi.x, k1), Hi16(hi.x, k1 + 1U), Lo16(hi.y, k1 + 2U), Hi16(hi.y, k1 + 3U)};
+        (void)rv;
     } else if constexpr (V == ValKind::GATH) {
         b.val.v[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
         b.val.v[1] =
@@ -1203,7 +1217,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             }
         };
         // the narrow kernel reads the 16-bit row offsets of short blocks
-        if (kNarrow && shortBlock) chunks(std::true_type{});
+        if (kNarrow && shortBlock && p.rp16 != nullptr) chunks(std::true_type{});
         else chunks(std::false_type{});
     };
     const int64_t first = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
@@ -2313,10 +2327,13 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
 // One-pass column kernel of banded fp32 transposes: the stream kernel on the
 // CSC pattern with each entry's row as its "column" (x gathered by row) and
 // its CSR position as its value (the value gathered by position).
-template <bool kGated>
+template <bool kGated, bool kNarrowB = false>
 void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStream_t stream)
 {
     RowBlockParams c = p;
+    c.rp16 = nullptr;
+    c.ncol = kNarrowB ? At<const int16_t>(l.ws, l.layout.key_a_offset) : nullptr;
+    c.npos = kNarrowB ? At<const int16_t>(l.ws, l.layout.val_b_offset) : nullptr;
     c.rp = At<void>(l.ws, l.layout.colptr_offset);
     c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
     c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
@@ -2335,17 +2352,17 @@ void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStre
     c.gval = static_cast<const float*>(l.val);
     c.gval_n = l.nnz;
     c.skip_flag = kGated ? &At<SpmvWsHeader>(l.ws, 0)->staged_flag : nullptr;
-    c.run_mask = 1U << 2;
+    c.run_mask = 1U << (kNarrowB ? kBandedNarrowFlag : 2);
     const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
     const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
     const dim3 wg(kWave * kFlatWaves);
     const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
     if (betaNz) {
-        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, true, kGated>), dim3(g), wg, 0,
-                           stream, c);
+        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, true, kGated, kNarrowB>), dim3(g),
+                           wg, 0, stream, c);
     } else {
-        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, false, kGated>), dim3(g), wg, 0,
-                           stream, c);
+        hipLaunchKernelGGL((SpmvStreamFlatKernel<int32_t, ValKind::GATH, OutKind::F32, false, kGated, kNarrowB>),
+                           dim3(g), wg, 0, stream, c);
     }
 }
 
@@ -2364,11 +2381,18 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
             // the CSC pattern gathering each entry's value and x, both local
             const bool banded = l.staged && l.y_stride == 1 && l.x_stride == 1 && l.val_stride == 1 &&
                                 l.nnz <= 0x1FFFFFFFLL;
+            if (banded && l.staged_choice == kBandedNarrowFlag) {
+                LaunchBandedTranspose<false, true>(l, p, stream);
+                return 0;
+            }
             if (banded && l.staged_choice == 2) {
                 LaunchBandedTranspose<false>(l, p, stream);
                 return 0;
             }
-            if (banded && l.staged_choice < 0) LaunchBandedTranspose<true>(l, p, stream);  // runs on choice 2 only
+            if (banded && l.staged_choice < 0) {  // each runs on its own choice only
+                LaunchBandedTranspose<true>(l, p, stream);
+                LaunchBandedTranspose<true, true>(l, p, stream);
+            }
         }
         CscParams q{};
         q.colptr = At<void>(l.ws, l.layout.colptr_offset);
@@ -2648,6 +2672,52 @@ void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
                        static_cast<const uint32_t*>(&h->narrow_bad));
 }
 
+// Banded transpose on 16-bit copies: one wave per CSC row block (columns as
+// rows) writes each entry's row as an offset from the block's first column
+// (into key_a) and its CSR position as an offset from its own CSC index (into
+// val_b); any entry out of range sets narrow_bad.  Runs only when the
+// bucketed Preprocess chose the banded kernel (flag 2), whose copies these
+// are; both regions are sort storage that only the CSC build uses.
+__global__ __launch_bounds__(kThreads) void BandedNarrowKernel(const int32_t* cblocks, const int32_t* cblockNnz,
+                                                               const int32_t* cscRow, const int32_t* cscPos,
+                                                               int64_t numBlocks, int16_t* nrow, int16_t* npos,
+                                                               const uint32_t* flag, uint32_t* bad)
+{
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (b >= numBlocks || *flag != 2U) return;
+    const int64_t c0 = cblocks[b];
+    const int64_t k1 = cblockNnz[b + 1];
+    bool out = false;
+    for (int64_t k = static_cast<int64_t>(cblockNnz[b]) + lane; k < k1; k += kWave) {
+        const int64_t d1 = static_cast<int64_t>(cscRow[k]) - c0;
+        const int64_t d2 = static_cast<int64_t>(cscPos[k]) - k;
+        out |= d1 < -32768 || d1 > 32767 || d2 < -32768 || d2 > 32767;
+        nrow[k] = static_cast<int16_t>(d1);
+        npos[k] = static_cast<int16_t>(d2);
+    }
+    if (__ballot(out) != 0 && lane == 0) __hip_atomic_fetch_or(bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void BandedNarrowDecideKernel(uint32_t* flag, const uint32_t* bad)
+{
+    if (*flag == 2U && *bad == 0U) *flag = static_cast<uint32_t>(kBandedNarrowFlag);
+}
+
+void BuildBandedNarrow(const SpmvLaunch& l, hipStream_t s)
+{
+    SpmvWsHeader* h = At<SpmvWsHeader>(l.ws, 0);
+    const int64_t nb = l.layout.csc_num_blocks;
+    hipLaunchKernelGGL(BandedNarrowKernel, dim3(static_cast<unsigned>((nb + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                       s, At<const int32_t>(l.ws, l.layout.csc_blocks_offset),
+                       At<const int32_t>(l.ws, l.layout.csc_block_nnz_offset),
+                       At<const int32_t>(l.ws, l.layout.key_b_offset), At<const int32_t>(l.ws, l.layout.csc_pos_offset),
+                       nb, At<int16_t>(l.ws, l.layout.key_a_offset), At<int16_t>(l.ws, l.layout.val_b_offset),
+                       static_cast<const uint32_t*>(&h->staged_flag), &h->narrow_bad);
+    hipLaunchKernelGGL(BandedNarrowDecideKernel, dim3(1), dim3(1), 0, s, &h->staged_flag,
+                       static_cast<const uint32_t*>(&h->narrow_bad));
+}
+
 template <typename RowT>
 int BuildCsc(const SpmvLaunch& l, hipStream_t s)
 {
@@ -2856,7 +2926,11 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) {
             if (BuildCsc<int32_t>(l, s) != 0) return 1;
-            return l.staged ? LaunchStagedPreprocess(l, stream) : 0;
+            if (!l.staged) return 0;
+            if (LaunchStagedPreprocess(l, stream) != 0) return 1;
+            // the banded kernel's 16-bit copies (32-bit offsets and positions only)
+            if (l.nnz <= 0x1FFFFFFFLL && l.val_kind == ValKind::F32) BuildBandedNarrow(l, s);
+            return 0;
         }
         if (l.layout.tasks && BuildTasks<int32_t>(l, s) != 0) return 1;
         if (l.staged && LaunchStagedPreprocess(l, stream) != 0) return 1;

@@ -157,13 +157,15 @@ def banded_workload(dev, n=1536, beta=0.5, base=0):
 
 
 def test_banded_transpose_takes_the_one_pass_kernel(dev):
-    """Long runs: Preprocess picks the one-pass banded column kernel (flag 2); repeated runs are
+    """Long runs: Preprocess picks the one-pass banded column kernel, on its 16-bit copies (flag 4: every
+    entry's row within 16 bits of its CSC block's first column, its CSR position within 16 bits of its CSC
+    index); repeated runs are
     bit-identical on a new plan (every kernel set launched, gated on the device flag) and on this plan
     once the choice has reached the host (only the banded kernel launched)."""
     w = banded_workload(dev)
     assert w.nnz >= 1 << 20
     y, plan = run(w)
-    assert header(plan)[0] == 2
+    assert header(plan)[0] == 4
     assert_close(w.to("cpu"), y)
     y3, _ = run(w)
     assert torch.equal(y.view(torch.int32), y3.view(torch.int32))
@@ -178,7 +180,7 @@ def test_banded_conjugate_transpose_base1_beta0_ignores_nan_y(dev):
     w = banded_workload(dev, n=1100, beta=0.0, base=1)
     y0 = torch.full((w.cols,), float("nan"), device=dev)
     y, plan = run(w, op=Operation.CONJUGATE_TRANSPOSE, y0=y0)
-    assert header(plan)[0] == 2
+    assert header(plan)[0] == 4
     assert bool(torch.isfinite(y).all())
     assert_close(host(w), y)
 
@@ -191,6 +193,40 @@ def test_banded_transpose_int64_offsets_keeps_the_csc_kernels(dev):
     w.row_ptr = w.row_ptr.to(torch.int64)
     y, plan = run(w)
     assert header(plan)[0] == 0
+    assert_close(w.to("cpu"), y)
+    first = y.clone()
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
+
+
+def test_banded_transpose_far_band_keeps_32_bit_streams(dev):
+    """A Laplacian plus a band 40 000 columns off the diagonal: still banded (long runs, flag 2), but those
+    entries' rows and positions are out of 16-bit reach, so the kernel streams the 32-bit arrays; the result
+    is checked against the oracle and is bit-identical on a second run."""
+    n = 1100
+    m = n * n
+    i = torch.arange(m, dtype=torch.int64)
+    cols = [i - n, i - 1, i, i + 1, i + n, i + 40000]
+    r = torch.cat([i] * len(cols))
+    c = torch.cat(cols)
+    ok = (c >= 0) & (c < m)
+    r, c = r[ok], c[ok]
+    order = torch.argsort(r * m + c)
+    r, c = r[order], c[order]
+    row_ptr = torch.zeros(m + 1, dtype=torch.int64)
+    row_ptr[1:] = torch.cumsum(torch.bincount(r, minlength=m), 0)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(12)
+    vals = torch.rand(c.numel(), generator=g) * 2 - 1
+    x = torch.rand(m, generator=g) * 2 - 1
+    y0 = torch.rand(m, generator=g) * 2 - 1
+    w = wl.Workload("laplace_far_T", m, m, row_ptr.to(torch.int32), c.to(torch.int32), vals, x, y0, 1.25, -0.5,
+                    trans="T").to(dev)
+    y, plan = run(w)
+    flag, _, _ = header(plan)
+    assert flag == 2
     assert_close(w.to("cpu"), y)
     first = y.clone()
     y.copy_(w.y0)

@@ -256,4 +256,4 @@ def test_transposes_in_a_hip_graph(kind, dev):
         w = wl.laplacian_2d(n=1536).to(dev)
         w.trans = "T"
     plan = _graph_matches_eager(w, dev, Operation.TRANSPOSE)
-    assert header(plan)[0] == (1 if kind == "bucketed" else 2)
+    assert header(plan)[0] == (1 if kind == "bucketed" else 4)
