@@ -2327,11 +2327,13 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
 // One-pass column kernel of banded fp32 transposes: the stream kernel on the
 // CSC pattern with each entry's row as its "column" (x gathered by row) and
 // its CSR position as its value (the value gathered by position).
+uint16_t* BandedCols16(const SpmvLaunch& l);
+
 template <bool kGated, bool kNarrowB = false>
 void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStream_t stream)
 {
     RowBlockParams c = p;
-    c.rp16 = nullptr;
+    c.rp16 = kNarrowB ? BandedCols16(l) : nullptr;
     c.ncol = kNarrowB ? At<const int16_t>(l.ws, l.layout.key_a_offset) : nullptr;
     c.npos = kNarrowB ? At<const int16_t>(l.ws, l.layout.val_b_offset) : nullptr;
     c.rp = At<void>(l.ws, l.layout.colptr_offset);
@@ -2699,6 +2701,26 @@ __global__ __launch_bounds__(kThreads) void BandedNarrowKernel(const int32_t* cb
     if (__ballot(out) != 0 && lane == 0) __hip_atomic_fetch_or(bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The low 16 bits of the column offsets, for the banded kernel's short blocks
+// (only when the banded kernel was chosen: the region is key_a's second half).
+__global__ __launch_bounds__(kThreads) void BandedNarrowColsKernel(const int32_t* colptr, int64_t cols, uint16_t* cp16,
+                                                                   const uint32_t* flag)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i > cols + 1 || *flag != 2U) return;
+    cp16[i] = i <= cols ? static_cast<uint16_t>(static_cast<uint32_t>(colptr[i]) & 0xFFFFU) : uint16_t{0};
+}
+
+// Where the banded kernel's 16-bit column offsets go: after the row offsets
+// in key_a (4 bytes per entry, half used), when cols + 2 of them fit.
+uint16_t* BandedCols16(const SpmvLaunch& l)
+{
+    const size_t n = static_cast<size_t>(l.nnz);
+    const size_t used = AlignUp(n * sizeof(int16_t));
+    if (used + (static_cast<size_t>(l.cols) + 2) * sizeof(uint16_t) > n * sizeof(int32_t)) return nullptr;
+    return reinterpret_cast<uint16_t*>(At<uint8_t>(l.ws, l.layout.key_a_offset) + used);
+}
+
 __global__ void BandedNarrowDecideKernel(uint32_t* flag, const uint32_t* bad)
 {
     if (*flag == 2U && *bad == 0U) *flag = static_cast<uint32_t>(kBandedNarrowFlag);
@@ -2714,6 +2736,11 @@ void BuildBandedNarrow(const SpmvLaunch& l, hipStream_t s)
                        At<const int32_t>(l.ws, l.layout.key_b_offset), At<const int32_t>(l.ws, l.layout.csc_pos_offset),
                        nb, At<int16_t>(l.ws, l.layout.key_a_offset), At<int16_t>(l.ws, l.layout.val_b_offset),
                        static_cast<const uint32_t*>(&h->staged_flag), &h->narrow_bad);
+    if (uint16_t* cp16 = BandedCols16(l)) {
+        hipLaunchKernelGGL(BandedNarrowColsKernel, dim3(static_cast<unsigned>((l.cols + 2 + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, s, At<const int32_t>(l.ws, l.layout.colptr_offset), l.cols, cp16,
+                           static_cast<const uint32_t*>(&h->staged_flag));
+    }
     hipLaunchKernelGGL(BandedNarrowDecideKernel, dim3(1), dim3(1), 0, s, &h->staged_flag,
                        static_cast<const uint32_t*>(&h->narrow_bad));
 }
