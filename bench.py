@@ -171,7 +171,7 @@ def measure(w, steps, warmup, flush_buf):
     path = "row kernels" if w.trans == "N" else "transpose"
     if w.trans == "N" and plan.workspace is not None and plan.workspace.numel() >= 192:
         head = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
-        path = {1: "staged gather", 3: NARROW_PATH}.get(int(head[16] & 0xFFFFFFFF), path)
+        path = {1: "staged gather", 3: NARROW_PATH, 5: NARROW_PATH}.get(int(head[16] & 0xFFFFFFFF), path)
 
     sink = torch.empty((), dtype=torch.float32, device=flush_buf.device)
 

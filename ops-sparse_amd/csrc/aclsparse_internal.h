@@ -167,7 +167,10 @@ struct SpmvWsHeader {
     // narrow columns: nonzero when some entry's column is too far from its
     // row block's first row for 16 bits (set by Preprocess)
     uint32_t narrow_bad;
-    uint32_t reserved[7];
+    // narrow columns: nonzero when the entry-aligned row blocks do not fit
+    // (some block of more than 127 rows, or whose rows run past its window)
+    uint32_t entry_bad;
+    uint32_t reserved[6];
 };
 static_assert(sizeof(SpmvWsHeader) <= kWsHeaderBytes, "header must fit 192 bytes");
 
@@ -271,8 +274,12 @@ struct SpmvLayout {
     // The low 16 bits of the normalised row offsets, nr uint16[rows+2], go
     // with it: a row block of at most kLongChunks chunks spans fewer than
     // 65536 entries, so the row kernel reads 2 bytes per row of such blocks.
+    // With it, the entry-aligned row blocks (see kEntryChunk): eb int32[E+1],
+    // the first row starting at or after entry 448*t, and en RowT[E+1], its offset.
     bool narrow = false;
     size_t nc_offset = 0, nr_offset = 0;
+    int64_t entry_blocks = 0;
+    size_t eb_offset = 0, en_offset = 0;
 };
 
 #ifndef SPMV_LONG_CHUNKS
@@ -343,6 +350,13 @@ constexpr int32_t kNarrowFlag = 3;  // staged_flag value of the narrow-column ro
 // first column, its CSR position as an offset from its CSC index), written
 // by Preprocess into key_a and val_b when every entry fits
 constexpr int32_t kBandedNarrowFlag = 4;
+// Entry-aligned row blocks (staged_flag 5: the narrow-column row kernel on
+// them): block t holds the rows that start in [448 t, 448 (t+1)); when every
+// block has at most 127 rows and its rows end within 512 entries of 448 t,
+// a wave can load its block's columns and values from 448 t on before its
+// block's first row and offset are known.
+constexpr int64_t kEntryChunk = 448;
+constexpr int32_t kEntryFlag = 5;
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run
 // of staged slots is padded to a multiple of this many slots.
@@ -542,6 +556,10 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
         l.narrow = true;
         l.nr_offset = AlignUp(l.total);
         l.total = AlignUp(l.nr_offset + (static_cast<size_t>(rows) + 2) * sizeof(uint16_t));
+        l.entry_blocks = static_cast<int64_t>((nnz + kEntryChunk - 1) / kEntryChunk);
+        l.eb_offset = l.total;
+        l.en_offset = AlignUp(l.eb_offset + static_cast<size_t>(l.entry_blocks + 1) * sizeof(int32_t));
+        l.total = AlignUp(l.en_offset + static_cast<size_t>(l.entry_blocks + 1) * l.rowptr_bytes);
         if (l.staged) {
             l.nc_offset = l.st_cl_offset;  // st_cl holds at least nnz + 8 uint16
         } else {

@@ -265,7 +265,8 @@ void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 // The path of the matching staged Preprocess if its copy has completed
 // (0 the row / CSC kernels, 1 the staged or column-bucketed kernels, 2 the
 // banded transpose kernel, 3 the narrow-column row kernel, 4 the banded
-// transpose kernel on 16-bit copies), else -1.
+// transpose kernel on 16-bit copies, 5 the narrow-column row kernel on
+// entry-aligned blocks), else -1.
 int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
 {
     if (!m->staged_choice_valid || m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
@@ -275,7 +276,7 @@ int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
         return -1;
     }
     const uint32_t v = *static_cast<volatile const uint32_t*>(m->staged_choice_host);
-    return v <= static_cast<uint32_t>(aclsp::kBandedNarrowFlag) ? static_cast<int32_t>(v) : -1;
+    return v <= static_cast<uint32_t>(aclsp::kEntryFlag) ? static_cast<int32_t>(v) : -1;
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,

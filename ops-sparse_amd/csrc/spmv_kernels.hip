@@ -515,7 +515,8 @@ __device__ __forceinline__ int32_t Hi16(int32_t w, uint32_t rb)
     return static_cast<int32_t>(rb + static_cast<uint32_t>(w >> 16));
 }
 
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kNarrow = false, bool kRows16 = false>
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kNarrow = false, bool kRows16 = false,
+          bool kEntry = false>
 __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                                 StreamLoad<RowT, V, O>& b)
 {
@@ -527,7 +528,9 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     // past the chunk read 0 without touching memory, so a short block does
     // not stream (and gather for) the next block's entries.
     const int64_t a0 = s.valid ? s.a0 : 0;
-    int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
+    // entry-aligned blocks: the whole window from a0 (known from the block's
+    // number alone), so these loads do not wait for the block's metadata
+    int64_t end = kEntry ? a0 + kWaveChunk : (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
     end = end < tailStart ? end : tailStart;
     const int64_t avail = s.valid ? end - a0 : 0;
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
@@ -692,10 +695,12 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
     // Slots past the chunk's last non-zero gather nothing (an offset past the
     // resource reads 0 without a memory request).
     const int32_t hiSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c1 - s.a0) : 0;
+    // (entry-aligned blocks: slots before the block's first entry gather nothing either)
+    const int32_t loSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c0 - s.a0) : 0;
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
         uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
-        off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+        off = StreamSlot(lane, j) < hiSlot && StreamSlot(lane, j) >= loSlot ? off : 0xFFFFFFF0U;
         if constexpr (sizeof(ValT) == 4) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else if constexpr (sizeof(ValT) == 2) {
@@ -1125,7 +1130,8 @@ __device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const St
 // a value whose bit is set in p.run_mask, and a capped grid loops over the
 // blocks (block_stride).  Ungated launches carry neither (one block per wave,
 // no flag load).  kNarrow: column indices from the narrow copy p.ncol.
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false, bool kNarrow = false>
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false, bool kNarrow = false,
+          bool kEntry = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(7)))
 void SpmvStreamFlatKernel(RowBlockParams p)
 {
@@ -1200,14 +1206,20 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     const int64_t per = (static_cast<int64_t>(gridDim.x) - p.task_wgs) / kXcds;
     auto block = [&](int64_t tile) {
         Stage cur = OpenTileFlat<RowT>(p, tile);
-        const bool shortBlock = BlockChunks(cur.k0, cur.kspan) <= kLongChunks;
+        if constexpr (kEntry) {
+            // one chunk: the window [kEntryChunk*tile, +kWaveChunk) holds the block
+            cur.a0 = tile * kEntryChunk;
+            cur.c1 = cur.kspan;
+            cur.last = true;
+        }
+        const bool shortBlock = kEntry || BlockChunks(cur.k0, cur.kspan) <= kLongChunks;
         if (p.task_waves > 0 && !shortBlock) return;  // served by tasks
         carry = 0;
         auto chunks = [&](auto rows16) {
             constexpr bool k16 = decltype(rows16)::value;
             while (cur.valid) {
                 L b;
-                StreamLoadStage<RowT, V, O, kBeta, kNarrow, k16>(p, cur, tailStart, lane, b);
+                StreamLoadStage<RowT, V, O, kBeta, kNarrow, k16, kEntry>(p, cur, tailStart, lane, b);
                 StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
                 StreamChunk<RowT, V, O, kBeta, false, k16>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
                 if (cur.last) break;
@@ -2257,6 +2269,24 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
             int64_t blockWgs = (wgs + kXcds - 1) / kXcds * kXcds;
             const dim3 wg(kWave * kFlatWaves);
             const bool narrow = l.narrow && p.ncol != nullptr;
+            // the entry-aligned blocks (no tasks: every block is one window)
+            RowBlockParams pe = p;
+            pe.blocks = At<const int32_t>(l.ws, l.layout.eb_offset);
+            pe.block_nnz = At<const void>(l.ws, l.layout.en_offset);
+            pe.num_blocks = l.layout.entry_blocks;
+            pe.task_wgs = 0;
+            pe.task_waves = 0;
+            const int64_t eWgs = ((pe.num_blocks + kFlatWaves - 1) / kFlatWaves + kXcds - 1) / kXcds * kXcds;
+            if (narrow && l.staged_choice == kEntryFlag) {
+                if (betaNz) {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, false, true, true>),
+                                       dim3(static_cast<unsigned>(eWgs)), wg, 0, stream_, pe);
+                } else {
+                    hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, false, true, true>),
+                                       dim3(static_cast<unsigned>(eWgs)), wg, 0, stream_, pe);
+                }
+                return 0;
+            }
             if (narrow && l.staged_choice == kNarrowFlag) {
                 const unsigned g = static_cast<unsigned>(taskWgs + blockWgs);
                 if (betaNz) {
@@ -2274,7 +2304,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
                 // exit cheap.  The plain row kernel runs on flag 0, and on
                 // the flags of paths whose kernels are not launched here.
                 p.skip_flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
-                p.run_mask = 1U | (l.staged ? 0U : 2U) | (narrow ? 0U : 1U << kNarrowFlag);
+                p.run_mask = 1U | (l.staged ? 0U : 2U) | (narrow ? 0U : (1U << kNarrowFlag) | (1U << kEntryFlag));
                 if (blockWgs > kStagedFallbackWgs) {
                     blockWgs = kStagedFallbackWgs;
                     p.block_stride = blockWgs * kFlatWaves;
@@ -2285,6 +2315,21 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
                 if (betaNz) hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, true>), dim3(g), wg, 0, stream_, p);
                 else hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, true>), dim3(g), wg, 0, stream_, p);
                 if (narrow) {
+                    RowBlockParams e = pe;
+                    e.skip_flag = p.skip_flag;
+                    e.run_mask = 1U << kEntryFlag;
+                    int64_t ew = eWgs;
+                    if (ew > kStagedFallbackWgs) {
+                        ew = kStagedFallbackWgs;
+                        e.block_stride = ew * kFlatWaves;
+                    }
+                    if (betaNz) {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, true, true, true, true>),
+                                           dim3(static_cast<unsigned>(ew)), wg, 0, stream_, e);
+                    } else {
+                        hipLaunchKernelGGL((SpmvStreamFlatKernel<RowT, V, O, false, true, true, true>),
+                                           dim3(static_cast<unsigned>(ew)), wg, 0, stream_, e);
+                    }
                     RowBlockParams q = p;
                     q.run_mask = 1U << kNarrowFlag;
                     if (betaNz) {
@@ -2616,16 +2661,64 @@ struct NarrowParams {
     int32_t base;
     const uint32_t* flag;  // staged_flag
     uint32_t* bad;         // narrow_bad
+    // the entry-aligned blocks, used instead when they fit (entry_bad == 0)
+    const int32_t* eblocks;
+    const void* eblock_nnz;
+    int64_t num_eblocks;
+    const uint32_t* entry_bad;
 };
+
+// Entry-aligned row blocks: block t starts at the first row whose offset is
+// at least kEntryChunk*t (lower bound over the normalised offsets; t = E gives
+// rows).  One thread per block boundary.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void EntryBlocksKernel(const RowT* norm, int64_t rows, int64_t numE,
+                                                             int32_t* eb, RowT* en)
+{
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t > numE) return;
+    int64_t lo = rows;
+    if (t < numE) {
+        const int64_t target = t * kEntryChunk;
+        int64_t hi = rows;
+        lo = 0;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (static_cast<int64_t>(norm[mid]) >= target) hi = mid;
+            else lo = mid + 1;
+        }
+    }
+    eb[t] = static_cast<int32_t>(lo);
+    en[t] = norm[lo];
+}
+
+// Every entry-aligned block must have at most kWaveRows rows and end within
+// kWaveChunk entries of its window's start; otherwise entry_bad is set.
+template <typename RowT>
+__global__ __launch_bounds__(kThreads) void EntryCheckKernel(const int32_t* eb, const RowT* en, int64_t numE,
+                                                            uint32_t* bad)
+{
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    bool out = false;
+    if (t < numE) {
+        out = eb[t + 1] - eb[t] > kWaveRows ||
+              static_cast<int64_t>(en[t + 1]) > t * kEntryChunk + kWaveChunk;
+    }
+    if (__ballot(out) != 0 && (threadIdx.x & (kWave - 1)) == 0) {
+        __hip_atomic_fetch_or(bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
 
 template <typename RowT>
 __global__ __launch_bounds__(kThreads) void NarrowColKernel(NarrowParams q)
 {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
-    if (b >= q.num_blocks || *q.flag == 1U) return;
-    const int64_t rb = static_cast<int64_t>(q.blocks[b]) + q.base;
-    const RowT* bn = static_cast<const RowT*>(q.block_nnz);
+    if (*q.flag == 1U) return;
+    const bool entry = q.eblocks != nullptr && *q.entry_bad == 0U;  // the partition the kernel will use
+    if (b >= (entry ? q.num_eblocks : q.num_blocks)) return;
+    const int64_t rb = static_cast<int64_t>(entry ? q.eblocks[b] : q.blocks[b]) + q.base;
+    const RowT* bn = static_cast<const RowT*>(entry ? q.eblock_nnz : q.block_nnz);
     const int64_t k1 = static_cast<int64_t>(bn[b + 1]);
     bool bad = false;
     for (int64_t k = static_cast<int64_t>(bn[b]) + lane; k < k1; k += kWave) {
@@ -2647,9 +2740,9 @@ __global__ __launch_bounds__(kThreads) void NarrowRowsKernel(const RowT* norm, i
 
 // Flag 3 (the narrow-column row kernel) unless the staged gather was chosen
 // or some entry did not fit.
-__global__ void NarrowDecideKernel(uint32_t* flag, const uint32_t* bad)
+__global__ void NarrowDecideKernel(uint32_t* flag, const uint32_t* bad, const uint32_t* entryBad)
 {
-    if (*flag != 1U && *bad == 0U) *flag = static_cast<uint32_t>(kNarrowFlag);
+    if (*flag != 1U && *bad == 0U) *flag = static_cast<uint32_t>(*entryBad == 0U ? kEntryFlag : kNarrowFlag);
 }
 
 template <typename RowT>
@@ -2665,13 +2758,25 @@ void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
     q.base = l.base;
     q.flag = &h->staged_flag;
     q.bad = &h->narrow_bad;
-    const unsigned grid = static_cast<unsigned>((q.num_blocks + kWaves - 1) / kWaves);
+    const int64_t ne = l.layout.entry_blocks;
+    q.eblocks = At<const int32_t>(l.ws, l.layout.eb_offset);
+    q.eblock_nnz = At<const void>(l.ws, l.layout.en_offset);
+    q.num_eblocks = ne;
+    q.entry_bad = &h->entry_bad;
+    const unsigned eg = static_cast<unsigned>((ne + 1 + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL((EntryBlocksKernel<RowT>), dim3(eg), dim3(kThreads), 0, s,
+                       At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, ne, At<int32_t>(l.ws, l.layout.eb_offset),
+                       At<RowT>(l.ws, l.layout.en_offset));
+    hipLaunchKernelGGL((EntryCheckKernel<RowT>), dim3(eg), dim3(kThreads), 0, s, q.eblocks,
+                       static_cast<const RowT*>(q.eblock_nnz), ne, &h->entry_bad);
+    const int64_t waves = q.num_blocks > ne ? q.num_blocks : ne;
+    const unsigned grid = static_cast<unsigned>((waves + kWaves - 1) / kWaves);
     hipLaunchKernelGGL((NarrowColKernel<RowT>), dim3(grid), dim3(kThreads), 0, s, q);
     hipLaunchKernelGGL((NarrowRowsKernel<RowT>), dim3(static_cast<unsigned>((l.rows + 2 + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, s, At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows,
                        At<uint16_t>(l.ws, l.layout.nr_offset));
     hipLaunchKernelGGL(NarrowDecideKernel, dim3(1), dim3(1), 0, s, &h->staged_flag,
-                       static_cast<const uint32_t*>(&h->narrow_bad));
+                       static_cast<const uint32_t*>(&h->narrow_bad), static_cast<const uint32_t*>(&h->entry_bad));
 }
 
 // Banded transpose on 16-bit copies: one wave per CSC row block (columns as

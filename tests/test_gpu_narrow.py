@@ -1,13 +1,16 @@
 """GPU parity of the narrow-column row kernel through the C ABI.
 
 For non-transpose matrices of at least 2^20 entries with fp32 / fp16 / bf16
-values and fp32 compute, Preprocess writes every entry's column as a signed
-16-bit offset from the first row of its row block when all of them fit, and
-the header's path flag then reads 3: the row kernel streams that copy (2
-bytes per entry) instead of col_ind (4 bytes).  The sums are the same
-operations in the same order as on col_ind, so each case checks the result
-against the oracle and bit for bit against the same SpMV without Preprocess
-(flag 0, col_ind streamed).
+values and fp32 compute (or int8 values with int32 compute), Preprocess writes
+every entry's column as a signed 16-bit offset from the first row of its row
+block when all of them fit, and the row kernel streams that copy (2 bytes per
+entry) instead of col_ind (4 bytes).  The header's path flag reads 5 when the
+entry-aligned row blocks fit (every 448-entry chunk's rows end within 512
+entries and number at most 127: a wave loads its window before its block's
+metadata arrives), else 3 (the merge-path blocks).  On the merge-path blocks
+the sums are the col_ind kernel's, in the same order, so those cases are also
+checked bit for bit against the SpMV without Preprocess (flag 0); every case
+is checked against the oracle.
 """
 import numpy as np
 import pytest
@@ -21,6 +24,9 @@ from ops_sparse.spmv import CsrSpMV
 pytestmark = pytest.mark.gpu
 
 NARROW_MIN_NNZ = 1 << 20
+NARROW = 3         # path flag: row kernel on the 16-bit copies, merge-path row blocks
+ENTRY = 5          # path flag: the same on entry-aligned row blocks (loads issued before the block's metadata)
+ENTRY_CHUNK = 448  # entries per entry-aligned block
 
 
 def flag(plan):
@@ -55,15 +61,18 @@ def host(w):
 
 
 def check(w, expect_flag, y0=None):
-    """Oracle parity, the expected path, and bit equality with the col_ind kernel (no Preprocess)
-    and with the first SpMV after Preprocess (issued before the choice reached the host: every
-    kernel set launched, each gated on the device flag)."""
+    """Oracle parity, the expected path, bit equality with the first SpMV after Preprocess (issued
+    before the choice reached the host: every kernel set launched, each gated on the device flag) and,
+    on the merge-path blocks, with the col_ind kernel (no Preprocess)."""
     y, plan = run(w, y0=y0)
     assert flag(plan)[0] == expect_flag
     assert_close(host(w), y)
     y_plain, plan0 = run(w, preprocess=False, y0=y0)
     assert flag(plan0)[0] == 0
-    assert torch.equal(bits(y), bits(y_plain))
+    if expect_flag == NARROW:  # the same row blocks: the same sums in the same order
+        assert torch.equal(bits(y), bits(y_plain))
+    else:  # other row blocks: a row that crossed a chunk edge is summed in another order
+        assert_close(host(w), y_plain)
     y_first, _ = run(w, y0=y0, settle=False)
     assert torch.equal(bits(y), bits(y_first))
     return y, plan
@@ -88,30 +97,28 @@ def banded(dev, rows, band, vdtype=torch.float32, rdtype=torch.int32, base=0, al
 
 def test_laplacian_c2_takes_the_narrow_kernel(dev):
     w = wl.laplacian_2d().to(dev)
-    check(w, 3)
+    check(w, ENTRY)
 
 
 @pytest.mark.parametrize("vdtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 def test_half_values_int64_offsets_base1(vdtype, dev):
     w = banded(dev, rows=1 << 18, band=9, vdtype=vdtype, rdtype=torch.int64, base=1, spread=3000)
-    check(w, 3)
+    check(w, ENTRY)
 
 
-def block_first_rows(plan, rows):
-    """First row of each row's block, from the partition Preprocess wrote (blocks int32[B+1])."""
-    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
-    nb, off = int(h[5]), int(h[7])
-    blocks = np.frombuffer(plan.workspace[off:off + 4 * (nb + 1)].cpu().numpy().tobytes(), dtype=np.int32)
-    b = np.searchsorted(blocks[:nb], np.arange(rows), side="right") - 1
-    return torch.from_numpy(blocks[b].astype(np.int64))
+def entry_block_first_rows(row_ptr):
+    """First row of each row's entry-aligned block: block t holds the rows starting in [448 t, 448 (t+1))."""
+    rp = row_ptr.cpu().numpy().astype(np.int64)
+    rp = rp - rp[0]
+    t = rp[:-1] // ENTRY_CHUNK
+    return torch.from_numpy(np.searchsorted(rp, t * ENTRY_CHUNK, side="left").astype(np.int64))
 
 
 def test_offsets_at_the_16_bit_limits(dev):
     """Columns at offsets -32768 and +32767 from the first row of their block fit; one more does not."""
     rows, band = 1 << 17, 9
     w = banded(dev, rows=rows, band=band, spread=1)
-    _, plan = run(w)
-    r0 = block_first_rows(plan, rows).to(dev)
+    r0 = entry_block_first_rows(w.row_ptr).to(dev)
     col = w.col_ind.view(rows, band).clone()
     lo, hi = r0 - 32768, r0 + 32767
     col[:, 0] = torch.where(lo >= 0, lo, col[:, 0].to(torch.int64)).to(torch.int32)
@@ -119,7 +126,7 @@ def test_offsets_at_the_16_bit_limits(dev):
     w.col_ind = col.reshape(-1).contiguous()
     assert int((w.col_ind.view(rows, band)[:, 0].to(torch.int64) - r0).min()) == -32768
     assert int((w.col_ind.view(rows, band)[:, -1].to(torch.int64) - r0).max()) == 32767
-    check(w, 3)
+    check(w, ENTRY)
     for delta in (-32769, 32768):
         far = w.col_ind.clone()
         i = rows // 2
@@ -134,11 +141,12 @@ def test_offsets_at_the_16_bit_limits(dev):
 
 
 def test_long_rows_run_as_tasks(dev):
-    """Rows of 3000 entries within +-1500 columns: blocks of one row, split into chunk tasks."""
+    """Rows of 3000 entries within +-1500 columns: blocks of one row, split into chunk tasks (too long for
+    the entry-aligned blocks' 512-entry windows: flag 3)."""
     rows = 1 << 10
     w = banded(dev, rows=rows, band=3001, spread=1, beta=0.0)
     assert w.nnz >= NARROW_MIN_NNZ
-    y, _ = check(w, 3, y0=torch.full_like(w.y0, float("nan")))  # beta = 0: y is never read
+    y, _ = check(w, NARROW, y0=torch.full_like(w.y0, float("nan")))  # beta = 0: y is never read
     assert bool(torch.isfinite(y).all())
 
 
@@ -148,7 +156,7 @@ def test_entries_outside_the_rows_are_ignored(dev):
     w.row_ptr = w.row_ptr + lead
     w.col_ind = torch.cat([torch.full((lead,), 1 << 30, dtype=torch.int32, device=dev), w.col_ind])
     w.values = torch.cat([torch.full((lead,), 1e6, device=dev), w.values])
-    check(w, 3)
+    check(w, ENTRY)
 
 
 def test_small_matrices_keep_col_ind(dev):
@@ -163,7 +171,7 @@ def test_values_updated_after_preprocess(dev):
     """Preprocess reads the pattern only: new values and x are used by the next SpMV."""
     w = banded(dev, rows=1 << 18, band=7, spread=100)
     y, plan = run(w)
-    assert flag(plan)[0] == 3
+    assert flag(plan)[0] == ENTRY
     w.values.mul_(-0.5).add_(0.25)
     w.x.copy_(torch.flip(w.x, [0]))
     y.copy_(w.y0)
@@ -176,7 +184,7 @@ def test_narrow_spmv_in_a_hip_graph(dev):
     from test_gpu_staged import _graph_matches_eager
     w = banded(dev, rows=1 << 18, band=11, vdtype=torch.float16, spread=50)
     plan = _graph_matches_eager(w, dev)
-    assert flag(plan)[0] == 3
+    assert flag(plan)[0] == ENTRY
 
 
 def int8_case(dev, rows, band, spread, alpha, beta, seed=7, extreme=False, i64=False):
@@ -217,7 +225,7 @@ def test_int8_narrow_exact(i64, dev):
     oracle (saturating epilogue), and equal to the col_ind kernel and to the first SpMV after Preprocess."""
     args, ref = int8_case(dev, rows=1 << 18, band=9, spread=1000, alpha=3, beta=-2, i64=i64)
     y, plan = run_int8(args, 3, -2)
-    assert flag(plan)[0] == 3
+    assert flag(plan)[0] == ENTRY
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
     y0, plan0 = run_int8(args, 3, -2, preprocess=False)
     assert flag(plan0)[0] == 0
@@ -233,7 +241,26 @@ def test_int8_long_rows_beyond_fp32_exactness(dev):
     sat = (ref == 2147483647) | (ref == -2147483648)
     assert np.any(sat) and not np.all(sat)
     y, plan = run_int8(args, 50, 1)
-    assert flag(plan)[0] == 3
+    assert flag(plan)[0] == NARROW
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
     y0, _ = run_int8(args, 50, 1, preprocess=False)
     np.testing.assert_array_equal(y0.cpu().numpy(), ref)
+
+
+def test_many_empty_rows_keep_the_merge_path_blocks(dev):
+    """Every other row empty and rows of 2 entries: 448 entries span 448 rows, more than a wave's 127, so the
+    entry-aligned blocks do not fit and the narrow copy follows the merge-path blocks (flag 3)."""
+    rows = 1 << 20
+    g = torch.Generator(device="cpu")
+    g.manual_seed(21)
+    lengths = torch.where(torch.arange(rows) % 2 == 0, 2, 0).to(torch.int64)
+    rp = torch.zeros(rows + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(lengths, 0)
+    r = torch.repeat_interleave(torch.arange(rows), lengths)
+    col = (r + torch.randint(-500, 500, (r.numel(),), generator=g)).clamp(0, rows - 1).to(torch.int32)
+    vals = torch.rand(col.numel(), generator=g) * 2 - 1
+    x = torch.rand(rows, generator=g) * 2 - 1
+    y0 = torch.rand(rows, generator=g) * 2 - 1
+    w = wl.Workload("alternate_empty", rows, rows, rp.to(torch.int32), col, vals, x, y0, 1.0, 0.5).to(dev)
+    assert w.nnz >= NARROW_MIN_NNZ
+    check(w, NARROW)

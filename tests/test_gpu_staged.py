@@ -146,8 +146,8 @@ def test_staged_path_matches_oracle(case, dev):
 
 def test_banded_matrix_keeps_the_row_kernels(dev):
     """Eligible by size, but each tile touches few x lines: Preprocess keeps the row kernels, on the
-    narrow column copy (flag 3: every column lies within 16 bits of its row block's first row; the
-    copy overlays the staged tables)."""
+    narrow column copy over entry-aligned row blocks (flag 5: every column lies within 16 bits of its row
+    block's first row; the copy overlays the staged tables)."""
     rows = 1 << 21
     band = 17
     rp = torch.arange(0, rows * band + 1, band, dtype=torch.int64, device=dev)
@@ -161,7 +161,7 @@ def test_banded_matrix_keeps_the_row_kernels(dev):
     w = wl.Workload("banded17", rows, rows, rp.to(torch.int32), col, vals, x, y0, 1.0, 0.5)
     assert w.nnz >= STAGE_MIN_NNZ
     y, plan = run(w, dev)
-    assert header(plan)[0] == 3
+    assert header(plan)[0] == 5
     assert_close(w.to("cpu"), y)
 
 
