@@ -275,7 +275,7 @@ struct SpmvLayout {
     // with it: a row block of at most kLongChunks chunks spans fewer than
     // 65536 entries, so the row kernel reads 2 bytes per row of such blocks.
     // With it, the entry-aligned row blocks (see kEntryChunk): eb int32[E+1],
-    // the first row starting at or after entry 448*t, and en RowT[E+1], its offset.
+    // the first row starting at or after entry 480*t, and en RowT[E+1], its offset.
     bool narrow = false;
     size_t nc_offset = 0, nr_offset = 0;
     int64_t entry_blocks = 0;
@@ -351,11 +351,11 @@ constexpr int32_t kNarrowFlag = 3;  // staged_flag value of the narrow-column ro
 // by Preprocess into key_a and val_b when every entry fits
 constexpr int32_t kBandedNarrowFlag = 4;
 // Entry-aligned row blocks (staged_flag 5: the narrow-column row kernel on
-// them): block t holds the rows that start in [448 t, 448 (t+1)); when every
-// block has at most 127 rows and its rows end within 512 entries of 448 t,
-// a wave can load its block's columns and values from 448 t on before its
+// them): block t holds the rows that start in [480 t, 480 (t+1)); when every
+// block has at most 127 rows and its rows end within 512 entries of 480 t,
+// a wave can load its block's columns and values from 480 t on before its
 // block's first row and offset are known.
-constexpr int64_t kEntryChunk = 448;
+constexpr int64_t kEntryChunk = 480;
 constexpr int32_t kEntryFlag = 5;
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run

@@ -5,7 +5,7 @@ values and fp32 compute (or int8 values with int32 compute), Preprocess writes
 every entry's column as a signed 16-bit offset from the first row of its row
 block when all of them fit, and the row kernel streams that copy (2 bytes per
 entry) instead of col_ind (4 bytes).  The header's path flag reads 5 when the
-entry-aligned row blocks fit (every 448-entry chunk's rows end within 512
+entry-aligned row blocks fit (every 480-entry chunk's rows end within 512
 entries and number at most 127: a wave loads its window before its block's
 metadata arrives), else 3 (the merge-path blocks).  On the merge-path blocks
 the sums are the col_ind kernel's, in the same order, so those cases are also
@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 NARROW_MIN_NNZ = 1 << 20
 NARROW = 3         # path flag: row kernel on the 16-bit copies, merge-path row blocks
 ENTRY = 5          # path flag: the same on entry-aligned row blocks (loads issued before the block's metadata)
-ENTRY_CHUNK = 448  # entries per entry-aligned block
+ENTRY_CHUNK = 480  # entries per entry-aligned block
 
 
 def flag(plan):
@@ -107,7 +107,7 @@ def test_half_values_int64_offsets_base1(vdtype, dev):
 
 
 def entry_block_first_rows(row_ptr):
-    """First row of each row's entry-aligned block: block t holds the rows starting in [448 t, 448 (t+1))."""
+    """First row of each row's entry-aligned block: block t holds the rows starting in [480 t, 480 (t+1))."""
     rp = row_ptr.cpu().numpy().astype(np.int64)
     rp = rp - rp[0]
     t = rp[:-1] // ENTRY_CHUNK
@@ -248,7 +248,7 @@ def test_int8_long_rows_beyond_fp32_exactness(dev):
 
 
 def test_many_empty_rows_keep_the_merge_path_blocks(dev):
-    """Every other row empty and rows of 2 entries: 448 entries span 448 rows, more than a wave's 127, so the
+    """Every other row empty and rows of 2 entries: 480 entries span 480 rows, more than a wave's 127, so the
     entry-aligned blocks do not fit and the narrow copy follows the merge-path blocks (flag 3)."""
     rows = 1 << 20
     g = torch.Generator(device="cpu")
