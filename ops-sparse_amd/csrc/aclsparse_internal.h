@@ -570,6 +570,13 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
     return l;
 }
 
+// Path choices made on the device by a Preprocess (spmv_host.cpp): publish
+// the header's path flag to the host behind an event, read it once the copy
+// has completed (-1 before, or under stream capture), release the copy.
+void PublishPathChoice(uint32_t*& host, void*& event, bool& valid, void* ws, void* stream);
+int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* stream);
+void ReleasePathChoice(uint32_t*& host, void*& event);
+
 // SpMV into a workspace that scratch() returns (resolved only after the
 // inputs are validated and the layout fits scratchBytes): the tables are
 // rebuilt on every call and the staged path is not used (spmv_host.cpp).
@@ -664,6 +671,12 @@ struct aclsparseSpMVOpDescr {
     aclsparseSpMVOpAlg_t alg = ACL_SPARSE_SPMVOP_ALG1;
     void* buffer = nullptr;   // ALG2 reorder / bin_edge tables (caller-owned)
     uint32_t num_bins = 0;    // ALG2 bins (workgroups)
+    // ALG2: createDescr built the narrow column copy in the buffer; the path it
+    // chose on the device, copied to pinned host memory behind an event
+    bool narrow = false;
+    uint32_t* choice_host = nullptr;
+    void* choice_event = nullptr;
+    bool choice_valid = false;
 };
 
 struct aclsparseSpMVOpPlan {
@@ -696,6 +709,10 @@ uint32_t SpmvOpNumBins(int64_t m);
 SpmvOpLayout SpmvOpComputeLayout(int64_t m, int64_t n, int64_t nnz, aclsparseIndexType_t rowType, uint32_t bins);
 
 int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream);
+// ALG2: whether createDescr builds the narrow column copy; where the SpMV
+// workspace (whose header holds the path flag) starts in the buffer.
+bool SpmvOpNarrowUsable(const aclsparseSpMVOpDescr& d);
+void* SpmvOpSpmvWorkspace(const aclsparseSpMVOpDescr& d);
 int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
                         float beta, const void* alphaPtr, const void* betaPtr, bool deviceScalars, void* stream);
 

@@ -215,68 +215,15 @@ bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsp
 // "unknown"; a previous copy is waited for first (it may be on another
 // stream).  Any failure leaves the choice unknown (SpMV then launches both
 // kernel sets, which read the device flag).
-bool Capturing(hipStream_t s)
-{
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
-        (void)hipGetLastError();
-        return true;  // unknown: take the path that needs no host call
-    }
-    return st != hipStreamCaptureStatusNone;
-}
-
 void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 {
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    m->staged_choice_valid = false;
-    // Under stream capture no event, copy, wait or allocation is made: the
-    // choice stays unknown and every SpMV reads the device flag.
-    if (Capturing(s)) return;
-    if (m->staged_choice_event != nullptr) {
-        (void)hipEventSynchronize(static_cast<hipEvent_t>(m->staged_choice_event));
-    } else {
-        hipEvent_t e = nullptr;
-        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
-        m->staged_choice_event = e;
-    }
-    if (m->staged_choice_host == nullptr) {
-        void* p = nullptr;
-        if (hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
-        m->staged_choice_host = static_cast<uint32_t*>(p);
-    }
-    *m->staged_choice_host = 0xFFFFFFFFU;
-    const auto* header = static_cast<const aclsp::SpmvWsHeader*>(ws);
-    if (hipMemcpyAsync(m->staged_choice_host, &header->staged_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s) !=
-            hipSuccess ||
-        hipEventRecord(static_cast<hipEvent_t>(m->staged_choice_event), s) != hipSuccess) {
-        (void)hipGetLastError();
-        *m->staged_choice_host = 0xFFFFFFFFU;
-        return;
-    }
-    m->staged_choice_valid = true;
+    aclsp::PublishPathChoice(m->staged_choice_host, m->staged_choice_event, m->staged_choice_valid, ws, stream);
 }
 
-// The path of the matching staged Preprocess if its copy has completed
-// (0 the row / CSC kernels, 1 the staged or column-bucketed kernels, 2 the
-// banded transpose kernel, 3 the narrow-column row kernel, 4 the banded
-// transpose kernel on 16-bit copies, 5 the narrow-column row kernel on
-// entry-aligned blocks), else -1.
+// The path of the matching staged Preprocess if its copy has completed, else -1.
 int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
 {
-    if (!m->staged_choice_valid || m->staged_choice_event == nullptr || m->staged_choice_host == nullptr) return -1;
-    if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
-    if (hipEventQuery(static_cast<hipEvent_t>(m->staged_choice_event)) != hipSuccess) {
-        (void)hipGetLastError();
-        return -1;
-    }
-    const uint32_t v = *static_cast<volatile const uint32_t*>(m->staged_choice_host);
-    return v <= static_cast<uint32_t>(aclsp::kEntryFlag) ? static_cast<int32_t>(v) : -1;
+    return aclsp::QueryPathChoice(m->staged_choice_host, m->staged_choice_event, m->staged_choice_valid, stream);
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
@@ -503,6 +450,88 @@ aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }
     return ACL_SPARSE_STATUS_SUCCESS;
+}
+
+namespace {
+
+bool Capturing(hipStream_t s)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;  // unknown: take the path that needs no host call
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+}  // namespace
+
+// After a Preprocess that may choose a path on the device: copy the path flag
+// it leaves in the workspace header to pinned host memory and record an event
+// after the copy.  The host value starts as a sentinel, so a copy that has not
+// run reads as "unknown"; a previous copy is waited for first (it may be on
+// another stream).  Under stream capture no event, copy, wait or allocation is
+// made: the choice stays unknown and every launch reads the device flag.  Any
+// failure also leaves the choice unknown.
+void PublishPathChoice(uint32_t*& host, void*& event, bool& valid, void* ws, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    valid = false;
+    if (Capturing(s)) return;
+    if (event != nullptr) {
+        (void)hipEventSynchronize(static_cast<hipEvent_t>(event));
+    } else {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        event = e;
+    }
+    if (host == nullptr) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        host = static_cast<uint32_t*>(p);
+    }
+    *host = 0xFFFFFFFFU;
+    const auto* header = static_cast<const SpmvWsHeader*>(ws);
+    if (hipMemcpyAsync(host, &header->staged_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipEventRecord(static_cast<hipEvent_t>(event), s) != hipSuccess) {
+        (void)hipGetLastError();
+        *host = 0xFFFFFFFFU;
+        return;
+    }
+    valid = true;
+}
+
+// The published path (0 the row / CSC kernels, 1 the staged or column-bucketed
+// kernels, 2 the banded transpose kernel, 3 the narrow-column row kernel, 4
+// the banded transpose kernel on 16-bit copies, 5 the narrow-column row kernel
+// on entry-aligned blocks) if its copy has completed, else -1.
+int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* stream)
+{
+    if (!valid || event == nullptr || host == nullptr) return -1;
+    if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
+    if (hipEventQuery(static_cast<hipEvent_t>(event)) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    const uint32_t v = *static_cast<volatile const uint32_t*>(host);
+    return v <= static_cast<uint32_t>(kEntryFlag) ? static_cast<int32_t>(v) : -1;
+}
+
+void ReleasePathChoice(uint32_t*& host, void*& event)
+{
+    if (event != nullptr) {
+        (void)hipEventSynchronize(static_cast<hipEvent_t>(event));
+        (void)hipEventDestroy(static_cast<hipEvent_t>(event));
+        event = nullptr;
+    }
+    if (host != nullptr) (void)hipHostFree(host);
+    host = nullptr;
 }
 
 }  // namespace aclsp

@@ -1738,12 +1738,19 @@ __device__ __forceinline__ Stage OpenFixedTile(const RowBlockParams& p, int64_t 
     return s;
 }
 
-template <typename RowT, bool kBeta, bool kFixed = false>
+// kGated / kNarrow / kEntry: as in SpmvStreamFlatKernel (the ALG2 buffer
+// holds the same narrow column copy and entry-aligned blocks).
+template <typename RowT, bool kBeta, bool kFixed = false, bool kGated = false, bool kNarrow = false,
+          bool kEntry = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlockParams p)
 {
     using L = StreamLoad<RowT, ValKind::F32, OutKind::F32>;
     __shared__ float sPAll[kFlatWaves][kStreamLds];
     __shared__ float sEAll[kFlatWaves][kStreamLds];
+    if constexpr (kGated) {
+        const uint32_t flag = ConstLoad<uint32_t>(p.skip_flag, 0);
+        if (flag >= 32U || ((p.run_mask >> flag) & 1U) == 0U) return;
+    }
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     float alpha, beta;
@@ -1755,11 +1762,16 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvOpStreamKernel(RowBlock
     const int64_t tile = ((wg % kXcds) * per + wg / kXcds) * kFlatWaves + wv;
     if (tile >= p.num_blocks) return;
     Stage cur = kFixed ? OpenFixedTile<RowT>(p, tile) : OpenTileFlat<RowT>(p, tile);
+    if constexpr (kEntry) {
+        cur.a0 = tile * kEntryChunk;  // the window holds the whole block
+        cur.c1 = cur.kspan;
+        cur.last = true;
+    }
     Triple carry{0.0f, 0.0f, 0.0f};
     int lg = 0;
     while (cur.valid) {
         L b;
-        StreamLoadStage<RowT, ValKind::F32, OutKind::F32, kBeta>(p, cur, tailStart, lane, b);
+        StreamLoadStage<RowT, ValKind::F32, OutKind::F32, kBeta, kNarrow, false, kEntry>(p, cur, tailStart, lane, b);
         StreamGather<RowT, ValKind::F32, OutKind::F32>(p, cur, tailStart, rx, lane, b, b.xg);
         StreamChunkOp<RowT, kBeta>(cur, b, sPAll[wv], sEAll[wv], lane, alpha, beta, carry, lg, p.z);
         if (cur.last) break;
@@ -2980,22 +2992,58 @@ int LaunchSpmvOpStreamFixed(const SpmvLaunch& l, float* z, void* stream)
     return 0;
 }
 
+template <typename RowT, bool kGated, bool kNarrow, bool kEntry>
+void LaunchOpStreamVariant(const RowBlockParams& p, bool betaNz, hipStream_t s)
+{
+    const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
+    const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+    if (betaNz) {
+        hipLaunchKernelGGL((SpmvOpStreamKernel<RowT, true, false, kGated, kNarrow, kEntry>), dim3(g),
+                           dim3(kWave * kFlatWaves), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((SpmvOpStreamKernel<RowT, false, false, kGated, kNarrow, kEntry>), dim3(g),
+                           dim3(kWave * kFlatWaves), 0, s, p);
+    }
+}
+
+template <typename RowT>
+void LaunchOpStreamTyped(const SpmvLaunch& l, RowBlockParams p, bool betaNz, hipStream_t s)
+{
+    const bool narrow = l.narrow && p.ncol != nullptr;
+    RowBlockParams pe = p;  // the entry-aligned blocks
+    pe.blocks = At<const int32_t>(l.ws, l.layout.eb_offset);
+    pe.block_nnz = At<const void>(l.ws, l.layout.en_offset);
+    pe.num_blocks = l.layout.entry_blocks;
+    if (narrow && l.staged_choice == kEntryFlag) {
+        LaunchOpStreamVariant<RowT, false, true, true>(pe, betaNz, s);
+    } else if (narrow && l.staged_choice == kNarrowFlag) {
+        LaunchOpStreamVariant<RowT, false, true, false>(p, betaNz, s);
+    } else if (narrow && l.staged_choice < 0) {
+        // choice not on the host yet: every variant, each runs on its own flag
+        const uint32_t* flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
+        p.skip_flag = flag;
+        pe.skip_flag = flag;
+        RowBlockParams pn = p;
+        p.run_mask = 1U;
+        pn.run_mask = 1U << kNarrowFlag;
+        pe.run_mask = 1U << kEntryFlag;
+        LaunchOpStreamVariant<RowT, true, false, false>(p, betaNz, s);
+        LaunchOpStreamVariant<RowT, true, true, false>(pn, betaNz, s);
+        LaunchOpStreamVariant<RowT, true, true, true>(pe, betaNz, s);
+    } else {
+        LaunchOpStreamVariant<RowT, false, false, false>(p, betaNz, s);
+    }
+}
+
 int LaunchSpmvOpStream(const SpmvLaunch& l, float* z, void* stream)
 {
     if (l.rows <= 0) return 0;
     RowBlockParams p = MakeRowBlockParams(l);
     p.z = z;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
-    const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
     const bool betaNz = l.device_scalars || l.beta_re != 0.0f;
-    if (l.rowptr64) {
-        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
-        else hipLaunchKernelGGL((SpmvOpStreamKernel<int64_t, false>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
-    } else {
-        if (betaNz) hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, true>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
-        else hipLaunchKernelGGL((SpmvOpStreamKernel<int32_t, false>), dim3(g), dim3(kWave * kFlatWaves), 0, s, p);
-    }
+    if (l.rowptr64) LaunchOpStreamTyped<int64_t>(l, p, betaNz, s);
+    else LaunchOpStreamTyped<int32_t>(l, p, betaNz, s);
     return 0;
 }
 

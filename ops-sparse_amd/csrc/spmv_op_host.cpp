@@ -132,9 +132,15 @@ aclsparseStatus_t aclsparseSpMVOp_createDescr(aclsparseHandle_t handle, aclspars
                 return ACL_SPARSE_STATUS_INVALID_VALUE;
             }
             (void)hipGetLastError();
+            d->narrow = aclsp::SpmvOpNarrowUsable(*d);
             if (aclsp::LaunchSpmvOpPreprocess(*d, StreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
+                aclsp::ReleasePathChoice(d->choice_host, d->choice_event);
                 delete d;
                 return ACL_SPARSE_STATUS_EXECUTION_FAILED;
+            }
+            if (d->narrow) {
+                aclsp::PublishPathChoice(d->choice_host, d->choice_event, d->choice_valid,
+                                         aclsp::SpmvOpSpmvWorkspace(*d), StreamOf(handle));
             }
         }
     }
@@ -147,6 +153,7 @@ aclsparseStatus_t aclsparseSpMVOp_destroyDescr(aclsparseSpMVOpDescr_t descr)
     if (descr == nullptr) return ACL_SPARSE_STATUS_SUCCESS;
     if (descr->signature != aclsp::kSpMVOpDescrSignature) return ACL_SPARSE_STATUS_INVALID_VALUE;
     descr->signature = 0;
+    aclsp::ReleasePathChoice(descr->choice_host, descr->choice_event);
     delete descr;
     return ACL_SPARSE_STATUS_SUCCESS;
 }

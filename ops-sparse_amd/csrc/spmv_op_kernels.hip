@@ -180,8 +180,9 @@ SpmvOpLayout SpmvOpComputeLayout(int64_t m, int64_t n, int64_t nnz, aclsparseInd
     l.temp = AlignUp(l.running + static_cast<size_t>(m) * sizeof(int64_t));
     l.temp_bytes = m > 0 ? SortScanTempBytes(m) : 0;
     l.spmv = AlignUp(l.temp + l.temp_bytes + 256);  // +256: the temp area is re-aligned to 256 bytes
+    // (with the narrow column copy for matrices that can have one)
     l.sl = ComputeLayout(static_cast<uint64_t>(m), static_cast<uint64_t>(n), static_cast<uint64_t>(nnz), rowType,
-                         ACL_FLOAT, false, false);
+                         ACL_FLOAT, false, false, 0U, true);
     l.total = AlignUp(l.spmv + l.sl.total);
     return l;
 }
@@ -218,8 +219,30 @@ SpmvLaunch OpLaunch(const aclsparseSpMVOpDescr& d, const SpmvOpLayout& l)
     sl.op = ACL_SPARSE_OP_NON_TRANSPOSE;
     sl.ws = static_cast<uint8_t*>(d.buffer) + l.spmv;
     sl.layout = l.sl;
+    sl.staged_choice = -1;
     return sl;
 }
+
+bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
+
+}  // namespace
+
+// ALG2: the narrow column copy is built when the layout has it and the
+// stream kernel reads these operands (16-byte aligned columns and values, x
+// addressable with 32-bit byte offsets).
+bool SpmvOpNarrowUsable(const aclsparseSpMVOpDescr& d)
+{
+    return d.alg == ACL_SPARSE_SPMVOP_ALG2 && LayoutOf(d).sl.narrow && d.col_ind != nullptr && d.values != nullptr &&
+           Aligned16(d.col_ind) && Aligned16(d.values) && d.nnz >= 4 && d.n * 4ULL <= 0x7FFFFFFFULL;
+}
+
+void* SpmvOpSpmvWorkspace(const aclsparseSpMVOpDescr& d)
+{
+    return static_cast<uint8_t*>(d.buffer) + LayoutOf(d).spmv;
+}
+
+namespace {
+
 
 }  // namespace
 
@@ -290,8 +313,10 @@ int LaunchSpmvOpPreprocess(const aclsparseSpMVOpDescr& d, void* stream)
     t.temp = ws + l.temp;
     t.temp_bytes = l.temp_bytes;
     if (LaunchLengthTables(t, stream) != 0) return 1;
-    // the execution kernel's row-block partition
-    return LaunchSpmvPreprocess(OpLaunch(d, l), stream);
+    // the execution kernel's row-block partition (and the narrow column copy)
+    SpmvLaunch sl = OpLaunch(d, l);
+    sl.narrow = d.narrow ? 1 : 0;
+    return LaunchSpmvPreprocess(sl, stream);
 }
 
 int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void* y, void* z, float alpha,
@@ -326,6 +351,8 @@ int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void
         // for its cores; the merge-path row blocks balance any row-length
         // distribution without them).
         SpmvLaunch sl = OpLaunch(d, LayoutOf(d));
+        sl.narrow = d.narrow ? 1 : 0;
+        sl.staged_choice = d.narrow ? QueryPathChoice(d.choice_host, d.choice_event, d.choice_valid, stream) : -1;
         sl.x = x;
         sl.y = const_cast<void*>(y);
         sl.device_scalars = deviceScalars ? 1 : 0;

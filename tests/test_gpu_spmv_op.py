@@ -356,3 +356,59 @@ def test_one_based_indices_and_long_rows(alg, i64, dev):
     ok, mere, mare = oracle.verify_mere_mare(golden, z.cpu().numpy(), 1e-6, 5.0)
     assert ok, (mere, mare)
     op.close()
+
+
+def _spmv_flag(op):
+    """The path flag in the header of the SpMV workspace inside an ALG2 buffer (found by its magic word,
+    after the reference's tables): 0 col_ind, 3 narrow columns, 5 narrow columns on entry-aligned blocks."""
+    buf = op.buffer.cpu().numpy()
+    words = buf[: buf.size // 4 * 4].view(np.uint32)
+    hits = np.nonzero(words[::16] == 0x4D505348)[0]  # 64-byte aligned header starts
+    assert hits.size >= 1
+    return int(words[hits[-1] * 16 + 32])
+
+
+@pytest.mark.parametrize("case", ["laplacian", "long_rows"])
+def test_alg2_narrow_columns(case, dev):
+    """ALG2 on matrices of at least 2^20 entries: createDescr builds the 16-bit column copy (flag 5 for the
+    Laplacian, whose 480-entry chunks fit; flag 3 for rows of 2000 entries). Bit-identical across runs and
+    rebuilt descriptors, within 2 ulp of the fp64 golden like every ALG2 result, and equal in value to ALG1
+    within the same bound."""
+    if case == "laplacian":
+        w = __import__("ops_sparse.workloads", fromlist=["laplacian_2d"]).laplacian_2d(n=1024)
+        rp, col, val = w.row_ptr.numpy().astype(np.int64), w.col_ind.numpy(), w.values.numpy()
+        m = k = w.rows
+        want = 5
+    else:
+        m = k = 1024
+        band = 2001
+        off = np.arange(band) - band // 2
+        col = np.clip(np.arange(m)[:, None] + off[None, :], 0, m - 1).reshape(-1).astype(np.int32)
+        rp = np.arange(0, m * band + 1, band, dtype=np.int64)
+        val = np.random.default_rng(3).uniform(-2, 2, col.size).astype(np.float32)
+        want = 3
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-3, 3, k).astype(np.float32)
+    y = rng.uniform(-3, 3, m).astype(np.float32)
+    d = [torch.from_numpy(a).to(dev) for a in (rp.astype(np.int32), col, val, x, y)]
+    outs = []
+    for alg in (SpMVOpAlg.ALG2, SpMVOpAlg.ALG2, SpMVOpAlg.ALG1):
+        z = torch.full((m,), float("nan"), device=dev)
+        op = SpMVOp(m, k, *d, z, alg=alg)
+        op.run(1.25, -0.5)  # issued right after createDescr: every kernel variant, gated on the device flag
+        torch.cuda.synchronize()
+        first = z.clone()
+        op.run(1.25, -0.5)  # the choice on the host: one kernel
+        torch.cuda.synchronize()
+        assert torch.equal(first.view(torch.int32), z.view(torch.int32))
+        if alg == SpMVOpAlg.ALG2:
+            assert _spmv_flag(op) == want
+        outs.append(z.cpu().numpy())
+        op.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    golden = oracle.spmv_f64(rp, col, val, x, y, 1.25, -0.5)
+    scale = oracle.row_scale(rp, col, val, x, y, oracle.K_F32, oracle.K_F32, 1.25, -0.5, cols=k)
+    ulp = np.spacing(np.abs(golden.astype(np.float32))).astype(np.float64)
+    for o in (outs[0], outs[2]):
+        err = np.abs(o.astype(np.float64) - golden)
+        assert np.all(err <= 2 * ulp + 1e-12 * scale), float(np.max(err / (ulp + 1e-30)))
