@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 #include "aclsparse_internal.h"
 
@@ -431,6 +432,7 @@ void SpmmOpKernel(MmParams p)
 // LDS; op(B) is read from L2 once per workgroup instead of once per entry.
 // One row per wave at a time, its entries shared by cross-lane reads.
 constexpr int kLdsBytes = 64 * 1024;
+constexpr int kLdsWideBytes = 128 * 1024;  // J = 4 tiles without compensation
 constexpr int kLdsThreads = 1024;  // 16 waves share one staged tile
 constexpr int kLdsRowsPerWave = 4;
 
@@ -532,6 +534,196 @@ __global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(8))
     }
 }
 
+// Stages op(B)[0:k, jt:jt+TW] in LDS as fp32 (row r at sB[r*TW]; columns past
+// n read as 0).  Full tiles of a row-major op(B) whose rows start on a
+// 4-element boundary move 4 elements per load, four loads in flight per
+// thread; other tiles element by element.
+template <bool kHalf, int TW>
+__device__ __forceinline__ void StageBTile(const MmParams& p, const typename Elem<kHalf>::T* b, float* sB, int64_t jt,
+                                          int k)
+{
+    using T = typename Elem<kHalf>::T;
+    if (p.b_contig && p.b_vec && jt + TW <= p.n) {
+        constexpr int kQ = TW / 4;  // 4-element groups per staged row
+        const int total = k * kQ;
+        for (int i0 = static_cast<int>(threadIdx.x); i0 < total; i0 += 4 * kLdsThreads) {
+            Vec<T, 4> w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = i0 + u * kLdsThreads;
+                const int r = idx < total ? idx / kQ : 0, q = idx < total ? idx % kQ : 0;
+                w[u] = *reinterpret_cast<const Vec<T, 4>*>(b + static_cast<int64_t>(r) * p.ldb + jt + 4 * q);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = i0 + u * kLdsThreads;
+                if (idx < total) {
+                    float4 f;
+                    if constexpr (kHalf) {
+                        f = make_float4(Half2Float(w[u].v[0]), Half2Float(w[u].v[1]), Half2Float(w[u].v[2]),
+                                        Half2Float(w[u].v[3]));
+                    } else {
+                        f = make_float4(w[u].v[0], w[u].v[1], w[u].v[2], w[u].v[3]);
+                    }
+                    *reinterpret_cast<float4*>(&sB[(idx / kQ) * TW + 4 * (idx % kQ)]) = f;
+                }
+            }
+        }
+    } else if (p.b_contig) {
+        for (int idx = static_cast<int>(threadIdx.x); idx < k * TW; idx += kLdsThreads) {
+            const int r = idx / TW, cj = idx - r * TW;
+            const int64_t j = jt + cj;
+            sB[idx] = j < p.n ? Elem<kHalf>::Load(b, static_cast<int64_t>(r) * p.ldb + j) : 0.0f;
+        }
+    } else {
+        for (int idx = static_cast<int>(threadIdx.x); idx < k * TW; idx += kLdsThreads) {
+            const int cj = idx / k, r = idx - cj * k;
+            const int64_t j = jt + cj;
+            sB[r * TW + cj] = j < p.n ? Elem<kHalf>::Load(b, j * p.ldb + r) : 0.0f;
+        }
+    }
+}
+
+// Lane Q of the lane's 16-lane row (DPP row_newbcast: the compiler folds it
+// into the instruction that uses the value).
+template <int Q>
+__device__ __forceinline__ int RowBcast(int v)
+{
+    return __builtin_amdgcn_mov_dpp(v, 0x150 + Q, 0xF, 0xF, true);
+}
+
+// Entry Q of a batch of 16 held by lanes 0..15 of every 16-lane row (byte
+// offset of its op(B) row in LDS, with the sign bit set for a skipped entry,
+// and its value): its products with the lane's J columns added in order.
+template <int J, bool kAll, int Q>
+__device__ __forceinline__ void BcastEntry(const char* sB, uint32_t laneOff, int off, float v, float acc[J])
+{
+    bool take = true;
+    int o;
+    if constexpr (kAll) {
+        o = RowBcast<Q>(off);
+    } else {
+        o = RowBcast<Q>(off);
+        take = o >= 0;
+        o &= 0x7FFFFFFF;  // a skipped entry reads row 0
+    }
+    const Vec<float, J> w = *reinterpret_cast<const Vec<float, J>*>(sB + (o + laneOff));
+    const float vq = __int_as_float(RowBcast<Q>(__float_as_int(v)));
+#pragma unroll
+    for (int t = 0; t < J; ++t) {
+        const float s2 = acc[t] + vq * w.v[t];
+        acc[t] = take ? s2 : acc[t];
+    }
+}
+
+template <int J, bool kAll, int... Q>
+__device__ __forceinline__ void BcastBatch(std::integer_sequence<int, Q...>, const char* sB, uint32_t laneOff, int off,
+                                           float v, float acc[J])
+{
+    (BcastEntry<J, kAll, Q>(sB, laneOff, off, v, acc), ...);
+}
+
+// Entries first..15 of a batch whose columns are all in range (a row's last
+// batch holds its entries in the top slots): wave-uniform branches, no selects.
+template <int J, int Q>
+__device__ __forceinline__ void BcastFrom(int first, const char* sB, uint32_t laneOff, int off, float v, float acc[J])
+{
+    if (first <= Q) BcastEntry<J, true, Q>(sB, laneOff, off, v, acc);
+    if constexpr (Q < 15) BcastFrom<J, Q + 1>(first, sB, laneOff, off, v, acc);
+}
+
+// The small-k LDS kernel without compensation, entries handed out by DPP
+// broadcasts instead of readlane: each 16-lane row of the wave loads the same
+// 16 entries (column as an LDS byte offset, value), and entry q reaches every
+// lane as the broadcast operand of the address add and of the multiplies.
+// Per entry and lane: one address add, one LDS read of J columns, J
+// multiplies and J adds.  Same tiles, rows and sums as SpmmOpLdsKernel.
+template <typename RowT, bool kHalf, int J>
+__global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(J >= 4 ? 4 : 8))) void SpmmOpLdsBcastKernel(MmParams p)
+{
+    using T = typename Elem<kHalf>::T;
+    extern __shared__ float sB[];
+    constexpr int TW = kMmWave * J;
+    constexpr int kBatch = 16;
+    constexpr int kWindow = 4;  // batches loaded together
+    const T* val = static_cast<const T*>(p.val);
+    const T* b = static_cast<const T*>(p.b);
+    T* c = static_cast<T*>(p.c);
+    const float alpha = p.alpha_ptr != nullptr ? *p.alpha_ptr : p.alpha;
+    const float beta = p.beta_ptr != nullptr ? *p.beta_ptr : p.beta;
+    const bool betaZero = beta == 0.0f;
+    const int lane = static_cast<int>(threadIdx.x) & (kMmWave - 1);
+    const int sub = lane & (kBatch - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMmWave);
+    const int64_t tile = static_cast<int64_t>(blockIdx.x) % p.tiles;
+    const int64_t chunk = static_cast<int64_t>(blockIdx.x) / p.tiles;
+    const int64_t jt = tile * TW;
+    const int k = static_cast<int>(p.k);
+    const int64_t row0 = (chunk * (kLdsThreads / kMmWave) + wv) * kLdsRowsPerWave;
+    const int nRows = static_cast<int>(p.m - row0 < kLdsRowsPerWave ? (p.m - row0 > 0 ? p.m - row0 : 0)
+                                                                     : kLdsRowsPerWave);
+    // A window of kWindow batches: lane sub of every 16-lane row holds slot
+    // sub of each batch; a batch's entries fill its slots first..15.
+    struct Window {
+        int off[kWindow];
+        float v[kWindow];
+        int first[kWindow];
+    };
+    auto load = [&](int64_t e0, int64_t re, Window& w) {
+#pragma unroll
+        for (int q = 0; q < kWindow; ++q) {
+            const int64_t left = re - (e0 + q * kBatch);
+            w.first[q] = left >= kBatch ? 0 : left > 0 ? kBatch - static_cast<int>(left) : kBatch;
+            const int64_t e = e0 + q * kBatch + sub - w.first[q];
+            int32_t ci = -1;
+            float x = 0.0f;
+            if (sub >= w.first[q]) {
+                ci = p.col[e] - p.base;
+                x = Elem<kHalf>::Load(val, e);
+            }
+            w.off[q] = ci >= 0 && ci < k ? ci * (TW * 4) : static_cast<int>(0x80000000U);
+            w.v[q] = x;
+        }
+    };
+    StageBTile<kHalf, TW>(p, b, sB, jt, k);
+    __syncthreads();
+    const char* sBytes = reinterpret_cast<const char*>(sB);
+    const uint32_t laneOff = static_cast<uint32_t>(lane * J * 4);
+    const int64_t j0 = jt + lane * J;
+    for (int rr = 0; rr < nRows; ++rr) {
+        const int64_t row = row0 + rr;
+        const int64_t rs = static_cast<int64_t>(ConstLoad<RowT>(p.rp, row)) - p.base;
+        const int64_t re = static_cast<int64_t>(ConstLoad<RowT>(p.rp, row + 1)) - p.base;
+        float acc[J], old[J];
+#pragma unroll
+        for (int q = 0; q < J; ++q) {
+            acc[q] = 0.0f;
+            old[q] = 0.0f;
+        }
+        if (j0 < p.n && !betaZero) SpmmLoadC<kHalf, J>(p, c, row, j0, old);
+        for (int64_t e0 = rs; e0 < re; e0 += kBatch * kWindow) {
+            Window cur;
+            load(e0, re, cur);
+#pragma unroll
+            for (int q = 0; q < kWindow; ++q) {
+                if (cur.first[q] == kBatch) break;  // wave-uniform: no entries left
+                if (__ballot(cur.off[q] < 0 && sub >= cur.first[q]) == 0) {  // every entry of the batch taken
+                    if (cur.first[q] == 0) {
+                        BcastBatch<J, true>(std::make_integer_sequence<int, kBatch>{}, sBytes, laneOff, cur.off[q],
+                                            cur.v[q], acc);
+                    } else {
+                        BcastFrom<J, 0>(cur.first[q], sBytes, laneOff, cur.off[q], cur.v[q], acc);
+                    }
+                } else {
+                    BcastBatch<J, false>(std::make_integer_sequence<int, kBatch>{}, sBytes, laneOff, cur.off[q],
+                                         cur.v[q], acc);
+                }
+            }
+        }
+        if (j0 < p.n) SpmmStore<kHalf, J>(p, c, row, j0, acc, alpha, beta, betaZero, old);
+    }
+}
+
 // nnz == 0: C = beta * C_old (0 when beta == 0), every element of the m x n view.
 template <bool kHalf>
 __global__ __launch_bounds__(kMmThreads) void SpmmOpBetaCKernel(MmParams p)
@@ -590,16 +782,25 @@ void DispatchLds(const MmParams& p, int J, bool kahan, unsigned grid, unsigned l
 {
 #define SPMM_LDS(JJ, KK) \
     hipLaunchKernelGGL((SpmmOpLdsKernel<RowT, kHalf, KK, JJ>), dim3(grid), dim3(kLdsThreads), lds, s, p)
+#define SPMM_BCAST(JJ) \
+    hipLaunchKernelGGL((SpmmOpLdsBcastKernel<RowT, kHalf, JJ>), dim3(grid), dim3(kLdsThreads), lds, s, p)
     if (kahan && !kHalf) {
         if (J == 4) SPMM_LDS(4, true);
         else if (J == 2) SPMM_LDS(2, true);
         else SPMM_LDS(1, true);
+    } else if (lds > static_cast<unsigned>(kLdsBytes)) {  // J = 4 over up to 128 KiB: one workgroup per CU
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&SpmmOpLdsBcastKernel<RowT, kHalf, 4>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsWideBytes));
+        (void)attr;
+        SPMM_BCAST(4);
     } else {
-        if (J == 4) SPMM_LDS(4, false);
-        else if (J == 2) SPMM_LDS(2, false);
-        else SPMM_LDS(1, false);
+        if (J == 4) SPMM_LDS(4, false);  // (the broadcast kernel spills at J = 4 and eight waves per SIMD)
+        else if (J == 2) SPMM_BCAST(2);
+        else SPMM_BCAST(1);
     }
 #undef SPMM_LDS
+#undef SPMM_BCAST
 }
 
 bool AlignedTo(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
@@ -642,10 +843,13 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     const bool kahan = l.high_precision != 0;
     // small k: op(B) column tiles staged in LDS (n of at least one wave's width)
     if (l.k > 0 && l.n >= kMmWave && l.k * kMmWave * 4 <= kLdsBytes) {
-        const int J = l.k * kMmWave * 4 * 4 <= kLdsBytes ? 4 : l.k * kMmWave * 4 * 2 <= kLdsBytes ? 2 : 1;
+        const int J = l.k * kMmWave * 4 * 4 <= (kahan ? kLdsBytes : kLdsWideBytes) ? 4
+                      : l.k * kMmWave * 4 * 2 <= kLdsBytes                      ? 2
+                                                                                : 1;
         const int64_t tw = int64_t{kMmWave} * J;
         p.tiles = (l.n + tw - 1) / tw;
         p.c_vec = l.c_row_major && l.ldc % J == 0 && AlignedTo(l.c, J * esz) ? 1 : 0;
+        p.b_vec = l.ldb % 4 == 0 && AlignedTo(l.b, 4 * esz) ? 1 : 0;  // staging 4 elements per load
         const int64_t rowsPerBlock = int64_t{kLdsThreads / kMmWave} * kLdsRowsPerWave;
         const int64_t blocks = (l.m + rowsPerBlock - 1) / rowsPerBlock * p.tiles;
         if (blocks <= 0x7FFFFFFF) {

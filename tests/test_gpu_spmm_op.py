@@ -267,6 +267,26 @@ def test_narrow_groups_bit_exact(n, alg, dev):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("k,n", [(128, 256), (128, 300), (100, 64), (200, 128), (64, 256)])
+@pytest.mark.parametrize("half", [False, True])
+def test_lds_tiles_long_rows_bit_exact(k, n, half, dev):
+    """The LDS paths (op(B) column tiles of 256, 128 or 64 columns) on rows of 0 to 300 entries in
+    any column order, repeated columns and columns outside [0, k) included: entries are handed out
+    16 at a time, 64 per window, so rows end in every slot of a batch and span several windows."""
+    m = 333
+    rng = np.random.default_rng(k + n)
+    lens = rng.integers(0, 301, m)
+    lens[::5] = rng.integers(0, 17, lens[::5].size)  # many single-batch rows
+    rp = np.zeros(m + 1, np.int64)
+    rp[1:] = np.cumsum(lens)
+    col = rng.integers(-2, k + 3, rp[-1]).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size)
+    b, c = rng.uniform(-1, 1, k * n), rng.uniform(-1, 1, m * n)
+    got, want, _ = _run_plan(dev, m, k, n, rp, col, val, b, c, Operation.NON_TRANSPOSE, Order.ROW, Order.ROW,
+                             SpMMOpAlg.ALG1, half, 0.5, 0.25)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("op_b", [Operation.NON_TRANSPOSE, Operation.TRANSPOSE])
 @pytest.mark.parametrize("order_b", [Order.ROW, Order.COL])
 @pytest.mark.parametrize("order_c", [Order.ROW, Order.COL])
