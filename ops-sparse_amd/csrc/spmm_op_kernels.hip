@@ -645,7 +645,7 @@ __global__ __launch_bounds__(kLdsThreads) __attribute__((amdgpu_waves_per_eu(J >
     extern __shared__ float sB[];
     constexpr int TW = kMmWave * J;
     constexpr int kBatch = 16;
-    constexpr int kWindow = 4;  // batches loaded together
+    constexpr int kWindow = J >= 4 ? 5 : 4;  // batches loaded together (J = 4: rows of up to 80 entries in one)
     const T* val = static_cast<const T*>(p.val);
     const T* b = static_cast<const T*>(p.b);
     T* c = static_cast<T*>(p.c);
