@@ -495,6 +495,17 @@ __device__ __forceinline__ float ValToFloat(uint32_t raw)
 // Chunk slot held in register j (0..7) of a lane.
 __device__ __forceinline__ int StreamSlot(int lane, int j) { return (j >> 2) * 256 + 4 * lane + (j & 3); }
 
+// The same in either layout: lane-contiguous groups of 4 (StreamSlot), or,
+// with kS, slot 64j + lane (the one-pass banded transpose, after its loads:
+// each of its value and x gathers then covers 64 consecutive slots, a few
+// columns, whose values and rows lie in a few cache lines instead of
+// spreading over 256 slots).
+template <bool kS>
+__device__ __forceinline__ int SlotOf(int lane, int j)
+{
+    return kS ? kWave * j + lane : StreamSlot(lane, j);
+}
+
 template <typename RowT, ValKind V, OutKind O>
 struct StreamLoad {
     v4i col[2];
@@ -544,10 +555,10 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
         // the previous block read before the chunk decode to other columns,
         // whose products are never summed)
         const __amdgpu_buffer_rsrc_t rn = Rsrc(p.ncol + a0, avail * 2);
+        const uint32_t rb = static_cast<uint32_t>(s.r0) + static_cast<uint32_t>(p.base);
         const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, lane * 8, 0, kBufNonTemporal));
         const v2i hi =
             __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, 512 + lane * 8, 0, kBufNonTemporal));
-        const uint32_t rb = static_cast<uint32_t>(s.r0) + static_cast<uint32_t>(p.base);
         b.col[0] = v4i{Lo16(lo.x, rb), Hi16(lo.x, rb), Lo16(lo.y, rb), Hi16(lo.y, rb)};
         b.col[1] = v4i{Lo16(hi.x, rb), Hi16(hi.x, rb), Lo16(hi.y, rb), Hi16(hi.y, rb)};
     } else {
@@ -650,11 +661,29 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
 // Gathers x for the 8 slots of this lane.  The last nnz % 4 entries of the
 // arrays (not covered by any 16-byte group) are read here, in the one chunk
 // that reaches them.
-template <typename RowT, ValKind V, OutKind O>
+template <typename RowT, ValKind V, OutKind O, bool kS = false>
 __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stage& s, int64_t tailStart,
                                              __amdgpu_buffer_rsrc_t rx, int lane, StreamLoad<RowT, V, O>& b,
-                                             uint32_t xg[kLaneItems])
+                                             uint32_t xg[kLaneItems], float* sVal = nullptr)
 {
+    if constexpr (kS) {
+        // The loads hold lane-contiguous groups (StreamSlot); register j of
+        // lane l moves to slot 64j + l (SlotOf<true>) through the wave's own
+        // LDS slice: the columns, then the positions.
+        int32_t* t = reinterpret_cast<int32_t*>(sVal);
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
+        int32_t c[kLaneItems];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) c[j] = t[kWave * j + lane];
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.val.v[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.val.v[1];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            b.col[j >> 2][j & 3] = c[j];
+            b.val.v[j >> 2][j & 3] = t[kWave * j + lane];
+        }
+    }
     using ValT = typename ValOf<V>::T;
     if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
         // Uniform branch: only the chunk that reaches the end of the arrays.
@@ -668,7 +697,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
         }
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
-            const int64_t k = s.a0 + StreamSlot(lane, j) - tailStart;
+            const int64_t k = s.a0 + SlotOf<kS>(lane, j) - tailStart;
             if (k >= 0 && k < 3) {
                 const int kk = static_cast<int>(k);
                 b.col[j >> 2][j & 3] = kk == 0 ? tc[0] : kk == 1 ? tc[1] : tc[2];
@@ -700,7 +729,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
         uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) * static_cast<uint32_t>(sizeof(ValT));
-        off = StreamSlot(lane, j) < hiSlot && StreamSlot(lane, j) >= loSlot ? off : 0xFFFFFFF0U;
+        off = SlotOf<kS>(lane, j) < hiSlot && SlotOf<kS>(lane, j) >= loSlot ? off : 0xFFFFFFF0U;
         if constexpr (sizeof(ValT) == 4) {
             xg[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<int>(off), 0, kGatherPolicy);
         } else if constexpr (sizeof(ValT) == 2) {
@@ -715,7 +744,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
             uint32_t off = static_cast<uint32_t>(b.val.v[j >> 2][j & 3]) * 4U;
-            off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+            off = SlotOf<kS>(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
             b.val.g[j] = __builtin_amdgcn_raw_buffer_load_b32(rg, static_cast<int>(off), 0, kGatherPolicy);
         }
     }
@@ -768,7 +797,7 @@ constexpr int kStreamLds = kWaveChunk + 8;
 // the chunk's first slot leave their partial sum in `head` (also when they
 // cross both ends), the row that crosses its last slot in `tail`, and neither
 // is written to y here.
-template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false, bool kRows16 = false>
+template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kTask = false, bool kRows16 = false, bool kS = false>
 __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<RowT, V, O>& lc, float* sVal, int lane,
                                             StreamScal<V> alpha, StreamScal<V> beta, StreamSum<V>& carry, int& lg,
                                             typename OutOf<O>::T* y,
@@ -800,8 +829,13 @@ __device__ __forceinline__ void StreamChunk(const Stage& cur, const StreamLoad<R
             while (lg < 6 && (nr << (lg + 1)) <= kWave) ++lg;
         }
     }
-    *reinterpret_cast<v4f*>(&sVal[4 * lane]) = v4f{prod[0], prod[1], prod[2], prod[3]};
-    *reinterpret_cast<v4f*>(&sVal[256 + 4 * lane]) = v4f{prod[4], prod[5], prod[6], prod[7]};
+    if constexpr (kS) {
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) sVal[SlotOf<true>(lane, j)] = prod[j];
+    } else {
+        *reinterpret_cast<v4f*>(&sVal[4 * lane]) = v4f{prod[0], prod[1], prod[2], prod[3]};
+        *reinterpret_cast<v4f*>(&sVal[256 + 4 * lane]) = v4f{prod[4], prod[5], prod[6], prod[7]};
+    }
 
     // Row offsets relative to the block's first non-zero.  Lane l holds rows
     // 2l and 2l+1: row 2l ends where row 2l+1 starts, row 2l+1 where lane
@@ -1138,6 +1172,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     using ValT = typename ValOf<V>::T;
     using OutT = typename OutOf<O>::T;
     using L = StreamLoad<RowT, V, O>;
+    constexpr bool kStrided = V == ValKind::GATH && kNarrow;  // slot layout SlotOf<true>
 
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
@@ -1177,9 +1212,10 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             ChunkBounds(cur);
             L bl;
             StreamLoadStage<RowT, V, O, kBeta, kNarrow>(p, cur, tailStart, lane, bl);
-            StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, bl, bl.xg);
+            StreamGather<RowT, V, O, kStrided>(p, cur, tailStart, rx, lane, bl, bl.xg, sVal);
             float head = 0.0f, tail = 0.0f;
-            StreamChunk<RowT, V, O, kBeta, true>(cur, bl, sVal, lane, alpha, beta, carry, lg, y, sink, &head, &tail);
+            StreamChunk<RowT, V, O, kBeta, true, false, kStrided>(cur, bl, sVal, lane, alpha, beta, carry, lg, y, sink,
+                                                                 &head, &tail);
             // The partial sums go to memory with device-scope stores (they
             // bypass this XCD's L2), complete before the arrival is counted,
             // and the last task reads them with device-scope loads: no
@@ -1220,8 +1256,9 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             while (cur.valid) {
                 L b;
                 StreamLoadStage<RowT, V, O, kBeta, kNarrow, k16, kEntry>(p, cur, tailStart, lane, b);
-                StreamGather<RowT, V, O>(p, cur, tailStart, rx, lane, b, b.xg);
-                StreamChunk<RowT, V, O, kBeta, false, k16>(cur, b, sVal, lane, alpha, beta, carry, lg, y, sink);
+                StreamGather<RowT, V, O, kStrided>(p, cur, tailStart, rx, lane, b, b.xg, sVal);
+                StreamChunk<RowT, V, O, kBeta, false, k16, kStrided>(cur, b, sVal, lane, alpha, beta, carry, lg, y,
+                                                                      sink);
                 if (cur.last) break;
                 cur.c0 = cur.c1;
                 cur.first = false;

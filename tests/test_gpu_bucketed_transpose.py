@@ -233,3 +233,40 @@ def test_banded_transpose_far_band_keeps_32_bit_streams(dev):
     plan.run()
     torch.cuda.synchronize()
     assert torch.equal(first.view(torch.int32), y.view(torch.int32))
+
+
+@pytest.mark.parametrize("extra", [5000, 9000])
+def test_banded_transpose_long_column_tasks(dev, extra):
+    """A Laplacian plus one column holding `extra` more entries (rows within extra/2 of it): still the
+    one-pass banded kernel on 16-bit copies (flag 4), with that column's block several chunks long, so
+    it is summed by tasks whose partial sums are combined; checked against the oracle and bit-identical
+    on a second run."""
+    n = 1100
+    m = n * n
+    i = torch.arange(m, dtype=torch.int64)
+    r = torch.cat([i] * 5)
+    c = torch.cat([i - n, i - 1, i, i + 1, i + n])
+    c0 = m // 2 + 17
+    rr = torch.arange(c0 - extra // 2, c0 + extra // 2 + 1, dtype=torch.int64)
+    r = torch.cat([r, rr])
+    c = torch.cat([c, torch.full_like(rr, c0)])
+    ok = (c >= 0) & (c < m)
+    key = torch.unique(r[ok] * m + c[ok])
+    r, c = key // m, key % m
+    row_ptr = torch.zeros(m + 1, dtype=torch.int64)
+    row_ptr[1:] = torch.cumsum(torch.bincount(r, minlength=m), 0)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(extra)
+    vals = torch.rand(c.numel(), generator=g) * 2 - 1
+    x = torch.rand(m, generator=g) * 2 - 1
+    y0 = torch.rand(m, generator=g) * 2 - 1
+    w = wl.Workload("laplace_longcol_T", m, m, row_ptr.to(torch.int32), c.to(torch.int32), vals, x, y0, 0.75, 1.5,
+                    trans="T").to(dev)
+    y, plan = run(w)
+    assert header(plan)[0] == 4
+    assert_close(w.to("cpu"), y)
+    first = y.clone()
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
