@@ -666,24 +666,6 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
                                              __amdgpu_buffer_rsrc_t rx, int lane, StreamLoad<RowT, V, O>& b,
                                              uint32_t xg[kLaneItems], float* sVal = nullptr)
 {
-    if constexpr (kS) {
-        // The loads hold lane-contiguous groups (StreamSlot); register j of
-        // lane l moves to slot 64j + l (SlotOf<true>) through the wave's own
-        // LDS slice: the columns, then the positions.
-        int32_t* t = reinterpret_cast<int32_t*>(sVal);
-        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
-        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
-        int32_t c[kLaneItems];
-#pragma unroll
-        for (int j = 0; j < kLaneItems; ++j) c[j] = t[kWave * j + lane];
-        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.val.v[0];
-        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.val.v[1];
-#pragma unroll
-        for (int j = 0; j < kLaneItems; ++j) {
-            b.col[j >> 2][j & 3] = c[j];
-            b.val.v[j >> 2][j & 3] = t[kWave * j + lane];
-        }
-    }
     using ValT = typename ValOf<V>::T;
     if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
         // Uniform branch: only the chunk that reaches the end of the arrays.
@@ -697,7 +679,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
         }
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
-            const int64_t k = s.a0 + SlotOf<kS>(lane, j) - tailStart;
+            const int64_t k = s.a0 + StreamSlot(lane, j) - tailStart;
             if (k >= 0 && k < 3) {
                 const int kk = static_cast<int>(k);
                 b.col[j >> 2][j & 3] = kk == 0 ? tc[0] : kk == 1 ? tc[1] : tc[2];
@@ -719,6 +701,25 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
                     b.val.v[j >> 1] = static_cast<int>(w);
                 }
             }
+        }
+    }
+    if constexpr (kS) {
+        static_assert(V == ValKind::GATH, "slot layout 64j + lane: gathered values only");
+        int32_t* t = reinterpret_cast<int32_t*>(sVal);
+        // The loads hold lane-contiguous groups (StreamSlot); register j of
+        // lane l moves to slot 64j + l (SlotOf<true>) through the wave's own
+        // LDS slice: the columns, and the positions of a gathered value.
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
+        int32_t c[kLaneItems];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) c[j] = t[kWave * j + lane];
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.val.v[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.val.v[1];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            b.col[j >> 2][j & 3] = c[j];
+            b.val.v[j >> 2][j & 3] = t[kWave * j + lane];
         }
     }
     // Slots past the chunk's last non-zero gather nothing (an offset past the
@@ -1172,7 +1173,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
     using ValT = typename ValOf<V>::T;
     using OutT = typename OutOf<O>::T;
     using L = StreamLoad<RowT, V, O>;
-    constexpr bool kStrided = V == ValKind::GATH && kNarrow;  // slot layout SlotOf<true>
+    constexpr bool kStrided = V == ValKind::GATH;  // slot layout SlotOf<true> (gathered values)
 
     __shared__ float sValAll[kFlatWaves][kStreamLds];
 
