@@ -516,6 +516,13 @@ struct StreamLoad {
     uint32_t xg[kLaneItems];  // gathered x of the 8 slots
 };
 
+// Half h of a and half h of b as the low and high halves of one word.
+__device__ __forceinline__ int32_t Pack16(int32_t a, int32_t b, int h)
+{
+    const uint32_t ua = static_cast<uint32_t>(a), ub = static_cast<uint32_t>(b);
+    return static_cast<int32_t>(h == 0 ? (ua & 0xFFFFU) | (ub << 16) : (ua >> 16) | (ub & 0xFFFF0000U));
+}
+
 // rb plus the signed 16-bit low / high half of w (wrapping 32-bit sums).
 __device__ __forceinline__ int32_t Lo16(int32_t w, uint32_t rb)
 {
@@ -549,7 +556,22 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     // 256h + 4l .. 256h + 4l + 3, so each load instruction reads 1 KiB of
     // col_ind (narrow columns 512 B; values: 1 KiB fp32, 512 B fp16) without
     // gaps.
-    if constexpr (kNarrow) {
+    if constexpr (kNarrow && V == ValKind::GATH) {
+        // the one-pass banded transpose on 16-bit copies: each slot's row
+        // offset (low half) and position offset (high half) packed in one
+        // word of b.col, decoded by StreamGather after the move to slot
+        // 64j + lane
+        const __amdgpu_buffer_rsrc_t rn = Rsrc(p.ncol + a0, avail * 2);
+        const __amdgpu_buffer_rsrc_t rq = Rsrc(p.npos + a0, avail * 2);
+        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, lane * 8, 0, kBufNonTemporal));
+        const v2i hi =
+            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, 512 + lane * 8, 0, kBufNonTemporal));
+        const v2i plo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, lane * 8, 0, kBufNonTemporal));
+        const v2i phi =
+            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, 512 + lane * 8, 0, kBufNonTemporal));
+        b.col[0] = v4i{Pack16(lo.x, plo.x, 0), Pack16(lo.x, plo.x, 1), Pack16(lo.y, plo.y, 0), Pack16(lo.y, plo.y, 1)};
+        b.col[1] = v4i{Pack16(hi.x, phi.x, 0), Pack16(hi.x, phi.x, 1), Pack16(hi.y, phi.y, 0), Pack16(hi.y, phi.y, 1)};
+    } else if constexpr (kNarrow) {
         // 16-bit offsets from the block's first row; decoded to col_ind's
         // values (the block is the one the chunk belongs to, so entries of
         // the previous block read before the chunk decode to other columns,
@@ -570,16 +592,7 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
     if constexpr (V == ValKind::UNIT) {
         (void)rv;  // no values
     } else if constexpr (V == ValKind::GATH && kNarrow) {
-        // positions from their 16-bit offsets to the slot's own index
-        const __amdgpu_buffer_rsrc_t rq = Rsrc(p.npos + a0, avail * 2);
-        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, lane * 8, 0, kBufNonTemporal));
-        const v2i hi =
-            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rq, 512 + lane * 8, 0, kBufNonTemporal));
-        const uint32_t k0 = static_cast<uint32_t>(a0) + 4U * static_cast<uint32_t>(lane);
-        const uint32_t k1 = k0 + 256U;
-        b.val.v[0] = v4i{Lo16(lo.x, k0), Hi16(lo.x, k0 + 1U), Lo16(lo.y, k0 + 2U), Hi16(lo.y, k0 + 3U)};
-        b.val.v[1] = v4i{Lo16(hi.x, k1), Hi16(hi.x, k1 + 1U), Lo16(hi.y, k1 + 2U), Hi16(hi.y, k1 + 3U)};
-        (void)rv;
+        (void)rv;  // positions: packed with the rows above
     } else if constexpr (V == ValKind::GATH) {
         b.val.v[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 0, kBufNonTemporal));
         b.val.v[1] =
@@ -661,12 +674,28 @@ __device__ __forceinline__ void StreamLoadStage(const RowBlockParams& p, const S
 // Gathers x for the 8 slots of this lane.  The last nnz % 4 entries of the
 // arrays (not covered by any 16-byte group) are read here, in the one chunk
 // that reaches them.
-template <typename RowT, ValKind V, OutKind O, bool kS = false>
+template <typename RowT, ValKind V, OutKind O, bool kS = false, bool kPacked = false>
 __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stage& s, int64_t tailStart,
                                              __amdgpu_buffer_rsrc_t rx, int lane, StreamLoad<RowT, V, O>& b,
                                              uint32_t xg[kLaneItems], float* sVal = nullptr)
 {
     using ValT = typename ValOf<V>::T;
+    if constexpr (kPacked) {
+        // packed 16-bit row / position offsets (StreamLoadStage): moved to
+        // slot 64j + lane through the wave's LDS slice, then decoded there
+        static_assert(kS && V == ValKind::GATH, "packed offsets: the banded transpose on 16-bit copies");
+        int32_t* t = reinterpret_cast<int32_t*>(sVal);
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
+        const uint32_t rb = static_cast<uint32_t>(s.r0) + static_cast<uint32_t>(p.base);
+        const uint32_t k0 = static_cast<uint32_t>(s.valid ? s.a0 : 0) + static_cast<uint32_t>(lane);
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            const int32_t w = t[kWave * j + lane];
+            b.col[j >> 2][j & 3] = Lo16(w, rb);
+            b.val.v[j >> 2][j & 3] = Hi16(w, k0 + static_cast<uint32_t>(kWave * j));
+        }
+    }
     if (s.valid && s.a0 + kWaveChunk > tailStart && tailStart < p.nnz) {
         // Uniform branch: only the chunk that reaches the end of the arrays.
         int32_t tc[3];
@@ -679,7 +708,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
         }
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
-            const int64_t k = s.a0 + StreamSlot(lane, j) - tailStart;
+            const int64_t k = s.a0 + SlotOf<kPacked>(lane, j) - tailStart;
             if (k >= 0 && k < 3) {
                 const int kk = static_cast<int>(k);
                 b.col[j >> 2][j & 3] = kk == 0 ? tc[0] : kk == 1 ? tc[1] : tc[2];
@@ -703,7 +732,7 @@ __device__ __forceinline__ void StreamGather(const RowBlockParams& p, const Stag
             }
         }
     }
-    if constexpr (kS) {
+    if constexpr (kS && !kPacked) {
         static_assert(V == ValKind::GATH, "slot layout 64j + lane: gathered values only");
         int32_t* t = reinterpret_cast<int32_t*>(sVal);
         // The loads hold lane-contiguous groups (StreamSlot); register j of
@@ -1213,7 +1242,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             ChunkBounds(cur);
             L bl;
             StreamLoadStage<RowT, V, O, kBeta, kNarrow>(p, cur, tailStart, lane, bl);
-            StreamGather<RowT, V, O, kStrided>(p, cur, tailStart, rx, lane, bl, bl.xg, sVal);
+            StreamGather<RowT, V, O, kStrided, kStrided && kNarrow>(p, cur, tailStart, rx, lane, bl, bl.xg, sVal);
             float head = 0.0f, tail = 0.0f;
             StreamChunk<RowT, V, O, kBeta, true, false, kStrided>(cur, bl, sVal, lane, alpha, beta, carry, lg, y, sink,
                                                                  &head, &tail);
@@ -1257,7 +1286,7 @@ void SpmvStreamFlatKernel(RowBlockParams p)
             while (cur.valid) {
                 L b;
                 StreamLoadStage<RowT, V, O, kBeta, kNarrow, k16, kEntry>(p, cur, tailStart, lane, b);
-                StreamGather<RowT, V, O, kStrided>(p, cur, tailStart, rx, lane, b, b.xg, sVal);
+                StreamGather<RowT, V, O, kStrided, kStrided && kNarrow>(p, cur, tailStart, rx, lane, b, b.xg, sVal);
                 StreamChunk<RowT, V, O, kBeta, false, k16, kStrided>(cur, b, sVal, lane, alpha, beta, carry, lg, y,
                                                                       sink);
                 if (cur.last) break;
