@@ -61,6 +61,7 @@ struct SpmvPlan {
     uint64_t stream_epoch = 0;
     bool staged = false;  // Preprocess built the staged-gather tables in the buffer
     bool narrow = false;  // Preprocess built the narrow column copy (if every entry fits)
+    bool cband = false;   // Preprocess wrote the complex banded transpose's CSC rows and decision
 };
 
 struct aclsparseSpMatDescr {
@@ -213,6 +214,10 @@ struct SpmvLayout {
     // accumulator type.  Transposes with nnz > INT32_MAX are rejected.
     bool csc = false;
     size_t colptr_offset = 0, entry_row_offset = 0, csc_pos_offset = 0, prod_offset = 0;
+    // complex64 transposes with 32-bit offsets (nnz < 2^28): Preprocess
+    // writes each CSC entry's row into val_b (free once the CSC pattern is
+    // built) for the one-pass banded kernel (kCbandFlag)
+    bool cband = false;
     // row-block partition of the CSC pattern (columns as rows), for the
     // column pass on the stream kernel: csc_blocks int32[Bc+1], csc_block_nnz RowT[Bc+1]
     size_t csc_blocks_offset = 0, csc_block_nnz_offset = 0;
@@ -357,6 +362,16 @@ constexpr int32_t kBandedNarrowFlag = 4;
 // block's first row and offset are known.
 constexpr int64_t kEntryChunk = 480;
 constexpr int32_t kEntryFlag = 5;
+// staged_flag value of the one-pass banded transpose of complex64 matrices
+// (values and compute complex64): written by Preprocess when at least 15/16
+// of the CSC entries lie within 2^16 positions of their CSR position and
+// their row within 2^16 of their column (value and x gathers then stay
+// local); otherwise the flag stays 0 (the CSC product and column passes).
+constexpr int32_t kCbandFlag = 2;
+inline bool CbandTypes(aclDataType valueType, aclDataType computeType)
+{
+    return valueType == ACL_COMPLEX64 && computeType == ACL_COMPLEX64;
+}
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run
 // of staged slots is padded to a multiple of this many slots.
@@ -429,7 +444,7 @@ inline size_t AccumulatorBytes(aclDataType computeType)
 
 inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
                                 aclDataType computeType, bool transpose, bool allowTasks = true,
-                                uint32_t stageValueBytes = 0, bool narrowTypes = false)
+                                uint32_t stageValueBytes = 0, bool narrowTypes = false, bool cbandTypes = false)
 {
     SpmvLayout l;
     l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
@@ -482,6 +497,7 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.csc_block_nnz_offset =
                 AlignUp(l.csc_blocks_offset + static_cast<size_t>(l.csc_num_blocks + 1) * sizeof(int32_t));
             l.row_groups = static_cast<int64_t>((n + kRowGroup - 1) / kRowGroup);
+            l.cband = cbandTypes && rb == 4U && nnz <= 0x0FFFFFFFULL;
             l.group_row_offset =
                 AlignUp(l.csc_block_nnz_offset + static_cast<size_t>(l.csc_num_blocks + 1) * rb);
             l.row_delta_offset = AlignUp(l.group_row_offset + static_cast<size_t>(l.row_groups) * sizeof(int32_t));
@@ -631,10 +647,13 @@ struct SpmvLaunch {
     int32_t staged;
     // narrow columns: Preprocess may have written the 16-bit column copy
     int32_t narrow;
-    // with staged or narrow: the path Preprocess chose, if known on the host
-    // (0 row / CSC kernels, 1 staged or column-bucketed kernels, 2 banded
-    // transpose kernel, 3 narrow-column row kernel), or -1: launch every
-    // set, each runs only on its flag values
+    // complex64 transposes: Preprocess wrote each CSC entry's row and the
+    // banded decision (path flag kCbandFlag)
+    int32_t cband;
+    // with staged, narrow or cband: the path Preprocess chose, if known on
+    // the host (0 row / CSC kernels, 1 staged or column-bucketed kernels, 2
+    // banded transpose kernel, 3 narrow-column row kernel), or -1: launch
+    // every set, each runs only on its flag values (cband: the CSC kernels)
     int32_t staged_choice;
 };
 

@@ -20,7 +20,13 @@ struct C64 {
 };
 
 __device__ __forceinline__ C64 operator+(C64 a, C64 b) { return {a.re + b.re, a.im + b.im}; }
-__device__ __forceinline__ C64 operator*(C64 a, C64 b) { return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re}; }
+// Each product and sum rounded as written (no fused multiply-add), so that
+// every kernel that multiplies the same operands gets the same bits.
+__device__ __forceinline__ C64 operator*(C64 a, C64 b)
+{
+#pragma clang fp contract(off)
+    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+}
 
 template <AccKind A> struct AccOf;
 template <> struct AccOf<AccKind::F32> { using T = float; };

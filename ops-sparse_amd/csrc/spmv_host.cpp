@@ -180,7 +180,8 @@ aclsparseStatus_t ValidateWorkspace(void* buffer)
 SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c)
 {
     return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op), true,
-                                aclsp::StageValueBytes(m->value_type, c), aclsp::NarrowTypes(m->value_type, c));
+                                aclsp::StageValueBytes(m->value_type, c), aclsp::NarrowTypes(m->value_type, c),
+                                aclsp::CbandTypes(m->value_type, c));
 }
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
@@ -207,6 +208,17 @@ bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsp
     return l.narrow && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values) &&
            m->cols * xBytes <= 0x7FFFFFFFULL;
+}
+
+// The complex banded transpose's rows and decision are built when the layout
+// has room for them and its kernel would read this matrix: unit strides,
+// bound column indices and values, x and y addressable with 32-bit byte
+// offsets.
+bool CbandUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x,
+                 const aclsparseDnVecDescr* y)
+{
+    return l.cband && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
+           x->stride == 1 && y->stride == 1 && m->rows * 8U <= 0x7FFFFFFFULL && m->nnz * 8U <= 0x7FFFFFFFULL;
 }
 
 // After a staged or narrow Preprocess: copy the path flag it leaves in the workspace
@@ -363,23 +375,26 @@ aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOpe
     if (m->rows > 0U && m->ptrs == nullptr) return ACL_SPARSE_STATUS_INVALID_VALUE;
     st = ValidateWorkspace(externalBuffer);
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
-    bool staged = false, narrow = false;
+    bool staged = false, narrow = false, cband = false;
     if (m->rows > 0U) {
         (void)hipGetLastError();
         aclsp::SpmvLaunch l = MakeLaunch(handle, opA, alpha, m, vecX, beta, vecY, computeType, alg, externalBuffer);
         staged = StageUsable(l.layout, m, vecX, vecY);
         narrow = NarrowUsable(l.layout, m, vecX, vecY);
+        cband = IsTranspose(opA) && CbandUsable(l.layout, m, vecX, vecY);
         l.staged = staged ? 1 : 0;
         l.narrow = narrow ? 1 : 0;
+        l.cband = cband ? 1 : 0;
         if (aclsp::LaunchSpmvPreprocess(l, HipStreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
             m->plan = SpmvPlan{};
             return ACL_SPARSE_STATUS_EXECUTION_FAILED;
         }
-        if (staged || narrow) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
+        if (staged || narrow || cband) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
     }
     m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
     m->plan.staged = staged;
     m->plan.narrow = narrow;
+    m->plan.cband = cband;
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
@@ -411,7 +426,8 @@ aclsparseStatus_t aclsparseSpMV(aclsparseHandle_t handle, aclsparseOperation_t o
     // pass A reads x as 16-byte vectors
     l.staged = planned && m->rows > 0U && m->plan.staged && Aligned16(vecX->values) ? 1 : 0;
     l.narrow = planned && m->rows > 0U && m->plan.narrow ? 1 : 0;
-    l.staged_choice = l.staged || l.narrow ? StagedChoice(m, stream) : -1;
+    l.cband = planned && m->rows > 0U && m->plan.cband ? 1 : 0;
+    l.staged_choice = l.staged || l.narrow || l.cband ? StagedChoice(m, stream) : -1;
     if (aclsp::LaunchSpmvCompute(l, stream) != 0 || hipGetLastError() != hipSuccess) {
         return ACL_SPARSE_STATUS_EXECUTION_FAILED;
     }

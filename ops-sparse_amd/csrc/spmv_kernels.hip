@@ -1360,10 +1360,16 @@ struct GenLoad {
     GenPart<V, A> xg[kLaneItems];
 };
 
-template <typename RowT, ValKind V, AccKind A>
+// kGath (complex64 only): the one-pass banded transpose on the CSC pattern:
+// p.col holds each entry's row (x is gathered by it), p.val its CSR position
+// (int32), and the value is gathered from p.gval by that position, conjugated
+// when p.conj is set.
+template <typename RowT, ValKind V, AccKind A, bool kGath = false>
 __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                              __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b)
 {
+    static_assert(!kGath || V == ValKind::C64, "gathered values: complex64");
+    v4i pos[2] = {};  // kGath: the slots' positions
     using ValT = typename ValOf<V>::T;
     const int64_t a0 = s.valid ? s.a0 : 0;
     int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
@@ -1373,7 +1379,12 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
     b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
-    if constexpr (V == ValKind::UNIT) {
+    if constexpr (kGath) {
+        const __amdgpu_buffer_rsrc_t rq = Rsrc(static_cast<const int32_t*>(p.val) + a0, avail * 4);
+        pos[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, 0, kBufNonTemporal));
+        pos[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rq, 1024 + lane * 16, 0, kBufNonTemporal));
+        (void)rv;
+    } else if constexpr (V == ValKind::UNIT) {
         (void)rv;
     } else if constexpr (V == ValKind::I8) {
         b.val.v[0] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, 0, kBufNonTemporal);
@@ -1411,7 +1422,9 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             const int64_t k = s.a0 + StreamSlot(lane, j);
             if (k >= tailStart && k < p.nnz) {
                 b.col[j >> 2][j & 3] = p.col[k];
-                if constexpr (V == ValKind::UNIT) {
+                if constexpr (kGath) {
+                    pos[j >> 2][j & 3] = static_cast<const int32_t*>(p.val)[k];
+                } else if constexpr (V == ValKind::UNIT) {
                 } else if constexpr (V == ValKind::I8) {
                     const ValT v = static_cast<const ValT*>(p.val)[k];
                     const uint32_t sh = 8U * static_cast<uint32_t>(j & 3);
@@ -1454,6 +1467,19 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0,
                                                                                      kGatherPolicy));
             b.xg[j] = C64{w.x, w.y};
+        }
+    }
+    if constexpr (kGath) {
+        const __amdgpu_buffer_rsrc_t rg = Rsrc(p.gval, p.gval_n * 8);
+        const bool conj = p.conj != 0;
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            uint32_t off = static_cast<uint32_t>(pos[j >> 2][j & 3]) * 8U;
+            off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+            const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rg, static_cast<int>(off), 0,
+                                                                                     kGatherPolicy));
+            b.val.v[j >> 1][(j & 1) * 2] = w.x;
+            b.val.v[j >> 1][(j & 1) * 2 + 1] = conj ? -w.y : w.y;  // as MaybeConj
         }
     }
 }
@@ -1606,7 +1632,7 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 }
 
-template <typename RowT, ValKind V, OutKind O, AccKind A>
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kGath = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
@@ -1627,7 +1653,7 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
     int lg = 0;
     while (cur.valid) {
         GenLoad<V, A> b;
-        GenLoadStage<RowT, V, A>(p, cur, tailStart, lane, rx, b);
+        GenLoadStage<RowT, V, A, kGath>(p, cur, tailStart, lane, rx, b);
         GenChunk<RowT, V, O, A>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
         if (cur.last) break;
         cur.c0 = cur.c1;
@@ -2520,6 +2546,39 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 LaunchBandedTranspose<true, true>(l, p, stream);
             }
         }
+        if constexpr (std::is_same<RowT, int32_t>::value && V == ValKind::C64 && A == AccKind::C64 &&
+                      O == OutKind::C64) {
+            // Banded complex transposes (Preprocess's choice kCbandFlag, known
+            // on the host): one pass over the CSC pattern gathering each
+            // entry's value (by its CSR position) and x (by its row)
+            if (l.cband && l.layout.cband && l.staged_choice == kCbandFlag && l.y_stride == 1 && l.x_stride == 1 &&
+                l.val_stride == 1) {
+                RowBlockParams c = p;
+                c.rp = At<void>(l.ws, l.layout.colptr_offset);
+                c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
+                c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
+                c.num_blocks = l.layout.csc_num_blocks;
+                c.col = At<const int32_t>(l.ws, l.layout.val_b_offset);  // each CSC entry's row
+                c.col_stride = 1;
+                c.val = At<const int32_t>(l.ws, l.layout.csc_pos_offset);
+                c.val_stride = 1;
+                c.gval = static_cast<const float*>(l.val);
+                c.gval_n = l.nnz;
+                c.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
+                c.x = l.x;
+                c.x_stride = 1;
+                c.rows = n;
+                c.cols = l.rows;  // length of x
+                c.base = 0;
+                c.task_wgs = 0;
+                c.task_waves = 0;
+                const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
+                const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+                hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true>), dim3(g),
+                                   dim3(kWave * kFlatWaves), 0, stream, c);
+                return 0;
+            }
+        }
         CscParams q{};
         q.colptr = At<void>(l.ws, l.layout.colptr_offset);
         q.entry_row = At<int32_t>(l.ws, l.layout.entry_row_offset);
@@ -2929,6 +2988,39 @@ void BuildBandedNarrow(const SpmvLaunch& l, hipStream_t s)
                        static_cast<const uint32_t*>(&h->narrow_bad));
 }
 
+// Complex banded transpose (kCbandFlag): each CSC entry's row, csc_row[j] =
+// entry_row[csc_pos[j]] (into val_b), and the count of entries far from the
+// band: a CSC entry more than 2^16 positions from its CSR position (its
+// value gather), or a CSR entry whose row is more than 2^16 from its column
+// (its x gather).
+__global__ __launch_bounds__(kThreads) void CbandRowKernel(const int32_t* pos, const int32_t* entryRow,
+                                                          const int32_t* col, int32_t base, int32_t* cscRow,
+                                                          int64_t nnz, uint32_t* far)
+{
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    uint32_t n = 0;
+    if (i < nnz) {
+        const int32_t q = pos[i];
+        cscRow[i] = entryRow[q];
+        const int64_t dv = static_cast<int64_t>(q) - i;
+        const int64_t dx = static_cast<int64_t>(entryRow[i]) - (static_cast<int64_t>(col[i]) - base);
+        n = (dv >= 65536 || dv <= -65536 ? 1U : 0U) + (dx >= 65536 || dx <= -65536 ? 1U : 0U);
+    }
+    const uint64_t b = __ballot(n != 0U);
+    if (b != 0U) {
+        // the wave's count, by its lanes' counts of 0..2
+        const uint32_t c = static_cast<uint32_t>(__popcll(b)) + static_cast<uint32_t>(__popcll(__ballot(n == 2U)));
+        if ((threadIdx.x & (kWave - 1)) == 0) __hip_atomic_fetch_add(far, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The complex banded decision: kCbandFlag when at most 1/16 of the 2*nnz
+// checks above failed, else 0 (the CSC product and column passes).
+__global__ void CbandDecideKernel(const uint32_t* far, int64_t nnz, uint32_t* flag)
+{
+    if (threadIdx.x == 0) *flag = static_cast<int64_t>(*far) * 16 <= 2 * nnz ? static_cast<uint32_t>(kCbandFlag) : 0U;
+}
+
 template <typename RowT>
 int BuildCsc(const SpmvLaunch& l, hipStream_t s)
 {
@@ -3173,6 +3265,16 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
         hipLaunchKernelGGL((SpmvPreprocessKernel<int32_t>), dim3(grid), dim3(kThreads), 0, s, p);
         if (l.layout.csc) {
             if (BuildCsc<int32_t>(l, s) != 0) return 1;
+            if (l.cband && l.layout.cband) {
+                SpmvWsHeader* h = At<SpmvWsHeader>(l.ws, 0);
+                hipLaunchKernelGGL(CbandRowKernel, dim3(GridFor(l.nnz)), dim3(kThreads), 0, s,
+                                   At<const int32_t>(l.ws, l.layout.csc_pos_offset),
+                                   At<const int32_t>(l.ws, l.layout.entry_row_offset), l.col,
+                                   static_cast<int32_t>(l.base), At<int32_t>(l.ws, l.layout.val_b_offset), l.nnz,
+                                   &h->narrow_bad);
+                hipLaunchKernelGGL(CbandDecideKernel, dim3(1), dim3(kWave), 0, s,
+                                   static_cast<const uint32_t*>(&h->narrow_bad), l.nnz, &h->staged_flag);
+            }
             if (!l.staged) return 0;
             if (LaunchStagedPreprocess(l, stream) != 0) return 1;
             // the banded kernel's 16-bit copies (32-bit offsets and positions only)

@@ -733,3 +733,49 @@ def test_fp16_output_rounding_edges(dev):
         got = host_bits(y)[i]
         want = np.array([tv], dtype=np.float32).astype(np.float16).view(np.uint16)[0]
         assert got == want, f"{tv!r}: got {got:#06x} want {want:#06x}"
+
+
+def _complex_laplacian(n, seed, far=0):
+    """The 5-point Laplacian of an n x n grid with complex64 values (plus, with far > 0, one entry per row
+    `far` columns off the diagonal)."""
+    m = n * n
+    i = torch.arange(m, dtype=torch.int64)
+    offs = [-n, -1, 0, 1, n] + ([far] if far else [])
+    r = torch.cat([i] * len(offs))
+    c = torch.cat([i + o for o in offs])
+    ok = (c >= 0) & (c < m)
+    key = torch.unique(r[ok] * m + c[ok])
+    r, c = key // m, key % m
+    row_ptr = torch.zeros(m + 1, dtype=torch.int64)
+    row_ptr[1:] = torch.cumsum(torch.bincount(r, minlength=m), 0)
+    g = torch.Generator().manual_seed(seed)
+    cplx = lambda k: torch.complex(torch.rand(k, generator=g) * 2 - 1, torch.rand(k, generator=g) * 2 - 1)
+    return m, row_ptr, c.to(torch.int32), cplx(c.numel()), cplx(m), cplx(m)
+
+
+@pytest.mark.parametrize("op,far,flag", [(Operation.CONJUGATE_TRANSPOSE, 0, 2), (Operation.TRANSPOSE, 0, 2),
+                                          (Operation.CONJUGATE_TRANSPOSE, 200000, 0)])
+def test_complex_banded_transpose_one_pass(op, far, flag, dev):
+    """complex64 T / H after Preprocess: a banded matrix takes the one-pass kernel over the CSC pattern
+    (path flag 2: values gathered by CSR position, x by row, conjugated for H), a matrix with an entry per
+    row far off the diagonal keeps the product and column passes (flag 0); both against the fp64 oracle,
+    and bit-identical to the same SpMV without Preprocess (the two-pass path: same products, same order)."""
+    m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 5 + far, far)
+    alpha, beta = complex(1.25, -0.5), complex(0.5, 0.25)
+    outs = []
+    for pre in (True, False):
+        y = y0.to(dev).clone()
+        plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta,
+                       op=op)
+        if pre:
+            plan.preprocess()
+            torch.cuda.synchronize()
+            h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+            assert int(h[16] & 0xFFFFFFFF) == flag
+        plan.run()  # after Preprocess synchronised: on the host's copy of the choice
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1])
+    mode = 2 if op == Operation.CONJUGATE_TRANSPOSE else 1
+    z = oracle.spmv_c64(row_ptr.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, mode, alpha, beta)
+    np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
