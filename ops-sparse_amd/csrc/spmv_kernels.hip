@@ -1366,7 +1366,7 @@ struct GenLoad {
 // when p.conj is set.
 template <typename RowT, ValKind V, AccKind A, bool kGath = false>
 __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
-                                             __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b)
+                                             __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b, int32_t* t = nullptr)
 {
     static_assert(!kGath || V == ValKind::C64, "gathered values: complex64");
     v4i pos[2] = {};  // kGath: the slots' positions
@@ -1441,12 +1441,29 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             }
         }
     }
+    if constexpr (kGath) {
+        // rows and positions move to slot 64j + lane (SlotOf<true>) through
+        // the wave's LDS slice: each gather instruction then covers 64
+        // consecutive slots
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
+        int32_t c[kLaneItems];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) c[j] = t[kWave * j + lane];
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = pos[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = pos[1];
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            b.col[j >> 2][j & 3] = c[j];
+            pos[j >> 2][j & 3] = t[kWave * j + lane];
+        }
+    }
     const int32_t hiSlot = s.valid ? static_cast<int32_t>(s.k0 + s.c1 - s.a0) : 0;
 #pragma unroll
     for (int j = 0; j < kLaneItems; ++j) {
         uint32_t off = static_cast<uint32_t>(b.col[j >> 2][j & 3] - p.base) *
                        static_cast<uint32_t>(GenXBytes<V, A>());
-        off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+        off = SlotOf<kGath>(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
         if constexpr (V == ValKind::UNIT) {
             const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0,
                                                                                      kGatherPolicy));
@@ -1475,7 +1492,7 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
             uint32_t off = static_cast<uint32_t>(pos[j >> 2][j & 3]) * 8U;
-            off = StreamSlot(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
+            off = SlotOf<true>(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
             const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rg, static_cast<int>(off), 0,
                                                                                      kGatherPolicy));
             b.val.v[j >> 1][(j & 1) * 2] = w.x;
@@ -1505,7 +1522,7 @@ __device__ __forceinline__ T WaveAllSum(T v)
     return v;
 }
 
-template <typename RowT, ValKind V, OutKind O, AccKind A>
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kS = false>
 __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& cur, const GenLoad<V, A>& lc,
                                          GenPart<V, A>* sVal, int lane, typename AccOf<A>::T alpha,
                                          typename AccOf<A>::T beta, bool betaNz, typename AccOf<A>::T& carry, int& lg)
@@ -1530,7 +1547,7 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
         }
     }
 #pragma unroll
-    for (int j = 0; j < kLaneItems; ++j) sVal[StreamSlot(lane, j)] = prod[j];
+    for (int j = 0; j < kLaneItems; ++j) sVal[SlotOf<kS>(lane, j)] = prod[j];
 
     const int32_t k0lo = static_cast<int32_t>(cur.k0);
     int32_t rs[2], re[2];
@@ -1653,8 +1670,8 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
     int lg = 0;
     while (cur.valid) {
         GenLoad<V, A> b;
-        GenLoadStage<RowT, V, A, kGath>(p, cur, tailStart, lane, rx, b);
-        GenChunk<RowT, V, O, A>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
+        GenLoadStage<RowT, V, A, kGath>(p, cur, tailStart, lane, rx, b, reinterpret_cast<int32_t*>(sValAll[wv]));
+        GenChunk<RowT, V, O, A, kGath>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
         if (cur.last) break;
         cur.c0 = cur.c1;
         cur.first = false;
