@@ -68,6 +68,20 @@ def profile_mode(name, steps):
             op.run(case["b"], case["c"], case["alpha"], case["beta"])
         torch.cuda.synchronize()
         return
+    if name.startswith("c2_spmvop_"):
+        from ops_sparse.spmv import SpMVOp
+        from ops_sparse._lib import SpMVOpAlg
+        from ops_sparse import workloads as wl
+
+        w = wl.config("c2", dev)
+        z = torch.empty_like(w.y0)
+        op = SpMVOp(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, w.y0, z,
+                    alg=getattr(SpMVOpAlg, name[len("c2_spmvop_"):].upper()))
+        for _ in range(steps):
+            op.run(w.alpha, w.beta)
+        torch.cuda.synchronize()
+        op.close()
+        return
     w = make(name, dev)
     y = w.y0.to(w.out_dtype).clone()
     op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]
