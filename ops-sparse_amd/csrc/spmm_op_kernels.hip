@@ -789,10 +789,16 @@ void DispatchLds(const MmParams& p, int J, bool kahan, unsigned grid, unsigned l
         else if (J == 2) SPMM_LDS(2, true);
         else SPMM_LDS(1, true);
     } else if (lds > static_cast<unsigned>(kLdsBytes)) {  // J = 4 over up to 128 KiB: one workgroup per CU
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&SpmmOpLdsBcastKernel<RowT, kHalf, 4>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsWideBytes));
-        (void)attr;
+        // gfx950 allows 160 KiB per workgroup; the attribute is set once, and
+        // a runtime that does not need it may decline it (the launch reports
+        // real failures)
+        static const bool once = [] {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&SpmmOpLdsBcastKernel<RowT, kHalf, 4>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsWideBytes));
+            (void)hipGetLastError();
+            return true;
+        }();
+        (void)once;
         SPMM_BCAST(4);
     } else {
         if (J == 4) SPMM_LDS(4, false);  // (the broadcast kernel spills at J = 4 and eight waves per SIMD)
