@@ -368,6 +368,11 @@ constexpr int32_t kEntryFlag = 5;
 // their row within 2^16 of their column (value and x gathers then stay
 // local); otherwise the flag stays 0 (the CSC product and column passes).
 constexpr int32_t kCbandFlag = 2;
+// ... and, when every entry's row lies within 16 bits of its CSC block's
+// first column and its CSR position within 16 bits of its CSC index, the
+// same kernel on both packed into one word per entry (in val_b)
+constexpr int32_t kCbandNarrowFlag = 6;
+constexpr int32_t kMaxPathFlag = 6;  // largest path flag a host copy may hold
 inline bool CbandTypes(aclDataType valueType, aclDataType computeType)
 {
     return valueType == ACL_COMPLEX64 && computeType == ACL_COMPLEX64;

@@ -536,7 +536,7 @@ int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* str
         return -1;
     }
     const uint32_t v = *static_cast<volatile const uint32_t*>(host);
-    return v <= static_cast<uint32_t>(kEntryFlag) ? static_cast<int32_t>(v) : -1;
+    return v <= static_cast<uint32_t>(kMaxPathFlag) ? static_cast<int32_t>(v) : -1;
 }
 
 void ReleasePathChoice(uint32_t*& host, void*& event)

@@ -1363,12 +1363,15 @@ struct GenLoad {
 // kGath (complex64 only): the one-pass banded transpose on the CSC pattern:
 // p.col holds each entry's row (x is gathered by it), p.val its CSR position
 // (int32), and the value is gathered from p.gval by that position, conjugated
-// when p.conj is set.
-template <typename RowT, ValKind V, AccKind A, bool kGath = false>
+// when p.conj is set.  With kPack, p.col holds one word per entry instead:
+// the row as an offset from the block's first column (low half) and the
+// position as an offset from the entry's own CSC index (high half).
+template <typename RowT, ValKind V, AccKind A, bool kGath = false, bool kPack = false>
 __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                              __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b, int32_t* t = nullptr)
 {
     static_assert(!kGath || V == ValKind::C64, "gathered values: complex64");
+    static_assert(!kPack || kGath, "packed offsets: the gathered-value transpose");
     v4i pos[2] = {};  // kGath: the slots' positions
     using ValT = typename ValOf<V>::T;
     const int64_t a0 = s.valid ? s.a0 : 0;
@@ -1379,7 +1382,9 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
     b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
     b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
-    if constexpr (kGath) {
+    if constexpr (kPack) {
+        (void)rv;  // positions: packed with the rows
+    } else if constexpr (kGath) {
         const __amdgpu_buffer_rsrc_t rq = Rsrc(static_cast<const int32_t*>(p.val) + a0, avail * 4);
         pos[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, 0, kBufNonTemporal));
         pos[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rq, 1024 + lane * 16, 0, kBufNonTemporal));
@@ -1422,7 +1427,8 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             const int64_t k = s.a0 + StreamSlot(lane, j);
             if (k >= tailStart && k < p.nnz) {
                 b.col[j >> 2][j & 3] = p.col[k];
-                if constexpr (kGath) {
+                if constexpr (kPack) {
+                } else if constexpr (kGath) {
                     pos[j >> 2][j & 3] = static_cast<const int32_t*>(p.val)[k];
                 } else if constexpr (V == ValKind::UNIT) {
                 } else if constexpr (V == ValKind::I8) {
@@ -1441,7 +1447,20 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
             }
         }
     }
-    if constexpr (kGath) {
+    if constexpr (kPack) {
+        // the packed words move to slot 64j + lane (SlotOf<true>) through
+        // the wave's LDS slice, then are decoded there
+        *reinterpret_cast<v4i*>(&t[4 * lane]) = b.col[0];
+        *reinterpret_cast<v4i*>(&t[256 + 4 * lane]) = b.col[1];
+        const uint32_t rb = static_cast<uint32_t>(s.valid ? s.r0 : 0) + static_cast<uint32_t>(p.base);
+        const uint32_t k0 = static_cast<uint32_t>(a0) + static_cast<uint32_t>(lane);
+#pragma unroll
+        for (int j = 0; j < kLaneItems; ++j) {
+            const int32_t w = t[kWave * j + lane];
+            b.col[j >> 2][j & 3] = Lo16(w, rb);
+            pos[j >> 2][j & 3] = Hi16(w, k0 + static_cast<uint32_t>(kWave * j));
+        }
+    } else if constexpr (kGath) {
         // rows and positions move to slot 64j + lane (SlotOf<true>) through
         // the wave's LDS slice: each gather instruction then covers 64
         // consecutive slots
@@ -1649,7 +1668,7 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 }
 
-template <typename RowT, ValKind V, OutKind O, AccKind A, bool kGath = false>
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kGath = false, bool kPack = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
@@ -1670,7 +1689,7 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
     int lg = 0;
     while (cur.valid) {
         GenLoad<V, A> b;
-        GenLoadStage<RowT, V, A, kGath>(p, cur, tailStart, lane, rx, b, reinterpret_cast<int32_t*>(sValAll[wv]));
+        GenLoadStage<RowT, V, A, kGath, kPack>(p, cur, tailStart, lane, rx, b, reinterpret_cast<int32_t*>(sValAll[wv]));
         GenChunk<RowT, V, O, A, kGath>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
         if (cur.last) break;
         cur.c0 = cur.c1;
@@ -2568,14 +2587,15 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
             // Banded complex transposes (Preprocess's choice kCbandFlag, known
             // on the host): one pass over the CSC pattern gathering each
             // entry's value (by its CSR position) and x (by its row)
-            if (l.cband && l.layout.cband && l.staged_choice == kCbandFlag && l.y_stride == 1 && l.x_stride == 1 &&
-                l.val_stride == 1) {
+            const bool packed = l.staged_choice == kCbandNarrowFlag;
+            if (l.cband && l.layout.cband && (l.staged_choice == kCbandFlag || packed) && l.y_stride == 1 &&
+                l.x_stride == 1 && l.val_stride == 1) {
                 RowBlockParams c = p;
                 c.rp = At<void>(l.ws, l.layout.colptr_offset);
                 c.blocks = At<int32_t>(l.ws, l.layout.csc_blocks_offset);
                 c.block_nnz = At<void>(l.ws, l.layout.csc_block_nnz_offset);
                 c.num_blocks = l.layout.csc_num_blocks;
-                c.col = At<const int32_t>(l.ws, l.layout.val_b_offset);  // each CSC entry's row
+                c.col = At<const int32_t>(l.ws, l.layout.val_b_offset);  // each CSC entry's row (packed: with its position)
                 c.col_stride = 1;
                 c.val = At<const int32_t>(l.ws, l.layout.csc_pos_offset);
                 c.val_stride = 1;
@@ -2591,8 +2611,13 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 c.task_waves = 0;
                 const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
                 const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
-                hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true>), dim3(g),
-                                   dim3(kWave * kFlatWaves), 0, stream, c);
+                if (packed) {
+                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true, true>), dim3(g),
+                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                } else {
+                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true>), dim3(g),
+                                       dim3(kWave * kFlatWaves), 0, stream, c);
+                }
                 return 0;
             }
         }
@@ -3014,28 +3039,77 @@ __global__ __launch_bounds__(kThreads) void CbandRowKernel(const int32_t* pos, c
                                                           const int32_t* col, int32_t base, int32_t* cscRow,
                                                           int64_t nnz, uint32_t* far)
 {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    uint32_t n = 0;
-    if (i < nnz) {
-        const int32_t q = pos[i];
-        cscRow[i] = entryRow[q];
-        const int64_t dv = static_cast<int64_t>(q) - i;
-        const int64_t dx = static_cast<int64_t>(entryRow[i]) - (static_cast<int64_t>(col[i]) - base);
-        n = (dv >= 65536 || dv <= -65536 ? 1U : 0U) + (dx >= 65536 || dx <= -65536 ? 1U : 0U);
-    }
-    const uint64_t b = __ballot(n != 0U);
-    if (b != 0U) {
-        // the wave's count, by its lanes' counts of 0..2
-        const uint32_t c = static_cast<uint32_t>(__popcll(b)) + static_cast<uint32_t>(__popcll(__ballot(n == 2U)));
-        if ((threadIdx.x & (kWave - 1)) == 0) __hip_atomic_fetch_add(far, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // grid-stride: the grid is capped (GridFor)
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    for (int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads; i0 < nnz; i0 += stride) {  // wave-uniform
+        const int64_t i = i0 + (first - static_cast<int64_t>(blockIdx.x) * kThreads);
+        uint32_t n = 0;
+        if (i < nnz) {
+            const int32_t q = pos[i];
+            cscRow[i] = entryRow[q];
+            const int64_t dv = static_cast<int64_t>(q) - i;
+            const int64_t dx = static_cast<int64_t>(entryRow[i]) - (static_cast<int64_t>(col[i]) - base);
+            n = (dv >= 65536 || dv <= -65536 ? 1U : 0U) + (dx >= 65536 || dx <= -65536 ? 1U : 0U);
+        }
+        const uint64_t b = __ballot(n != 0U);
+        if (b != 0U) {
+            // the wave's count, by its lanes' counts of 0..2
+            const uint32_t c =
+                static_cast<uint32_t>(__popcll(b)) + static_cast<uint32_t>(__popcll(__ballot(n == 2U)));
+            if ((threadIdx.x & (kWave - 1)) == 0) {
+                __hip_atomic_fetch_add(far, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
     }
 }
 
-// The complex banded decision: kCbandFlag when at most 1/16 of the 2*nnz
-// checks above failed, else 0 (the CSC product and column passes).
-__global__ void CbandDecideKernel(const uint32_t* far, int64_t nnz, uint32_t* flag)
+// One wave per CSC block (first column cb, entries [k0, k1)): every entry's
+// row minus cb and CSR position minus its CSC index within int16, else bad.
+__global__ __launch_bounds__(kThreads) void CbandNarrowCheckKernel(const int32_t* cscRow, const int32_t* pos,
+                                                                  const int32_t* blocks, const int32_t* blockNnz,
+                                                                  int64_t numBlocks, uint32_t* bad)
 {
-    if (threadIdx.x == 0) *flag = static_cast<int64_t>(*far) * 16 <= 2 * nnz ? static_cast<uint32_t>(kCbandFlag) : 0U;
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (b >= numBlocks) return;
+    const int64_t cb = blocks[b], k0 = blockNnz[b], k1 = blockNnz[b + 1];
+    bool out = false;
+    for (int64_t j = k0 + lane; j < k1; j += kWave) {
+        const int64_t dr = static_cast<int64_t>(cscRow[j]) - cb, dp = static_cast<int64_t>(pos[j]) - j;
+        out = out || dr < -32768 || dr > 32767 || dp < -32768 || dp > 32767;
+    }
+    if (__ballot(out) != 0 && lane == 0) __hip_atomic_fetch_or(bad, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// With flag kCbandNarrowFlag: the rows and positions packed in place of the
+// rows (cscRow[j] becomes (row - cb) | (pos - j) << 16).
+__global__ __launch_bounds__(kThreads) void CbandNarrowPackKernel(int32_t* cscRow, const int32_t* pos,
+                                                                 const int32_t* blocks, const int32_t* blockNnz,
+                                                                 int64_t numBlocks, const uint32_t* flag)
+{
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (*flag != static_cast<uint32_t>(kCbandNarrowFlag) || b >= numBlocks) return;
+    const int64_t cb = blocks[b], k0 = blockNnz[b], k1 = blockNnz[b + 1];
+    for (int64_t j = k0 + lane; j < k1; j += kWave) {
+        const uint32_t dr = static_cast<uint32_t>(cscRow[j] - static_cast<int32_t>(cb));
+        const uint32_t dp = static_cast<uint32_t>(pos[j] - static_cast<int32_t>(j));
+        cscRow[j] = static_cast<int32_t>((dr & 0xFFFFU) | (dp << 16));
+    }
+}
+
+// The complex banded decision: when at most 1/16 of the 2*nnz checks of
+// CbandRowKernel failed, kCbandNarrowFlag if every entry fits 16 bits
+// (CbandNarrowCheckKernel), else kCbandFlag; otherwise 0 (the CSC product and
+// column passes).
+__global__ void CbandDecideKernel(const uint32_t* far, const uint32_t* narrowBad, int64_t nnz, uint32_t* flag)
+{
+    if (threadIdx.x == 0) {
+        const bool banded = static_cast<int64_t>(*far) * 16 <= 2 * nnz;
+        *flag = !banded ? 0U : *narrowBad == 0U ? static_cast<uint32_t>(kCbandNarrowFlag)
+                                                : static_cast<uint32_t>(kCbandFlag);
+    }
 }
 
 template <typename RowT>
@@ -3289,8 +3363,22 @@ int LaunchSpmvPreprocess(const SpmvLaunch& l, void* stream)
                                    At<const int32_t>(l.ws, l.layout.entry_row_offset), l.col,
                                    static_cast<int32_t>(l.base), At<int32_t>(l.ws, l.layout.val_b_offset), l.nnz,
                                    &h->narrow_bad);
+                const int64_t nb = l.layout.csc_num_blocks;
+                const unsigned bg = static_cast<unsigned>((nb + kWaves - 1) / kWaves);
+                hipLaunchKernelGGL(CbandNarrowCheckKernel, dim3(bg), dim3(kThreads), 0, s,
+                                   At<const int32_t>(l.ws, l.layout.val_b_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_pos_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_blocks_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_block_nnz_offset), nb, &h->entry_bad);
                 hipLaunchKernelGGL(CbandDecideKernel, dim3(1), dim3(kWave), 0, s,
-                                   static_cast<const uint32_t*>(&h->narrow_bad), l.nnz, &h->staged_flag);
+                                   static_cast<const uint32_t*>(&h->narrow_bad),
+                                   static_cast<const uint32_t*>(&h->entry_bad), l.nnz, &h->staged_flag);
+                hipLaunchKernelGGL(CbandNarrowPackKernel, dim3(bg), dim3(kThreads), 0, s,
+                                   At<int32_t>(l.ws, l.layout.val_b_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_pos_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_blocks_offset),
+                                   At<const int32_t>(l.ws, l.layout.csc_block_nnz_offset), nb,
+                                   static_cast<const uint32_t*>(&h->staged_flag));
             }
             if (!l.staged) return 0;
             if (LaunchStagedPreprocess(l, stream) != 0) return 1;

@@ -735,14 +735,14 @@ def test_fp16_output_rounding_edges(dev):
         assert got == want, f"{tv!r}: got {got:#06x} want {want:#06x}"
 
 
-def _complex_laplacian(n, seed, far=0):
-    """The 5-point Laplacian of an n x n grid with complex64 values (plus, with far > 0, one entry per row
-    `far` columns off the diagonal)."""
+def _complex_laplacian(n, seed, far=0, every=1):
+    """The 5-point Laplacian of an n x n grid with complex64 values (plus, with far > 0, one entry `far`
+    columns off the diagonal in every `every`-th row)."""
     m = n * n
     i = torch.arange(m, dtype=torch.int64)
-    offs = [-n, -1, 0, 1, n] + ([far] if far else [])
-    r = torch.cat([i] * len(offs))
-    c = torch.cat([i + o for o in offs])
+    offs = [-n, -1, 0, 1, n]
+    r = torch.cat([i] * len(offs) + ([i[::every]] if far else []))
+    c = torch.cat([i + o for o in offs] + ([i[::every] + far] if far else []))
     ok = (c >= 0) & (c < m)
     key = torch.unique(r[ok] * m + c[ok])
     r, c = key // m, key % m
@@ -753,14 +753,17 @@ def _complex_laplacian(n, seed, far=0):
     return m, row_ptr, c.to(torch.int32), cplx(c.numel()), cplx(m), cplx(m)
 
 
-@pytest.mark.parametrize("op,far,flag", [(Operation.CONJUGATE_TRANSPOSE, 0, 2), (Operation.TRANSPOSE, 0, 2),
-                                          (Operation.CONJUGATE_TRANSPOSE, 200000, 0)])
-def test_complex_banded_transpose_one_pass(op, far, flag, dev):
+@pytest.mark.parametrize("op,far,every,flag", [(Operation.CONJUGATE_TRANSPOSE, 0, 1, 6), (Operation.TRANSPOSE, 0, 1, 6),
+                                                (Operation.TRANSPOSE, 40000, 8, 2),
+                                                (Operation.CONJUGATE_TRANSPOSE, 200000, 1, 0)])
+def test_complex_banded_transpose_one_pass(op, far, every, flag, dev):
     """complex64 T / H after Preprocess: a banded matrix takes the one-pass kernel over the CSC pattern
-    (path flag 2: values gathered by CSR position, x by row, conjugated for H), a matrix with an entry per
-    row far off the diagonal keeps the product and column passes (flag 0); both against the fp64 oracle,
-    and bit-identical to the same SpMV without Preprocess (the two-pass path: same products, same order)."""
-    m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 5 + far, far)
+    (values gathered by CSR position, x by row, conjugated for H) on rows and positions packed as 16-bit
+    offsets (path flag 6); one entry 40 000 columns off the diagonal in every eighth row keeps it banded
+    but out of 16-bit reach (flag 2: the 32-bit rows and positions); an entry per row 200 000 columns off
+    keeps the product and column passes (flag 0). Each against the fp64 oracle, and bit-identical to the
+    same SpMV without Preprocess (the two-pass path: same products, same order)."""
+    m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 5 + far, far, every)
     alpha, beta = complex(1.25, -0.5), complex(0.5, 0.25)
     outs = []
     for pre in (True, False):
