@@ -104,3 +104,28 @@ def test_complex_laplacian_transpose_full_size(op, dev):
     z = oracle.spmv_c64(w.row_ptr.cpu().numpy(), w.col_ind.cpu().numpy(), w.values.cpu().numpy(),
                         w.x.cpu().numpy(), w.y0.cpu().numpy(), w.cols, 1 if op == "T" else 2, w.alpha, w.beta)
     np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+
+
+def test_laplacian_transpose_full_size(dev):
+    """The headline Laplacian with opA = T after Preprocess at full size: the banded one-pass kernel on
+    its 16-bit copies (path flag 4) against the oracle on every column, and bit-identical on a second run."""
+    import bench
+    from helpers import assert_close
+    from ops_sparse._lib import Operation
+
+    w = bench.make("c2_T", dev)
+    y = w.y0.clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta,
+                   op=Operation.TRANSPOSE)
+    plan.preprocess()
+    torch.cuda.synchronize()
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint32)
+    assert int(h[32]) == 4
+    plan.run()
+    torch.cuda.synchronize()
+    first = y.clone()
+    assert_close(w, y)
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first.view(torch.int32), y.view(torch.int32))
