@@ -158,18 +158,23 @@ struct SpmvWsHeader {
     uint64_t max_tasks;
     // the path Preprocess chose (0 when the plan has no choice): 0 = row /
     // CSC kernels, 1 = staged gather or column-bucketed transpose, 2 = banded
-    // one-pass transpose, 3 = row kernels on the narrow column copy; the
-    // staged bucket and tile counts and where the tile corners are
+    // one-pass transpose (fp32 or complex64), 3 = row kernels on the narrow
+    // column copy, 4 = banded fp32 transpose on 16-bit copies, 5 = narrow
+    // row kernels on entry-aligned blocks, 6 = banded complex64 transpose on
+    // packed 16-bit offsets; the staged bucket and tile counts and where the
+    // tile corners are
     uint32_t staged_flag;
     uint32_t staged_buckets;
     uint64_t staged_tiles;
     uint64_t staged_tile_row_offset;
     uint64_t staged_tile_nnz_offset;
     // narrow columns: nonzero when some entry's column is too far from its
-    // row block's first row for 16 bits (set by Preprocess)
+    // row block's first row for 16 bits (set by Preprocess); complex64
+    // transposes: the count of band checks that failed
     uint32_t narrow_bad;
     // narrow columns: nonzero when the entry-aligned row blocks do not fit
-    // (some block of more than 127 rows, or whose rows run past its window)
+    // (some block of more than 127 rows, or whose rows run past its window);
+    // complex64 transposes: nonzero when some entry's offsets exceed 16 bits
     uint32_t entry_bad;
     uint32_t reserved[6];
 };
