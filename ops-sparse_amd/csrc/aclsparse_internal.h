@@ -380,7 +380,9 @@ constexpr int32_t kCbandNarrowFlag = 6;
 constexpr int32_t kMaxPathFlag = 6;  // largest path flag a host copy may hold
 inline bool CbandTypes(aclDataType valueType, aclDataType computeType)
 {
-    return valueType == ACL_COMPLEX64 && computeType == ACL_COMPLEX64;
+    return (valueType == ACL_COMPLEX64 && computeType == ACL_COMPLEX64) ||
+           (valueType == ACL_FLOAT && computeType == ACL_COMPLEX64) ||
+           (valueType == ACL_INT8 && computeType == ACL_INT32);
 }
 
 // Staged x values are moved in chunks of 8 bytes: every (tile, bucket) run

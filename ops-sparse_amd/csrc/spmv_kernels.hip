@@ -1360,7 +1360,8 @@ struct GenLoad {
     GenPart<V, A> xg[kLaneItems];
 };
 
-// kGath (complex64 only): the one-pass banded transpose on the CSC pattern:
+// kGath (complex64, fp32 values with complex compute, int8): the one-pass
+// banded transpose on the CSC pattern:
 // p.col holds each entry's row (x is gathered by it), p.val its CSR position
 // (int32), and the value is gathered from p.gval by that position, conjugated
 // when p.conj is set.  With kPack, p.col holds one word per entry instead:
@@ -1370,7 +1371,8 @@ template <typename RowT, ValKind V, AccKind A, bool kGath = false, bool kPack = 
 __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                              __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b, int32_t* t = nullptr)
 {
-    static_assert(!kGath || V == ValKind::C64, "gathered values: complex64");
+    static_assert(!kGath || V == ValKind::C64 || V == ValKind::F32 || V == ValKind::I8,
+                  "gathered values: complex64, fp32 (complex compute) or int8");
     static_assert(!kPack || kGath, "packed offsets: the gathered-value transpose");
     v4i pos[2] = {};  // kGath: the slots' positions
     using ValT = typename ValOf<V>::T;
@@ -1506,16 +1508,28 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
         }
     }
     if constexpr (kGath) {
-        const __amdgpu_buffer_rsrc_t rg = Rsrc(p.gval, p.gval_n * 8);
+        const __amdgpu_buffer_rsrc_t rg = Rsrc(p.gval, p.gval_n * static_cast<int64_t>(sizeof(ValT)));
         const bool conj = p.conj != 0;
+        if constexpr (V == ValKind::I8) {
+            b.val.v[0] = 0U;
+            b.val.v[1] = 0U;
+        }
 #pragma unroll
         for (int j = 0; j < kLaneItems; ++j) {
-            uint32_t off = static_cast<uint32_t>(pos[j >> 2][j & 3]) * 8U;
+            uint32_t off = static_cast<uint32_t>(pos[j >> 2][j & 3]) * static_cast<uint32_t>(sizeof(ValT));
             off = SlotOf<true>(lane, j) < hiSlot ? off : 0xFFFFFFF0U;
-            const v2f w = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rg, static_cast<int>(off), 0,
-                                                                                     kGatherPolicy));
-            b.val.v[j >> 1][(j & 1) * 2] = w.x;
-            b.val.v[j >> 1][(j & 1) * 2 + 1] = conj ? -w.y : w.y;  // as MaybeConj
+            if constexpr (V == ValKind::C64) {
+                const v2f w = __builtin_bit_cast(
+                    v2f, __builtin_amdgcn_raw_buffer_load_b64(rg, static_cast<int>(off), 0, kGatherPolicy));
+                b.val.v[j >> 1][(j & 1) * 2] = w.x;
+                b.val.v[j >> 1][(j & 1) * 2 + 1] = conj ? -w.y : w.y;  // as MaybeConj
+            } else if constexpr (V == ValKind::F32) {  // (no conjugate: launched for opA = T only)
+                b.val.v[j >> 2][j & 3] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rg, static_cast<int>(off), 0, kGatherPolicy));
+            } else {
+                const uint32_t raw = __builtin_amdgcn_raw_buffer_load_b8(rg, static_cast<int>(off), 0, kGatherPolicy);
+                b.val.v[j >> 2] |= (raw & 0xFFU) << (8U * static_cast<uint32_t>(j & 3));
+            }
         }
     }
 }
@@ -2582,13 +2596,18 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 LaunchBandedTranspose<true, true>(l, p, stream);
             }
         }
-        if constexpr (std::is_same<RowT, int32_t>::value && V == ValKind::C64 && A == AccKind::C64 &&
-                      O == OutKind::C64) {
-            // Banded complex transposes (Preprocess's choice kCbandFlag, known
-            // on the host): one pass over the CSC pattern gathering each
-            // entry's value (by its CSR position) and x (by its row)
+        if constexpr (std::is_same<RowT, int32_t>::value &&
+                      ((V == ValKind::C64 && A == AccKind::C64) || (V == ValKind::F32 && A == AccKind::C64) ||
+                       (V == ValKind::I8 && A == AccKind::I64))) {
+            // Banded complex64, real-to-complex and int8 transposes
+            // (Preprocess's choice kCbandFlag or kCbandNarrowFlag, known on
+            // the host): one pass over the CSC pattern gathering each entry's
+            // value (by its CSR position) and x (by its row)
             const bool packed = l.staged_choice == kCbandNarrowFlag;
-            if (l.cband && l.layout.cband && (l.staged_choice == kCbandFlag || packed) && l.y_stride == 1 &&
+            // (real values under opA = H keep the product pass, which conjugates
+            // them to a -0 imaginary part)
+            const bool opOk = V != ValKind::F32 || l.op == ACL_SPARSE_OP_TRANSPOSE;
+            if (opOk && l.cband && l.layout.cband && (l.staged_choice == kCbandFlag || packed) && l.y_stride == 1 &&
                 l.x_stride == 1 && l.val_stride == 1) {
                 RowBlockParams c = p;
                 c.rp = At<void>(l.ws, l.layout.colptr_offset);
@@ -2612,10 +2631,10 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                 const int64_t wgs = (c.num_blocks + kFlatWaves - 1) / kFlatWaves;
                 const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
                 if (packed) {
-                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true, true>), dim3(g),
+                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, V, O, A, true, true>), dim3(g),
                                        dim3(kWave * kFlatWaves), 0, stream, c);
                 } else {
-                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, ValKind::C64, O, A, true>), dim3(g),
+                    hipLaunchKernelGGL((SpmvStreamGenKernel<int32_t, V, O, A, true>), dim3(g),
                                        dim3(kWave * kFlatWaves), 0, stream, c);
                 }
                 return 0;

@@ -782,3 +782,48 @@ def test_complex_banded_transpose_one_pass(op, far, every, flag, dev):
     mode = 2 if op == Operation.CONJUGATE_TRANSPOSE else 1
     z = oracle.spmv_c64(row_ptr.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, mode, alpha, beta)
     np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("kind", ["int8", "real_complex"])
+def test_banded_transpose_one_pass_other_types(kind, dev):
+    """int8 -> int32 and fp32 values with complex64 y (real A, complex compute) under opA = T after
+    Preprocess: the one-pass banded kernel on packed 16-bit offsets (path flag 6), bit-identical to the
+    product and column passes (the same SpMV without Preprocess) and equal to the exact result (int8) or
+    within fp32 error of the fp64 oracle (complex)."""
+    m, row_ptr, col, _, _, _ = _complex_laplacian(600, 13)
+    g = torch.Generator().manual_seed(13)
+    nnz = col.numel()
+    if kind == "int8":
+        v = torch.randint(-128, 128, (nnz,), generator=g, dtype=torch.int8)
+        x = torch.randint(-128, 128, (m,), generator=g, dtype=torch.int8)
+        y0 = torch.randint(-1000, 1000, (m,), generator=g, dtype=torch.int32)
+        alpha, beta = 2, 3
+    else:
+        v = torch.rand(nnz, generator=g) * 2 - 1
+        x = torch.rand(m, generator=g) * 2 - 1
+        y0 = torch.complex(torch.rand(m, generator=g) * 2 - 1, torch.rand(m, generator=g) * 2 - 1)
+        alpha, beta = complex(0.75, 1.25), complex(-0.5, 0.25)
+    outs = []
+    for pre in (True, False):
+        y = y0.to(dev).clone()
+        plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta,
+                       op=Operation.TRANSPOSE)
+        if pre:
+            plan.preprocess()
+            torch.cuda.synchronize()
+            h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+            assert int(h[16] & 0xFFFFFFFF) == 6
+        plan.run()
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1])
+    rp = row_ptr.numpy()
+    rows = np.repeat(np.arange(m), np.diff(rp))
+    if kind == "int8":
+        acc = np.zeros(m, np.int64)
+        np.add.at(acc, col.numpy().astype(np.int64), v.numpy().astype(np.int64) * x.numpy().astype(np.int64)[rows])
+        want = np.clip(alpha * acc + beta * y0.numpy().astype(np.int64), -2**31, 2**31 - 1)
+        np.testing.assert_array_equal(outs[0].numpy().astype(np.int64), want)
+    else:
+        z = oracle.spmv_c64(rp, col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 1, alpha, beta, val_is_real=True)
+        np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
