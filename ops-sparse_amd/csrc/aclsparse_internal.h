@@ -349,6 +349,7 @@ inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
 inline bool NarrowTypes(aclDataType valueType, aclDataType computeType)
 {
     if (computeType == ACL_FLOAT) return valueType == ACL_FLOAT || valueType == ACL_FLOAT16 || valueType == ACL_BF16;
+    if (computeType == ACL_COMPLEX64) return valueType == ACL_COMPLEX64;
     return computeType == ACL_INT32 && valueType == ACL_INT8;
 }
 

@@ -204,6 +204,7 @@ bool NarrowUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclsp
 {
     const uint64_t xBytes = m->value_type == ACL_FLOAT16 || m->value_type == ACL_BF16 ? 2U
                             : m->value_type == ACL_INT8                                 ? 1U
+                            : m->value_type == ACL_COMPLEX64                            ? 8U
                                                                                         : 4U;
     return l.narrow && m->idxs != nullptr && m->values != nullptr && m->idx_stride == 1 && m->value_stride == 1 &&
            x->stride == 1 && y->stride == 1 && Aligned16(m->idxs) && Aligned16(m->values) &&

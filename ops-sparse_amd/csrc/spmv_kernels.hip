@@ -1367,7 +1367,7 @@ struct GenLoad {
 // when p.conj is set.  With kPack, p.col holds one word per entry instead:
 // the row as an offset from the block's first column (low half) and the
 // position as an offset from the entry's own CSC index (high half).
-template <typename RowT, ValKind V, AccKind A, bool kGath = false, bool kPack = false>
+template <typename RowT, ValKind V, AccKind A, bool kGath = false, bool kPack = false, bool kNc = false>
 __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stage& s, int64_t tailStart, int lane,
                                              __amdgpu_buffer_rsrc_t rx, GenLoad<V, A>& b, int32_t* t = nullptr)
 {
@@ -1380,10 +1380,23 @@ __device__ __forceinline__ void GenLoadStage(const RowBlockParams& p, const Stag
     int64_t end = (s.k0 + s.c1 + 3) & ~static_cast<int64_t>(3);
     end = end < tailStart ? end : tailStart;
     const int64_t avail = s.valid ? end - a0 : 0;
-    const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
     const __amdgpu_buffer_rsrc_t rv = Rsrc(static_cast<const ValT*>(p.val) + a0, avail * sizeof(ValT));
-    b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
-    b.col[1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    if constexpr (kNc) {
+        // the narrow column copy (16-bit offsets from the block's first row),
+        // as the row kernel of fp32 values reads it
+        const __amdgpu_buffer_rsrc_t rn = Rsrc(p.ncol + a0, avail * 2);
+        const uint32_t rb = static_cast<uint32_t>(s.valid ? s.r0 : 0) + static_cast<uint32_t>(p.base);
+        const v2i lo = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, lane * 8, 0, kBufNonTemporal));
+        const v2i hi =
+            __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rn, 512 + lane * 8, 0, kBufNonTemporal));
+        b.col[0] = v4i{Lo16(lo.x, rb), Hi16(lo.x, rb), Lo16(lo.y, rb), Hi16(lo.y, rb)};
+        b.col[1] = v4i{Lo16(hi.x, rb), Hi16(hi.x, rb), Lo16(hi.y, rb), Hi16(hi.y, rb)};
+    } else {
+        const __amdgpu_buffer_rsrc_t rc = Rsrc(p.col + a0, avail * 4);
+        b.col[0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, lane * 16, 0, kBufNonTemporal));
+        b.col[1] =
+            __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rc, 1024 + lane * 16, 0, kBufNonTemporal));
+    }
     if constexpr (kPack) {
         (void)rv;  // positions: packed with the rows
     } else if constexpr (kGath) {
@@ -1682,7 +1695,7 @@ __device__ __forceinline__ void GenChunk(const RowBlockParams& p, const Stage& c
     WaveLdsSync();  // this chunk's LDS reads complete before the next chunk overwrites
 }
 
-template <typename RowT, ValKind V, OutKind O, AccKind A, bool kGath = false, bool kPack = false>
+template <typename RowT, ValKind V, OutKind O, AccKind A, bool kGath = false, bool kPack = false, bool kNc = false>
 __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBlockParams p)
 {
     using Acc = typename AccOf<A>::T;
@@ -1703,7 +1716,7 @@ __global__ __launch_bounds__(kWave* kFlatWaves) void SpmvStreamGenKernel(RowBloc
     int lg = 0;
     while (cur.valid) {
         GenLoad<V, A> b;
-        GenLoadStage<RowT, V, A, kGath, kPack>(p, cur, tailStart, lane, rx, b, reinterpret_cast<int32_t*>(sValAll[wv]));
+        GenLoadStage<RowT, V, A, kGath, kPack, kNc>(p, cur, tailStart, lane, rx, b, reinterpret_cast<int32_t*>(sValAll[wv]));
         GenChunk<RowT, V, O, A, kGath>(p, cur, b, sValAll[wv], lane, alpha, beta, betaNz, carry, lg);
         if (cur.last) break;
         cur.c0 = cur.c1;
@@ -2514,6 +2527,14 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
         if (gen) {
             const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
             const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
+            if constexpr (V == ValKind::C64) {
+                // the narrow column copy, once Preprocess's choice of it is on the host
+                if (l.narrow && p.ncol != nullptr && l.staged_choice == kNarrowFlag) {
+                    hipLaunchKernelGGL((SpmvStreamGenKernel<RowT, V, O, A, false, false, true>), dim3(g),
+                                       dim3(kWave * kFlatWaves), 0, stream_, p);
+                    return 0;
+                }
+            }
             hipLaunchKernelGGL((SpmvStreamGenKernel<RowT, V, O, A>), dim3(g), dim3(kWave * kFlatWaves), 0, stream_,
                                p);
             return 0;
@@ -2944,6 +2965,12 @@ __global__ void NarrowDecideKernel(uint32_t* flag, const uint32_t* bad, const ui
     if (*flag != 1U && *bad == 0U) *flag = static_cast<uint32_t>(*entryBad == 0U ? kEntryFlag : kNarrowFlag);
 }
 
+// *flag = v (one thread).
+__global__ void SetFlagKernel(uint32_t* flag, uint32_t v)
+{
+    if (threadIdx.x == 0) *flag = v;
+}
+
 template <typename RowT>
 void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
 {
@@ -2957,17 +2984,24 @@ void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
     q.base = l.base;
     q.flag = &h->staged_flag;
     q.bad = &h->narrow_bad;
-    const int64_t ne = l.layout.entry_blocks;
-    q.eblocks = At<const int32_t>(l.ws, l.layout.eb_offset);
+    // complex64 values run on the stream kernel of non-fp32 accumulators,
+    // which has no entry-aligned variant: the merge-path blocks only
+    const bool entry = l.val_kind != ValKind::C64;
+    const int64_t ne = entry ? l.layout.entry_blocks : 0;
+    q.eblocks = entry ? At<const int32_t>(l.ws, l.layout.eb_offset) : nullptr;
     q.eblock_nnz = At<const void>(l.ws, l.layout.en_offset);
     q.num_eblocks = ne;
     q.entry_bad = &h->entry_bad;
-    const unsigned eg = static_cast<unsigned>((ne + 1 + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL((EntryBlocksKernel<RowT>), dim3(eg), dim3(kThreads), 0, s,
-                       At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, ne, At<int32_t>(l.ws, l.layout.eb_offset),
-                       At<RowT>(l.ws, l.layout.en_offset));
-    hipLaunchKernelGGL((EntryCheckKernel<RowT>), dim3(eg), dim3(kThreads), 0, s, q.eblocks,
-                       static_cast<const RowT*>(q.eblock_nnz), ne, &h->entry_bad);
+    if (entry) {
+        const unsigned eg = static_cast<unsigned>((ne + 1 + kThreads - 1) / kThreads);
+        hipLaunchKernelGGL((EntryBlocksKernel<RowT>), dim3(eg), dim3(kThreads), 0, s,
+                           At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, ne,
+                           At<int32_t>(l.ws, l.layout.eb_offset), At<RowT>(l.ws, l.layout.en_offset));
+        hipLaunchKernelGGL((EntryCheckKernel<RowT>), dim3(eg), dim3(kThreads), 0, s, q.eblocks,
+                           static_cast<const RowT*>(q.eblock_nnz), ne, &h->entry_bad);
+    } else {
+        hipLaunchKernelGGL(SetFlagKernel, dim3(1), dim3(1), 0, s, &h->entry_bad, 1U);
+    }
     const int64_t waves = q.num_blocks > ne ? q.num_blocks : ne;
     const unsigned grid = static_cast<unsigned>((waves + kWaves - 1) / kWaves);
     hipLaunchKernelGGL((NarrowColKernel<RowT>), dim3(grid), dim3(kThreads), 0, s, q);

@@ -827,3 +827,26 @@ def test_banded_transpose_one_pass_other_types(kind, dev):
     else:
         z = oracle.spmv_c64(rp, col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 1, alpha, beta, val_is_real=True)
         np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+
+
+def test_complex_rows_on_narrow_columns(dev):
+    """complex64 y = alpha*A*x + beta*y after Preprocess on a matrix of 2.4 M entries: the narrow
+    column copy on the merge-path blocks (path flag 3; complex values have no entry-aligned variant),
+    bit-identical to the same SpMV on col_ind (without Preprocess) and within fp32 error of the oracle."""
+    m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 29)
+    alpha, beta = complex(0.5, -1.25), complex(1.5, 0.5)
+    outs = []
+    for pre in (True, False):
+        y = y0.to(dev).clone()
+        plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta)
+        if pre:
+            plan.preprocess()
+            torch.cuda.synchronize()
+            h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+            assert int(h[16] & 0xFFFFFFFF) == 3
+        plan.run()
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1])
+    z = oracle.spmv_c64(row_ptr.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 0, alpha, beta)
+    np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
