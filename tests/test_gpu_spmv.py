@@ -829,7 +829,8 @@ def test_banded_transpose_one_pass_other_types(kind, dev):
         np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
 
 
-def test_complex_rows_on_narrow_columns(dev):
+@pytest.mark.parametrize("rdtype", [torch.int32, torch.int64])
+def test_complex_rows_on_narrow_columns(rdtype, dev):
     """complex64 y = alpha*A*x + beta*y after Preprocess on a matrix of 2.4 M entries: the narrow
     column copy on the merge-path blocks (path flag 3; complex values have no entry-aligned variant),
     bit-identical to the same SpMV on col_ind (without Preprocess) and within fp32 error of the oracle."""
@@ -838,7 +839,7 @@ def test_complex_rows_on_narrow_columns(dev):
     outs = []
     for pre in (True, False):
         y = y0.to(dev).clone()
-        plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta)
+        plan = CsrSpMV(m, m, row_ptr.to(rdtype).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta)
         if pre:
             plan.preprocess()
             torch.cuda.synchronize()
