@@ -348,8 +348,10 @@ inline uint32_t StageValueBytes(aclDataType valueType, aclDataType computeType)
 // fp16 and bf16 values with fp32 compute, int8 values with int32 compute.
 inline bool NarrowTypes(aclDataType valueType, aclDataType computeType)
 {
-    if (computeType == ACL_FLOAT) return valueType == ACL_FLOAT || valueType == ACL_FLOAT16 || valueType == ACL_BF16;
-    if (computeType == ACL_COMPLEX64) return valueType == ACL_COMPLEX64;
+    if (computeType == ACL_FLOAT) {
+        return valueType == ACL_FLOAT || valueType == ACL_FLOAT16 || valueType == ACL_BF16 || valueType == ACL_INT8;
+    }
+    if (computeType == ACL_COMPLEX64) return valueType == ACL_COMPLEX64 || valueType == ACL_FLOAT;
     return computeType == ACL_INT32 && valueType == ACL_INT8;
 }
 

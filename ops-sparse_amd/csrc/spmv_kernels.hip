@@ -2527,7 +2527,7 @@ int LaunchRowBlock(const SpmvLaunch& l, hipStream_t stream)
         if (gen) {
             const int64_t wgs = (p.num_blocks + kFlatWaves - 1) / kFlatWaves;
             const unsigned g = static_cast<unsigned>((wgs + kXcds - 1) / kXcds * kXcds);
-            if constexpr (V == ValKind::C64) {
+            {
                 // the narrow column copy, once Preprocess's choice of it is on the host
                 if (l.narrow && p.ncol != nullptr && l.staged_choice == kNarrowFlag) {
                     hipLaunchKernelGGL((SpmvStreamGenKernel<RowT, V, O, A, false, false, true>), dim3(g),
@@ -2984,9 +2984,11 @@ void BuildNarrow(const SpmvLaunch& l, hipStream_t s)
     q.base = l.base;
     q.flag = &h->staged_flag;
     q.bad = &h->narrow_bad;
-    // complex64 values run on the stream kernel of non-fp32 accumulators,
-    // which has no entry-aligned variant: the merge-path blocks only
-    const bool entry = l.val_kind != ValKind::C64;
+    // complex64, int8 -> fp32 and real-to-complex values run on the stream
+    // kernel of non-fp32 accumulators, which has no entry-aligned variant:
+    // the merge-path blocks only
+    const bool entry = l.val_kind != ValKind::C64 && l.acc_kind != AccKind::C64 &&
+                       !(l.val_kind == ValKind::I8 && l.acc_kind == AccKind::F32);
     const int64_t ne = entry ? l.layout.entry_blocks : 0;
     q.eblocks = entry ? At<const int32_t>(l.ws, l.layout.eb_offset) : nullptr;
     q.eblock_nnz = At<const void>(l.ws, l.layout.en_offset);

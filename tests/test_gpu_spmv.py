@@ -829,13 +829,24 @@ def test_banded_transpose_one_pass_other_types(kind, dev):
         np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("rdtype", [torch.int32, torch.int64])
-def test_complex_rows_on_narrow_columns(rdtype, dev):
-    """complex64 y = alpha*A*x + beta*y after Preprocess on a matrix of 2.4 M entries: the narrow
-    column copy on the merge-path blocks (path flag 3; complex values have no entry-aligned variant),
-    bit-identical to the same SpMV on col_ind (without Preprocess) and within fp32 error of the oracle."""
+@pytest.mark.parametrize("kind,rdtype", [("c64", torch.int32), ("c64", torch.int64), ("int8_fp32", torch.int32),
+                                         ("real_c64", torch.int32)])
+def test_gen_rows_on_narrow_columns(kind, rdtype, dev):
+    """The stream kernel of non-fp32 accumulators (complex64; int8 values and x with fp32 y; fp32 values
+    and x with complex64 y) after Preprocess on a matrix of 2.4 M entries: the narrow column copy on the
+    merge-path blocks (path flag 3; these kinds have no entry-aligned variant), bit-identical to the same
+    SpMV on col_ind (without Preprocess) and within fp32 error of the oracle."""
     m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 29)
     alpha, beta = complex(0.5, -1.25), complex(1.5, 0.5)
+    g = torch.Generator().manual_seed(31)
+    if kind == "int8_fp32":
+        v = torch.randint(-128, 128, (col.numel(),), generator=g, dtype=torch.int8)
+        x = torch.randint(-128, 128, (m,), generator=g, dtype=torch.int8)
+        y0 = torch.rand(m, generator=g) * 2 - 1
+        alpha, beta = 1.5, 0.5
+    elif kind == "real_c64":
+        v = torch.rand(col.numel(), generator=g) * 2 - 1
+        x = torch.rand(m, generator=g) * 2 - 1
     outs = []
     for pre in (True, False):
         y = y0.to(dev).clone()
@@ -849,5 +860,14 @@ def test_complex_rows_on_narrow_columns(rdtype, dev):
         torch.cuda.synchronize()
         outs.append(y.cpu())
     assert torch.equal(outs[0], outs[1])
-    z = oracle.spmv_c64(row_ptr.numpy(), col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 0, alpha, beta)
-    np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+    rp = row_ptr.numpy()
+    if kind == "int8_fp32":
+        rows = np.repeat(np.arange(m), np.diff(rp))
+        seg = np.zeros(m)
+        np.add.at(seg, rows, v.numpy().astype(np.float64) * x.numpy().astype(np.float64)[col.numpy()])
+        want = alpha * seg + beta * y0.numpy().astype(np.float64)
+        np.testing.assert_allclose(outs[0].numpy(), want, rtol=1e-5, atol=1e-3)
+    else:
+        z = oracle.spmv_c64(rp, col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 0, alpha, beta,
+                            val_is_real=kind == "real_c64")
+        np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
