@@ -334,9 +334,12 @@ __global__ __launch_bounds__(kThreads) void SpmvRowBlockKernel(RowBlockParams p)
 constexpr int kWaveChunk = static_cast<int>(kChunkNnz);  // 512 slots, 8 per lane
 constexpr int kLaneItems = kWaveChunk / kWave;           // 8
 constexpr int kWaveRows = static_cast<int>(kMaxRowsPerBlock);
-// Waves per workgroup of the stream kernels (1 and 2 measured slower on the
-// power-law and fp16 matrices, equal on the Laplacian).
-constexpr int kFlatWaves = 4;
+// Waves per workgroup of the stream kernels: one.  On the Laplacian after
+// Preprocess (narrow columns, entry-aligned blocks, banded transposes) one
+// wave per workgroup measured 0.3-2.5 µs faster than four (and than two);
+// eight were slower.  Without Preprocess the power-law c3 takes 2.08 ms
+// against 2.04 ms with four.
+constexpr int kFlatWaves = 1;
 // Block workgroups of the stream kernel when the staged path may take the
 // matrix instead (multiple of the XCD count).
 constexpr int64_t kStagedFallbackWgs = 2048;
