@@ -871,3 +871,39 @@ def test_gen_rows_on_narrow_columns(kind, rdtype, dev):
         z = oracle.spmv_c64(rp, col.numpy(), v.numpy(), x.numpy(), y0.numpy(), m, 0, alpha, beta,
                             val_is_real=kind == "real_c64")
         np.testing.assert_allclose(outs[0].numpy(), z, rtol=1e-4, atol=1e-4)
+
+@pytest.mark.parametrize("kind", ["fp32", "c64"])
+def test_banded_transpose_values_updated_in_place(kind, dev):
+    """Preprocess keeps the pattern only: after values are overwritten in place (same pointer), the next
+    SpMV of the one-pass banded transpose (fp32 flag 4, complex64 flag 6) uses the new values."""
+    m, row_ptr, col, v, x, y0 = _complex_laplacian(1100, 41)
+    if kind == "fp32":
+        v, x, y0 = v.real.contiguous(), x.real.contiguous(), y0.real.contiguous()
+        alpha, beta, flag = 1.25, -0.5, 4
+    else:
+        alpha, beta, flag = complex(1.25, 0.5), complex(-0.5, 0.25), 6
+    dv = v.to(dev)
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), dv, x.to(dev), y, alpha, beta,
+                   op=Operation.TRANSPOSE)
+    plan.preprocess()
+    torch.cuda.synchronize()
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+    assert int(h[16] & 0xFFFFFFFF) == flag
+    plan.run()
+    g = torch.Generator().manual_seed(42)
+    if kind == "fp32":
+        v2 = torch.rand(v.shape, generator=g) * 4 - 2
+    else:
+        v2 = torch.complex(torch.rand(v.numel(), generator=g) * 4 - 2, torch.rand(v.numel(), generator=g) * 4 - 2)
+    dv.copy_(v2.to(dev))
+    y.copy_(y0.to(dev))
+    plan.run()
+    torch.cuda.synchronize()
+    rp = row_ptr.numpy()
+    if kind == "fp32":
+        z = oracle.spmv_c64(rp, col.numpy(), v2.numpy(), x.numpy(), y0.to(torch.complex64).numpy(), m, 1,
+                            alpha, beta, val_is_real=True).real
+    else:
+        z = oracle.spmv_c64(rp, col.numpy(), v2.numpy(), x.numpy(), y0.numpy(), m, 1, alpha, beta)
+    np.testing.assert_allclose(y.cpu().numpy(), z, rtol=1e-4, atol=1e-4)
