@@ -531,12 +531,19 @@ void PublishPathChoice(uint32_t*& host, void*& event, bool& valid, void* ws, voi
 int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* stream)
 {
     if (!valid || event == nullptr || host == nullptr) return -1;
-    if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
-    if (hipEventQuery(static_cast<hipEvent_t>(event)) != hipSuccess) {
-        (void)hipGetLastError();
-        return -1;
+    // The copy is one aligned 4-byte write over the sentinel that Publish
+    // stored before enqueuing it: a value other than the sentinel is the
+    // final one, readable without a runtime call (so also under stream
+    // capture, once an earlier call's copy has landed).
+    uint32_t v = *static_cast<volatile const uint32_t*>(host);
+    if (v == 0xFFFFFFFFU) {
+        if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
+        if (hipEventQuery(static_cast<hipEvent_t>(event)) != hipSuccess) {
+            (void)hipGetLastError();
+            return -1;
+        }
+        v = *static_cast<volatile const uint32_t*>(host);
     }
-    const uint32_t v = *static_cast<volatile const uint32_t*>(host);
     return v <= static_cast<uint32_t>(kMaxPathFlag) ? static_cast<int32_t>(v) : -1;
 }
 

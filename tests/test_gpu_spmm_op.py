@@ -397,6 +397,7 @@ def test_hip_graph_capture_and_replay(k, n, dev):
     d_val = torch.from_numpy(val.astype(np.float32)).to(dev)
     s = torch.cuda.Stream()
     c = c0.clone()
+    torch.cuda.synchronize()  # the inputs were written on the default stream
     with torch.cuda.stream(s):
         plan = SpMMOp(m, k, d_rp, d_col, d_val, b, c)
         plan.run(b, c, 1.25, 0.5)

@@ -598,11 +598,13 @@ def test_hip_graph_capture_and_replay(name, trans, dev):
     d = w.to(dev)
     s = torch.cuda.Stream()
     y = d.y0.clone()
+    torch.cuda.synchronize()  # the inputs were written on the default stream
     with torch.cuda.stream(s):
         plan = CsrSpMV(w.rows, w.cols, d.row_ptr, d.col_ind, d.values, d.x, y, w.alpha, w.beta, op=OP[trans])
         plan.preprocess()
     torch.cuda.synchronize()
     y.copy_(d.y0)
+    torch.cuda.synchronize()
     with torch.cuda.stream(s):
         plan.run()
     torch.cuda.synchronize()
@@ -907,3 +909,48 @@ def test_banded_transpose_values_updated_in_place(kind, dev):
     else:
         z = oracle.spmv_c64(rp, col.numpy(), v2.numpy(), x.numpy(), y0.numpy(), m, 1, alpha, beta)
     np.testing.assert_allclose(y.cpu().numpy(), z, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("op", ["N", "H"])
+def test_complex_graph_capture_on_chosen_paths(op, dev):
+    """complex64 SpMV captured in a HIP graph once Preprocess's choice is on the host: N on the narrow
+    column copy (flag 3), H on the banded one-pass kernel (flag 6); every replay, with eager work between,
+    matches the eager result bit for bit."""
+    m, row_ptr, col, v, x, y0 = _complex_laplacian(700, 53)
+    alpha, beta = complex(1.25, -0.5), complex(0.5, 0.75)
+    o = Operation.NON_TRANSPOSE if op == "N" else Operation.CONJUGATE_TRANSPOSE
+    s = torch.cuda.Stream()
+    dy0 = y0.to(dev)
+    y = dy0.clone()
+    torch.cuda.synchronize()  # the inputs were written on the default stream
+    with torch.cuda.stream(s):
+        plan = CsrSpMV(m, m, row_ptr.to(torch.int32).to(dev), col.to(dev), v.to(dev), x.to(dev), y, alpha, beta,
+                       op=o)
+        plan.preprocess()
+    torch.cuda.synchronize()
+    h = np.frombuffer(plan.workspace[:192].cpu().numpy().tobytes(), dtype=np.uint64)
+    assert int(h[16] & 0xFFFFFFFF) == (3 if op == "N" else 6)
+    with torch.cuda.stream(s):
+        plan.run()
+    torch.cuda.synchronize()
+    y.copy_(dy0)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        plan.run()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    y.copy_(dy0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        plan.run()
+    for _ in range(3):
+        y.copy_(dy0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        with torch.cuda.stream(s):
+            plan.run()
+        torch.cuda.synchronize()

@@ -212,6 +212,7 @@ def _graph_matches_eager(w, dev, op=None):
     op = Operation.NON_TRANSPOSE if op is None else op
     s = torch.cuda.Stream()
     y = w.y0.to(w.out_dtype).clone()
+    torch.cuda.synchronize()  # the inputs were written on the default stream
     with torch.cuda.stream(s):
         plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op,
                        base=w.meta.get("base", 0))
@@ -233,6 +234,7 @@ def _graph_matches_eager(w, dev, op=None):
         torch.cuda.synchronize()
         assert torch.equal(bits(y), bits(eager))
         y.copy_(w.y0.to(w.out_dtype))
+        torch.cuda.synchronize()
         with torch.cuda.stream(s):  # eager work between replays
             plan.run()
         torch.cuda.synchronize()
