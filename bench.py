@@ -456,7 +456,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
-              "the SpMV path is single-device, see DESIGN.md for how it would shard", file=sys.stderr)
+              "the SpMV path runs on one device (rows would shard by nnz-balanced ranges with x all-gathered)", file=sys.stderr)
         sys.exit(2)
     from ops_sparse.workloads import algorithmic_bytes, flops
 
