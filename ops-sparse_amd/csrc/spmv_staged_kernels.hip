@@ -224,11 +224,12 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
     }
 }
 
-// Per tile: stable radix sort of (column, position) so that the tile's
-// entries are in bucket order; perm[k] = slot of entry k in the tile's
-// padded bucket-ordered runs, cl[start(t,s) + rank] = column within the
-// bucket (0 in the runs' padding); adds the tile's count of distinct x lines
-// to the metric.
+// Per tile: stable radix sort of (x line, position), the line being the
+// column's 128-byte line of x, so that the tile's entries are in bucket order
+// (and by line within a bucket, in entry order within a line); perm[k] = slot
+// of entry k in the tile's padded bucket-ordered runs, cl[start(t,s) + rank]
+// = column within the bucket (0 in the runs' padding); adds the tile's count
+// of distinct x lines to the metric.
 template <int kItems, int kEndBit>
 __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
 {
@@ -262,8 +263,10 @@ __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
     constexpr uint32_t kPad = kEndBit >= 32 ? 0xFFFFFFFFU : ((1U << kEndBit) - 1U);
     for (int u = 0; u < kSortIpt; ++u) {
         const int i = threadIdx.x * kSortIpt + u;
-        keys[u] = i < n ? KeyOf(q, q.col[e0 + i]) : kPad;
-        vals[u] = static_cast<uint32_t>(i);
+        const uint32_t key = i < n ? KeyOf(q, q.col[e0 + i]) : 0U;
+        keys[u] = i < n ? key >> q.line_shift : kPad;
+        // the column within its bucket rides in the high half (the key holds only its line)
+        vals[u] = static_cast<uint32_t>(i) | ((key & ((1U << q.wshift) - 1U)) << 16);
     }
     if (threadIdx.x == 0) {
         lineCount = 0U;
@@ -276,31 +279,30 @@ __global__ __launch_bounds__(kSortThreads) void StageSortKernel(StageParams q)
     uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
     uint32_t lines = 0U;
     const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
+    const int bshift = q.wshift - q.line_shift;  // line -> bucket
     for (int u = 0; u < kSortIpt; ++u) {
         const int i = threadIdx.x * kSortIpt + u;
         if (i < n) {
             const uint32_t key = keys[u];
-            const uint32_t b = key >> q.wshift;
-            if (prev == 0xFFFFFFFFU || (prev >> q.wshift) != b) firstSlot[b] = static_cast<uint32_t>(i);
-            if (b != nullBucket && (prev == 0xFFFFFFFFU || (prev >> q.line_shift) != (key >> q.line_shift))) ++lines;
+            const uint32_t b = key >> bshift;
+            if (prev == 0xFFFFFFFFU || (prev >> bshift) != b) firstSlot[b] = static_cast<uint32_t>(i);
+            if (b != nullBucket && prev != key) ++lines;
         }
         prev = keys[u];
     }
     if (lines != 0U) atomicAdd(&lineCount, lines);
     __syncthreads();
-    const uint32_t mask = (1U << q.wshift) - 1U;
     for (int u = 0; u < kSortIpt; ++u) {
         const int i = threadIdx.x * kSortIpt + u;
         if (i < n) {
-            const uint32_t key = keys[u];
-            const uint32_t b = key >> q.wshift;
+            const uint32_t b = keys[u] >> bshift;
             const uint32_t rank = static_cast<uint32_t>(i) - firstSlot[b];
-            q.perm[e0 + vals[u]] = static_cast<uint16_t>(padOff[b] + rank);
+            q.perm[e0 + (vals[u] & 0xFFFFU)] = static_cast<uint16_t>(padOff[b] + rank);
             const uint32_t start = q.start[t * nb + b];
-            q.cl[start + rank] = static_cast<uint16_t>(b == nullBucket ? 0U : (key & mask));
+            q.cl[start + rank] = static_cast<uint16_t>(b == nullBucket ? 0U : (vals[u] >> 16));
             // the run's last entry clears the run's padding
             const uint32_t next = u + 1 < kSortIpt ? keys[u + 1] : firstKey[threadIdx.x + 1];
-            if (i + 1 == n || (next >> q.wshift) != b) {
+            if (i + 1 == n || (next >> bshift) != b) {
                 const uint32_t runSlots = q.counts[b * (q.tiles + 1) + t];
                 for (uint32_t j = rank + 1U; j < runSlots; ++j) q.cl[start + j] = 0U;
             }
@@ -1359,11 +1361,12 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL(StageTransposeKernel,
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
-    // sort keys: columns below (S+1) << wshift, plus an all-ones pad key
-    const uint64_t maxKey = (static_cast<uint64_t>(L.st_buckets) + 1) << L.st_wshift;
+    // sort keys: x lines of columns below (S+1) << wshift, plus an all-ones pad key
+    const uint64_t maxKey = ((static_cast<uint64_t>(L.st_buckets) + 1) << L.st_wshift) >> q.line_shift;
     int bits = 1;
     while ((uint64_t{1} << bits) <= maxKey) ++bits;
-    if (bits <= 20) LaunchSort<20>(q, s);
+    if (bits <= 16) LaunchSort<16>(q, s);
+    else if (bits <= 20) LaunchSort<20>(q, s);
     else if (bits <= 24) LaunchSort<24>(q, s);
     else if (bits <= 28) LaunchSort<28>(q, s);
     else LaunchSort<32>(q, s);
