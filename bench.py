@@ -154,7 +154,7 @@ def _timed(stream, fn, reps):
     return a.elapsed_time(b) / reps
 
 
-def measure(w, steps, warmup, flush_buf):
+def measure(w, steps, warmup, flush_buf, alg=None):
     """SpMV time per step (ms) with L2/MALL flushed before every SpMV.
 
     A step is a read of a 512 MiB buffer (evicting the L2 and the 256 MB
@@ -171,16 +171,26 @@ def measure(w, steps, warmup, flush_buf):
     from ops_sparse.spmv import CsrSpMV
     from ops_sparse._lib import Operation
 
+    from ops_sparse._lib import SpMVAlg
+
     op = {"N": Operation.NON_TRANSPOSE, "T": Operation.TRANSPOSE, "H": Operation.CONJUGATE_TRANSPOSE}[w.trans]
     y = w.y0.to(w.out_dtype).clone()
-    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op)
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta, op=op,
+                   alg=SpMVAlg.DEFAULT if alg is None else alg)
     stream = torch.cuda.current_stream()
-    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    p0.record(stream)
+    # Preprocess: the median of three calls after a first one (the first
+    # Preprocess of a process also pays for loading code objects)
     plan.preprocess()
-    p1.record(stream)
     torch.cuda.synchronize()
-    pre_ms = p0.elapsed_time(p1)
+    pre = []
+    for _ in range(3):
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        plan.preprocess()
+        p1.record(stream)
+        torch.cuda.synchronize()
+        pre.append(p0.elapsed_time(p1))
+    pre_ms = statistics.median(pre)
     # the path Preprocess chose: the path flag in the workspace header
     path = "row kernels" if w.trans == "N" else "transpose"
     if w.trans == "N" and plan.workspace is not None and plan.workspace.numel() >= 192:
@@ -421,10 +431,23 @@ def cpu_baseline(w, seconds):
             "ms_per_spmv": per * 1e3, "gflops": 2 * w.nnz / per / 1e9,
             "sample": f"{n} full SpMVs of the headline matrix {w.name} ({w.rows} rows, {w.nnz} nnz) in {el:.1f} s, "
                       f"oracle/spmv_oracle.c {fn_name}, 1 thread",
-            "cpu": platform.processor() or platform.machine(), "host_nproc": os.cpu_count()}
+            "cpu": cpu_model(), "host_nproc": os.cpu_count()}
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else the machine type."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 NARROW_PATH = "row kernels, narrow columns"
+ALG1_CONFIGS = ("c3", "c4h", "c5")  # also measured on CSR_ALG1's reference-sized workspace
 LINE_RATE = 64e9  # 128-byte lines per second from the MALL (random x gathers), measured on MI355X
 
 
@@ -472,6 +495,11 @@ def main():
     # c2 first when measured: the first SpMV of the process also pays for
     # loading the code objects (and c2's variants reuse its matrix)
     names = [n for n in names if n == "c2"] + [n for n in names if n != "c2"]
+    # load the code objects before anything is timed: one small SpMV
+    from ops_sparse import workloads as wl_warm
+    warm_w = wl_warm.laplacian_2d(n=256, device=dev)
+    measure(warm_w, 2, 1, flush_buf)
+    del warm_w
     results, headline_w, headline = {}, None, None
     for name in names:
         w = make(name, dev)
@@ -483,6 +511,7 @@ def main():
                  algorithmic_bytes=nbytes, gbs=gbs, frac=gbs / HBM_PEAK_GBS,
                  gflops=flops(w) / (m["median_ms"] * 1e-3) / 1e9,
                  warm_gbs=nbytes / (m["warm_ms"] * 1e-3) / 1e9, **m)
+        r["workspace_per_algorithmic_byte"] = m["workspace_bytes"] / nbytes
         r["ceilings_ms"] = ceilings(w, nbytes, m["path"])
         bound_key = {"staged gather": "staged_traffic_hbm", NARROW_PATH: "narrow_traffic_hbm"}.get(
             m["path"], "algorithmic_hbm")
@@ -494,6 +523,18 @@ def main():
             r["graph_gbs"] = nbytes / (r["graph_ms"] * 1e-3) / 1e9
         print(f"# {name}: {json.dumps(r)}", file=sys.stderr, flush=True)
         results[name] = r
+        if name in ALG1_CONFIGS and not args.only_headline:
+            # the same matrix on CSR_ALG1's reference-sized workspace (row
+            # kernels; atomic scatter for opA = T)
+            from ops_sparse._lib import SpMVAlg
+            ma = measure(w, args.steps, args.warmup, flush_buf, alg=SpMVAlg.CSR_ALG1)
+            ra = dict(workload=w.name + " (CSR_ALG1)", rows=w.rows, nnz=w.nnz, op=w.trans, algorithmic_bytes=nbytes,
+                      median_ms=ma["median_ms"], gbs=nbytes / (ma["median_ms"] * 1e-3) / 1e9,
+                      frac=nbytes / (ma["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, preprocess_ms=ma["preprocess_ms"],
+                      workspace_bytes=ma["workspace_bytes"],
+                      workspace_per_algorithmic_byte=ma["workspace_bytes"] / nbytes)
+            print(f"# {name}_alg1: {json.dumps(ra)}", file=sys.stderr, flush=True)
+            results[name + "_alg1"] = ra
         if name == HEADLINE:
             headline_w, headline = w, r
             cpu = None if args.no_cpu_baseline else cpu_baseline(headline_w, args.cpu_seconds)
@@ -507,7 +548,8 @@ def main():
                                         gbs=vb / (mv["median_ms"] * 1e-3) / 1e9,
                                         frac=vb / (mv["median_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                         median_ms=mv["median_ms"], p90_ms=mv["p90_ms"], warm_ms=mv["warm_ms"],
-                                        preprocess_ms=mv["preprocess_ms"])
+                                        preprocess_ms=mv["preprocess_ms"], workspace_bytes=mv["workspace_bytes"],
+                                        workspace_per_algorithmic_byte=mv["workspace_bytes"] / vb)
                     del v
             from ops_sparse._lib import SpMVOpAlg
             for alg in (SpMVOpAlg.ALG1, SpMVOpAlg.ALG2):

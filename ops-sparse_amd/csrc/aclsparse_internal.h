@@ -25,6 +25,10 @@ constexpr uint32_t kSpMMOpPlanSignature = 0x534D4D50U;   // "SMMP"
 constexpr int kVersion = 10000;  // 1.0.0, encoded MAJOR*10000+MINOR*100+PATCH
 constexpr size_t kDefaultWorkspaceBytes = 4U * 1024U * 1024U;
 
+// A pinned 4-byte host copy of a path flag and the event recorded after the
+// copy; slots live in a process-wide pool (spmv_host.cpp) and are never freed.
+struct ChoiceSlot;
+
 }  // namespace aclsp
 
 // The public typedefs name these structs in the global namespace.
@@ -78,13 +82,12 @@ struct aclsparseSpMatDescr {
     int64_t ptr_stride = 1, idx_stride = 1, value_stride = 1;  // in elements
     SpmvPlan plan;  // plan.buffer == nullptr means "no active SpMV plan"
     // The path the last staged Preprocess chose, copied from the workspace
-    // header into pinned host memory, and an event recorded after the copy
-    // (hipEvent_t): once the event has completed, SpMV launches only the
-    // chosen kernels; before that, both sets, which read the device flag.
-    // Created by the first staged Preprocess, released with the descriptor.
-    uint32_t* staged_choice_host = nullptr;
-    void* staged_choice_event = nullptr;
-    bool staged_choice_valid = false;  // the copy above belongs to the last Preprocess
+    // header into a pooled pinned host slot with an event recorded after the
+    // copy: once the copy has landed, SpMV launches only the chosen kernels
+    // (outside stream capture); before that, every kernel set, each reading
+    // the device flag.  Taken from the pool by Preprocess, handed back (never
+    // waited for) by the next Preprocess and by aclsparseDestroySpMat.
+    aclsp::ChoiceSlot* staged_choice = nullptr;
 };
 
 struct aclsparseDnVecDescr {
@@ -198,6 +201,10 @@ inline int64_t NumBlocks(uint64_t rows, uint64_t nnz)
 }
 
 struct SpmvLayout {
+    // CSR_ALG1: the reference-sized workspace (normalised row offsets, the
+    // row-block partition, the long-block tasks; for a transpose a cols-long
+    // accumulator for the atomic scatter): no staged, narrow or CSC tables
+    bool lean = false;
     size_t rowptr_offset = 0;
     size_t blocks_offset = 0;
     size_t block_nnz_offset = 0;
@@ -459,9 +466,16 @@ inline size_t AccumulatorBytes(aclDataType computeType)
 
 inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, aclsparseIndexType_t ptrType,
                                 aclDataType computeType, bool transpose, bool allowTasks = true,
-                                uint32_t stageValueBytes = 0, bool narrowTypes = false, bool cbandTypes = false)
+                                uint32_t stageValueBytes = 0, bool narrowTypes = false, bool cbandTypes = false,
+                                bool lean = false)
 {
     SpmvLayout l;
+    l.lean = lean;
+    if (lean) {
+        stageValueBytes = 0;
+        narrowTypes = false;
+        cbandTypes = false;
+    }
     l.rowptr_bytes = ptrType == ACL_SPARSE_INDEX_64I ? 8U : 4U;
     l.items_per_block = ItemsPerBlock(rows, nnz);
     l.num_blocks = NumBlocks(rows, nnz);
@@ -489,7 +503,9 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
             l.total = AlignUp(l.task_scan_offset + l.task_scan_bytes + 256);  // re-aligned to 256 bytes at use
         }
     }
-    if (transpose) {
+    if (transpose && lean) {
+        l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));
+    } else if (transpose) {
         l.csc = nnz > 0 && nnz <= 0x7FFFFFFFULL;
         if (!l.csc) {
             l.total = AlignUp(l.acc_offset + static_cast<size_t>(cols) * AccumulatorBytes(computeType));
@@ -602,11 +618,13 @@ inline SpmvLayout ComputeLayout(uint64_t rows, uint64_t cols, uint64_t nnz, acls
 }
 
 // Path choices made on the device by a Preprocess (spmv_host.cpp): publish
-// the header's path flag to the host behind an event, read it once the copy
-// has completed (-1 before, or under stream capture), release the copy.
-void PublishPathChoice(uint32_t*& host, void*& event, bool& valid, void* ws, void* stream);
-int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* stream);
-void ReleasePathChoice(uint32_t*& host, void*& event);
+// the header's path flag to the host through a pooled pinned slot (the
+// previous slot goes back to the pool), read it once the copy has completed
+// (-1 before, and always under stream capture), hand the slot back.  None of
+// them waits for the device.
+void PublishPathChoice(ChoiceSlot*& slot, void* ws, void* stream);
+int32_t QueryPathChoice(const ChoiceSlot* slot, void* stream);
+void ReleasePathChoice(ChoiceSlot*& slot);
 
 // SpMV into a workspace that scratch() returns (resolved only after the
 // inputs are validated and the layout fits scratchBytes): the tables are
@@ -708,9 +726,7 @@ struct aclsparseSpMVOpDescr {
     // ALG2: createDescr built the narrow column copy in the buffer; the path it
     // chose on the device, copied to pinned host memory behind an event
     bool narrow = false;
-    uint32_t* choice_host = nullptr;
-    void* choice_event = nullptr;
-    bool choice_valid = false;
+    aclsp::ChoiceSlot* choice = nullptr;
 };
 
 struct aclsparseSpMVOpPlan {

@@ -357,11 +357,7 @@ aclsparseStatus_t aclsparseDestroySpMat(aclsparseConstSpMatDescr_t spMatDescr)
     if (spMatDescr == nullptr) return ACL_SPARSE_STATUS_SUCCESS;
     if (!IsMat(spMatDescr)) return ACL_SPARSE_STATUS_INVALID_VALUE;
     auto* d = const_cast<aclsparseSpMatDescr*>(spMatDescr);
-    if (d->staged_choice_event != nullptr) {
-        (void)hipEventSynchronize(static_cast<hipEvent_t>(d->staged_choice_event));
-        (void)hipEventDestroy(static_cast<hipEvent_t>(d->staged_choice_event));
-    }
-    if (d->staged_choice_host != nullptr) (void)hipHostFree(d->staged_choice_host);
+    aclsp::ReleasePathChoice(d->staged_choice);  // back to the pool, without waiting for its copy
     d->signature = 0;
     delete d;
     return ACL_SPARSE_STATUS_SUCCESS;

@@ -12,6 +12,8 @@
 
 #include <cstring>
 #include <limits>
+#include <mutex>
+#include <vector>
 
 #include "aclsparse_internal.h"
 
@@ -177,11 +179,18 @@ aclsparseStatus_t ValidateWorkspace(void* buffer)
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
-SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c)
+// CSR_ALG1 takes the reference-sized workspace (sparse/spmv/arch35/
+// spmv_tiling_data.h:104-141: the normalised row offsets, plus a cols-long
+// accumulator for a transpose) and the kernels that need nothing more: the row
+// kernels for opA = N, the atomic scatter for T and H.  DEFAULT and CSR_ALG2
+// take the larger workspace of the staged, narrow-column and CSC tables.
+bool LeanAlg(aclsparseSpMVAlg_t alg) { return alg == ACL_SPARSE_SPMV_CSR_ALG1; }
+
+SpmvLayout LayoutFor(const aclsparseSpMatDescr* m, aclsparseOperation_t op, aclDataType c, aclsparseSpMVAlg_t alg)
 {
     return aclsp::ComputeLayout(m->rows, m->cols, m->nnz, m->ptr_type, c, IsTranspose(op), true,
                                 aclsp::StageValueBytes(m->value_type, c), aclsp::NarrowTypes(m->value_type, c),
-                                aclsp::CbandTypes(m->value_type, c));
+                                aclsp::CbandTypes(m->value_type, c), LeanAlg(alg));
 }
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15U) == 0U; }
@@ -222,21 +231,19 @@ bool CbandUsable(const SpmvLayout& l, const aclsparseSpMatDescr* m, const aclspa
            x->stride == 1 && y->stride == 1 && m->rows * 8U <= 0x7FFFFFFFULL && m->nnz * 8U <= 0x7FFFFFFFULL;
 }
 
-// After a staged or narrow Preprocess: copy the path flag it leaves in the workspace
-// header to pinned host memory and record an event after the copy.  The
-// host value starts as a sentinel, so a copy that has not run reads as
-// "unknown"; a previous copy is waited for first (it may be on another
-// stream).  Any failure leaves the choice unknown (SpMV then launches both
-// kernel sets, which read the device flag).
+// After a staged or narrow Preprocess: publish the path flag it leaves in the
+// workspace header to the host (a pooled pinned slot, no wait); any failure
+// leaves the choice unknown (SpMV then launches every kernel set, each reading
+// the device flag).
 void PublishStagedChoice(aclsparseSpMatDescr* m, void* ws, void* stream)
 {
-    aclsp::PublishPathChoice(m->staged_choice_host, m->staged_choice_event, m->staged_choice_valid, ws, stream);
+    aclsp::PublishPathChoice(m->staged_choice, ws, stream);
 }
 
 // The path of the matching staged Preprocess if its copy has completed, else -1.
 int32_t StagedChoice(const aclsparseSpMatDescr* m, void* stream)
 {
-    return aclsp::QueryPathChoice(m->staged_choice_host, m->staged_choice_event, m->staged_choice_valid, stream);
+    return aclsp::QueryPathChoice(m->staged_choice, stream);
 }
 
 SpmvPlan MakePlan(const aclsparseSpMatDescr* m, const aclsparseDnVecDescr* x, const aclsparseDnVecDescr* y,
@@ -343,7 +350,7 @@ aclsp::SpmvLaunch MakeLaunch(const aclsparseContext* h, aclsparseOperation_t op,
         std::memcpy(&l.beta_re, beta, sizeof(float));
     }
     l.ws = ws;
-    l.layout = LayoutFor(m, op, c);
+    l.layout = LayoutFor(m, op, c, alg);
     return l;
 }
 
@@ -360,7 +367,7 @@ aclsparseStatus_t aclsparseSpMVGetBufferSize(aclsparseHandle_t handle, aclsparse
     *bufferSize = 0U;
     aclsparseStatus_t st = ValidateInputs(handle, opA, alpha, matA, vecX, beta, vecY, computeType, alg);
     if (st != ACL_SPARSE_STATUS_SUCCESS) return st;
-    *bufferSize = LayoutFor(matA, opA, computeType).total;
+    *bufferSize = LayoutFor(matA, opA, computeType, alg).total;
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
@@ -391,6 +398,7 @@ aclsparseStatus_t aclsparseSpMVPreprocess(aclsparseHandle_t handle, aclsparseOpe
             return ACL_SPARSE_STATUS_EXECUTION_FAILED;
         }
         if (staged || narrow || cband) PublishStagedChoice(m, externalBuffer, HipStreamOf(handle));
+        else aclsp::ReleasePathChoice(m->staged_choice);
     }
     m->plan = MakePlan(m, vecX, vecY, opA, computeType, alg, externalBuffer, handle);
     m->plan.staged = staged;
@@ -469,7 +477,64 @@ aclsparseStatus_t SpmvWithScratch(aclsparseHandle_t handle, aclsparseOperation_t
     return ACL_SPARSE_STATUS_SUCCESS;
 }
 
+// Pool of path-choice slots.  Preprocess takes a slot, copies the header's
+// flag into it asynchronously and records the slot's event after the copy.
+// A slot handed back (by the next Preprocess of the same descriptor or by its
+// destruction) may still have that copy in flight, so it is reused only once
+// its event reports completion (hipEventQuery, never a wait).  Slots are
+// allocated in batches of pinned memory and kept for the life of the process,
+// so a late copy always lands in memory the pool owns.
+struct ChoiceSlot {
+    uint32_t* host;
+    hipEvent_t event;
+    bool recorded;  // an event record (and the copy before it) was enqueued
+};
+
 namespace {
+
+constexpr uint32_t kChoiceUnknown = 0xFFFFFFFFU;
+constexpr int kSlotBatch = 64;
+
+std::mutex gSlotMutex;
+std::vector<ChoiceSlot*> gFreeSlots;
+std::vector<ChoiceSlot*> gPendingSlots;  // handed back, copy possibly in flight
+
+// A slot ready for a new copy, or nullptr.  Called with gSlotMutex held.
+ChoiceSlot* TakeSlotLocked()
+{
+    for (size_t i = 0; i < gPendingSlots.size();) {
+        ChoiceSlot* c = gPendingSlots[i];
+        const hipError_t e = c->recorded ? hipEventQuery(c->event) : hipSuccess;
+        if (e == hipSuccess) {
+            gFreeSlots.push_back(c);
+            gPendingSlots[i] = gPendingSlots.back();
+            gPendingSlots.pop_back();
+        } else {
+            if (e != hipErrorNotReady) (void)hipGetLastError();
+            ++i;
+        }
+    }
+    if (gFreeSlots.empty()) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, kSlotBatch * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        auto* words = static_cast<uint32_t*>(p);
+        for (int k = 0; k < kSlotBatch; ++k) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+                (void)hipGetLastError();
+                break;  // the remaining words stay unused
+            }
+            gFreeSlots.push_back(new ChoiceSlot{words + k, e, false});
+        }
+        if (gFreeSlots.empty()) return nullptr;
+    }
+    ChoiceSlot* c = gFreeSlots.back();
+    gFreeSlots.pop_back();
+    return c;
+}
 
 bool Capturing(hipStream_t s)
 {
@@ -483,79 +548,72 @@ bool Capturing(hipStream_t s)
 
 }  // namespace
 
-// After a Preprocess that may choose a path on the device: copy the path flag
-// it leaves in the workspace header to pinned host memory and record an event
-// after the copy.  The host value starts as a sentinel, so a copy that has not
-// run reads as "unknown"; a previous copy is waited for first (it may be on
-// another stream).  Under stream capture no event, copy, wait or allocation is
-// made: the choice stays unknown and every launch reads the device flag.  Any
-// failure also leaves the choice unknown.
-void PublishPathChoice(uint32_t*& host, void*& event, bool& valid, void* ws, void* stream)
+// Hand a slot back to the pool (its copy may still be in flight).
+void ReleasePathChoice(ChoiceSlot*& slot)
 {
+    if (slot == nullptr) return;
+    std::lock_guard<std::mutex> lock(gSlotMutex);
+    gPendingSlots.push_back(slot);
+    slot = nullptr;
+}
+
+// After a Preprocess that may choose a path on the device: hand back the
+// previous slot, take a fresh one, set it to the "unknown" sentinel, copy the
+// header's flag into it and record its event after the copy.  Nothing waits
+// for the device.  Under stream capture no copy is made and the choice stays
+// unknown (the captured SpMVs read the device flag).
+void PublishPathChoice(ChoiceSlot*& slot, void* ws, void* stream)
+{
+    ReleasePathChoice(slot);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    valid = false;
     if (Capturing(s)) return;
-    if (event != nullptr) {
-        (void)hipEventSynchronize(static_cast<hipEvent_t>(event));
-    } else {
-        hipEvent_t e = nullptr;
-        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
-        event = e;
+    ChoiceSlot* c = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(gSlotMutex);
+        c = TakeSlotLocked();
     }
-    if (host == nullptr) {
-        void* p = nullptr;
-        if (hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
-        host = static_cast<uint32_t*>(p);
-    }
-    *host = 0xFFFFFFFFU;
+    if (c == nullptr) return;
+    *static_cast<volatile uint32_t*>(c->host) = kChoiceUnknown;
+    c->recorded = false;
     const auto* header = static_cast<const SpmvWsHeader*>(ws);
-    if (hipMemcpyAsync(host, &header->staged_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipEventRecord(static_cast<hipEvent_t>(event), s) != hipSuccess) {
+    if (hipMemcpyAsync(c->host, &header->staged_flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess) {
         (void)hipGetLastError();
-        *host = 0xFFFFFFFFU;
+        ReleasePathChoice(c);  // nothing was enqueued: free at once
         return;
     }
-    valid = true;
+    c->recorded = true;  // a copy is enqueued: the slot is reused only after its event
+    if (hipEventRecord(c->event, s) != hipSuccess) {
+        (void)hipGetLastError();
+        // without the event the copy's completion cannot be observed: the
+        // slot is retired for good (its word may still be written)
+        return;
+    }
+    slot = c;
 }
 
 // The published path (0 the row / CSC kernels, 1 the staged or column-bucketed
 // kernels, 2 the banded transpose kernel, 3 the narrow-column row kernel, 4
 // the banded transpose kernel on 16-bit copies, 5 the narrow-column row kernel
-// on entry-aligned blocks) if its copy has completed, else -1.
-int32_t QueryPathChoice(const uint32_t* host, void* event, bool valid, void* stream)
+// on entry-aligned blocks, 6 the packed banded transpose) if its copy has
+// completed, else -1.  Always -1 under stream capture: a captured graph then
+// holds every kernel set, each gated on the device flag, so that it stays
+// correct when a later Preprocess into the same workspace chooses another path.
+int32_t QueryPathChoice(const ChoiceSlot* slot, void* stream)
 {
-    if (!valid || event == nullptr || host == nullptr) return -1;
-    // The copy is one aligned 4-byte write over the sentinel that Publish
-    // stored before enqueuing it: a value other than the sentinel is the
-    // final one, readable without a runtime call (so also under stream
-    // capture, once an earlier call's copy has landed).
-    uint32_t v = *static_cast<volatile const uint32_t*>(host);
-    if (v == 0xFFFFFFFFU) {
-        if (Capturing(static_cast<hipStream_t>(stream))) return -1;  // no event query under capture
-        if (hipEventQuery(static_cast<hipEvent_t>(event)) != hipSuccess) {
+    if (slot == nullptr) return -1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (Capturing(s)) return -1;
+    // The copy is one aligned 4-byte write over the sentinel stored before it
+    // was enqueued: a value other than the sentinel is the final one.
+    uint32_t v = *static_cast<volatile const uint32_t*>(slot->host);
+    if (v == kChoiceUnknown) {
+        if (hipEventQuery(slot->event) != hipSuccess) {
             (void)hipGetLastError();
             return -1;
         }
-        v = *static_cast<volatile const uint32_t*>(host);
+        v = *static_cast<volatile const uint32_t*>(slot->host);
     }
     return v <= static_cast<uint32_t>(kMaxPathFlag) ? static_cast<int32_t>(v) : -1;
-}
-
-void ReleasePathChoice(uint32_t*& host, void*& event)
-{
-    if (event != nullptr) {
-        (void)hipEventSynchronize(static_cast<hipEvent_t>(event));
-        (void)hipEventDestroy(static_cast<hipEvent_t>(event));
-        event = nullptr;
-    }
-    if (host != nullptr) (void)hipHostFree(host);
-    host = nullptr;
 }
 
 }  // namespace aclsp

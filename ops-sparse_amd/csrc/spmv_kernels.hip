@@ -2592,6 +2592,134 @@ void LaunchBandedTranspose(const SpmvLaunch& l, const RowBlockParams& p, hipStre
     }
 }
 
+// ------------------- transpose by atomic scatter (CSR_ALG1) ------------------
+//
+// The reference's non-deterministic transpose (sparse/spmv/arch35/
+// spmv_kernel.cpp:579-668): acc is cleared, every entry adds
+// conj?(a_k) * x[row(k)] to acc[col(k)] atomically, then y = alpha*acc +
+// beta*y with the output's epilogue.  It needs only the normalised row
+// offsets and the row-block partition beside the cols-long accumulator, so it
+// is the route of the reference-sized workspace (CSR_ALG1); the order in which
+// a column's products arrive is not fixed, so fp32 results can differ in the
+// last bits from run to run (int64 accumulation is exact in any order).
+
+struct AtomicParams {
+    const void* norm;        // RowT[rows+2], normalised row offsets
+    const int32_t* blocks;   // int32[B+1], first row of each row block
+    const void* block_nnz;   // RowT[B+1]
+    int64_t num_blocks;
+    const int32_t* col;
+    int64_t col_stride;
+    const void* val;
+    int64_t val_stride;
+    const void* x;
+    int64_t x_stride;
+    void* acc;
+    int64_t cols;
+    int32_t base;
+    int32_t conj;
+};
+
+template <AccKind A>
+__device__ __forceinline__ void AtomicAcc(typename AccOf<A>::T* acc, int64_t c, typename AccOf<A>::T v)
+{
+    if constexpr (A == AccKind::F32) {
+        unsafeAtomicAdd(acc + c, v);  // the hardware float atomic (coarse-grained device memory)
+    } else if constexpr (A == AccKind::C64) {
+        float* f = reinterpret_cast<float*>(acc + c);
+        unsafeAtomicAdd(f, v.re);
+        unsafeAtomicAdd(f + 1, v.im);
+    } else {
+        atomicAdd(reinterpret_cast<unsigned long long*>(acc + c), static_cast<unsigned long long>(v));
+    }
+}
+
+// One row block (at most kWaveRows rows) per wave, 4 waves per workgroup; the
+// block's row offsets go to the wave's LDS slice and each lane finds the row
+// of its entry by binary search there.
+template <typename RowT, ValKind V, AccKind A>
+__global__ __launch_bounds__(kThreads) void AtomicTransposeKernel(AtomicParams p)
+{
+    using Acc = typename AccOf<A>::T;
+    using ValT = typename ValOf<V>::T;
+    constexpr int kW = kThreads / kWave;
+    __shared__ int64_t sOff[kW][kWaveRows + 2];
+    const int wv = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kW + wv;
+    if (b >= p.num_blocks) return;
+    const RowT* norm = static_cast<const RowT*>(p.norm);
+    const int64_t r0 = p.blocks[b];
+    const int nr = static_cast<int>(p.blocks[b + 1] - r0);
+    const int64_t e0 = static_cast<int64_t>(static_cast<const RowT*>(p.block_nnz)[b]);
+    const int64_t e1 = static_cast<int64_t>(static_cast<const RowT*>(p.block_nnz)[b + 1]);
+    for (int i = lane; i <= nr; i += kWave) sOff[wv][i] = static_cast<int64_t>(norm[r0 + i]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const ValT* val = static_cast<const ValT*>(p.val);
+    const ValT* x = static_cast<const ValT*>(p.x);
+    Acc* acc = static_cast<Acc*>(p.acc);
+    for (int64_t k = e0 + lane; k < e1; k += kWave) {
+        // the row of entry k: the last i with sOff[i] <= k (rows may be empty)
+        int lo = 0, hi = nr;  // sOff[0] <= k < sOff[nr]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (sOff[wv][mid] <= k) lo = mid;
+            else hi = mid;
+        }
+        const int64_t c = static_cast<int64_t>(p.col[k * p.col_stride]) - p.base;
+        if (c < 0 || c >= p.cols) continue;
+        const Acc a = MaybeConj<V, A>(ToAcc<V, A>(val[k * p.val_stride]), p.conj);
+        AtomicAcc<A>(acc, c, a * ToAcc<V, A>(x[(r0 + lo) * p.x_stride]));
+    }
+}
+
+// y = alpha*acc + beta*y (y not read when beta == 0), the row kernels' epilogue.
+template <OutKind O, AccKind A>
+__global__ __launch_bounds__(kThreads) void AtomicFinalizeKernel(const typename AccOf<A>::T* acc,
+                                                                  typename OutOf<O>::T* y, int64_t n, int64_t stride,
+                                                                  Scalars s)
+{
+    using Acc = typename AccOf<A>::T;
+    Acc alpha, beta;
+    LoadScalars<A>(s, alpha, beta);
+    const bool betaNz = !IsZero(beta);
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; j < n;
+         j += static_cast<int64_t>(gridDim.x) * kThreads) {
+        StoreRow<O, A>(y, j * stride, acc[j], alpha, beta, betaNz);
+    }
+}
+
+template <typename RowT, ValKind V, OutKind O, AccKind A>
+void LaunchAtomicTranspose(const SpmvLaunch& l, const RowBlockParams& rb, hipStream_t stream)
+{
+    using Acc = typename AccOf<A>::T;
+    Acc* acc = At<Acc>(l.ws, l.layout.acc_offset);
+    const int64_t n = l.cols;
+    hipLaunchKernelGGL((ClearKernel<A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc, n);
+    AtomicParams p{};
+    p.norm = rb.rp;
+    p.blocks = rb.blocks;
+    p.block_nnz = rb.block_nnz;
+    p.num_blocks = l.layout.num_blocks;
+    p.col = l.col;
+    p.col_stride = l.col_stride;
+    p.val = l.val;
+    p.val_stride = l.val_stride;
+    p.x = l.x;
+    p.x_stride = l.x_stride;
+    p.acc = acc;
+    p.cols = n;
+    p.base = l.base;
+    p.conj = l.op == ACL_SPARSE_OP_CONJUGATE_TRANSPOSE ? 1 : 0;
+    constexpr int kW = kThreads / kWave;
+    const unsigned g = static_cast<unsigned>((p.num_blocks + kW - 1) / kW);
+    hipLaunchKernelGGL((AtomicTransposeKernel<RowT, V, A>), dim3(g), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((AtomicFinalizeKernel<O, A>), dim3(GridFor(n)), dim3(kThreads), 0, stream, acc,
+                       static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, rb.s);
+}
+
 template <typename RowT, ValKind V, OutKind O, AccKind A>
 int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
 {
@@ -2773,6 +2901,10 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
         hipLaunchKernelGGL((SpmvCscGatherKernel<RowT, V, O, A>), dim3(grid), dim3(kThreads), 0, stream, q);
         return 0;
     }
+    if (l.layout.lean && l.nnz > 0 && n > 0) {  // CSR_ALG1: the reference-sized workspace
+        LaunchAtomicTranspose<RowT, V, O, A>(l, p, stream);
+        return 0;
+    }
     // No non-zeros (the CSC path covers 0 < nnz <= INT32_MAX; larger
     // transposes are rejected by the host): y = beta*y.
     constexpr bool kDirect = (O == OutKind::F32 && A == AccKind::F32) || (O == OutKind::C64 && A == AccKind::C64);
@@ -2786,6 +2918,60 @@ int LaunchTranspose(const SpmvLaunch& l, hipStream_t stream)
                            static_cast<typename OutOf<O>::T*>(l.y), n, l.y_stride, p.s);
     }
     return 0;
+}
+
+// fp32 matrices of at most kSmallFloatRows rows (fp32 values, x, y and
+// compute, opA = N): one thread per row sums its entries in CSR order with
+// Kahan compensation and keeps the rounding error of every product (FMA
+// residual), then applies both corrections in the epilogue; when a product or
+// the plain running sum is not finite the plain sum is used instead.  This is
+// the reference's small-matrix path (sparse/spmv/arch35/spmv_kernel.cpp:448-499,
+// taken for rows <= 64 at :569-572), so {2^24, 1, -2^24} . {1, 1, 1} gives
+// exactly 1 as it does there.  Reads the caller's arrays (strides, index
+// base); entries outside [0, nnz) or columns outside [0, cols) are skipped.
+constexpr int64_t kSmallFloatRows = 64;
+
+template <typename RowT>
+__global__ __launch_bounds__(kWave) void SpmvSmallFloatKernel(const RowT* rp, int64_t rpStride, const int32_t* col,
+                                                             int64_t colStride, const float* val, int64_t valStride,
+                                                             const float* x, int64_t xStride, float* y,
+                                                             int64_t yStride, int64_t rows, int64_t cols,
+                                                             int64_t nnz, int32_t base, Scalars sc)
+{
+#pragma clang fp contract(off)
+    const int64_t row = threadIdx.x;
+    if (row >= rows) return;
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(sc, alpha, beta);
+    const int64_t begin = static_cast<int64_t>(rp[row * rpStride]) - base;
+    const int64_t end = static_cast<int64_t>(rp[(row + 1) * rpStride]) - base;
+    float sum = 0.0f, plain = 0.0f, comp = 0.0f, resid = 0.0f;
+    bool special = false;
+    if (begin >= 0 && end >= begin) {
+        for (int64_t p = begin; p < end && p < nnz; ++p) {
+            const int64_t c = static_cast<int64_t>(col[p * colStride]) - base;
+            if (c < 0 || c >= cols) continue;
+            const float a = val[p * valStride];
+            const float b = x[c * xStride];
+            const float prod = a * b;
+            plain = plain + prod;
+            special = special || !__builtin_isfinite(prod) || !__builtin_isfinite(plain);
+            resid = resid + __builtin_fmaf(a, b, -prod);
+            const float adj = prod - comp;
+            const float next = sum + adj;
+            comp = (next - sum) - adj;
+            sum = next;
+        }
+    }
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0
+    float out;
+    if (special) {
+        out = betaNz ? alpha * plain + beta * y[row * yStride] : alpha * plain;
+    } else {
+        const float corr = alpha * (resid - comp);
+        out = betaNz ? __builtin_fmaf(alpha, sum, beta * y[row * yStride]) + corr : __builtin_fmaf(alpha, sum, corr);
+    }
+    y[row * yStride] = out;
 }
 
 template <typename RowT, ValKind V, OutKind O, AccKind A>
@@ -3235,7 +3421,7 @@ size_t TaskScanTempBytes(int64_t n)
     size_t bytes = 0;
     if (hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, static_cast<int32_t*>(nullptr),
                                          static_cast<int32_t*>(nullptr), static_cast<int>(n)) != hipSuccess) {
-        bytes = static_cast<size_t>(n) * 8 + (1 << 20);
+        bytes = static_cast<size_t>(n) * 16 + (64 << 10);  // no device to ask: a generous bound
     }
     return bytes;
 }
@@ -3455,6 +3641,23 @@ int LaunchSpmvCompute(const SpmvLaunch& l, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= 0) return 0;
+    if (l.op == ACL_SPARSE_OP_NON_TRANSPOSE && l.rows <= kSmallFloatRows && l.val_kind == ValKind::F32 &&
+        l.out_kind == OutKind::F32 && l.acc_kind == AccKind::F32) {
+        // the reference's compensated small-matrix path (no staged or narrow kernels)
+        const Scalars sc = MakeRowBlockParams(l).s;
+        if (l.rowptr64) {
+            hipLaunchKernelGGL((SpmvSmallFloatKernel<int64_t>), dim3(1), dim3(kWave), 0, s,
+                               static_cast<const int64_t*>(l.row_ptr), l.row_stride, l.col, l.col_stride,
+                               static_cast<const float*>(l.val), l.val_stride, static_cast<const float*>(l.x),
+                               l.x_stride, static_cast<float*>(l.y), l.y_stride, l.rows, l.cols, l.nnz, l.base, sc);
+        } else {
+            hipLaunchKernelGGL((SpmvSmallFloatKernel<int32_t>), dim3(1), dim3(kWave), 0, s,
+                               static_cast<const int32_t*>(l.row_ptr), l.row_stride, l.col, l.col_stride,
+                               static_cast<const float*>(l.val), l.val_stride, static_cast<const float*>(l.x),
+                               l.x_stride, static_cast<float*>(l.y), l.y_stride, l.rows, l.cols, l.nnz, l.base, sc);
+        }
+        return 0;
+    }
     const int rc = l.rowptr64 ? DispatchTypes<int64_t>(l, s) : DispatchTypes<int32_t>(l, s);
     // staged gather: the row kernel above exits when Preprocess chose this path
     if (rc == 0 && l.staged && (l.staged_choice == 1 || l.staged_choice < 0)) return LaunchStagedCompute(l, stream);

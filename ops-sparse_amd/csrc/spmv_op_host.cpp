@@ -134,13 +134,12 @@ aclsparseStatus_t aclsparseSpMVOp_createDescr(aclsparseHandle_t handle, aclspars
             (void)hipGetLastError();
             d->narrow = aclsp::SpmvOpNarrowUsable(*d);
             if (aclsp::LaunchSpmvOpPreprocess(*d, StreamOf(handle)) != 0 || hipGetLastError() != hipSuccess) {
-                aclsp::ReleasePathChoice(d->choice_host, d->choice_event);
+                aclsp::ReleasePathChoice(d->choice);
                 delete d;
                 return ACL_SPARSE_STATUS_EXECUTION_FAILED;
             }
             if (d->narrow) {
-                aclsp::PublishPathChoice(d->choice_host, d->choice_event, d->choice_valid,
-                                         aclsp::SpmvOpSpmvWorkspace(*d), StreamOf(handle));
+                aclsp::PublishPathChoice(d->choice, aclsp::SpmvOpSpmvWorkspace(*d), StreamOf(handle));
             }
         }
     }
@@ -153,7 +152,7 @@ aclsparseStatus_t aclsparseSpMVOp_destroyDescr(aclsparseSpMVOpDescr_t descr)
     if (descr == nullptr) return ACL_SPARSE_STATUS_SUCCESS;
     if (descr->signature != aclsp::kSpMVOpDescrSignature) return ACL_SPARSE_STATUS_INVALID_VALUE;
     descr->signature = 0;
-    aclsp::ReleasePathChoice(descr->choice_host, descr->choice_event);
+    aclsp::ReleasePathChoice(descr->choice);
     delete descr;
     return ACL_SPARSE_STATUS_SUCCESS;
 }

@@ -352,7 +352,7 @@ int LaunchSpmvOpExecute(const aclsparseSpMVOpDescr& d, const void* x, const void
         // distribution without them).
         SpmvLaunch sl = OpLaunch(d, LayoutOf(d));
         sl.narrow = d.narrow ? 1 : 0;
-        sl.staged_choice = d.narrow ? QueryPathChoice(d.choice_host, d.choice_event, d.choice_valid, stream) : -1;
+        sl.staged_choice = d.narrow ? QueryPathChoice(d.choice, stream) : -1;
         sl.x = x;
         sl.y = const_cast<void*>(y);
         sl.device_scalars = deviceScalars ? 1 : 0;

@@ -172,9 +172,29 @@ def zipf_rows(rows=8388608, device="cpu", seed=20260504, mean=16.0, cap=200000, 
     rng = np.random.default_rng(seed)
     cap = min(cap, rows)
     z = np.minimum(rng.zipf(exponent, size=rows), cap).astype(np.float64)
-    scaled = z * (mean * rows / z.sum())
-    lengths = np.floor(scaled + rng.random(rows)).astype(np.int64)  # unbiased rounding keeps the mean
-    lengths = np.clip(lengths, 0, cap)
+    u = rng.random(rows)  # unbiased rounding of the scaled lengths
+    target = int(round(mean * rows))
+
+    def total(f):
+        # expected entries once duplicate columns are dropped: a row of L
+        # uniform draws over `rows` columns keeps rows*(1-(1-1/rows)^L)
+        lengths = np.minimum(np.floor(z * f + u), cap)
+        return float(-rows * np.expm1(lengths * np.log1p(-1.0 / rows)).sum())
+
+    # The cap takes mass from the longest rows (and dropping duplicate columns
+    # a little more), so a plain rescale to the mean falls short of it: bisect
+    # the scale factor until the expected entry count reaches the target.
+    lo = mean * rows / z.sum()
+    hi = lo
+    while total(hi) < target and hi < 1e12:
+        hi *= 2.0
+    for _ in range(64):
+        mid = 0.5 * (lo + hi)
+        if total(mid) >= target:
+            hi = mid
+        else:
+            lo = mid
+    lengths = np.minimum(np.floor(z * hi + u), cap).astype(np.int64)
     lengths = lengths[rng.permutation(rows)]
     g = _gen(device, seed)
     row_ptr, col = csr_from_lengths(torch.from_numpy(lengths), rows, g, device)

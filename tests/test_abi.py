@@ -201,6 +201,39 @@ def test_spmv_buffer_size_positive_and_aligned(env):
     assert st == Status.SUCCESS and nt >= 64 and nt % 64 == 0
 
 
+# (name, rows, cols, nnz, row offset type, value type, op) of the five benchmark configurations
+BENCH_SHAPES = [
+    ("c1", 4096, 4096, 167936, IndexType.I32, DataType.FLOAT, N),
+    ("c2", 4194304, 4194304, 20963328, IndexType.I32, DataType.FLOAT, N),
+    ("c3", 8388608, 8388608, 134217728, IndexType.I32, DataType.FLOAT, N),
+    ("c4", 16777216, 16777216, 536870912, IndexType.I64, DataType.FLOAT16, N),
+    ("c5", 2097152, 2097152, 22649242, IndexType.I32, DataType.FLOAT, T),
+]
+
+
+def _align64(n):
+    return (n + 63) // 64 * 64
+
+
+@pytest.mark.parametrize("shape", BENCH_SHAPES, ids=[s[0] for s in BENCH_SHAPES])
+def test_spmv_alg1_workspace_is_reference_sized(shape, env):
+    """CSR_ALG1 sizes the reference's workspace (sparse/spmv/arch35/spmv_tiling_data.h:104-141):
+    align64(align64(192 + (rows+1)*rowBytes) + cols*accBytes for a transpose), within 2x plus a
+    fixed 128 KiB (the row-block partition, the long-row tasks and their scan storage come on top);
+    DEFAULT keeps the larger layout of the staged / narrow / CSC tables, never smaller than ALG1's."""
+    name, rows, cols, nnz, ptype, vtype, op = shape
+    A = env.csr(rows=rows, cols=cols, nnz=nnz, ptrs=False, vtype=vtype, ptr_type=ptype)
+    xr, yr = (rows, cols) if op == T else (cols, rows)
+    x, y = env.vec(xr, 0, vtype), env.vec(yr, 0, vtype)
+    st, lean = env.size(op, A, x, y, alg=int(SpMVAlg.CSR_ALG1))
+    assert st == Status.SUCCESS and lean % 64 == 0
+    rb = 8 if ptype == IndexType.I64 else 4
+    ref = _align64(_align64(192 + (rows + 1) * rb) + (cols * 4 if op == T else 0))
+    assert ref <= lean <= 2 * ref + (128 << 10), (name, lean, ref)
+    st, full = env.size(op, A, x, y, alg=int(SpMVAlg.DEFAULT))
+    assert st == Status.SUCCESS and full >= lean
+
+
 def test_spmv_handle_checks(env, lib):
     A = env.csr()
     x, y = env.vec(3, env.xv), env.vec(2, env.yv)

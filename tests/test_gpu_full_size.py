@@ -75,6 +75,25 @@ def test_config4_full_size_sampled_oracle(dtype, dev):
     assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
 
 
+def test_config4_full_size_reference_sized_workspace(dev):
+    """c4 fp16 under CSR_ALG1: the reference-sized workspace (normalised row offsets and the row-block
+    partition, no staged tables) and the row kernel, on the sampled oracle."""
+    from ops_sparse._lib import SpMVAlg
+
+    w = wl.uniform_rows_lowp(device=dev, dtype=torch.float16)
+    y = torch.full((w.rows,), float("nan"), dtype=torch.float16, device=dev)
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta,
+                   alg=SpMVAlg.CSR_ALG1)
+    ref = (192 + (w.rows + 1) * 8 + 63) // 64 * 64  # the reference's formula with 8-byte row offsets
+    assert plan.buffer_size <= 2 * ref
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    err = check_sampled(w, y)
+    print(f"{w.name} ALG1: workspace {plan.buffer_size} B, sampled max scaled error {err:.3e}")
+
+
 @pytest.mark.parametrize("op", ["T", "H"])
 def test_complex_laplacian_transpose_full_size(op, dev):
     """The headline Laplacian (4,194,304 rows, 20,963,328 entries: more entries than one capped grid

@@ -95,6 +95,58 @@ def test_reference_repeated_coordinates(dev):
     assert y.item() == k["expected"][0]
 
 
+@pytest.mark.parametrize("alg", ["DEFAULT", "CSR_ALG1", "CSR_ALG2"])
+@pytest.mark.parametrize("mode", ["HOST", "DEVICE"])
+def test_reference_golden_precision_on_the_device(alg, mode, dev):
+    """{2^24, 1, -2^24} . {1, 1, 1} = 1 exactly (test/spmv/arch22/spmv_test.cpp:350-361).  A plain fp32
+    sum gives 0; the reference device sums matrices of at most 64 rows with Kahan compensation and an
+    FMA product residual (sparse/spmv/arch35/spmv_kernel.cpp:448-499), and so does this build."""
+    k = KATS["golden_precision"]
+    y = t([7.0], torch.float32, dev)
+    plan = CsrSpMV(1, 3, t(k["row_ptr"], torch.int32, dev), t(k["col_ind"], torch.int32, dev),
+                   t(k["values"], torch.float32, dev), t(k["x"], torch.float32, dev), y, 1.0, 0.0,
+                   alg=ALG[alg])
+    if mode == "DEVICE":
+        plan.handle.set_pointer_mode(PointerMode.DEVICE)
+        da, db = t([1.0], torch.float32, dev), t([0.0], torch.float32, dev)
+        plan.alpha = type("P", (), {"ptr": ctypes.c_void_p(da.data_ptr())})()
+        plan.beta = type("P", (), {"ptr": ctypes.c_void_p(db.data_ptr())})()
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    assert y.item() == k["expected"]
+
+
+@pytest.mark.parametrize("rows", [1, 33, 64, 65])
+def test_small_fp32_rows_compensated_up_to_64(rows, dev):
+    """Each row holds {2^24, 1, -2^24} (and a tail of ordinary values): up to 64 rows every row comes
+    out exact, as on the reference device; from 65 rows on the row kernels run (plain fp32 sums, within
+    the 1e-5 row-scaled tolerance).  beta != 0 reads y; a non-finite product takes the plain sum."""
+    per = [16777216.0, 1.0, -16777216.0, 0.5]
+    rp = torch.arange(0, 4 * rows + 1, 4, dtype=torch.int32)
+    ci = torch.tensor([0, 1, 2, 3] * rows, dtype=torch.int32)
+    va = torch.tensor(per * rows, dtype=torch.float32)
+    x = torch.tensor([1.0, 1.0, 1.0, 2.0])
+    y0 = torch.arange(rows, dtype=torch.float32)
+    if rows == 33:
+        va[4 * 5 + 3] = float("inf")  # row 5: inf * 2 -> the plain sum, inf
+    y = y0.to(dev).clone()
+    plan = CsrSpMV(rows, 4, rp.to(dev), ci.to(dev), va.to(dev), x.to(dev), y, 2.0, 0.5)
+    plan.preprocess()
+    plan.run()
+    torch.cuda.synchronize()
+    got = y.cpu()
+    exact = 2.0 * 2.0 + 0.5 * y0  # alpha * (1 + 0.5*2) + beta * y
+    if rows <= 64:
+        want = exact.clone()
+        if rows == 33:
+            want[5] = float("inf")
+        assert torch.equal(got, want)
+    else:
+        scale = 2.0 * (2 * 16777216.0 + 2.0) + 0.5 * y0.abs()
+        assert float(((got - exact).abs() / scale).max()) <= 1e-5
+
+
 @pytest.mark.parametrize("op", ["N", "T", "H"])
 @pytest.mark.parametrize("alg", ["DEFAULT", "CSR_ALG2"])
 @pytest.mark.parametrize("rows", [2, 4096])
@@ -229,6 +281,19 @@ def test_config_parity_full_size(name, dev):
     w = wl.config(name, dev, 1)
     w, y, _ = run_workload(w, dev)
     print(f"{w.name}: rows={w.rows} nnz={w.nnz} err={assert_close(w.to('cpu'), y):.3e}")
+
+
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_config_parity_full_size_reference_sized_workspace(name, dev):
+    """CSR_ALG1 on the reference-sized workspace: the row kernels (c3) and the atomic scatter into a
+    cols-long accumulator (c5, opA = T), at full size against the oracle."""
+    w = wl.config(name, dev, 1)
+    w, y, plan = run_workload(w, dev, alg=SpMVAlg.CSR_ALG1)
+    rb = 4
+    ref = (192 + (w.rows + 1) * rb + 63) // 64 * 64 + (w.cols * 4 if w.trans != "N" else 0)
+    assert plan.buffer_size <= 2 * ref
+    print(f"{w.name} ALG1: workspace {plan.buffer_size} B (reference formula {ref} B) "
+          f"err={assert_close(w.to('cpu'), y):.3e}")
 
 
 @pytest.mark.parametrize("name,scale,i64", [("c3", 64, False), ("c2", 16, False), ("c5", 64, False),
