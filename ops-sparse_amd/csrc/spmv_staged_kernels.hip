@@ -10,11 +10,12 @@
 //  * Preprocess (pattern only; values, x and y may change between calls, the
 //    reference's contract, sparse/spmv/README.md aclsparseSpMVPreprocess):
 //    merge-path tiles of kStageTileItems rows+entries; every entry goes to the
-//    bucket of its column's x segment (128 KiB of x); per tile, a stable radix
-//    sort by column gives each entry its slot in the tile's bucket-ordered runs
-//    (st_perm) and, in bucket order, its column within the bucket (st_cl).  A
-//    per-tile count of distinct x lines decides the path: when the lines are
-//    few (banded matrices) the row kernels keep the matrix.
+//    bucket of its column's x segment (128 KiB of x); per tile, a stable
+//    counting rank by bucket (StageRankKernel) gives each entry its slot in the
+//    tile's bucket-ordered runs (st_perm) and, in bucket order, its column
+//    within the bucket (st_cl).  A per-tile estimate of the distinct x lines
+//    decides the path: when the lines are few (banded matrices) the row
+//    kernels keep the matrix.
 //  * Pass A (StageGatherKernel), one workgroup per slice of the bucket-ordered
 //    slots: loads the slice's x segment into LDS (128 KiB) and writes
 //    xg[j] = segment[cl[j]]: a sequential read of cl and a sequential write.
@@ -192,9 +193,28 @@ __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
     for (int s = threadIdx.x; s < nb; s += kSortThreads) hist[s] = 0U;
     __syncthreads();
     if (t < q.tiles) {
+        // column loads in batches of 8 per thread, issued before the batch's atomics
         const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-        for (int64_t k = e0 + threadIdx.x; k < e1; k += kSortThreads) {
-            atomicAdd(&hist[KeyOf(q, q.col[k]) >> q.wshift], 1U);
+        const int n = static_cast<int>(e1 - e0);
+        const int64_t cBytes = (q.nnz - e0) * 4;
+        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(q.col + e0), 0, static_cast<int>(cBytes < 0x7FFFFFFFLL ? cBytes : 0x7FFFFFFFLL),
+            0x00020000);
+        constexpr int kBatch = 8;
+        for (int i0 = 0; i0 < n; i0 += kBatch * kSortThreads) {
+            int32_t raw[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                raw[u] = static_cast<int32_t>(
+                    __builtin_amdgcn_raw_buffer_load_b32(rc, (i0 + u * kSortThreads + threadIdx.x) * 4, 0, 0));
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (i0 + u * kSortThreads + static_cast<int>(threadIdx.x) < n) {
+                    atomicAdd(&hist[KeyOf(q, raw[u]) >> q.wshift], 1U);
+                }
+            }
         }
     }
     __syncthreads();
@@ -224,91 +244,126 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
     }
 }
 
-// Per tile: stable radix sort of (x line, position), the line being the
-// column's 128-byte line of x, so that the tile's entries are in bucket order
-// (and by line within a bucket, in entry order within a line); perm[k] = slot
-// of entry k in the tile's padded bucket-ordered runs, cl[start(t,s) + rank]
-// = column within the bucket (0 in the runs' padding); adds the tile's count
-// of distinct x lines to the metric.
-template <int kItems, int kEndBit, int kThr>
-__global__ __launch_bounds__(kThr) void StageSortKernel(StageParams q)
+// Per tile, without a sort: every entry's slot in the tile's bucket-ordered
+// runs (st_perm) and, in bucket order, its column within the bucket (st_cl).
+// Each entry takes the next place of its bucket's run with an LDS atomic, so
+// the order of the entries inside a run is the order the atomics landed in.
+// That order is free: pass A fills each slot from its own column and pass B
+// looks each entry's x value up by its own slot, while every row is still
+// summed in CSR order, so SpMV results do not depend on it.  The columns are
+// placed at their slots in LDS (run padding stays zero) and every run is
+// copied out whole.  The tile's distinct x lines (the path decision's metric)
+// are estimated by linear counting over a 2^15-bit LDS bitmap of hashed lines
+// (order-independent, hence the same on every run).
+template <int kItems, int kThr>
+__global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
 {
-    constexpr int kSortIpt = CeilDiv(kItems, kThr);
-    using Sort = hipcub::BlockRadixSort<uint32_t, kThr, kSortIpt, uint32_t>;
+    constexpr int kNb = kStageMaxBuckets + 1;
+    constexpr int kMapBits = 1 << 15;
+    constexpr int kMapWords = kMapBits / 32;
+    constexpr int kSlotCap = kItems + 3 * kNb;             // padded slots of a tile (runs padded to <= 4 slots)
+    constexpr int kStageWords = (kSlotCap + 1) / 2;
+    constexpr int kRunIpt = CeilDiv(kNb, kThr);
+    constexpr int kBatch = 8;                              // column loads in flight per thread
     using Scan = hipcub::BlockScan<uint32_t, kThr>;
-    constexpr int kRunIpt = (kStageMaxBuckets + 1 + kThr - 1) / kThr;
-    __shared__ typename Sort::TempStorage sortStorage;
+    __shared__ uint32_t stagedW[kStageWords];
+    __shared__ uint32_t map[kMapWords];
+    __shared__ uint32_t cnt[kNb];       // next place in each bucket's run
+    __shared__ uint32_t padOff[kNb + 1];
+    __shared__ uint32_t runStart[kNb];  // first st_cl slot of each bucket's run of this tile
     __shared__ typename Scan::TempStorage scanStorage;
-    __shared__ uint32_t firstSlot[kStageMaxBuckets + 1];
-    __shared__ uint32_t padOff[kStageMaxBuckets + 1];
-    __shared__ uint32_t firstKey[kThr + 1];
-    __shared__ uint32_t lastKey[kThr];
-    __shared__ uint32_t lineCount;
+    __shared__ uint32_t mapSet;
+    uint16_t* staged = reinterpret_cast<uint16_t*>(stagedW);
+
     const int64_t t = blockIdx.x;
+    const int tid = threadIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
     const int n = static_cast<int>(e1 - e0);
     const int nb = q.buckets + 1;
-    // the tile's run offsets in padded slots
+    const uint32_t* startRow = q.start + t * nb;  // first slot of each bucket's run: this tile, then the next
+
+    // the tile's run offsets in padded slots (run lengths from two tile-major rows of the scan)
     uint32_t pc[kRunIpt];
+#pragma unroll
     for (int u = 0; u < kRunIpt; ++u) {
-        const int s = threadIdx.x * kRunIpt + u;
-        pc[u] = s < nb ? q.counts[s * (q.tiles + 1) + t] : 0U;
+        const int sb = tid * kRunIpt + u;
+        const uint32_t a = sb < nb ? startRow[sb] : 0U;
+        pc[u] = sb < nb ? startRow[nb + sb] - a : 0U;
+        if (sb < nb) runStart[sb] = a;
     }
-    Scan(scanStorage).ExclusiveSum(pc, pc);
+    uint32_t total;
+    Scan(scanStorage).ExclusiveSum(pc, pc, total);
+#pragma unroll
     for (int u = 0; u < kRunIpt; ++u) {
-        const int s = threadIdx.x * kRunIpt + u;
-        if (s < nb) padOff[s] = pc[u];
-    }
-    uint32_t keys[kSortIpt], vals[kSortIpt];
-    constexpr uint32_t kPad = kEndBit >= 32 ? 0xFFFFFFFFU : ((1U << kEndBit) - 1U);
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        const uint32_t key = i < n ? KeyOf(q, q.col[e0 + i]) : 0U;
-        keys[u] = i < n ? key >> q.line_shift : kPad;
-        // the column within its bucket rides in the high half (the key holds only its line)
-        vals[u] = static_cast<uint32_t>(i) | ((key & ((1U << q.wshift) - 1U)) << 16);
-    }
-    if (threadIdx.x == 0) {
-        lineCount = 0U;
-        firstKey[kThr] = 0xFFFFFFFFU;
-    }
-    Sort(sortStorage).Sort(keys, vals, 0, kEndBit);
-    lastKey[threadIdx.x] = keys[kSortIpt - 1];
-    firstKey[threadIdx.x] = keys[0];
-    __syncthreads();
-    uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
-    uint32_t lines = 0U;
-    const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
-    const int bshift = q.wshift - q.line_shift;  // line -> bucket
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        if (i < n) {
-            const uint32_t key = keys[u];
-            const uint32_t b = key >> bshift;
-            if (prev == 0xFFFFFFFFU || (prev >> bshift) != b) firstSlot[b] = static_cast<uint32_t>(i);
-            if (b != nullBucket && prev != key) ++lines;
+        const int sb = tid * kRunIpt + u;
+        if (sb < nb) {
+            padOff[sb] = pc[u];
+            cnt[sb] = pc[u];
         }
-        prev = keys[u];
     }
-    if (lines != 0U) atomicAdd(&lineCount, lines);
+    if (tid == 0) {
+        padOff[nb] = total;
+        mapSet = 0U;
+    }
+    for (int i = tid; i < kStageWords; i += kThr) stagedW[i] = 0U;
+    for (int i = tid; i < kMapWords; i += kThr) map[i] = 0U;
     __syncthreads();
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        if (i < n) {
-            const uint32_t b = keys[u] >> bshift;
-            const uint32_t rank = static_cast<uint32_t>(i) - firstSlot[b];
-            q.perm[e0 + (vals[u] & 0xFFFFU)] = static_cast<uint16_t>(padOff[b] + rank);
-            const uint32_t start = q.start[t * nb + b];
-            q.cl[start + rank] = static_cast<uint16_t>(b == nullBucket ? 0U : (vals[u] >> 16));
-            // the run's last entry clears the run's padding
-            const uint32_t next = u + 1 < kSortIpt ? keys[u + 1] : firstKey[threadIdx.x + 1];
-            if (i + 1 == n || (next >> bshift) != b) {
-                const uint32_t runSlots = q.counts[b * (q.tiles + 1) + t];
-                for (uint32_t j = rank + 1U; j < runSlots; ++j) q.cl[start + j] = 0U;
+
+    const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
+    const uint32_t inMask = (1U << q.wshift) - 1U;
+    // the tile's column indices through a buffer resource (32-bit offsets;
+    // loads past the array's end read zero and belong to no entry)
+    const int64_t cBytes = (q.nnz - e0) * 4;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(q.col + e0), 0, static_cast<int>(cBytes < 0x7FFFFFFFLL ? cBytes : 0x7FFFFFFFLL),
+        0x00020000);
+    for (int i0 = 0; i0 < n; i0 += kBatch * kThr) {
+        int32_t raw[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            raw[u] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, (i0 + u * kThr + tid) * 4, 0, 0));
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = i0 + u * kThr + tid;
+            if (i < n) {
+                const uint32_t key = KeyOf(q, raw[u]);
+                const uint32_t b = key >> q.wshift;
+                const uint32_t slot = atomicAdd(&cnt[b], 1U);
+                q.perm[e0 + i] = static_cast<uint16_t>(slot);
+                if (b != nullBucket) {
+                    staged[slot] = static_cast<uint16_t>(key & inMask);
+                    const uint32_t h = ((key >> q.line_shift) * 2654435761U) >> 17;
+                    atomicOr(&map[h >> 5], 1U << (h & 31U));
+                }
             }
         }
     }
-    if (threadIdx.x == 0 && lineCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(lineCount));
+    __syncthreads();
+    {
+        uint32_t z = 0U;
+        for (int i = tid; i < kMapWords; i += kThr) z += static_cast<uint32_t>(__builtin_popcount(map[i]));
+        if (z != 0U) atomicAdd(&mapSet, z);
+    }
+    // every run out whole, two slots per store (runs and their starts are
+    // padded to whole chunks of at least two slots), one wave per bucket
+    const int lane = tid & (kWave - 1);
+    for (int sb = tid / kWave; sb < nb; sb += kThr / kWave) {
+        const uint32_t a = padOff[sb], len = padOff[sb + 1] - a;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(q.cl + runStart[sb]);
+        const uint32_t* src = stagedW + a / 2;
+        for (uint32_t j = lane; j < len / 2; j += kWave) dst[j] = src[j];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t z = mapSet;
+        const double m = static_cast<double>(kMapBits);
+        const double est = z >= static_cast<uint32_t>(kMapBits) ? static_cast<double>(n)
+                                                                 : -m * log1p(-static_cast<double>(z) / m);
+        const unsigned long long lines = static_cast<unsigned long long>(est + 0.5);
+        if (lines != 0ULL) atomicAdd(q.metric, lines);
+    }
 }
 
 // The path decision: staged when the tiles' distinct x lines exceed
@@ -1329,19 +1384,6 @@ StageParams MakeStageParams(const SpmvLaunch& l)
 
 unsigned XcdGrid(int64_t n) { return static_cast<unsigned>((n + kXcds - 1) / kXcds * kXcds); }
 
-template <int kEndBit>
-void LaunchSort(const StageParams& q, hipStream_t s)
-{
-    if (q.tile_items == kWide) {
-        // 1024 threads of 16 keys: 7% faster than 512 threads of 32 (more waves in flight per CU)
-        hipLaunchKernelGGL((StageSortKernel<kWide, kEndBit, 2 * kSortThreads>), dim3(static_cast<unsigned>(q.tiles)),
-                           dim3(2 * kSortThreads), 0, s, q);
-    } else {
-        hipLaunchKernelGGL((StageSortKernel<kNarrow, kEndBit, kSortThreads>), dim3(static_cast<unsigned>(q.tiles)),
-                           dim3(kSortThreads), 0, s, q);
-    }
-}
-
 template <typename RowT>
 int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
 {
@@ -1362,15 +1404,13 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL(StageTransposeKernel,
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
-    // sort keys: x lines of columns below (S+1) << wshift, plus an all-ones pad key
-    const uint64_t maxKey = ((static_cast<uint64_t>(L.st_buckets) + 1) << L.st_wshift) >> q.line_shift;
-    int bits = 1;
-    while ((uint64_t{1} << bits) <= maxKey) ++bits;
-    if (bits <= 16) LaunchSort<16>(q, s);
-    else if (bits <= 20) LaunchSort<20>(q, s);
-    else if (bits <= 24) LaunchSort<24>(q, s);
-    else if (bits <= 28) LaunchSort<28>(q, s);
-    else LaunchSort<32>(q, s);
+    if (q.tile_items == kWide) {
+        hipLaunchKernelGGL((StageRankKernel<kWide, kSortThreads>), dim3(static_cast<unsigned>(T)),
+                           dim3(kSortThreads), 0, s, q);
+    } else {
+        hipLaunchKernelGGL((StageRankKernel<kNarrow, kSortThreads>), dim3(static_cast<unsigned>(T)),
+                           dim3(kSortThreads), 0, s, q);
+    }
     hipLaunchKernelGGL(StageDecideKernel, dim3(1), dim3(1), 0, s, q);
     return 0;
 }
