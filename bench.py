@@ -447,7 +447,7 @@ def cpu_model():
 
 
 NARROW_PATH = "row kernels, narrow columns"
-ALG1_CONFIGS = ("c3", "c4h", "c5")  # also measured on CSR_ALG1's reference-sized workspace
+ALG1_CONFIGS = ("c1", "c2", "c3", "c4h", "c5")  # also measured on CSR_ALG1's reference-sized workspace
 LINE_RATE = 64e9  # 128-byte lines per second from the MALL (random x gathers), measured on MI355X
 
 
