@@ -64,7 +64,6 @@ constexpr int kWide = static_cast<int>(kStageTileItemsWide);
 // Per-tile shapes of a tile of kItems rows + entries.
 template <int kItems>
 struct Tile {
-    static constexpr int kSortIpt = CeilDiv(kItems, kSortThreads);                  // keys per thread of the sort
     static constexpr int kMaxLong = kItems / kLongRow + 1;                          // long rows of a tile
     static constexpr int kGroupSlots = CeilDiv((kItems + 3) / 4 + 1, kTileThreads);  // groups of 4 entries per thread
     static constexpr int kStageLanes = CeilDiv(kItems, kTileThreads);               // 64-slot windows per wave
@@ -958,63 +957,81 @@ __global__ __launch_bounds__(kSortThreads) void BtCountKernel(StageParams q)
     for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
 }
 
-// Per tile: stable sort of the entries by bucket; perm[k] = slot of entry k
-// in the tile's bucket-ordered runs; cl[start(t,b) + rank] = the entry's
-// place in bucket b's column-ordered products.
+// Per tile: perm[k] = slot of entry k in the tile's bucket-ordered runs;
+// cl[start(t,b) + (slot - run start)] = the entry's place in bucket b's
+// column-ordered products.  Each entry takes the next place of its bucket's
+// run with an LDS atomic: the order inside a run is free, because pass 1 puts
+// every product at its own slot and pass 2 moves it to its own column-order
+// place before the columns are summed in row order, so results do not depend
+// on it.  Adds the tile's count of non-empty runs (the path metric).
 template <int kItems, typename RowT>
-__global__ __launch_bounds__(kSortThreads) void BtSortKernel(StageParams q)
+__global__ __launch_bounds__(kSortThreads) void BtRankKernel(StageParams q)
 {
-    constexpr int kSortIpt = Tile<kItems>::kSortIpt;
-    using Sort = hipcub::BlockRadixSort<uint32_t, kSortThreads, kSortIpt, uint32_t>;
-    __shared__ typename Sort::TempStorage sortStorage;
-    __shared__ uint32_t firstSlot[kBtMaxBuckets + 1];
-    __shared__ uint32_t lastKey[kSortThreads];
+    constexpr int kNb = kBtMaxBuckets + 1;
+    constexpr int kRunIpt = CeilDiv(kNb, kSortThreads);
+    constexpr int kBatch = 4;
+    using Scan = hipcub::BlockScan<uint32_t, kSortThreads>;
+    __shared__ uint32_t cnt[kNb];       // next slot of each bucket's run (tile-local)
+    __shared__ uint32_t runBase[kNb];   // st_cl slot of each run's first entry minus its tile-local first slot
+    __shared__ uint32_t colBase[kNb];   // CSC index of each bucket's first entry
+    __shared__ typename Scan::TempStorage scanStorage;
     __shared__ uint32_t runCount;
     const int64_t t = blockIdx.x;
+    const int tid = threadIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-    const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
-    if (threadIdx.x == 0) runCount = 0U;
     const int n = static_cast<int>(e1 - e0);
-    uint32_t keys[kSortIpt], vals[kSortIpt];
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        keys[u] = i < n ? BtKey(q, e0 + i, first, last) : 0xFFFFU;
-        vals[u] = static_cast<uint32_t>(i);
-    }
-    Sort(sortStorage).Sort(keys, vals, 0, 16);
-    lastKey[threadIdx.x] = keys[kSortIpt - 1];
-    __syncthreads();
-    uint32_t prev = threadIdx.x > 0 ? lastKey[threadIdx.x - 1] : 0xFFFFFFFFU;
+    const int nb = q.buckets + 1;
+    const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
+    const uint32_t* startRow = q.start + t * nb;
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    if (tid == 0) runCount = 0U;
+    uint32_t pc[kRunIpt], a[kRunIpt];
     uint32_t runs = 0U;
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        if (i < n) {
-            if (keys[u] != prev) {
-                firstSlot[keys[u]] = static_cast<uint32_t>(i);
-                if (keys[u] < static_cast<uint32_t>(q.buckets)) ++runs;
-            }
-            q.perm[e0 + vals[u]] = static_cast<uint16_t>(i);
+#pragma unroll
+    for (int u = 0; u < kRunIpt; ++u) {
+        const int sb = tid * kRunIpt + u;
+        a[u] = sb < nb ? startRow[sb] : 0U;
+        pc[u] = sb < nb ? startRow[nb + sb] - a[u] : 0U;
+        if (sb < q.buckets && pc[u] != 0U) ++runs;
+        if (sb < q.buckets) colBase[sb] = static_cast<uint32_t>(colptr[static_cast<int64_t>(sb) << q.wshift]);
+    }
+    Scan(scanStorage).ExclusiveSum(pc, pc);
+#pragma unroll
+    for (int u = 0; u < kRunIpt; ++u) {
+        const int sb = tid * kRunIpt + u;
+        if (sb < nb) {
+            cnt[sb] = pc[u];
+            runBase[sb] = a[u] - pc[u];
         }
-        prev = keys[u];
     }
     if (runs != 0U) atomicAdd(&runCount, runs);
     __syncthreads();
-    if (threadIdx.x == 0 && runCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(runCount));
-    const int nb = q.buckets + 1;
-    const RowT* colptr = static_cast<const RowT*>(q.colptr);
-    for (int u = 0; u < kSortIpt; ++u) {
-        const int i = threadIdx.x * kSortIpt + u;
-        if (i < n) {
-            const uint32_t b = keys[u];
-            const uint32_t slot = q.start[t * nb + b] + (static_cast<uint32_t>(i) - firstSlot[b]);
-            uint32_t place = 0U;
-            if (b < static_cast<uint32_t>(q.buckets)) {
-                place = static_cast<uint32_t>(static_cast<int64_t>(q.inv[e0 + vals[u]]) -
-                                              static_cast<int64_t>(colptr[static_cast<int64_t>(b) << q.wshift]));
+    for (int i0 = 0; i0 < n; i0 += kBatch * kSortThreads) {
+        uint32_t key[kBatch];
+        int32_t inv[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = i0 + u * kSortThreads + tid;
+            key[u] = i < n ? BtKey(q, e0 + i, first, last) : 0U;
+            inv[u] = i < n ? q.inv[e0 + i] : 0;
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = i0 + u * kSortThreads + tid;
+            if (i < n) {
+                const uint32_t b = key[u];
+                const uint32_t slot = atomicAdd(&cnt[b], 1U);
+                q.perm[e0 + i] = static_cast<uint16_t>(slot);
+                const uint32_t place = b < static_cast<uint32_t>(q.buckets)
+                                           ? static_cast<uint32_t>(inv[u]) - colBase[b]
+                                           : 0U;
+                q.cl[runBase[b] + slot] = static_cast<uint16_t>(place);
             }
-            q.cl[slot] = static_cast<uint16_t>(place);
         }
     }
+    __syncthreads();
+    if (tid == 0 && runCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(runCount));
 }
 
 // csc_row[j] = entry_row[csc_pos[j]] (into the inv array, no longer needed).
@@ -1436,7 +1453,7 @@ int BtPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL(StageTransposeKernel,
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
-    hipLaunchKernelGGL((BtSortKernel<kWide, RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
+    hipLaunchKernelGGL((BtRankKernel<kWide, RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
     hipLaunchKernelGGL((BtCscRowKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
     hipLaunchKernelGGL((BtDecideKernel<RowT>), dim3(1), dim3(256), 0, s, q);
     return 0;
