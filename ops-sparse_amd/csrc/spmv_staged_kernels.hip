@@ -39,6 +39,7 @@
 #include <hipcub/hipcub.hpp>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "aclsparse_internal.h"
 #include "spmv_device.h"
@@ -69,7 +70,7 @@ struct Tile {
     static constexpr int kStageLanes = CeilDiv(kItems, kTileThreads);               // 64-slot windows per wave
     static constexpr int kWindows = (kItems + 63) / 64;                             // 64-slot windows of a tile
     static_assert(kTileWaves * kStageLanes * kWave >= kItems, "staging capacity");
-    static_assert(kItems + 3 * (kStageMaxBuckets + 1) < 65536, "uint16 slot numbers");
+    static_assert(kItems + 7 * (kStageMaxBuckets + 1) < 65536, "uint16 slot numbers");
 };
 
 struct StageParams {
@@ -260,7 +261,8 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
     constexpr int kNb = kStageMaxBuckets + 1;
     constexpr int kMapBits = 1 << 15;
     constexpr int kMapWords = kMapBits / 32;
-    constexpr int kSlotCap = kItems + 3 * kNb;             // padded slots of a tile (runs padded to <= 4 slots)
+    constexpr int kMaxChunk = static_cast<int>(kStageChunkBytes) / 2;  // slots per chunk, at most (2-byte x)
+    constexpr int kSlotCap = kItems + (kMaxChunk - 1) * kNb;           // padded slots of a tile
     constexpr int kStageWords = (kSlotCap + 1) / 2;
     constexpr int kRunIpt = CeilDiv(kNb, kThr);
     constexpr int kBatch = 8;                              // column loads in flight per thread
@@ -515,6 +517,14 @@ struct StageVal<ValKind::BF16> {
     }
 };
 
+// Word i of a 2- or 4-word vector (0 past its end).
+template <int I, typename T>
+__device__ __forceinline__ uint32_t GetW(const T& v)
+{
+    if constexpr (sizeof(T) == 16) return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
+    else return I == 0 ? v.x : I == 1 ? v.y : 0U;
+}
+
 // Sum over groups of 2^lg consecutive lanes (lg <= 6), fixed butterfly order.
 __device__ __forceinline__ float GroupSum(float v, int lg)
 {
@@ -609,17 +619,25 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
-    constexpr int kGroupSlots = Tile<kItems>::kGroupSlots;
+    // entries per group: one 16-byte load of values (4 fp32, or 8 fp16 / bf16)
+    // and of slots (8) where it fits: half the load instructions of groups of
+    // 4 for 16-bit values (pass B 762 -> 748 µs on c4)
+    constexpr int kG = sizeof(typename StageVal<V>::Raw) == 2 ? 8 : 4;
+    constexpr int kGroupSlots = CeilDiv((kItems + kG - 1) / kG + 1, kTileThreads);  // groups per thread
     using SV = StageVal<V>;
     using Raw = typename SV::Raw;
     using Group = typename SV::Group;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
-    // staged x moves in 8-byte chunks of kP slots (runs are padded to whole chunks)
-    constexpr int kP = 8 / static_cast<int>(sizeof(Raw));
+    // staged x moves in chunks of kP slots (runs are padded to whole chunks)
+    constexpr int kCB = static_cast<int>(kStageChunkBytes);
+    using ChunkT = typename std::conditional<kCB == 16, uint4, uint2>::type;
+    static_assert(kCB == 8 || kCB == 16, "8- or 16-byte chunks");
+    constexpr int kP = kCB / static_cast<int>(sizeof(Raw));
     constexpr int kChunkCap = (kTileItems + (kP - 1) * (kStageMaxBuckets + 1) + kP - 1) / kP;
     constexpr int kChunkIters = (kChunkCap + kTileThreads - 1) / kTileThreads;  // 64-chunk windows per wave
     constexpr int kChunkWindows = kTileWaves * kChunkIters;
-    constexpr int kAreaFloats = (kTileItems + 8 > 2 * kChunkCap ? kTileItems + 8 : 2 * kChunkCap);
+    constexpr int kChunkFloats = kCB / 4 * kChunkCap;
+    constexpr int kAreaFloats = (kTileItems + 2 * kG > kChunkFloats ? kTileItems + 2 * kG : kChunkFloats);
     __shared__ uint32_t runDelta[kStageMaxBuckets + 1];
     __shared__ uint32_t startBits[2 * kChunkWindows];
     __shared__ uint32_t firstRank[kChunkWindows];
@@ -645,20 +663,30 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     //   2. row offsets, values and slots (need the corners), then the staged
     //      x runs (need the run table's scan); the wave waits for the row
     //      offsets, then for the runs, while the values are still arriving.
-    // Every vector load is an unconditional buffer load (a load under a
-    // branch makes the wave wait for it where the branches join): addresses
-    // outside a buffer read zero, and lanes with nothing to load are masked
-    // afterwards.  Compiler barriers keep the issue order.
+    // Vector loads are buffer loads under no lane-divergent branch (a load
+    // under such a branch makes the wave wait for it where the branches
+    // join): addresses outside a buffer read zero, and lanes with nothing to
+    // load are masked afterwards.  Whole waves skip the loads that lie
+    // entirely past their data (wave-uniform branches: the run table past the
+    // last bucket, row offsets past the tile's rows, staging windows past the
+    // wave's chunks), which keeps those instructions out of the address unit's
+    // queue (3% of pass B on c4).  Compiler barriers keep the issue order.
     const uint32_t* startRow = q.start + t * nb;
     asm volatile("" ::"s"(startRow) : "memory");  // the kernel arguments the run loads need, first
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(startRow), 0, static_cast<int>(2 * nb * sizeof(uint32_t)), 0x00020000);
     uint32_t runA[kScanIpt], runB[kScanIpt];
+    // waves whose run-table entries all lie past the last bucket issue no loads
+    if (__builtin_amdgcn_readfirstlane(wv) * kWave * kScanIpt < nb) {
 #pragma unroll
-    for (int u = 0; u < kScanIpt; ++u) {
-        const int s = tid * kScanIpt + u;
-        runA[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, s * 4, 0, 0);
-        runB[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, (nb + s) * 4, 0, 0);
+        for (int u = 0; u < kScanIpt; ++u) {
+            const int s = tid * kScanIpt + u;
+            runA[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, s * 4, 0, 0);
+            runB[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, (nb + s) * 4, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kScanIpt; ++u) runA[u] = runB[u] = 0U;
     }
     asm volatile("" ::: "memory");
     typedef const __attribute__((address_space(4))) int32_t* CI32;
@@ -684,6 +712,10 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int i = tid + u * kTileThreads;
+        if (u == 1 && R < kTileThreads) {  // the second half of the offsets is past the tile's rows
+            rowOff[u] = 0;
+            continue;
+        }
         if constexpr (sizeof(RowT) == 8) {
             rowOff[u] = static_cast<int64_t>(
                 __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rn, i * 8, 0, 0)));
@@ -692,31 +724,37 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
         }
     }
     asm volatile("" ::: "memory");
-    // 2b. values and slots of this thread's groups of 4 entries (CSR order),
+    // 2b. values and slots of this thread's groups of kG entries (CSR order),
     //     from the tile's first group; loads past an array's last dword read
     //     zero (byte counts are rounded up to a dword, which never leaves the
     //     array's 16-byte block; st_perm is padded by 8 slots)
-    const int64_t g0 = e0 >> 2;
-    const int a0 = static_cast<int>(e0 - g0 * 4);  // entry e0's place in its group
-    const int ng = (a0 + E + 3) >> 2;              // groups of 4 entries touching the tile
-    const int64_t vBytes = ((q.nnz - g0 * 4) * static_cast<int64_t>(sizeof(Raw)) + 3) & ~int64_t{3};
+    const int64_t g0 = e0 / kG;
+    const int a0 = static_cast<int>(e0 - g0 * kG);  // entry e0's place in its group
+    const int ng = (a0 + E + kG - 1) / kG;          // groups of kG entries touching the tile
+    const int64_t vBytes = ((q.nnz - g0 * kG) * static_cast<int64_t>(sizeof(Raw)) + 3) & ~int64_t{3};
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<Raw*>(static_cast<const Raw*>(q.val) + g0 * 4), 0,
+        const_cast<Raw*>(static_cast<const Raw*>(q.val) + g0 * kG), 0,
         static_cast<int>(vBytes < 0x7FFFFFFFLL ? vBytes : 0x7FFFFFFFLL), 0x00020000);
-    const int64_t pBytes = (q.nnz + 8 - g0 * 4) * 2;
+    const int64_t pBytes = (q.nnz + 8 - g0 * kG) * 2;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-        q.perm + g0 * 4, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
-    Group gv[kGroupSlots];
-    uint2 gp[kGroupSlots];
+        q.perm + g0 * kG, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
+    using GroupT = typename std::conditional<kG == 8 || sizeof(Raw) == 4, uint4, uint2>::type;
+    using SlotsT = typename std::conditional<kG == 8, uint4, uint2>::type;
+    GroupT gv[kGroupSlots];
+    SlotsT gp[kGroupSlots];
 #pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        if constexpr (sizeof(Raw) == 4) {
+        if constexpr (sizeof(GroupT) == 16) {
             gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
         } else {
             gv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, gi * 8, 0, 0));
         }
-        gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+        if constexpr (kG == 8) {
+            gp[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, gi * 16, 0, 0));
+        } else {
+            gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+        }
     }
     asm volatile("" ::: "memory");
 
@@ -765,8 +803,8 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     //    words are the same for the whole wave), the loads after it; lanes
     //    past the range load chunk 0 and discard it.
     {
-        const uint2* xg = static_cast<const uint2*>(q.xg);
-        uint2* xl = reinterpret_cast<uint2*>(area);
+        const ChunkT* xg = static_cast<const ChunkT*>(q.xg);
+        ChunkT* xl = reinterpret_cast<ChunkT*>(area);
         const int span = (C + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
         const int i0 = __builtin_amdgcn_readfirstlane(wv) * span;  // wave-uniform
         const int i1 = i0 + span < C ? i0 + span : C;
@@ -784,9 +822,15 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
             const uint32_t d = runDelta[r];  // read by every lane: no load under a branch
             src[m] = i < i1 ? d + static_cast<uint32_t>(i) : 0U;
         }
-        uint2 v[kChunkIters];
+        ChunkT v[kChunkIters];
 #pragma unroll
-        for (int m = 0; m < kChunkIters; ++m) v[m] = xg[src[m]];  // xg holds fewer than 2^32 slots
+        for (int m = 0; m < kChunkIters; ++m) {  // xg holds fewer than 2^32 slots
+            if (i0 + m * kWave >= i1) {  // a 64-chunk window wholly past the wave's range: no load
+                v[m] = ChunkT{};
+                continue;
+            }
+            v[m] = xg[src[m]];
+        }
         asm volatile("" ::: "memory");  // all loads before the first store
         if (tid == 0) headFlag = rowOff[0] < e0 ? 1 : 0;  // the tile's first row started in an earlier tile
 #pragma unroll
@@ -799,39 +843,53 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     const bool headRow = headFlag != 0;
 
     // 5. products a_k * x(slot_k) in registers, then into the area by groups
-    //    of 4 (entry e0 at a0), with the tile's row offsets relative to the
+    //    of kG (entry e0 at a0), with the tile's row offsets relative to the
     //    first group (clamped to the tile) after them.  The tile's two edge
     //    groups also hold entries of the neighbouring tiles: their slots are
     //    other tiles' (still inside the staged area) and their products are
     //    replaced by zero.
-    float4 prod[kGroupSlots];
+    float4 prod[kGroupSlots][kG / 4];
     {
         const Raw* xlr = reinterpret_cast<const Raw*>(area);
 #pragma unroll
         for (int u = 0; u < kGroupSlots; ++u) {
             const int gi = tid + u * kTileThreads;
-            float pr[4];
+            float pr[kG];
+            const uint32_t pws[4] = {gp[u].x, gp[u].y, kG == 8 ? GetW<2>(gp[u]) : 0U, kG == 8 ? GetW<3>(gp[u]) : 0U};
+            const uint32_t vws[4] = {gv[u].x, gv[u].y, sizeof(GroupT) == 16 ? GetW<2>(gv[u]) : 0U,
+                                     sizeof(GroupT) == 16 ? GetW<3>(gv[u]) : 0U};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
-                const int slot = static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU);
-                pr[k] = SV::ToF(SV::Get(gv[u], k)) * SV::ToF(xlr[slot]);
+            for (int k = 0; k < kG; ++k) {
+                const int slot = static_cast<int>((pws[k >> 1] >> ((k & 1) * 16)) & 0xFFFFU);
+                Raw a;
+                if constexpr (sizeof(Raw) == 4) {
+                    a = vws[k];
+                } else {
+                    a = static_cast<Raw>(vws[k >> 1] >> ((k & 1) * 16));
+                }
+                pr[k] = SV::ToF(a) * SV::ToF(xlr[slot]);
             }
-            const int lo = a0 - gi * 4, hi = a0 + E - gi * 4;  // entries [lo, hi) of the group are the tile's
-            if (lo > 0 || hi < 4) {
+            const int lo = a0 - gi * kG, hi = a0 + E - gi * kG;  // entries [lo, hi) of the group are the tile's
+            if (lo > 0 || hi < kG) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) pr[k] = k >= lo && k < hi ? pr[k] : 0.0f;
+                for (int k = 0; k < kG; ++k) pr[k] = k >= lo && k < hi ? pr[k] : 0.0f;
             }
-            prod[u] = make_float4(pr[0], pr[1], pr[2], pr[3]);
+#pragma unroll
+            for (int h = 0; h < kG / 4; ++h) {
+                prod[u][h] = make_float4(pr[4 * h], pr[4 * h + 1], pr[4 * h + 2], pr[4 * h + 3]);
+            }
         }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        if (gi < ng) areaV[gi] = prod[u];
+        if (gi < ng) {
+#pragma unroll
+            for (int h = 0; h < kG / 4; ++h) areaV[gi * (kG / 4) + h] = prod[u][h];
+        }
     }
-    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);  // after the products
+    int32_t* rel = reinterpret_cast<int32_t*>(area) + ng * kG;  // after the products
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int i = tid + u * kTileThreads;

@@ -66,6 +66,7 @@ def algorithmic_bytes(w):
 
 
 STAGE_SEGMENT_BYTES = 128 * 1024  # x per bucket of the staged path
+STAGE_CHUNK_BYTES = 8  # staged x moves in chunks of this many bytes (runs padded to whole chunks)
 
 
 def staged_bytes(w):
@@ -76,7 +77,7 @@ def staged_bytes(w):
     every entry's slot (2 B) and the staged x values again, the normalised row
     offsets, the run table (4 B per tile and bucket) and y; col_ind is not
     read at all after Preprocess.  Staged slots are the entries plus the
-    padding of every (tile, bucket) run to whole 8-byte chunks (half a chunk
+    padding of every (tile, bucket) run to whole chunks of STAGE_CHUNK_BYTES (half a chunk
     less one slot per run on average).  Tiles hold 8184 rows + entries for
     fp32 values and 16376 for fp16 / bf16.
     """
@@ -86,7 +87,7 @@ def staged_bytes(w):
     items = 8184 if vb == 4 else 16376
     tiles = -(-(w.rows + w.nnz) // items)
     buckets = -(-(w.cols * vb) // STAGE_SEGMENT_BYTES) + 1
-    chunk = 8 // vb
+    chunk = STAGE_CHUNK_BYTES // vb
     slots = w.nnz + (chunk - 1) / 2 * buckets * tiles
     y_bytes = ob * w.rows * (2 if w.beta != 0 else 1)
     return int(rb * (w.rows + 2) + (2 + vb) * slots + (vb + 2) * w.nnz + vb * slots + vb * w.cols + y_bytes
