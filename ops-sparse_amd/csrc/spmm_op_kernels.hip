@@ -47,6 +47,8 @@ constexpr int kMmThreads = 256;
 constexpr int kMmWave = 64;
 constexpr float kFp16Max = 65504.0f;
 constexpr int kU = 8;  // entries whose B rows are in flight together
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 #ifndef SPMM_MAX_BLOCKS
 #define SPMM_MAX_BLOCKS 8192
 #endif
@@ -135,6 +137,14 @@ struct MmParams {
     int32_t c_row;       // C(i, j) = c[i*ldc + j]; else c[j*ldc + i]
     int32_t c_vec;
     int32_t has_b;       // k > 0: op(B) has rows to read
+    int32_t b_ubuf;      // fp32 rows of op(B) read as 16-byte buffer loads from any 4-byte
+                         // boundary (widths not a multiple of 4, or rows not 16-byte aligned);
+                         // loads past B's last element read 0
+    int32_t b_bytes;     // B's extent in bytes when b_ubuf
+    int32_t c_ubuf;      // fp32 row-major C whose rows are not 16-byte aligned: J = 4 columns
+                         // read and (when wholly inside the row) written by 16-byte buffer
+                         // accesses from any 4-byte boundary
+    int32_t c_bytes;     // C's extent in bytes when c_ubuf
     int32_t lg;          // log2 of lanes per row
     int64_t tiles;       // column tiles per row group
     int64_t waves;       // row groups * tiles
@@ -167,7 +177,20 @@ __device__ __forceinline__ void SpmmLoad(const MmParams& p, const typename Elem<
                                          bool strided, const int32_t cc[kU], float bv[kU][J])
 {
     using T = typename Elem<kHalf>::T;
-    if (fast) {
+    if (fast && !kHalf && J == 4 && p.b_ubuf) {
+        // one 16-byte buffer load per entry at any 4-byte boundary; columns
+        // past n read the next row (never stored), past B's end read 0
+        const __amdgpu_buffer_rsrc_t rb =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(b), 0, p.b_bytes, 0x00020000);
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            const int64_t r = cc[q] >= 0 ? cc[q] : 0;
+            const int off = static_cast<int>((r * p.ldb + j0) * 4);
+            const v4f w = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+#pragma unroll
+            for (int t = 0; t < J; ++t) bv[q][t] = w[t];
+        }
+    } else if (fast) {
         // one unconditional vector load per entry (a skipped entry reads row 0)
 #pragma unroll
         for (int q = 0; q < kU; ++q) {
@@ -234,7 +257,15 @@ template <bool kHalf, int J>
 __device__ __forceinline__ void SpmmLoadC(const MmParams& p, const typename Elem<kHalf>::T* c, int64_t row, int64_t j0,
                                           float old[J])
 {
-    if (p.c_row) {
+    if (!kHalf && J == 4 && p.c_ubuf) {
+        // columns past n read the next row (never stored), past C's end read 0
+        const __amdgpu_buffer_rsrc_t rc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<typename Elem<kHalf>::T*>(c), 0, p.c_bytes, 0x00020000);
+        const v4f w = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(rc, static_cast<int>((row * p.ldc + j0) * 4), 0, 0));
+#pragma unroll
+        for (int q = 0; q < J; ++q) old[q] = j0 + q < p.n ? w[q] : 0.0f;
+    } else if (p.c_row) {
         LoadRowJ<kHalf, J>(c + row * p.ldc, j0, p.n, 1, p.c_vec != 0, old);
     } else {
 #pragma unroll
@@ -257,7 +288,12 @@ __device__ __forceinline__ void SpmmStore(const MmParams& p, typename Elem<kHalf
 #pragma unroll
         for (int q = 0; q < J; ++q) out[q] = out[q] + beta * old[q];
     }
-    if (p.c_row) {
+    if (!kHalf && J == 4 && p.c_ubuf && j0 + J <= p.n) {
+        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(c, 0, p.c_bytes, 0x00020000);
+        const v4f w = {out[0], out[1], J > 2 ? out[2 % J] : 0.0f, J > 3 ? out[3 % J] : 0.0f};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w), rc,
+                                               static_cast<int>((row * p.ldc + j0) * 4), 0, 0);
+    } else if (p.c_row) {
         T* crow = c + row * p.ldc;
         if (p.c_vec && j0 + J <= p.n && !kHalf) {
             Vec<T, J> wv;
@@ -353,7 +389,7 @@ void SpmmOpKernel(MmParams p)
         const bool fullTile = (tile + 1) * g * J <= p.n;
         // (n a multiple of J: a lane's J columns lie wholly inside or wholly
         // past n, and lanes past n read column 0 of the same rows)
-        const bool fast = p.has_b && p.b_contig && p.b_vec && (fullTile || p.n % J == 0);
+        const bool fast = p.has_b && p.b_contig && ((p.b_vec && (fullTile || p.n % J == 0)) || p.b_ubuf);
         const int64_t jf = j0 < p.n ? j0 : 0;
         const bool strided = p.has_b && !p.b_contig;
         int64_t rs = 0, re = 0;
@@ -872,7 +908,25 @@ int LaunchSpmmOp(const SpmmLaunch& l, void* stream)
     }
     // lanes per row (power of two) and columns per lane
     int J = 1, lg = 6;
-    if (l.n >= 8 && l.n % 4 == 0) {
+    const int64_t bElems = p.b_contig ? (l.k - 1) * l.ldb + l.n : 0;
+    const bool aligned4 = l.n % 4 == 0 && l.ldb % 4 == 0 && AlignedTo(l.b, 4 * esz);
+    if (!l.fp16 && p.b_contig && p.has_b && l.n >= 8 && !aligned4 && bElems * 4 + 16 <= 0x7FFFFFFF &&
+        AlignedTo(l.b, 4)) {
+        // fp32 rows of op(B) that 16-byte loads cannot take aligned (a width
+        // or leading dimension not a multiple of 4): 4 columns per lane by
+        // buffer loads from 4-byte boundaries, 2 ... 64 lanes per row
+        J = 4;
+        lg = 1;
+        while (lg < 6 && (int64_t{4} << lg) < l.n) ++lg;
+        p.b_ubuf = 1;
+        p.b_bytes = static_cast<int32_t>(bElems * 4);
+        const int64_t cElems = (l.m - 1) * l.ldc + l.n;
+        if (l.c_row_major && (l.ldc % 4 != 0 || !AlignedTo(l.c, 16)) && cElems * 4 + 16 <= 0x7FFFFFFF &&
+            AlignedTo(l.c, 4)) {
+            p.c_ubuf = 1;
+            p.c_bytes = static_cast<int32_t>(cElems * 4);
+        }
+    } else if (l.n >= 8 && l.n % 4 == 0) {
         J = 4;  // 2, 4, ... 64 lanes of 4 columns per row
         lg = 1;
         while (lg < 6 && (int64_t{4} << lg) < l.n) ++lg;
