@@ -98,6 +98,7 @@ struct StageParams {
     float* tail;
     unsigned long long* metric;
     uint32_t* flag;
+    const uint16_t* rp16;  // low 16 bits of the normalised row offsets (the narrow copy's), or null
     int64_t part;  // pass A: bucket-ordered slots per workgroup
     int32_t chunk; // staged slots per 8-byte chunk: runs are padded to a multiple
     int32_t banded_ok;  // bucketed transpose: the one-pass banded kernel exists for this matrix
@@ -614,7 +615,7 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
 // followed by the tile's row offsets relative to the first group.  As many
 // waves per SIMD as the LDS allows: six for the narrow tiles (three
 // workgroups per CU), four for the wide ones.
-template <int kItems, typename RowT, ValKind V, OutKind O>
+template <int kItems, typename RowT, ValKind V, OutKind O, bool kRows16>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kNarrow ? 6 : kTileWaves / 2))) void StageTileKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
@@ -703,11 +704,15 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     const int E = static_cast<int>(e1 - e0);
     const int R = static_cast<int>(r1 - r0);
 
-    // 2a. row offsets of the tile's first 2*kTileThreads+1 rows
-    const int64_t nBytes = (q.rows + 2 - r0) * static_cast<int64_t>(sizeof(RowT));
+    // 2a. row offsets of the tile's first 2*kTileThreads+1 rows.  kRows16:
+    //     their low 16 bits only (2 bytes per row): rows 1..R of the tile
+    //     start inside it, so offset - e0 lies in [0, E] (E < 2^16) and
+    //     follows from the low halves; row 0 is clamped to the tile anyway
+    const int64_t nBytes = (q.rows + 2 - r0) * static_cast<int64_t>(kRows16 ? 2 : sizeof(RowT));
     const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<RowT*>(static_cast<const RowT*>(q.norm) + r0), 0,
-        static_cast<int>(nBytes < 0x7FFFFFFFLL ? nBytes : 0x7FFFFFFFLL), 0x00020000);
+        kRows16 ? static_cast<void*>(const_cast<uint16_t*>(q.rp16 + r0))
+                : static_cast<void*>(const_cast<RowT*>(static_cast<const RowT*>(q.norm) + r0)),
+        0, static_cast<int>(nBytes < 0x7FFFFFFFLL ? nBytes : 0x7FFFFFFFLL), 0x00020000);
     int64_t rowOff[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -716,7 +721,9 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
             rowOff[u] = 0;
             continue;
         }
-        if constexpr (sizeof(RowT) == 8) {
+        if constexpr (kRows16) {
+            rowOff[u] = static_cast<int64_t>(__builtin_amdgcn_raw_buffer_load_b16(rn, i * 2, 0, 0));
+        } else if constexpr (sizeof(RowT) == 8) {
             rowOff[u] = static_cast<int64_t>(
                 __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rn, i * 8, 0, 0)));
         } else {
@@ -832,7 +839,9 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
             v[m] = xg[src[m]];
         }
         asm volatile("" ::: "memory");  // all loads before the first store
-        if (tid == 0) headFlag = rowOff[0] < e0 ? 1 : 0;  // the tile's first row started in an earlier tile
+        if (tid == 0) {  // the tile's first row started in an earlier tile
+            headFlag = (kRows16 ? Norm<RowT>(q, r0) : rowOff[0]) < e0 ? 1 : 0;
+        }
 #pragma unroll
         for (int m = 0; m < kChunkIters; ++m) {
             const int i = i0 + m * kWave + lane;
@@ -890,16 +899,24 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
         }
     }
     int32_t* rel = reinterpret_cast<int32_t*>(area) + ng * kG;  // after the products
+    const auto relOf = [&](int i, int64_t off) {
+        if constexpr (kRows16) {
+            if (i == 0) return a0;
+            const int32_t d = static_cast<int32_t>((static_cast<uint32_t>(off) - static_cast<uint32_t>(e0)) & 0xFFFFU);
+            return a0 + (d > E ? E : d);
+        } else {
+            const int64_t d = off - e0;
+            return a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        }
+    };
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int i = tid + u * kTileThreads;
-        const int64_t d = rowOff[u] - e0;
-        if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        if (i <= R) rel[i] = relOf(i, rowOff[u]);
     }
     if (tid == 0) rel[R + 1] = a0 + E;
     for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
-        const int64_t d = Norm<RowT>(q, r0 + i) - e0;
-        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        rel[i] = relOf(i, kRows16 ? static_cast<int64_t>(q.rp16[r0 + i]) : Norm<RowT>(q, r0 + i));
     }
     __syncthreads();
 
@@ -1439,6 +1456,7 @@ StageParams MakeStageParams(const SpmvLaunch& l)
     q.metric = At<unsigned long long>(l.ws, L.st_metric_offset);
     q.flag = &At<SpmvWsHeader>(l.ws, 0)->staged_flag;
     q.part = L.st_part_size;
+    q.rp16 = l.narrow && L.narrow ? At<uint16_t>(l.ws, L.nr_offset) : nullptr;
     q.tile_items = L.st_tile_items;
     // the one-pass banded transpose: 32-bit row offsets and positions whose
     // byte offsets fit a buffer resource (LaunchBandedTranspose)
@@ -1535,7 +1553,13 @@ void LaunchStagedTyped(const SpmvLaunch& l, const StageParams& q, hipStream_t s)
                        static_cast<unsigned>(kStageSegmentBytes), s, q);
     // fp32 values: the narrow tiles; fp16 / bf16: the wide ones (StageTileItems)
     constexpr int kItems = V == ValKind::F32 ? kNarrow : kWide;
-    hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads), 0, s, q);
+    if (q.rp16 != nullptr) {
+        hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O, true>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads),
+                           0, s, q);
+    } else {
+        hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O, false>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads),
+                           0, s, q);
+    }
     hipLaunchKernelGGL((StageFixupKernel<RowT, O>), dim3(static_cast<unsigned>((L.st_tiles + 255) / 256)), dim3(256),
                        0, s, q);
 }
