@@ -74,8 +74,9 @@ def staged_bytes(w):
 
     Pass A reads every staged slot's column within its bucket (2 B) and
     writes the gathered x value (vb), reading x once; pass B reads the values,
-    every entry's slot (2 B) and the staged x values again, the normalised row
-    offsets, the run table (4 B per tile and bucket) and y; col_ind is not
+    every entry's slot (2 B) and the staged x values again, the low 16 bits of
+    the normalised row offsets (2 B per row), the run table (4 B per tile and
+    bucket) and y; col_ind is not
     read at all after Preprocess.  Staged slots are the entries plus the
     padding of every (tile, bucket) run to whole chunks of STAGE_CHUNK_BYTES (half a chunk
     less one slot per run on average).  Tiles hold 8184 rows + entries for
@@ -83,7 +84,7 @@ def staged_bytes(w):
     """
     vb = _elem_bytes(w.values.dtype)
     ob = _elem_bytes(w.out_dtype)
-    rb = 8 if w.row_ptr.dtype == torch.int64 else 4
+    rb = 2  # pass B reads the low halves of the row offsets
     items = 8184 if vb == 4 else 16376
     tiles = -(-(w.rows + w.nnz) // items)
     buckets = -(-(w.cols * vb) // STAGE_SEGMENT_BYTES) + 1
