@@ -169,14 +169,14 @@ __device__ __forceinline__ void LoadScalars(const Scalars& s, typename AccOf<A>:
     }
 }
 
-// y = alpha*sum + beta*y; y is not read when beta == 0
-// (sparse/spmv/arch35/spmv_kernel.cpp:341-345,544-552).
+// y[idx] = alpha*sum + beta*oldY, oldY being y[idx] as the caller read it
+// (unused when beta == 0).
 template <OutKind O, AccKind A>
-__device__ __forceinline__ void StoreRow(typename OutOf<O>::T* y, int64_t idx, typename AccOf<A>::T sum,
-                                         typename AccOf<A>::T alpha, typename AccOf<A>::T beta, bool betaNz)
+__device__ __forceinline__ void StoreRowOld(typename OutOf<O>::T* y, int64_t idx, typename AccOf<A>::T sum,
+                                            typename AccOf<A>::T alpha, typename AccOf<A>::T beta, bool betaNz,
+                                            typename AccOf<A>::T oldY)
 {
     using Acc = typename AccOf<A>::T;
-    const Acc oldY = betaNz ? OutToAcc<O, A>(y[idx]) : Zero<Acc>();
     Acc r;
     if constexpr (A == AccKind::I64) {
         r = ScaledI64(sum, alpha, beta, oldY);
@@ -186,6 +186,15 @@ __device__ __forceinline__ void StoreRow(typename OutOf<O>::T* y, int64_t idx, t
     y[idx] = FromAcc<O, A>(r);
 }
 
+// y = alpha*sum + beta*y; y is not read when beta == 0
+// (sparse/spmv/arch35/spmv_kernel.cpp:341-345,544-552).
+template <OutKind O, AccKind A>
+__device__ __forceinline__ void StoreRow(typename OutOf<O>::T* y, int64_t idx, typename AccOf<A>::T sum,
+                                         typename AccOf<A>::T alpha, typename AccOf<A>::T beta, bool betaNz)
+{
+    using Acc = typename AccOf<A>::T;
+    StoreRowOld<O, A>(y, idx, sum, alpha, beta, betaNz, betaNz ? OutToAcc<O, A>(y[idx]) : Zero<Acc>());
+}
 
 }  // namespace dev
 }  // namespace aclsp

@@ -526,6 +526,12 @@ __device__ __forceinline__ uint32_t GetW(const T& v)
     else return I == 0 ? v.x : I == 1 ? v.y : 0U;
 }
 
+// Word i of a 4-word vector (i a constant once loops are unrolled).
+__device__ __forceinline__ uint32_t WordOf(const uint4& v, int i)
+{
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 // Sum over groups of 2^lg consecutive lanes (lg <= 6), fixed butterfly order.
 __device__ __forceinline__ float GroupSum(float v, int lg)
 {
@@ -1143,7 +1149,12 @@ __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
     if (threadIdx.x == 0) *q.flag = scattered ? (ok != 0 ? 1U : 0U) : (q.banded_ok != 0 ? 2U : 0U);
 }
 
-// Pass 1: products of one tile into its runs (see above).
+// Pass 1: products of one tile into its runs (see above).  The row offsets
+// and x of the tile's first kBtPreRows*kTileThreads rows are loaded with the
+// values and slots (tiles of the Poisson-like c5 pattern hold about 1400
+// rows); rows past them, in tiles of many short rows, are read after.
+constexpr int kBtPreRows = 4;
+
 template <int kItems, typename RowT>
 __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
 {
@@ -1208,11 +1219,16 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(static_cast<const float*>(q.x) + r0), 0,
         static_cast<int>(xBytes < 0x7FFFFFFFLL ? xBytes : 0x7FFFFFFFLL), 0x00020000);
-    int64_t rowOff[2];
-    float xRow[2];
+    int64_t rowOff[kBtPreRows];
+    float xRow[kBtPreRows];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kBtPreRows; ++u) {
         const int i = tid + u * kTileThreads;
+        if (u > 0 && R < u * kTileThreads) {  // past the tile's rows (uniform over the workgroup)
+            rowOff[u] = 0;
+            xRow[u] = 0.0f;
+            continue;
+        }
         if constexpr (sizeof(RowT) == 8) {
             rowOff[u] = static_cast<int64_t>(
                 __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rn, i * 8, 0, 0)));
@@ -1269,12 +1285,12 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     // row offsets relative to the first group, clamped to the tile, after the entry area
     int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kBtPreRows; ++u) {
         const int i = tid + u * kTileThreads;
         const int64_t d = rowOff[u] - e0;
         if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
     }
-    for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
+    for (int i = tid + kBtPreRows * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
         const int64_t d = Norm<RowT>(q, r0 + i) - e0;
         rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
     }
@@ -1291,7 +1307,10 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
             longRows[atomicAdd(&longCount, 1)] = loc;
             continue;
         }
-        const float xv = u == 0 ? xRow[0] : u == 1 ? xRow[1] : static_cast<const float*>(q.x)[r0 + loc];
+        float xv = 0.0f;
+#pragma unroll
+        for (int h = 0; h < kBtPreRows; ++h) xv = u == h ? xRow[h] : xv;
+        if (u >= kBtPreRows) xv = static_cast<const float*>(q.x)[r0 + loc];
         for (int k = a; k < b; ++k) area[k] = xv;
     }
     __syncthreads();
@@ -1353,7 +1372,14 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     }
 }
 
-// Pass 2: one bucket's columns (see above).
+// Pass 2: one bucket's columns (see above).  Every load a thread makes is
+// issued before the first is used: the offsets, and with beta != 0 the old
+// y, of its first kBtColPre columns, then all of the bucket's products and
+// places by 16-byte loads from the 8-entry boundary at or before the
+// bucket's first slot (entries outside the bucket are read and dropped).
+constexpr int kBtColPre = 2;                                              // columns per thread prefetched
+constexpr int kBtColRounds = CeilDiv(static_cast<int>(kBtRegionCap) + 7, 8 * kBtColThreads);
+
 template <typename RowT>
 __global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
 {
@@ -1369,44 +1395,73 @@ __global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
     const RowT* colptr = static_cast<const RowT*>(q.colptr);
     const int64_t c0 = b << q.wshift;
     const int64_t c1 = c0 + (int64_t{1} << q.wshift) < q.cols ? c0 + (int64_t{1} << q.wshift) : q.cols;
-    const int64_t rs = static_cast<int64_t>(colptr[c0]);
-    const int n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - rs);
     float alpha, beta;
     LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
+    float* y = static_cast<float*>(q.y);
+    int64_t pa[kBtColPre], pe[kBtColPre];
+    float py[kBtColPre];
+#pragma unroll
+    for (int u = 0; u < kBtColPre; ++u) {
+        const int64_t c = c0 + tid + u * kBtColThreads;
+        const int64_t cc = c < c1 ? c : c1;
+        pa[u] = static_cast<int64_t>(colptr[cc]);
+        pe[u] = static_cast<int64_t>(colptr[c < c1 ? c + 1 : c1]);
+        py[u] = betaNz && c < c1 ? y[c] : 0.0f;
+    }
+    const int64_t rs = static_cast<int64_t>(colptr[c0]);
+    const int n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - rs);
+    const int64_t j0 = rs & ~int64_t{7};
+    const int skew = static_cast<int>(rs - j0);
+    const int64_t avail = q.nnz - j0;
+    // (place bytes rounded up to a dword: the range check drops a dword that
+    // crosses the limit, and st_cl is padded by 8 places)
+    const int64_t pBytes = avail * 4, lBytes = (avail * 2 + 3) & ~int64_t{3};
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        q.prod + j0, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+        q.cl + j0, 0, static_cast<int>(lBytes < 0x7FFFFFFFLL ? lBytes : 0x7FFFFFFFLL), 0x00020000);
+    uint4 pv[kBtColRounds][2];
+    uint4 lv[kBtColRounds];
+#pragma unroll
+    for (int r = 0; r < kBtColRounds; ++r) {
+        if (r * 8 * kBtColThreads >= skew + n) break;  // uniform over the workgroup
+        const int i = r * 8 * kBtColThreads + tid * 8;
+        pv[r][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4, 0, 0));
+        pv[r][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4 + 16, 0, 0));
+        lv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rl, i * 2, 0, 0));
+    }
     if (tid == 0) longCount = 0;
-    // products to their column-order places, 8 per thread per round (loads
-    // first, unconditional: lanes past the bucket read its first slot)
-    constexpr int kU = 8;
-    for (int base = 0; base < n; base += kU * kBtColThreads) {
-        float v[kU];
-        uint32_t p[kU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int i = base + u * kBtColThreads + tid;
-            const int64_t j = rs + (i < n ? i : 0);
-            v[u] = q.prod[j];
-            p[u] = q.cl[j];
-        }
-        asm volatile("" ::: "memory");
+    for (int r = 0; r < kBtColRounds; ++r) {
+        if (r * 8 * kBtColThreads >= skew + n) break;
+        const int i = r * 8 * kBtColThreads + tid * 8 - skew;  // the bucket's entry of the first lane slot
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int i = base + u * kBtColThreads + tid;
-            if (i < n) buf[p[u]] = v[u];
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t w = WordOf(lv[r], k >> 1);
+            const uint32_t place = (k & 1) ? w >> 16 : w & 0xFFFFU;
+            if (i + k >= 0 && i + k < n) buf[place] = __uint_as_float(WordOf(pv[r][k >> 2], k & 3));
         }
     }
     __syncthreads();
-    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
-    float* y = static_cast<float*>(q.y);
-    for (int64_t c = c0 + tid; c < c1; c += kBtColThreads) {
-        const int a = static_cast<int>(static_cast<int64_t>(colptr[c]) - rs);
-        const int e = static_cast<int>(static_cast<int64_t>(colptr[c + 1]) - rs);
+    auto column = [&](int64_t c, int64_t ca, int64_t ce, float old) {
+        const int a = static_cast<int>(ca - rs);
+        const int e = static_cast<int>(ce - rs);
         if (e - a > kBtLongCol) {
             longCols[atomicAdd(&longCount, 1)] = static_cast<int32_t>(c - c0);
-            continue;
+            return;
         }
         float sum = 0.0f;
         for (int k = a; k < e; ++k) sum += buf[k];
-        StoreRow<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz);
+        StoreRowOld<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz, old);
+    };
+#pragma unroll
+    for (int u = 0; u < kBtColPre; ++u) {
+        const int64_t c = c0 + tid + u * kBtColThreads;
+        if (c < c1) column(c, pa[u], pe[u], py[u]);
+    }
+    for (int64_t c = c0 + tid + kBtColPre * kBtColThreads; c < c1; c += kBtColThreads) {
+        column(c, static_cast<int64_t>(colptr[c]), static_cast<int64_t>(colptr[c + 1]), betaNz ? y[c] : 0.0f);
     }
     __syncthreads();
     const int nLong = longCount;

@@ -270,3 +270,23 @@ def test_banded_transpose_long_column_tasks(dev, extra):
     plan.run()
     torch.cuda.synchronize()
     assert torch.equal(first.view(torch.int32), y.view(torch.int32))
+
+
+@pytest.mark.parametrize("tail", [1, 2, 3, 5, 7, 8])
+def test_entry_counts_of_every_remainder_mod_8(dev, tail):
+    """nnz = 8q + tail (tail = 8: a multiple of 8): pass 2 reads each bucket's products and places
+    by 16-byte loads from an 8-entry boundary, so the last bucket's final loads cross the end of the
+    arrays at every offset; every column, the last bucket's included, must match the oracle."""
+    w = transpose_workload(dev, rows=1 << 20, cols=1 << 20, mean=5.0, seed=20 + tail)
+    keep = (w.nnz // 8 - 1) * 8 + tail
+    drop = w.nnz - keep
+    rp = w.row_ptr.clone()
+    rp[-1] -= drop  # the last rows lose their final entries
+    rp = torch.minimum(rp, rp[-1])
+    w.row_ptr = rp
+    w.col_ind = w.col_ind[:keep].contiguous()
+    w.values = w.values[:keep].contiguous()
+    assert w.nnz == keep and keep % 8 == tail % 8
+    y, plan = run(w)
+    assert header(plan)[0] == 1
+    assert_close(w.to("cpu"), y)
