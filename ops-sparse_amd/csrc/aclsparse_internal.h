@@ -436,8 +436,8 @@ inline bool StageEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t v
 // ---------------------------------------------------------------------------
 constexpr int64_t kBtMinNnz = int64_t{1} << 20;
 constexpr int32_t kBtMaxBuckets = 2048;
-constexpr int64_t kBtRegionTarget = 12288;  // mean entries per bucket the width aims at
-constexpr int64_t kBtRegionCap = 16384;     // entries per bucket that pass 2's LDS holds
+constexpr int64_t kBtRegionTarget = 24576;  // mean entries per bucket the width aims at
+constexpr int64_t kBtRegionCap = 32768;     // entries per bucket that pass 2's LDS holds
 
 // Columns per bucket (a power of two): about kBtRegionTarget entries each.
 inline int32_t BtBucketShift(uint64_t cols, uint64_t nnz)

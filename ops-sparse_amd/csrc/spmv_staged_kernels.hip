@@ -991,15 +991,17 @@ __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
 //    over its entries in LDS), placed in LDS at their slots, then written as
 //    the tile's runs; runs of neighbouring tiles are adjacent, so their
 //    partial lines merge in L2.
-//  * Pass 2 (BtColumnKernel), one workgroup per bucket: its products
-//    (sequential) go to LDS at their column-order places, then every column
+//  * Pass 2 (BtColumnKernel), one workgroup per CU looping over the buckets
+//    (each bucket's region of up to kBtRegionCap products takes most of a
+//    CU's LDS; the next bucket's loads fly while the current one is summed):
+//    its products (sequential) go to LDS at their column-order places, then every column
 //    is summed in row order, the order the reference's ALG2 accumulates in
 //    (sparse/spmv/README.md:252), and y = alpha*sum + beta*y.
 // Counterpart: the transpose of sparse/spmv/arch35/spmv_kernel.cpp:579-668,
 // which scatters a_k * x[row] into y with atomics.
 
 constexpr int kBtScanIpt = CeilDiv(kBtMaxBuckets + 1, kTileThreads);  // run lengths per thread
-constexpr int kBtColThreads = 512;                                     // pass 2
+constexpr int kBtColThreads = 1024;                                    // pass 2
 constexpr int kBtLongCol = 64;  // columns longer than this are summed by a wave
 constexpr int kBtRunEntries = 64;  // mean run length (entries) below which the bucketed kernels are chosen
 constexpr int kBtMaxLongCols = static_cast<int>(kBtRegionCap) / (kBtLongCol + 1) + 1;
@@ -1173,7 +1175,7 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     __shared__ typename Scan::TempStorage scanStorage;
     float* area = reinterpret_cast<float*>(areaV);
 
-    const int64_t t = XcdIndex();
+    const int64_t t = ChunkedXcdIndex();  // as pass B: tiles in flight consecutive chip-wide
     if (t >= q.tiles) return;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -1372,47 +1374,45 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     }
 }
 
-// Pass 2: one bucket's columns (see above).  Every load a thread makes is
-// issued before the first is used: the offsets, and with beta != 0 the old
-// y, of its first kBtColPre columns, then all of the bucket's products and
-// places by 16-byte loads from the 8-entry boundary at or before the
-// bucket's first slot (entries outside the bucket are read and dropped).
-constexpr int kBtColPre = 2;                                              // columns per thread prefetched
+// Pass 2: the buckets' columns (see above).  Persistent: kBtColGrid
+// workgroups, one per CU (the bucket region takes most of a CU's LDS), each
+// taking buckets w, w + grid, ...  While a bucket's columns are summed from
+// LDS, the next bucket's loads are in flight: its products and places (by
+// 16-byte loads from the 8-entry boundary at or before its first slot;
+// entries outside the bucket are read and dropped) and the offsets, and with
+// beta != 0 the old y, of each thread's first kBtColPre columns.
+constexpr int kBtColPre = 2;  // columns per thread prefetched
 constexpr int kBtColRounds = CeilDiv(static_cast<int>(kBtRegionCap) + 7, 8 * kBtColThreads);
+constexpr int kBtColGrid = 256;
 
-template <typename RowT>
-__global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
-{
-    __shared__ float buf[kBtRegionCap];
-    __shared__ int32_t longCols[kBtMaxLongCols];
-    __shared__ int longCount;
-    if (FlagSet(q.flag) != 1U) return;
-    const int64_t b = XcdIndex();
-    if (b >= q.buckets) return;
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wv = tid / kWave;
-    const RowT* colptr = static_cast<const RowT*>(q.colptr);
-    const int64_t c0 = b << q.wshift;
-    const int64_t c1 = c0 + (int64_t{1} << q.wshift) < q.cols ? c0 + (int64_t{1} << q.wshift) : q.cols;
-    float alpha, beta;
-    LoadScalars<AccKind::F32>(q.s, alpha, beta);
-    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
-    float* y = static_cast<float*>(q.y);
+struct BtBucketLoads {
+    int64_t rs;  // the bucket's first slot
+    int n;       // its entries
+    int skew;    // rs minus the 8-entry boundary the loads start at
+    uint4 pv[kBtColRounds][2];
+    uint4 lv[kBtColRounds];
     int64_t pa[kBtColPre], pe[kBtColPre];
     float py[kBtColPre];
+};
+
+template <typename RowT>
+__device__ __forceinline__ void BtLoadBucket(const StageParams& q, int64_t b, bool betaNz, int tid, BtBucketLoads& L)
+{
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    const float* y = static_cast<const float*>(q.y);
+    const int64_t c0 = b << q.wshift;
+    const int64_t c1 = c0 + (int64_t{1} << q.wshift) < q.cols ? c0 + (int64_t{1} << q.wshift) : q.cols;
 #pragma unroll
     for (int u = 0; u < kBtColPre; ++u) {
         const int64_t c = c0 + tid + u * kBtColThreads;
-        const int64_t cc = c < c1 ? c : c1;
-        pa[u] = static_cast<int64_t>(colptr[cc]);
-        pe[u] = static_cast<int64_t>(colptr[c < c1 ? c + 1 : c1]);
-        py[u] = betaNz && c < c1 ? y[c] : 0.0f;
+        L.pa[u] = static_cast<int64_t>(colptr[c < c1 ? c : c1]);
+        L.pe[u] = static_cast<int64_t>(colptr[c < c1 ? c + 1 : c1]);
+        L.py[u] = betaNz && c < c1 ? y[c] : 0.0f;
     }
-    const int64_t rs = static_cast<int64_t>(colptr[c0]);
-    const int n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - rs);
-    const int64_t j0 = rs & ~int64_t{7};
-    const int skew = static_cast<int>(rs - j0);
+    L.rs = static_cast<int64_t>(colptr[c0]);
+    L.n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - L.rs);
+    const int64_t j0 = L.rs & ~int64_t{7};
+    L.skew = static_cast<int>(L.rs - j0);
     const int64_t avail = q.nnz - j0;
     // (place bytes rounded up to a dword: the range check drops a dword that
     // crosses the limit, and st_cl is padded by 8 places)
@@ -1421,58 +1421,95 @@ __global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
         q.prod + j0, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
     const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
         q.cl + j0, 0, static_cast<int>(lBytes < 0x7FFFFFFFLL ? lBytes : 0x7FFFFFFFLL), 0x00020000);
-    uint4 pv[kBtColRounds][2];
-    uint4 lv[kBtColRounds];
 #pragma unroll
     for (int r = 0; r < kBtColRounds; ++r) {
-        if (r * 8 * kBtColThreads >= skew + n) break;  // uniform over the workgroup
+        if (r * 8 * kBtColThreads >= L.skew + L.n) break;  // uniform over the workgroup
         const int i = r * 8 * kBtColThreads + tid * 8;
-        pv[r][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4, 0, 0));
-        pv[r][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4 + 16, 0, 0));
-        lv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rl, i * 2, 0, 0));
+        L.pv[r][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4, 0, 0));
+        L.pv[r][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, i * 4 + 16, 0, 0));
+        L.lv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rl, i * 2, 0, 0));
     }
-    if (tid == 0) longCount = 0;
+}
+
+template <typename RowT>
+__global__ __launch_bounds__(kBtColThreads) void BtColumnKernel(StageParams q)
+{
+    __shared__ float buf[kBtRegionCap];
+    __shared__ int32_t longCols[kBtMaxLongCols];
+    __shared__ int longCount;
+    if (FlagSet(q.flag) != 1U) return;
+    int64_t b = blockIdx.x;
+    if (b >= q.buckets) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid / kWave;
+    const RowT* colptr = static_cast<const RowT*>(q.colptr);
+    float alpha, beta;
+    LoadScalars<AccKind::F32>(q.s, alpha, beta);
+    const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
+    float* y = static_cast<float*>(q.y);
+    BtBucketLoads cur;
+    BtLoadBucket<RowT>(q, b, betaNz, tid, cur);
+    for (; b < q.buckets; b += gridDim.x) {
+        const int64_t c0 = b << q.wshift;
+        const int64_t c1 = c0 + (int64_t{1} << q.wshift) < q.cols ? c0 + (int64_t{1} << q.wshift) : q.cols;
+        const int64_t rs = cur.rs;
+        const int n = cur.n;
+        // products to their column-order places
 #pragma unroll
-    for (int r = 0; r < kBtColRounds; ++r) {
-        if (r * 8 * kBtColThreads >= skew + n) break;
-        const int i = r * 8 * kBtColThreads + tid * 8 - skew;  // the bucket's entry of the first lane slot
+        for (int r = 0; r < kBtColRounds; ++r) {
+            if (r * 8 * kBtColThreads >= cur.skew + n) break;
+            const int i = r * 8 * kBtColThreads + tid * 8 - cur.skew;  // the bucket's entry of the first lane slot
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t w = WordOf(lv[r], k >> 1);
-            const uint32_t place = (k & 1) ? w >> 16 : w & 0xFFFFU;
-            if (i + k >= 0 && i + k < n) buf[place] = __uint_as_float(WordOf(pv[r][k >> 2], k & 3));
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t w = WordOf(cur.lv[r], k >> 1);
+                const uint32_t place = (k & 1) ? w >> 16 : w & 0xFFFFU;
+                if (i + k >= 0 && i + k < n) buf[place] = __uint_as_float(WordOf(cur.pv[r][k >> 2], k & 3));
+            }
         }
-    }
-    __syncthreads();
-    auto column = [&](int64_t c, int64_t ca, int64_t ce, float old) {
-        const int a = static_cast<int>(ca - rs);
-        const int e = static_cast<int>(ce - rs);
-        if (e - a > kBtLongCol) {
-            longCols[atomicAdd(&longCount, 1)] = static_cast<int32_t>(c - c0);
-            return;
-        }
-        float sum = 0.0f;
-        for (int k = a; k < e; ++k) sum += buf[k];
-        StoreRowOld<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz, old);
-    };
+        if (tid == 0) longCount = 0;
+        __syncthreads();
+        int64_t pa[kBtColPre], pe[kBtColPre];
+        float py[kBtColPre];
 #pragma unroll
-    for (int u = 0; u < kBtColPre; ++u) {
-        const int64_t c = c0 + tid + u * kBtColThreads;
-        if (c < c1) column(c, pa[u], pe[u], py[u]);
-    }
-    for (int64_t c = c0 + tid + kBtColPre * kBtColThreads; c < c1; c += kBtColThreads) {
-        column(c, static_cast<int64_t>(colptr[c]), static_cast<int64_t>(colptr[c + 1]), betaNz ? y[c] : 0.0f);
-    }
-    __syncthreads();
-    const int nLong = longCount;
-    for (int li = wv; li < nLong; li += kBtColThreads / kWave) {
-        const int64_t c = c0 + longCols[li];
-        const int a = static_cast<int>(static_cast<int64_t>(colptr[c]) - rs);
-        const int e = static_cast<int>(static_cast<int64_t>(colptr[c + 1]) - rs);
-        float part = 0.0f;
-        for (int k = a + lane; k < e; k += kWave) part += buf[k];
-        const float sum = WaveSum(part);
-        if (lane == 0) StoreRow<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz);
+        for (int u = 0; u < kBtColPre; ++u) {
+            pa[u] = cur.pa[u];
+            pe[u] = cur.pe[u];
+            py[u] = cur.py[u];
+        }
+        if (b + gridDim.x < q.buckets) BtLoadBucket<RowT>(q, b + gridDim.x, betaNz, tid, cur);  // uniform
+        asm volatile("" ::: "memory");
+        auto column = [&](int64_t c, int64_t ca, int64_t ce, float old) {
+            const int a = static_cast<int>(ca - rs);
+            const int e = static_cast<int>(ce - rs);
+            if (e - a > kBtLongCol) {
+                longCols[atomicAdd(&longCount, 1)] = static_cast<int32_t>(c - c0);
+                return;
+            }
+            float sum = 0.0f;
+            for (int k = a; k < e; ++k) sum += buf[k];
+            StoreRowOld<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz, old);
+        };
+#pragma unroll
+        for (int u = 0; u < kBtColPre; ++u) {
+            const int64_t c = c0 + tid + u * kBtColThreads;
+            if (c < c1) column(c, pa[u], pe[u], py[u]);
+        }
+        for (int64_t c = c0 + tid + kBtColPre * kBtColThreads; c < c1; c += kBtColThreads) {
+            column(c, static_cast<int64_t>(colptr[c]), static_cast<int64_t>(colptr[c + 1]), betaNz ? y[c] : 0.0f);
+        }
+        __syncthreads();
+        const int nLong = longCount;
+        for (int li = wv; li < nLong; li += kBtColThreads / kWave) {
+            const int64_t c = c0 + longCols[li];
+            const int a = static_cast<int>(static_cast<int64_t>(colptr[c]) - rs);
+            const int e = static_cast<int>(static_cast<int64_t>(colptr[c + 1]) - rs);
+            float part = 0.0f;
+            for (int k = a + lane; k < e; k += kWave) part += buf[k];
+            const float sum = WaveSum(part);
+            if (lane == 0) StoreRow<OutKind::F32, AccKind::F32>(y, c, sum, alpha, beta, betaNz);
+        }
+        __syncthreads();  // the region is free for the next bucket
     }
 }
 
@@ -1596,7 +1633,8 @@ void BtComputeTyped(const SpmvLaunch& l, hipStream_t s)
     const StageParams q = MakeStageParams(l);
     hipLaunchKernelGGL((BtScatterKernel<kWide, RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads), 0, s,
                        q);
-    hipLaunchKernelGGL((BtColumnKernel<RowT>), dim3(XcdGrid(l.layout.st_buckets)), dim3(kBtColThreads), 0, s, q);
+    const int64_t colGrid = l.layout.st_buckets < kBtColGrid ? l.layout.st_buckets : kBtColGrid;
+    hipLaunchKernelGGL((BtColumnKernel<RowT>), dim3(static_cast<unsigned>(colGrid)), dim3(kBtColThreads), 0, s, q);
 }
 
 template <typename RowT, ValKind V, OutKind O>

@@ -18,8 +18,8 @@ from ops_sparse import workloads as wl
 
 pytestmark = pytest.mark.gpu
 
-REGION_TARGET = 12288
-REGION_CAP = 16384
+REGION_TARGET = 24576
+REGION_CAP = 32768
 
 
 def header(plan):
