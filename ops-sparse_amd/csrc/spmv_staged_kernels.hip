@@ -1413,14 +1413,13 @@ __device__ __forceinline__ void BtLoadBucket(const StageParams& q, int64_t b, bo
     L.n = static_cast<int>(static_cast<int64_t>(colptr[c1]) - L.rs);
     const int64_t j0 = L.rs & ~int64_t{7};
     L.skew = static_cast<int>(L.rs - j0);
-    const int64_t avail = q.nnz - j0;
-    // (place bytes rounded up to a dword: the range check drops a dword that
-    // crosses the limit, and st_cl is padded by 8 places)
-    const int64_t pBytes = avail * 4, lBytes = (avail * 2 + 3) & ~int64_t{3};
-    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-        q.prod + j0, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
-        q.cl + j0, 0, static_cast<int>(lBytes < 0x7FFFFFFFLL ? lBytes : 0x7FFFFFFFLL), 0x00020000);
+    // the resources end with the bucket: loads past it read zero without
+    // touching memory (place bytes rounded up to a dword, since the range
+    // check drops a dword that crosses the limit; st_cl is padded by 8 places)
+    const int64_t avail = L.skew + L.n;
+    const int pBytes = static_cast<int>(avail * 4), lBytes = static_cast<int>((avail * 2 + 3) & ~int64_t{3});
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(q.prod + j0, 0, pBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(q.cl + j0, 0, lBytes, 0x00020000);
 #pragma unroll
     for (int r = 0; r < kBtColRounds; ++r) {
         if (r * 8 * kBtColThreads >= L.skew + L.n) break;  // uniform over the workgroup
