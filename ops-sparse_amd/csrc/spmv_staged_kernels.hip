@@ -1117,12 +1117,15 @@ __global__ __launch_bounds__(kSortThreads) void BtRankKernel(StageParams q)
     if (tid == 0 && runCount != 0U) atomicAdd(q.metric, static_cast<unsigned long long>(runCount));
 }
 
-// csc_row[j] = entry_row[csc_pos[j]] (into the inv array, no longer needed).
+// csc_row[j] = entry_row[csc_pos[j]] (into the inv array, no longer
+// needed), for the one-pass banded kernel only: launched after the path
+// decision, it does nothing unless that kernel was chosen (a gather of one
+// line per entry, which the other paths would pay for nothing).
 template <typename RowT>
 __global__ __launch_bounds__(256) void BtCscRowKernel(StageParams q)
 {
     const int64_t j = blockIdx.x * int64_t{256} + threadIdx.x;
-    if (j >= q.nnz) return;
+    if (j >= q.nnz || FlagSet(q.flag) != 2U) return;
     q.inv[j] = q.entry_row[static_cast<int64_t>(static_cast<const RowT*>(q.csc_pos)[j])];
 }
 
@@ -1621,8 +1624,8 @@ int BtPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
                        dim3(static_cast<unsigned>((T + 1 + 31) / 32), static_cast<unsigned>((L.st_buckets + 1 + 31) / 32)),
                        dim3(32, 8), 0, s, q);
     hipLaunchKernelGGL((BtRankKernel<kWide, RowT>), dim3(static_cast<unsigned>(T)), dim3(kSortThreads), 0, s, q);
-    hipLaunchKernelGGL((BtCscRowKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
     hipLaunchKernelGGL((BtDecideKernel<RowT>), dim3(1), dim3(256), 0, s, q);
+    hipLaunchKernelGGL((BtCscRowKernel<RowT>), dim3(static_cast<unsigned>((l.nnz + 255) / 256)), dim3(256), 0, s, q);
     return 0;
 }
 
