@@ -92,6 +92,11 @@ CASES = [
     ("one_giant_row_fp32", 1024, 1 << 22, "giant", torch.float32, torch.int32, -2.0, 1.0, 0),
     ("one_giant_sorted_row_fp32", 1024, 1 << 22, "giant_sorted", torch.float32, torch.int32, -2.0, 1.0, 0),
     ("sparse_rows_fp16", 3 << 23, 1 << 23, "sparse", torch.float16, torch.int64, 1.0, 0.0, 0),
+    # odd sizes: rows and columns not multiples of anything, an odd entry count (the value,
+    # slot and row-offset loads of the last tile end inside a dword), a partial last segment
+    ("ragged_fp16_i32_odd", (1 << 20) + 7, 3 * (1 << 21) + 12345, "ragged", torch.float16, torch.int32, 0.75, 0.25,
+     0),
+    ("ragged_fp32_i64_odd_base1", (1 << 20) + 3, (1 << 22) + 1, "ragged", torch.float32, torch.int64, 1.0, 0.0, 1),
 ]
 
 
@@ -106,6 +111,11 @@ def lengths_for(kind, rows, seed=3):
     if kind in ("giant", "giant_sorted"):  # one row spans thousands of tiles, the others are empty or short
         ln = rng.integers(0, 3, rows)
         ln[rows // 3] = STAGE_MIN_NNZ + 12345
+        return torch.from_numpy(ln.astype(np.int64))
+    if kind == "ragged":  # 25..40 entries per row, an odd total
+        ln = rng.integers(25, 41, rows)
+        if ln.sum() % 2 == 0:
+            ln[-1] += 1
         return torch.from_numpy(ln.astype(np.int64))
     if kind == "sparse":  # 2 entries per row on average, 40% empty rows: tiles hold many rows
         ln = np.where(rng.random(rows) < 0.4, 0, rng.integers(1, 6, rows))
