@@ -192,6 +192,34 @@ def test_staged_values_updated_in_place_and_no_preprocess(dev):
     assert_close(w.to("cpu"), y2)
 
 
+def test_staged_plan_with_an_unaligned_x_runs_the_row_kernels(dev):
+    """Pass A reads x by 16-byte vectors: after a staged Preprocess, an SpMV whose x is bound at a
+    4-byte offset (the plan still matches: x is not part of it) takes the row kernels instead, on
+    the whole matrix, and then an aligned x takes the staged kernels again."""
+    from ops_sparse.spmv import DnVecDescr
+
+    rows, cols = 1 << 20, 1 << 22
+    w = random_rows(dev, rows, cols, lengths_for("uniform32", rows), torch.float32, torch.int32, 1.0, 0.5)
+    y, plan = run(w, dev)
+    assert header(plan)[0] == 1
+    want = host_workload(w)
+    big = torch.zeros(cols + 4, dtype=torch.float32, device=dev)
+    xm = big[1:cols + 1]
+    xm.copy_(w.x)
+    assert xm.data_ptr() % 16 != 0
+    aligned = plan.x
+    plan.x = DnVecDescr(cols, xm)
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert_close(want, y)
+    plan.x = aligned
+    y.copy_(w.y0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert_close(want, y)
+
+
 def test_staged_device_scalars_and_beta_zero_ignores_nan_y(dev):
     from ops_sparse._lib import PointerMode
 
