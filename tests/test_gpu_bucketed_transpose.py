@@ -276,8 +276,9 @@ def test_banded_transpose_long_column_tasks(dev, extra):
 def test_entry_counts_of_every_remainder_mod_8(dev, tail):
     """nnz = 8q + tail (tail = 8: a multiple of 8): pass 2 reads each bucket's products and places
     by 16-byte loads from an 8-entry boundary, so the last bucket's final loads cross the end of the
-    arrays at every offset; every column, the last bucket's included, must match the oracle."""
-    w = transpose_workload(dev, rows=1 << 20, cols=1 << 20, mean=5.0, seed=20 + tail)
+    arrays at every offset; every column, the last (partial) bucket's included, must match the
+    oracle."""
+    w = transpose_workload(dev, rows=1 << 20, cols=(1 << 20) + 1237 * tail, mean=5.0, seed=20 + tail)
     keep = (w.nnz // 8 - 1) * 8 + tail
     drop = w.nnz - keep
     rp = w.row_ptr.clone()
