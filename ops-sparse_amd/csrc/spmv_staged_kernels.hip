@@ -952,7 +952,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
 
 // Rows that cross tile ends: the tile where such a row ends adds, in tile
 // order, the tail partial of the tile where it starts and the head partials
-// of every tile after it, then stores y.
+// of every tile after it, then stores y.  The tile where row r starts
+// follows from the merge path: its first entry s is item r + s of the
+// merged sequence (the ends of rows 0..r-1 and entries 0..s-1 come before
+// it), so it lies in tile (r + s) / tile_items; the partials are then read
+// with independent loads, however many tiles the row spans.
 template <typename RowT, OutKind O>
 __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
 {
@@ -964,8 +968,7 @@ __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
     if (q.tile_row[t + 1] == r0) return;                 // no row ends in tile t
     const int64_t start = Norm<RowT>(q, r0);
     if (start >= q.tile_nnz[t]) return;                  // its first row starts inside it
-    int64_t u = t - 1;
-    while (u > 0 && q.tile_row[u] == r0 && start < q.tile_nnz[u]) --u;  // tiles wholly inside the row
+    const int64_t u = (r0 + start) / q.tile_items;       // the tile where that row starts (< t)
     float sum = q.tail[u];
     for (int64_t v = u + 1; v <= t; ++v) sum += q.head[v];
     float alpha, beta;
