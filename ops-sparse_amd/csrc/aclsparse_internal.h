@@ -313,10 +313,18 @@ size_t TaskScanTempBytes(int64_t n);
 // 4-byte x value.  The staged path instead (pass A) loads each x segment into
 // one workgroup's LDS and writes the values its bucket's entries need, in
 // bucket order (sequential reads and writes), then (pass B) each merge-path
-// tile reads its runs of those values into LDS and sums its rows.  It is used
-// for matrices of at least kStageMinNnz entries whose x is at least
-// kStageMinXBytes; Preprocess measures the columns' spread and keeps the row
-// kernels when x accesses are local (banded matrices).
+// tile reads its runs of those values into LDS and sums its rows.  It is
+// considered for matrices whose x is at least kStageL2XBytes with at least
+// kStageMinNnz entries, and for those whose x is smaller (down to
+// kStageMinXBytes: the row kernels' gathers then hit L2 more often and cost
+// less) with at least kStageMinNnzSmallX entries; Preprocess measures the
+// columns' spread and keeps the row kernels when x accesses are local
+// (banded matrices).  Measured on MI355X, random columns, fp32 unless noted
+// (row kernels -> staged, µs per SpMV after a flush): x 16 MB: 2 M entries
+// 36 -> 45, 4 M 66 -> 50, 8 M 125 -> 61, 16 M 235 -> 83 (243 -> 90 in rows
+// of 4); x 8 MB: 16 M 172 -> 83; x 4 MB: 4 M 35 -> 46, 8 M 59 -> 57; x 2 MB:
+// 8 M 51 -> 59, 33.5 M fp16 169 -> 94.  The staged path costs about 35 µs of fixed
+// latency (three dependent launches) plus about 3 µs per million entries.
 // ---------------------------------------------------------------------------
 // Rows + entries per merge-path tile: 8184 for fp32 staged gather, 16376
 // for fp16 / bf16 staged gather and for the column-bucketed transpose (the
@@ -329,8 +337,10 @@ inline int64_t StageTileItems(bool transpose, uint32_t valueBytes)
 {
     return !transpose && valueBytes == 4U ? kStageTileItemsNarrow : kStageTileItemsWide;
 }
-constexpr int64_t kStageMinNnz = int64_t{1} << 25;
-constexpr int64_t kStageMinXBytes = int64_t{8} << 20;
+constexpr int64_t kStageMinNnz = int64_t{1} << 22;
+constexpr int64_t kStageMinNnzSmallX = int64_t{1} << 24;
+constexpr int64_t kStageMinXBytes = int64_t{1} << 20;
+constexpr int64_t kStageL2XBytes = int64_t{8} << 20;
 constexpr int64_t kStageSegmentBytes = 128 * 1024;  // x per bucket, staged in one workgroup's LDS
 constexpr int32_t kStageMaxBuckets = 1024;  // x up to 128 MiB
 constexpr int64_t kStageMinParts = 512;           // pass A workgroups (two per CU at least)
@@ -413,8 +423,10 @@ inline uint64_t StageSlotCap(uint64_t rows, uint64_t nnz, uint64_t buckets, uint
 inline bool StageEligible(uint64_t rows, uint64_t cols, uint64_t nnz, uint32_t valueBytes)
 {
     if (valueBytes == 0U || rows == 0U) return false;
-    if (nnz < static_cast<uint64_t>(kStageMinNnz) || nnz > 0xF0000000ULL) return false;
-    if (cols * valueBytes < static_cast<uint64_t>(kStageMinXBytes)) return false;
+    const uint64_t xBytes = cols * valueBytes;
+    if (xBytes < static_cast<uint64_t>(kStageMinXBytes) || nnz > 0xF0000000ULL) return false;
+    const int64_t minNnz = xBytes < static_cast<uint64_t>(kStageL2XBytes) ? kStageMinNnzSmallX : kStageMinNnz;
+    if (nnz < static_cast<uint64_t>(minNnz)) return false;
     const uint64_t w = static_cast<uint64_t>(kStageSegmentBytes) / valueBytes;
     const uint64_t buckets = (cols + w - 1) / w;
     if (buckets > static_cast<uint64_t>(kStageMaxBuckets)) return false;

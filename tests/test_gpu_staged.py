@@ -1,9 +1,10 @@
 """GPU parity of the staged-gather path (x segments staged in LDS, merge-path tiles) through the C ABI.
 
-The path is taken for non-transpose fp32-compute matrices of at least 2^25
-entries whose x is at least 8 MiB, when Preprocess finds the columns
-scattered; every case here is that large, so the oracle runs on 33.5M+
-entries (well under a second each).  Each test also reads the path
+The path is considered for non-transpose fp32-compute matrices of at least
+2^22 entries whose x is at least 8 MiB (2^24 entries for an x of 1 to 8 MiB),
+and taken when Preprocess finds the columns scattered; most cases here hold
+33.5M+ entries (the oracle runs well under a second each), and the size rule
+itself is checked at its edges.  Each test also reads the path
 Preprocess chose from the workspace header, so a case meant for the staged
 kernels cannot pass on the row kernels, and the other way round.
 """
@@ -152,6 +153,20 @@ def test_staged_path_matches_oracle(case, dev):
         assert torch.equal(y.view(torch.int16) if y.element_size() == 2 else y.view(torch.int32),
                            y1.view(torch.int16) if y.element_size() == 2 else y1.view(torch.int32))
     print(f"{name}: nnz={w.nnz} tiles={tiles} buckets={buckets} max scaled error {err:.3e}")
+
+
+@pytest.mark.parametrize("rows,per,cols,staged", [
+    (1 << 19, 8, 1 << 22, True),     # 4 M entries, x 16 MiB: staged
+    ((1 << 19) - 64, 8, 1 << 22, False),  # just under 2^22 entries: the row kernels
+    (1 << 20, 8, 1 << 19, False),    # 8 M entries, x 2 MiB: the row kernels (L2-sized x)
+    (1 << 20, 16, 1 << 19, True),    # 16 M entries, x 2 MiB: staged
+])
+def test_staged_size_rule(rows, per, cols, staged, dev):
+    w = random_rows(dev, rows, cols, torch.full((rows,), per, dtype=torch.int64), torch.float32, torch.int32, 1.25,
+                    -0.5)
+    y, plan = run(w, dev)
+    assert header(plan)[0] == (1 if staged else 0)
+    assert_close(host_workload(w), y)
 
 
 def test_banded_matrix_keeps_the_row_kernels(dev):

@@ -51,7 +51,7 @@ def bits(y):
 CASES = [
     # (first workload, second smaller workload)
     ("laplacian_then_uniform", lambda: wl.laplacian_2d(n=1024), lambda: wl.c1_uniform41(rows=3000, cols=5000)),
-    ("zipf_then_laplacian", lambda: wl.zipf_rows(rows=1 << 20, mean=16.0, cap=20000),
+    ("zipf_then_laplacian", lambda: wl.zipf_rows(rows=1 << 19, mean=16.0, cap=20000),
      lambda: wl.laplacian_2d(n=300)),
     ("transpose_then_smaller", lambda: wl.poisson_transpose(rows=1 << 16),
      lambda: wl.poisson_transpose(rows=1 << 12, seed=7)),
