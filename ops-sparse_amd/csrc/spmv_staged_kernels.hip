@@ -184,6 +184,31 @@ __global__ __launch_bounds__(256) void StageTileSplitKernel(StageParams q)
     q.tile_nnz[t] = d - lo;
 }
 
+// A tile's column indices (entries e0 .. e0+n-1, n at most the wide tile's
+// items) by 16-byte buffer loads of 4 from any 4-byte boundary, all issued
+// before the first is used: thread tid holds entries (u*kSortThreads+tid)*4
+// .. +3 in raw[u] (zero past the array's end; entries past n are the next
+// tile's, which the caller skips).
+constexpr int kColGroups = CeilDiv(static_cast<int>(kStageTileItemsWide), 4 * kSortThreads);
+__device__ __forceinline__ uint32_t WordOf(const uint4& v, int i)
+{
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ void LoadTileCols(const StageParams& q, int64_t e0, int n, uint4 (&raw)[kColGroups])
+{
+    const int64_t cBytes = (q.nnz - e0) * 4;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(q.col + e0), 0, static_cast<int>(cBytes < 0x7FFFFFFFLL ? cBytes : 0x7FFFFFFFLL),
+        0x00020000);
+#pragma unroll
+    for (int u = 0; u < kColGroups; ++u) {
+        if (u * 4 * kSortThreads >= n) break;  // uniform over the workgroup
+        const int i = (u * kSortThreads + static_cast<int>(threadIdx.x)) * 4;
+        raw[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rc, i * 4, 0, 0));
+    }
+    asm volatile("" ::: "memory");
+}
+
 // counts[s*(T+1) + t] = staged slots of tile t in bucket s: its entries,
 // padded to a multiple of q.chunk (column T is zero).
 __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
@@ -194,27 +219,19 @@ __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
     for (int s = threadIdx.x; s < nb; s += kSortThreads) hist[s] = 0U;
     __syncthreads();
     if (t < q.tiles) {
-        // column loads in batches of 8 per thread, issued before the batch's atomics
+        // all of the tile's column indices in one round trip (16-byte loads of
+        // 4), then the atomics
         const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
         const int n = static_cast<int>(e1 - e0);
-        const int64_t cBytes = (q.nnz - e0) * 4;
-        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int32_t*>(q.col + e0), 0, static_cast<int>(cBytes < 0x7FFFFFFFLL ? cBytes : 0x7FFFFFFFLL),
-            0x00020000);
-        constexpr int kBatch = 8;
-        for (int i0 = 0; i0 < n; i0 += kBatch * kSortThreads) {
-            int32_t raw[kBatch];
+        uint4 raw[kColGroups];
+        LoadTileCols(q, e0, n, raw);
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                raw[u] = static_cast<int32_t>(
-                    __builtin_amdgcn_raw_buffer_load_b32(rc, (i0 + u * kSortThreads + threadIdx.x) * 4, 0, 0));
-            }
-            asm volatile("" ::: "memory");
+        for (int u = 0; u < kColGroups; ++u) {
+            if (u * 4 * kSortThreads >= n) break;  // uniform
+            const int i = (u * kSortThreads + static_cast<int>(threadIdx.x)) * 4;
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                if (i0 + u * kSortThreads + static_cast<int>(threadIdx.x) < n) {
-                    atomicAdd(&hist[KeyOf(q, raw[u]) >> q.wshift], 1U);
-                }
+            for (int k = 0; k < 4; ++k) {
+                if (i + k < n) atomicAdd(&hist[KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k))) >> q.wshift], 1U);
             }
         }
     }
@@ -259,6 +276,8 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
 template <int kItems, int kThr>
 __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
 {
+    static_assert(kThr == kSortThreads, "the column loads assume kSortThreads threads");
+    static_assert(kItems <= kColGroups * 4 * kSortThreads, "a tile's entries fit the column loads");
     constexpr int kNb = kStageMaxBuckets + 1;
     constexpr int kMapBits = 1 << 15;
     constexpr int kMapWords = kMapBits / 32;
@@ -266,7 +285,6 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
     constexpr int kSlotCap = kItems + (kMaxChunk - 1) * kNb;           // padded slots of a tile
     constexpr int kStageWords = (kSlotCap + 1) / 2;
     constexpr int kRunIpt = CeilDiv(kNb, kThr);
-    constexpr int kBatch = 8;                              // column loads in flight per thread
     using Scan = hipcub::BlockScan<uint32_t, kThr>;
     __shared__ uint32_t stagedW[kStageWords];
     __shared__ uint32_t map[kMapWords];
@@ -313,24 +331,18 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
 
     const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
     const uint32_t inMask = (1U << q.wshift) - 1U;
-    // the tile's column indices through a buffer resource (32-bit offsets;
-    // loads past the array's end read zero and belong to no entry)
-    const int64_t cBytes = (q.nnz - e0) * 4;
-    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(q.col + e0), 0, static_cast<int>(cBytes < 0x7FFFFFFFLL ? cBytes : 0x7FFFFFFFLL),
-        0x00020000);
-    for (int i0 = 0; i0 < n; i0 += kBatch * kThr) {
-        int32_t raw[kBatch];
+    // the tile's column indices in one round trip, then per entry its slot
+    uint4 raw[kColGroups];
+    LoadTileCols(q, e0, n, raw);
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            raw[u] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, (i0 + u * kThr + tid) * 4, 0, 0));
-        }
-        asm volatile("" ::: "memory");
+    for (int u = 0; u < kColGroups; ++u) {
+        if (u * 4 * kThr >= n) break;  // uniform
+        const int i4 = (u * kThr + tid) * 4;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = i0 + u * kThr + tid;
+        for (int k = 0; k < 4; ++k) {
+            const int i = i4 + k;
             if (i < n) {
-                const uint32_t key = KeyOf(q, raw[u]);
+                const uint32_t key = KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k)));
                 const uint32_t b = key >> q.wshift;
                 const uint32_t slot = atomicAdd(&cnt[b], 1U);
                 q.perm[e0 + i] = static_cast<uint16_t>(slot);
@@ -524,12 +536,6 @@ __device__ __forceinline__ uint32_t GetW(const T& v)
 {
     if constexpr (sizeof(T) == 16) return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
     else return I == 0 ? v.x : I == 1 ? v.y : 0U;
-}
-
-// Word i of a 4-word vector (i a constant once loops are unrolled).
-__device__ __forceinline__ uint32_t WordOf(const uint4& v, int i)
-{
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
 // Sum over groups of 2^lg consecutive lanes (lg <= 6), fixed butterfly order.
