@@ -1139,17 +1139,26 @@ __global__ __launch_bounds__(256) void BtCscRowKernel(StageParams q)
 }
 
 // The path decision (header flag): 1, the column-bucketed kernels, when the
-// tiles' runs are short (their entries scattered over the columns: mean run
-// below kBtRunEntries entries) and every bucket's entries fit pass 2's LDS;
-// 2, the one-pass banded column kernel, when the runs are long (the values
-// and x an entry needs are then near those of its neighbours in column
-// order); 0, the CSC product and column passes.
+// entries are scattered over the columns and every bucket's entries fit pass
+// 2's LDS; 2, the one-pass banded column kernel, when they are not (the
+// values and x an entry needs are then near those of its neighbours in
+// column order); 0, the CSC product and column passes.  Scattered: the
+// tiles' runs are short (mean below kBtRunEntries entries), or, from
+// kBtWideNnz entries on, a tile has a run in at least half of the buckets on
+// average (a random pattern with few, wide buckets has long runs too; a
+// banded one touches a few buckets per tile).  Measured on random patterns
+// (banded kernel -> bucketed kernels, µs per SpMV): 1 M entries 22 -> 34,
+// 2 M 40 -> 27-30, 4 M 78 (CSC kernels) -> 38.
+constexpr int64_t kBtWideNnz = int64_t{1} << 21;
 template <typename RowT>
 __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
 {
     __shared__ int ok;
+    const unsigned long long runs = *q.metric;
     const bool scattered =
-        *q.metric * static_cast<unsigned long long>(kBtRunEntries) > static_cast<unsigned long long>(q.nnz);
+        runs * static_cast<unsigned long long>(kBtRunEntries) > static_cast<unsigned long long>(q.nnz) ||
+        (q.nnz >= kBtWideNnz && 2ULL * runs >= static_cast<unsigned long long>(q.tiles) *
+                                                     static_cast<unsigned long long>(q.buckets));
     if (threadIdx.x == 0) ok = 1;
     __syncthreads();
     const RowT* colptr = static_cast<const RowT*>(q.colptr);

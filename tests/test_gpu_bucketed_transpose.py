@@ -291,3 +291,16 @@ def test_entry_counts_of_every_remainder_mod_8(dev, tail):
     y, plan = run(w)
     assert header(plan)[0] == 1
     assert_close(w.to("cpu"), y)
+
+
+def test_random_pattern_with_few_wide_buckets_takes_the_bucketed_kernels(dev):
+    """2 M random entries over 1 M columns: the buckets are few and wide, so the tiles' runs are long
+    (about 110 entries), but every tile has a run in every bucket: the pattern is scattered and the
+    bucketed kernels take it (the one-pass banded kernel would gather every value from afar)."""
+    w = transpose_workload(dev, rows=1 << 18, cols=1 << 20, mean=8.5, seed=31)
+    assert w.nnz >= 1 << 21
+    y, plan = run(w)
+    flag, buckets, tiles = header(plan)
+    assert flag == 1
+    assert w.nnz / (buckets * tiles) > 64  # long runs, yet scattered
+    assert_close(w.to("cpu"), y)
