@@ -210,35 +210,69 @@ __device__ __forceinline__ void LoadTileCols(const StageParams& q, int64_t e0, i
 }
 
 // counts[s*(T+1) + t] = staged slots of tile t in bucket s: its entries,
-// padded to a multiple of q.chunk (column T is zero).
+// padded to a multiple of q.chunk (column T is zero).  Also the path
+// decision's metric: the tile's distinct x lines, estimated by linear
+// counting over a 2^15-bit LDS bitmap of hashed lines (order-independent,
+// hence the same on every run), added to q.metric.  The decision follows
+// this kernel, so a matrix that keeps the row kernels skips the rest.
+constexpr int kMapBits = 1 << 15;
+constexpr int kMapWords = kMapBits / 32;
 __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
 {
     __shared__ uint32_t hist[kStageMaxBuckets + 1];
+    __shared__ uint32_t map[kMapWords];
+    __shared__ uint32_t mapSet;
     const int64_t t = blockIdx.x;
     const int nb = q.buckets + 1;
     for (int s = threadIdx.x; s < nb; s += kSortThreads) hist[s] = 0U;
+    for (int i = threadIdx.x; i < kMapWords; i += kSortThreads) map[i] = 0U;
+    if (threadIdx.x == 0) mapSet = 0U;
     __syncthreads();
+    int n = 0;
     if (t < q.tiles) {
         // all of the tile's column indices in one round trip (16-byte loads of
         // 4), then the atomics
         const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-        const int n = static_cast<int>(e1 - e0);
+        n = static_cast<int>(e1 - e0);
         uint4 raw[kColGroups];
         LoadTileCols(q, e0, n, raw);
+        const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
 #pragma unroll
         for (int u = 0; u < kColGroups; ++u) {
             if (u * 4 * kSortThreads >= n) break;  // uniform
             const int i = (u * kSortThreads + static_cast<int>(threadIdx.x)) * 4;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if (i + k < n) atomicAdd(&hist[KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k))) >> q.wshift], 1U);
+                if (i + k < n) {
+                    const uint32_t key = KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k)));
+                    const uint32_t b = key >> q.wshift;
+                    atomicAdd(&hist[b], 1U);
+                    if (b != nullBucket) {
+                        const uint32_t h = ((key >> q.line_shift) * 2654435761U) >> 17;
+                        atomicOr(&map[h >> 5], 1U << (h & 31U));
+                    }
+                }
             }
         }
     }
     __syncthreads();
+    {
+        uint32_t z = 0U;
+        for (int i = threadIdx.x; i < kMapWords; i += kSortThreads) z += static_cast<uint32_t>(__builtin_popcount(map[i]));
+        if (z != 0U) atomicAdd(&mapSet, z);
+    }
     // padded to whole 8-byte chunks of staged x
     const uint32_t m = static_cast<uint32_t>(q.chunk) - 1U;
     for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = (hist[s] + m) & ~m;
+    __syncthreads();
+    if (threadIdx.x == 0 && t < q.tiles) {
+        const uint32_t z = mapSet;
+        const double mb = static_cast<double>(kMapBits);
+        const double est = z >= static_cast<uint32_t>(kMapBits) ? static_cast<double>(n)
+                                                                  : -mb * log1p(-static_cast<double>(z) / mb);
+        const unsigned long long lines = static_cast<unsigned long long>(est + 0.5);
+        if (lines != 0ULL) atomicAdd(q.metric, lines);
+    }
 }
 
 // start[t*(S+1) + s] = start_bm[s*(T+1) + t].
@@ -270,31 +304,27 @@ __global__ __launch_bounds__(256) void StageTransposeKernel(StageParams q)
 // looks each entry's x value up by its own slot, while every row is still
 // summed in CSR order, so SpMV results do not depend on it.  The columns are
 // placed at their slots in LDS (run padding stays zero) and every run is
-// copied out whole.  The tile's distinct x lines (the path decision's metric)
-// are estimated by linear counting over a 2^15-bit LDS bitmap of hashed lines
-// (order-independent, hence the same on every run).
+// copied out whole.  Runs only when the path decision chose the staged
+// kernels.
 template <int kItems, int kThr>
 __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
 {
     static_assert(kThr == kSortThreads, "the column loads assume kSortThreads threads");
     static_assert(kItems <= kColGroups * 4 * kSortThreads, "a tile's entries fit the column loads");
     constexpr int kNb = kStageMaxBuckets + 1;
-    constexpr int kMapBits = 1 << 15;
-    constexpr int kMapWords = kMapBits / 32;
     constexpr int kMaxChunk = static_cast<int>(kStageChunkBytes) / 2;  // slots per chunk, at most (2-byte x)
     constexpr int kSlotCap = kItems + (kMaxChunk - 1) * kNb;           // padded slots of a tile
     constexpr int kStageWords = (kSlotCap + 1) / 2;
     constexpr int kRunIpt = CeilDiv(kNb, kThr);
     using Scan = hipcub::BlockScan<uint32_t, kThr>;
     __shared__ uint32_t stagedW[kStageWords];
-    __shared__ uint32_t map[kMapWords];
     __shared__ uint32_t cnt[kNb];       // next place in each bucket's run
     __shared__ uint32_t padOff[kNb + 1];
     __shared__ uint32_t runStart[kNb];  // first st_cl slot of each bucket's run of this tile
     __shared__ typename Scan::TempStorage scanStorage;
-    __shared__ uint32_t mapSet;
     uint16_t* staged = reinterpret_cast<uint16_t*>(stagedW);
 
+    if (FlagSet(q.flag) != 1U) return;
     const int64_t t = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
@@ -321,12 +351,8 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
             cnt[sb] = pc[u];
         }
     }
-    if (tid == 0) {
-        padOff[nb] = total;
-        mapSet = 0U;
-    }
+    if (tid == 0) padOff[nb] = total;
     for (int i = tid; i < kStageWords; i += kThr) stagedW[i] = 0U;
-    for (int i = tid; i < kMapWords; i += kThr) map[i] = 0U;
     __syncthreads();
 
     const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
@@ -346,20 +372,11 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
                 const uint32_t b = key >> q.wshift;
                 const uint32_t slot = atomicAdd(&cnt[b], 1U);
                 q.perm[e0 + i] = static_cast<uint16_t>(slot);
-                if (b != nullBucket) {
-                    staged[slot] = static_cast<uint16_t>(key & inMask);
-                    const uint32_t h = ((key >> q.line_shift) * 2654435761U) >> 17;
-                    atomicOr(&map[h >> 5], 1U << (h & 31U));
-                }
+                if (b != nullBucket) staged[slot] = static_cast<uint16_t>(key & inMask);
             }
         }
     }
     __syncthreads();
-    {
-        uint32_t z = 0U;
-        for (int i = tid; i < kMapWords; i += kThr) z += static_cast<uint32_t>(__builtin_popcount(map[i]));
-        if (z != 0U) atomicAdd(&mapSet, z);
-    }
     // every run out whole, two slots per store (runs and their starts are
     // padded to whole chunks of at least two slots), one wave per bucket
     const int lane = tid & (kWave - 1);
@@ -368,15 +385,6 @@ __global__ __launch_bounds__(kThr) void StageRankKernel(StageParams q)
         uint32_t* dst = reinterpret_cast<uint32_t*>(q.cl + runStart[sb]);
         const uint32_t* src = stagedW + a / 2;
         for (uint32_t j = lane; j < len / 2; j += kWave) dst[j] = src[j];
-    }
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t z = mapSet;
-        const double m = static_cast<double>(kMapBits);
-        const double est = z >= static_cast<uint32_t>(kMapBits) ? static_cast<double>(n)
-                                                                 : -m * log1p(-static_cast<double>(z) / m);
-        const unsigned long long lines = static_cast<unsigned long long>(est + 0.5);
-        if (lines != 0ULL) atomicAdd(q.metric, lines);
     }
 }
 
@@ -1598,6 +1606,7 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
     hipLaunchKernelGGL((StageTileSplitKernel<RowT>), dim3(static_cast<unsigned>((T + 1 + 255) / 256)), dim3(256), 0,
                        s, q);
     hipLaunchKernelGGL(StageCountKernel, dim3(static_cast<unsigned>(T + 1)), dim3(kSortThreads), 0, s, q);
+    hipLaunchKernelGGL(StageDecideKernel, dim3(1), dim3(1), 0, s, q);  // the rank kernel runs only when staged
     const int64_t cells = static_cast<int64_t>(L.st_buckets + 1) * (T + 1);
     void* temp = reinterpret_cast<void*>(
         (reinterpret_cast<uintptr_t>(At<uint8_t>(l.ws, L.st_scan_offset)) + 255) & ~uintptr_t{255});
@@ -1616,7 +1625,6 @@ int StagedPreprocessTyped(const SpmvLaunch& l, hipStream_t s)
         hipLaunchKernelGGL((StageRankKernel<kNarrow, kSortThreads>), dim3(static_cast<unsigned>(T)),
                            dim3(kSortThreads), 0, s, q);
     }
-    hipLaunchKernelGGL(StageDecideKernel, dim3(1), dim3(1), 0, s, q);
     return 0;
 }
 
