@@ -2047,29 +2047,86 @@ __global__ __launch_bounds__(kThreads) void CscColPtrKernel(const int32_t* keys,
 // Row of every entry in CSR order (the last row whose normalised offset is
 // <= k; entries outside [norm[0], norm[rows]) get row 0 and are never used);
 // the sorted positions move to their final array if the sort left them in
-// the other buffer.
+// the other buffer.  One wave per workgroup; a wave takes kFinishSpan
+// consecutive entries: it finds the rows ra and rb of its first and last
+// in-range entry (wave-uniform searches), marks in LDS the first entry of
+// every row after ra that starts in its span (the largest row where several
+// empty rows share a start), and a running maximum over the marks gives each
+// entry its row: 16 consecutive entries per lane, then a prefix maximum over
+// the lanes.  The rows go out through LDS again, so that the stores are
+// coalesced.
+constexpr int kFinishPer = 16;
+constexpr int kFinishSpan = kFinishPer * kWave;
 template <typename RowT>
-__global__ __launch_bounds__(kThreads) void CscFinishKernel(const RowT* sortedPos, RowT* pos, int32_t* entryRow,
-                                                            const RowT* norm, int64_t rows, int64_t n)
+__device__ __forceinline__ int64_t LastRowAtOrBefore(const RowT* norm, int64_t lo, int64_t hi, int64_t k)
 {
-    const int64_t first = static_cast<int64_t>(norm[0]);
-    const int64_t last = static_cast<int64_t>(norm[rows]);
-    for (int64_t k = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; k < n;
-         k += static_cast<int64_t>(gridDim.x) * kThreads) {
-        if (sortedPos != pos) pos[k] = sortedPos[k];
-        int64_t lo = 0;
-        if (k >= first && k < last) {
-            int64_t hi = rows - 1;
-            while (lo < hi) {
-                const int64_t mid = (lo + hi + 1) >> 1;
-                if (static_cast<int64_t>(norm[mid]) <= k) lo = mid;
-                else hi = mid - 1;
-            }
-        }
-        entryRow[k] = static_cast<int32_t>(lo);
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (static_cast<int64_t>(norm[mid]) <= k) lo = mid;
+        else hi = mid - 1;
     }
+    return lo;
 }
 
+template <typename RowT>
+__global__ __launch_bounds__(kWave) void CscFinishKernel(const RowT* sortedPos, RowT* pos, int32_t* entryRow,
+                                                         const RowT* norm, int64_t rows, int64_t n)
+{
+    __shared__ int32_t mark[kFinishSpan];
+    const int64_t first = static_cast<int64_t>(norm[0]);
+    const int64_t last = static_cast<int64_t>(norm[rows]);
+    const int lane = threadIdx.x;
+    for (int64_t w = blockIdx.x; w * kFinishSpan < n; w += gridDim.x) {
+        const int64_t base = w * kFinishSpan;
+        const int64_t end = base + kFinishSpan < n ? base + kFinishSpan : n;
+        if (sortedPos != pos) {
+            for (int64_t k = base + lane; k < end; k += kWave) pos[k] = sortedPos[k];
+        }
+        const int64_t a = base > first ? base : first;
+        const int64_t b = (end < last ? end : last) - 1;
+        if (a > b) {  // no entry of the span lies in a row (uniform)
+            for (int64_t k = base + lane; k < end; k += kWave) entryRow[k] = 0;
+            continue;
+        }
+        const int64_t ra = LastRowAtOrBefore(norm, 0, rows - 1, a);
+        const int64_t rb = LastRowAtOrBefore(norm, ra, rows - 1, b);
+        for (int i = lane; i < kFinishSpan; i += kWave) mark[i] = -1;
+        __syncthreads();
+        for (int64_t r = ra + 1 + lane; r <= rb; r += kWave) {
+            const int64_t st = static_cast<int64_t>(norm[r]) - base;
+            if (st >= 0 && st < kFinishSpan) atomicMax(&mark[st], static_cast<int32_t>(r));
+        }
+        __syncthreads();
+        // running maximum over the lane's 16 entries, then over the lanes before it
+        int32_t v[kFinishPer];
+        int32_t run = -1;
+#pragma unroll
+        for (int j = 0; j < kFinishPer; ++j) {
+            const int32_t m = mark[lane * kFinishPer + j];
+            run = m > run ? m : run;
+            v[j] = run;
+        }
+        int32_t carry = run;  // inclusive prefix maximum of the lanes' maxima
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int32_t o = __shfl_up(carry, d, kWave);
+            if (lane >= d) carry = o > carry ? o : carry;
+        }
+        int32_t before = __shfl_up(carry, 1, kWave);
+        before = lane == 0 ? -1 : before;
+        const int32_t start = before > static_cast<int32_t>(ra) ? before : static_cast<int32_t>(ra);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kFinishPer; ++j) {
+            const int64_t k = base + lane * kFinishPer + j;
+            const int32_t r = v[j] > start ? v[j] : start;
+            mark[lane * kFinishPer + j] = k >= first && k < last ? r : 0;
+        }
+        __syncthreads();
+        for (int64_t k = base + lane; k < end; k += kWave) entryRow[k] = mark[k - base];
+        __syncthreads();
+    }
+}
 
 // Compact row table: one workgroup per group of kRowGroup entries.  Rows are
 // non-decreasing over [norm[0], norm[rows]), so the span of a group is its
@@ -3385,7 +3442,10 @@ int BuildCsc(const SpmvLaunch& l, hipStream_t s)
     }
     hipLaunchKernelGGL((CscColPtrKernel<RowT>), dim3(GridFor(nnz + 1)), dim3(kThreads), 0, s, keys.Current(), nnz,
                        l.cols, At<RowT>(l.ws, l.layout.colptr_offset));
-    hipLaunchKernelGGL((CscFinishKernel<RowT>), dim3(GridFor(nnz)), dim3(kThreads), 0, s, vals.Current(),
+    const int64_t finishWaves = (nnz + kFinishSpan - 1) / kFinishSpan;
+    hipLaunchKernelGGL((CscFinishKernel<RowT>),
+                       dim3(static_cast<unsigned>(finishWaves < 65536 ? (finishWaves > 0 ? finishWaves : 1) : 65536)),
+                       dim3(kWave), 0, s, vals.Current(),
                        At<RowT>(l.ws, l.layout.csc_pos_offset), At<int32_t>(l.ws, l.layout.entry_row_offset),
                        At<const RowT>(l.ws, l.layout.rowptr_offset), l.rows, nnz);
     hipLaunchKernelGGL((CscRowDeltaKernel<RowT>), dim3(static_cast<unsigned>(l.layout.row_groups)), dim3(kThreads),
