@@ -1024,10 +1024,10 @@ constexpr int kBtRunEntries = 64;  // mean run length (entries) below which the 
 constexpr int kBtMaxLongCols = static_cast<int>(kBtRegionCap) / (kBtLongCol + 1) + 1;
 
 // Bucket of entry k (S: outside the rows' range or a column outside [0, cols)).
-__device__ __forceinline__ uint32_t BtKey(const StageParams& q, int64_t k, int64_t first, int64_t last)
+__device__ __forceinline__ uint32_t BtKey(const StageParams& q, int64_t k, int64_t first, int64_t last, int32_t col)
 {
     if (k < first || k >= last) return static_cast<uint32_t>(q.buckets);
-    return KeyOf(q, q.col[k]) >> q.wshift;
+    return KeyOf(q, col) >> q.wshift;
 }
 
 // inv[csc_pos[j]] = j.
@@ -1051,7 +1051,20 @@ __global__ __launch_bounds__(kSortThreads) void BtCountKernel(StageParams q)
     if (t < q.tiles) {
         const int64_t first = Norm<RowT>(q, 0), last = Norm<RowT>(q, q.rows);
         const int64_t e0 = q.tile_nnz[t], e1 = q.tile_nnz[t + 1];
-        for (int64_t k = e0 + threadIdx.x; k < e1; k += kSortThreads) atomicAdd(&hist[BtKey(q, k, first, last)], 1U);
+        const int n = static_cast<int>(e1 - e0);
+        uint4 raw[kColGroups];
+        LoadTileCols(q, e0, n, raw);  // one round trip
+#pragma unroll
+        for (int u = 0; u < kColGroups; ++u) {
+            if (u * 4 * kSortThreads >= n) break;  // uniform
+            const int i = (u * kSortThreads + static_cast<int>(threadIdx.x)) * 4;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (i + k < n) {
+                    atomicAdd(&hist[BtKey(q, e0 + i + k, first, last, static_cast<int32_t>(WordOf(raw[u], k)))], 1U);
+                }
+            }
+        }
     }
     __syncthreads();
     for (int s = threadIdx.x; s < nb; s += kSortThreads) q.counts[s * (q.tiles + 1) + t] = hist[s];
@@ -1069,7 +1082,7 @@ __global__ __launch_bounds__(kSortThreads) void BtRankKernel(StageParams q)
 {
     constexpr int kNb = kBtMaxBuckets + 1;
     constexpr int kRunIpt = CeilDiv(kNb, kSortThreads);
-    constexpr int kBatch = 4;
+    static_assert(kItems <= kColGroups * 4 * kSortThreads, "a tile's entries fit the column loads");
     using Scan = hipcub::BlockScan<uint32_t, kSortThreads>;
     __shared__ uint32_t cnt[kNb];       // next slot of each bucket's run (tile-local)
     __shared__ uint32_t runBase[kNb];   // st_cl slot of each run's first entry minus its tile-local first slot
@@ -1106,26 +1119,35 @@ __global__ __launch_bounds__(kSortThreads) void BtRankKernel(StageParams q)
     }
     if (runs != 0U) atomicAdd(&runCount, runs);
     __syncthreads();
-    for (int i0 = 0; i0 < n; i0 += kBatch * kSortThreads) {
-        uint32_t key[kBatch];
-        int32_t inv[kBatch];
+    // the tile's column indices and CSC indices (inv) in one round trip of
+    // 16-byte loads, then per entry its slot and place
+    uint4 raw[kColGroups], rinv[kColGroups];
+    LoadTileCols(q, e0, n, raw);
+    {
+        const int64_t iBytes = (q.nnz - e0) * 4;
+        const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc(
+            q.inv + e0, 0, static_cast<int>(iBytes < 0x7FFFFFFFLL ? iBytes : 0x7FFFFFFFLL), 0x00020000);
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = i0 + u * kSortThreads + tid;
-            key[u] = i < n ? BtKey(q, e0 + i, first, last) : 0U;
-            inv[u] = i < n ? q.inv[e0 + i] : 0;
+        for (int u = 0; u < kColGroups; ++u) {
+            if (u * 4 * kSortThreads >= n) break;  // uniform
+            const int i = (u * kSortThreads + tid) * 4;
+            rinv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ri, i * 4, 0, 0));
         }
         asm volatile("" ::: "memory");
+    }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = i0 + u * kSortThreads + tid;
+    for (int u = 0; u < kColGroups; ++u) {
+        if (u * 4 * kSortThreads >= n) break;
+        const int i4 = (u * kSortThreads + tid) * 4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = i4 + k;
             if (i < n) {
-                const uint32_t b = key[u];
+                const uint32_t b = BtKey(q, e0 + i, first, last, static_cast<int32_t>(WordOf(raw[u], k)));
                 const uint32_t slot = atomicAdd(&cnt[b], 1U);
                 q.perm[e0 + i] = static_cast<uint16_t>(slot);
-                const uint32_t place = b < static_cast<uint32_t>(q.buckets)
-                                           ? static_cast<uint32_t>(inv[u]) - colBase[b]
-                                           : 0U;
+                const uint32_t place =
+                    b < static_cast<uint32_t>(q.buckets) ? WordOf(rinv[u], k) - colBase[b] : 0U;
                 q.cl[runBase[b] + slot] = static_cast<uint16_t>(place);
             }
         }
