@@ -112,15 +112,6 @@ struct StageParams {
     Scalars s;
 };
 
-// Workgroup index remapped so that each XCD serves a contiguous range
-// (hardware hands workgroup ids to the 8 XCDs round-robin); the grid is a
-// multiple of 8.
-__device__ __forceinline__ int64_t XcdIndex()
-{
-    const int64_t per = gridDim.x / kXcds;
-    return static_cast<int64_t>(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
-}
-
 // Workgroup -> tile of pass B (and slice of pass A): tiles in chunks of
 // kTileChunk per XCD, the chunks dealt to the XCDs round-robin, so that the
 // tiles in flight at any time are consecutive over the whole chip (their
@@ -546,13 +537,6 @@ __device__ __forceinline__ uint32_t GetW(const T& v)
     else return I == 0 ? v.x : I == 1 ? v.y : 0U;
 }
 
-// Sum over groups of 2^lg consecutive lanes (lg <= 6), fixed butterfly order.
-__device__ __forceinline__ float GroupSum(float v, int lg)
-{
-    for (int m = 1; m < (1 << lg); m <<= 1) v += __shfl_xor(v, m, kWave);
-    return v;
-}
-
 __device__ __forceinline__ float WaveSum(float v)
 {
     for (int m = kWave / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
@@ -647,7 +631,6 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     constexpr int kGroupSlots = CeilDiv((kItems + kG - 1) / kG + 1, kTileThreads);  // groups per thread
     using SV = StageVal<V>;
     using Raw = typename SV::Raw;
-    using Group = typename SV::Group;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
     // staged x moves in chunks of kP slots (runs are padded to whole chunks)
     constexpr int kCB = static_cast<int>(kStageChunkBytes);
