@@ -235,6 +235,29 @@ def test_staged_plan_with_an_unaligned_x_runs_the_row_kernels(dev):
     assert_close(want, y)
 
 
+def test_re_preprocess_switches_between_staged_and_row_kernels(dev):
+    """The same descriptor and workspace: random columns (staged gather), then the columns rewritten
+    in place to a band and Preprocess called again (the row kernels on the 16-bit column copy), then
+    random again: every SpMV matches the oracle for the columns it was given."""
+    rows, cols, per = 1 << 20, 1 << 22, 8
+    w = random_rows(dev, rows, cols, torch.full((rows,), per, dtype=torch.int64), torch.float32, torch.int32, 1.0,
+                    0.5)
+    y = w.y0.clone()
+    plan = CsrSpMV(w.rows, w.cols, w.row_ptr, w.col_ind, w.values, w.x, y, w.alpha, w.beta)
+    scattered = w.col_ind.clone()
+    band = (torch.arange(rows, device=dev, dtype=torch.int32)[:, None] +
+            torch.arange(per, device=dev, dtype=torch.int32)[None, :]).reshape(-1)  # columns row .. row+7
+    for cols_now, want_flag in ((scattered, (1,)), (band, (3, 5)), (scattered, (1,))):
+        w.col_ind.copy_(cols_now)
+        torch.cuda.synchronize()
+        plan.preprocess()
+        y.copy_(w.y0)
+        plan.run()
+        torch.cuda.synchronize()
+        assert header(plan)[0] in want_flag
+        assert_close(host_workload(w), y)
+
+
 def test_staged_device_scalars_and_beta_zero_ignores_nan_y(dev):
     from ops_sparse._lib import PointerMode
 
