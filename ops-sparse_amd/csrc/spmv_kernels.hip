@@ -1199,7 +1199,7 @@ __device__ __forceinline__ void FixupLongBlock(const RowBlockParams& p, const St
 // no flag load).  kNarrow: column indices from the narrow copy p.ncol.
 template <typename RowT, ValKind V, OutKind O, bool kBeta, bool kGated = false, bool kNarrow = false,
           bool kEntry = false>
-__global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(7)))
+__global__ __launch_bounds__(kWave* kFlatWaves) __attribute__((amdgpu_waves_per_eu(6)))
 void SpmvStreamFlatKernel(RowBlockParams p)
 {
     using ValT = typename ValOf<V>::T;
