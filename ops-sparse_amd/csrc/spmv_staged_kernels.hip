@@ -228,21 +228,37 @@ __global__ __launch_bounds__(kSortThreads) void StageCountKernel(StageParams q)
         uint4 raw[kColGroups];
         LoadTileCols(q, e0, n, raw);
         const uint32_t nullBucket = static_cast<uint32_t>(q.buckets);
+        // Banded tiles put most of their entries in one bucket and many on the
+        // same x lines: a group of 4 whose entries share a bucket counts once,
+        // and an entry on the same line as the one before it sets no bit, so
+        // that fewer LDS atomics pile up on one address.
 #pragma unroll
         for (int u = 0; u < kColGroups; ++u) {
             if (u * 4 * kSortThreads >= n) break;  // uniform
             const int i = (u * kSortThreads + static_cast<int>(threadIdx.x)) * 4;
+            uint32_t key[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) key[k] = KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k)));
+            const uint32_t b0 = key[0] >> q.wshift;
+            const bool whole = i + 4 <= n && (key[1] >> q.wshift) == b0 && (key[2] >> q.wshift) == b0 &&
+                               (key[3] >> q.wshift) == b0;
+            if (whole) {
+                atomicAdd(&hist[b0], 4U);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (i + k < n) atomicAdd(&hist[key[k] >> q.wshift], 1U);
+                }
+            }
+            uint32_t prevLine = 0xFFFFFFFFU;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if (i + k < n) {
-                    const uint32_t key = KeyOf(q, static_cast<int32_t>(WordOf(raw[u], k)));
-                    const uint32_t b = key >> q.wshift;
-                    atomicAdd(&hist[b], 1U);
-                    if (b != nullBucket) {
-                        const uint32_t h = ((key >> q.line_shift) * 2654435761U) >> 17;
-                        atomicOr(&map[h >> 5], 1U << (h & 31U));
-                    }
+                const uint32_t line = key[k] >> q.line_shift;
+                if (i + k < n && (key[k] >> q.wshift) != nullBucket && line != prevLine) {
+                    const uint32_t h = (line * 2654435761U) >> 17;
+                    atomicOr(&map[h >> 5], 1U << (h & 31U));
                 }
+                prevLine = line;
             }
         }
     }
