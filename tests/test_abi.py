@@ -586,3 +586,18 @@ def test_bridge_int32_scalar_checks():
                       (0, -2**31 - 1, "fit int32")):
         with pytest.raises(RuntimeError, match=msg):
             _check_int32_scalars(a, b)
+
+
+@pytest.mark.parametrize("rows,cols,nnz", [(1 << 19, 1 << 22, 1 << 22), (1 << 20, 1 << 19, 1 << 24)])
+def test_staged_tables_follow_the_size_rule(rows, cols, nnz, env):
+    """The DEFAULT workspace holds the staged-gather tables (slots, columns and gathered x: several
+    bytes per entry) from 2^22 entries with an x of 8 MB or more, and from 2^24 entries with an x
+    of 1 to 8 MB; one entry below the threshold it does not."""
+    sizes = []
+    for n in (nnz - 1, nnz):
+        A = env.csr(rows=rows, cols=cols, nnz=n, ptrs=False)
+        x, y = env.vec(cols, 0), env.vec(rows, 0)
+        st, full = env.size(N, A, x, y, alg=int(SpMVAlg.DEFAULT))
+        assert st == Status.SUCCESS
+        sizes.append(full)
+    assert sizes[1] - sizes[0] > 4 * nnz, sizes  # the staged tables appear at the threshold
