@@ -72,7 +72,7 @@ def _host(w):
     return h
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(16))
 def test_large_random_matrix(seed, dev):
     w = _case(seed, dev)
     op = Operation.TRANSPOSE if w.trans == "T" else Operation.NON_TRANSPOSE
