@@ -469,8 +469,20 @@ __global__ __launch_bounds__(kGatherThreads) void StageGatherKernel(StageParams 
             const int64_t c0 = static_cast<int64_t>(s) << q.wshift;
             const int64_t n = q.cols - c0 < segLen ? q.cols - c0 : segLen;
             const int64_t nv = n / kVec;
-            for (int64_t i = threadIdx.x; i < nv; i += kGatherThreads) {
-                segRaw[i] = reinterpret_cast<const uint4*>(x + c0)[i];
+            // the segment in one round trip: all of a thread's 16-byte loads,
+            // then its LDS stores
+            constexpr int kSegIters = static_cast<int>(kStageSegmentBytes) / 16 / kGatherThreads;
+            const uint4* xs = reinterpret_cast<const uint4*>(x + c0);
+            uint4 sv[kSegIters];
+#pragma unroll
+            for (int it = 0; it < kSegIters; ++it) {
+                const int64_t i = it * kGatherThreads + threadIdx.x;
+                sv[it] = i < nv ? xs[i] : uint4{};
+            }
+#pragma unroll
+            for (int it = 0; it < kSegIters; ++it) {
+                const int64_t i = it * kGatherThreads + threadIdx.x;
+                if (i < nv) segRaw[i] = sv[it];
             }
             for (int64_t i = nv * kVec + threadIdx.x; i < n; i += kGatherThreads) seg[i] = x[c0 + i];
             __syncthreads();
