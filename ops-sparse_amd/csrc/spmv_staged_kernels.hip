@@ -641,14 +641,17 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
     }
 }
 
-// One workgroup per tile (XCD-contiguous).  LDS: the run map (runDelta,
-// startBits, firstRank), then one area (at least kItems+8 words) that holds
-// the staged x values, then (in place) the products by groups of 4 entries,
-// followed by the tile's row offsets relative to the first group.  As many
-// waves per SIMD as the LDS allows: six for the narrow tiles (three
-// workgroups per CU), four for the wide ones.
+// One workgroup per tile (tiles dealt to the XCDs in chunks).  LDS: the run
+// map (runDelta, startBits, firstRank), then one area that holds the staged x
+// values, then (in place) the tile's row ends relative to the first group
+// (uint16) followed by the products by groups of kG entries.  The wide tiles
+// write and sum their products in two phases of half the groups each, so
+// that the area is no larger than the staged x: 48 KB of LDS per workgroup,
+// three workgroups (six waves per SIMD) per CU, as for the narrow tiles (two
+// workgroups of 75 KB with every product in LDS at once: pass B 747 -> 691
+// µs on the 16.8 M-row fp16 matrix with 32 random columns per row).
 template <int kItems, typename RowT, ValKind V, OutKind O, bool kRows16>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kNarrow ? 6 : kTileWaves / 2))) void StageTileKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6))) void StageTileKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
@@ -669,7 +672,12 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     constexpr int kChunkIters = (kChunkCap + kTileThreads - 1) / kTileThreads;  // 64-chunk windows per wave
     constexpr int kChunkWindows = kTileWaves * kChunkIters;
     constexpr int kChunkFloats = kCB / 4 * kChunkCap;
-    constexpr int kAreaFloats = (kTileItems + 2 * kG > kChunkFloats ? kTileItems + 2 * kG : kChunkFloats);
+    // products of one phase (a half of the tile's groups for the wide tiles)
+    // after the 16-bit row ends: at most R/2 + 8 words of row ends and
+    // E/kPhases + 1.5 kG words of products, R + E = kItems
+    constexpr int kPhases = kItems == kWide ? 2 : 1;
+    constexpr int kProdFloats = kTileItems / kPhases + 2 * kG + 8;
+    constexpr int kAreaFloats = kProdFloats > kChunkFloats ? kProdFloats : kChunkFloats;
     __shared__ uint32_t runDelta[kStageMaxBuckets + 1];
     __shared__ uint32_t startBits[2 * kChunkWindows];
     __shared__ uint32_t firstRank[kChunkWindows];
@@ -921,15 +929,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
         }
     }
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kGroupSlots; ++u) {
-        const int gi = tid + u * kTileThreads;
-        if (gi < ng) {
-#pragma unroll
-            for (int h = 0; h < kG / 4; ++h) areaV[gi * (kG / 4) + h] = prod[u][h];
-        }
-    }
-    int32_t* rel = reinterpret_cast<int32_t*>(area) + ng * kG;  // after the products
+    // row ends relative to the first group (uint16: at most a0 + E < 2^16),
+    // at the start of the area, the products of the current phase after them
+    uint16_t* rel = reinterpret_cast<uint16_t*>(area);
+    const int relWords = ((R + 2 + 1) / 2 + 3) & ~3;
+    float4* prodV = areaV + relWords / 4;
     const auto relOf = [&](int i, int64_t off) {
         if constexpr (kRows16) {
             if (i == 0) return a0;
@@ -943,35 +947,82 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int i = tid + u * kTileThreads;
-        if (i <= R) rel[i] = relOf(i, rowOff[u]);
+        if (i <= R) rel[i] = static_cast<uint16_t>(relOf(i, rowOff[u]));
     }
-    if (tid == 0) rel[R + 1] = a0 + E;
+    if (tid == 0) rel[R + 1] = static_cast<uint16_t>(a0 + E);
     for (int i = tid + 2 * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
-        rel[i] = relOf(i, kRows16 ? static_cast<int64_t>(q.rp16[r0 + i]) : Norm<RowT>(q, r0 + i));
+        rel[i] = static_cast<uint16_t>(relOf(i, kRows16 ? static_cast<int64_t>(q.rp16[r0 + i]) : Norm<RowT>(q, r0 + i)));
     }
-    __syncthreads();
 
-    // 6. rows: short ones by one thread, long ones queued for a wave
+    // 6. rows, by phases: phase p holds the products of groups [p*gs, ...)
+    //    (entries [p*em, ...) relative to the first group).  A row is summed
+    //    over its part in each phase it touches, the phase where it ends
+    //    finishes it; the one row that crosses em carries its first part in
+    //    crossPart.  Short parts by one thread, long ones queued for a wave.
     const bool betaNz = beta != 0.0f;  // y is not read when beta == 0, wherever beta lives
-    const bool tailHasEntries = lastRowInside && rel[R] < a0 + E;
-    for (int loc = tid; loc < nLoc; loc += kTileThreads) {
-        const int a = rel[loc], b = rel[loc + 1];
-        if (b - a > kLongRow) {
-            longRows[atomicAdd(&longCount, 1)] = loc;
-            continue;
+    const int gs = kPhases == 1 ? ng : ng / 2;
+    const int em = gs * kG;
+    __shared__ float crossPart;
+#pragma unroll
+    for (int ph = 0; ph < kPhases; ++ph) {
+        const int g1 = ph + 1 == kPhases ? ng : gs;
+        const int off = ph == 0 ? 0 : em;
+#pragma unroll
+        for (int u = 0; u < kGroupSlots; ++u) {
+            const int gi = tid + u * kTileThreads;
+            if (gi >= ph * gs && gi < g1) {
+#pragma unroll
+                for (int h = 0; h < kG / 4; ++h) prodV[(gi - ph * gs) * (kG / 4) + h] = prod[u][h];
+            }
         }
-        const float sum = ShortRowSum(areaV, a, b, lane);
-        FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
-    }
-    __syncthreads();
-    const int nLong = longCount;
-    for (int li = wv; li < nLong; li += kTileWaves) {
-        const int loc = longRows[li];
-        const int a = rel[loc], b = rel[loc + 1];
-        float part = 0.0f;
-        for (int k = a + lane; k < b; k += kWave) part += area[k];
-        const float sum = WaveSum(part);
-        if (lane == 0) FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
+        if (tid == 0) longCount = 0;
+        __syncthreads();
+        const bool tailHasEntries = lastRowInside && rel[R] < a0 + E;
+        for (int loc = tid; loc < nLoc; loc += kTileThreads) {
+            int a = rel[loc], b = rel[loc + 1];
+            bool finish = true, carry = false;
+            if constexpr (kPhases == 2) {
+                if (ph == 0) {
+                    if (a >= em) continue;
+                    if (b > em) { b = em; finish = false; }
+                } else {
+                    if (a < em && b <= em) continue;
+                    if (a < em) { a = em; carry = true; }
+                }
+            }
+            if (b - a > kLongRow) {
+                longRows[atomicAdd(&longCount, 1)] = loc;
+                continue;
+            }
+            float sum = ShortRowSum(prodV, a - off, b - off, lane);
+            if (carry) sum = crossPart + sum;
+            if (finish) FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
+            else crossPart = sum;
+        }
+        __syncthreads();
+        const int nLong = longCount;
+        for (int li = wv; li < nLong; li += kTileWaves) {
+            const int loc = longRows[li];
+            int a = rel[loc], b = rel[loc + 1];
+            bool finish = true, carry = false;
+            if constexpr (kPhases == 2) {
+                if (ph == 0) {
+                    if (b > em) { b = em; finish = false; }
+                } else if (a < em) {
+                    a = em;
+                    carry = true;
+                }
+            }
+            float part = 0.0f;
+            for (int k = a + lane; k < b; k += kWave) part += area[relWords + k - off];
+            float sum = WaveSum(part);
+            if (carry) sum = crossPart + sum;
+            if (lane == 0) {
+                if (finish) FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
+                else crossPart = sum;
+            }
+        }
+        if (ph + 1 < kPhases) __syncthreads();  // phase 1's products are read before phase 2 overwrites them
     }
 }
 
