@@ -641,17 +641,44 @@ __device__ __forceinline__ void FinishRow(const StageParams& q, int64_t t, int l
     }
 }
 
+// Pass B's LDS that depends on the bucket count (nb = S + 1), sized at
+// launch: the run map's first chunks (nb words), then the area of staged x
+// chunks / row ends and products (both in words, rounded to 16 bytes).
+template <int kItems, typename Raw>
+struct TileLds {
+    static constexpr int kG = sizeof(Raw) == 2 ? 8 : 4;  // entries per group
+    static constexpr int kP = static_cast<int>(kStageChunkBytes) / static_cast<int>(sizeof(Raw));
+    static constexpr int kPhases = kItems == kWide ? 2 : 1;
+    // products of one phase (a half of the tile's groups for the wide tiles)
+    // after the 16-bit row ends: at most R/2 + 8 words of row ends and
+    // E/kPhases + 1.5 kG words of products, R + E = kItems
+    static constexpr int kProdFloats = kItems / kPhases + 2 * kG + 8;
+    __host__ __device__ static constexpr int ChunkCap(int nb) { return (kItems + (kP - 1) * nb + kP - 1) / kP; }
+    __host__ __device__ static constexpr int RunWords(int nb) { return (nb + 3) & ~3; }
+    __host__ __device__ static constexpr int AreaWords(int nb)
+    {
+        const int staged = static_cast<int>(kStageChunkBytes) / 4 * ChunkCap(nb);
+        return ((staged > kProdFloats ? staged : kProdFloats) + 3) & ~3;
+    }
+    __host__ __device__ static constexpr int DynBytes(int nb) { return 4 * (RunWords(nb) + AreaWords(nb)); }
+};
+
 // One workgroup per tile (tiles dealt to the XCDs in chunks).  LDS: the run
-// map (runDelta, startBits, firstRank), then one area that holds the staged x
-// values, then (in place) the tile's row ends relative to the first group
-// (uint16) followed by the products by groups of kG entries.  The wide tiles
-// write and sum their products in two phases of half the groups each, so
-// that the area is no larger than the staged x: 48 KB of LDS per workgroup,
-// three workgroups (six waves per SIMD) per CU, as for the narrow tiles (two
-// workgroups of 75 KB with every product in LDS at once: pass B 747 -> 691
-// µs on the 16.8 M-row fp16 matrix with 32 random columns per row).
+// map (runDelta, sized at launch for the matrix's buckets, startBits,
+// firstRank), then one area that holds the staged x values, then (in place)
+// the tile's row ends relative to the first group (uint16) followed by the
+// products by groups of kG entries.  The wide tiles write and sum their
+// products in two phases of half the groups each, so that the area is no
+// larger than the staged x.  For x of 32 MB (257 buckets) that is 37 KB per
+// workgroup: four workgroups per CU (eight waves per SIMD) for the narrow
+// tiles (c3-like fp32 matrices: pass B 364 -> 334 µs against three
+// workgroups with room for 1025 buckets), three for the wide ones, whose
+// registers do not fit eight waves per SIMD without spilling (780 µs against
+// 691 at six).  Two workgroups of 75 KB per CU, every wide tile's products in
+// LDS at once, took 747 µs on the 16.8 M-row fp16 matrix with 32 random
+// columns per row.
 template <int kItems, typename RowT, ValKind V, OutKind O, bool kRows16>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6))) void StageTileKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kWide ? 6 : 8))) void StageTileKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
@@ -671,18 +698,14 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
     constexpr int kChunkCap = (kTileItems + (kP - 1) * (kStageMaxBuckets + 1) + kP - 1) / kP;
     constexpr int kChunkIters = (kChunkCap + kTileThreads - 1) / kTileThreads;  // 64-chunk windows per wave
     constexpr int kChunkWindows = kTileWaves * kChunkIters;
-    constexpr int kChunkFloats = kCB / 4 * kChunkCap;
-    // products of one phase (a half of the tile's groups for the wide tiles)
-    // after the 16-bit row ends: at most R/2 + 8 words of row ends and
-    // E/kPhases + 1.5 kG words of products, R + E = kItems
-    constexpr int kPhases = kItems == kWide ? 2 : 1;
-    constexpr int kProdFloats = kTileItems / kPhases + 2 * kG + 8;
-    constexpr int kAreaFloats = kProdFloats > kChunkFloats ? kProdFloats : kChunkFloats;
-    __shared__ uint32_t runDelta[kStageMaxBuckets + 1];
+    using Lds = TileLds<kItems, Raw>;
+    constexpr int kPhases = Lds::kPhases;
+    extern __shared__ float4 tileDyn[];  // Lds::DynBytes(nb) bytes
+    uint32_t* runDelta = reinterpret_cast<uint32_t*>(tileDyn);
+    float4* areaV = tileDyn + Lds::RunWords(q.buckets + 1) / 4;
     __shared__ uint32_t startBits[2 * kChunkWindows];
     __shared__ uint32_t firstRank[kChunkWindows];
-    __shared__ float4 areaV[(kAreaFloats + 3) / 4];
-    __shared__ int32_t longRows[kMaxLong];
+    __shared__ uint16_t longRows[kMaxLong];
     __shared__ int longCount;
     __shared__ int headFlag;
     float* area = reinterpret_cast<float*>(areaV);
@@ -991,7 +1014,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6)
                 }
             }
             if (b - a > kLongRow) {
-                longRows[atomicAdd(&longCount, 1)] = loc;
+                longRows[atomicAdd(&longCount, 1)] = static_cast<uint16_t>(loc);
                 continue;
             }
             float sum = ShortRowSum(prodV, a - off, b - off, lane);
@@ -1758,12 +1781,13 @@ void LaunchStagedTyped(const SpmvLaunch& l, const StageParams& q, hipStream_t s)
                        static_cast<unsigned>(kStageSegmentBytes), s, q);
     // fp32 values: the narrow tiles; fp16 / bf16: the wide ones (StageTileItems)
     constexpr int kItems = V == ValKind::F32 ? kNarrow : kWide;
+    const unsigned lds = static_cast<unsigned>(TileLds<kItems, Raw>::DynBytes(L.st_buckets + 1));
     if (q.rp16 != nullptr) {
         hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O, true>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads),
-                           0, s, q);
+                           lds, s, q);
     } else {
         hipLaunchKernelGGL((StageTileKernel<kItems, RowT, V, O, false>), dim3(XcdGrid(L.st_tiles)), dim3(kTileThreads),
-                           0, s, q);
+                           lds, s, q);
     }
     hipLaunchKernelGGL((StageFixupKernel<RowT, O>), dim3(static_cast<unsigned>((L.st_tiles + 255) / 256)), dim3(256),
                        0, s, q);
