@@ -586,7 +586,10 @@ __device__ __forceinline__ float GroupPart(const float4& f, int lo, int hi)
 // between them (at most 7) in an order rotated by the lane, so that the
 // lanes of rows of equal length (which start a multiple of the length apart)
 // spread over the LDS banks.  A fixed order per row and lane: the same row
-// always has the same lane.
+// always has the same lane.  kMidUnroll: how many of the middle groups' loads
+// may be in flight at once (1 keeps the registers of a caller that holds
+// many live values down; the sum is the same either way).
+template <int kMidUnroll = 7>
 __device__ __forceinline__ float ShortRowSum(const float4* areaV, int a, int b, int lane)
 {
     if (b <= a) return 0.0f;
@@ -601,7 +604,7 @@ __device__ __forceinline__ float ShortRowSum(const float4* areaV, int a, int b, 
         const int r = (lane & 7) & (p - 1);
         float mid[2] = {0.0f, 0.0f};
         if (__ballot(m > 3) != 0) {
-#pragma unroll
+#pragma unroll kMidUnroll
             for (int c = 0; c < 7; ++c) {
                 int u = r + c;
                 u = u >= m ? u - m : u;
@@ -670,15 +673,17 @@ struct TileLds {
 // products by groups of kG entries.  The wide tiles write and sum their
 // products in two phases of half the groups each, so that the area is no
 // larger than the staged x.  For x of 32 MB (257 buckets) that is 37 KB per
-// workgroup: four workgroups per CU (eight waves per SIMD) for the narrow
-// tiles (c3-like fp32 matrices: pass B 364 -> 334 µs against three
-// workgroups with room for 1025 buckets), three for the wide ones, whose
-// registers do not fit eight waves per SIMD without spilling (780 µs against
-// 691 at six).  Two workgroups of 75 KB per CU, every wide tile's products in
-// LDS at once, took 747 µs on the 16.8 M-row fp16 matrix with 32 random
-// columns per row.
+// workgroup: four workgroups per CU, eight waves per SIMD, for both tile
+// sizes.  The wide tiles fit eight waves' registers (63 VGPRs) by loading
+// their slots after the staging loads and by summing a row's middle groups
+// in a loop rather than seven loads at once (with either one missing, 4-12
+// VGPRs spill and pass B is slower than at six waves).  On the 16.8 M-row
+// fp16 matrix with 32 random columns per row pass B took 747 µs with two
+// workgroups of 75 KB per CU (every product in LDS at once), 691-698 µs with
+// three, 647 µs with four; on the c3-like fp32 matrix 364 -> 334 µs from
+// three workgroups (room for 1025 buckets) to four.
 template <int kItems, typename RowT, ValKind V, OutKind O, bool kRows16>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kItems == kWide ? 6 : 8))) void StageTileKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(8))) void StageTileKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
@@ -700,6 +705,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     constexpr int kChunkWindows = kTileWaves * kChunkIters;
     using Lds = TileLds<kItems, Raw>;
     constexpr int kPhases = Lds::kPhases;
+    constexpr bool kLateSlots = kItems == kWide;
     extern __shared__ float4 tileDyn[];  // Lds::DynBytes(nb) bytes
     uint32_t* runDelta = reinterpret_cast<uint32_t*>(tileDyn);
     float4* areaV = tileDyn + Lds::RunWords(q.buckets + 1) / 4;
@@ -726,6 +732,8 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
     //   2. row offsets, values and slots (need the corners), then the staged
     //      x runs (need the run table's scan); the wave waits for the row
     //      offsets, then for the runs, while the values are still arriving.
+    //      The wide tiles issue their slots after the staging instead, so
+    //      that fewer registers are live at once (kLateSlots).
     // Vector loads are buffer loads under no lane-divergent branch (a load
     // under such a branch makes the wave wait for it where the branches
     // join): addresses outside a buffer read zero, and lanes with nothing to
@@ -819,10 +827,12 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
         } else {
             gv[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, gi * 8, 0, 0));
         }
-        if constexpr (kG == 8) {
-            gp[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, gi * 16, 0, 0));
-        } else {
-            gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+        if constexpr (!kLateSlots) {
+            if constexpr (kG == 8) {
+                gp[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, gi * 16, 0, 0));
+            } else {
+                gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+            }
         }
     }
     asm volatile("" ::: "memory");
@@ -908,6 +918,17 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
         for (int m = 0; m < kChunkIters; ++m) {
             const int i = i0 + m * kWave + lane;
             if (i < i1) xl[i] = v[m];
+        }
+    }
+    if constexpr (kLateSlots) {  // the slots after the staging: fewer registers live at once
+#pragma unroll
+        for (int u = 0; u < kGroupSlots; ++u) {
+            const int gi = tid + u * kTileThreads;
+            if constexpr (kG == 8) {
+                gp[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rp, gi * 16, 0, 0));
+            } else {
+                gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
+            }
         }
     }
     __syncthreads();
@@ -1017,7 +1038,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kI
                 longRows[atomicAdd(&longCount, 1)] = static_cast<uint16_t>(loc);
                 continue;
             }
-            float sum = ShortRowSum(prodV, a - off, b - off, lane);
+            float sum = ShortRowSum<kPhases == 2 ? 1 : 7>(prodV, a - off, b - off, lane);
             if (carry) sum = crossPart + sum;
             if (finish) FinishRow<O>(q, t, loc, R, headRow, tailHasEntries, sum, alpha, beta, betaNz, r0);
             else crossPart = sum;
