@@ -1111,9 +1111,9 @@ __global__ __launch_bounds__(256) void StageFixupKernel(StageParams q)
 // columns' CSC range.
 //  * Pass 1 (BtScatterKernel), one workgroup per tile: the products
 //    a_k * x[row(k)] (values in CSR order, coalesced; each row's x spread
-//    over its entries in LDS), placed in LDS at their slots, then written as
-//    the tile's runs; runs of neighbouring tiles are adjacent, so their
-//    partial lines merge in L2.
+//    over its entries in LDS, half a tile at a time), placed in LDS at their
+//    slots (again by halves), then written as the tile's runs; runs of
+//    neighbouring tiles are adjacent, so their partial lines merge in L2.
 //  * Pass 2 (BtColumnKernel), one workgroup per CU looping over the buckets
 //    (each bucket's region of up to kBtRegionCap products takes most of a
 //    CU's LDS; the next bucket's loads fly while the current one is summed):
@@ -1308,14 +1308,27 @@ __global__ __launch_bounds__(256) void BtDecideKernel(StageParams q)
     if (threadIdx.x == 0) *q.flag = scattered ? (ok != 0 ? 1U : 0U) : (q.banded_ok != 0 ? 2U : 0U);
 }
 
+// Pass 1's LDS sized at launch: the run map's first slots (nb words), then
+// an area for the 16-bit row ends plus x over half the tile's entries, or
+// half the tile's products at their slots (kWide/2 + 80 words either way).
+constexpr unsigned BtScatterLdsBytes(int64_t nb)
+{
+    return static_cast<unsigned>(4 * (((nb + 3) & ~int64_t{3}) + ((kWide / 2 + 80 + 3) & ~3)));
+}
+
 // Pass 1: products of one tile into its runs (see above).  The row offsets
 // and x of the tile's first kBtPreRows*kTileThreads rows are loaded with the
-// values and slots (tiles of the Poisson-like c5 pattern hold about 1400
-// rows); rows past them, in tiles of many short rows, are read after.
+// values (tiles of the Poisson-like c5 pattern hold about 1400 rows); rows
+// past them, in tiles of many short rows, are read after.  The x spread and
+// the slot placement each go in two halves, so that the LDS area is half a
+// tile (43 KB per workgroup with 1025 buckets: three workgroups per CU, six
+// waves per SIMD at 77 VGPRs, the products taking the values' registers and
+// the slots loaded after the products): c5 pass 1 66.4 -> 62.3 µs against two
+// workgroups of 81 KB.  Eight waves per SIMD spill 25-30 VGPRs.
 constexpr int kBtPreRows = 4;
 
 template <int kItems, typename RowT>
-__global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(6))) void BtScatterKernel(StageParams q)
 {
     constexpr int kTileItems = kItems;
     constexpr int kMaxLong = Tile<kItems>::kMaxLong;
@@ -1323,12 +1336,13 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     constexpr int kStageLanes = Tile<kItems>::kStageLanes;
     constexpr int kWindows = Tile<kItems>::kWindows;
     using Scan = hipcub::BlockScan<uint32_t, kTileThreads>;
-    __shared__ uint32_t runDelta[kBtMaxBuckets + 1];
+    extern __shared__ float4 btDyn[];  // BtScatterLdsBytes(nb) bytes: the run map's first slots, then the area
+    uint32_t* runDelta = reinterpret_cast<uint32_t*>(btDyn);
+    float4* areaV = btDyn + ((q.buckets + 1 + 3) & ~3) / 4;
     __shared__ uint32_t startBits[2 * kWindows];
     __shared__ uint32_t firstRank[kWindows];
-    __shared__ float4 areaV[(kTileItems + 8 + 3) / 4];
-    __shared__ int32_t longRows[kMaxLong];
-    __shared__ int longCount;
+    __shared__ uint16_t longRows[kMaxLong];
+    __shared__ int longCount[2];
     __shared__ typename Scan::TempStorage scanStorage;
     float* area = reinterpret_cast<float*>(areaV);
 
@@ -1407,12 +1421,10 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         q.perm + g0 * 4, 0, static_cast<int>(pBytes < 0x7FFFFFFFLL ? pBytes : 0x7FFFFFFFLL), 0x00020000);
     uint4 gv[kGroupSlots];
-    uint2 gp[kGroupSlots];
 #pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
         gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, gi * 16, 0, 0));
-        gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
     }
     asm volatile("" ::: "memory");
 
@@ -1441,93 +1453,127 @@ __global__ __launch_bounds__(kTileThreads) void BtScatterKernel(StageParams q)
             for (uint32_t w = (o + 63U) >> 6; w * 64U < o + c; ++w) firstRank[w] = r;
         }
     }
-    // row offsets relative to the first group, clamped to the tile, after the entry area
-    int32_t* rel = reinterpret_cast<int32_t*>(area) + ((a0 + E + 3) & ~3);
+    // row ends relative to the first group (uint16: at most a0 + E < 2^16),
+    // at the start of the area
+    uint16_t* rel = reinterpret_cast<uint16_t*>(area);
+    const int relWords = ((R + 2 + 1) / 2 + 3) & ~3;
+    float* xs = area + relWords;  // x over the entries of the current half
+    const float4* xs4 = reinterpret_cast<const float4*>(xs);
 #pragma unroll
     for (int u = 0; u < kBtPreRows; ++u) {
         const int i = tid + u * kTileThreads;
         const int64_t d = rowOff[u] - e0;
-        if (i <= R) rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        if (i <= R) rel[i] = static_cast<uint16_t>(a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d));
     }
     for (int i = tid + kBtPreRows * kTileThreads; i <= R; i += kTileThreads) {  // tiles of many short rows
         const int64_t d = Norm<RowT>(q, r0 + i) - e0;
-        rel[i] = a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d);
+        rel[i] = static_cast<uint16_t>(a0 + static_cast<int32_t>(d < 0 ? 0 : d > E ? E : d));
     }
     if (tid == 0) {
-        rel[R + 1] = a0 + E;
-        longCount = 0;
+        rel[R + 1] = static_cast<uint16_t>(a0 + E);
+        longCount[0] = 0;
+        longCount[1] = 0;
     }
     __syncthreads();
 
-    // 4. each row's x over its entries (area, by entry), long rows by a wave
-    for (int loc = tid, u = 0; loc < nLoc; loc += kTileThreads, ++u) {
-        const int a = rel[loc], b = rel[loc + 1];
-        if (b - a > kLongRow) {
-            longRows[atomicAdd(&longCount, 1)] = loc;
-            continue;
-        }
-        float xv = 0.0f;
+    // 4. products in two halves of the tile's groups: each row's x over its
+    //    entries of the half (xs, by entry; long rows by a wave), then the
+    //    half's products into registers.  The tile's two edge groups also
+    //    hold entries of the neighbouring tiles, which are skipped below.
+    const int gs = ng / 2, em = gs * 4;
+    // each group's products replace its values in gv (the same registers)
 #pragma unroll
-        for (int h = 0; h < kBtPreRows; ++h) xv = u == h ? xRow[h] : xv;
-        if (u >= kBtPreRows) xv = static_cast<const float*>(q.x)[r0 + loc];
-        for (int k = a; k < b; ++k) area[k] = xv;
+    for (int ph = 0; ph < 2; ++ph) {
+        const int lo = ph == 0 ? 0 : em, hi = ph == 0 ? em : ng * 4;
+        for (int loc = tid, u = 0; loc < nLoc; loc += kTileThreads, ++u) {
+            int a = rel[loc], b = rel[loc + 1];
+            a = a > lo ? a : lo;
+            b = b < hi ? b : hi;
+            if (b <= a) continue;
+            if (b - a > kLongRow) {
+                longRows[atomicAdd(&longCount[ph], 1)] = static_cast<uint16_t>(loc);
+                continue;
+            }
+            float xv = 0.0f;
+#pragma unroll
+            for (int h = 0; h < kBtPreRows; ++h) xv = u == h ? xRow[h] : xv;
+            if (u >= kBtPreRows) xv = static_cast<const float*>(q.x)[r0 + loc];
+            for (int k = a; k < b; ++k) xs[k - lo] = xv;
+        }
+        __syncthreads();
+        const int nLong = longCount[ph];
+        for (int li = wv; li < nLong; li += kTileWaves) {
+            const int loc = longRows[li];
+            int a = rel[loc], b = rel[loc + 1];
+            a = a > lo ? a : lo;
+            b = b < hi ? b : hi;
+            const float xv = static_cast<const float*>(q.x)[r0 + loc];
+            for (int k = a + lane; k < b; k += kWave) xs[k - lo] = xv;
+        }
+        __syncthreads();
+        const int gb = ph == 0 ? 0 : gs, ge = ph == 0 ? gs : ng;
+#pragma unroll
+        for (int u = 0; u < kGroupSlots; ++u) {
+            const int gi = tid + u * kTileThreads;
+            if (gi >= gb && gi < ge) {
+                const float4 xv4 = xs4[gi - gb];
+                gv[u] = make_uint4(__float_as_uint(__uint_as_float(gv[u].x) * xv4.x),
+                                   __float_as_uint(__uint_as_float(gv[u].y) * xv4.y),
+                                   __float_as_uint(__uint_as_float(gv[u].z) * xv4.z),
+                                   __float_as_uint(__uint_as_float(gv[u].w) * xv4.w));
+            }
+        }
+        __syncthreads();  // xs is overwritten next
     }
-    __syncthreads();
-    const int nLong = longCount;
-    for (int li = wv; li < nLong; li += kTileWaves) {
-        const int loc = longRows[li];
-        const int a = rel[loc], b = rel[loc + 1];
-        const float xv = static_cast<const float*>(q.x)[r0 + loc];
-        for (int k = a + lane; k < b; k += kWave) area[k] = xv;
-    }
-    __syncthreads();
 
-    // 5. products in registers, then at their slots; the tile's two edge
-    //    groups also hold entries of the neighbouring tiles, which are skipped
-    float pr[kGroupSlots][4];
+    // 5. the slots (loaded only now: fewer registers live at once), then the
+    //    products at their slots and the tile's runs, in two halves of the
+    //    slots split at a 64-slot window: slot i of the 64-slot windows of
+    //    wave w goes to prod[runDelta[run(i)] + i]
+    uint2 gp[kGroupSlots];
 #pragma unroll
     for (int u = 0; u < kGroupSlots; ++u) {
         const int gi = tid + u * kTileThreads;
-        const float4 xv4 = gi < ng ? areaV[gi] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        pr[u][0] = __uint_as_float(gv[u].x) * xv4.x;
-        pr[u][1] = __uint_as_float(gv[u].y) * xv4.y;
-        pr[u][2] = __uint_as_float(gv[u].z) * xv4.z;
-        pr[u][3] = __uint_as_float(gv[u].w) * xv4.w;
+        gp[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, gi * 8, 0, 0));
     }
-    __syncthreads();
+    constexpr int kHalfLanes = CeilDiv(kTileItems / 2 + 64, kTileThreads);  // 64-slot windows per wave and half
+    const int H = (E / 2 + 63) & ~63;
+    const uint32_t maskLo = lane < 32 ? (2U << lane) - 2U : 0xFFFFFFFEU;
+    const uint32_t maskHi = lane < 32 ? 0U : (2U << (lane - 32)) - 1U;
 #pragma unroll
-    for (int u = 0; u < kGroupSlots; ++u) {
-        const int gi = tid + u * kTileThreads;
-        const int lo = a0 - gi * 4, hi = a0 + E - gi * 4;  // entries [lo, hi) of the group are the tile's
+    for (int ph = 0; ph < 2; ++ph) {
+        const int s0 = ph == 0 ? 0 : H;
+        const int s1 = ph == 0 ? (H < E ? H : E) : E;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
-            const int slot = static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU);
-            if (k >= lo && k < hi) area[slot] = pr[u][k];
+        for (int u = 0; u < kGroupSlots; ++u) {
+            const int gi = tid + u * kTileThreads;
+            const int lo = a0 - gi * 4, hi = a0 + E - gi * 4;  // entries [lo, hi) of the group are the tile's
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t pw = k < 2 ? gp[u].x : gp[u].y;
+                const int slot = static_cast<int>((pw >> ((k & 1) * 16)) & 0xFFFFU);
+                const uint32_t pv = k == 0 ? gv[u].x : k == 1 ? gv[u].y : k == 2 ? gv[u].z : gv[u].w;
+                if (k >= lo && k < hi && slot >= s0 && slot < s1) area[slot - s0] = __uint_as_float(pv);
+            }
         }
-    }
-    __syncthreads();
-
-    // 6. the tile's runs: slot i of the 64-slot windows of wave w goes to
-    //    prod[runDelta[run(i)] + i]
-    {
-        const int span = (E + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
-        const int i0 = __builtin_amdgcn_readfirstlane(wv) * span;
-        const int i1 = i0 + span < E ? i0 + span : E;
-        const uint32_t maskLo = lane < 32 ? (2U << lane) - 2U : 0xFFFFFFFEU;
-        const uint32_t maskHi = lane < 32 ? 0U : (2U << (lane - 32)) - 1U;
+        __syncthreads();
+        const int n = s1 - s0;
+        const int span = (n + kTileWaves * kWave - 1) / (kTileWaves * kWave) * kWave;
+        const int i0 = s0 + __builtin_amdgcn_readfirstlane(wv) * span;
+        const int i1 = i0 + span < s1 ? i0 + span : s1;
 #pragma unroll
-        for (int m = 0; m < kStageLanes; ++m) {
+        for (int m = 0; m < kHalfLanes; ++m) {
             const int w = (i0 >> 6) + m;
             const int i = (w << 6) + lane;
-            const uint32_t fr = firstRank[w];
-            const uint32_t bLo = startBits[2 * w], bHi = startBits[2 * w + 1];
+            const uint32_t fr = firstRank[w < kWindows ? w : 0];
+            const uint32_t bLo = startBits[2 * (w < kWindows ? w : 0)], bHi = startBits[2 * (w < kWindows ? w : 0) + 1];
             const uint32_t r = fr + static_cast<uint32_t>(__builtin_popcount(bLo & maskLo)) +
                                static_cast<uint32_t>(__builtin_popcount(bHi & maskHi));
             const uint32_t d = runDelta[r];
-            const float v = area[i < i1 ? i : 0];
+            const float v = area[i < i1 ? i - s0 : 0];
             if (i < i1) q.prod[d + static_cast<uint32_t>(i)] = v;
         }
+        if (ph == 0) __syncthreads();  // the first half's runs are read before the second half is placed
     }
 }
 
@@ -1787,8 +1833,8 @@ template <typename RowT>
 void BtComputeTyped(const SpmvLaunch& l, hipStream_t s)
 {
     const StageParams q = MakeStageParams(l);
-    hipLaunchKernelGGL((BtScatterKernel<kWide, RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads), 0, s,
-                       q);
+    hipLaunchKernelGGL((BtScatterKernel<kWide, RowT>), dim3(XcdGrid(l.layout.st_tiles)), dim3(kTileThreads),
+                       BtScatterLdsBytes(l.layout.st_buckets + 1), s, q);
     const int64_t colGrid = l.layout.st_buckets < kBtColGrid ? l.layout.st_buckets : kBtColGrid;
     hipLaunchKernelGGL((BtColumnKernel<RowT>), dim3(static_cast<unsigned>(colGrid)), dim3(kBtColThreads), 0, s, q);
 }
