@@ -304,3 +304,26 @@ def test_random_pattern_with_few_wide_buckets_takes_the_bucketed_kernels(dev):
     assert flag == 1
     assert w.nnz / (buckets * tiles) > 64  # long runs, yet scattered
     assert_close(w.to("cpu"), y)
+
+
+@pytest.mark.parametrize("seed", [41, 42])
+def test_mixed_row_lengths_meet_the_middle_of_every_tile(dev, seed):
+    """Rows of 0-120 entries (10% empty) with random columns: pass 1 spreads x and places the
+    products half a tile at a time, so short rows, rows longer than 32 entries (spread by a wave)
+    and empty rows meet the middle of the tile's entries, and runs cross the middle of its slots,
+    at every offset.  Bit-identical on a second run."""
+    rows, cols = 300_001, (1 << 20) + 77
+    rng = np.random.default_rng(seed)
+    lengths = torch.from_numpy(np.where(rng.random(rows) < 0.1, 0, rng.integers(1, 121, rows)).astype(np.int64))
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    row_ptr, col = wl.csr_from_lengths(lengths, cols, g, "cpu", distinct=False)
+    n = col.numel()
+    w = wl.Workload(f"bt_mixed_{seed}", rows, cols, row_ptr.to(torch.int32), col.to(torch.int32),
+                    torch.rand(n, generator=g) * 2 - 1, torch.rand(rows, generator=g) * 2 - 1,
+                    torch.rand(cols, generator=g) * 2 - 1, 0.75, -1.0, trans="T").to(dev)
+    y, plan = run(w)
+    assert header(plan)[0] == 1
+    assert_close(w.to("cpu"), y)
+    y2, _ = run(w)
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))

@@ -98,6 +98,11 @@ CASES = [
     ("ragged_fp16_i32_odd", (1 << 20) + 7, 3 * (1 << 21) + 12345, "ragged", torch.float16, torch.int32, 0.75, 0.25,
      0),
     ("ragged_fp32_i64_odd_base1", (1 << 20) + 3, (1 << 22) + 1, "ragged", torch.float32, torch.int64, 1.0, 0.0, 1),
+    # rows of 0-120 entries: the wide (fp16 / bf16) tiles sum their products in two halves, and
+    # short rows, rows longer than 32 entries (summed by a wave) and empty rows all meet the
+    # middle of some tile, on either side of it or across it
+    ("mixed_lengths_fp16_i64", 650_000, 1 << 22, "mixed", torch.float16, torch.int64, 1.0, 0.0, 0),
+    ("mixed_lengths_bf16_i32_beta", 650_001, (1 << 22) + 5, "mixed", torch.bfloat16, torch.int32, -1.25, 0.5, 0),
 ]
 
 
@@ -117,6 +122,9 @@ def lengths_for(kind, rows, seed=3):
         ln = rng.integers(25, 41, rows)
         if ln.sum() % 2 == 0:
             ln[-1] += 1
+        return torch.from_numpy(ln.astype(np.int64))
+    if kind == "mixed":  # 0..120 entries per row, 10% empty rows
+        ln = np.where(rng.random(rows) < 0.1, 0, rng.integers(1, 121, rows))
         return torch.from_numpy(ln.astype(np.int64))
     if kind == "sparse":  # 2 entries per row on average, 40% empty rows: tiles hold many rows
         ln = np.where(rng.random(rows) < 0.4, 0, rng.integers(1, 6, rows))
