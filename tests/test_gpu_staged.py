@@ -101,6 +101,10 @@ CASES = [
     # rows of 0-120 entries: the wide (fp16 / bf16) tiles sum their products in two halves, and
     # short rows, rows longer than 32 entries (summed by a wave) and empty rows all meet the
     # middle of some tile, on either side of it or across it
+    # x of just under 128 MiB: 1024 buckets, the most the staged tables allow, so pass B's run map
+    # and staging area (sized at launch for the bucket count) are at their largest
+    ("max_buckets_fp16", 1 << 20, (1 << 26) - 3, "uniform32", torch.float16, torch.int32, 1.0, 0.0, 0),
+    ("max_buckets_fp32_beta", 1 << 20, (1 << 25) - 1, "uniform32", torch.float32, torch.int64, 0.5, 1.5, 0),
     ("mixed_lengths_fp16_i64", 650_000, 1 << 22, "mixed", torch.float16, torch.int64, 1.0, 0.0, 0),
     ("mixed_lengths_bf16_i32_beta", 650_001, (1 << 22) + 5, "mixed", torch.bfloat16, torch.int32, -1.25, 0.5, 0),
 ]
