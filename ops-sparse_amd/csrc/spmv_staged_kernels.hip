@@ -675,7 +675,7 @@ struct TileLds {
 // larger than the staged x.  For x of 32 MB (257 buckets) that is 37 KB per
 // workgroup: four workgroups per CU, eight waves per SIMD, for both tile
 // sizes.  The wide tiles fit eight waves' registers (63 VGPRs) by loading
-// their slots after the staging loads and by summing a row's middle groups
+// their slots after the staging stores and by summing a row's middle groups
 // in a loop rather than seven loads at once (with either one missing, 4-12
 // VGPRs spill and pass B is slower than at six waves).  On the 16.8 M-row
 // fp16 matrix with 32 random columns per row pass B took 747 µs with two
@@ -1066,7 +1066,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(8)
                 else crossPart = sum;
             }
         }
-        if (ph + 1 < kPhases) __syncthreads();  // phase 1's products are read before phase 2 overwrites them
+        if (ph + 1 < kPhases) __syncthreads();  // the first half's products are read before the second half overwrites them
     }
 }
 
